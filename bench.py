@@ -1,0 +1,215 @@
+#!/usr/bin/env python
+"""bench.py -- quantized-GEMV weight-stream throughput on one MI355X.
+
+Workload: the Q5_0 batch-1 projections of
+Qwen2-0.5B -- attn_q 896x896 run as one descriptor with num_tiles=224 and
+tile_res_rows=4, ffn_gate and ffn_up 4864x896 -- on a seeded N(0,1) fp32
+activation.  The three tensors are replicated over enough distinct weight
+sets that one step streams more than the 256 MiB Infinity Cache (42 sets,
+275 MB); a step is one pass of the descriptor chain over all of them: one
+activation-quantisation launch plus one launch of every GEMV.
+
+value  = ggml weight bytes streamed per step / step time  (GB/s)
+roofline.achieved = the same bytes / average duration of the GEMV launch
+         alone (HIP events on the library's stream), against 8 TB/s.
+cpu_baseline = the reference's own matmul_fpga_q5_0 (sim/tmac_gguf.cpp:1221,
+         compiled in place into oracle/_ref) or, where that was not built, its
+         C restatement, on one host core over the same shapes.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "tmac-zynq-fpga_amd")
+sys.path.insert(0, PKG)
+
+PEAK_GBPS = 8000.0  # MI355X HBM3E, datasheet
+METRIC = "quant GEMV weight GB/s (% HBM peak); Qwen2-0.5B batch-1 decode tok/s"
+SETS = 42           # 42 x (551936 + 2 x 2996224) B = 274.9 MB > 256 MiB
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chain_q5_0_c2_traffic.txt")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_workload(ctx, torch, dev, sets):
+    import tmq
+    from tmq import synth
+    shapes = [("attn_q", 896, 896), ("ffn_gate", 4864, 896), ("ffn_up", 4864, 896)]
+    x = synth.gen_x(896, 12345)
+    x_d = torch.from_numpy(x).to(dev)
+    tensors, descs, ys = [], [], []
+    for s in range(sets):
+        for k, (name, rows, cols) in enumerate(shapes):
+            w = synth.gen_weights(tmq.Q5_0, rows, cols, seed=1000 * s + k)
+            t = ctx.upload(tmq.Q5_0, rows, cols, w)
+            y = torch.empty(rows, dtype=torch.float32, device=dev)
+            tensors.append(t)
+            ys.append(y)
+            # PhaseB Q5_0 descriptor semantics: 4-row tiles, num_tiles = rows/4
+            descs.append((t, x_d.data_ptr(), y.data_ptr(), None, rows // 4, 4, 1))
+        if s % 10 == 0:
+            log(f"uploaded weight set {s + 1}/{sets}")
+    return x, x_d, tensors, descs, ys, shapes
+
+
+def time_events(torch, stream, fn, iters):
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters  # ms
+
+
+def read_traffic():
+    """HBM bytes per chain launch measured with rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE (scaled by a copy-kernel calibration), if committed."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def cpu_baseline(shapes, seconds):
+    """Reference CPU path on one core, bounded sample of the same workload."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle, Reference
+    from tmq import synth
+    kind = "reference" if Reference.available() else "port"
+    impl = Reference() if kind == "reference" else Oracle()
+    x = synth.gen_x(896, 12345)
+    ws = [(synth.gen_weights(6, r, c, seed=k), r, c) for k, (_, r, c) in enumerate(shapes)]
+    nbytes = sum(w.size for w, _, _ in ws)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for w, r, c in ws:
+            impl.matmul(6, w, x, r, c)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    gbps = done * nbytes / el / 1e9
+    name = "sim matmul_fpga_q5_0 (compiled reference)" if kind == "reference" else "C restatement of matmul_fpga_q5_0"
+    return {"value": round(gbps, 5), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{name} over attn_q 896x896 + ffn_gate/ffn_up 4864x896 "
+                      f"({nbytes} weight bytes) x {done} passes = {el:.1f} s on one host thread, "
+                      f"per-call row scan included as in the reference"}
+
+
+def copy_calibration(torch, dev, nbytes=1 << 30):
+    """A plain device copy of known size, for scaling FETCH_SIZE/WRITE_SIZE."""
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "launches": 3}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--sets", type=int, default=SETS)
+    ap.add_argument("--copy-calibration", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only; the GEMV shards by output rows with "
+              "no exchange (see DESIGN.md), multi-GPU runs are not part of it", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import tmq
+    dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(torch, dev)
+        return
+
+    ctx = tmq.Context(0)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    log(f"building workload: {args.sets} sets of Q5_0 attn_q/ffn_gate/ffn_up")
+    x, x_d, tensors, descs, ys, shapes = build_workload(ctx, torch, dev, args.sets)
+    chain = ctx.chain(descs)
+    wbytes = chain.weight_bytes
+    log(f"chain: {len(descs)} descriptors, {wbytes} weight bytes per step")
+
+    for _ in range(args.warmup):
+        chain.run()
+    ctx.sync()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    step_ms = time_events(torch, stream, chain.run, args.steps)
+    ctx.sync()
+    torch.cuda.synchronize()
+    chain.prepare()
+    kern_ms = time_events(torch, stream, chain.launch, args.steps)
+    ctx.sync()
+    torch.cuda.synchronize()
+
+    value = wbytes / (step_ms * 1e-3) / 1e9
+    achieved = wbytes / (kern_ms * 1e-3) / 1e9
+    traffic = read_traffic()
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int16",
+        "data": "synthetic (seeded ggml Q5_0 blocks: random qs/qh bits, d=fp16(|N(0,1)|*0.02); x ~ N(0,1))",
+        "config": {
+            "workload": "BASELINE configs[1]: Q5_0 attn_q 896x896 (1 descriptor, num_tiles=224, "
+                        "tile_res_rows=4) + ffn_gate/ffn_up 4864x896, batch 1, "
+                        f"{args.sets} weight sets cycled ({wbytes} B > 256 MiB), one chain launch per step",
+            "descriptors_per_step": len(descs),
+            "weight_bytes_per_step": wbytes,
+            "pct_hbm_peak": round(100.0 * value / PEAK_GBPS, 2),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "chain_kernel",
+            "kernel_ms": round(kern_ms, 5),
+        },
+    }
+    chain.free()
+    for t in tensors:
+        t.free()
+    ctx.close()
+    if not args.no_cpu:
+        log(f"CPU baseline ({args.cpu_seconds:.0f} s sample)")
+        out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,179 @@
+/*
+ * tmq.h -- C ABI of the MI355X (gfx950) quantized-GEMV library (libtmq.so).
+ *
+ * Drop-in for the quantized matrix-vector path of liuwantao3/tmac-zynq-fpga
+ * that the reference offloads to its FPGA cores.  Each entry point names the
+ * reference interface it replaces (paths relative to that repository).
+ * Plain C types only: pointers, sizes, status codes.  Nothing aborts; every
+ * call returns TMQ_OK or a negative status and records a message that
+ * tmq_last_error() returns (per host thread).
+ *
+ * Arithmetic contract (identical to the reference's --fpga-* CPU path):
+ *   x_scale = max|x|/32767 (1 if max|x| < 1e-10), xq = (int16)roundf(x/x_scale)
+ *   Q5_0/Q4_K/Q6_K: w = clamp16(roundf(E * row_inv)), row_inv = 32767/max_row|E|
+ *                   acc = sum w*xq (int64), y = (float)((double)acc*x_scale/row_inv)
+ *   Q8_0:           deq = (q8 * cs) >> 8 with cs the UQ8.8 block/row scale,
+ *                   per-64-column-tile int64 partials folded in double, in order.
+ * The int64 partials and the fp32 outputs are bit-identical to the reference.
+ */
+#ifndef TMQ_H
+#define TMQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define TMQ_OK 0
+#define TMQ_ERR_ARG (-1)       /* null pointer, bad type, unsupported shape   */
+#define TMQ_ERR_HIP (-2)       /* HIP runtime error (message has the detail)  */
+#define TMQ_ERR_NONFINITE (-3) /* an fp16 block scale is Inf or NaN           */
+#define TMQ_ERR_NOMEM (-4)     /* device allocation failed                    */
+#define TMQ_ERR_DESC (-5)      /* malformed descriptor / chain                */
+#define TMQ_ERR_NODEV (-6)     /* no usable gfx950 device                     */
+
+/* ggml tensor types, same codes as sim/tmac_gguf.cpp:154-159 and the PhaseB
+ * DESC_TYPE_* constants of sim/fpga_sim.hpp:1272-1279 */
+#define TMQ_TYPE_Q5_0 6
+#define TMQ_TYPE_Q8_0 8
+#define TMQ_TYPE_Q4_K 12
+#define TMQ_TYPE_Q6_K 14
+#define TMQ_TYPE_CPU_OP 15
+
+typedef struct tmq_ctx tmq_ctx;
+typedef struct tmq_tensor tmq_tensor;
+typedef struct tmq_chain tmq_chain;
+
+/* Last error message of the calling host thread ("" if none). */
+const char* tmq_last_error(void);
+
+/* Library version string. */
+const char* tmq_version(void);
+
+/* ---- context ---------------------------------------------------------
+ * One context per device (and per host thread that issues work).  Owns a
+ * non-blocking HIP stream at default priority.  Replaces the accelerator
+ * singleton fpga_sim::accel() (sim/fpga_sim.hpp:431-434) and its
+ * register/DDR model. */
+int tmq_open(int device, tmq_ctx** out);
+int tmq_close(tmq_ctx* ctx);
+/* hipStream_t of the context, as void* */
+void* tmq_stream(tmq_ctx* ctx);
+int tmq_sync(tmq_ctx* ctx);
+
+/* ---- tensors ---------------------------------------------------------
+ * Upload one ggml tensor (rows = ne[1] outputs, cols = ne[0] inputs; the
+ * Tensor of sim/tmac_gguf.cpp:163-169 as filled by load_tmac :1894-1947).
+ * `data` holds rows*cols/QK ggml blocks, row-major.  The bytes are repacked
+ * into a row-interleaved device layout and the per-row normaliser (row_inv;
+ * Q8_0: row_scale) is computed once here, on the device, instead of on every
+ * call as matmul_fpga_* do (sim/tmac_gguf.cpp:1242-1263 etc.).  For Q8_0,
+ * `row_max_abs` may carry the `<name>_row_max_abs` aux tensor
+ * (sim/matmul_q8.cpp:24-30); NULL computes it from the weights (the two are
+ * identical, scripts/extract_tmac.py:231-259).  Requires cols % QK == 0
+ * (QK = 32 for Q8_0/Q5_0, 256 for K-quants) and, for Q8_0, cols <= 16384.
+ * Returns TMQ_ERR_NONFINITE if any fp16 scale is Inf/NaN. */
+int tmq_tensor_upload(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols,
+                      const void* data, uint64_t n_bytes, const float* row_max_abs,
+                      tmq_tensor** out);
+/* Same, from device memory (ggml bytes already resident in HBM). */
+int tmq_tensor_upload_dev(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols,
+                          const void* data_dev, uint64_t n_bytes, const float* row_max_abs_dev,
+                          tmq_tensor** out);
+int tmq_tensor_free(tmq_tensor* t);
+/* type/rows/cols and ggml weight bytes of an uploaded tensor */
+int tmq_tensor_info(const tmq_tensor* t, uint32_t* type, uint64_t* rows, uint64_t* cols,
+                    uint64_t* weight_bytes);
+/* Per-row normaliser as computed at upload: row_inv (Q5_0/K-quants) or
+ * row_scale (Q8_0); host array of `rows` floats. */
+int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out);
+
+/* ---- GEMV (boundary 1) -------------------------------------------------
+ * Drop-in for the --fpga-* dispatch of `matmul` (sim/tmac_gguf.cpp:473-493):
+ * matmul_fpga_q8 (:948, logits via q8_logits_matmul_with_tensor,
+ * sim/matmul_q8.cpp:22), matmul_fpga_q5_0 (:1221), matmul_fpga_q4_k (:1097),
+ * matmul_fpga_q6_k (:1367).  Host x[cols] in, host y[rows] overwritten,
+ * synchronous.  rows/cols must equal the tensor's. */
+int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int rows, int cols);
+
+/* Device-pointer, stream-ordered form of tmq_matmul: x_dev fp32[cols],
+ * y_dev fp32[rows] (may be NULL), acc_dev optional int64 partials: per row
+ * (Q5_0/K-quants) or per row and 64-column tile, [rows][ceil(cols/64)]
+ * (Q8_0, the tile results of sim/fpga_sim.hpp:466-491). */
+int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev,
+                 int64_t* acc_dev);
+
+/* Host form returning the integer partials (layout as acc_dev above) and
+ * x_scale; used by parity tests. */
+int tmq_gemv_partials(tmq_ctx* ctx, const tmq_tensor* t, const float* x, int64_t* acc,
+                      uint64_t acc_len, float* x_scale);
+
+/* ---- tile primitives (boundary 2) ----------------------------------------
+ * Mirror the fpga_sim tile calls, executed on the GPU; host pointers,
+ * synchronous.  Same accumulate/overwrite behaviour as the reference. */
+/* axi_vecmul_tile_q8 (sim/fpga_sim.hpp:466): q8_W 64x64 int8 column-major
+ * [k][n], cs u16[128] UQ8.8 at [n*2+k/32], vec int16[64]; result int64[64]
+ * overwritten. */
+int tmq_vecmul_tile_q8(tmq_ctx* ctx, const uint8_t* q8_W, const uint16_t* cs,
+                       const int16_t* vec, int64_t* result);
+/* axi_vecmul_tile_q5_0_8x896_axilite (sim/fpga_sim.hpp:1004): 224 blocks
+ * (8 rows x 896), act int16[896], row_inv[8]; result[row_base+i] += acc_i. */
+int tmq_vecmul_tile_q5_0_8x896(tmq_ctx* ctx, const uint8_t* blocks, const int16_t* act,
+                               const float* row_inv, int64_t* result, int row_base);
+/* axi_vecmul_tile_q6_k_axilite (sim/fpga_sim.hpp:1058) and
+ * axi_vecmul_tile_q4k_axilite (sim/fpga_sim.hpp:821): nblocks one-row blocks,
+ * act int16[ncols] (ncols <= 256 columns of each block are used), row_inv
+ * indexed by absolute row; result[row_base+bi] += acc (rows < 896 only). */
+int tmq_vecmul_tile_q6_k(tmq_ctx* ctx, const uint8_t* blocks, int nblocks, const int16_t* act,
+                         int ncols, const float* row_inv, int64_t* result, int row_base);
+int tmq_vecmul_tile_q4k(tmq_ctx* ctx, const uint8_t* blocks, int nblocks, const int16_t* act,
+                        int ncols, const float* row_inv, int64_t* result, int row_base);
+
+/* ---- descriptor chains (boundary 3) ---------------------------------------
+ * Replay of a PhaseB descriptor chain held in a byte arena
+ * (struct PhaseBDescriptor, sim/fpga_sim.hpp:1254-1270; replay semantics of
+ * phaseb_run_descriptor, sim/tmac_gguf.cpp:761-831).  `arena` holds the
+ * reference DDR arena from offset `arena_base` (descriptor addresses are
+ * arena offsets).  Every matmul descriptor of the chain starting at
+ * `head_off` runs in one kernel launch; its int64 row results are written
+ * into the arena at result_addr, as the hardware would, and its row count
+ * into rows_out[i] (up to max_desc entries).  Returns the number of
+ * descriptors walked, or a negative status. */
+int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t arena_base,
+                   uint32_t head_off, uint32_t* rows_out, int max_desc);
+
+/* Device-resident chain over uploaded tensors: the GPU equivalent of a
+ * descriptor chain built by phaseb_add_descriptor (sim/tmac_gguf.cpp:533-574).
+ * num_tiles/tile_res_rows/num_col_groups keep the PhaseB meaning: output rows
+ * = num_tiles*tile_res_rows (Q5_0, Q8_0) or (num_tiles/num_col_groups)*
+ * tile_res_rows (Q4_K, Q6_K), and must match the tensor.  All descriptors run
+ * in one kernel launch (plus one activation-quantisation launch). */
+typedef struct {
+    const tmq_tensor* weight;
+    const float* x_dev;   /* fp32 activation, device */
+    float* y_dev;         /* fp32 output rows, device (may be NULL) */
+    int64_t* acc_dev;     /* int64 partials, device (may be NULL) */
+    uint16_t num_tiles;
+    uint8_t tile_res_rows;
+    uint8_t num_col_groups;
+} tmq_desc;
+
+int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out);
+/* tmq_chain_run = tmq_chain_prepare (quantise the chain's activations, one
+ * launch) + tmq_chain_launch (all matmul descriptors, one launch).  The two
+ * halves are exposed so a caller can re-run the matmuls on activations that
+ * have not changed. */
+int tmq_chain_run(tmq_ctx* ctx, tmq_chain* chain);
+int tmq_chain_prepare(tmq_ctx* ctx, tmq_chain* chain);
+int tmq_chain_launch(tmq_ctx* ctx, tmq_chain* chain);
+int tmq_chain_free(tmq_chain* chain);
+/* total ggml weight bytes streamed by one run of the chain */
+uint64_t tmq_chain_weight_bytes(const tmq_chain* chain);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TMQ_H */

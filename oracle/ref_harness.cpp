@@ -1,0 +1,109 @@
+// ref_harness.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// Compiles the reference's own simulation engine (sim/tmac_gguf.cpp, which
+// pulls in sim/fpga_sim.hpp) in place from the reference tree, with its
+// main() renamed, and exposes the file-static functions the quantized-GEMV
+// path is made of through extern "C" wrappers.  Used in this container only,
+// to cross-check the CPU restatement (tmq_oracle.c) and to write the golden
+// vectors under tests/golden/.  No reference source is copied here: the
+// #include below reads it from the reference tree at build time.
+#define main tmac_ref_main
+#include "tmac_gguf.cpp"
+#undef main
+
+#include <cstdlib>
+
+static Tensor ref_make_tensor(uint32_t type, uint64_t rows, uint64_t cols,
+                              const uint8_t* data, uint64_t n_bytes) {
+    Tensor t;
+    memset(&t, 0, sizeof(t));
+    snprintf(t.name, sizeof(t.name), "harness");
+    t.rows = rows;
+    t.cols = cols;
+    t.type = type;
+    t.n_bytes = n_bytes;
+    t.data = const_cast<uint8_t*>(data);
+    return t;
+}
+
+extern "C" {
+
+float ref_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
+float ref_read_f16(const uint8_t* p) { return fpga_sim::read_f16(p); }
+
+void ref_dequant_q4k_block_to_float(const uint8_t* blk, float* out) {
+    fpga_sim::dequant_q4k_block_to_float(blk, out);
+}
+
+// matmul_fpga_{q8,q5_0,q4_k,q6_k} (sim/tmac_gguf.cpp:948,1221,1097,1367)
+int ref_matmul(uint32_t type, const uint8_t* data, uint64_t n_bytes, int rows, int cols,
+               const float* x, float* y, const float* row_max_abs) {
+    Tensor t = ref_make_tensor(type, (uint64_t)rows, (uint64_t)cols, data, n_bytes);
+    switch (type) {
+    case TENSOR_Q8_0: matmul_fpga_q8(&t, x, y, rows, cols, row_max_abs); return 0;
+    case TENSOR_Q5_0: matmul_fpga_q5_0(&t, x, y, rows, cols); return 0;
+    case TENSOR_Q4_K: matmul_fpga_q4_k(&t, x, y, rows, cols); return 0;
+    case TENSOR_Q6_K: matmul_fpga_q6_k(&t, x, y, rows, cols); return 0;
+    default: return -1;
+    }
+}
+
+// The no-flag FP32 path of `matmul` (sim/tmac_gguf.cpp:488-492)
+void ref_matmul_fp32(uint32_t type, const uint8_t* data, uint64_t n_bytes, int rows, int cols,
+                     const float* x, float* y) {
+    Tensor t = ref_make_tensor(type, (uint64_t)rows, (uint64_t)cols, data, n_bytes);
+    bool saved = g_use_fpga;
+    g_use_fpga = false;
+    matmul(&t, x, y, rows, cols);
+    g_use_fpga = saved;
+}
+
+// fpga_sim tile primitives
+void ref_tile_q8(const uint8_t* q8_W, const uint16_t* cs, const int16_t* vec, int64_t* result) {
+    fpga_sim::axi_vecmul_tile_q8(q8_W, cs, vec, result);
+}
+void ref_tile_q5_0_8x896(const uint8_t* blocks, const int16_t* act, const float* row_inv,
+                         int64_t* result, int row_base) {
+    fpga_sim::axi_vecmul_tile_q5_0_8x896_axilite(blocks, act, row_inv, result, row_base);
+}
+void ref_tile_q6_k(const uint8_t* blocks, int nblocks, const int16_t* act, int ncols,
+                   const float* row_inv, int64_t* result, int row_base) {
+    fpga_sim::axi_vecmul_tile_q6_k_axilite(blocks, nblocks, act, ncols, row_inv, result, row_base);
+}
+void ref_tile_q4_k(const uint8_t* blocks, int nblocks, const int16_t* act, int ncols,
+                   const float* row_inv, int64_t* result, int row_base) {
+    fpga_sim::axi_vecmul_tile_q4k_axilite(blocks, nblocks, act, ncols, row_inv, result, row_base);
+}
+void ref_tile_q5_0_4x896(const uint8_t* blocks56, const int16_t* act, const float* row_norm,
+                         int64_t* result, int row_base) {
+    fpga_sim::axi_vecmul_tile_q5_0_4x896_axilite(blocks56, act, row_norm, result, row_base);
+}
+// Q4_K 16-block constant KAT entry (sim/fpga_sim.hpp:844-855)
+void ref_tile_q4k_16(const uint8_t* blocks, const int16_t* vec, int64_t* result) {
+    fpga_sim::axi_vecmul_tile_q4k_axilite(blocks, vec, result);
+}
+
+// PhaseB descriptor chain (sim/tmac_gguf.cpp:513-880).  begin() turns on
+// descriptor building inside the matmul_fpga_* calls that follow.
+int ref_phaseb_begin(void) {
+    if (!g_ddr) {
+        g_ddr = (uint8_t*)calloc(DDR_SIZE, 1);
+        if (!g_ddr) return -1;
+    }
+    phaseb_init();
+    g_fpga_phaseb = true;
+    return 0;
+}
+void ref_phaseb_end(void) { g_fpga_phaseb = false; }
+uint32_t ref_phaseb_head(void) { return g_phaseb.head; }
+uint32_t ref_phaseb_next_off(void) { return g_phaseb.next_off; }
+int ref_phaseb_count(void) { return (int)g_phaseb.slots.size(); }
+const uint8_t* ref_ddr(void) { return g_ddr; }
+int ref_phaseb_run(uint32_t desc_off, int64_t* acc) { return phaseb_run_descriptor(desc_off, acc); }
+uint32_t ref_phaseb_add_descriptor(uint32_t w, uint32_t a, uint32_t r, uint16_t nt, uint16_t tb,
+                                   uint8_t type, uint8_t trr, uint8_t flags, uint16_t atb,
+                                   uint8_t ncg) {
+    return phaseb_add_descriptor(w, a, r, nt, tb, type, trr, flags, atb, ncg);
+}
+
+}  // extern "C"

@@ -1,0 +1,200 @@
+"""GPU parity: libtmq.so on gfx950 vs the CPU oracle and the golden vectors.
+
+Bar: bit-exact int64 partials (per row, per Q8 tile) and bit-exact fp32
+outputs (the north-star tolerance is 1e-5 relative; exactness is met).
+Everything goes through the C ABI (ctypes).
+"""
+import numpy as np
+import pytest
+from conftest import load_golden
+from oracle import Q4_K, Q5_0, Q6_K, Q8_0
+from tmq import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.asarray(a, dtype=np.float32).view(np.uint32)
+
+
+def report(name, got, exp):
+    bad = np.flatnonzero(got != exp)
+    return f"{name}: {bad.size} mismatches, first at {bad[:5]}"
+
+
+SHAPES = [
+    (Q5_0, 896, 896), (Q5_0, 4864, 896), (Q5_0, 128, 896), (Q5_0, 100, 896),
+    (Q4_K, 896, 4864), (Q6_K, 896, 4864), (Q4_K, 40, 512), (Q6_K, 72, 768),
+    (Q8_0, 128, 896), (Q8_0, 1000, 896), (Q8_0, 64, 4864), (Q8_0, 8, 96),
+]
+
+
+@pytest.mark.parametrize("qt,rows,cols", SHAPES)
+def test_gemv_bitexact(ctx, oracle, qt, rows, cols):
+    print(f"[gemv] type={qt} {rows}x{cols}", flush=True)
+    w = synth.gen_weights(qt, rows, cols, 500 + rows)
+    x = synth.gen_x(cols, 600 + cols)
+    t = ctx.upload(qt, rows, cols, w)
+    y = ctx.matmul(t, x)
+    ye = oracle.matmul(qt, w, x, rows, cols)
+    assert np.array_equal(bits(y), bits(ye)), report("y", bits(y), bits(ye))
+    acc, xs = ctx.partials(t, x)
+    xq, xse = oracle.quantize_act(x)
+    assert xs == xse
+    if qt == Q8_0:
+        rn = t.row_norm()
+        rse = oracle.q8_row_scale(oracle.row_max_abs_q8(w, rows, cols))
+        assert np.array_equal(bits(rn), bits(rse))
+        P = oracle.tiles_q8(w, rows, cols, xq, rse)
+        assert np.array_equal(acc, P), report("tiles", acc, P)
+    else:
+        ri = oracle.row_inv(qt, w, rows, cols)
+        assert np.array_equal(bits(t.row_norm()), bits(ri))
+        ae = oracle.acc(qt, w, rows, cols, xq, ri)
+        assert np.array_equal(acc, ae), report("acc", acc, ae)
+    t.free()
+
+
+def test_q8_logits_full_size(ctx, oracle):
+    """151936 x 896 Q8_0 logits matvec, with and without
+    the row_max_abs aux tensor."""
+    rows, cols = 151936, 896
+    print("[gemv] Q8_0 logits 151936x896", flush=True)
+    w = synth.gen_weights(Q8_0, rows, cols, 1)
+    x = synth.gen_x(cols, 2)
+    ye = oracle.matmul(Q8_0, w, x, rows, cols)
+    t = ctx.upload(Q8_0, rows, cols, w)
+    y = ctx.matmul(t, x)
+    assert np.array_equal(bits(y), bits(ye)), report("y", bits(y), bits(ye))
+    t.free()
+    aux = oracle.row_max_abs_q8(w, rows, cols)
+    t2 = ctx.upload(Q8_0, rows, cols, w, row_max_abs=aux)
+    assert np.array_equal(bits(ctx.matmul(t2, x)), bits(ye))
+    t2.free()
+
+
+@pytest.mark.parametrize("name", ["q5_0", "q8_0", "q8_0_c64", "q4_k", "q6_k"])
+def test_golden_matmul(ctx, name):
+    g = load_golden(f"matmul_{name}.npz")
+    qt, rows, cols = int(g["qtype"]), int(g["rows"]), int(g["cols"])
+    print(f"[golden] {name}", flush=True)
+    t = ctx.upload(qt, rows, cols, g["w"])
+    assert np.array_equal(bits(ctx.matmul(t, g["x"])), bits(g["y"]))
+    t.free()
+    if qt == Q8_0:
+        t = ctx.upload(qt, rows, cols, g["w"], row_max_abs=g["aux"])
+        assert np.array_equal(bits(ctx.matmul(t, g["x"])), bits(g["y_aux"]))
+        t.free()
+
+
+def test_golden_edges(ctx):
+    g = load_golden("edge_q5_0.npz")
+    t = ctx.upload(Q5_0, 8, 896, g["w"])
+    assert np.array_equal(bits(ctx.matmul(t, g["x0"])), bits(g["y0"]))
+    assert np.array_equal(bits(ctx.matmul(t, g["xs"])), bits(g["ys"]))
+    t.free()
+
+
+def test_golden_tiles(ctx):
+    g = load_golden("tiles.npz")
+    print("[tiles]", flush=True)
+    assert np.array_equal(ctx.tile_q8(g["W"], g["cs"], g["vec"]), g["tq8"])
+    r5 = g["res5_in"].copy()
+    ctx.tile_q5_0_8x896(g["b5"], g["act896"], g["ri8"], r5, 8)
+    assert np.array_equal(r5, g["res5"])
+    r6 = np.zeros(896, np.int64)
+    ctx.tile_kquant(Q6_K, g["b6"], 32, g["act256"], 256, g["ri896"], r6, 864)
+    assert np.array_equal(r6, g["res6"])
+    r4 = np.zeros(896, np.int64)
+    ctx.tile_kquant(Q4_K, g["b4"], 56, g["act256"], 200, g["ri896"], r4, 840)
+    assert np.array_equal(r4, g["res4"])
+
+
+def test_tiles_vs_oracle_clamp(ctx, oracle):
+    """External row_inv large enough to saturate: the clamp path."""
+    rng = np.random.Generator(np.random.PCG64(5))
+    b5 = synth.gen_weights(Q5_0, 8, 896, 9)
+    act = rng.integers(-32767, 32768, size=896, dtype=np.int16)
+    ri = (rng.random(8, dtype=np.float32) * np.float32(1e7)).astype(np.float32)
+    a, b = np.zeros(16, np.int64), np.zeros(16, np.int64)
+    ctx.tile_q5_0_8x896(b5, act, ri, a, 3)
+    oracle.tile_q5_0_8x896(b5, act, ri, b, 3)
+    assert np.array_equal(a, b)
+    for qt in (Q6_K, Q4_K):
+        blocks = synth.gen_weights(qt, 40, 256, 8)
+        act256 = rng.integers(-32767, 32768, size=256, dtype=np.int16)
+        ri1 = (rng.random(1024, dtype=np.float32) * np.float32(5e5)).astype(np.float32)
+        a, b = np.zeros(896, np.int64), np.zeros(896, np.int64)
+        ctx.tile_kquant(qt, blocks, 40, act256, 256, ri1, a, 870)
+        oracle.tile_kquant(qt, blocks, 40, act256, 256, ri1, b, 870)
+        assert np.array_equal(a, b)
+
+
+def test_golden_phaseb(ctx):
+    g = load_golden("phaseb.npz")
+    arena = g["arena"].copy()
+    base, head = int(g["base"]), int(g["head"])
+    print("[phaseb]", flush=True)
+    n, rows = ctx.phaseb_run(arena, base, head)
+    assert n == len(g["rows"]) and list(rows) == list(g["rows"])
+    # results written at each descriptor's result_addr
+    off, k, got = head, 0, []
+    while off:
+        d = arena[off - base: off - base + 32]
+        ra = int(d[12:16].view(np.uint32)[0])
+        got.append(arena[ra - base: ra - base + 8 * int(rows[k])].view(np.int64))
+        off = int(d[0:4].view(np.uint32)[0])
+        k += 1
+    assert np.array_equal(np.concatenate(got), g["acc"])
+
+
+def test_chain_matches_single_gemvs(ctx, oracle):
+    """A device chain (one launch) over mixed formats equals per-GEMV results."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda:0")
+    specs = [(Q5_0, 896, 896, 224, 4, 1), (Q5_0, 4864, 896, 1216, 4, 1), (Q8_0, 128, 896, 2, 64, 14),
+             (Q4_K, 896, 4864, 304, 56, 19), (Q6_K, 896, 4864, 532, 32, 19)]
+    xa = synth.gen_x(896, 1)
+    xb = synth.gen_x(4864, 2)
+    xa_d = torch.from_numpy(xa).to(dev)
+    xb_d = torch.from_numpy(xb).to(dev)
+    descs, outs, ws, ts = [], [], [], []
+    for i, (qt, rows, cols, nt, tr, ncg) in enumerate(specs):
+        w = synth.gen_weights(qt, rows, cols, 70 + i)
+        t = ctx.upload(qt, rows, cols, w)
+        y = torch.zeros(rows, dtype=torch.float32, device=dev)
+        x = xa_d if cols == 896 else xb_d
+        descs.append((t, x.data_ptr(), y.data_ptr(), None, nt, tr, ncg))
+        outs.append(y)
+        ws.append(w)
+        ts.append(t)
+    print("[chain] 5 descriptors", flush=True)
+    ch = ctx.chain(descs)
+    ch.run()
+    ctx.sync()
+    for (qt, rows, cols, *_), w, y in zip(specs, ws, outs):
+        ye = oracle.matmul(qt, w, xa if cols == 896 else xb, rows, cols)
+        assert np.array_equal(bits(y.cpu().numpy()), bits(ye))
+    ch.free()
+    for t in ts:
+        t.free()
+
+
+def test_error_paths(ctx):
+    import tmq
+    w = synth.gen_weights(Q5_0, 8, 896, 1)
+    with pytest.raises(tmq.TmqError) as e:
+        ctx.upload(Q5_0, 8, 900, w)          # cols not a multiple of 32
+    assert e.value.code == -1
+    with pytest.raises(tmq.TmqError) as e:
+        ctx.upload(Q5_0, 8, 896, w[:-1])     # short buffer
+    assert e.value.code == -1
+    bad = w.copy()
+    bad[22 * 5: 22 * 5 + 2] = np.array([np.float16(np.inf)], np.float16).view(np.uint8)
+    with pytest.raises(tmq.TmqError) as e:
+        ctx.upload(Q5_0, 8, 896, bad)         # Inf scale
+    assert e.value.code == -3
+    t = ctx.upload(Q5_0, 8, 896, w)
+    with pytest.raises(tmq.TmqError):
+        tmq._check(tmq.lib().tmq_matmul(ctx.handle, t.handle, None, None, 8, 896))
+    t.free()

@@ -1,0 +1,799 @@
+// tmq_api.hip -- host runtime behind include/tmq.h.
+//
+// Owns contexts (device + stream + scratch), uploaded tensors (planes +
+// per-row normalisers), descriptor chains, and the PhaseB arena replay.
+// Nothing here computes on the CPU: every numeric result comes from the
+// kernels in tmq_kernels.hip.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/tmq.h"
+#include "tmq_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return fail(TMQ_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));   \
+    } while (0)
+
+#define LAUNCH_TRY(expr)                                                                \
+    do {                                                                                \
+        int e_ = (expr);                                                                \
+        if (e_ != 0)                                                                    \
+            return fail(TMQ_ERR_HIP, "%s: %s", #expr, hipGetErrorString((hipError_t)e_)); \
+    } while (0)
+
+int qk_of(uint32_t type) {
+    switch (type) {
+    case TMQ_TYPE_Q8_0: case TMQ_TYPE_Q5_0: return 32;
+    case TMQ_TYPE_Q4_K: case TMQ_TYPE_Q6_K: return 256;
+    default: return 0;
+    }
+}
+int block_bytes(uint32_t type) {
+    switch (type) {
+    case TMQ_TYPE_Q8_0: return 34;
+    case TMQ_TYPE_Q5_0: return 22;
+    case TMQ_TYPE_Q4_K: return 144;
+    case TMQ_TYPE_Q6_K: return 210;
+    default: return 0;
+    }
+}
+
+// growable device buffer
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    int ensure(size_t n) {
+        if (n <= cap) return 0;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        hipError_t e = hipMalloc(&p, n);
+        if (e != hipSuccess) return fail(TMQ_ERR_NOMEM, "hipMalloc(%zu): %s", n, hipGetErrorString(e));
+        cap = n;
+        return 0;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+}  // namespace
+
+struct tmq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    DevBuf x, y, act, acc, misc, works, gmap;
+};
+
+struct tmq_tensor {
+    tmq_ctx* ctx = nullptr;
+    TmqTensorDev dev{};
+    void* alloc = nullptr;  // planes + row_inv + row_scale
+    uint64_t weight_bytes = 0;
+};
+
+struct tmq_chain {
+    tmq_ctx* ctx = nullptr;
+    std::vector<TmqWork> works;
+    TmqActJobs jobs{};
+    void* works_dev = nullptr;
+    void* gmap_dev = nullptr;
+    void* act_dev = nullptr;
+    int total_groups = 0;
+    uint64_t weight_bytes = 0;
+};
+
+namespace {
+
+int set_device(tmq_ctx* ctx) {
+    HIP_TRY(hipSetDevice(ctx->device));
+    return 0;
+}
+
+int groups_of(const TmqTensorDev& t) {
+    int g64 = t.rows_pad / TMQ_ROWS_PER_GROUP;
+    if (t.type == TMQ_TYPE_Q8_0) return (g64 + TMQ_WAVES - 1) / TMQ_WAVES;
+    return g64;
+}
+
+// Allocate planes + normalisers for a rows x cols tensor (zero filled).
+int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_tensor** out) {
+    const int qk = qk_of(type);
+    if (!qk) return fail(TMQ_ERR_ARG, "unsupported tensor type %u", type);
+    if (rows == 0 || cols == 0 || cols % qk)
+        return fail(TMQ_ERR_ARG, "shape %llux%llu invalid for type %u (cols %% %d)",
+                    (unsigned long long)rows, (unsigned long long)cols, type, qk);
+    if (rows > (1u << 30) || cols > (1u << 20))
+        return fail(TMQ_ERR_ARG, "shape %llux%llu too large", (unsigned long long)rows,
+                    (unsigned long long)cols);
+    if (type == TMQ_TYPE_Q8_0 && cols > 64 * TMQ_Q8_MAX_TILES)
+        return fail(TMQ_ERR_ARG, "Q8_0 cols %llu > %d", (unsigned long long)cols, 64 * TMQ_Q8_MAX_TILES);
+    tmq_tensor* t = new tmq_tensor();
+    t->ctx = ctx;
+    TmqTensorDev& d = t->dev;
+    d.type = (int)type;
+    d.rows = (int)rows;
+    d.cols = (int)cols;
+    d.rows_pad = (int)((rows + 63) / 64 * 64);
+    d.nb = (int)(cols / qk);
+    const size_t R = d.rows_pad, nb = d.nb;
+    size_t sa = 0, sb = 0, sc = 0, sd = 0;
+    switch (type) {
+    case TMQ_TYPE_Q8_0: sa = nb * 2 * R * 16; sd = nb * R * 2; break;
+    case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; break;
+    case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; break;
+    case TMQ_TYPE_Q6_K: sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; break;
+    }
+    auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(R * 4) * 2;
+    hipError_t e = hipMalloc(&t->alloc, total);
+    if (e != hipSuccess) {
+        delete t;
+        return fail(TMQ_ERR_NOMEM, "hipMalloc(%zu) for tensor: %s", total, hipGetErrorString(e));
+    }
+    e = hipMemsetAsync(t->alloc, 0, total, ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(t->alloc);
+        delete t;
+        return fail(TMQ_ERR_HIP, "hipMemsetAsync: %s", hipGetErrorString(e));
+    }
+    uint8_t* p = (uint8_t*)t->alloc;
+    d.pa = p; p += al(sa);
+    d.pb = sb ? p : nullptr; p += al(sb);
+    d.pc = sc ? p : nullptr; p += al(sc);
+    d.pd = sd ? p : nullptr; p += al(sd);
+    d.row_inv = (const float*)p; p += al(R * 4);
+    d.row_scale = (const float*)p;
+    t->weight_bytes = rows * (cols / qk) * (uint64_t)block_bytes(type);
+    *out = t;
+    return 0;
+}
+
+// Upload ggml bytes (host or device) into a freshly allocated tensor and
+// repack.  When `ext_row_inv` is given (host floats, `rows` of them) it is
+// used as the normaliser and the clamp path is enabled; otherwise the
+// normalisers are computed on the device.
+int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
+                  bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
+                  const float* ext_row_inv, tmq_tensor** out) {
+    if (!ctx || !data || !out) return fail(TMQ_ERR_ARG, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    tmq_tensor* t = nullptr;
+    rc = tensor_alloc(ctx, type, rows, cols, &t);
+    if (rc) return rc;
+    if (n_bytes != t->weight_bytes) {
+        tmq_tensor_free(t);
+        return fail(TMQ_ERR_ARG, "n_bytes %llu != %llu for %llux%llu type %u",
+                    (unsigned long long)n_bytes, (unsigned long long)t->weight_bytes,
+                    (unsigned long long)rows, (unsigned long long)cols, type);
+    }
+    const uint8_t* src = (const uint8_t*)data;
+    void* staging = nullptr;
+    auto cleanup = [&](int code) {
+        if (staging) (void)hipFree(staging);
+        if (code) tmq_tensor_free(t);
+        return code;
+    };
+    if (!data_on_device) {
+        hipError_t e = hipMalloc(&staging, n_bytes);
+        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_NOMEM, "staging hipMalloc: %s", hipGetErrorString(e)));
+        e = hipMemcpyAsync(staging, data, n_bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "staging copy: %s", hipGetErrorString(e)));
+        src = (const uint8_t*)staging;
+    }
+    int le = tmq_launch_repack((int)type, src, t->dev, ctx->stream);
+    if (le) return cleanup(fail(TMQ_ERR_HIP, "repack launch: %s", hipGetErrorString((hipError_t)le)));
+    if (ext_row_inv) {
+        t->dev.clamp = 1;
+        std::vector<float> ri(t->dev.rows_pad, 1.0f);
+        memcpy(ri.data(), ext_row_inv, sizeof(float) * rows);
+        hipError_t e = hipMemcpyAsync((void*)t->dev.row_inv, ri.data(), sizeof(float) * ri.size(),
+                                      hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "row_inv copy: %s", hipGetErrorString(e)));
+        cleanup(0);
+        *out = t;
+        return 0;
+    }
+    // aux row_max_abs (Q8_0) -> device
+    const float* aux_dev = nullptr;
+    void* aux_tmp = nullptr;
+    if (aux && type == TMQ_TYPE_Q8_0) {
+        if (aux_on_device) {
+            aux_dev = aux;
+        } else {
+            hipError_t e = hipMalloc(&aux_tmp, sizeof(float) * rows);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(aux_tmp, aux, sizeof(float) * rows, hipMemcpyHostToDevice, ctx->stream);
+            if (e != hipSuccess) {
+                if (aux_tmp) (void)hipFree(aux_tmp);
+                return cleanup(fail(TMQ_ERR_HIP, "aux copy: %s", hipGetErrorString(e)));
+            }
+            aux_dev = (const float*)aux_tmp;
+        }
+    }
+    int rc2 = ctx->misc.ensure(256);
+    if (rc2) return cleanup(rc2);
+    int* bad = (int*)ctx->misc.p;
+    hipError_t e = hipMemsetAsync(bad, 0, sizeof(int), ctx->stream);
+    if (e == hipSuccess) {
+        le = tmq_launch_rowstat(t->dev, aux_dev, (float*)t->dev.row_inv, (float*)t->dev.row_scale,
+                                bad, ctx->stream);
+        if (le) e = (hipError_t)le;
+    }
+    int badh = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&badh, bad, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (aux_tmp) (void)hipFree(aux_tmp);
+    if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "rowstat: %s", hipGetErrorString(e)));
+    if (badh) return cleanup(fail(TMQ_ERR_NONFINITE, "non-finite fp16 block scale in %llux%llu type %u tensor",
+                                  (unsigned long long)rows, (unsigned long long)cols, type));
+    cleanup(0);
+    *out = t;
+    return 0;
+}
+
+// host-side preparation of an int16 activation (x_scale unused -> 1)
+void act_from_int16(const int16_t* xq, int n, std::vector<uint8_t>& buf) {
+    buf.assign(tmq_act_bytes(n), 0);
+    float one = 1.0f;
+    memcpy(buf.data(), &one, 4);
+    memcpy(buf.data() + 4, &n, 4);
+    uint32_t* xh = (uint32_t*)(buf.data() + 16);
+    uint32_t* xl = xh + n / 2;
+    int16_t* q = (int16_t*)(xl + n / 2);
+    for (int k = 0; k < n / 2; k++) {
+        int a = xq[2 * k], c = xq[2 * k + 1];
+        xh[k] = ((uint32_t)(a >> 8) & 0xffffu) | ((uint32_t)(c >> 8) << 16);
+        xl[k] = ((uint32_t)a & 0xffu) | (((uint32_t)c & 0xffu) << 16);
+    }
+    memcpy(q, xq, sizeof(int16_t) * n);
+}
+
+TmqWork make_work(const tmq_tensor* t, const uint8_t* act, float* y, int64_t* acc) {
+    TmqWork w{};
+    w.t = t->dev;
+    w.act = act;
+    w.y = y;
+    w.acc = acc;
+    w.first_group = 0;
+    w.ngroups = groups_of(t->dev);
+    return w;
+}
+
+// run a GEMV with an int16 activation given on the host; int64 per-row
+// results returned on the host (tile API and PhaseB replay share this)
+int run_int16(tmq_ctx* ctx, const tmq_tensor* t, const int16_t* xq, std::vector<int64_t>& acc) {
+    std::vector<uint8_t> act;
+    act_from_int16(xq, t->dev.cols, act);
+    int rc = ctx->act.ensure(act.size());
+    if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * (size_t)t->dev.rows);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->act.p, act.data(), act.size(), hipMemcpyHostToDevice, ctx->stream));
+    TmqWork w = make_work(t, (const uint8_t*)ctx->act.p, nullptr, (int64_t*)ctx->acc.p);
+    LAUNCH_TRY(tmq_launch_gemv(w, ctx->stream));
+    acc.resize(t->dev.rows);
+    HIP_TRY(hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc.size(), hipMemcpyDeviceToHost,
+                           ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+inline uint32_t rd32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+}  // namespace
+
+// =========================================================================
+extern "C" {
+
+const char* tmq_last_error(void) { return g_err.c_str(); }
+const char* tmq_version(void) { return "tmq 0.1 (gfx950)"; }
+
+int tmq_open(int device, tmq_ctx** out) {
+    if (!out) return fail(TMQ_ERR_ARG, "null out");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) return fail(TMQ_ERR_NODEV, "no HIP device (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= n) return fail(TMQ_ERR_ARG, "device %d out of range (%d devices)", device, n);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(TMQ_ERR_NODEV, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
+    tmq_ctx* c = new tmq_ctx();
+    c->device = device;
+    e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(TMQ_ERR_HIP, "stream create: %s", hipGetErrorString(e));
+    }
+    *out = c;
+    return 0;
+}
+
+int tmq_close(tmq_ctx* ctx) {
+    if (!ctx) return 0;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (DevBuf* b : {&ctx->x, &ctx->y, &ctx->act, &ctx->acc, &ctx->misc, &ctx->works, &ctx->gmap}) b->release();
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return 0;
+}
+
+void* tmq_stream(tmq_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int tmq_sync(tmq_ctx* ctx) {
+    if (!ctx) return fail(TMQ_ERR_ARG, "null ctx");
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_tensor_upload(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
+                      uint64_t n_bytes, const float* row_max_abs, tmq_tensor** out) {
+    return tensor_create(ctx, type, rows, cols, data, false, n_bytes, row_max_abs, false, nullptr, out);
+}
+
+int tmq_tensor_upload_dev(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols,
+                          const void* data_dev, uint64_t n_bytes, const float* row_max_abs_dev,
+                          tmq_tensor** out) {
+    return tensor_create(ctx, type, rows, cols, data_dev, true, n_bytes, row_max_abs_dev, true, nullptr, out);
+}
+
+int tmq_tensor_free(tmq_tensor* t) {
+    if (!t) return 0;
+    if (t->alloc) {
+        (void)hipSetDevice(t->ctx->device);
+        (void)hipStreamSynchronize(t->ctx->stream);
+        (void)hipFree(t->alloc);
+    }
+    delete t;
+    return 0;
+}
+
+int tmq_tensor_info(const tmq_tensor* t, uint32_t* type, uint64_t* rows, uint64_t* cols,
+                    uint64_t* weight_bytes) {
+    if (!t) return fail(TMQ_ERR_ARG, "null tensor");
+    if (type) *type = (uint32_t)t->dev.type;
+    if (rows) *rows = (uint64_t)t->dev.rows;
+    if (cols) *cols = (uint64_t)t->dev.cols;
+    if (weight_bytes) *weight_bytes = t->weight_bytes;
+    return 0;
+}
+
+int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out) {
+    if (!ctx || !t || !out) return fail(TMQ_ERR_ARG, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const float* src = t->dev.type == TMQ_TYPE_Q8_0 ? t->dev.row_scale : t->dev.row_inv;
+    HIP_TRY(hipMemcpyAsync(out, src, sizeof(float) * t->dev.rows, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev, int64_t* acc_dev) {
+    if (!ctx || !t || !x_dev) return fail(TMQ_ERR_ARG, "null argument");
+    int rc = set_device(ctx);
+    if (!rc) rc = ctx->act.ensure(tmq_act_bytes(t->dev.cols));
+    if (rc) return rc;
+    TmqActJobs jobs{};
+    jobs.count = 1;
+    jobs.j[0].x = x_dev;
+    jobs.j[0].act = (uint8_t*)ctx->act.p;
+    jobs.j[0].n = t->dev.cols;
+    LAUNCH_TRY(tmq_launch_act_prep(jobs, ctx->stream));
+    TmqWork w = make_work(t, (const uint8_t*)ctx->act.p, y_dev, acc_dev);
+    LAUNCH_TRY(tmq_launch_gemv(w, ctx->stream));
+    return 0;
+}
+
+int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int rows, int cols) {
+    if (!ctx || !t || !x || !y) return fail(TMQ_ERR_ARG, "null argument");
+    if (rows != t->dev.rows || cols != t->dev.cols)
+        return fail(TMQ_ERR_ARG, "shape %dx%d does not match tensor %dx%d", rows, cols, t->dev.rows, t->dev.cols);
+    int rc = set_device(ctx);
+    if (!rc) rc = ctx->x.ensure(sizeof(float) * cols);
+    if (!rc) rc = ctx->y.ensure(sizeof(float) * rows);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->x.p, x, sizeof(float) * cols, hipMemcpyHostToDevice, ctx->stream));
+    rc = tmq_gemv_dev(ctx, t, (const float*)ctx->x.p, (float*)ctx->y.p, nullptr);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(y, ctx->y.p, sizeof(float) * rows, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_gemv_partials(tmq_ctx* ctx, const tmq_tensor* t, const float* x, int64_t* acc,
+                      uint64_t acc_len, float* x_scale) {
+    if (!ctx || !t || !x || !acc) return fail(TMQ_ERR_ARG, "null argument");
+    const uint64_t need = t->dev.type == TMQ_TYPE_Q8_0
+                              ? (uint64_t)t->dev.rows * ((t->dev.cols + 63) / 64)
+                              : (uint64_t)t->dev.rows;
+    if (acc_len < need) return fail(TMQ_ERR_ARG, "acc_len %llu < %llu", (unsigned long long)acc_len,
+                                    (unsigned long long)need);
+    int rc = set_device(ctx);
+    if (!rc) rc = ctx->x.ensure(sizeof(float) * t->dev.cols);
+    if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * need);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->x.p, x, sizeof(float) * t->dev.cols, hipMemcpyHostToDevice, ctx->stream));
+    rc = tmq_gemv_dev(ctx, t, (const float*)ctx->x.p, nullptr, (int64_t*)ctx->acc.p);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(acc, ctx->acc.p, sizeof(int64_t) * need, hipMemcpyDeviceToHost, ctx->stream));
+    if (x_scale) HIP_TRY(hipMemcpyAsync(x_scale, ctx->act.p, sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+// ---------------------------------------------------------------- tiles
+int tmq_vecmul_tile_q8(tmq_ctx* ctx, const uint8_t* q8_W, const uint16_t* cs, const int16_t* vec,
+                       int64_t* result) {
+    if (!ctx || !q8_W || !cs || !vec || !result) return fail(TMQ_ERR_ARG, "null argument");
+    int rc = set_device(ctx);
+    if (!rc) rc = ctx->misc.ensure(4096 + 256 + 128 + 512);
+    if (rc) return rc;
+    uint8_t* p = (uint8_t*)ctx->misc.p;
+    HIP_TRY(hipMemcpyAsync(p, q8_W, 4096, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(p + 4096, cs, 256, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(p + 4352, vec, 128, hipMemcpyHostToDevice, ctx->stream));
+    LAUNCH_TRY(tmq_launch_tile_q8(p, (const uint16_t*)(p + 4096), (const int16_t*)(p + 4352),
+                                  (int64_t*)(p + 4480), ctx->stream));
+    HIP_TRY(hipMemcpyAsync(result, p + 4480, 512, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_vecmul_tile_q5_0_8x896(tmq_ctx* ctx, const uint8_t* blocks, const int16_t* act,
+                               const float* row_inv, int64_t* result, int row_base) {
+    if (!ctx || !blocks || !act || !row_inv || !result) return fail(TMQ_ERR_ARG, "null argument");
+    tmq_tensor* t = nullptr;
+    int rc = tensor_create(ctx, TMQ_TYPE_Q5_0, 8, 896, blocks, false, 224 * 22, nullptr, false, row_inv, &t);
+    if (rc) return rc;
+    std::vector<int64_t> acc;
+    rc = run_int16(ctx, t, act, acc);
+    tmq_tensor_free(t);
+    if (rc) return rc;
+    for (int i = 0; i < 8; i++) result[row_base + i] += acc[i];
+    return 0;
+}
+
+static int tile_kquant(tmq_ctx* ctx, uint32_t type, const uint8_t* blocks, int nblocks,
+                       const int16_t* act, int ncols, const float* row_inv, int64_t* result,
+                       int row_base) {
+    if (!ctx || !blocks || !act || !row_inv || !result) return fail(TMQ_ERR_ARG, "null argument");
+    if (nblocks <= 0 || ncols < 0) return fail(TMQ_ERR_ARG, "nblocks %d ncols %d", nblocks, ncols);
+    tmq_tensor* t = nullptr;
+    int rc = tensor_create(ctx, type, (uint64_t)nblocks, 256, blocks, false,
+                           (uint64_t)nblocks * block_bytes(type), nullptr, false, row_inv + row_base, &t);
+    if (rc) return rc;
+    // columns past ncols do not contribute (the reference stops at wi >= ncols)
+    std::vector<int16_t> a(256, 0);
+    for (int i = 0; i < ncols && i < 256; i++) a[i] = act[i];
+    std::vector<int64_t> acc;
+    rc = run_int16(ctx, t, a.data(), acc);
+    tmq_tensor_free(t);
+    if (rc) return rc;
+    for (int bi = 0; bi < nblocks; bi++)
+        if (row_base + bi < 896) result[row_base + bi] += acc[bi];
+    return 0;
+}
+
+int tmq_vecmul_tile_q6_k(tmq_ctx* ctx, const uint8_t* blocks, int nblocks, const int16_t* act,
+                         int ncols, const float* row_inv, int64_t* result, int row_base) {
+    return tile_kquant(ctx, TMQ_TYPE_Q6_K, blocks, nblocks, act, ncols, row_inv, result, row_base);
+}
+
+int tmq_vecmul_tile_q4k(tmq_ctx* ctx, const uint8_t* blocks, int nblocks, const int16_t* act,
+                        int ncols, const float* row_inv, int64_t* result, int row_base) {
+    return tile_kquant(ctx, TMQ_TYPE_Q4_K, blocks, nblocks, act, ncols, row_inv, result, row_base);
+}
+
+// ---------------------------------------------------------------- chains
+int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out) {
+    if (!ctx || !descs || n <= 0 || !out) return fail(TMQ_ERR_ARG, "bad chain arguments");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    tmq_chain* ch = new tmq_chain();
+    ch->ctx = ctx;
+    std::map<const float*, int> xs;  // distinct activations
+    std::vector<int> act_of(n);
+    std::vector<int> ncols_of;
+    for (int i = 0; i < n; i++) {
+        const tmq_desc& d = descs[i];
+        const tmq_tensor* t = d.weight;
+        if (!t || !d.x_dev) {
+            delete ch;
+            return fail(TMQ_ERR_DESC, "descriptor %d: null weight or x", i);
+        }
+        const TmqTensorDev& td = t->dev;
+        long rows;
+        if (td.type == TMQ_TYPE_Q4_K || td.type == TMQ_TYPE_Q6_K) {
+            if (d.num_col_groups == 0 || d.num_tiles % d.num_col_groups || d.num_col_groups * 256 != td.cols) {
+                delete ch;
+                return fail(TMQ_ERR_DESC, "descriptor %d: num_col_groups %d / num_tiles %d inconsistent with cols %d",
+                            i, d.num_col_groups, d.num_tiles, td.cols);
+            }
+            rows = (long)(d.num_tiles / d.num_col_groups) * d.tile_res_rows;
+        } else {
+            rows = (long)d.num_tiles * d.tile_res_rows;
+        }
+        if (rows != td.rows) {
+            delete ch;
+            return fail(TMQ_ERR_DESC, "descriptor %d: tiles give %ld rows, tensor has %d", i, rows, td.rows);
+        }
+        auto it = xs.find(d.x_dev);
+        if (it == xs.end()) {
+            if ((int)xs.size() >= TMQ_MAX_ACT) {
+                delete ch;
+                return fail(TMQ_ERR_DESC, "more than %d distinct activations in one chain", TMQ_MAX_ACT);
+            }
+            int id = (int)xs.size();
+            xs[d.x_dev] = id;
+            ncols_of.push_back(td.cols);
+            act_of[i] = id;
+        } else {
+            act_of[i] = it->second;
+            if (ncols_of[it->second] != td.cols) {
+                delete ch;
+                return fail(TMQ_ERR_DESC, "descriptor %d: activation shared with a different width", i);
+            }
+        }
+    }
+    // activation buffers
+    std::vector<size_t> act_off(xs.size());
+    size_t act_total = 0;
+    for (size_t a = 0; a < xs.size(); a++) {
+        act_off[a] = act_total;
+        act_total += (tmq_act_bytes(ncols_of[a]) + 255) & ~(size_t)255;
+    }
+    hipError_t e = hipMalloc(&ch->act_dev, act_total);
+    if (e != hipSuccess) {
+        delete ch;
+        return fail(TMQ_ERR_NOMEM, "chain act alloc: %s", hipGetErrorString(e));
+    }
+    ch->jobs.count = (int)xs.size();
+    for (auto& kv : xs) {
+        TmqActJob& j = ch->jobs.j[kv.second];
+        j.x = kv.first;
+        j.act = (uint8_t*)ch->act_dev + act_off[kv.second];
+        j.n = ncols_of[kv.second];
+    }
+    // work list
+    std::vector<int32_t> gmap;
+    for (int i = 0; i < n; i++) {
+        const tmq_desc& d = descs[i];
+        TmqWork w = make_work(d.weight, (const uint8_t*)ch->act_dev + act_off[act_of[i]], d.y_dev, d.acc_dev);
+        w.first_group = (int)gmap.size();
+        for (int g = 0; g < w.ngroups; g++) gmap.push_back(i);
+        ch->works.push_back(w);
+        ch->weight_bytes += d.weight->weight_bytes;
+    }
+    ch->total_groups = (int)gmap.size();
+    e = hipMalloc(&ch->works_dev, sizeof(TmqWork) * ch->works.size());
+    if (e == hipSuccess) e = hipMalloc(&ch->gmap_dev, sizeof(int32_t) * gmap.size());
+    if (e == hipSuccess)
+        e = hipMemcpy(ch->works_dev, ch->works.data(), sizeof(TmqWork) * ch->works.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(ch->gmap_dev, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        tmq_chain_free(ch);
+        return fail(TMQ_ERR_NOMEM, "chain alloc: %s", hipGetErrorString(e));
+    }
+    *out = ch;
+    return 0;
+}
+
+int tmq_chain_prepare(tmq_ctx* ctx, tmq_chain* ch) {
+    if (!ctx || !ch) return fail(TMQ_ERR_ARG, "null argument");
+    LAUNCH_TRY(tmq_launch_act_prep(ch->jobs, ctx->stream));
+    return 0;
+}
+
+int tmq_chain_launch(tmq_ctx* ctx, tmq_chain* ch) {
+    if (!ctx || !ch) return fail(TMQ_ERR_ARG, "null argument");
+    LAUNCH_TRY(tmq_launch_chain((const TmqWork*)ch->works_dev, (const int32_t*)ch->gmap_dev,
+                                ch->total_groups, ctx->stream));
+    return 0;
+}
+
+int tmq_chain_run(tmq_ctx* ctx, tmq_chain* ch) {
+    int rc = tmq_chain_prepare(ctx, ch);
+    return rc ? rc : tmq_chain_launch(ctx, ch);
+}
+
+int tmq_chain_free(tmq_chain* ch) {
+    if (!ch) return 0;
+    if (ch->ctx) {
+        (void)hipSetDevice(ch->ctx->device);
+        (void)hipStreamSynchronize(ch->ctx->stream);
+    }
+    if (ch->works_dev) (void)hipFree(ch->works_dev);
+    if (ch->gmap_dev) (void)hipFree(ch->gmap_dev);
+    if (ch->act_dev) (void)hipFree(ch->act_dev);
+    delete ch;
+    return 0;
+}
+
+uint64_t tmq_chain_weight_bytes(const tmq_chain* ch) { return ch ? ch->weight_bytes : 0; }
+
+// ---------------------------------------------------------------- PhaseB
+// Walks the chain on the host (descriptors are 32 bytes each), rebuilds
+// each matmul descriptor's weights as a device tensor and runs all of them
+// in one chain launch; results land in the arena at result_addr.
+int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t arena_base,
+                   uint32_t head_off, uint32_t* rows_out, int max_desc) {
+    if (!ctx || !arena) return fail(TMQ_ERR_ARG, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    auto in_arena = [&](uint64_t off, uint64_t len) {
+        return off >= arena_base && off - arena_base + len <= arena_bytes;
+    };
+    struct Item {
+        tmq_tensor* t;
+        uint32_t result_addr;
+        int nrows;
+        std::vector<uint8_t> act;
+        int kquant_rows_lt896;
+    };
+    std::vector<Item> items;
+    std::vector<uint32_t> rows_list;
+    auto cleanup = [&](int code) {
+        for (Item& it : items) tmq_tensor_free(it.t);
+        return code;
+    };
+    uint32_t off = head_off;
+    int walked = 0;
+    while (off) {
+        if (walked >= (1 << 16)) return cleanup(fail(TMQ_ERR_DESC, "descriptor chain longer than 65536 (cycle?)"));
+        if (!in_arena(off, 32)) return cleanup(fail(TMQ_ERR_DESC, "descriptor at 0x%x outside arena", off));
+        const uint8_t* d = arena + (off - arena_base);
+        const uint32_t next = rd32(d), wa = rd32(d + 4), aa = rd32(d + 8), ra = rd32(d + 12);
+        const int nt = rd16(d + 0x10), tb = rd16(d + 0x12), type = d[0x14], tr = d[0x15];
+        const int cg = d[0x19];
+        int nrows = 0;
+        if (type == TMQ_TYPE_Q5_0) {
+            // sim tile: 8 rows x 896 (224 blocks) + row_inv section; replay
+            // recomputes row_inv per tile (sim/tmac_gguf.cpp:766-777)
+            if (tr != 8 || tb < 224 * 22)
+                return cleanup(fail(TMQ_ERR_DESC, "Q5_0 descriptor at 0x%x: tile_res_rows %d / tile_bytes %d not the 8x896 tile", off, tr, tb));
+            nrows = nt * tr;
+            if (!in_arena(wa, (uint64_t)nt * tb) || !in_arena(aa, 896 * 2) || !in_arena(ra, (uint64_t)nrows * 8))
+                return cleanup(fail(TMQ_ERR_DESC, "Q5_0 descriptor at 0x%x: address out of arena", off));
+            std::vector<uint8_t> w((size_t)nt * 224 * 22);
+            for (int ti = 0; ti < nt; ti++)
+                memcpy(w.data() + (size_t)ti * 224 * 22, arena + (wa - arena_base) + (size_t)ti * tb, 224 * 22);
+            Item it{};
+            int rc2 = tensor_create(ctx, TMQ_TYPE_Q5_0, (uint64_t)nrows, 896, w.data(), false, w.size(),
+                                    nullptr, false, nullptr, &it.t);
+            if (rc2) return cleanup(rc2);
+            it.t->dev.clamp = 1;
+            act_from_int16((const int16_t*)(arena + (aa - arena_base)), 896, it.act);
+            it.result_addr = ra;
+            it.nrows = nrows;
+            it.kquant_rows_lt896 = 0;
+            items.push_back(std::move(it));
+        } else if (type == TMQ_TYPE_Q6_K || type == TMQ_TYPE_Q4_K) {
+            const bool k6 = type == TMQ_TYPE_Q6_K;
+            const int bb = k6 ? 210 : 144, blk_bytes = k6 ? 32 * 210 : 56 * 144;
+            if (cg == 0 || tr == 0 || nt % cg)
+                return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: num_col_groups %d tile_res_rows %d num_tiles %d", off, cg, tr, nt));
+            if (tb < blk_bytes + tr * 4 || tr * bb > blk_bytes)
+                return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: tile_bytes %d too small", off, tb));
+            nrows = (nt / cg) * tr;
+            const int cols = cg * 256;
+            if (!in_arena(wa, (uint64_t)nt * tb) || !in_arena(aa, (uint64_t)cols * 2) || !in_arena(ra, (uint64_t)nrows * 8))
+                return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: address out of arena", off));
+            std::vector<uint8_t> w((size_t)nrows * cg * bb);
+            std::vector<float> ri(nrows, 0.0f);
+            std::vector<char> seen(nrows, 0);
+            for (int ti = 0; ti < nt; ti++) {
+                const int cgi = ti % cg, rg = ti / cg, row0 = rg * tr;
+                const uint8_t* tile = arena + (wa - arena_base) + (size_t)ti * tb;
+                for (int i = 0; i < tr; i++) {
+                    memcpy(w.data() + ((size_t)(row0 + i) * cg + cgi) * bb, tile + (size_t)i * bb, bb);
+                    float v = (float)rd32(tile + blk_bytes + i * 4) / 256.0f;  // UQ24.8 (:791-795)
+                    if (seen[row0 + i] && ri[row0 + i] != v)
+                        return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: row %d has differing row_inv across tiles", off, row0 + i));
+                    ri[row0 + i] = v;
+                    seen[row0 + i] = 1;
+                }
+            }
+            Item it{};
+            int rc2 = tensor_create(ctx, (uint32_t)type, (uint64_t)nrows, (uint64_t)cols, w.data(), false,
+                                    w.size(), nullptr, false, ri.data(), &it.t);
+            if (rc2) return cleanup(rc2);
+            act_from_int16((const int16_t*)(arena + (aa - arena_base)), cols, it.act);
+            it.result_addr = ra;
+            it.nrows = nrows;
+            it.kquant_rows_lt896 = 1;
+            items.push_back(std::move(it));
+        } else {
+            nrows = 0;  // CPU_OP and unsupported types: no matmul rows (:823-829)
+        }
+        rows_list.push_back((uint32_t)nrows);
+        walked++;
+        off = next;
+    }
+    // one launch over all matmul descriptors
+    if (!items.empty()) {
+        size_t act_total = 0, acc_total = 0;
+        std::vector<size_t> aoff, coff;
+        for (Item& it : items) {
+            aoff.push_back(act_total);
+            act_total += (it.act.size() + 255) & ~(size_t)255;
+            coff.push_back(acc_total);
+            acc_total += (size_t)it.t->dev.rows;
+        }
+        rc = ctx->act.ensure(act_total);
+        if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * acc_total);
+        if (rc) return cleanup(rc);
+        std::vector<TmqWork> works;
+        std::vector<int32_t> gmap;
+        for (size_t i = 0; i < items.size(); i++) {
+            hipError_t e = hipMemcpyAsync((uint8_t*)ctx->act.p + aoff[i], items[i].act.data(), items[i].act.size(),
+                                          hipMemcpyHostToDevice, ctx->stream);
+            if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "act copy: %s", hipGetErrorString(e)));
+            TmqWork w = make_work(items[i].t, (const uint8_t*)ctx->act.p + aoff[i], nullptr,
+                                  (int64_t*)ctx->acc.p + coff[i]);
+            w.first_group = (int)gmap.size();
+            for (int g = 0; g < w.ngroups; g++) gmap.push_back((int32_t)i);
+            works.push_back(w);
+        }
+        rc = ctx->works.ensure(sizeof(TmqWork) * works.size());
+        if (!rc) rc = ctx->gmap.ensure(sizeof(int32_t) * gmap.size());
+        if (rc) return cleanup(rc);
+        hipError_t e = hipMemcpyAsync(ctx->works.p, works.data(), sizeof(TmqWork) * works.size(),
+                                      hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(ctx->gmap.p, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "chain upload: %s", hipGetErrorString(e)));
+        int le = tmq_launch_chain((const TmqWork*)ctx->works.p, (const int32_t*)ctx->gmap.p, (int)gmap.size(), ctx->stream);
+        if (le) return cleanup(fail(TMQ_ERR_HIP, "chain launch: %s", hipGetErrorString((hipError_t)le)));
+        std::vector<int64_t> acc(acc_total);
+        e = hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc_total, hipMemcpyDeviceToHost, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "chain results: %s", hipGetErrorString(e)));
+        for (size_t i = 0; i < items.size(); i++) {
+            uint8_t* dst = arena + (items[i].result_addr - arena_base);
+            for (int r = 0; r < items[i].nrows; r++) {
+                // K-quant tiles only accumulate rows < 896 (sim/fpga_sim.hpp:1112, :779)
+                int64_t v = (items[i].kquant_rows_lt896 && r >= 896) ? 0 : acc[coff[i] + r];
+                memcpy(dst + (size_t)r * 8, &v, 8);
+            }
+        }
+    }
+    if (rows_out)
+        for (int i = 0; i < (int)rows_list.size() && i < max_desc; i++) rows_out[i] = rows_list[i];
+    cleanup(0);
+    return walked;
+}
+
+}  // extern "C"

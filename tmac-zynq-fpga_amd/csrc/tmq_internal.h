@@ -1,0 +1,81 @@
+// tmq_internal.h -- device data layout shared by the kernels and the host runtime.
+//
+// Weights live in HBM in a row-interleaved "plane" layout built once at
+// upload from the ggml bytes (same byte count, no decoding):
+//
+//   for every block column b (QK weights wide) and every 16-byte chunk c of
+//   a block's field, the chunks of all rows are contiguous:
+//       plane16(p, b, c, C, r) = p + ((b*C + c)*rows_pad + r) * 16
+//   so the 64 lanes of a wave (one row each) read 1 KiB contiguous per load.
+//
+//   Q8_0  A: q    [b][2][r] x16B     D: d [b][r] u16
+//   Q5_0  A: qs   [b][r]    x16B     B: qh [b][r] u32      D: d [b][r] u16
+//   Q4_K  A: qs   [b][8][r] x16B     B: hdr (d,dmin,scales[12]) [b][r] x16B
+//   Q6_K  A: ql   [b][8][r] x16B     B: qh [b][4][r] x16B   C: sc [b][r] x16B
+//         D: d [b][r] u16
+//
+// rows_pad = rows rounded up to 64; padding rows are zero (they compute 0).
+#pragma once
+#include <stdint.h>
+
+#define TMQ_ROWS_PER_GROUP 64
+#define TMQ_WAVES 4
+#define TMQ_WG (64 * TMQ_WAVES)
+#define TMQ_Q8_MAX_TILES 256  // cols <= 16384 for Q8_0
+
+struct TmqTensorDev {
+    int32_t type;
+    int32_t rows, cols, rows_pad;
+    int32_t nb;        // blocks per row: cols/32 (Q8_0, Q5_0) or cols/256 (K-quants)
+    int32_t clamp;     // 1: clamp before rounding (externally supplied row_inv)
+    const uint8_t* pa;
+    const uint8_t* pb;
+    const uint8_t* pc;
+    const uint8_t* pd;
+    const float* row_inv;    // Q5_0/K-quants: row_inv; Q8_0: 1/row_scale (guarded)
+    const float* row_scale;  // Q8_0 only
+};
+
+// Prepared activation, written by act_prep (or by the host for int16 input):
+//   +0  float x_scale   +4 int32 n   +16 u32 XH[n/2]   +16+2n u32 XL[n/2]
+//   +16+4n int16 xq[n]
+// XH/XL hold (xq >> 8, xq & 255) as int16 pairs (elements 2k, 2k+1), so that
+// sum w*xq = 256*sum w*xh + sum w*xl with every partial inside int32.
+static inline uint64_t tmq_act_bytes(int n) { return 16 + (uint64_t)n * 6 + 16; }
+
+struct TmqWork {
+    TmqTensorDev t;
+    const uint8_t* act;
+    float* y;        // may be null
+    int64_t* acc;    // may be null; Q8_0: [rows][ntiles]
+    int32_t first_group;
+    int32_t ngroups;
+};
+
+// Activation-quantisation jobs: one workgroup each, at most TMQ_MAX_ACT per launch.
+#define TMQ_MAX_ACT 16
+struct TmqActJob {
+    const float* x;
+    uint8_t* act;
+    int32_t n;
+    int32_t pad_;
+};
+struct TmqActJobs {
+    int32_t count;
+    int32_t pad_;
+    TmqActJob j[TMQ_MAX_ACT];
+};
+
+// Launchers (tmq_kernels.hip); all asynchronous on `stream`, return a
+// hipError_t value (0 = success).
+struct ihipStream_t;
+typedef struct ihipStream_t* hipStream_t;
+int tmq_launch_act_prep(const TmqActJobs& jobs, hipStream_t s);
+int tmq_launch_repack(int type, const uint8_t* src, const TmqTensorDev& t, hipStream_t s);
+int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux_max_abs, float* row_inv,
+                       float* row_scale, int* bad_flag, hipStream_t s);
+int tmq_launch_gemv(const TmqWork& w, hipStream_t s);
+int tmq_launch_chain(const TmqWork* works_dev, const int32_t* group_work_dev, int total_groups,
+                     hipStream_t s);
+int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
+                       hipStream_t s);

@@ -1,0 +1,249 @@
+"""Python binding of libtmq.so, the MI355X quantized-GEMV library (include/tmq.h).
+
+A thin ctypes layer: every numeric result comes from the HIP kernels.  There
+is no CPU fallback -- if libtmq.so is missing or the device is not a gfx950,
+the calls raise.
+
+    import tmq
+    ctx = tmq.Context(0)
+    t = ctx.upload(tmq.Q5_0, rows, cols, ggml_bytes)
+    y = ctx.matmul(t, x)          # matmul_fpga_q5_0 drop-in
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import synth  # noqa: F401  (re-export)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtmq.so")
+
+Q5_0, Q8_0, Q4_K, Q6_K, CPU_OP = 6, 8, 12, 14, 15
+QK = {Q8_0: 32, Q5_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210}
+
+EXPORTS = [
+    "tmq_last_error", "tmq_version", "tmq_open", "tmq_close", "tmq_stream", "tmq_sync",
+    "tmq_tensor_upload", "tmq_tensor_upload_dev", "tmq_tensor_free", "tmq_tensor_info",
+    "tmq_tensor_row_norm", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_partials",
+    "tmq_vecmul_tile_q8", "tmq_vecmul_tile_q5_0_8x896", "tmq_vecmul_tile_q6_k",
+    "tmq_vecmul_tile_q4k", "tmq_phaseb_run", "tmq_chain_create", "tmq_chain_run",
+    "tmq_chain_prepare", "tmq_chain_launch",
+    "tmq_chain_free", "tmq_chain_weight_bytes",
+]
+
+
+class TmqError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"tmq error {code}: {msg}")
+        self.code = code
+
+
+class Desc(C.Structure):
+    """tmq_desc"""
+    _fields_ = [("weight", C.c_void_p), ("x_dev", C.c_void_p), ("y_dev", C.c_void_p),
+                ("acc_dev", C.c_void_p), ("num_tiles", C.c_uint16),
+                ("tile_res_rows", C.c_uint8), ("num_col_groups", C.c_uint8)]
+
+
+_lib = None
+
+
+def lib(path: str = LIB_PATH):
+    """Load libtmq.so (raises if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() "
+                                f"or `make -C tmac-zynq-fpga_amd`")
+    L = C.CDLL(path)
+    P, I, U32, U64 = C.c_void_p, C.c_int, C.c_uint32, C.c_uint64
+    sig = {
+        "tmq_last_error": (C.c_char_p, []),
+        "tmq_version": (C.c_char_p, []),
+        "tmq_open": (I, [I, C.POINTER(P)]),
+        "tmq_close": (I, [P]),
+        "tmq_stream": (P, [P]),
+        "tmq_sync": (I, [P]),
+        "tmq_tensor_upload": (I, [P, U32, U64, U64, P, U64, P, C.POINTER(P)]),
+        "tmq_tensor_upload_dev": (I, [P, U32, U64, U64, P, U64, P, C.POINTER(P)]),
+        "tmq_tensor_free": (I, [P]),
+        "tmq_tensor_info": (I, [P, P, P, P, P]),
+        "tmq_tensor_row_norm": (I, [P, P, P]),
+        "tmq_matmul": (I, [P, P, P, P, I, I]),
+        "tmq_gemv_dev": (I, [P, P, P, P, P]),
+        "tmq_gemv_partials": (I, [P, P, P, P, U64, P]),
+        "tmq_vecmul_tile_q8": (I, [P, P, P, P, P]),
+        "tmq_vecmul_tile_q5_0_8x896": (I, [P, P, P, P, P, I]),
+        "tmq_vecmul_tile_q6_k": (I, [P, P, I, P, I, P, P, I]),
+        "tmq_vecmul_tile_q4k": (I, [P, P, I, P, I, P, P, I]),
+        "tmq_phaseb_run": (I, [P, P, U64, U32, U32, P, I]),
+        "tmq_chain_create": (I, [P, P, I, C.POINTER(P)]),
+        "tmq_chain_run": (I, [P, P]),
+        "tmq_chain_prepare": (I, [P, P]),
+        "tmq_chain_launch": (I, [P, P]),
+        "tmq_chain_free": (I, [P]),
+        "tmq_chain_weight_bytes": (U64, [P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc < 0:
+        raise TmqError(rc, lib().tmq_last_error().decode())
+    return rc
+
+
+def _p(a):
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Tensor:
+    def __init__(self, ctx: "Context", handle, qtype: int, rows: int, cols: int):
+        self.ctx, self.handle, self.qtype, self.rows, self.cols = ctx, handle, qtype, rows, cols
+        wb = C.c_uint64()
+        _check(lib().tmq_tensor_info(handle, None, None, None, C.byref(wb)))
+        self.weight_bytes = wb.value
+
+    def row_norm(self) -> np.ndarray:
+        out = np.empty(self.rows, dtype=np.float32)
+        _check(lib().tmq_tensor_row_norm(self.ctx.handle, self.handle, _p(out)))
+        return out
+
+    def free(self):
+        if self.handle:
+            lib().tmq_tensor_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Chain:
+    def __init__(self, ctx: "Context", descs):
+        self.ctx = ctx
+        arr = (Desc * len(descs))()
+        self._keep = []
+        for i, d in enumerate(descs):
+            t, x, y, acc, nt, tr, ncg = d
+            self._keep.append(t)
+            arr[i] = Desc(t.handle, x, y, acc, nt, tr, ncg)
+        h = C.c_void_p()
+        _check(lib().tmq_chain_create(ctx.handle, arr, len(descs), C.byref(h)))
+        self.handle = h
+        self.weight_bytes = lib().tmq_chain_weight_bytes(h)
+
+    def run(self):
+        _check(lib().tmq_chain_run(self.ctx.handle, self.handle))
+
+    def prepare(self):
+        _check(lib().tmq_chain_prepare(self.ctx.handle, self.handle))
+
+    def launch(self):
+        _check(lib().tmq_chain_launch(self.ctx.handle, self.handle))
+
+    def free(self):
+        if self.handle:
+            lib().tmq_chain_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        _check(lib().tmq_open(device, C.byref(h)))
+        self.handle = h
+
+    @property
+    def stream(self) -> int:
+        return lib().tmq_stream(self.handle)
+
+    def sync(self):
+        _check(lib().tmq_sync(self.handle))
+
+    def close(self):
+        if self.handle:
+            lib().tmq_close(self.handle)
+            self.handle = None
+
+    # -- tensors ---------------------------------------------------------
+    def upload(self, qtype: int, rows: int, cols: int, data: np.ndarray, row_max_abs=None) -> Tensor:
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        if row_max_abs is not None:
+            row_max_abs = np.ascontiguousarray(row_max_abs, dtype=np.float32)
+        h = C.c_void_p()
+        _check(lib().tmq_tensor_upload(self.handle, qtype, rows, cols, _p(data), data.size,
+                                       _p(row_max_abs), C.byref(h)))
+        return Tensor(self, h, qtype, rows, cols)
+
+    def upload_dev(self, qtype: int, rows: int, cols: int, data_ptr: int, nbytes: int) -> Tensor:
+        h = C.c_void_p()
+        _check(lib().tmq_tensor_upload_dev(self.handle, qtype, rows, cols, data_ptr, nbytes, None,
+                                           C.byref(h)))
+        return Tensor(self, h, qtype, rows, cols)
+
+    # -- GEMV ------------------------------------------------------------
+    def matmul(self, t: Tensor, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(t.rows, dtype=np.float32)
+        _check(lib().tmq_matmul(self.handle, t.handle, _p(x), _p(y), t.rows, t.cols))
+        return y
+
+    def partials(self, t: Tensor, x: np.ndarray):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if t.qtype == Q8_0:
+            acc = np.empty((t.rows, (t.cols + 63) // 64), dtype=np.int64)
+        else:
+            acc = np.empty(t.rows, dtype=np.int64)
+        xs = np.zeros(1, dtype=np.float32)
+        _check(lib().tmq_gemv_partials(self.handle, t.handle, _p(x), _p(acc), acc.size, _p(xs)))
+        return acc, xs[0]
+
+    def gemv_dev(self, t: Tensor, x_ptr: int, y_ptr: int | None, acc_ptr: int | None = None):
+        _check(lib().tmq_gemv_dev(self.handle, t.handle, x_ptr, y_ptr, acc_ptr))
+
+    # -- tiles -----------------------------------------------------------
+    def tile_q8(self, W, cs, vec) -> np.ndarray:
+        out = np.zeros(64, dtype=np.int64)
+        _check(lib().tmq_vecmul_tile_q8(self.handle, _p(W), _p(cs), _p(vec), _p(out)))
+        return out
+
+    def tile_q5_0_8x896(self, blocks, act, row_inv, result, row_base):
+        _check(lib().tmq_vecmul_tile_q5_0_8x896(self.handle, _p(blocks), _p(act), _p(row_inv),
+                                                _p(result), row_base))
+
+    def tile_kquant(self, qtype, blocks, nblocks, act, ncols, row_inv, result, row_base):
+        f = lib().tmq_vecmul_tile_q6_k if qtype == Q6_K else lib().tmq_vecmul_tile_q4k
+        _check(f(self.handle, _p(blocks), nblocks, _p(act), ncols, _p(row_inv), _p(result), row_base))
+
+    # -- chains ----------------------------------------------------------
+    def phaseb_run(self, arena: np.ndarray, arena_base: int, head: int, max_desc: int = 4096):
+        rows = np.zeros(max_desc, dtype=np.uint32)
+        n = _check(lib().tmq_phaseb_run(self.handle, _p(arena), arena.size, arena_base, head,
+                                        _p(rows), max_desc))
+        return n, rows[:n].copy()
+
+    def chain(self, descs) -> Chain:
+        return Chain(self, descs)
