@@ -60,6 +60,13 @@ def lib(path: str = LIB_PATH):
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() "
                                 f"or `make -C tmac-zynq-fpga_amd`")
+    # PyTorch-ROCm ships its own libamdhip64 (same soname, libamdhip64.so.7).
+    # Loading torch first lets libtmq.so bind to that runtime, so a process
+    # that uses both has one HIP runtime (two runtimes cannot share the GPU).
+    try:
+        import torch  # noqa: F401
+    except Exception:
+        pass
     L = C.CDLL(path)
     P, I, U32, U64 = C.c_void_p, C.c_int, C.c_uint32, C.c_uint64
     sig = {
