@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -82,6 +83,10 @@ struct DevBuf {
     }
 };
 
+struct Segment {
+    int type, clamp, gmap_off, ngroups;
+};
+
 }  // namespace
 
 struct tmq_ctx {
@@ -104,7 +109,7 @@ struct tmq_chain {
     void* works_dev = nullptr;
     void* gmap_dev = nullptr;
     void* act_dev = nullptr;
-    int total_groups = 0;
+    std::vector<Segment> segs;
     uint64_t weight_bytes = 0;
 };
 
@@ -302,6 +307,36 @@ int run_int16(tmq_ctx* ctx, const tmq_tensor* t, const int16_t* xq, std::vector<
     HIP_TRY(hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc.size(), hipMemcpyDeviceToHost,
                            ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+// Descriptors of one format (and clamp mode) form a segment that runs as one
+// launch of that format's kernel; `works` is reordered by segment and
+// first_group made relative to the segment's first workgroup.
+void plan_segments(std::vector<TmqWork>& works, std::vector<int32_t>& gmap, std::vector<Segment>& segs) {
+    std::stable_sort(works.begin(), works.end(), [](const TmqWork& a, const TmqWork& b) {
+        return a.t.type != b.t.type ? a.t.type < b.t.type : a.t.clamp < b.t.clamp;
+    });
+    gmap.clear();
+    segs.clear();
+    for (size_t i = 0; i < works.size(); i++) {
+        TmqWork& w = works[i];
+        if (segs.empty() || segs.back().type != w.t.type || segs.back().clamp != w.t.clamp)
+            segs.push_back(Segment{w.t.type, w.t.clamp, (int)gmap.size(), 0});
+        Segment& sg = segs.back();
+        w.first_group = sg.ngroups;
+        for (int g = 0; g < w.ngroups; g++) gmap.push_back((int32_t)i);
+        sg.ngroups += w.ngroups;
+    }
+}
+
+int launch_segments(const std::vector<Segment>& segs, const void* works_dev, const void* gmap_dev,
+                    hipStream_t s) {
+    for (const Segment& sg : segs) {
+        int e = tmq_launch_chain(sg.type, sg.clamp, (const TmqWork*)works_dev,
+                                 (const int32_t*)gmap_dev + sg.gmap_off, sg.ngroups, s);
+        if (e) return fail(TMQ_ERR_HIP, "chain segment launch: %s", hipGetErrorString((hipError_t)e));
+    }
     return 0;
 }
 
@@ -586,17 +621,14 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
         j.act = (uint8_t*)ch->act_dev + act_off[kv.second];
         j.n = ncols_of[kv.second];
     }
-    // work list
+    // work list, one segment per format
     std::vector<int32_t> gmap;
     for (int i = 0; i < n; i++) {
         const tmq_desc& d = descs[i];
-        TmqWork w = make_work(d.weight, (const uint8_t*)ch->act_dev + act_off[act_of[i]], d.y_dev, d.acc_dev);
-        w.first_group = (int)gmap.size();
-        for (int g = 0; g < w.ngroups; g++) gmap.push_back(i);
-        ch->works.push_back(w);
+        ch->works.push_back(make_work(d.weight, (const uint8_t*)ch->act_dev + act_off[act_of[i]], d.y_dev, d.acc_dev));
         ch->weight_bytes += d.weight->weight_bytes;
     }
-    ch->total_groups = (int)gmap.size();
+    plan_segments(ch->works, gmap, ch->segs);
     e = hipMalloc(&ch->works_dev, sizeof(TmqWork) * ch->works.size());
     if (e == hipSuccess) e = hipMalloc(&ch->gmap_dev, sizeof(int32_t) * gmap.size());
     if (e == hipSuccess)
@@ -619,9 +651,7 @@ int tmq_chain_prepare(tmq_ctx* ctx, tmq_chain* ch) {
 
 int tmq_chain_launch(tmq_ctx* ctx, tmq_chain* ch) {
     if (!ctx || !ch) return fail(TMQ_ERR_ARG, "null argument");
-    LAUNCH_TRY(tmq_launch_chain((const TmqWork*)ch->works_dev, (const int32_t*)ch->gmap_dev,
-                                ch->total_groups, ctx->stream));
-    return 0;
+    return launch_segments(ch->segs, ch->works_dev, ch->gmap_dev, ctx->stream);
 }
 
 int tmq_chain_run(tmq_ctx* ctx, tmq_chain* ch) {
@@ -757,16 +787,15 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
         if (rc) return cleanup(rc);
         std::vector<TmqWork> works;
         std::vector<int32_t> gmap;
+        std::vector<Segment> segs;
         for (size_t i = 0; i < items.size(); i++) {
             hipError_t e = hipMemcpyAsync((uint8_t*)ctx->act.p + aoff[i], items[i].act.data(), items[i].act.size(),
                                           hipMemcpyHostToDevice, ctx->stream);
             if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "act copy: %s", hipGetErrorString(e)));
-            TmqWork w = make_work(items[i].t, (const uint8_t*)ctx->act.p + aoff[i], nullptr,
-                                  (int64_t*)ctx->acc.p + coff[i]);
-            w.first_group = (int)gmap.size();
-            for (int g = 0; g < w.ngroups; g++) gmap.push_back((int32_t)i);
-            works.push_back(w);
+            works.push_back(make_work(items[i].t, (const uint8_t*)ctx->act.p + aoff[i], nullptr,
+                                      (int64_t*)ctx->acc.p + coff[i]));
         }
+        plan_segments(works, gmap, segs);
         rc = ctx->works.ensure(sizeof(TmqWork) * works.size());
         if (!rc) rc = ctx->gmap.ensure(sizeof(int32_t) * gmap.size());
         if (rc) return cleanup(rc);
@@ -775,8 +804,8 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
         if (e == hipSuccess)
             e = hipMemcpyAsync(ctx->gmap.p, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice, ctx->stream);
         if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "chain upload: %s", hipGetErrorString(e)));
-        int le = tmq_launch_chain((const TmqWork*)ctx->works.p, (const int32_t*)ctx->gmap.p, (int)gmap.size(), ctx->stream);
-        if (le) return cleanup(fail(TMQ_ERR_HIP, "chain launch: %s", hipGetErrorString((hipError_t)le)));
+        int le = launch_segments(segs, ctx->works.p, ctx->gmap.p, ctx->stream);
+        if (le) return cleanup(le);
         std::vector<int64_t> acc(acc_total);
         e = hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc_total, hipMemcpyDeviceToHost, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);

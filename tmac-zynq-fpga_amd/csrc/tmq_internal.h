@@ -9,7 +9,8 @@
 //   so the 64 lanes of a wave (one row each) read 1 KiB contiguous per load.
 //
 //   Q8_0  A: q    [b][2][r] x16B     D: d [b][r] u16
-//   Q5_0  A: qs   [b][r]    x16B     B: qh [b][r] u32      D: d [b][r] u16
+//   Q5_0  A: qs   [b][r]    x16B     B: qh' [b][r] u32     D: d [b][r] u16
+//         (qh' = qh with bit 8k+g holding the high bit of element 4g+k)
 //   Q4_K  A: qs   [b][8][r] x16B     B: hdr (d,dmin,scales[12]) [b][r] x16B
 //   Q6_K  A: ql   [b][8][r] x16B     B: qh [b][4][r] x16B   C: sc [b][r] x16B
 //         D: d [b][r] u16
@@ -75,7 +76,8 @@ int tmq_launch_repack(int type, const uint8_t* src, const TmqTensorDev& t, hipSt
 int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux_max_abs, float* row_inv,
                        float* row_scale, int* bad_flag, hipStream_t s);
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s);
-int tmq_launch_chain(const TmqWork* works_dev, const int32_t* group_work_dev, int total_groups,
-                     hipStream_t s);
+// one launch per chain segment (descriptors of one format / clamp mode)
+int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_t* group_work_dev,
+                     int total_groups, hipStream_t s);
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s);

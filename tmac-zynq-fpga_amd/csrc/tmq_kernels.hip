@@ -18,6 +18,10 @@
 #include "tmq_internal.h"
 
 typedef short tmq_s16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 tmq_h2 __attribute__((ext_vector_type(2)));
+// Activation words are wave-uniform: reading them through the constant
+// address space makes the compiler use scalar (SMEM) loads.
+typedef __attribute__((address_space(4))) const uint32_t cu32;
 
 namespace {
 
@@ -58,23 +62,42 @@ __device__ __forceinline__ int dot2(uint32_t w, uint32_t x, int c) {
                                   __builtin_bit_cast(tmq_s16x2, x), c, false);
 }
 
-__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *(const uint4*)p; }
+// weight planes live in global memory (address space 1): plain global loads
+typedef uint32_t tmq_u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const tmq_u32x4 gu4;
+typedef __attribute__((address_space(1))) const uint32_t gu32;
+typedef __attribute__((address_space(1))) const uint16_t gu16;
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) {
+    const tmq_u32x4 v = *(const gu4*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *(const gu32*)p; }
+__device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const gu16*)p; }
+
+// wave index, known to the compiler to be wave-uniform (an SGPR)
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 __device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
     uint32_t d = (i < 4) ? v.x : (i < 8) ? v.y : (i < 12) ? v.z : v.w;
     return (d >> (8 * (i & 3))) & 0xffu;
 }
+__device__ __forceinline__ uint32_t dw_of(const uint4& v, int i) {
+    return (i == 0) ? v.x : (i == 1) ? v.y : (i == 2) ? v.z : v.w;
+}
+// byte k of a dword as float (v_cvt_f32_ubyteN)
+__device__ __forceinline__ float ubf(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xffu); }
 
 struct Act {
     float xs;
-    const uint32_t* xh;
-    const uint32_t* xl;
+    const cu32* xh;
+    const cu32* xl;
 };
 __device__ __forceinline__ Act act_view(const uint8_t* a) {
+    const cu32* p = (const cu32*)a;
     Act r;
-    r.xs = *(const float*)a;
-    int n = *(const int*)(a + 4);
-    r.xh = (const uint32_t*)(a + 16);
+    r.xs = __builtin_bit_cast(float, p[0]);
+    const int n = (int)p[1];
+    r.xh = p + 4;
     r.xl = r.xh + n / 2;
     return r;
 }
@@ -83,34 +106,44 @@ __device__ __forceinline__ size_t p16(int b, int c, int C, size_t R, int r) {
     return (((size_t)b * C + c) * R + (size_t)r) * 16;
 }
 
-// ---------------------------------------------------------------- Q5_0
-// block: d f16, qh u32, qs[16]; element e<16: low nibble of qs[e], e>=16:
-// high nibble of qs[e-16]; bit 4 from qh bit e; q = u - 16.
+// 4 weights (quantised value u_k, normaliser E_k = f(u_k)) -> two int16
+// pairs -> dot with the activation pairs kx, kx+1
 template <bool CLAMP>
-__device__ __forceinline__ int64_t q5_0_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                              float inv) {
-    const size_t R = t.rows_pad;
-    const uint4 qs = ld16(t.pa + p16(b, 0, 1, R, r));
-    const uint32_t qh = *(const uint32_t*)(t.pb + ((size_t)b * R + r) * 4);
-    const float d = h2f(*(const uint16_t*)(t.pd + ((size_t)b * R + r) * 2));
-    const uint32_t* xh = A.xh + b * 16;
-    const uint32_t* xl = A.xl + b * 16;
-    int sh = 0, sl = 0;
+__device__ __forceinline__ void mac4(float e0, float e1, float e2, float e3, float inv,
+                                     const Act& A, int kx, int& sh, int& sl) {
+    const uint32_t P0 = pk16(wq<CLAMP>(e0 * inv), wq<CLAMP>(e1 * inv));
+    const uint32_t P1 = pk16(wq<CLAMP>(e2 * inv), wq<CLAMP>(e3 * inv));
+    sh = dot2(P0, A.xh[kx], sh);
+    sl = dot2(P0, A.xl[kx], sl);
+    sh = dot2(P1, A.xh[kx + 1], sh);
+    sl = dot2(P1, A.xl[kx + 1], sl);
+}
+
+// ---------------------------------------------------------------- Q5_0
+// Planes: qs[16] as in ggml; qh' = qh with its bits transposed so that bit
+// (8k + g) holds the high bit of element 4g + k; d f16.  Group g of four
+// weights (elements 4g..4g+3) is decoded SWAR-style into four bytes
+// u = nibble | hb<<4, spread into f16 lanes 0x6400|u (= 1024+u) and turned
+// into E = (u-16)*d exactly by one v_fma_mix: (1024+u)*d - 1040*d.
+template <bool CLAMP>
+__device__ __forceinline__ void q5_0_block(const TmqTensorDev& t, const Act& A, int b, int r,
+                                           float inv, int& sh, int& sl) {
+    const size_t o = (size_t)b * t.rows_pad + r;
+    const uint4 qs = ld16(t.pa + o * 16);
+    const uint32_t qhp = ld4(t.pb + o * 4);
+    const float d = h2f(ld2(t.pd + o * 2));
+    const float c = -1040.0f * d;  // exact: 7-bit x 11-bit
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        int e0 = 2 * k, e1 = 2 * k + 1;
-        uint32_t b0 = byte_of(qs, e0 & 15), b1 = byte_of(qs, e1 & 15);
-        int n0 = (e0 < 16) ? (int)(b0 & 15u) : (int)(b0 >> 4);
-        int n1 = (e1 < 16) ? (int)(b1 & 15u) : (int)(b1 >> 4);
-        int q0 = (int)(((qh >> e0) & 1u) << 4) + n0 - 16;
-        int q1 = (int)(((qh >> e1) & 1u) << 4) + n1 - 16;
-        float m0 = (d * (float)q0) * inv;
-        float m1 = (d * (float)q1) * inv;
-        uint32_t P = pk16(wq<CLAMP>(m0), wq<CLAMP>(m1));
-        sh = dot2(P, xh[k], sh);
-        sl = dot2(P, xl[k], sl);
+    for (int g = 0; g < 8; g++) {
+        const uint32_t nib = (g < 4) ? (dw_of(qs, g) & 0x0f0f0f0fu) : ((dw_of(qs, g - 4) >> 4) & 0x0f0f0f0fu);
+        const uint32_t hs = (g <= 4) ? (qhp << (4 - g)) : (qhp >> (g - 4));
+        const uint32_t U = (hs & 0x10101010u) | nib;
+        const tmq_h2 v0 = __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0x64646464u, U, 0x04010400u));
+        const tmq_h2 v1 = __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0x64646464u, U, 0x04030402u));
+        mac4<CLAMP>(__builtin_fmaf((float)v0.x, d, c), __builtin_fmaf((float)v0.y, d, c),
+                    __builtin_fmaf((float)v1.x, d, c), __builtin_fmaf((float)v1.y, d, c), inv, A,
+                    b * 16 + 2 * g, sh, sl);
     }
-    return (int64_t)sh * 256 + sl;
 }
 
 // ---------------------------------------------------------------- Q4_K
@@ -125,56 +158,49 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& h, int s, int& sc, in
     }
 }
 
+// E = fl(d*sc*q4 - dmin*m): d*sc*q4 is exact, so one fma with -dmin*m rounds
+// exactly where the reference's multiply-then-subtract does.
 template <bool CLAMP>
-__device__ __forceinline__ int64_t q4_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                              float inv) {
+__device__ __forceinline__ void q4_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
+                                           float inv, int& sh, int& sl) {
     const size_t R = t.rows_pad;
     const uint4 h = ld16(t.pb + p16(b, 0, 1, R, r));
     const float d = h2f(h.x), dmin = h2f(h.x >> 16);
-    int64_t acc = 0;
 #pragma unroll
     for (int sp = 0; sp < 4; sp++) {
         int sc0, m0, sc1, m1;
         q4k_scale_min(h, 2 * sp, sc0, m0);
         q4k_scale_min(h, 2 * sp + 1, sc1, m1);
-        const float A0 = d * (float)sc0, B0 = dmin * (float)m0;
-        const float A1 = d * (float)sc1, B1 = dmin * (float)m1;
-        int sh = 0, sl = 0;
+        const float A0 = d * (float)sc0, B0 = -(dmin * (float)m0);
+        const float A1 = d * (float)sc1, B1 = -(dmin * (float)m1);
 #pragma unroll
         for (int hf = 0; hf < 2; hf++) {
             const uint4 qs = ld16(t.pa + p16(b, 2 * sp + hf, 8, R, r));
-            const int x0 = (b * 256 + 64 * sp + 16 * hf) / 2;  // lo nibbles: sub-block 2sp
-            const int x1 = x0 + 16;                             // hi nibbles: sub-block 2sp+1
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                uint32_t c0 = byte_of(qs, 2 * k), c1 = byte_of(qs, 2 * k + 1);
-                // E = fl(A*q4 - B); A*q4 is exact, so one fma rounds as the
-                // reference's multiply-then-subtract does
-                float e0 = __builtin_fmaf((float)(c0 & 15u), A0, -B0);
-                float e1 = __builtin_fmaf((float)(c1 & 15u), A0, -B0);
-                float f0 = __builtin_fmaf((float)(c0 >> 4), A1, -B1);
-                float f1 = __builtin_fmaf((float)(c1 >> 4), A1, -B1);
-                uint32_t P = pk16(wq<CLAMP>(e0 * inv), wq<CLAMP>(e1 * inv));
-                uint32_t Q = pk16(wq<CLAMP>(f0 * inv), wq<CLAMP>(f1 * inv));
-                sh = dot2(P, A.xh[x0 + k], sh);
-                sl = dot2(P, A.xl[x0 + k], sl);
-                sh = dot2(Q, A.xh[x1 + k], sh);
-                sl = dot2(Q, A.xl[x1 + k], sl);
+            for (int i = 0; i < 4; i++) {
+                const uint32_t w = dw_of(qs, i);
+                const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+                const int kx = (b * 256 + 64 * sp + 16 * hf + 4 * i) / 2;
+                mac4<CLAMP>(__builtin_fmaf(ubf(lo, 0), A0, B0), __builtin_fmaf(ubf(lo, 1), A0, B0),
+                            __builtin_fmaf(ubf(lo, 2), A0, B0), __builtin_fmaf(ubf(lo, 3), A0, B0),
+                            inv, A, kx, sh, sl);
+                mac4<CLAMP>(__builtin_fmaf(ubf(hi, 0), A1, B1), __builtin_fmaf(ubf(hi, 1), A1, B1),
+                            __builtin_fmaf(ubf(hi, 2), A1, B1), __builtin_fmaf(ubf(hi, 3), A1, B1),
+                            inv, A, kx + 16, sh, sl);
             }
         }
-        acc += (int64_t)sh * 256 + sl;
     }
-    return acc;
 }
 
 // ---------------------------------------------------------------- Q6_K
+// u6 = ql nibble | (qh 2 bits) << 4, built four at a time in byte lanes;
+// E = S*(u-32) = fma(u, S, -32*S) exactly (S = d*sc, |E| < 2^24 ulps).
 template <bool CLAMP>
-__device__ __forceinline__ int64_t q6_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                              float inv) {
+__device__ __forceinline__ void q6_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
+                                           float inv, int& sh, int& sl) {
     const size_t R = t.rows_pad;
     const uint4 sc = ld16(t.pc + p16(b, 0, 1, R, r));
-    const float ss = h2f(*(const uint16_t*)(t.pd + ((size_t)b * R + r) * 2));
-    int64_t acc = 0;
+    const float ss = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
 #pragma unroll
     for (int half = 0; half < 2; half++) {
 #pragma unroll
@@ -182,31 +208,25 @@ __device__ __forceinline__ int64_t q6_k_block(const TmqTensorDev& t, const Act& 
             const uint4 qla = ld16(t.pa + p16(b, half * 4 + lc, 8, R, r));
             const uint4 qlb = ld16(t.pa + p16(b, half * 4 + 2 + lc, 8, R, r));
             const uint4 qhc = ld16(t.pb + p16(b, half * 2 + lc, 4, R, r));
-            int sh = 0, sl = 0;
 #pragma unroll
             for (int sub = 0; sub < 4; sub++) {
                 const float S = ss * (float)(int8_t)byte_of(sc, half * 8 + lc + 2 * sub);
                 const float nS = -32.0f * S;
                 const uint4& src = (sub & 1) ? qlb : qla;
-                const int xb = (b * 256 + half * 128 + sub * 32 + 16 * lc) / 2;
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    uint32_t l0 = byte_of(src, 2 * k), l1 = byte_of(src, 2 * k + 1);
-                    uint32_t h0 = byte_of(qhc, 2 * k), h1 = byte_of(qhc, 2 * k + 1);
-                    uint32_t u0 = ((sub < 2) ? (l0 & 15u) : (l0 >> 4)) | (((h0 >> (2 * sub)) & 3u) << 4);
-                    uint32_t u1 = ((sub < 2) ? (l1 & 15u) : (l1 >> 4)) | (((h1 >> (2 * sub)) & 3u) << 4);
-                    // E = S*(u-32) exactly (fits 24 bits)
-                    float e0 = __builtin_fmaf((float)u0, S, nS);
-                    float e1 = __builtin_fmaf((float)u1, S, nS);
-                    uint32_t P = pk16(wq<CLAMP>(e0 * inv), wq<CLAMP>(e1 * inv));
-                    sh = dot2(P, A.xh[xb + k], sh);
-                    sl = dot2(P, A.xl[xb + k], sl);
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t ql = dw_of(src, i), qh = dw_of(qhc, i);
+                    const uint32_t nib = (sub < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+                    const uint32_t hs = (sub == 0) ? (qh << 4) : (sub == 1) ? (qh << 2) : (sub == 2) ? qh : (qh >> 2);
+                    const uint32_t U = (hs & 0x30303030u) | nib;
+                    const int kx = (b * 256 + half * 128 + sub * 32 + 16 * lc + 4 * i) / 2;
+                    mac4<CLAMP>(__builtin_fmaf(ubf(U, 0), S, nS), __builtin_fmaf(ubf(U, 1), S, nS),
+                                __builtin_fmaf(ubf(U, 2), S, nS), __builtin_fmaf(ubf(U, 3), S, nS),
+                                inv, A, kx, sh, sl);
                 }
             }
-            acc += (int64_t)sh * 256 + sl;
         }
     }
-    return acc;
 }
 
 // ---------------------------------------------------------------- Q8_0
@@ -220,46 +240,58 @@ __device__ __forceinline__ uint32_t q8_cs(float bs, float ri) {
     return (uint32_t)(int)tf & 0xffffu;
 }
 
-__device__ __forceinline__ int64_t q8_0_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                              float ri) {
+// deq = (q8*cs) >> 8: with |q8*cs| < 2^23, bytes 1..2 of the product are
+// exactly that int16, so one v_perm packs two of them.
+__device__ __forceinline__ void q8_0_block(const TmqTensorDev& t, const Act& A, int b, int r,
+                                           float ri, int& sh, int& sl) {
     const size_t R = t.rows_pad;
     const uint4 v0 = ld16(t.pa + p16(b, 0, 2, R, r));
     const uint4 v1 = ld16(t.pa + p16(b, 1, 2, R, r));
-    const float bs = h2f(*(const uint16_t*)(t.pd + ((size_t)b * R + r) * 2));
-    const int cs = (int)q8_cs(bs, ri);
-    const uint32_t* xh = A.xh + b * 16;
-    const uint32_t* xl = A.xl + b * 16;
-    int sh = 0, sl = 0;
+    const int cs = (int)q8_cs(h2f(ld2(t.pd + ((size_t)b * R + r) * 2)), ri);
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         const uint4& v = (k < 8) ? v0 : v1;
-        int i0 = (2 * k) & 15, i1 = (2 * k + 1) & 15;
-        int p0 = (int)(int8_t)byte_of(v, i0) * cs;
-        int p1 = (int)(int8_t)byte_of(v, i1) * cs;
-        // bytes 1..2 of p = (p >> 8) as int16 (|p| < 2^23)
-        uint32_t P = __builtin_amdgcn_perm((uint32_t)p1, (uint32_t)p0, 0x06050201u);
-        sh = dot2(P, xh[k], sh);
-        sl = dot2(P, xl[k], sl);
+        const int p0 = (int)(int8_t)byte_of(v, (2 * k) & 15) * cs;
+        const int p1 = (int)(int8_t)byte_of(v, (2 * k + 1) & 15) * cs;
+        const uint32_t P = __builtin_amdgcn_perm((uint32_t)p1, (uint32_t)p0, 0x06050201u);
+        sh = dot2(P, A.xh[b * 16 + k], sh);
+        sl = dot2(P, A.xl[b * 16 + k], sl);
     }
-    return (int64_t)sh * 256 + sl;
 }
 
 // ------------------------------------------------------------ row groups
 // K-split group (Q5_0 / K-quants): 4 waves share 64 rows, wave w takes
-// blocks w, w+4, ...; int64 partials are combined in LDS.
+// blocks w, w+4, ...; the int32 pair sums are folded into int64 every
+// 256 weights at most (|sum| < 2^31), then the waves meet in LDS.
 template <int FMT, bool CLAMP>
 __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
     __shared__ int64_t part[TMQ_WAVES][64];
     const TmqTensorDev& t = w.t;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
     const float inv = t.row_inv[r];
     const Act A = act_view(w.act);
     int64_t acc = 0;
-    for (int b = wave; b < t.nb; b += TMQ_WAVES) {
-        if (FMT == kQ5_0) acc += q5_0_block<CLAMP>(t, A, b, r, inv);
-        if (FMT == kQ4_K) acc += q4_k_block<CLAMP>(t, A, b, r, inv);
-        if (FMT == kQ6_K) acc += q6_k_block<CLAMP>(t, A, b, r, inv);
+    if (FMT == kQ5_0) {
+        int b = wave;
+        for (; b + TMQ_WAVES < t.nb; b += 2 * TMQ_WAVES) {
+            int sh = 0, sl = 0;
+            q5_0_block<CLAMP>(t, A, b, r, inv, sh, sl);
+            q5_0_block<CLAMP>(t, A, b + TMQ_WAVES, r, inv, sh, sl);
+            acc += (int64_t)sh * 256 + sl;
+        }
+        if (b < t.nb) {
+            int sh = 0, sl = 0;
+            q5_0_block<CLAMP>(t, A, b, r, inv, sh, sl);
+            acc += (int64_t)sh * 256 + sl;
+        }
+    } else {
+        for (int b = wave; b < t.nb; b += TMQ_WAVES) {
+            int sh = 0, sl = 0;
+            if (FMT == kQ4_K) q4_k_block<CLAMP>(t, A, b, r, inv, sh, sl);
+            if (FMT == kQ6_K) q6_k_block<CLAMP>(t, A, b, r, inv, sh, sl);
+            acc += (int64_t)sh * 256 + sl;
+        }
     }
     part[wave][lane] = acc;
     __syncthreads();
@@ -278,7 +310,7 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
 // into y in double exactly as sim/tmac_gguf.cpp:1075-1076 does.
 __device__ __forceinline__ void group_q8(const TmqWork& w, int g) {
     const TmqTensorDev& t = w.t;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int r0 = (g * TMQ_WAVES + wave) * 64;
     if (r0 >= t.rows_pad) return;
     const int r = r0 + lane;
@@ -287,42 +319,35 @@ __device__ __forceinline__ void group_q8(const TmqWork& w, int g) {
     const int nt = (t.cols + 63) / 64;
     float y = 0.0f;
     for (int tt = 0; tt < nt; tt++) {
-        int64_t P = q8_0_block(t, A, 2 * tt, r, ri);
-        if (2 * tt + 1 < t.nb) P += q8_0_block(t, A, 2 * tt + 1, r, ri);
+        int sh = 0, sl = 0;
+        q8_0_block(t, A, 2 * tt, r, ri, sh, sl);
+        if (2 * tt + 1 < t.nb) q8_0_block(t, A, 2 * tt + 1, r, ri, sh, sl);
+        const int64_t P = (int64_t)sh * 256 + sl;
         if (w.acc && r < t.rows) w.acc[(size_t)r * nt + tt] = P;
         y = (float)((double)y + ((double)P * (double)A.xs) * (double)rs);
     }
     if (w.y && r < t.rows) w.y[r] = y;
 }
 
-__device__ __forceinline__ void dispatch_group(const TmqWork& w, int g) {
-    switch (w.t.type) {
-    case kQ5_0:
-        if (w.t.clamp) group_ksplit<kQ5_0, true>(w, g); else group_ksplit<kQ5_0, false>(w, g);
-        break;
-    case kQ4_K:
-        if (w.t.clamp) group_ksplit<kQ4_K, true>(w, g); else group_ksplit<kQ4_K, false>(w, g);
-        break;
-    case kQ6_K:
-        if (w.t.clamp) group_ksplit<kQ6_K, true>(w, g); else group_ksplit<kQ6_K, false>(w, g);
-        break;
-    case kQ8_0:
-        group_q8(w, g);
-        break;
-    default:
-        break;
-    }
+template <int FMT, bool CLAMP>
+__device__ __forceinline__ void run_group(const TmqWork& w, int g) {
+    if (FMT == kQ8_0) group_q8(w, g);
+    else group_ksplit<FMT, CLAMP>(w, g);
 }
 
+// one GEMV
+template <int FMT, bool CLAMP>
 __global__ __launch_bounds__(TMQ_WG) void gemv_kernel(TmqWork w) {
-    dispatch_group(w, blockIdx.x);
+    run_group<FMT, CLAMP>(w, blockIdx.x);
 }
 
-// One launch over a whole descriptor chain: workgroup -> (descriptor, group).
+// A chain segment: every descriptor of one format in one launch,
+// workgroup -> (descriptor, group) through the group map.
+template <int FMT, bool CLAMP>
 __global__ __launch_bounds__(TMQ_WG) void chain_kernel(const TmqWork* __restrict__ works,
                                                        const int32_t* __restrict__ group_work) {
     const TmqWork& w = works[group_work[blockIdx.x]];
-    dispatch_group(w, blockIdx.x - w.first_group);
+    run_group<FMT, CLAMP>(w, blockIdx.x - w.first_group);
 }
 
 // ------------------------------------------------------ activation prep
@@ -381,7 +406,10 @@ __global__ void repack_kernel(int type, const uint8_t* __restrict__ src, TmqTens
         const uint8_t* s = src + idx * 22;
         pd[((size_t)b * R + r) * 2 + 0] = s[0];
         pd[((size_t)b * R + r) * 2 + 1] = s[1];
-        for (int i = 0; i < 4; i++) pb[((size_t)b * R + r) * 4 + i] = s[2 + i];
+        const uint32_t qh = (uint32_t)s[2] | ((uint32_t)s[3] << 8) | ((uint32_t)s[4] << 16) | ((uint32_t)s[5] << 24);
+        uint32_t qhp = 0;  // bit 8k+g <- bit 4g+k
+        for (int e = 0; e < 32; e++) qhp |= ((qh >> e) & 1u) << (8 * (e & 3) + (e >> 2));
+        *(uint32_t*)(pb + ((size_t)b * R + r) * 4) = qhp;
         for (int i = 0; i < 16; i++) pa[p16(b, 0, 1, R, r) + i] = s[6 + i];
     } else if (type == kQ4_K) {
         const uint8_t* s = src + idx * 144;
@@ -416,11 +444,12 @@ __global__ void rowstat_kernel(TmqTensorDev t, const float* __restrict__ aux, fl
             ok &= finite_h(db);
             const float d = h2f(db);
             const uint4 qs = ld16(t.pa + p16(b, 0, 1, R, r));
-            const uint32_t qh = *(const uint32_t*)(t.pb + ((size_t)b * R + r) * 4);
+            const uint32_t qhp = *(const uint32_t*)(t.pb + ((size_t)b * R + r) * 4);
             for (int e = 0; e < 32; e++) {
                 uint32_t by = byte_of(qs, e & 15);
                 int nib = (e < 16) ? (int)(by & 15u) : (int)(by >> 4);
-                int q = (int)(((qh >> e) & 1u) << 4) + nib - 16;
+                int hb = (int)((qhp >> (8 * (e & 3) + (e >> 2))) & 1u);
+                int q = (hb << 4) + nib - 16;
                 float ab = fabsf(d * (float)q);
                 if (ab > mx) mx = ab;
             }
@@ -521,18 +550,35 @@ int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux, float* row_inv, 
     return (int)hipGetLastError();
 }
 
+template <template <int, bool> class K>
+static void* kernel_for(int type, int clamp) {
+    switch (type) {
+    case kQ5_0: return clamp ? (void*)K<kQ5_0, true>::fn() : (void*)K<kQ5_0, false>::fn();
+    case kQ4_K: return clamp ? (void*)K<kQ4_K, true>::fn() : (void*)K<kQ4_K, false>::fn();
+    case kQ6_K: return clamp ? (void*)K<kQ6_K, true>::fn() : (void*)K<kQ6_K, false>::fn();
+    case kQ8_0: return (void*)K<kQ8_0, false>::fn();
+    default: return nullptr;
+    }
+}
+template <int F, bool C> struct GemvK { static auto fn() { return gemv_kernel<F, C>; } };
+template <int F, bool C> struct ChainK { static auto fn() { return chain_kernel<F, C>; } };
+
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s) {
     if (w.ngroups <= 0) return 0;
-    hipLaunchKernelGGL(gemv_kernel, dim3(w.ngroups), dim3(TMQ_WG), 0, s, w);
-    return (int)hipGetLastError();
+    void* k = kernel_for<GemvK>(w.t.type, w.t.clamp);
+    if (!k) return (int)hipErrorInvalidValue;
+    TmqWork arg = w;
+    void* args[] = {&arg};
+    return (int)hipLaunchKernel(k, dim3(w.ngroups), dim3(TMQ_WG), args, 0, s);
 }
 
-int tmq_launch_chain(const TmqWork* works_dev, const int32_t* group_work_dev, int total_groups,
-                     hipStream_t s) {
+int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_t* group_work_dev,
+                     int total_groups, hipStream_t s) {
     if (total_groups <= 0) return 0;
-    hipLaunchKernelGGL(chain_kernel, dim3(total_groups), dim3(TMQ_WG), 0, s, works_dev,
-                       group_work_dev);
-    return (int)hipGetLastError();
+    void* k = kernel_for<ChainK>(type, clamp);
+    if (!k) return (int)hipErrorInvalidValue;
+    void* args[] = {&works_dev, &group_work_dev};
+    return (int)hipLaunchKernel(k, dim3(total_groups), dim3(TMQ_WG), args, 0, s);
 }
 
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
