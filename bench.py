@@ -40,25 +40,38 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_workload(ctx, torch, dev, sets):
-    import tmq
+# name -> (description, [(qtype, rows, cols, num_tiles, tile_res_rows, num_col_groups)], copies, x len)
+WORKLOADS = {
+    "c2": ("BASELINE configs[1]: Q5_0 attn_q 896x896 (1 descriptor, num_tiles=224, tile_res_rows=4) "
+           "+ ffn_gate/ffn_up 4864x896, batch 1",
+           [(6, 896, 896, 224, 4, 1), (6, 4864, 896, 1216, 4, 1), (6, 4864, 896, 1216, 4, 1)], SETS, 896),
+    "c1": ("BASELINE configs[0]: Q8_0 logits 151936x896 (num_tiles=2374 64-row tiles), batch 1",
+           [(8, 151936, 896, 2374, 64, 14)], 3, 896),
+    "c3q4k": ("BASELINE configs[2]: Q4_K ffn_down 896x4864 (56-row tiles, 19 column groups), batch 1",
+              [(12, 896, 4864, 304, 56, 19)], 111, 4864),
+    "c3q6k": ("BASELINE configs[2]: Q6_K ffn_down 896x4864 (32-row tiles, 19 column groups), batch 1",
+              [(14, 896, 4864, 532, 32, 19)], 77, 4864),
+}
+
+
+def build_workload(ctx, torch, dev, name, copies=None):
     from tmq import synth
-    shapes = [("attn_q", 896, 896), ("ffn_gate", 4864, 896), ("ffn_up", 4864, 896)]
-    x = synth.gen_x(896, 12345)
+    desc_txt, shapes, ncopies, n = WORKLOADS[name]
+    copies = copies or ncopies
+    x = synth.gen_x(n, 12345)
     x_d = torch.from_numpy(x).to(dev)
     tensors, descs, ys = [], [], []
-    for s in range(sets):
-        for k, (name, rows, cols) in enumerate(shapes):
-            w = synth.gen_weights(tmq.Q5_0, rows, cols, seed=1000 * s + k)
-            t = ctx.upload(tmq.Q5_0, rows, cols, w)
+    for s in range(copies):
+        for k, (qt, rows, cols, nt, tr, ncg) in enumerate(shapes):
+            w = synth.gen_weights(qt, rows, cols, seed=1000 * s + k)
+            t = ctx.upload(qt, rows, cols, w)
             y = torch.empty(rows, dtype=torch.float32, device=dev)
             tensors.append(t)
             ys.append(y)
-            # PhaseB Q5_0 descriptor semantics: 4-row tiles, num_tiles = rows/4
-            descs.append((t, x_d.data_ptr(), y.data_ptr(), None, rows // 4, 4, 1))
-        if s % 10 == 0:
-            log(f"uploaded weight set {s + 1}/{sets}")
-    return x, x_d, tensors, descs, ys, shapes
+            descs.append((t, x_d.data_ptr(), y.data_ptr(), None, nt, tr, ncg))
+        if s % 20 == 0:
+            log(f"{name}: uploaded weight set {s + 1}/{copies}")
+    return desc_txt, x_d, tensors, descs, ys
 
 
 def time_events(torch, stream, fn, iters):
@@ -83,16 +96,15 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(shapes, seconds):
+def cpu_baseline(seconds):
     """Reference CPU path on one core, bounded sample of the same workload."""
-    import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, Reference
     from tmq import synth
     kind = "reference" if Reference.available() else "port"
     impl = Reference() if kind == "reference" else Oracle()
     x = synth.gen_x(896, 12345)
-    ws = [(synth.gen_weights(6, r, c, seed=k), r, c) for k, (_, r, c) in enumerate(shapes)]
+    ws = [(synth.gen_weights(qt, r, c, seed=k), r, c) for k, (qt, r, c, *_) in enumerate(WORKLOADS["c2"][1])]
     nbytes = sum(w.size for w, _, _ in ws)
     done, t0 = 0, time.perf_counter()
     while True:
@@ -108,6 +120,44 @@ def cpu_baseline(shapes, seconds):
             "sample": f"{name} over attn_q 896x896 + ffn_gate/ffn_up 4864x896 "
                       f"({nbytes} weight bytes) x {done} passes = {el:.1f} s on one host thread, "
                       f"per-call row scan included as in the reference"}
+
+
+def measure(ctx, torch, dev, stream, name, steps, warmup, copies=None):
+    """Returns (desc, weight bytes, step ms, kernel-only ms, n descriptors)."""
+    desc_txt, x_d, tensors, descs, ys = build_workload(ctx, torch, dev, name, copies)
+    chain = ctx.chain(descs)
+    wbytes = chain.weight_bytes
+    log(f"{name}: {len(descs)} descriptors, {wbytes} weight bytes per step")
+    for _ in range(warmup):
+        chain.run()
+    ctx.sync()
+    torch.cuda.synchronize()
+    step_ms = time_events(torch, stream, chain.run, steps)
+    ctx.sync()
+    chain.prepare()
+    ctx.sync()
+    kern_ms = time_events(torch, stream, chain.launch, steps)
+    ctx.sync()
+    torch.cuda.synchronize()
+    chain.free()
+    for t in tensors:
+        t.free()
+    return desc_txt, wbytes, step_ms, kern_ms, len(descs)
+
+
+def single_launch_us(ctx, torch, dev, stream, steps):
+    """Latency of one attn_q GEMV launch (896x896 Q5_0), kernel only."""
+    desc_txt, x_d, tensors, descs, ys = build_workload(ctx, torch, dev, "c2", copies=1)
+    chain = ctx.chain(descs[:1])
+    chain.run()
+    chain.prepare()
+    ctx.sync()
+    ms = time_events(torch, stream, chain.launch, steps)
+    ctx.sync()
+    chain.free()
+    for t in tensors:
+        t.free()
+    return ms * 1e3
 
 
 def copy_calibration(torch, dev, nbytes=1 << 30):
@@ -129,6 +179,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--sets", type=int, default=SETS)
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE GEMV configs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -145,28 +197,12 @@ def main():
 
     ctx = tmq.Context(0)
     stream = torch.cuda.ExternalStream(ctx.stream)
-    log(f"building workload: {args.sets} sets of Q5_0 attn_q/ffn_gate/ffn_up")
-    x, x_d, tensors, descs, ys, shapes = build_workload(ctx, torch, dev, args.sets)
-    chain = ctx.chain(descs)
-    wbytes = chain.weight_bytes
-    log(f"chain: {len(descs)} descriptors, {wbytes} weight bytes per step")
-
-    for _ in range(args.warmup):
-        chain.run()
-    ctx.sync()
-    torch.cuda.synchronize()
-    log(f"timing {args.steps} steps")
-    step_ms = time_events(torch, stream, chain.run, args.steps)
-    ctx.sync()
-    torch.cuda.synchronize()
-    chain.prepare()
-    kern_ms = time_events(torch, stream, chain.launch, args.steps)
-    ctx.sync()
-    torch.cuda.synchronize()
-
+    wl = args.workload
+    copies = args.sets if wl == "c2" else None
+    desc_txt, wbytes, step_ms, kern_ms, ndesc = measure(ctx, torch, dev, stream, wl, args.steps, args.warmup, copies)
     value = wbytes / (step_ms * 1e-3) / 1e9
     achieved = wbytes / (kern_ms * 1e-3) / 1e9
-    traffic = read_traffic()
+    traffic = read_traffic() if wl == "c2" else None
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -179,12 +215,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int16",
-        "data": "synthetic (seeded ggml Q5_0 blocks: random qs/qh bits, d=fp16(|N(0,1)|*0.02); x ~ N(0,1))",
+        "data": "synthetic (seeded ggml blocks as BASELINE.json specifies per format; x ~ N(0,1))",
         "config": {
-            "workload": "BASELINE configs[1]: Q5_0 attn_q 896x896 (1 descriptor, num_tiles=224, "
-                        "tile_res_rows=4) + ffn_gate/ffn_up 4864x896, batch 1, "
-                        f"{args.sets} weight sets cycled ({wbytes} B > 256 MiB), one chain launch per step",
-            "descriptors_per_step": len(descs),
+            "workload": f"{desc_txt}; weight sets cycled ({wbytes} B > 256 MiB), one chain launch per step",
+            "descriptors_per_step": ndesc,
             "weight_bytes_per_step": wbytes,
             "pct_hbm_peak": round(100.0 * value / PEAK_GBPS, 2),
         },
@@ -199,13 +233,19 @@ def main():
             "kernel_ms": round(kern_ms, 5),
         },
     }
-    chain.free()
-    for t in tensors:
-        t.free()
+    if not args.no_extra and wl == "c2":
+        extra = {}
+        for name in ("c1", "c3q4k", "c3q6k"):
+            _, wb, sm, km, nd = measure(ctx, torch, dev, stream, name, max(10, args.steps // 2), 2)
+            extra[name] = {"weight_bytes": wb, "descriptors": nd, "ms_per_launch": round(km, 5),
+                           "gbps": round(wb / (km * 1e-3) / 1e9, 2),
+                           "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
+        extra["c2_attn_q_single_launch_us"] = round(single_launch_us(ctx, torch, dev, stream, 50), 2)
+        out["extra"] = extra
     ctx.close()
     if not args.no_cpu:
         log(f"CPU baseline ({args.cpu_seconds:.0f} s sample)")
-        out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

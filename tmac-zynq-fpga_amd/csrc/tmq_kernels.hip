@@ -87,6 +87,16 @@ __device__ __forceinline__ uint32_t dw_of(const uint4& v, int i) {
 // byte k of a dword as float (v_cvt_f32_ubyteN)
 __device__ __forceinline__ float ubf(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xffu); }
 
+// bytes 0,1 (sel 0x0c010c00) or 2,3 (0x0c030c02) of w, each zero-extended
+// into a 16-bit lane: as f16 those lanes are the subnormals b * 2^-24, exact
+// inputs for v_fma_mix_f32 (fp16 denormals are not flushed)
+__device__ __forceinline__ tmq_h2 lanes01(uint32_t w) {
+    return __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0u, w, 0x0c010c00u));
+}
+__device__ __forceinline__ tmq_h2 lanes23(uint32_t w) {
+    return __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0u, w, 0x0c030c02u));
+}
+
 struct Act {
     float xs;
     const cu32* xh;
@@ -159,7 +169,10 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& h, int s, int& sc, in
 }
 
 // E = fl(d*sc*q4 - dmin*m): d*sc*q4 is exact, so one fma with -dmin*m rounds
-// exactly where the reference's multiply-then-subtract does.
+// exactly where the reference's multiply-then-subtract does.  The nibbles go
+// into f16 lanes as subnormals q*2^-24 (low nibbles) and 16q*2^-24 (high
+// nibbles, masked in place), so E = fma_mix(lane, A*2^24 or A*2^20, -B):
+// the scalings by powers of two are exact and the product is A*q exactly.
 template <bool CLAMP>
 __device__ __forceinline__ void q4_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
                                            float inv, int& sh, int& sl) {
@@ -171,21 +184,22 @@ __device__ __forceinline__ void q4_k_block(const TmqTensorDev& t, const Act& A, 
         int sc0, m0, sc1, m1;
         q4k_scale_min(h, 2 * sp, sc0, m0);
         q4k_scale_min(h, 2 * sp + 1, sc1, m1);
-        const float A0 = d * (float)sc0, B0 = -(dmin * (float)m0);
-        const float A1 = d * (float)sc1, B1 = -(dmin * (float)m1);
+        const float A0 = (d * (float)sc0) * 0x1p24f, B0 = -(dmin * (float)m0);
+        const float A1 = (d * (float)sc1) * 0x1p20f, B1 = -(dmin * (float)m1);
 #pragma unroll
         for (int hf = 0; hf < 2; hf++) {
             const uint4 qs = ld16(t.pa + p16(b, 2 * sp + hf, 8, R, r));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t w = dw_of(qs, i);
-                const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+                const uint32_t lo = w & 0x0f0f0f0fu, hi = w & 0xf0f0f0f0u;
+                const tmq_h2 l0 = lanes01(lo), l1 = lanes23(lo), h0 = lanes01(hi), h1 = lanes23(hi);
                 const int kx = (b * 256 + 64 * sp + 16 * hf + 4 * i) / 2;
-                mac4<CLAMP>(__builtin_fmaf(ubf(lo, 0), A0, B0), __builtin_fmaf(ubf(lo, 1), A0, B0),
-                            __builtin_fmaf(ubf(lo, 2), A0, B0), __builtin_fmaf(ubf(lo, 3), A0, B0),
+                mac4<CLAMP>(__builtin_fmaf((float)l0.x, A0, B0), __builtin_fmaf((float)l0.y, A0, B0),
+                            __builtin_fmaf((float)l1.x, A0, B0), __builtin_fmaf((float)l1.y, A0, B0),
                             inv, A, kx, sh, sl);
-                mac4<CLAMP>(__builtin_fmaf(ubf(hi, 0), A1, B1), __builtin_fmaf(ubf(hi, 1), A1, B1),
-                            __builtin_fmaf(ubf(hi, 2), A1, B1), __builtin_fmaf(ubf(hi, 3), A1, B1),
+                mac4<CLAMP>(__builtin_fmaf((float)h0.x, A1, B1), __builtin_fmaf((float)h0.y, A1, B1),
+                            __builtin_fmaf((float)h1.x, A1, B1), __builtin_fmaf((float)h1.y, A1, B1),
                             inv, A, kx + 16, sh, sl);
             }
         }
@@ -194,7 +208,7 @@ __device__ __forceinline__ void q4_k_block(const TmqTensorDev& t, const Act& A, 
 
 // ---------------------------------------------------------------- Q6_K
 // u6 = ql nibble | (qh 2 bits) << 4, built four at a time in byte lanes;
-// E = S*(u-32) = fma(u, S, -32*S) exactly (S = d*sc, |E| < 2^24 ulps).
+// E = S*(u-32) exactly (S = d*sc has <= 18 significant bits, u-32 <= 6).
 template <bool CLAMP>
 __device__ __forceinline__ void q6_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
                                            float inv, int& sh, int& sl) {
@@ -211,7 +225,7 @@ __device__ __forceinline__ void q6_k_block(const TmqTensorDev& t, const Act& A, 
 #pragma unroll
             for (int sub = 0; sub < 4; sub++) {
                 const float S = ss * (float)(int8_t)byte_of(sc, half * 8 + lc + 2 * sub);
-                const float nS = -32.0f * S;
+                const float nS = -32.0f * S, S24 = S * 0x1p24f;
                 const uint4& src = (sub & 1) ? qlb : qla;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -220,8 +234,10 @@ __device__ __forceinline__ void q6_k_block(const TmqTensorDev& t, const Act& A, 
                     const uint32_t hs = (sub == 0) ? (qh << 4) : (sub == 1) ? (qh << 2) : (sub == 2) ? qh : (qh >> 2);
                     const uint32_t U = (hs & 0x30303030u) | nib;
                     const int kx = (b * 256 + half * 128 + sub * 32 + 16 * lc + 4 * i) / 2;
-                    mac4<CLAMP>(__builtin_fmaf(ubf(U, 0), S, nS), __builtin_fmaf(ubf(U, 1), S, nS),
-                                __builtin_fmaf(ubf(U, 2), S, nS), __builtin_fmaf(ubf(U, 3), S, nS),
+                    // E = S*(u-32) = fma_mix(u*2^-24, S*2^24, -32*S), exact
+                    const tmq_h2 u0 = lanes01(U), u1 = lanes23(U);
+                    mac4<CLAMP>(__builtin_fmaf((float)u0.x, S24, nS), __builtin_fmaf((float)u0.y, S24, nS),
+                                __builtin_fmaf((float)u1.x, S24, nS), __builtin_fmaf((float)u1.y, S24, nS),
                                 inv, A, kx, sh, sl);
                 }
             }
@@ -242,20 +258,28 @@ __device__ __forceinline__ uint32_t q8_cs(float bs, float ri) {
 
 // deq = (q8*cs) >> 8: with |q8*cs| < 2^23, bytes 1..2 of the product are
 // exactly that int16, so one v_perm packs two of them.
-__device__ __forceinline__ void q8_0_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                           float ri, int& sh, int& sl) {
+struct Q8Blk {
+    uint4 v0, v1;
+    uint32_t d;
+};
+__device__ __forceinline__ Q8Blk q8_load(const TmqTensorDev& t, int b, int r) {
     const size_t R = t.rows_pad;
-    const uint4 v0 = ld16(t.pa + p16(b, 0, 2, R, r));
-    const uint4 v1 = ld16(t.pa + p16(b, 1, 2, R, r));
-    const int cs = (int)q8_cs(h2f(ld2(t.pd + ((size_t)b * R + r) * 2)), ri);
+    Q8Blk k;
+    k.v0 = ld16(t.pa + p16(b, 0, 2, R, r));
+    k.v1 = ld16(t.pa + p16(b, 1, 2, R, r));
+    k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
+    return k;
+}
+__device__ __forceinline__ void q8_mac(const Q8Blk& k, const Act& A, int b, float ri, int& sh, int& sl) {
+    const int cs = (int)q8_cs(h2f(k.d), ri);
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const uint4& v = (k < 8) ? v0 : v1;
-        const int p0 = (int)(int8_t)byte_of(v, (2 * k) & 15) * cs;
-        const int p1 = (int)(int8_t)byte_of(v, (2 * k + 1) & 15) * cs;
+    for (int j = 0; j < 16; j++) {
+        const uint4& v = (j < 8) ? k.v0 : k.v1;
+        const int p0 = (int)(int8_t)byte_of(v, (2 * j) & 15) * cs;
+        const int p1 = (int)(int8_t)byte_of(v, (2 * j + 1) & 15) * cs;
         const uint32_t P = __builtin_amdgcn_perm((uint32_t)p1, (uint32_t)p0, 0x06050201u);
-        sh = dot2(P, A.xh[b * 16 + k], sh);
-        sl = dot2(P, A.xl[b * 16 + k], sl);
+        sh = dot2(P, A.xh[b * 16 + j], sh);
+        sl = dot2(P, A.xl[b * 16 + j], sl);
     }
 }
 
@@ -318,10 +342,21 @@ __device__ __forceinline__ void group_q8(const TmqWork& w, int g) {
     const Act A = act_view(w.act);
     const int nt = (t.cols + 63) / 64;
     float y = 0.0f;
+    // software pipeline: the next block's loads are in flight while the
+    // current block is multiplied
+    Q8Blk cur = q8_load(t, 0, r);
     for (int tt = 0; tt < nt; tt++) {
         int sh = 0, sl = 0;
-        q8_0_block(t, A, 2 * tt, r, ri, sh, sl);
-        if (2 * tt + 1 < t.nb) q8_0_block(t, A, 2 * tt + 1, r, ri, sh, sl);
+        const int b0 = 2 * tt, b1 = 2 * tt + 1;
+        const bool has1 = b1 < t.nb;
+        Q8Blk nxt = has1 ? q8_load(t, b1, r) : cur;
+        q8_mac(cur, A, b0, ri, sh, sl);
+        if (has1) {
+            cur = (b1 + 1 < t.nb) ? q8_load(t, b1 + 1, r) : nxt;
+            q8_mac(nxt, A, b1, ri, sh, sl);
+        } else if (b0 + 1 < t.nb) {
+            cur = q8_load(t, b0 + 1, r);
+        }
         const int64_t P = (int64_t)sh * 256 + sl;
         if (w.acc && r < t.rows) w.acc[(size_t)r * nt + tt] = P;
         y = (float)((double)y + ((double)P * (double)A.xs) * (double)rs);
