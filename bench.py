@@ -26,6 +26,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "tmac-zynq-fpga_amd")
 sys.path.insert(0, PKG)
@@ -160,6 +162,61 @@ def single_launch_us(ctx, torch, dev, stream, steps):
     return ms * 1e3
 
 
+def decode_bench(ctx, torch, stream, tokens=128, warmup=8):
+    """greedy batch-1 decode of the synthetic Qwen2-0.5B
+    model (tmq.model_synth, seed 2024) from one seeded prompt token; one
+    step = logits GEMV + argmax + embedding + 24 layers, graph-replayed."""
+    import tmq
+    from tmq import model_synth, tmacfile
+    log("decode: generating the synthetic C4 model")
+    blob = tmacfile.to_bytes(model_synth.gen_model(2024))
+    m = tmq.Model(ctx, blob, max_seq=512)
+    del blob
+    prompt = [int(np.random.Generator(np.random.PCG64(7)).integers(0, 151936))]
+    m.prompt(prompt)
+    m.generate(warmup)
+    m.prompt(prompt)
+    ctx.sync()
+    ms = time_events(torch, stream, lambda: m.generate_async(tokens), 1) / tokens
+    got = m.tokens(1, tokens)
+    wb = m.weight_bytes
+    m.free()
+    return {"tokens": tokens, "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+            "weight_gbps": round(wb / (ms * 1e-3) / 1e9, 1), "weight_bytes_per_token": wb,
+            "first_tokens": got[:8].tolist()}
+
+
+def cpu_decode_baseline(seconds):
+    """The reference engine (oracle/_ref: load_tmac + forward_all_layers +
+    get_logits_q8 with the --fpga-* paths) on one host thread, greedy steps
+    until `seconds` have passed."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Reference
+    if not Reference.available():
+        return None
+    import tempfile
+    from tmq import model_synth, tmacfile
+    R = Reference()
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "c4.tmac")
+        tmacfile.write(path, model_synth.gen_model(2024))
+        R.model_load(path)
+    tok = int(np.random.Generator(np.random.PCG64(7)).integers(0, 151936))
+    R.model_reset()
+    hidden = np.zeros(R.HIDDEN, dtype=np.float32)
+    R.model_step(hidden, tok, 0)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        lg = R.model_logits(hidden)
+        R.model_step(hidden, int(np.argmax(lg)), 1 + done)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done / el, 4), "unit": "tok/s", "cores": 1, "kind": "reference",
+            "sample": f"{done} greedy decode steps (positions 1..{done}) of the same model, {el:.1f} s"}
+
+
 def copy_calibration(torch, dev, nbytes=1 << 30):
     """A plain device copy of known size, for scaling FETCH_SIZE/WRITE_SIZE."""
     a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -241,11 +298,16 @@ def main():
                            "gbps": round(wb / (km * 1e-3) / 1e9, 2),
                            "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
         extra["c2_attn_q_single_launch_us"] = round(single_launch_us(ctx, torch, dev, stream, 50), 2)
+        extra["c4_decode"] = decode_bench(ctx, torch, stream)
         out["extra"] = extra
     ctx.close()
     if not args.no_cpu:
         log(f"CPU baseline ({args.cpu_seconds:.0f} s sample)")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        if not args.no_extra and wl == "c2":
+            dec = cpu_decode_baseline(args.cpu_seconds)
+            if dec is not None:
+                out["cpu_baseline"]["c4_decode"] = dec
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

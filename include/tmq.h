@@ -173,6 +173,58 @@ int tmq_chain_free(tmq_chain* chain);
 /* total ggml weight bytes streamed by one run of the chain */
 uint64_t tmq_chain_weight_bytes(const tmq_chain* chain);
 
+/* ------------------------------------------------------------------------
+ * Decode engine: a .tmac model resident on the GPU, run one position at a
+ * time.  Replaces the reference engine's host loop around the matmuls
+ * (sim/tmac_gguf.cpp:1559-1711 forward_layer_with_cache, :1820 get_logits_q8,
+ * :1950-2045 reset_cache / process_embedding / process_prompt / generate) run
+ * with --fpga-q8 --fpga-q5-0 --fpga-q4k --fpga-q6-k.  Results follow that
+ * path's arithmetic (fp32 operations in the reference's order); the token
+ * choice is greedy (first index of the largest logit) where the reference
+ * samples top-k with rand() (:1975-1994).
+ * ------------------------------------------------------------------------ */
+typedef struct tmq_model tmq_model;
+
+typedef struct {
+    int32_t n_layers, hidden, inter, vocab;
+    int32_t n_heads, n_kv_heads, head_dim, max_seq;
+    float rope_base, norm_eps;
+} tmq_model_config;
+
+/* load_tmac (sim/tmac_gguf.cpp:1894-1947): the .tmac container of
+ * scripts/extract_tmac.py:6-24, uploaded and checked (shapes, types, sizes).
+ * Shapes are taken from the tensors (head_dim 64, RoPE base 1e6, RMSNorm eps
+ * 1e-6 as the reference's constants, :136-148, :418, :1528).  max_seq <= 4096
+ * positions of KV cache (0: 512); the reference fixes 256 (:148). */
+int tmq_model_load(tmq_ctx* ctx, const char* path, int max_seq, tmq_model** out);
+int tmq_model_load_mem(tmq_ctx* ctx, const void* data, uint64_t n_bytes, int max_seq, tmq_model** out);
+int tmq_model_free(tmq_model* m);
+int tmq_model_get_config(const tmq_model* m, tmq_model_config* out);
+/* ggml weight bytes streamed per generated token (all layers + logits) */
+uint64_t tmq_model_weight_bytes(const tmq_model* m);
+/* number of positions processed since the last prompt */
+int tmq_model_position(const tmq_model* m);
+/* capture the step sequences as HIP graphs (default on; TMQ_GRAPHS=0 off) */
+int tmq_model_set_graphs(tmq_model* m, int enable);
+/* reset_cache + process_prompt (sim/tmac_gguf.cpp:1950-1997) */
+int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n);
+/* process_embedding + forward_all_layers of one more token (:1955-1967) */
+int tmq_model_feed(tmq_model* m, int32_t token);
+/* as tmq_model_feed, also returning the hidden state after the embedding
+ * and after every layer ((n_layers+1) x hidden floats; --dump-layers, :1976) */
+int tmq_model_feed_dump(tmq_model* m, int32_t token, float* layers_out);
+/* get_logits_q8 (:1820-1845) of the last processed position -> vocab floats */
+int tmq_model_logits(tmq_model* m, float* logits);
+/* generate (:2001-2025) with greedy choice: n x (logits, argmax, feed);
+ * the chosen tokens are returned in out_tokens[n] */
+int tmq_model_generate(tmq_model* m, int n, int32_t* out_tokens);
+/* the same, queued without waiting; read the tokens with tmq_model_tokens */
+int tmq_model_generate_async(tmq_model* m, int n);
+/* tokens of positions [first, first+n) (prompt and generated) */
+int tmq_model_tokens(tmq_model* m, int first, int n, int32_t* out);
+/* current hidden state (hidden floats) */
+int tmq_model_hidden(tmq_model* m, float* out);
+
 #ifdef __cplusplus
 }
 #endif

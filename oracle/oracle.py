@@ -155,6 +155,44 @@ class Reference:
         _setup(L, "ref_phaseb_count", _i, [])
         _setup(L, "ref_ddr", _P, [])
         _setup(L, "ref_phaseb_run", _i, [_u32, _P])
+        _setup(L, "ref_model_load", _i, [C.c_char_p])
+        _setup(L, "ref_model_prompt", _i, [_P, _i, _P])
+        _setup(L, "ref_model_reset", None, [])
+        _setup(L, "ref_model_logits", None, [_P, _P])
+        _setup(L, "ref_model_step", None, [_P, _i, _i])
+        _setup(L, "ref_model_step_dump", None, [_P, _i, _i, _P])
+        _setup(L, "ref_apply_rope", None, [_P, _P, _i])
+
+    # ---- whole-model engine (sim/tmac_gguf.cpp:1894-2045), 896-wide only
+    HIDDEN, VOCAB, LAYERS = 896, 151936, 24
+
+    def model_load(self, path: str) -> None:
+        assert self.lib.ref_model_load(path.encode()) == 0, "load_tmac failed"
+
+    def model_prompt(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        h = np.empty(self.HIDDEN, dtype=np.float32)
+        assert self.lib.ref_model_prompt(_ptr(t), t.size, _ptr(h)) == 0
+        return h
+
+    def model_reset(self) -> None:
+        self.lib.ref_model_reset()
+
+    def model_logits(self, hidden) -> np.ndarray:
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        out = np.empty(self.VOCAB, dtype=np.float32)
+        self.lib.ref_model_logits(_ptr(h), _ptr(out))
+        return out
+
+    def model_step(self, hidden: np.ndarray, token: int, pos: int, dump: bool = False):
+        """process_embedding + all layers at pos; hidden updated in place.
+        With dump, returns the hidden state after the embedding and each layer."""
+        if dump:
+            d = np.empty((self.LAYERS + 1, self.HIDDEN), dtype=np.float32)
+            self.lib.ref_model_step_dump(_ptr(hidden), int(token), int(pos), _ptr(d))
+            return d
+        self.lib.ref_model_step(_ptr(hidden), int(token), int(pos))
+        return None
 
     def matmul(self, qtype, w, x, rows, cols, row_max_abs=None) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)

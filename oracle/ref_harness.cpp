@@ -106,4 +106,39 @@ uint32_t ref_phaseb_add_descriptor(uint32_t w, uint32_t a, uint32_t r, uint16_t 
     return phaseb_add_descriptor(w, a, r, nt, tb, type, trr, flags, atb, ncg);
 }
 
+// Whole-model engine, run as `tmac_gguf model.tmac --fpga-q8 --fpga-q5-0
+// --fpga-q4k --fpga-q6-k` would (sim/tmac_gguf.cpp:2066-2091): load_tmac
+// into the arena, then process_prompt / get_logits_q8 / one generate step.
+int ref_model_load(const char* path) {
+    if (!g_ddr) {
+        g_ddr = (uint8_t*)calloc(DDR_SIZE, 1);
+        if (!g_ddr) return -1;
+    }
+    if (load_tmac(path) != 0) return -1;
+    g_use_fpga = g_fpga_q8 = g_fpga_q4k = g_fpga_q5_0 = g_fpga_q6_k = true;
+    return 0;
+}
+int ref_model_prompt(const int* tokens, int n, float* hidden) {
+    std::vector<int> v(tokens, tokens + n);
+    return process_prompt(hidden, v, false);
+}
+void ref_model_reset(void) { reset_cache(); }
+void ref_model_logits(const float* hidden, float* logits) { get_logits_q8(logits, hidden); }
+// generate()'s body after sampling (sim/tmac_gguf.cpp:2020-2021)
+void ref_model_step(float* hidden, int token, int pos) {
+    process_embedding(hidden, token);
+    forward_all_layers(hidden, pos);
+}
+// the same with the hidden state after the embedding and after each layer
+void ref_model_step_dump(float* hidden, int token, int pos, float* dump) {
+    process_embedding(hidden, token);
+    memcpy(dump, hidden, sizeof(float) * HIDDEN_DIM);
+    for (int l = 0; l < NUM_LAYERS; l++) {
+        forward_layer_with_cache(hidden, l, pos);
+        memcpy(dump + (size_t)(l + 1) * HIDDEN_DIM, hidden, sizeof(float) * HIDDEN_DIM);
+    }
+}
+// apply_rope (sim/tmac_gguf.cpp:1527): q [14*64], k [2*64] rotated in place
+void ref_apply_rope(float* q, float* k, int pos) { apply_rope(q, k, pos); }
+
 }  // extern "C"

@@ -1,0 +1,150 @@
+"""GPU parity of the decode engine (tmq_model_*) against the compiled
+reference engine's greedy decode of the synthetic full model
+(tests/golden/model_c4.npz, written by tests/golden/gen_model_golden.py).
+
+Bar (north star): greedy tokens identical, logits within 1e-3 (absolute, on
+logits of magnitude ~100); the hidden states are expected bit-exact except
+where the engine's logf (fp64 log rounded once) differs from the host libm's
+logf by one ulp, so they are checked to 1e-5 relative and the bit-exact
+fraction is reported.
+"""
+import numpy as np
+import pytest
+from conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return load_golden("model_c4.npz")
+
+
+@pytest.fixture(scope="module")
+def model(ctx, golden):
+    import tmq
+    from tmq import model_synth, tmacfile
+    print("[model] generating the synthetic C4 model", flush=True)
+    blob = tmacfile.to_bytes(model_synth.gen_model(int(golden["model_seed"])))
+    m = tmq.Model(ctx, blob, max_seq=512)
+    del blob
+    yield m
+    m.free()
+
+
+def test_config(model):
+    c = model.config
+    assert (c["n_layers"], c["hidden"], c["inter"], c["vocab"]) == (24, 896, 4864, 151936)
+    assert (c["n_heads"], c["n_kv_heads"], c["head_dim"]) == (14, 2, 64)
+    assert model.weight_bytes == 391573504
+
+
+def test_prompt_hidden(model, golden):
+    """hidden state after a one-token prompt (position 0, all 24 layers)"""
+    print("[model] prompt of one token", flush=True)
+    model.set_graphs(False)
+    model.prompt(golden["prompt"])
+    h = model.hidden()
+    exp = golden["layers0"][-1]
+    exact = np.mean(h.view(np.uint32) == exp.view(np.uint32))
+    print(f"[model] hidden at position 0: {exact:.4f} bit-exact", flush=True)
+    np.testing.assert_allclose(h, exp, rtol=0, atol=1e-5 * np.abs(exp).max())
+
+
+def test_layer_dump_matches(ctx, golden):
+    """tmq_model_feed_dump on a fresh model: every layer's output at position 0"""
+    import tmq
+    from tmq import model_synth, tmacfile
+    blob = tmacfile.to_bytes(model_synth.gen_model(int(golden["model_seed"])))
+    m = tmq.Model(ctx, blob, max_seq=16)
+    del blob
+    d = m.feed(int(golden["prompt"][0]), dump=True)
+    exp = golden["layers0"]
+    for l in range(exp.shape[0]):
+        scale = np.abs(exp[l]).max()
+        err = np.abs(d[l] - exp[l]).max() / scale
+        ex = np.mean(d[l].view(np.uint32) == exp[l].view(np.uint32))
+        print(f"[model] layer {l}: max rel err {err:.3e}, bit-exact {ex:.4f}", flush=True)
+        assert err < 1e-5, f"layer {l}: rel err {err}"
+    m.free()
+
+
+def test_greedy_logits_per_step(model, golden):
+    """logits of every step vs the reference (top-10 ids and values, every
+    64th logit at a few steps), feeding the reference's tokens"""
+    model.set_graphs(True)
+    model.prompt(golden["prompt"])
+    toks = golden["tokens"]
+    subs = {int(s): i for i, s in enumerate(golden["sub_steps"])}
+    worst = 0.0
+    for step in range(toks.size):
+        lg = model.logits()
+        ids = np.lexsort((np.arange(lg.size), -lg))[:10]
+        assert int(ids[0]) == int(toks[step]), f"step {step}: token {ids[0]} != {toks[step]}"
+        np.testing.assert_allclose(lg[golden["top_ids"][step]], golden["top_vals"][step], rtol=0, atol=LOGIT_TOL)
+        worst = max(worst, float(np.abs(lg[golden["top_ids"][step]] - golden["top_vals"][step]).max()))
+        if step in subs:
+            ref = golden["logits_sub"][subs[step]]
+            d = np.abs(lg[::64] - ref).max()
+            worst = max(worst, float(d))
+            assert d <= LOGIT_TOL, f"step {step}: logit subsample max diff {d}"
+        model.feed(int(toks[step]))
+        if step % 32 == 31:
+            print(f"[model] step {step}: worst logit diff so far {worst:.3e}", flush=True)
+    print(f"[model] worst logit diff over {toks.size} steps: {worst:.3e}", flush=True)
+
+
+def test_greedy_generate(model, golden):
+    """tmq_model_generate (graph-captured decode steps): the reference's tokens"""
+    model.set_graphs(True)
+    model.prompt(golden["prompt"])
+    got = model.generate(int(golden["tokens"].size))
+    exp = golden["tokens"]
+    assert np.array_equal(got, exp), f"first difference at {np.flatnonzero(got != exp)[:3]}"
+    h = model.hidden()
+    np.testing.assert_allclose(h, golden["hidden_final"], rtol=1e-4,
+                               atol=1e-4 * np.abs(golden["hidden_final"]).max())
+    assert model.position == 1 + exp.size
+
+
+def test_graphs_match_eager(model, golden):
+    """the captured step replays exactly what the eager launch sequence does"""
+    n = 8
+    res = []
+    for graphs in (False, True):
+        model.set_graphs(graphs)
+        model.prompt(golden["prompt"])
+        toks = model.generate(n)
+        res.append((toks, model.hidden(), model.logits()))
+    assert np.array_equal(res[0][0], res[1][0])
+    assert np.array_equal(res[0][1].view(np.uint32), res[1][1].view(np.uint32))
+    assert np.array_equal(res[0][2].view(np.uint32), res[1][2].view(np.uint32))
+
+
+def test_errors(model, golden):
+    import tmq
+    with pytest.raises(tmq.TmqError):
+        model.prompt(np.array([151936], dtype=np.int32))
+    with pytest.raises(tmq.TmqError):
+        model.prompt(np.zeros(513, dtype=np.int32))
+    model.prompt(golden["prompt"])
+    with pytest.raises(tmq.TmqError):
+        model.generate(512)  # positions 1..512 exceed max_seq 512
+    # still usable afterwards
+    model.prompt(golden["prompt"])
+    assert np.array_equal(model.generate(3), golden["tokens"][:3])
+
+
+def test_load_errors(ctx):
+    import tmq
+    from tmq import tmacfile
+    with pytest.raises(tmq.TmqError):
+        tmq.Model(ctx, b"NOPE" + b"\0" * 64)
+    with pytest.raises(tmq.TmqError):  # truncated
+        tmq.Model(ctx, b"TMAC" + (5).to_bytes(8, "little"))
+    # a model with only an embedding
+    emb = tmacfile.TmacTensor("token_embd.weight", 64, 64, tmacfile.Q8_0, np.zeros(64 * 2 * 34, np.uint8))
+    with pytest.raises(tmq.TmqError):
+        tmq.Model(ctx, tmacfile.to_bytes([emb]))

@@ -16,12 +16,13 @@
 
 #include "../../include/tmq.h"
 #include "tmq_internal.h"
+#include "tmq_runtime.h"
 
 namespace {
-
 thread_local std::string g_err;
+}  // namespace
 
-int fail(int code, const char* fmt, ...) {
+int tmq_fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -31,19 +32,7 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-#define HIP_TRY(expr)                                                                   \
-    do {                                                                                \
-        hipError_t e_ = (expr);                                                         \
-        if (e_ != hipSuccess)                                                           \
-            return fail(TMQ_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));   \
-    } while (0)
-
-#define LAUNCH_TRY(expr)                                                                \
-    do {                                                                                \
-        int e_ = (expr);                                                                \
-        if (e_ != 0)                                                                    \
-            return fail(TMQ_ERR_HIP, "%s: %s", #expr, hipGetErrorString((hipError_t)e_)); \
-    } while (0)
+namespace {
 
 int qk_of(uint32_t type) {
     switch (type) {
@@ -62,45 +51,11 @@ int block_bytes(uint32_t type) {
     }
 }
 
-// growable device buffer
-struct DevBuf {
-    void* p = nullptr;
-    size_t cap = 0;
-    int ensure(size_t n) {
-        if (n <= cap) return 0;
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        cap = 0;
-        hipError_t e = hipMalloc(&p, n);
-        if (e != hipSuccess) return fail(TMQ_ERR_NOMEM, "hipMalloc(%zu): %s", n, hipGetErrorString(e));
-        cap = n;
-        return 0;
-    }
-    void release() {
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        cap = 0;
-    }
-};
-
 struct Segment {
     int type, clamp, gmap_off, ngroups;
 };
 
 }  // namespace
-
-struct tmq_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    DevBuf x, y, act, acc, misc, works, gmap;
-};
-
-struct tmq_tensor {
-    tmq_ctx* ctx = nullptr;
-    TmqTensorDev dev{};
-    void* alloc = nullptr;  // planes + row_inv + row_scale
-    uint64_t weight_bytes = 0;
-};
 
 struct tmq_chain {
     tmq_ctx* ctx = nullptr;
@@ -113,12 +68,12 @@ struct tmq_chain {
     uint64_t weight_bytes = 0;
 };
 
-namespace {
-
-int set_device(tmq_ctx* ctx) {
+int tmq_rt_set_device(tmq_ctx* ctx) {
     HIP_TRY(hipSetDevice(ctx->device));
     return 0;
 }
+
+namespace {
 
 int groups_of(const TmqTensorDev& t) {
     int g64 = t.rows_pad / TMQ_ROWS_PER_GROUP;
@@ -129,15 +84,15 @@ int groups_of(const TmqTensorDev& t) {
 // Allocate planes + normalisers for a rows x cols tensor (zero filled).
 int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_tensor** out) {
     const int qk = qk_of(type);
-    if (!qk) return fail(TMQ_ERR_ARG, "unsupported tensor type %u", type);
+    if (!qk) return tmq_fail(TMQ_ERR_ARG, "unsupported tensor type %u", type);
     if (rows == 0 || cols == 0 || cols % qk)
-        return fail(TMQ_ERR_ARG, "shape %llux%llu invalid for type %u (cols %% %d)",
+        return tmq_fail(TMQ_ERR_ARG, "shape %llux%llu invalid for type %u (cols %% %d)",
                     (unsigned long long)rows, (unsigned long long)cols, type, qk);
     if (rows > (1u << 30) || cols > (1u << 20))
-        return fail(TMQ_ERR_ARG, "shape %llux%llu too large", (unsigned long long)rows,
+        return tmq_fail(TMQ_ERR_ARG, "shape %llux%llu too large", (unsigned long long)rows,
                     (unsigned long long)cols);
     if (type == TMQ_TYPE_Q8_0 && cols > 64 * TMQ_Q8_MAX_TILES)
-        return fail(TMQ_ERR_ARG, "Q8_0 cols %llu > %d", (unsigned long long)cols, 64 * TMQ_Q8_MAX_TILES);
+        return tmq_fail(TMQ_ERR_ARG, "Q8_0 cols %llu > %d", (unsigned long long)cols, 64 * TMQ_Q8_MAX_TILES);
     tmq_tensor* t = new tmq_tensor();
     t->ctx = ctx;
     TmqTensorDev& d = t->dev;
@@ -159,13 +114,13 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     hipError_t e = hipMalloc(&t->alloc, total);
     if (e != hipSuccess) {
         delete t;
-        return fail(TMQ_ERR_NOMEM, "hipMalloc(%zu) for tensor: %s", total, hipGetErrorString(e));
+        return tmq_fail(TMQ_ERR_NOMEM, "hipMalloc(%zu) for tensor: %s", total, hipGetErrorString(e));
     }
     e = hipMemsetAsync(t->alloc, 0, total, ctx->stream);
     if (e != hipSuccess) {
         (void)hipFree(t->alloc);
         delete t;
-        return fail(TMQ_ERR_HIP, "hipMemsetAsync: %s", hipGetErrorString(e));
+        return tmq_fail(TMQ_ERR_HIP, "hipMemsetAsync: %s", hipGetErrorString(e));
     }
     uint8_t* p = (uint8_t*)t->alloc;
     d.pa = p; p += al(sa);
@@ -186,15 +141,15 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
 int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
                   bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
                   const float* ext_row_inv, tmq_tensor** out) {
-    if (!ctx || !data || !out) return fail(TMQ_ERR_ARG, "null argument");
-    int rc = set_device(ctx);
+    if (!ctx || !data || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    int rc = tmq_rt_set_device(ctx);
     if (rc) return rc;
     tmq_tensor* t = nullptr;
     rc = tensor_alloc(ctx, type, rows, cols, &t);
     if (rc) return rc;
     if (n_bytes != t->weight_bytes) {
         tmq_tensor_free(t);
-        return fail(TMQ_ERR_ARG, "n_bytes %llu != %llu for %llux%llu type %u",
+        return tmq_fail(TMQ_ERR_ARG, "n_bytes %llu != %llu for %llux%llu type %u",
                     (unsigned long long)n_bytes, (unsigned long long)t->weight_bytes,
                     (unsigned long long)rows, (unsigned long long)cols, type);
     }
@@ -207,13 +162,13 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
     };
     if (!data_on_device) {
         hipError_t e = hipMalloc(&staging, n_bytes);
-        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_NOMEM, "staging hipMalloc: %s", hipGetErrorString(e)));
+        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_NOMEM, "staging hipMalloc: %s", hipGetErrorString(e)));
         e = hipMemcpyAsync(staging, data, n_bytes, hipMemcpyHostToDevice, ctx->stream);
-        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "staging copy: %s", hipGetErrorString(e)));
+        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "staging copy: %s", hipGetErrorString(e)));
         src = (const uint8_t*)staging;
     }
     int le = tmq_launch_repack((int)type, src, t->dev, ctx->stream);
-    if (le) return cleanup(fail(TMQ_ERR_HIP, "repack launch: %s", hipGetErrorString((hipError_t)le)));
+    if (le) return cleanup(tmq_fail(TMQ_ERR_HIP, "repack launch: %s", hipGetErrorString((hipError_t)le)));
     if (ext_row_inv) {
         t->dev.clamp = 1;
         std::vector<float> ri(t->dev.rows_pad, 1.0f);
@@ -221,7 +176,7 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
         hipError_t e = hipMemcpyAsync((void*)t->dev.row_inv, ri.data(), sizeof(float) * ri.size(),
                                       hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "row_inv copy: %s", hipGetErrorString(e)));
+        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "row_inv copy: %s", hipGetErrorString(e)));
         cleanup(0);
         *out = t;
         return 0;
@@ -238,7 +193,7 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
                 e = hipMemcpyAsync(aux_tmp, aux, sizeof(float) * rows, hipMemcpyHostToDevice, ctx->stream);
             if (e != hipSuccess) {
                 if (aux_tmp) (void)hipFree(aux_tmp);
-                return cleanup(fail(TMQ_ERR_HIP, "aux copy: %s", hipGetErrorString(e)));
+                return cleanup(tmq_fail(TMQ_ERR_HIP, "aux copy: %s", hipGetErrorString(e)));
             }
             aux_dev = (const float*)aux_tmp;
         }
@@ -256,8 +211,8 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
     if (e == hipSuccess) e = hipMemcpyAsync(&badh, bad, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (aux_tmp) (void)hipFree(aux_tmp);
-    if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "rowstat: %s", hipGetErrorString(e)));
-    if (badh) return cleanup(fail(TMQ_ERR_NONFINITE, "non-finite fp16 block scale in %llux%llu type %u tensor",
+    if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "rowstat: %s", hipGetErrorString(e)));
+    if (badh) return cleanup(tmq_fail(TMQ_ERR_NONFINITE, "non-finite fp16 block scale in %llux%llu type %u tensor",
                                   (unsigned long long)rows, (unsigned long long)cols, type));
     cleanup(0);
     *out = t;
@@ -335,7 +290,7 @@ int launch_segments(const std::vector<Segment>& segs, const void* works_dev, con
     for (const Segment& sg : segs) {
         int e = tmq_launch_chain(sg.type, sg.clamp, (const TmqWork*)works_dev,
                                  (const int32_t*)gmap_dev + sg.gmap_off, sg.ngroups, s);
-        if (e) return fail(TMQ_ERR_HIP, "chain segment launch: %s", hipGetErrorString((hipError_t)e));
+        if (e) return tmq_fail(TMQ_ERR_HIP, "chain segment launch: %s", hipGetErrorString((hipError_t)e));
     }
     return 0;
 }
@@ -347,6 +302,19 @@ inline uint32_t rd32(const uint8_t* p) {
 
 }  // namespace
 
+int tmq_rt_groups_of(const TmqTensorDev& t) { return groups_of(t); }
+
+int tmq_rt_tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
+                         bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
+                         tmq_tensor** out) {
+    return tensor_create(ctx, type, rows, cols, data, data_on_device, n_bytes, aux, aux_on_device,
+                         nullptr, out);
+}
+
+TmqWork tmq_rt_make_work(const tmq_tensor* t, const uint8_t* act, float* y, int64_t* acc) {
+    return make_work(t, act, y, acc);
+}
+
 // =========================================================================
 extern "C" {
 
@@ -354,22 +322,22 @@ const char* tmq_last_error(void) { return g_err.c_str(); }
 const char* tmq_version(void) { return "tmq 0.1 (gfx950)"; }
 
 int tmq_open(int device, tmq_ctx** out) {
-    if (!out) return fail(TMQ_ERR_ARG, "null out");
+    if (!out) return tmq_fail(TMQ_ERR_ARG, "null out");
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
-    if (e != hipSuccess || n <= 0) return fail(TMQ_ERR_NODEV, "no HIP device (%s)", hipGetErrorString(e));
-    if (device < 0 || device >= n) return fail(TMQ_ERR_ARG, "device %d out of range (%d devices)", device, n);
+    if (e != hipSuccess || n <= 0) return tmq_fail(TMQ_ERR_NODEV, "no HIP device (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= n) return tmq_fail(TMQ_ERR_ARG, "device %d out of range (%d devices)", device, n);
     hipDeviceProp_t prop;
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
-        return fail(TMQ_ERR_NODEV, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
+        return tmq_fail(TMQ_ERR_NODEV, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
     tmq_ctx* c = new tmq_ctx();
     c->device = device;
     e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete c;
-        return fail(TMQ_ERR_HIP, "stream create: %s", hipGetErrorString(e));
+        return tmq_fail(TMQ_ERR_HIP, "stream create: %s", hipGetErrorString(e));
     }
     *out = c;
     return 0;
@@ -379,7 +347,7 @@ int tmq_close(tmq_ctx* ctx) {
     if (!ctx) return 0;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (DevBuf* b : {&ctx->x, &ctx->y, &ctx->act, &ctx->acc, &ctx->misc, &ctx->works, &ctx->gmap}) b->release();
+    for (TmqDevBuf* b : {&ctx->x, &ctx->y, &ctx->act, &ctx->acc, &ctx->misc, &ctx->works, &ctx->gmap}) b->release();
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return 0;
@@ -388,7 +356,7 @@ int tmq_close(tmq_ctx* ctx) {
 void* tmq_stream(tmq_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
 
 int tmq_sync(tmq_ctx* ctx) {
-    if (!ctx) return fail(TMQ_ERR_ARG, "null ctx");
+    if (!ctx) return tmq_fail(TMQ_ERR_ARG, "null ctx");
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     return 0;
 }
@@ -417,7 +385,7 @@ int tmq_tensor_free(tmq_tensor* t) {
 
 int tmq_tensor_info(const tmq_tensor* t, uint32_t* type, uint64_t* rows, uint64_t* cols,
                     uint64_t* weight_bytes) {
-    if (!t) return fail(TMQ_ERR_ARG, "null tensor");
+    if (!t) return tmq_fail(TMQ_ERR_ARG, "null tensor");
     if (type) *type = (uint32_t)t->dev.type;
     if (rows) *rows = (uint64_t)t->dev.rows;
     if (cols) *cols = (uint64_t)t->dev.cols;
@@ -426,8 +394,8 @@ int tmq_tensor_info(const tmq_tensor* t, uint32_t* type, uint64_t* rows, uint64_
 }
 
 int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out) {
-    if (!ctx || !t || !out) return fail(TMQ_ERR_ARG, "null argument");
-    int rc = set_device(ctx);
+    if (!ctx || !t || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    int rc = tmq_rt_set_device(ctx);
     if (rc) return rc;
     const float* src = t->dev.type == TMQ_TYPE_Q8_0 ? t->dev.row_scale : t->dev.row_inv;
     HIP_TRY(hipMemcpyAsync(out, src, sizeof(float) * t->dev.rows, hipMemcpyDeviceToHost, ctx->stream));
@@ -436,8 +404,8 @@ int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out) {
 }
 
 int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev, int64_t* acc_dev) {
-    if (!ctx || !t || !x_dev) return fail(TMQ_ERR_ARG, "null argument");
-    int rc = set_device(ctx);
+    if (!ctx || !t || !x_dev) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    int rc = tmq_rt_set_device(ctx);
     if (!rc) rc = ctx->act.ensure(tmq_act_bytes(t->dev.cols));
     if (rc) return rc;
     TmqActJobs jobs{};
@@ -452,10 +420,10 @@ int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y
 }
 
 int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int rows, int cols) {
-    if (!ctx || !t || !x || !y) return fail(TMQ_ERR_ARG, "null argument");
+    if (!ctx || !t || !x || !y) return tmq_fail(TMQ_ERR_ARG, "null argument");
     if (rows != t->dev.rows || cols != t->dev.cols)
-        return fail(TMQ_ERR_ARG, "shape %dx%d does not match tensor %dx%d", rows, cols, t->dev.rows, t->dev.cols);
-    int rc = set_device(ctx);
+        return tmq_fail(TMQ_ERR_ARG, "shape %dx%d does not match tensor %dx%d", rows, cols, t->dev.rows, t->dev.cols);
+    int rc = tmq_rt_set_device(ctx);
     if (!rc) rc = ctx->x.ensure(sizeof(float) * cols);
     if (!rc) rc = ctx->y.ensure(sizeof(float) * rows);
     if (rc) return rc;
@@ -469,13 +437,13 @@ int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int 
 
 int tmq_gemv_partials(tmq_ctx* ctx, const tmq_tensor* t, const float* x, int64_t* acc,
                       uint64_t acc_len, float* x_scale) {
-    if (!ctx || !t || !x || !acc) return fail(TMQ_ERR_ARG, "null argument");
+    if (!ctx || !t || !x || !acc) return tmq_fail(TMQ_ERR_ARG, "null argument");
     const uint64_t need = t->dev.type == TMQ_TYPE_Q8_0
                               ? (uint64_t)t->dev.rows * ((t->dev.cols + 63) / 64)
                               : (uint64_t)t->dev.rows;
-    if (acc_len < need) return fail(TMQ_ERR_ARG, "acc_len %llu < %llu", (unsigned long long)acc_len,
+    if (acc_len < need) return tmq_fail(TMQ_ERR_ARG, "acc_len %llu < %llu", (unsigned long long)acc_len,
                                     (unsigned long long)need);
-    int rc = set_device(ctx);
+    int rc = tmq_rt_set_device(ctx);
     if (!rc) rc = ctx->x.ensure(sizeof(float) * t->dev.cols);
     if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * need);
     if (rc) return rc;
@@ -491,8 +459,8 @@ int tmq_gemv_partials(tmq_ctx* ctx, const tmq_tensor* t, const float* x, int64_t
 // ---------------------------------------------------------------- tiles
 int tmq_vecmul_tile_q8(tmq_ctx* ctx, const uint8_t* q8_W, const uint16_t* cs, const int16_t* vec,
                        int64_t* result) {
-    if (!ctx || !q8_W || !cs || !vec || !result) return fail(TMQ_ERR_ARG, "null argument");
-    int rc = set_device(ctx);
+    if (!ctx || !q8_W || !cs || !vec || !result) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    int rc = tmq_rt_set_device(ctx);
     if (!rc) rc = ctx->misc.ensure(4096 + 256 + 128 + 512);
     if (rc) return rc;
     uint8_t* p = (uint8_t*)ctx->misc.p;
@@ -508,7 +476,7 @@ int tmq_vecmul_tile_q8(tmq_ctx* ctx, const uint8_t* q8_W, const uint16_t* cs, co
 
 int tmq_vecmul_tile_q5_0_8x896(tmq_ctx* ctx, const uint8_t* blocks, const int16_t* act,
                                const float* row_inv, int64_t* result, int row_base) {
-    if (!ctx || !blocks || !act || !row_inv || !result) return fail(TMQ_ERR_ARG, "null argument");
+    if (!ctx || !blocks || !act || !row_inv || !result) return tmq_fail(TMQ_ERR_ARG, "null argument");
     tmq_tensor* t = nullptr;
     int rc = tensor_create(ctx, TMQ_TYPE_Q5_0, 8, 896, blocks, false, 224 * 22, nullptr, false, row_inv, &t);
     if (rc) return rc;
@@ -523,8 +491,8 @@ int tmq_vecmul_tile_q5_0_8x896(tmq_ctx* ctx, const uint8_t* blocks, const int16_
 static int tile_kquant(tmq_ctx* ctx, uint32_t type, const uint8_t* blocks, int nblocks,
                        const int16_t* act, int ncols, const float* row_inv, int64_t* result,
                        int row_base) {
-    if (!ctx || !blocks || !act || !row_inv || !result) return fail(TMQ_ERR_ARG, "null argument");
-    if (nblocks <= 0 || ncols < 0) return fail(TMQ_ERR_ARG, "nblocks %d ncols %d", nblocks, ncols);
+    if (!ctx || !blocks || !act || !row_inv || !result) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (nblocks <= 0 || ncols < 0) return tmq_fail(TMQ_ERR_ARG, "nblocks %d ncols %d", nblocks, ncols);
     tmq_tensor* t = nullptr;
     int rc = tensor_create(ctx, type, (uint64_t)nblocks, 256, blocks, false,
                            (uint64_t)nblocks * block_bytes(type), nullptr, false, row_inv + row_base, &t);
@@ -553,8 +521,8 @@ int tmq_vecmul_tile_q4k(tmq_ctx* ctx, const uint8_t* blocks, int nblocks, const 
 
 // ---------------------------------------------------------------- chains
 int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out) {
-    if (!ctx || !descs || n <= 0 || !out) return fail(TMQ_ERR_ARG, "bad chain arguments");
-    int rc = set_device(ctx);
+    if (!ctx || !descs || n <= 0 || !out) return tmq_fail(TMQ_ERR_ARG, "bad chain arguments");
+    int rc = tmq_rt_set_device(ctx);
     if (rc) return rc;
     tmq_chain* ch = new tmq_chain();
     ch->ctx = ctx;
@@ -566,14 +534,14 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
         const tmq_tensor* t = d.weight;
         if (!t || !d.x_dev) {
             delete ch;
-            return fail(TMQ_ERR_DESC, "descriptor %d: null weight or x", i);
+            return tmq_fail(TMQ_ERR_DESC, "descriptor %d: null weight or x", i);
         }
         const TmqTensorDev& td = t->dev;
         long rows;
         if (td.type == TMQ_TYPE_Q4_K || td.type == TMQ_TYPE_Q6_K) {
             if (d.num_col_groups == 0 || d.num_tiles % d.num_col_groups || d.num_col_groups * 256 != td.cols) {
                 delete ch;
-                return fail(TMQ_ERR_DESC, "descriptor %d: num_col_groups %d / num_tiles %d inconsistent with cols %d",
+                return tmq_fail(TMQ_ERR_DESC, "descriptor %d: num_col_groups %d / num_tiles %d inconsistent with cols %d",
                             i, d.num_col_groups, d.num_tiles, td.cols);
             }
             rows = (long)(d.num_tiles / d.num_col_groups) * d.tile_res_rows;
@@ -582,13 +550,13 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
         }
         if (rows != td.rows) {
             delete ch;
-            return fail(TMQ_ERR_DESC, "descriptor %d: tiles give %ld rows, tensor has %d", i, rows, td.rows);
+            return tmq_fail(TMQ_ERR_DESC, "descriptor %d: tiles give %ld rows, tensor has %d", i, rows, td.rows);
         }
         auto it = xs.find(d.x_dev);
         if (it == xs.end()) {
             if ((int)xs.size() >= TMQ_MAX_ACT) {
                 delete ch;
-                return fail(TMQ_ERR_DESC, "more than %d distinct activations in one chain", TMQ_MAX_ACT);
+                return tmq_fail(TMQ_ERR_DESC, "more than %d distinct activations in one chain", TMQ_MAX_ACT);
             }
             int id = (int)xs.size();
             xs[d.x_dev] = id;
@@ -598,7 +566,7 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
             act_of[i] = it->second;
             if (ncols_of[it->second] != td.cols) {
                 delete ch;
-                return fail(TMQ_ERR_DESC, "descriptor %d: activation shared with a different width", i);
+                return tmq_fail(TMQ_ERR_DESC, "descriptor %d: activation shared with a different width", i);
             }
         }
     }
@@ -612,7 +580,7 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
     hipError_t e = hipMalloc(&ch->act_dev, act_total);
     if (e != hipSuccess) {
         delete ch;
-        return fail(TMQ_ERR_NOMEM, "chain act alloc: %s", hipGetErrorString(e));
+        return tmq_fail(TMQ_ERR_NOMEM, "chain act alloc: %s", hipGetErrorString(e));
     }
     ch->jobs.count = (int)xs.size();
     for (auto& kv : xs) {
@@ -637,20 +605,20 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
         e = hipMemcpy(ch->gmap_dev, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         tmq_chain_free(ch);
-        return fail(TMQ_ERR_NOMEM, "chain alloc: %s", hipGetErrorString(e));
+        return tmq_fail(TMQ_ERR_NOMEM, "chain alloc: %s", hipGetErrorString(e));
     }
     *out = ch;
     return 0;
 }
 
 int tmq_chain_prepare(tmq_ctx* ctx, tmq_chain* ch) {
-    if (!ctx || !ch) return fail(TMQ_ERR_ARG, "null argument");
+    if (!ctx || !ch) return tmq_fail(TMQ_ERR_ARG, "null argument");
     LAUNCH_TRY(tmq_launch_act_prep(ch->jobs, ctx->stream));
     return 0;
 }
 
 int tmq_chain_launch(tmq_ctx* ctx, tmq_chain* ch) {
-    if (!ctx || !ch) return fail(TMQ_ERR_ARG, "null argument");
+    if (!ctx || !ch) return tmq_fail(TMQ_ERR_ARG, "null argument");
     return launch_segments(ch->segs, ch->works_dev, ch->gmap_dev, ctx->stream);
 }
 
@@ -680,8 +648,8 @@ uint64_t tmq_chain_weight_bytes(const tmq_chain* ch) { return ch ? ch->weight_by
 // in one chain launch; results land in the arena at result_addr.
 int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t arena_base,
                    uint32_t head_off, uint32_t* rows_out, int max_desc) {
-    if (!ctx || !arena) return fail(TMQ_ERR_ARG, "null argument");
-    int rc = set_device(ctx);
+    if (!ctx || !arena) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    int rc = tmq_rt_set_device(ctx);
     if (rc) return rc;
     auto in_arena = [&](uint64_t off, uint64_t len) {
         return off >= arena_base && off - arena_base + len <= arena_bytes;
@@ -702,8 +670,8 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
     uint32_t off = head_off;
     int walked = 0;
     while (off) {
-        if (walked >= (1 << 16)) return cleanup(fail(TMQ_ERR_DESC, "descriptor chain longer than 65536 (cycle?)"));
-        if (!in_arena(off, 32)) return cleanup(fail(TMQ_ERR_DESC, "descriptor at 0x%x outside arena", off));
+        if (walked >= (1 << 16)) return cleanup(tmq_fail(TMQ_ERR_DESC, "descriptor chain longer than 65536 (cycle?)"));
+        if (!in_arena(off, 32)) return cleanup(tmq_fail(TMQ_ERR_DESC, "descriptor at 0x%x outside arena", off));
         const uint8_t* d = arena + (off - arena_base);
         const uint32_t next = rd32(d), wa = rd32(d + 4), aa = rd32(d + 8), ra = rd32(d + 12);
         const int nt = rd16(d + 0x10), tb = rd16(d + 0x12), type = d[0x14], tr = d[0x15];
@@ -713,10 +681,10 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
             // sim tile: 8 rows x 896 (224 blocks) + row_inv section; replay
             // recomputes row_inv per tile (sim/tmac_gguf.cpp:766-777)
             if (tr != 8 || tb < 224 * 22)
-                return cleanup(fail(TMQ_ERR_DESC, "Q5_0 descriptor at 0x%x: tile_res_rows %d / tile_bytes %d not the 8x896 tile", off, tr, tb));
+                return cleanup(tmq_fail(TMQ_ERR_DESC, "Q5_0 descriptor at 0x%x: tile_res_rows %d / tile_bytes %d not the 8x896 tile", off, tr, tb));
             nrows = nt * tr;
             if (!in_arena(wa, (uint64_t)nt * tb) || !in_arena(aa, 896 * 2) || !in_arena(ra, (uint64_t)nrows * 8))
-                return cleanup(fail(TMQ_ERR_DESC, "Q5_0 descriptor at 0x%x: address out of arena", off));
+                return cleanup(tmq_fail(TMQ_ERR_DESC, "Q5_0 descriptor at 0x%x: address out of arena", off));
             std::vector<uint8_t> w((size_t)nt * 224 * 22);
             for (int ti = 0; ti < nt; ti++)
                 memcpy(w.data() + (size_t)ti * 224 * 22, arena + (wa - arena_base) + (size_t)ti * tb, 224 * 22);
@@ -734,13 +702,13 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
             const bool k6 = type == TMQ_TYPE_Q6_K;
             const int bb = k6 ? 210 : 144, blk_bytes = k6 ? 32 * 210 : 56 * 144;
             if (cg == 0 || tr == 0 || nt % cg)
-                return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: num_col_groups %d tile_res_rows %d num_tiles %d", off, cg, tr, nt));
+                return cleanup(tmq_fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: num_col_groups %d tile_res_rows %d num_tiles %d", off, cg, tr, nt));
             if (tb < blk_bytes + tr * 4 || tr * bb > blk_bytes)
-                return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: tile_bytes %d too small", off, tb));
+                return cleanup(tmq_fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: tile_bytes %d too small", off, tb));
             nrows = (nt / cg) * tr;
             const int cols = cg * 256;
             if (!in_arena(wa, (uint64_t)nt * tb) || !in_arena(aa, (uint64_t)cols * 2) || !in_arena(ra, (uint64_t)nrows * 8))
-                return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: address out of arena", off));
+                return cleanup(tmq_fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: address out of arena", off));
             std::vector<uint8_t> w((size_t)nrows * cg * bb);
             std::vector<float> ri(nrows, 0.0f);
             std::vector<char> seen(nrows, 0);
@@ -751,7 +719,7 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
                     memcpy(w.data() + ((size_t)(row0 + i) * cg + cgi) * bb, tile + (size_t)i * bb, bb);
                     float v = (float)rd32(tile + blk_bytes + i * 4) / 256.0f;  // UQ24.8 (:791-795)
                     if (seen[row0 + i] && ri[row0 + i] != v)
-                        return cleanup(fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: row %d has differing row_inv across tiles", off, row0 + i));
+                        return cleanup(tmq_fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: row %d has differing row_inv across tiles", off, row0 + i));
                     ri[row0 + i] = v;
                     seen[row0 + i] = 1;
                 }
@@ -791,7 +759,7 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
         for (size_t i = 0; i < items.size(); i++) {
             hipError_t e = hipMemcpyAsync((uint8_t*)ctx->act.p + aoff[i], items[i].act.data(), items[i].act.size(),
                                           hipMemcpyHostToDevice, ctx->stream);
-            if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "act copy: %s", hipGetErrorString(e)));
+            if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "act copy: %s", hipGetErrorString(e)));
             works.push_back(make_work(items[i].t, (const uint8_t*)ctx->act.p + aoff[i], nullptr,
                                       (int64_t*)ctx->acc.p + coff[i]));
         }
@@ -803,13 +771,13 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
                                       hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess)
             e = hipMemcpyAsync(ctx->gmap.p, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice, ctx->stream);
-        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "chain upload: %s", hipGetErrorString(e)));
+        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "chain upload: %s", hipGetErrorString(e)));
         int le = launch_segments(segs, ctx->works.p, ctx->gmap.p, ctx->stream);
         if (le) return cleanup(le);
         std::vector<int64_t> acc(acc_total);
         e = hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc_total, hipMemcpyDeviceToHost, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess) return cleanup(fail(TMQ_ERR_HIP, "chain results: %s", hipGetErrorString(e)));
+        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "chain results: %s", hipGetErrorString(e)));
         for (size_t i = 0; i < items.size(); i++) {
             uint8_t* dst = arena + (items[i].result_addr - arena_base);
             for (int r = 0; r < items[i].nrows; r++) {

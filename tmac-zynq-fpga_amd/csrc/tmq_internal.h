@@ -44,13 +44,50 @@ struct TmqTensorDev {
 // sum w*xq = 256*sum w*xh + sum w*xl with every partial inside int32.
 static inline uint64_t tmq_act_bytes(int n) { return 16 + (uint64_t)n * 6 + 16; }
 
+// One GEMV of a chain.  The output epilogue of row r is
+//     v = finalize(acc_r);  if (bias) v = v + bias[r];  if (resid) v = y[r] + v;
+//     y[r] = v
+// (bias: sim/tmac_gguf.cpp:1595-1597; residual: :1663, :1706).
 struct TmqWork {
     TmqTensorDev t;
     const uint8_t* act;
-    float* y;        // may be null
-    int64_t* acc;    // may be null; Q8_0: [rows][ntiles]
+    float* y;            // may be null
+    int64_t* acc;        // may be null; Q8_0: [rows][ntiles]
+    const float* bias;   // may be null
+    uint64_t* cand;      // Q8_0, engine GEMV: per-wave argmax candidate keys (may be null)
     int32_t first_group;
-    int32_t ngroups;
+    int32_t ngroups;     // row groups (workgroups) of this GEMV
+    int32_t resid;
+    int32_t pad_;
+};
+
+// Decode-engine state in device memory.  pos = the position being processed
+// (-1 after a reset); it is advanced by the first kernel of a step, so a
+// captured step replays without host involvement.  err != 0 stops the step.
+struct TmqEngState {
+    int32_t pos;
+    int32_t err;
+    int32_t pad_[2];
+};
+
+// Activation recipe of an engine GEMV launch: every workgroup computes the
+// int16 activation of its launch into LDS before its row groups (the
+// reference's rms_norm / silu / matmul quantisation, sim/tmac_gguf.cpp:415-439,
+// :1225-1231), so no separate normalisation launch is needed.
+enum { TMQ_ACT_NORM = 0, TMQ_ACT_PLAIN = 1, TMQ_ACT_SILU = 2, TMQ_ACT_EMBED_NORM = 3 };
+#define TMQ_ENG_MAXN 6144
+struct TmqEngAct {
+    int32_t mode;
+    int32_t n;
+    const float* x;        // NORM / PLAIN: input vector; SILU: gate
+    const float* x2;       // SILU: up
+    const float* w;        // NORM / EMBED_NORM: RMSNorm weight
+    float eps;
+    int32_t pad_;
+    TmqEngState* state;    // EMBED_NORM: token = tokens[state->pos]
+    const int32_t* tokens;
+    float* hidden_out;     // EMBED_NORM: embedding row (written by workgroup 0)
+    TmqTensorDev emb;      // EMBED_NORM: quantized embedding
 };
 
 // Activation-quantisation jobs: one workgroup each, at most TMQ_MAX_ACT per launch.
@@ -79,5 +116,10 @@ int tmq_launch_gemv(const TmqWork& w, hipStream_t s);
 // one launch per chain segment (descriptors of one format / clamp mode)
 int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_t* group_work_dev,
                      int total_groups, hipStream_t s);
+// engine GEMV: activation recipe + works of any formats; waves = 16 (K split
+// over the waves of a workgroup) or 4
+int tmq_launch_eng_gemv(const TmqEngAct& act, const TmqWork* works_dev, const int32_t* group_work_dev,
+                        int total_groups, int waves, hipStream_t s);
+size_t tmq_eng_lds_bytes(int n, int waves);
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s);

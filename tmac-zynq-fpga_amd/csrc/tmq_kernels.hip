@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include "tmq_internal.h"
+#include "tmq_mathf.h"
 
 typedef short tmq_s16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 tmq_h2 __attribute__((ext_vector_type(2)));
@@ -97,11 +98,19 @@ __device__ __forceinline__ tmq_h2 lanes23(uint32_t w) {
     return __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0u, w, 0x0c030c02u));
 }
 
-struct Act {
+// Activation view: x_scale and the XH/XL pair arrays, read either through
+// the scalar cache (standalone GEMVs: a prepared activation in HBM) or from
+// LDS (engine GEMVs: each workgroup quantises its activation itself).
+typedef __attribute__((address_space(3))) const uint32_t lu32;
+template <class P>
+struct ActT {
     float xs;
-    const cu32* xh;
-    const cu32* xl;
+    P xh;
+    P xl;
 };
+typedef ActT<const cu32*> Act;
+typedef ActT<const lu32*> ActL;
+
 __device__ __forceinline__ Act act_view(const uint8_t* a) {
     const cu32* p = (const cu32*)a;
     Act r;
@@ -118,9 +127,9 @@ __device__ __forceinline__ size_t p16(int b, int c, int C, size_t R, int r) {
 
 // 4 weights (quantised value u_k, normaliser E_k = f(u_k)) -> two int16
 // pairs -> dot with the activation pairs kx, kx+1
-template <bool CLAMP>
+template <bool CLAMP, class AT>
 __device__ __forceinline__ void mac4(float e0, float e1, float e2, float e3, float inv,
-                                     const Act& A, int kx, int& sh, int& sl) {
+                                     const AT& A, int kx, int& sh, int& sl) {
     const uint32_t P0 = pk16(wq<CLAMP>(e0 * inv), wq<CLAMP>(e1 * inv));
     const uint32_t P1 = pk16(wq<CLAMP>(e2 * inv), wq<CLAMP>(e3 * inv));
     sh = dot2(P0, A.xh[kx], sh);
@@ -129,24 +138,35 @@ __device__ __forceinline__ void mac4(float e0, float e1, float e2, float e3, flo
     sl = dot2(P1, A.xl[kx + 1], sl);
 }
 
+// Each format: Blk = one block of one row in registers, blk_load() fetches
+// it from the planes, blk_mac() multiplies it into the pair sums.
+
 // ---------------------------------------------------------------- Q5_0
 // Planes: qs[16] as in ggml; qh' = qh with its bits transposed so that bit
 // (8k + g) holds the high bit of element 4g + k; d f16.  Group g of four
 // weights (elements 4g..4g+3) is decoded SWAR-style into four bytes
 // u = nibble | hb<<4, spread into f16 lanes 0x6400|u (= 1024+u) and turned
 // into E = (u-16)*d exactly by one v_fma_mix: (1024+u)*d - 1040*d.
-template <bool CLAMP>
-__device__ __forceinline__ void q5_0_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                           float inv, int& sh, int& sl) {
+struct Q5Blk {
+    uint4 qs;
+    uint32_t qh, d;
+};
+__device__ __forceinline__ Q5Blk q5_load(const TmqTensorDev& t, int b, int r) {
     const size_t o = (size_t)b * t.rows_pad + r;
-    const uint4 qs = ld16(t.pa + o * 16);
-    const uint32_t qhp = ld4(t.pb + o * 4);
-    const float d = h2f(ld2(t.pd + o * 2));
+    Q5Blk k;
+    k.qs = ld16(t.pa + o * 16);
+    k.qh = ld4(t.pb + o * 4);
+    k.d = ld2(t.pd + o * 2);
+    return k;
+}
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q5_mac(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
+    const float d = h2f(k.d);
     const float c = -1040.0f * d;  // exact: 7-bit x 11-bit
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-        const uint32_t nib = (g < 4) ? (dw_of(qs, g) & 0x0f0f0f0fu) : ((dw_of(qs, g - 4) >> 4) & 0x0f0f0f0fu);
-        const uint32_t hs = (g <= 4) ? (qhp << (4 - g)) : (qhp >> (g - 4));
+        const uint32_t nib = (g < 4) ? (dw_of(k.qs, g) & 0x0f0f0f0fu) : ((dw_of(k.qs, g - 4) >> 4) & 0x0f0f0f0fu);
+        const uint32_t hs = (g <= 4) ? (k.qh << (4 - g)) : (k.qh >> (g - 4));
         const uint32_t U = (hs & 0x10101010u) | nib;
         const tmq_h2 v0 = __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0x64646464u, U, 0x04010400u));
         const tmq_h2 v1 = __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0x64646464u, U, 0x04030402u));
@@ -173,22 +193,31 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& h, int s, int& sc, in
 // into f16 lanes as subnormals q*2^-24 (low nibbles) and 16q*2^-24 (high
 // nibbles, masked in place), so E = fma_mix(lane, A*2^24 or A*2^20, -B):
 // the scalings by powers of two are exact and the product is A*q exactly.
-template <bool CLAMP>
-__device__ __forceinline__ void q4_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                           float inv, int& sh, int& sl) {
+struct Q4KBlk {
+    uint4 h;
+    uint4 qs[8];
+};
+__device__ __forceinline__ Q4KBlk q4k_load(const TmqTensorDev& t, int b, int r) {
     const size_t R = t.rows_pad;
-    const uint4 h = ld16(t.pb + p16(b, 0, 1, R, r));
-    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+    Q4KBlk k;
+    k.h = ld16(t.pb + p16(b, 0, 1, R, r));
+#pragma unroll
+    for (int i = 0; i < 8; i++) k.qs[i] = ld16(t.pa + p16(b, i, 8, R, r));
+    return k;
+}
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q4k_mac(const Q4KBlk& k, const AT& A, int b, float inv, int& sh, int& sl) {
+    const float d = h2f(k.h.x), dmin = h2f(k.h.x >> 16);
 #pragma unroll
     for (int sp = 0; sp < 4; sp++) {
         int sc0, m0, sc1, m1;
-        q4k_scale_min(h, 2 * sp, sc0, m0);
-        q4k_scale_min(h, 2 * sp + 1, sc1, m1);
+        q4k_scale_min(k.h, 2 * sp, sc0, m0);
+        q4k_scale_min(k.h, 2 * sp + 1, sc1, m1);
         const float A0 = (d * (float)sc0) * 0x1p24f, B0 = -(dmin * (float)m0);
         const float A1 = (d * (float)sc1) * 0x1p20f, B1 = -(dmin * (float)m1);
 #pragma unroll
         for (int hf = 0; hf < 2; hf++) {
-            const uint4 qs = ld16(t.pa + p16(b, 2 * sp + hf, 8, R, r));
+            const uint4& qs = k.qs[2 * sp + hf];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t w = dw_of(qs, i);
@@ -209,22 +238,36 @@ __device__ __forceinline__ void q4_k_block(const TmqTensorDev& t, const Act& A, 
 // ---------------------------------------------------------------- Q6_K
 // u6 = ql nibble | (qh 2 bits) << 4, built four at a time in byte lanes;
 // E = S*(u-32) exactly (S = d*sc has <= 18 significant bits, u-32 <= 6).
-template <bool CLAMP>
-__device__ __forceinline__ void q6_k_block(const TmqTensorDev& t, const Act& A, int b, int r,
-                                           float inv, int& sh, int& sl) {
+struct Q6KBlk {
+    uint4 ql[8];
+    uint4 qh[4];
+    uint4 sc;
+    uint32_t d;
+};
+__device__ __forceinline__ Q6KBlk q6k_load(const TmqTensorDev& t, int b, int r) {
     const size_t R = t.rows_pad;
-    const uint4 sc = ld16(t.pc + p16(b, 0, 1, R, r));
-    const float ss = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
+    Q6KBlk k;
+#pragma unroll
+    for (int i = 0; i < 8; i++) k.ql[i] = ld16(t.pa + p16(b, i, 8, R, r));
+#pragma unroll
+    for (int i = 0; i < 4; i++) k.qh[i] = ld16(t.pb + p16(b, i, 4, R, r));
+    k.sc = ld16(t.pc + p16(b, 0, 1, R, r));
+    k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
+    return k;
+}
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q6k_mac(const Q6KBlk& k, const AT& A, int b, float inv, int& sh, int& sl) {
+    const float ss = h2f(k.d);
 #pragma unroll
     for (int half = 0; half < 2; half++) {
 #pragma unroll
         for (int lc = 0; lc < 2; lc++) {
-            const uint4 qla = ld16(t.pa + p16(b, half * 4 + lc, 8, R, r));
-            const uint4 qlb = ld16(t.pa + p16(b, half * 4 + 2 + lc, 8, R, r));
-            const uint4 qhc = ld16(t.pb + p16(b, half * 2 + lc, 4, R, r));
+            const uint4& qla = k.ql[half * 4 + lc];
+            const uint4& qlb = k.ql[half * 4 + 2 + lc];
+            const uint4& qhc = k.qh[half * 2 + lc];
 #pragma unroll
             for (int sub = 0; sub < 4; sub++) {
-                const float S = ss * (float)(int8_t)byte_of(sc, half * 8 + lc + 2 * sub);
+                const float S = ss * (float)(int8_t)byte_of(k.sc, half * 8 + lc + 2 * sub);
                 const float nS = -32.0f * S, S24 = S * 0x1p24f;
                 const uint4& src = (sub & 1) ? qlb : qla;
 #pragma unroll
@@ -243,6 +286,25 @@ __device__ __forceinline__ void q6_k_block(const TmqTensorDev& t, const Act& A, 
             }
         }
     }
+}
+
+// format dispatch for the K-split group code
+template <int FMT> struct BlkOf;
+template <> struct BlkOf<kQ5_0> { typedef Q5Blk T; };
+template <> struct BlkOf<kQ4_K> { typedef Q4KBlk T; };
+template <> struct BlkOf<kQ6_K> { typedef Q6KBlk T; };
+template <int FMT>
+__device__ __forceinline__ typename BlkOf<FMT>::T blk_load(const TmqTensorDev& t, int b, int r) {
+    if constexpr (FMT == kQ5_0) return q5_load(t, b, r);
+    else if constexpr (FMT == kQ4_K) return q4k_load(t, b, r);
+    else return q6k_load(t, b, r);
+}
+template <int FMT, bool CLAMP, class AT>
+__device__ __forceinline__ void blk_mac(const typename BlkOf<FMT>::T& k, const AT& A, int b, float inv,
+                                        int& sh, int& sl) {
+    if constexpr (FMT == kQ5_0) q5_mac<CLAMP>(k, A, b, inv, sh, sl);
+    else if constexpr (FMT == kQ4_K) q4k_mac<CLAMP>(k, A, b, inv, sh, sl);
+    else q6k_mac<CLAMP>(k, A, b, inv, sh, sl);
 }
 
 // ---------------------------------------------------------------- Q8_0
@@ -270,7 +332,8 @@ __device__ __forceinline__ Q8Blk q8_load(const TmqTensorDev& t, int b, int r) {
     k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
     return k;
 }
-__device__ __forceinline__ void q8_mac(const Q8Blk& k, const Act& A, int b, float ri, int& sh, int& sl) {
+template <class AT>
+__device__ __forceinline__ void q8_mac(const Q8Blk& k, const AT& A, int b, float ri, int& sh, int& sl) {
     const int cs = (int)q8_cs(h2f(k.d), ri);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
@@ -284,48 +347,54 @@ __device__ __forceinline__ void q8_mac(const Q8Blk& k, const Act& A, int b, floa
 }
 
 // ------------------------------------------------------------ row groups
+// Output epilogue shared by all formats: bias, then residual (TmqWork).
+__device__ __forceinline__ void store_y(const TmqWork& w, int r, float v) {
+    if (w.bias) v = v + w.bias[r];
+    if (w.resid) v = w.y[r] + v;
+    w.y[r] = v;
+}
+
 // K-split group (Q5_0 / K-quants): 4 waves share 64 rows, wave w takes
-// blocks w, w+4, ...; the int32 pair sums are folded into int64 every
-// 256 weights at most (|sum| < 2^31), then the waves meet in LDS.
+// blocks w, w+4, ...; the int32 pair sums are folded into int64 every 256
+// weights at most (|sum| < 2^31), then the waves meet in LDS.
 template <int FMT, bool CLAMP>
 __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
     __shared__ int64_t part[TMQ_WAVES][64];
     const TmqTensorDev& t = w.t;
+    const int b0 = 0, b1 = t.nb;
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
     const float inv = t.row_inv[r];
     const Act A = act_view(w.act);
     int64_t acc = 0;
     if (FMT == kQ5_0) {
-        int b = wave;
-        for (; b + TMQ_WAVES < t.nb; b += 2 * TMQ_WAVES) {
+        int b = b0 + wave;
+        for (; b + TMQ_WAVES < b1; b += 2 * TMQ_WAVES) {
             int sh = 0, sl = 0;
-            q5_0_block<CLAMP>(t, A, b, r, inv, sh, sl);
-            q5_0_block<CLAMP>(t, A, b + TMQ_WAVES, r, inv, sh, sl);
+            q5_mac<CLAMP>(q5_load(t, b, r), A, b, inv, sh, sl);
+            q5_mac<CLAMP>(q5_load(t, b + TMQ_WAVES, r), A, b + TMQ_WAVES, inv, sh, sl);
             acc += (int64_t)sh * 256 + sl;
         }
-        if (b < t.nb) {
+        if (b < b1) {
             int sh = 0, sl = 0;
-            q5_0_block<CLAMP>(t, A, b, r, inv, sh, sl);
+            q5_mac<CLAMP>(q5_load(t, b, r), A, b, inv, sh, sl);
             acc += (int64_t)sh * 256 + sl;
         }
     } else {
-        for (int b = wave; b < t.nb; b += TMQ_WAVES) {
+        for (int b = b0 + wave; b < b1; b += TMQ_WAVES) {
             int sh = 0, sl = 0;
-            if (FMT == kQ4_K) q4_k_block<CLAMP>(t, A, b, r, inv, sh, sl);
-            if (FMT == kQ6_K) q6_k_block<CLAMP>(t, A, b, r, inv, sh, sl);
+            blk_mac<FMT, CLAMP>(blk_load<FMT>(t, b, r), A, b, inv, sh, sl);
             acc += (int64_t)sh * 256 + sl;
         }
     }
     part[wave][lane] = acc;
     __syncthreads();
+    int64_t tot = 0;
+    if (wave == 0) tot = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
     if (wave == 0 && r < t.rows) {
-        int64_t tot = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
         if (w.acc) w.acc[r] = tot;
-        if (w.y) {
-            // sim/tmac_gguf.cpp:1303-1305: y = 0.0f; y += (double)acc*x_scale/(double)row_inv
-            w.y[r] = (float)(((double)tot * (double)A.xs) / (double)inv);
-        }
+        // sim/tmac_gguf.cpp:1303-1305: y = 0.0f; y += (double)acc*x_scale/(double)row_inv
+        if (w.y) store_y(w, r, (float)(((double)tot * (double)A.xs) / (double)inv));
     }
 }
 
@@ -361,12 +430,12 @@ __device__ __forceinline__ void group_q8(const TmqWork& w, int g) {
         if (w.acc && r < t.rows) w.acc[(size_t)r * nt + tt] = P;
         y = (float)((double)y + ((double)P * (double)A.xs) * (double)rs);
     }
-    if (w.y && r < t.rows) w.y[r] = y;
+    if (w.y && r < t.rows) store_y(w, r, y);
 }
 
 template <int FMT, bool CLAMP>
 __device__ __forceinline__ void run_group(const TmqWork& w, int g) {
-    if (FMT == kQ8_0) group_q8(w, g);
+    if constexpr (FMT == kQ8_0) group_q8(w, g);
     else group_ksplit<FMT, CLAMP>(w, g);
 }
 
@@ -383,6 +452,272 @@ __global__ __launch_bounds__(TMQ_WG) void chain_kernel(const TmqWork* __restrict
                                                        const int32_t* __restrict__ group_work) {
     const TmqWork& w = works[group_work[blockIdx.x]];
     run_group<FMT, CLAMP>(w, blockIdx.x - w.first_group);
+}
+
+// ------------------------------------------------------------ engine GEMV
+// One launch = one activation recipe (TmqEngAct) + row groups of works of
+// any formats.  Every workgroup first issues the loads of its first weight
+// block(s), then computes the launch's activation into LDS (the loads are in
+// flight meanwhile), then multiplies.  K is split over the NW waves of the
+// workgroup (Q5_0 / K-quants); a Q8_0 wave owns 64 rows and walks all tiles.
+
+// Exact dequantised element (row r, column j) of an uploaded tensor, read
+// from its planes (sim/tmac_gguf.cpp:236-393, read_embedding :400-411).
+__device__ float tensor_elem(const TmqTensorDev& t, int r, int j) {
+    const size_t R = t.rows_pad;
+    if (t.type == kQ8_0) {
+        const int b = j >> 5, i = j & 31;
+        const float d = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
+        const int q = (int)(int8_t)t.pa[p16(b, i >> 4, 2, R, r) + (i & 15)];
+        return (float)q * d;  // :247 val * scale
+    }
+    if (t.type == kQ5_0) {
+        const int b = j >> 5, e = j & 31;
+        const float d = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
+        const uint32_t by = t.pa[p16(b, 0, 1, R, r) + (e & 15)];
+        const uint32_t qhp = ld4(t.pb + ((size_t)b * R + r) * 4);
+        const int nib = (e < 16) ? (int)(by & 15u) : (int)(by >> 4);
+        const int hb = (int)((qhp >> (8 * (e & 3) + (e >> 2))) & 1u);
+        return d * (float)((hb << 4) + nib - 16);  // :307-322
+    }
+    if (t.type == kQ4_K) {
+        const int b = j >> 8, off = j & 255, s = off >> 5, qp = off & 31;
+        const uint8_t* h = t.pb + p16(b, 0, 1, R, r);
+        const float d = h2f(ld2(h)), dmin = h2f(ld2(h + 2));
+        const uint8_t* sc = h + 4;
+        int scv, m;
+        if (s < 4) {
+            scv = sc[s] & 63;
+            m = sc[s + 4] & 63;
+        } else {
+            scv = (sc[s + 4] & 0xf) | ((sc[s - 4] >> 6) << 4);
+            m = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
+        }
+        const int qi = (s >> 1) * 32 + qp;
+        const uint32_t by = t.pa[p16(b, qi >> 4, 8, R, r) + (qi & 15)];
+        const int q4 = (s & 1) ? (int)(by >> 4) : (int)(by & 15u);
+        return d * (float)scv * (float)q4 - dmin * (float)m;  // :363-393
+    }
+    if (t.type == kQ6_K) {
+        const int b = j >> 8, off = j & 255, half = off >> 7, pos = off & 127, l = pos & 31, sub = pos >> 5;
+        const float d = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
+        const int qlo = half * 64 + l + (sub & 1) * 32;
+        const uint32_t qlb = t.pa[p16(b, qlo >> 4, 8, R, r) + (qlo & 15)];
+        const int qho = half * 32 + l;
+        const uint32_t qhb = t.pb[p16(b, qho >> 4, 4, R, r) + (qho & 15)];
+        const uint32_t nib = (sub < 2) ? (qlb & 15u) : (qlb >> 4);
+        const int q = (int)(nib | (((qhb >> (2 * sub)) & 3u) << 4)) - 32;
+        const int sc = (int)(int8_t)t.pc[p16(b, 0, 1, R, r) + half * 8 + (l >> 4) + sub * 2];
+        return d * (float)sc * (float)q;  // :324-361
+    }
+    return 0.0f;
+}
+
+// LDS carve-up of an engine workgroup: x[n] fp32 | xh[n/2] xl[n/2] (the
+// squares of RMSNorm alias xh/xl before the quantisation) | part[NW*64] int64
+// | red[64]
+struct EngLds {
+    float* x;
+    uint32_t* xh;
+    uint32_t* xl;
+    int64_t* part;
+    float* red;
+};
+__device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw) {
+    EngLds L;
+    L.x = (float*)base;
+    L.xh = (uint32_t*)(base + 4 * (size_t)n);
+    L.xl = L.xh + n / 2;
+    L.part = (int64_t*)(base + 8 * (size_t)n);
+    L.red = (float*)(L.part + nw * 64);
+    return L;
+}
+
+// The activation of the launch, quantised into L.xh / L.xl; returns x_scale.
+// rms_norm: sim/tmac_gguf.cpp:415-422 (sequential fp32 sum of squares, by one
+// lane, from LDS); silu*up: :434-439, :1693-1697; quantisation: :1225-1231.
+__device__ float eng_prologue(const TmqEngAct& a, const EngLds& L) {
+    const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
+    if (a.mode == TMQ_ACT_EMBED_NORM) {
+        const int tok = a.tokens[a.state->pos];
+        for (int i = tid; i < n; i += nt) {
+            const float v = tensor_elem(a.emb, tok, i);
+            L.x[i] = v;
+            if (blockIdx.x == 0) a.hidden_out[i] = v;
+        }
+    } else if (a.mode == TMQ_ACT_SILU) {
+        for (int i = tid; i < n; i += nt) {
+            const float g = a.x[i];
+            L.x[i] = (g / (1.0f + tmq_math::tmq_expf(-g))) * a.x2[i];
+        }
+    } else {
+        for (int i = tid; i < n; i += nt) L.x[i] = a.x[i];
+    }
+    if (a.mode == TMQ_ACT_NORM || a.mode == TMQ_ACT_EMBED_NORM) {
+        float* sq = (float*)L.xh;
+        for (int i = tid; i < n; i += nt) sq[i] = L.x[i] * L.x[i];
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
+            int i = 0;
+            // 16 squares per batch of LDS reads, added in index order
+            for (; i + 16 <= n; i += 16) {
+                float4 v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = *(const float4*)(sq + i + 4 * j);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    sum += v[j].x;
+                    sum += v[j].y;
+                    sum += v[j].z;
+                    sum += v[j].w;
+                }
+            }
+            for (; i < n; i++) sum += sq[i];
+            const float mean = sum / (float)n;
+            L.red[0] = 1.0f / sqrtf(mean + a.eps);
+        }
+        __syncthreads();
+        const float scale = L.red[0];
+        for (int i = tid; i < n; i += nt) L.x[i] = L.x[i] * a.w[i] * scale;
+    }
+    float m = 0.0f;
+    for (int i = tid; i < n; i += nt) m = fmaxf(m, fabsf(L.x[i]));
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __syncthreads();  // all reads of red[0] / the squares are done
+    if ((tid & 63) == 0) L.red[1 + (tid >> 6)] = m;
+    __syncthreads();
+    float mm = 0.0f;
+    for (int i = 0; i < (int)(nt >> 6); i++) mm = fmaxf(mm, L.red[1 + i]);
+    const float s = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
+    for (int k = tid; k < n / 2; k += nt) {
+        const int p = (int)(int16_t)roundf(L.x[2 * k] / s);
+        const int q = (int)(int16_t)roundf(L.x[2 * k + 1] / s);
+        L.xh[k] = ((uint32_t)(p >> 8) & 0xffffu) | ((uint32_t)(q >> 8) << 16);
+        L.xl[k] = ((uint32_t)p & 0xffu) | (((uint32_t)q & 0xffu) << 16);
+    }
+    __syncthreads();
+    return s;
+}
+
+__device__ __forceinline__ ActL eng_act(const EngLds& L, float xs) {
+    ActL A;
+    A.xs = xs;
+    A.xh = (const lu32*)L.xh;
+    A.xl = (const lu32*)L.xl;
+    return A;
+}
+
+template <int FMT, int NW>
+__device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int g) {
+    typedef typename BlkOf<FMT>::T Blk;
+    const TmqTensorDev& t = w.t;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    Blk cur{};
+    if (wave < t.nb) cur = blk_load<FMT>(t, wave, r);
+    const float inv = t.row_inv[r];
+    const ActL A = eng_act(L, eng_prologue(a, L));
+    int64_t acc = 0;
+    // Q5_0 / Q4_K keep the next block in flight while multiplying; a Q6_K
+    // block (53 registers) is loaded when needed (at most a few per wave)
+    if constexpr (FMT != kQ6_K) {
+        for (int b = wave; b < t.nb; b += NW) {
+            const bool more = b + NW < t.nb;
+            Blk nxt{};
+            if (more) nxt = blk_load<FMT>(t, b + NW, r);
+            int sh = 0, sl = 0;
+            blk_mac<FMT, false>(cur, A, b, inv, sh, sl);
+            acc += (int64_t)sh * 256 + sl;
+            if (more) cur = nxt;
+        }
+    } else {
+        for (int b = wave; b < t.nb; b += NW) {
+            if (b != wave) cur = blk_load<FMT>(t, b, r);
+            int sh = 0, sl = 0;
+            blk_mac<FMT, false>(cur, A, b, inv, sh, sl);
+            acc += (int64_t)sh * 256 + sl;
+        }
+    }
+    L.part[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave == 0 && r < t.rows) {
+        int64_t tot = 0;
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += L.part[i * 64 + lane];
+        if (w.acc) w.acc[r] = tot;
+        if (w.y) store_y(w, r, (float)(((double)tot * (double)A.xs) / (double)inv));
+    }
+}
+
+// Orderable key of (logit, row): larger logit first, then smaller row.
+__device__ __forceinline__ uint64_t argmax_key(float v, int r) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)r);
+}
+
+template <int NW>
+__device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int g) {
+    const TmqTensorDev& t = w.t;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int grp = g * NW + wave;
+    const int r0 = grp * 64;
+    const bool active = r0 < t.rows_pad;
+    const int r = active ? r0 + lane : lane;
+    Q8Blk cur{};
+    float ri = 0.0f, rs = 0.0f;
+    if (active) {
+        cur = q8_load(t, 0, r);
+        ri = t.row_inv[r];
+        rs = t.row_scale[r];
+    }
+    const ActL A = eng_act(L, eng_prologue(a, L));
+    if (!active) return;
+    const int nt = (t.cols + 63) / 64;
+    float y = 0.0f;
+    for (int tt = 0; tt < nt; tt++) {
+        int sh = 0, sl = 0;
+        const int b0 = 2 * tt, b1 = 2 * tt + 1;
+        const bool has1 = b1 < t.nb;
+        Q8Blk nxt = has1 ? q8_load(t, b1, r) : cur;
+        q8_mac(cur, A, b0, ri, sh, sl);
+        if (has1) {
+            cur = (b1 + 1 < t.nb) ? q8_load(t, b1 + 1, r) : nxt;
+            q8_mac(nxt, A, b1, ri, sh, sl);
+        } else if (b0 + 1 < t.nb) {
+            cur = q8_load(t, b0 + 1, r);
+        }
+        const int64_t P = (int64_t)sh * 256 + sl;
+        if (w.acc && r < t.rows) w.acc[(size_t)r * nt + tt] = P;
+        y = (float)((double)y + ((double)P * (double)A.xs) * (double)rs);
+    }
+    if (w.y && r < t.rows) store_y(w, r, y);
+    if (w.cand) {
+        uint64_t k = (r < t.rows) ? argmax_key(y, r) : 0ull;
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t ok = __shfl_xor(k, o);
+            k = ok > k ? ok : k;
+        }
+        if (lane == 0) w.cand[grp] = k;
+    }
+}
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngAct a, const TmqWork* __restrict__ works,
+                                                          const int32_t* __restrict__ gmap) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char eng_smem[];
+    const EngLds L = eng_lds(eng_smem, a.n, NW);
+    if (a.state && a.state->err) return;
+    const TmqWork& w = works[gmap[blockIdx.x]];
+    const int g = blockIdx.x - w.first_group;
+    switch (w.t.type) {
+    case kQ5_0: eng_group_k<kQ5_0, NW>(a, L, w, g); break;
+    case kQ4_K: eng_group_k<kQ4_K, NW>(a, L, w, g); break;
+    case kQ6_K: eng_group_k<kQ6_K, NW>(a, L, w, g); break;
+    case kQ8_0: eng_group_q8<NW>(a, L, w, g); break;
+    default: break;
+    }
 }
 
 // ------------------------------------------------------ activation prep
@@ -614,6 +949,22 @@ int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_
     if (!k) return (int)hipErrorInvalidValue;
     void* args[] = {&works_dev, &group_work_dev};
     return (int)hipLaunchKernel(k, dim3(total_groups), dim3(TMQ_WG), args, 0, s);
+}
+
+size_t tmq_eng_lds_bytes(int n, int waves) { return 8 * (size_t)n + 8 * 64 * (size_t)waves + 256; }
+
+int tmq_launch_eng_gemv(const TmqEngAct& act, const TmqWork* works_dev, const int32_t* group_work_dev,
+                        int total_groups, int waves, hipStream_t s) {
+    if (total_groups <= 0) return 0;
+    if (act.n <= 0 || act.n > TMQ_ENG_MAXN || act.n % 2) return (int)hipErrorInvalidValue;
+    const size_t lds = tmq_eng_lds_bytes(act.n, waves);
+    if (waves == 16)
+        hipLaunchKernelGGL(eng_gemv_kernel<16>, dim3(total_groups), dim3(1024), lds, s, act, works_dev, group_work_dev);
+    else if (waves == 4)
+        hipLaunchKernelGGL(eng_gemv_kernel<4>, dim3(total_groups), dim3(256), lds, s, act, works_dev, group_work_dev);
+    else
+        return (int)hipErrorInvalidValue;
+    return (int)hipGetLastError();
 }
 
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,

@@ -1,0 +1,93 @@
+// tmq_mathf.h -- fp32 transcendental functions matching the reference host.
+//
+// The reference engine calls glibc's expf/logf (sim/tmac_gguf.cpp:438,
+// :1650-1654).  glibc 2.35 implements expf with the table-driven method of
+// Szabolcs Nagy (Arm optimized-routines, "expf.c", MIT/Apache-2.0): with
+// N = 32, x*N/ln2 = k + r, exp(x) = 2^(k/N) * p(r) where p is a cubic
+// evaluated in double.  The x86-64 build used on FMA-capable hosts contracts
+// every multiply-add into an fma.  tmq_expf restates that method; the table
+// is the correctly rounded 2^(i/32) minus (i << 47) (derivable from first
+// principles).  It agrees with the host's expf on all 2^32 inputs.
+//
+// logf: glibc's table of (1/c, log c) pairs is not derivable from first
+// principles, so tmq_logf is the correctly rounded fp32 log (fp64 log then
+// one rounding); it differs from glibc's logf by one ulp on ~2e-4 of inputs.
+#pragma once
+#include <stdint.h>
+#include <string.h>
+
+#if defined(__HIPCC__)
+#define TMQ_HD __host__ __device__
+#else
+#define TMQ_HD
+#endif
+
+namespace tmq_math {
+
+TMQ_HD inline double as_double(uint64_t u) {
+    double d;
+    memcpy(&d, &u, 8);
+    return d;
+}
+TMQ_HD inline uint64_t as_u64(double d) {
+    uint64_t u;
+    memcpy(&u, &d, 8);
+    return u;
+}
+TMQ_HD inline uint32_t as_u32(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+// 2^(i/32), correctly rounded, with i<<47 subtracted from the bit pattern so
+// that adding k<<47 for k = i + 32*m scales it by 2^m.
+TMQ_HD inline uint64_t exp2_tab(int i) {
+    switch (i) {
+    case 0: return 0x3ff0000000000000ull; case 1: return 0x3fefd9b0d3158574ull;
+    case 2: return 0x3fefb5586cf9890full; case 3: return 0x3fef9301d0125b51ull;
+    case 4: return 0x3fef72b83c7d517bull; case 5: return 0x3fef54873168b9aaull;
+    case 6: return 0x3fef387a6e756238ull; case 7: return 0x3fef1e9df51fdee1ull;
+    case 8: return 0x3fef06fe0a31b715ull; case 9: return 0x3feef1a7373aa9cbull;
+    case 10: return 0x3feedea64c123422ull; case 11: return 0x3feece086061892dull;
+    case 12: return 0x3feebfdad5362a27ull; case 13: return 0x3feeb42b569d4f82ull;
+    case 14: return 0x3feeab07dd485429ull; case 15: return 0x3feea47eb03a5585ull;
+    case 16: return 0x3feea09e667f3bcdull; case 17: return 0x3fee9f75e8ec5f74ull;
+    case 18: return 0x3feea11473eb0187ull; case 19: return 0x3feea589994cce13ull;
+    case 20: return 0x3feeace5422aa0dbull; case 21: return 0x3feeb737b0cdc5e5ull;
+    case 22: return 0x3feec49182a3f090ull; case 23: return 0x3feed503b23e255dull;
+    case 24: return 0x3feee89f995ad3adull; case 25: return 0x3feeff76f2fb5e47ull;
+    case 26: return 0x3fef199bdd85529cull; case 27: return 0x3fef3720dcef9069ull;
+    case 28: return 0x3fef5818dcfba487ull; case 29: return 0x3fef7c97337b9b5full;
+    case 30: return 0x3fefa4afa2a490daull; default: return 0x3fefd0765b6e4540ull;
+    }
+}
+
+TMQ_HD inline float tmq_expf(float x) {
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    const double Shift = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const uint32_t abstop = (as_u32(x) >> 20) & 0x7ffu;
+    if (abstop >= (as_u32(88.0f) >> 20)) {
+        if (as_u32(x) == 0xff800000u) return 0.0f;          // -inf
+        if (abstop >= (0x7f800000u >> 20)) return x + x;     // +inf, nan
+        if (x > 0x1.62e42ep6f) return __builtin_inff();      // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;                 // underflow
+    }
+    const double xd = (double)x;
+    double kd = __builtin_fma(InvLn2N, xd, Shift);
+    const uint64_t ki = as_u64(kd);
+    kd -= Shift;
+    const double r = __builtin_fma(InvLn2N, xd, -kd);
+    const uint64_t t = exp2_tab((int)(ki % 32)) + (ki << 47);
+    const double s = as_double(t);
+    const double z = __builtin_fma(C0, r, C1);
+    const double r2 = r * r;
+    double y = __builtin_fma(C2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return (float)(y * s);
+}
+
+}  // namespace tmq_math

@@ -1,0 +1,695 @@
+// tmq_model.hip -- batch-1 decode engine: a .tmac model resident in HBM and
+// the launch sequence of one decode step, optionally captured as a HIP graph.
+//
+// Mirrors the reference engine (sim/tmac_gguf.cpp): load_tmac (:1894),
+// reset_cache/process_prompt (:1950, :1969), forward_layer_with_cache
+// (:1559), get_logits_q8 (:1820) and generate (:2001) with greedy selection.
+// The host only orders launches; every number is computed on the GPU, except
+// the RoPE cos/sin table, which is filled once per model from the host libm
+// exactly as apply_rope (:1527-1554) computes its factors.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/tmq.h"
+#include "tmq_engine.h"
+#include "tmq_internal.h"
+#include "tmq_runtime.h"
+
+namespace {
+
+struct Entry {
+    std::string name;
+    uint64_t rows, cols, n_bytes;
+    uint32_t type;
+    const uint8_t* data;
+};
+
+// one engine GEMV launch: activation recipe + a contiguous gmap range
+struct Launch {
+    TmqEngAct act{};
+    int gmap_off = 0, ngroups = 0, waves = 16;
+};
+
+struct Layer {
+    tmq_tensor *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    tmq_tensor *gate = nullptr, *up = nullptr, *down = nullptr;
+    size_t attn_norm = 0, ffn_norm = 0;  // offsets into fvec (floats)
+    long bq = -1, bk = -1, bv = -1;      // bias offsets or -1
+    Launch qkv, o_l, gu, dn;
+};
+
+inline uint64_t rd64(const uint8_t* p) {
+    uint64_t v;
+    memcpy(&v, p, 8);
+    return v;
+}
+inline uint32_t rd32(const uint8_t* p) {
+    uint32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+
+// Parse the .tmac container (scripts/extract_tmac.py:6-24): "TMAC", u64
+// count, then per tensor u64 name_len, name, u64 rows, u64 cols, u32 type,
+// u64 n_bytes, data.  Every field is bounds checked.
+int parse_tmac(const uint8_t* base, uint64_t size, std::vector<Entry>& out) {
+    if (size < 12 || memcmp(base, "TMAC", 4) != 0) return tmq_fail(TMQ_ERR_ARG, "not a .tmac file (magic)");
+    const uint64_t n = rd64(base + 4);
+    uint64_t off = 12;
+    if (n > (1u << 20)) return tmq_fail(TMQ_ERR_ARG, ".tmac: implausible tensor count %llu", (unsigned long long)n);
+    for (uint64_t i = 0; i < n; i++) {
+        if (size - off < 8) return tmq_fail(TMQ_ERR_ARG, ".tmac: truncated at tensor %llu", (unsigned long long)i);
+        const uint64_t nl = rd64(base + off);
+        off += 8;
+        if (nl == 0 || nl > 4096 || size - off < nl + 28)
+            return tmq_fail(TMQ_ERR_ARG, ".tmac: bad name length %llu at tensor %llu", (unsigned long long)nl,
+                            (unsigned long long)i);
+        Entry e;
+        e.name.assign((const char*)base + off, (size_t)nl);
+        off += nl;
+        e.rows = rd64(base + off);
+        e.cols = rd64(base + off + 8);
+        e.type = rd32(base + off + 16);
+        e.n_bytes = rd64(base + off + 20);
+        off += 28;
+        if (e.n_bytes > size - off)
+            return tmq_fail(TMQ_ERR_ARG, ".tmac: tensor %s data (%llu B) past end of file", e.name.c_str(),
+                            (unsigned long long)e.n_bytes);
+        e.data = base + off;
+        off += e.n_bytes;
+        out.push_back(e);
+    }
+    return 0;
+}
+
+uint64_t ggml_bytes(uint32_t type, uint64_t rows, uint64_t cols) {
+    switch (type) {
+    case TMQ_TYPE_Q8_0: return cols % 32 ? 0 : rows * (cols / 32) * 34;
+    case TMQ_TYPE_Q5_0: return cols % 32 ? 0 : rows * (cols / 32) * 22;
+    case TMQ_TYPE_Q4_K: return cols % 256 ? 0 : rows * (cols / 256) * 144;
+    case TMQ_TYPE_Q6_K: return cols % 256 ? 0 : rows * (cols / 256) * 210;
+    default: return 0;
+    }
+}
+
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    return s && *s ? atoi(s) : dflt;
+}
+
+}  // namespace
+
+struct tmq_model {
+    tmq_ctx* ctx = nullptr;
+    tmq_model_config cfg{};
+    tmq_tensor* emb = nullptr;
+    std::vector<Layer> layers;
+    long out_norm = -1;
+    std::vector<tmq_tensor*> owned;
+    // device memory (one allocation)
+    void* dmem = nullptr;
+    void* tail_mem = nullptr;
+    float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ctxv = nullptr;
+    float *gate = nullptr, *up = nullptr, *logits = nullptr, *fvec = nullptr, *dump = nullptr;
+    uint64_t* cand = nullptr;  // logits argmax candidates, one per 64 rows
+    int n_cand = 0;
+    float *kc = nullptr, *vc = nullptr;
+    float2* rope = nullptr;
+    TmqEngState* state = nullptr;
+    int32_t* tokens = nullptr;
+    TmqWork* works_dev = nullptr;
+    int32_t* gmap_dev = nullptr;
+    Launch logits_l;
+    uint64_t weight_bytes = 0;
+    int pos = -1;  // host mirror of state.pos
+    bool use_graphs = true;
+    hipGraphExec_t g_feed = nullptr, g_decode = nullptr;
+};
+
+namespace {
+
+void model_release(tmq_model* m) {
+    if (!m) return;
+    if (m->ctx) {
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipStreamSynchronize(m->ctx->stream);
+    }
+    if (m->g_feed) (void)hipGraphExecDestroy(m->g_feed);
+    if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
+    for (tmq_tensor* t : m->owned) tmq_tensor_free(t);
+    if (m->dmem) (void)hipFree(m->dmem);
+    if (m->tail_mem) (void)hipFree(m->tail_mem);
+    delete m;
+}
+
+// ---------------------------------------------------------------- launches
+int launch_gemv(tmq_model* m, const Launch& l) {
+    LAUNCH_TRY(tmq_launch_eng_gemv(l.act, m->works_dev, m->gmap_dev + l.gmap_off, l.ngroups, l.waves,
+                                   m->ctx->stream));
+    return 0;
+}
+
+// all layers at the current position (forward_all_layers); layer 0's QKV
+// launch also performs process_embedding of tokens[pos].  With dump, the
+// hidden state after the embedding and after every layer is copied to
+// dump[(l+1)*H].
+int launch_layers(tmq_model* m, bool dump) {
+    hipStream_t s = m->ctx->stream;
+    const tmq_model_config& c = m->cfg;
+    const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM;
+    for (int l = 0; l < c.n_layers; l++) {
+        const Layer& L = m->layers[l];
+        int rc = launch_gemv(m, L.qkv);
+        if (rc) return rc;
+        if (dump && l == 0) HIP_TRY(hipMemcpyAsync(m->dump, m->hidden, sizeof(float) * H, hipMemcpyDeviceToDevice, s));
+        TmqAttnArgs aa{};
+        aa.q = m->q;
+        aa.k = m->k;
+        aa.v = m->v;
+        aa.kc = m->kc + (size_t)l * c.max_seq * KV;
+        aa.vc = m->vc + (size_t)l * c.max_seq * KV;
+        aa.rope = m->rope;
+        aa.state = m->state;
+        aa.ctx = m->ctxv;
+        aa.n_heads = c.n_heads;
+        aa.n_kv = c.n_kv_heads;
+        aa.max_pos = c.max_seq;
+        LAUNCH_TRY(tmq_launch_attn(aa, s));
+        if ((rc = launch_gemv(m, L.o_l))) return rc;
+        if ((rc = launch_gemv(m, L.gu))) return rc;
+        if ((rc = launch_gemv(m, L.dn))) return rc;
+        if (dump)
+            HIP_TRY(hipMemcpyAsync(m->dump + (size_t)(l + 1) * H, m->hidden, sizeof(float) * H,
+                                   hipMemcpyDeviceToDevice, s));
+    }
+    return 0;
+}
+
+// one position whose token the host stored at tokens[pos+1]
+int launch_feed_impl(tmq_model* m, bool dump) {
+    LAUNCH_TRY(tmq_launch_advance(m->state, m->cfg.max_seq, m->ctx->stream));
+    return launch_layers(m, dump);
+}
+int launch_feed(tmq_model* m) { return launch_feed_impl(m, false); }
+
+// get_logits_q8: output_norm (when present) + the Q8_0 logits GEMV, which
+// also leaves per-wave argmax candidates
+int launch_logits(tmq_model* m) { return launch_gemv(m, m->logits_l); }
+
+// one greedy generate() iteration: logits, argmax -> tokens[pos+1] (and
+// pos+1), then all layers of that token
+int launch_decode(tmq_model* m) {
+    int rc = launch_logits(m);
+    if (rc) return rc;
+    LAUNCH_TRY(tmq_launch_argmax(m->cand, m->n_cand, m->state, m->tokens, m->cfg.max_seq, m->ctx->stream));
+    return launch_layers(m, false);
+}
+
+int capture(tmq_model* m, int (*fn)(tmq_model*), hipGraphExec_t* out) {
+    hipStream_t s = m->ctx->stream;
+    HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = fn(m);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_HIP, "graph capture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_HIP, "graph instantiate: %s", hipGetErrorString(e));
+    return 0;
+}
+
+int run_feed(tmq_model* m) {
+    if (m->use_graphs) {
+        if (!m->g_feed) {
+            int rc = capture(m, launch_feed, &m->g_feed);
+            if (rc) return rc;
+        }
+        HIP_TRY(hipGraphLaunch(m->g_feed, m->ctx->stream));
+        return 0;
+    }
+    return launch_feed(m);
+}
+int run_decode(tmq_model* m) {
+    if (m->use_graphs) {
+        if (!m->g_decode) {
+            int rc = capture(m, launch_decode, &m->g_decode);
+            if (rc) return rc;
+        }
+        HIP_TRY(hipGraphLaunch(m->g_decode, m->ctx->stream));
+        return 0;
+    }
+    return launch_decode(m);
+}
+
+int check_state(tmq_model* m) {
+    TmqEngState st{};
+    HIP_TRY(hipMemcpyAsync(&st, m->state, sizeof st, hipMemcpyDeviceToHost, m->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    if (st.err) return tmq_fail(TMQ_ERR_ARG, "decode step failed on the device (token or position out of range)");
+    if (st.pos != m->pos) return tmq_fail(TMQ_ERR_HIP, "device position %d != expected %d", st.pos, m->pos);
+    return 0;
+}
+
+// ------------------------------------------------------------------ build
+int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
+    tmq_ctx* ctx = m->ctx;
+    std::map<std::string, const Entry*> by;
+    for (const Entry& e : ents) by[e.name] = &e;
+    auto get = [&](const std::string& n) -> const Entry* {
+        auto it = by.find(n);
+        return it == by.end() ? nullptr : it->second;
+    };
+    const Entry* emb = get("token_embd.weight");
+    if (!emb) return tmq_fail(TMQ_ERR_ARG, "model has no token_embd.weight");
+    if (emb->type != TMQ_TYPE_Q8_0)
+        return tmq_fail(TMQ_ERR_ARG, "token_embd.weight is type %u; the Q8_0 logits path needs Q8_0", emb->type);
+    tmq_model_config& c = m->cfg;
+    c.vocab = (int)emb->rows;
+    c.hidden = (int)emb->cols;
+    int L = 0;
+    while (get("blk." + std::to_string(L) + ".attn_q.weight")) L++;
+    if (L == 0) return tmq_fail(TMQ_ERR_ARG, "model has no blk.0.attn_q.weight");
+    c.n_layers = L;
+    const Entry* k0 = get("blk.0.attn_k.weight");
+    const Entry* g0 = get("blk.0.ffn_gate.weight");
+    if (!k0 || !g0) return tmq_fail(TMQ_ERR_ARG, "model lacks blk.0.attn_k / ffn_gate");
+    c.head_dim = TMQ_HEAD_DIM;
+    c.n_heads = c.hidden / TMQ_HEAD_DIM;
+    c.n_kv_heads = (int)(k0->rows / TMQ_HEAD_DIM);
+    c.inter = (int)g0->rows;
+    c.max_seq = max_seq;
+    c.rope_base = 1000000.0f;
+    c.norm_eps = 1e-6f;
+    const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM, I = c.inter;
+    if (H % TMQ_HEAD_DIM || H % 32 || c.n_kv_heads <= 0 || (int)k0->rows % TMQ_HEAD_DIM ||
+        c.n_heads % c.n_kv_heads || I <= 0 || I > 65536 || I % 2)
+        return tmq_fail(TMQ_ERR_ARG, "unsupported model shape hidden %d, kv rows %llu, ffn %d", H,
+                        (unsigned long long)k0->rows, I);
+    if (c.vocab <= 0) return tmq_fail(TMQ_ERR_ARG, "empty vocabulary");
+    if (H > TMQ_ENG_MAXN || I > TMQ_ENG_MAXN)
+        return tmq_fail(TMQ_ERR_ARG, "hidden %d / ffn %d above the engine's %d", H, I, TMQ_ENG_MAXN);
+
+    // fp32 vectors: norms and biases
+    std::vector<float> fv;
+    auto add_vec = [&](const std::string& n, int count, bool required, long* off) -> int {
+        const Entry* e = get(n);
+        if (!e) {
+            if (required) return tmq_fail(TMQ_ERR_ARG, "model lacks %s", n.c_str());
+            *off = -1;
+            return 0;
+        }
+        if (e->type != 0 || e->n_bytes != (uint64_t)count * 4 || e->rows * e->cols != (uint64_t)count)
+            return tmq_fail(TMQ_ERR_ARG, "%s: expected %d F32 values (type %u, %llu bytes)", n.c_str(), count,
+                            e->type, (unsigned long long)e->n_bytes);
+        *off = (long)fv.size();
+        const size_t at = fv.size();
+        fv.resize(at + ((count + 63) / 64) * 64, 0.0f);
+        memcpy(fv.data() + at, e->data, (size_t)count * 4);
+        return 0;
+    };
+    auto upload = [&](const std::string& n, uint64_t rows, uint64_t cols, tmq_tensor** out) -> int {
+        const Entry* e = get(n);
+        if (!e) return tmq_fail(TMQ_ERR_ARG, "model lacks %s", n.c_str());
+        if (e->rows != rows || e->cols != cols)
+            return tmq_fail(TMQ_ERR_ARG, "%s: shape %llux%llu, expected %llux%llu", n.c_str(),
+                            (unsigned long long)e->rows, (unsigned long long)e->cols, (unsigned long long)rows,
+                            (unsigned long long)cols);
+        const uint64_t need = ggml_bytes(e->type, rows, cols);
+        if (!need) return tmq_fail(TMQ_ERR_ARG, "%s: type %u unsupported for %llux%llu", n.c_str(), e->type,
+                                   (unsigned long long)rows, (unsigned long long)cols);
+        if (e->n_bytes != need)
+            return tmq_fail(TMQ_ERR_ARG, "%s: %llu bytes, expected %llu", n.c_str(), (unsigned long long)e->n_bytes,
+                            (unsigned long long)need);
+        const float* aux = nullptr;
+        if (e->type == TMQ_TYPE_Q8_0) {  // sim/matmul_q8.cpp:24-30
+            const Entry* a = get(n + "_row_max_abs");
+            if (a && a->type == 0 && a->cols == 1 && a->rows == rows && a->n_bytes == rows * 4)
+                aux = (const float*)a->data;
+        }
+        int rc = tmq_rt_tensor_create(ctx, e->type, rows, cols, e->data, false, e->n_bytes, aux, false, out);
+        if (rc) return tmq_fail(rc, "%s: %s", n.c_str(), tmq_last_error());
+        m->owned.push_back(*out);
+        m->weight_bytes += e->n_bytes;
+        return 0;
+    };
+    int rc = upload("token_embd.weight", c.vocab, H, &m->emb);
+    if (rc) return rc;
+    m->layers.resize(L);
+    for (int l = 0; l < L; l++) {
+        Layer& Y = m->layers[l];
+        const std::string p = "blk." + std::to_string(l) + ".";
+        long off;
+        if ((rc = add_vec(p + "attn_norm.weight", H, true, &off))) return rc;
+        Y.attn_norm = (size_t)off;
+        if ((rc = add_vec(p + "ffn_norm.weight", H, true, &off))) return rc;
+        Y.ffn_norm = (size_t)off;
+        if ((rc = add_vec(p + "attn_q.bias", H, false, &Y.bq))) return rc;
+        if ((rc = add_vec(p + "attn_k.bias", KV, false, &Y.bk))) return rc;
+        if ((rc = add_vec(p + "attn_v.bias", KV, false, &Y.bv))) return rc;
+        if ((rc = upload(p + "attn_q.weight", H, H, &Y.q))) return rc;
+        if ((rc = upload(p + "attn_k.weight", KV, H, &Y.k))) return rc;
+        if ((rc = upload(p + "attn_v.weight", KV, H, &Y.v))) return rc;
+        if ((rc = upload(p + "attn_output.weight", H, H, &Y.o))) return rc;
+        if ((rc = upload(p + "ffn_gate.weight", I, H, &Y.gate))) return rc;
+        if ((rc = upload(p + "ffn_up.weight", I, H, &Y.up))) return rc;
+        if ((rc = upload(p + "ffn_down.weight", H, I, &Y.down))) return rc;
+    }
+    if ((rc = add_vec("output_norm.weight", H, false, &m->out_norm))) return rc;
+
+    // device buffer layout
+    auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const int n_cand = (int)((c.vocab + 63) / 64);
+    size_t off = 0;
+    std::map<std::string, size_t> lay;
+    auto place = [&](const char* n, size_t bytes) {
+        lay[n] = off;
+        off += al(bytes);
+    };
+    place("state", sizeof(TmqEngState));
+    place("tokens", sizeof(int32_t) * (size_t)(max_seq + 1));
+    place("hidden", 4 * (size_t)H);
+    place("q", 4 * (size_t)H);
+    place("k", 4 * (size_t)KV);
+    place("v", 4 * (size_t)KV);
+    place("ctx", 4 * (size_t)H);
+    place("gate", 4 * (size_t)I);
+    place("up", 4 * (size_t)I);
+    place("logits", 4 * (size_t)c.vocab);
+    place("cand", 8 * (size_t)n_cand);
+    place("dump", 4 * (size_t)H * (L + 1));
+    place("fvec", 4 * fv.size() + 4);
+    place("rope", sizeof(float2) * 32 * (size_t)max_seq);
+    place("kc", 4 * (size_t)L * max_seq * KV);
+    place("vc", 4 * (size_t)L * max_seq * KV);
+    hipError_t e = hipMalloc(&m->dmem, off);
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_NOMEM, "model buffers (%zu B): %s", off, hipGetErrorString(e));
+    uint8_t* B = (uint8_t*)m->dmem;
+    m->state = (TmqEngState*)(B + lay["state"]);
+    m->tokens = (int32_t*)(B + lay["tokens"]);
+    m->hidden = (float*)(B + lay["hidden"]);
+    m->q = (float*)(B + lay["q"]);
+    m->k = (float*)(B + lay["k"]);
+    m->v = (float*)(B + lay["v"]);
+    m->ctxv = (float*)(B + lay["ctx"]);
+    m->gate = (float*)(B + lay["gate"]);
+    m->up = (float*)(B + lay["up"]);
+    m->logits = (float*)(B + lay["logits"]);
+    m->cand = (uint64_t*)(B + lay["cand"]);
+    m->n_cand = n_cand;
+    m->dump = (float*)(B + lay["dump"]);
+    m->fvec = (float*)(B + lay["fvec"]);
+    m->rope = (float2*)(B + lay["rope"]);
+    m->kc = (float*)(B + lay["kc"]);
+    m->vc = (float*)(B + lay["vc"]);
+    auto fv_ptr = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
+
+    // Work lists.  Every launch is one engine GEMV: per layer qkv / o /
+    // gate+up / down, then the logits.  A K-quant or Q5_0 row group is 64
+    // rows on one workgroup whose waves split the blocks; a Q8_0 wave owns 64
+    // rows, so a workgroup covers waves*64 rows.
+    std::vector<TmqWork> works;
+    std::vector<int32_t> gmap;
+    auto add_work = [&](Launch& ln, const tmq_tensor* t, float* y, const float* bias, int resid) {
+        TmqWork w = tmq_rt_make_work(t, nullptr, y, nullptr);
+        w.bias = bias;
+        w.resid = resid;
+        const int g64 = t->dev.rows_pad / 64;
+        w.ngroups = t->dev.type == TMQ_TYPE_Q8_0 ? (g64 + ln.waves - 1) / ln.waves : g64;
+        w.first_group = ln.ngroups;
+        for (int g = 0; g < w.ngroups; g++) gmap.push_back((int32_t)works.size());
+        ln.ngroups += w.ngroups;
+        works.push_back(w);
+        return works.size() - 1;
+    };
+    auto recipe = [&](int mode, const float* x, const float* x2, const float* w, int n) {
+        TmqEngAct a{};
+        a.mode = mode;
+        a.n = n;
+        a.x = x;
+        a.x2 = x2;
+        a.w = w;
+        a.eps = c.norm_eps;
+        a.state = m->state;
+        return a;
+    };
+    for (int l = 0; l < L; l++) {
+        Layer& Y = m->layers[l];
+        if (l == 0) {
+            Y.qkv.act = recipe(TMQ_ACT_EMBED_NORM, nullptr, nullptr, m->fvec + Y.attn_norm, H);
+            Y.qkv.act.tokens = m->tokens;
+            Y.qkv.act.hidden_out = m->hidden;
+            Y.qkv.act.emb = m->emb->dev;
+        } else {
+            Y.qkv.act = recipe(TMQ_ACT_NORM, m->hidden, nullptr, m->fvec + Y.attn_norm, H);
+        }
+        add_work(Y.qkv, Y.q, m->q, fv_ptr(Y.bq), 0);
+        add_work(Y.qkv, Y.k, m->k, fv_ptr(Y.bk), 0);
+        add_work(Y.qkv, Y.v, m->v, fv_ptr(Y.bv), 0);
+        Y.o_l.act = recipe(TMQ_ACT_PLAIN, m->ctxv, nullptr, nullptr, H);
+        add_work(Y.o_l, Y.o, m->hidden, nullptr, 1);
+        Y.gu.act = recipe(TMQ_ACT_NORM, m->hidden, nullptr, m->fvec + Y.ffn_norm, H);
+        add_work(Y.gu, Y.gate, m->gate, nullptr, 0);
+        add_work(Y.gu, Y.up, m->up, nullptr, 0);
+        Y.dn.act = recipe(TMQ_ACT_SILU, m->gate, m->up, nullptr, I);
+        add_work(Y.dn, Y.down, m->hidden, nullptr, 1);
+    }
+    m->logits_l.waves = 4;
+    m->logits_l.act = m->out_norm >= 0 ? recipe(TMQ_ACT_NORM, m->hidden, nullptr, m->fvec + m->out_norm, H)
+                                       : recipe(TMQ_ACT_PLAIN, m->hidden, nullptr, nullptr, H);
+    works[add_work(m->logits_l, m->emb, m->logits, nullptr, 0)].cand = m->cand;
+    // gmap offsets of each launch, in the order add_work filled gmap
+    {
+        int g = 0;
+        for (int l = 0; l < L; l++) {
+            Layer& Y = m->layers[l];
+            for (Launch* ln : {&Y.qkv, &Y.o_l, &Y.gu, &Y.dn}) {
+                ln->gmap_off = g;
+                g += ln->ngroups;
+            }
+        }
+        m->logits_l.gmap_off = g;
+    }
+    const size_t tail = al(sizeof(TmqWork) * works.size()) + al(4 * gmap.size());
+    void* tmem = nullptr;
+    e = hipMalloc(&tmem, tail);
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_NOMEM, "model work lists (%zu B): %s", tail, hipGetErrorString(e));
+    m->tail_mem = tmem;
+    m->works_dev = (TmqWork*)tmem;
+    m->gmap_dev = (int32_t*)((uint8_t*)tmem + al(sizeof(TmqWork) * works.size()));
+
+    hipStream_t s = ctx->stream;
+    HIP_TRY(hipMemcpyAsync(m->works_dev, works.data(), sizeof(TmqWork) * works.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(m->gmap_dev, gmap.data(), 4 * gmap.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(m->fvec, fv.data(), 4 * fv.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemsetAsync(m->kc, 0, 4 * (size_t)L * max_seq * KV, s));
+    HIP_TRY(hipMemsetAsync(m->vc, 0, 4 * (size_t)L * max_seq * KV, s));
+    // RoPE factors exactly as apply_rope forms them (sim/tmac_gguf.cpp:1531-1535)
+    std::vector<float2> rope((size_t)max_seq * 32);
+    volatile float base_v = c.rope_base;
+    const float base = base_v;
+    for (int d = 0; d < TMQ_HEAD_DIM; d += 2) {
+        const float theta = 1.0f / powf(base, (float)d / TMQ_HEAD_DIM);
+        for (int p = 0; p < max_seq; p++) {
+            const float freq = p * theta;
+            rope[(size_t)p * 32 + d / 2] = make_float2(cosf(freq), sinf(freq));
+        }
+    }
+    HIP_TRY(hipMemcpyAsync(m->rope, rope.data(), sizeof(float2) * rope.size(), hipMemcpyHostToDevice, s));
+    TmqEngState st{-1, 0, {0, 0}};
+    HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    m->use_graphs = env_int("TMQ_GRAPHS", 1) != 0;
+    return 0;
+}
+
+int reset(tmq_model* m) {
+    hipStream_t s = m->ctx->stream;
+    TmqEngState st{-1, 0, {0, 0}};
+    HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
+    m->pos = -1;
+    return 0;
+}
+
+int load_common(tmq_ctx* ctx, const uint8_t* data, uint64_t n, int max_seq, tmq_model** out) {
+    if (!ctx || !data || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (max_seq <= 0) max_seq = 512;
+    if (max_seq > TMQ_MAX_POS) return tmq_fail(TMQ_ERR_ARG, "max_seq %d > %d", max_seq, TMQ_MAX_POS);
+    int rc = tmq_rt_set_device(ctx);
+    if (rc) return rc;
+    std::vector<Entry> ents;
+    rc = parse_tmac(data, n, ents);
+    if (rc) return rc;
+    tmq_model* m = new tmq_model();
+    m->ctx = ctx;
+    rc = build_model(m, ents, max_seq);
+    if (rc) {
+        std::string msg = tmq_last_error();
+        model_release(m);
+        return tmq_fail(rc, "%s", msg.c_str());
+    }
+    *out = m;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tmq_model_load_mem(tmq_ctx* ctx, const void* data, uint64_t n_bytes, int max_seq, tmq_model** out) {
+    return load_common(ctx, (const uint8_t*)data, n_bytes, max_seq, out);
+}
+
+int tmq_model_load(tmq_ctx* ctx, const char* path, int max_seq, tmq_model** out) {
+    if (!path) return tmq_fail(TMQ_ERR_ARG, "null path");
+    FILE* f = fopen(path, "rb");
+    if (!f) return tmq_fail(TMQ_ERR_ARG, "cannot open %s", path);
+    std::vector<uint8_t> buf;
+    if (fseek(f, 0, SEEK_END) == 0) {
+        long sz = ftell(f);
+        if (sz > 0) {
+            buf.resize((size_t)sz);
+            (void)fseek(f, 0, SEEK_SET);
+            if (fread(buf.data(), 1, buf.size(), f) != buf.size()) buf.clear();
+        }
+    }
+    fclose(f);
+    if (buf.empty()) return tmq_fail(TMQ_ERR_ARG, "cannot read %s", path);
+    return load_common(ctx, buf.data(), buf.size(), max_seq, out);
+}
+
+int tmq_model_free(tmq_model* m) {
+    model_release(m);
+    return 0;
+}
+
+int tmq_model_get_config(const tmq_model* m, tmq_model_config* out) {
+    if (!m || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    *out = m->cfg;
+    return 0;
+}
+
+uint64_t tmq_model_weight_bytes(const tmq_model* m) { return m ? m->weight_bytes : 0; }
+
+int tmq_model_position(const tmq_model* m) { return m ? m->pos + 1 : -1; }
+
+int tmq_model_set_graphs(tmq_model* m, int enable) {
+    if (!m) return tmq_fail(TMQ_ERR_ARG, "null model");
+    m->use_graphs = enable != 0;
+    return 0;
+}
+
+int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n) {
+    if (!m || !tokens || n <= 0) return tmq_fail(TMQ_ERR_ARG, "bad prompt arguments");
+    if (n > m->cfg.max_seq) return tmq_fail(TMQ_ERR_ARG, "prompt of %d tokens exceeds max_seq %d", n, m->cfg.max_seq);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab)
+            return tmq_fail(TMQ_ERR_ARG, "token %d at %d outside [0, %d)", tokens[i], i, m->cfg.vocab);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (!rc) rc = reset(m);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(m->tokens, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, m->ctx->stream));
+    for (int i = 0; i < n; i++) {
+        if ((rc = run_feed(m))) return rc;
+        m->pos++;
+    }
+    return check_state(m);
+}
+
+int tmq_model_feed(tmq_model* m, int32_t token) {
+    if (!m) return tmq_fail(TMQ_ERR_ARG, "null model");
+    if (token < 0 || token >= m->cfg.vocab) return tmq_fail(TMQ_ERR_ARG, "token %d outside [0, %d)", token, m->cfg.vocab);
+    if (m->pos + 1 >= m->cfg.max_seq) return tmq_fail(TMQ_ERR_ARG, "context full (max_seq %d)", m->cfg.max_seq);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(m->tokens + m->pos + 1, &token, 4, hipMemcpyHostToDevice, m->ctx->stream));
+    if ((rc = run_feed(m))) return rc;
+    m->pos++;
+    return check_state(m);
+}
+
+int tmq_model_logits(tmq_model* m, float* logits) {
+    if (!m || !logits) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (m->pos < 0) return tmq_fail(TMQ_ERR_ARG, "no position processed yet");
+    int rc = tmq_rt_set_device(m->ctx);
+    if (!rc) rc = launch_logits(m);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(logits, m->logits, sizeof(float) * m->cfg.vocab, hipMemcpyDeviceToHost, m->ctx->stream));
+    return check_state(m);
+}
+
+int tmq_model_generate(tmq_model* m, int n, int32_t* out_tokens) {
+    if (!m || n < 0 || (n > 0 && !out_tokens)) return tmq_fail(TMQ_ERR_ARG, "bad generate arguments");
+    if (m->pos < 0) return tmq_fail(TMQ_ERR_ARG, "no prompt processed");
+    if (m->pos + n >= m->cfg.max_seq)
+        return tmq_fail(TMQ_ERR_ARG, "%d more positions exceed max_seq %d", n, m->cfg.max_seq);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    const int first = m->pos + 1;
+    for (int i = 0; i < n; i++) {
+        if ((rc = run_decode(m))) return rc;
+        m->pos++;
+    }
+    if (n > 0)
+        HIP_TRY(hipMemcpyAsync(out_tokens, m->tokens + first, sizeof(int32_t) * n, hipMemcpyDeviceToHost,
+                               m->ctx->stream));
+    return check_state(m);
+}
+
+int tmq_model_generate_async(tmq_model* m, int n) {
+    if (!m || n < 0) return tmq_fail(TMQ_ERR_ARG, "bad generate arguments");
+    if (m->pos < 0) return tmq_fail(TMQ_ERR_ARG, "no prompt processed");
+    if (m->pos + n >= m->cfg.max_seq)
+        return tmq_fail(TMQ_ERR_ARG, "%d more positions exceed max_seq %d", n, m->cfg.max_seq);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    for (int i = 0; i < n; i++) {
+        if ((rc = run_decode(m))) return rc;
+        m->pos++;
+    }
+    return 0;
+}
+
+int tmq_model_tokens(tmq_model* m, int first, int n, int32_t* out) {
+    if (!m || !out || first < 0 || n < 0 || first + n > m->pos + 1)
+        return tmq_fail(TMQ_ERR_ARG, "token range [%d, %d) outside the %d processed positions", first, first + n,
+                        m ? m->pos + 1 : 0);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(out, m->tokens + first, sizeof(int32_t) * n, hipMemcpyDeviceToHost, m->ctx->stream));
+    return check_state(m);
+}
+
+int tmq_model_hidden(tmq_model* m, float* out) {
+    if (!m || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(out, m->hidden, sizeof(float) * m->cfg.hidden, hipMemcpyDeviceToHost, m->ctx->stream));
+    return check_state(m);
+}
+
+int tmq_model_feed_dump(tmq_model* m, int32_t token, float* layers_out) {
+    if (!m || !layers_out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (token < 0 || token >= m->cfg.vocab) return tmq_fail(TMQ_ERR_ARG, "token %d outside [0, %d)", token, m->cfg.vocab);
+    if (m->pos + 1 >= m->cfg.max_seq) return tmq_fail(TMQ_ERR_ARG, "context full (max_seq %d)", m->cfg.max_seq);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(m->tokens + m->pos + 1, &token, 4, hipMemcpyHostToDevice, m->ctx->stream));
+    if ((rc = launch_feed_impl(m, true))) return rc;
+    m->pos++;
+    const size_t nb = sizeof(float) * m->cfg.hidden * (size_t)(m->cfg.n_layers + 1);
+    HIP_TRY(hipMemcpyAsync(layers_out, m->dump, nb, hipMemcpyDeviceToHost, m->ctx->stream));
+    return check_state(m);
+}
+
+}  // extern "C"

@@ -33,6 +33,10 @@ EXPORTS = [
     "tmq_vecmul_tile_q4k", "tmq_phaseb_run", "tmq_chain_create", "tmq_chain_run",
     "tmq_chain_prepare", "tmq_chain_launch",
     "tmq_chain_free", "tmq_chain_weight_bytes",
+    "tmq_model_load", "tmq_model_load_mem", "tmq_model_free", "tmq_model_get_config",
+    "tmq_model_weight_bytes", "tmq_model_position", "tmq_model_set_graphs", "tmq_model_prompt",
+    "tmq_model_feed", "tmq_model_feed_dump", "tmq_model_logits", "tmq_model_generate",
+    "tmq_model_generate_async", "tmq_model_tokens", "tmq_model_hidden",
 ]
 
 
@@ -95,6 +99,21 @@ def lib(path: str = LIB_PATH):
         "tmq_chain_launch": (I, [P, P]),
         "tmq_chain_free": (I, [P]),
         "tmq_chain_weight_bytes": (U64, [P]),
+        "tmq_model_load": (I, [P, C.c_char_p, I, C.POINTER(P)]),
+        "tmq_model_load_mem": (I, [P, P, U64, I, C.POINTER(P)]),
+        "tmq_model_free": (I, [P]),
+        "tmq_model_get_config": (I, [P, P]),
+        "tmq_model_weight_bytes": (U64, [P]),
+        "tmq_model_position": (I, [P]),
+        "tmq_model_set_graphs": (I, [P, I]),
+        "tmq_model_prompt": (I, [P, P, I]),
+        "tmq_model_feed": (I, [P, C.c_int32]),
+        "tmq_model_feed_dump": (I, [P, C.c_int32, P]),
+        "tmq_model_logits": (I, [P, P]),
+        "tmq_model_generate": (I, [P, I, P]),
+        "tmq_model_generate_async": (I, [P, I]),
+        "tmq_model_tokens": (I, [P, I, I, P]),
+        "tmq_model_hidden": (I, [P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -254,3 +273,83 @@ class Context:
 
     def chain(self, descs) -> Chain:
         return Chain(self, descs)
+
+
+class ModelConfig(C.Structure):
+    """tmq_model_config"""
+    _fields_ = [("n_layers", C.c_int32), ("hidden", C.c_int32), ("inter", C.c_int32),
+                ("vocab", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+                ("head_dim", C.c_int32), ("max_seq", C.c_int32), ("rope_base", C.c_float),
+                ("norm_eps", C.c_float)]
+
+
+class Model:
+    """A .tmac model resident on the GPU (tmq_model_*): the reference engine's
+    load_tmac / process_prompt / get_logits_q8 / generate (greedy)."""
+
+    def __init__(self, ctx: Context, src, max_seq: int = 512):
+        h = C.c_void_p()
+        if isinstance(src, (str, os.PathLike)):
+            _check(lib().tmq_model_load(ctx.handle, os.fspath(src).encode(), max_seq, C.byref(h)))
+        else:
+            buf = np.frombuffer(src, dtype=np.uint8) if not isinstance(src, np.ndarray) else src
+            buf = np.ascontiguousarray(buf, dtype=np.uint8)
+            _check(lib().tmq_model_load_mem(ctx.handle, _p(buf), buf.size, max_seq, C.byref(h)))
+        self.ctx, self.handle = ctx, h
+        cfg = ModelConfig()
+        _check(lib().tmq_model_get_config(h, C.byref(cfg)))
+        self.config = {f: getattr(cfg, f) for f, _ in ModelConfig._fields_}
+        self.weight_bytes = lib().tmq_model_weight_bytes(h)
+
+    @property
+    def position(self) -> int:
+        return lib().tmq_model_position(self.handle)
+
+    def set_graphs(self, enable: bool):
+        _check(lib().tmq_model_set_graphs(self.handle, int(bool(enable))))
+
+    def prompt(self, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        _check(lib().tmq_model_prompt(self.handle, _p(t), t.size))
+
+    def feed(self, token: int, dump: bool = False):
+        if dump:
+            out = np.empty((self.config["n_layers"] + 1, self.config["hidden"]), dtype=np.float32)
+            _check(lib().tmq_model_feed_dump(self.handle, int(token), _p(out)))
+            return out
+        _check(lib().tmq_model_feed(self.handle, int(token)))
+        return None
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.config["vocab"], dtype=np.float32)
+        _check(lib().tmq_model_logits(self.handle, _p(out)))
+        return out
+
+    def generate(self, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.int32)
+        _check(lib().tmq_model_generate(self.handle, n, _p(out)))
+        return out
+
+    def generate_async(self, n: int):
+        _check(lib().tmq_model_generate_async(self.handle, n))
+
+    def tokens(self, first: int, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.int32)
+        _check(lib().tmq_model_tokens(self.handle, first, n, _p(out)))
+        return out
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty(self.config["hidden"], dtype=np.float32)
+        _check(lib().tmq_model_hidden(self.handle, _p(out)))
+        return out
+
+    def free(self):
+        if self.handle:
+            lib().tmq_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
