@@ -194,7 +194,7 @@ typedef struct {
 /* load_tmac (sim/tmac_gguf.cpp:1894-1947): the .tmac container of
  * scripts/extract_tmac.py:6-24, uploaded and checked (shapes, types, sizes).
  * Shapes are taken from the tensors (head_dim 64, RoPE base 1e6, RMSNorm eps
- * 1e-6 as the reference's constants, :136-148, :418, :1528).  max_seq <= 4096
+ * 1e-6 as the reference's constants, :136-148, :418, :1528).  max_seq <= 3072
  * positions of KV cache (0: 512); the reference fixes 256 (:148). */
 int tmq_model_load(tmq_ctx* ctx, const char* path, int max_seq, tmq_model** out);
 int tmq_model_load_mem(tmq_ctx* ctx, const void* data, uint64_t n_bytes, int max_seq, tmq_model** out);

@@ -7,13 +7,11 @@
 #include "tmq_internal.h"
 
 #define TMQ_HEAD_DIM 64
-#define TMQ_MAX_POS 4096
+#define TMQ_MAX_POS 3072  // scores + weights (8 B each) beside 32 KB of staged V rows in 64 KB of LDS
 
 
 struct TmqAttnArgs {
-    const float* q;          // [n_heads*64] projections with bias
-    const float* k;          // [n_kv*64]
-    const float* v;
+    TmqDeferred q, k, v;     // the QKV projections (K-split, with bias)
     float* kc;               // this layer's caches [max_pos][n_kv*64]
     float* vc;
     const float2* rope;      // [max_pos][32] (cos, sin)

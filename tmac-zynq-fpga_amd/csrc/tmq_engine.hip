@@ -14,6 +14,7 @@
 // involvement.
 #include <hip/hip_runtime.h>
 
+#include "tmq_device.h"
 #include "tmq_engine.h"
 #include "tmq_mathf.h"
 
@@ -21,13 +22,15 @@ namespace {
 
 // RoPE (sim/tmac_gguf.cpp:1527-1554, adjacent pairs, cos/sin table from the
 // host) + KV cache append (:1616-1617) + attention of one query head
-// (:1619-1655).  One workgroup per query head; head_dim is 64.
+// (:1619-1655).  One workgroup per query head; head_dim is 64.  The cached
+// K row of each thread's first position and the first 64 V rows are read at
+// entry, so their latency overlaps the q/k/v finalisation.
 __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     extern __shared__ float lds[];
     float* sc = lds;                  // scores, max_pos
     float* ex = lds + a.max_pos;      // exp terms / weights, max_pos
     __shared__ float qr[64], kr[64], vn[64];
-    __shared__ float vbuf[2][32][64];
+    __shared__ float vbuf[2][64][64];
     __shared__ float red[8];
     __shared__ float s_stat[2];
     const int h = blockIdx.x, tid = threadIdx.x;
@@ -36,21 +39,42 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     const int KV = a.n_kv * 64;
     const int pos = a.state->pos;
     if (a.state->err || pos < 0 || pos >= a.max_pos) return;
+    const float* kb = a.kc + kv * 64;
+    const float* vb = a.vc + kv * 64;
+    // V rows [c0, c0+64) of cached positions (< pos) into vbuf[buf], by the
+    // threads from `first` on
+    auto stage = [&](int c0, int buf, int first) {
+        const int nrow = min(64, pos - c0);
+        for (int i = tid - first; i < nrow * 16; i += blockDim.x - first) {
+            const int pr = i >> 4, q4 = i & 15;
+            *(float4*)&vbuf[buf][pr][4 * q4] = *(const float4*)(vb + (size_t)(c0 + pr) * KV + 4 * q4);
+        }
+    };
+    float4 kk[16];
+    if (tid < pos) {
+        const float4* kp = (const float4*)(kb + (size_t)tid * KV);
+#pragma unroll
+        for (int i = 0; i < 16; i++) kk[i] = kp[i];
+    }
+    stage(0, 0, 0);
     if (tid < 32) {
         const float2 cs = a.rope[(size_t)pos * 32 + tid];
-        const float q0 = a.q[h * 64 + 2 * tid], q1 = a.q[h * 64 + 2 * tid + 1];
+        const float q0 = tmq_fin(a.q, h * 64 + 2 * tid), q1 = tmq_fin(a.q, h * 64 + 2 * tid + 1);
         qr[2 * tid] = q0 * cs.x - q1 * cs.y;
         qr[2 * tid + 1] = q0 * cs.y + q1 * cs.x;
-        const float k0 = a.k[kv * 64 + 2 * tid], k1 = a.k[kv * 64 + 2 * tid + 1];
+        const float k0 = tmq_fin(a.k, kv * 64 + 2 * tid), k1 = tmq_fin(a.k, kv * 64 + 2 * tid + 1);
         kr[2 * tid] = k0 * cs.x - k1 * cs.y;
         kr[2 * tid + 1] = k0 * cs.y + k1 * cs.x;
     } else if (tid >= 64 && tid < 128) {
-        vn[tid - 64] = a.v[kv * 64 + tid - 64];
+        vn[tid - 64] = tmq_fin(a.v, kv * 64 + tid - 64);
     }
     __syncthreads();
-    if (h % qpk == 0 && tid < 64) {
-        a.kc[(size_t)pos * KV + kv * 64 + tid] = kr[tid];
-        a.vc[(size_t)pos * KV + kv * 64 + tid] = vn[tid];
+    if (tid < 64) {
+        if (h % qpk == 0) {
+            a.kc[(size_t)pos * KV + kv * 64 + tid] = kr[tid];
+            a.vc[(size_t)pos * KV + kv * 64 + tid] = vn[tid];
+        }
+        if (pos < 64) vbuf[0][pos][tid] = vn[tid];
     }
     // scores[p] = sum_d q[d]*k[p][d] (d ascending), / sqrt(64)
     for (int p = tid; p <= pos; p += blockDim.x) {
@@ -58,10 +82,11 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
         if (p == pos) {
             for (int d = 0; d < 64; d++) s += qr[d] * kr[d];
         } else {
-            const float4* kp = (const float4*)(a.kc + (size_t)p * KV + kv * 64);
-            float4 kk[16];
+            if (p != tid) {
+                const float4* kp = (const float4*)(kb + (size_t)p * KV);
 #pragma unroll
-            for (int i = 0; i < 16; i++) kk[i] = kp[i];
+                for (int i = 0; i < 16; i++) kk[i] = kp[i];
+            }
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 s += qr[4 * i + 0] * kk[i].x;
@@ -103,26 +128,19 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     __syncthreads();
     const float ls = s_stat[0];
     for (int p = tid; p <= pos; p += blockDim.x) ex[p] = tmq_math::tmq_expf(sc[p] - ls);
-    // context[d] = sum_p w[p]*v[p][d] (p ascending); V rows are staged in LDS
-    // 32 at a time, the next chunk loading while wave 0 adds the current one
-    auto stage = [&](int c0, int buf) {
-        const int nrow = min(32, pos + 1 - c0);
-        for (int i = tid; i < nrow * 16; i += blockDim.x) {
-            const int pr = i >> 4, q4 = i & 15, p = c0 + pr;
-            float4 v4;
-            if (p == pos) v4 = make_float4(vn[4 * q4], vn[4 * q4 + 1], vn[4 * q4 + 2], vn[4 * q4 + 3]);
-            else v4 = *(const float4*)(a.vc + (size_t)p * KV + kv * 64 + 4 * q4);
-            *(float4*)&vbuf[buf][pr][4 * q4] = v4;
-        }
-    };
-    stage(0, 0);
     __syncthreads();
+    // context[d] = sum_p w[p]*v[p][d] (p ascending): wave 0 adds chunk c0
+    // while waves 1-3 stage the next 64 rows
     float acc = 0.0f;
     int buf = 0;
-    for (int c0 = 0; c0 <= pos; c0 += 32) {
-        if (c0 + 32 <= pos) stage(c0 + 32, buf ^ 1);
+    for (int c0 = 0; c0 <= pos; c0 += 64) {
+        const int c1 = c0 + 64;
+        if (c1 <= pos && tid >= 64) {
+            stage(c1, buf ^ 1, 64);
+            if (c1 + 64 > pos && tid < 128) vbuf[buf ^ 1][pos - c1][tid - 64] = vn[tid - 64];
+        }
         if (tid < 64) {
-            const int nrow = min(32, pos + 1 - c0);
+            const int nrow = min(64, pos + 1 - c0);
             int pr = 0;
             for (; pr + 4 <= nrow; pr += 4) {
                 const float4 e4 = *(const float4*)(ex + c0 + pr);

@@ -48,6 +48,13 @@ static inline uint64_t tmq_act_bytes(int n) { return 16 + (uint64_t)n * 6 + 16; 
 //     v = finalize(acc_r);  if (bias) v = v + bias[r];  if (resid) v = y[r] + v;
 //     y[r] = v
 // (bias: sim/tmac_gguf.cpp:1595-1597; residual: :1663, :1706).
+//
+// Engine GEMVs may instead split K over `kc` workgroups per 64-row group
+// and leave int64 row sums in `kacc` (accumulated with device-scope atomics:
+// integer addition is associative, so the sums are exact in any order;
+// Q8_0: one int64 per row and 64-column tile, [rows][ntiles]) plus the
+// activation's x_scale in `xs_out`; the next launch finalises the rows (see
+// TmqDeferred).
 struct TmqWork {
     TmqTensorDev t;
     const uint8_t* act;
@@ -55,9 +62,27 @@ struct TmqWork {
     int64_t* acc;        // may be null; Q8_0: [rows][ntiles]
     const float* bias;   // may be null
     uint64_t* cand;      // Q8_0, engine GEMV: per-wave argmax candidate keys (may be null)
+    int64_t* kacc;       // engine K-split: int64 row sums (zero before the launch)
+    float* xs_out;       // engine K-split: x_scale of the launch's activation
     int32_t first_group;
-    int32_t ngroups;     // row groups (workgroups) of this GEMV
+    int32_t ngroups;     // workgroups of this GEMV (row groups x kc)
+    int32_t kc;          // engine K-split: workgroups per row group (>= 1)
     int32_t resid;
+};
+
+// Rows of a K-split engine GEMV finalised by the consumer:
+//   Q5_0 / K-quants  v = (float)((double)acc[i] * xs / (double)row_inv[i])
+//                    (sim/tmac_gguf.cpp:1303-1305)
+//   Q8_0             v = fold over tiles t of (float)((double)v + (double)P*xs*row_scale[i])
+//                    (:1075-1076)
+//   then v = v + bias[i] when a bias is given (:1595-1597).
+struct TmqDeferred {
+    const int64_t* acc;
+    const float* xs;
+    const float* row_inv;
+    const float* row_scale;
+    const float* bias;
+    int32_t ntiles;        // 0: Q5_0 / K-quants; > 0: Q8_0 tiles per row
     int32_t pad_;
 };
 
@@ -74,20 +99,38 @@ struct TmqEngState {
 // int16 activation of its launch into LDS before its row groups (the
 // reference's rms_norm / silu / matmul quantisation, sim/tmac_gguf.cpp:415-439,
 // :1225-1231), so no separate normalisation launch is needed.
-enum { TMQ_ACT_NORM = 0, TMQ_ACT_PLAIN = 1, TMQ_ACT_SILU = 2, TMQ_ACT_EMBED_NORM = 3 };
+//   EMBED_NORM  x = embedding row of tokens[pos] (process_embedding, :1955)
+//   RESID_NORM  x = x_in + d1 (the residual adds, :1663, :1706)
+//   PLAIN       x = x_in (the attention context)
+//   PRESCALED   x = x_in with max|x| given (SiLU*up from tmq_launch_silu)
+// then, for the two NORM modes, x = rms_norm(x, w) (:415-422) when w is
+// set.  x before the norm is stored to hidden_out by workgroup 0 when
+// hidden_out is set.
+enum { TMQ_ACT_RESID_NORM = 0, TMQ_ACT_PLAIN = 1, TMQ_ACT_PRESCALED = 2, TMQ_ACT_EMBED_NORM = 3 };
 #define TMQ_ENG_MAXN 6144
 struct TmqEngAct {
     int32_t mode;
     int32_t n;
-    const float* x;        // NORM / PLAIN: input vector; SILU: gate
-    const float* x2;       // SILU: up
-    const float* w;        // NORM / EMBED_NORM: RMSNorm weight
+    const float* x;            // RESID_NORM / PLAIN / PRESCALED input
+    const float* w;            // NORM modes: RMSNorm weight (null: no norm)
+    const uint32_t* max_bits;  // PRESCALED: bits of max|x| (atomic max of non-negative floats)
     float eps;
     int32_t pad_;
-    TmqEngState* state;    // EMBED_NORM: token = tokens[state->pos]
+    TmqDeferred d1;            // RESID_NORM: the residual term
+    float* hidden_out;
+    TmqEngState* state;        // EMBED_NORM: token = tokens[state->pos]
     const int32_t* tokens;
-    float* hidden_out;     // EMBED_NORM: embedding row (written by workgroup 0)
-    TmqTensorDev emb;      // EMBED_NORM: quantized embedding
+    TmqTensorDev emb;          // EMBED_NORM: quantized embedding
+};
+
+// One engine GEMV launch, passed by value: the activation recipe and up to
+// TMQ_ENG_MAXW works whose workgroups follow each other (first_group).
+#define TMQ_ENG_MAXW 3
+struct TmqEngLaunch {
+    TmqEngAct act;
+    TmqWork w[TMQ_ENG_MAXW];
+    int32_t nworks;
+    int32_t ngroups;   // total workgroups
 };
 
 // Activation-quantisation jobs: one workgroup each, at most TMQ_MAX_ACT per launch.
@@ -116,10 +159,16 @@ int tmq_launch_gemv(const TmqWork& w, hipStream_t s);
 // one launch per chain segment (descriptors of one format / clamp mode)
 int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_t* group_work_dev,
                      int total_groups, hipStream_t s);
-// engine GEMV: activation recipe + works of any formats; waves = 16 (K split
-// over the waves of a workgroup) or 4
-int tmq_launch_eng_gemv(const TmqEngAct& act, const TmqWork* works_dev, const int32_t* group_work_dev,
-                        int total_groups, int waves, hipStream_t s);
+// engine GEMV: activation recipe + works of any formats; waves = 16 or 4
+int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s);
+// x = silu(g) * u over n rows of two K-split GEMVs; *max_bits = max over
+// the bits of |x| (atomic; zero before)
+int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x, uint32_t* max_bits,
+                    hipStream_t s);
 size_t tmq_eng_lds_bytes(int n, int waves);
+// out[i] = x[i] + finalise(d, i), i < n
+int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* out, hipStream_t s);
+// zero n int64 K-split accumulators
+int tmq_launch_zero_acc(int64_t* p, size_t n, hipStream_t s);
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s);

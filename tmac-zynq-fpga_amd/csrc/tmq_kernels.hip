@@ -17,6 +17,7 @@
 
 #include "tmq_internal.h"
 #include "tmq_mathf.h"
+#include "tmq_device.h"
 
 typedef short tmq_s16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 tmq_h2 __attribute__((ext_vector_type(2)));
@@ -205,34 +206,38 @@ __device__ __forceinline__ Q4KBlk q4k_load(const TmqTensorDev& t, int b, int r) 
     for (int i = 0; i < 8; i++) k.qs[i] = ld16(t.pa + p16(b, i, 8, R, r));
     return k;
 }
+// one quarter (sub-blocks 2sp, 2sp+1: 64 weights) of a Q4_K block
 template <bool CLAMP, class AT>
-__device__ __forceinline__ void q4k_mac(const Q4KBlk& k, const AT& A, int b, float inv, int& sh, int& sl) {
-    const float d = h2f(k.h.x), dmin = h2f(k.h.x >> 16);
+__device__ __forceinline__ void q4k_mac_q(const uint4& h, const uint4& qsa, const uint4& qsb, const AT& A, int b,
+                                          int sp, float inv, int& sh, int& sl) {
+    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+    int sc0, m0, sc1, m1;
+    q4k_scale_min(h, 2 * sp, sc0, m0);
+    q4k_scale_min(h, 2 * sp + 1, sc1, m1);
+    const float A0 = (d * (float)sc0) * 0x1p24f, B0 = -(dmin * (float)m0);
+    const float A1 = (d * (float)sc1) * 0x1p20f, B1 = -(dmin * (float)m1);
 #pragma unroll
-    for (int sp = 0; sp < 4; sp++) {
-        int sc0, m0, sc1, m1;
-        q4k_scale_min(k.h, 2 * sp, sc0, m0);
-        q4k_scale_min(k.h, 2 * sp + 1, sc1, m1);
-        const float A0 = (d * (float)sc0) * 0x1p24f, B0 = -(dmin * (float)m0);
-        const float A1 = (d * (float)sc1) * 0x1p20f, B1 = -(dmin * (float)m1);
+    for (int hf = 0; hf < 2; hf++) {
+        const uint4& qs = hf ? qsb : qsa;
 #pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            const uint4& qs = k.qs[2 * sp + hf];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t w = dw_of(qs, i);
-                const uint32_t lo = w & 0x0f0f0f0fu, hi = w & 0xf0f0f0f0u;
-                const tmq_h2 l0 = lanes01(lo), l1 = lanes23(lo), h0 = lanes01(hi), h1 = lanes23(hi);
-                const int kx = (b * 256 + 64 * sp + 16 * hf + 4 * i) / 2;
-                mac4<CLAMP>(__builtin_fmaf((float)l0.x, A0, B0), __builtin_fmaf((float)l0.y, A0, B0),
-                            __builtin_fmaf((float)l1.x, A0, B0), __builtin_fmaf((float)l1.y, A0, B0),
-                            inv, A, kx, sh, sl);
-                mac4<CLAMP>(__builtin_fmaf((float)h0.x, A1, B1), __builtin_fmaf((float)h0.y, A1, B1),
-                            __builtin_fmaf((float)h1.x, A1, B1), __builtin_fmaf((float)h1.y, A1, B1),
-                            inv, A, kx + 16, sh, sl);
-            }
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = dw_of(qs, i);
+            const uint32_t lo = w & 0x0f0f0f0fu, hi = w & 0xf0f0f0f0u;
+            const tmq_h2 l0 = lanes01(lo), l1 = lanes23(lo), h0 = lanes01(hi), h1 = lanes23(hi);
+            const int kx = (b * 256 + 64 * sp + 16 * hf + 4 * i) / 2;
+            mac4<CLAMP>(__builtin_fmaf((float)l0.x, A0, B0), __builtin_fmaf((float)l0.y, A0, B0),
+                        __builtin_fmaf((float)l1.x, A0, B0), __builtin_fmaf((float)l1.y, A0, B0),
+                        inv, A, kx, sh, sl);
+            mac4<CLAMP>(__builtin_fmaf((float)h0.x, A1, B1), __builtin_fmaf((float)h0.y, A1, B1),
+                        __builtin_fmaf((float)h1.x, A1, B1), __builtin_fmaf((float)h1.y, A1, B1),
+                        inv, A, kx + 16, sh, sl);
         }
     }
+}
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q4k_mac(const Q4KBlk& k, const AT& A, int b, float inv, int& sh, int& sl) {
+#pragma unroll
+    for (int sp = 0; sp < 4; sp++) q4k_mac_q<CLAMP>(k.h, k.qs[2 * sp], k.qs[2 * sp + 1], A, b, sp, inv, sh, sl);
 }
 
 // ---------------------------------------------------------------- Q6_K
@@ -255,37 +260,68 @@ __device__ __forceinline__ Q6KBlk q6k_load(const TmqTensorDev& t, int b, int r) 
     k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
     return k;
 }
+// one quarter (half, lc: 64 weights) of a Q6_K block
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q6k_mac_q(const uint4& sc, float ss, const uint4& qla, const uint4& qlb,
+                                          const uint4& qhc, const AT& A, int b, int half, int lc, float inv,
+                                          int& sh, int& sl) {
+#pragma unroll
+    for (int sub = 0; sub < 4; sub++) {
+        const float S = ss * (float)(int8_t)byte_of(sc, half * 8 + lc + 2 * sub);
+        const float nS = -32.0f * S, S24 = S * 0x1p24f;
+        const uint4& src = (sub & 1) ? qlb : qla;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t ql = dw_of(src, i), qh = dw_of(qhc, i);
+            const uint32_t nib = (sub < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+            const uint32_t hs = (sub == 0) ? (qh << 4) : (sub == 1) ? (qh << 2) : (sub == 2) ? qh : (qh >> 2);
+            const uint32_t U = (hs & 0x30303030u) | nib;
+            const int kx = (b * 256 + half * 128 + sub * 32 + 16 * lc + 4 * i) / 2;
+            // E = S*(u-32) = fma_mix(u*2^-24, S*2^24, -32*S), exact
+            const tmq_h2 u0 = lanes01(U), u1 = lanes23(U);
+            mac4<CLAMP>(__builtin_fmaf((float)u0.x, S24, nS), __builtin_fmaf((float)u0.y, S24, nS),
+                        __builtin_fmaf((float)u1.x, S24, nS), __builtin_fmaf((float)u1.y, S24, nS),
+                        inv, A, kx, sh, sl);
+        }
+    }
+}
 template <bool CLAMP, class AT>
 __device__ __forceinline__ void q6k_mac(const Q6KBlk& k, const AT& A, int b, float inv, int& sh, int& sl) {
     const float ss = h2f(k.d);
 #pragma unroll
-    for (int half = 0; half < 2; half++) {
+    for (int half = 0; half < 2; half++)
 #pragma unroll
-        for (int lc = 0; lc < 2; lc++) {
-            const uint4& qla = k.ql[half * 4 + lc];
-            const uint4& qlb = k.ql[half * 4 + 2 + lc];
-            const uint4& qhc = k.qh[half * 2 + lc];
-#pragma unroll
-            for (int sub = 0; sub < 4; sub++) {
-                const float S = ss * (float)(int8_t)byte_of(k.sc, half * 8 + lc + 2 * sub);
-                const float nS = -32.0f * S, S24 = S * 0x1p24f;
-                const uint4& src = (sub & 1) ? qlb : qla;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t ql = dw_of(src, i), qh = dw_of(qhc, i);
-                    const uint32_t nib = (sub < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
-                    const uint32_t hs = (sub == 0) ? (qh << 4) : (sub == 1) ? (qh << 2) : (sub == 2) ? qh : (qh >> 2);
-                    const uint32_t U = (hs & 0x30303030u) | nib;
-                    const int kx = (b * 256 + half * 128 + sub * 32 + 16 * lc + 4 * i) / 2;
-                    // E = S*(u-32) = fma_mix(u*2^-24, S*2^24, -32*S), exact
-                    const tmq_h2 u0 = lanes01(U), u1 = lanes23(U);
-                    mac4<CLAMP>(__builtin_fmaf((float)u0.x, S24, nS), __builtin_fmaf((float)u0.y, S24, nS),
-                                __builtin_fmaf((float)u1.x, S24, nS), __builtin_fmaf((float)u1.y, S24, nS),
-                                inv, A, kx, sh, sl);
-                }
-            }
-        }
-    }
+        for (int lc = 0; lc < 2; lc++)
+            q6k_mac_q<CLAMP>(k.sc, ss, k.ql[half * 4 + lc], k.ql[half * 4 + 2 + lc], k.qh[half * 2 + lc], A, b,
+                             half, lc, inv, sh, sl);
+}
+
+// Quarter-block units (64 weights) of the K-quants, for the engine's K split.
+struct Q4KQ {
+    uint4 h, qa, qb;
+};
+__device__ __forceinline__ Q4KQ q4kq_load(const TmqTensorDev& t, int b, int q, int r) {
+    const size_t R = t.rows_pad;
+    Q4KQ k;
+    k.h = ld16(t.pb + p16(b, 0, 1, R, r));
+    k.qa = ld16(t.pa + p16(b, 2 * q, 8, R, r));
+    k.qb = ld16(t.pa + p16(b, 2 * q + 1, 8, R, r));
+    return k;
+}
+struct Q6KQ {
+    uint4 qla, qlb, qhc, sc;
+    uint32_t d;
+};
+__device__ __forceinline__ Q6KQ q6kq_load(const TmqTensorDev& t, int b, int q, int r) {
+    const size_t R = t.rows_pad;
+    const int half = q >> 1, lc = q & 1;
+    Q6KQ k;
+    k.qla = ld16(t.pa + p16(b, half * 4 + lc, 8, R, r));
+    k.qlb = ld16(t.pa + p16(b, half * 4 + 2 + lc, 8, R, r));
+    k.qhc = ld16(t.pb + p16(b, half * 2 + lc, 4, R, r));
+    k.sc = ld16(t.pc + p16(b, 0, 1, R, r));
+    k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
+    return k;
 }
 
 // format dispatch for the K-split group code
@@ -533,71 +569,148 @@ __device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw) {
     return L;
 }
 
-// The activation of the launch, quantised into L.xh / L.xl; returns x_scale.
-// rms_norm: sim/tmac_gguf.cpp:415-422 (sequential fp32 sum of squares, by one
-// lane, from LDS); silu*up: :434-439, :1693-1697; quantisation: :1225-1231.
-__device__ float eng_prologue(const TmqEngAct& a, const EngLds& L) {
-    const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
-    if (a.mode == TMQ_ACT_EMBED_NORM) {
-        const int tok = a.tokens[a.state->pos];
-        for (int i = tid; i < n; i += nt) {
-            const float v = tensor_elem(a.emb, tok, i);
-            L.x[i] = v;
-            if (blockIdx.x == 0) a.hidden_out[i] = v;
-        }
-    } else if (a.mode == TMQ_ACT_SILU) {
-        for (int i = tid; i < n; i += nt) {
-            const float g = a.x[i];
-            L.x[i] = (g / (1.0f + tmq_math::tmq_expf(-g))) * a.x2[i];
-        }
-    } else {
-        for (int i = tid; i < n; i += nt) L.x[i] = a.x[i];
+// Sequential fp32 sum of v[0..n) in index order (the reference's loops),
+// by the calling lane, from LDS.  A dependent fp32 add issues every ~8
+// cycles; the reads of the next 32 values overlap the current 32 adds
+// (two register batches used in turn, no copies between them).
+__device__ __forceinline__ float seq_sum_lds(const float* v, int n) {
+    float sum = 0.0f;
+    const int n64 = n & ~63;
+    const float4* q = (const float4*)v;
+    float4 A[8], B[8];
+    if (n64) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) A[j] = q[j];
     }
-    if (a.mode == TMQ_ACT_NORM || a.mode == TMQ_ACT_EMBED_NORM) {
-        float* sq = (float*)L.xh;
-        for (int i = tid; i < n; i += nt) sq[i] = L.x[i] * L.x[i];
-        __syncthreads();
-        if (tid == 0) {
-            float sum = 0.0f;
-            int i = 0;
-            // 16 squares per batch of LDS reads, added in index order
-            for (; i + 16 <= n; i += 16) {
-                float4 v[4];
+    for (int i = 0; i < n64; i += 64) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) v[j] = *(const float4*)(sq + i + 4 * j);
+        for (int j = 0; j < 8; j++) B[j] = q[i / 4 + 8 + j];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    sum += v[j].x;
-                    sum += v[j].y;
-                    sum += v[j].z;
-                    sum += v[j].w;
-                }
+        for (int j = 0; j < 8; j++) {
+            sum += A[j].x;
+            sum += A[j].y;
+            sum += A[j].z;
+            sum += A[j].w;
+        }
+        if (i + 64 < n64) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) A[j] = q[i / 4 + 16 + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            sum += B[j].x;
+            sum += B[j].y;
+            sum += B[j].z;
+            sum += B[j].w;
+        }
+    }
+    for (int i = n64; i < n; i++) sum += v[i];
+    return sum;
+}
+
+// The activation of the launch (TmqEngAct), quantised into L.xh / L.xl over
+// the columns [c0, c1) the workgroup reads (all of them for the modes that
+// need the whole vector); returns x_scale.
+//   rms_norm (sim/tmac_gguf.cpp:415-422): o = fl(fl(x*w)*s), s from the
+//   sequential sum of squares (one lane, from LDS).  The max of |o| is taken
+//   as fl(max|fl(x*w)| * s) while that lane sums: rounding is monotone and
+//   s > 0, so it is the same value, without waiting for s.
+//   quantisation (:1225-1231): x_scale = max|o| / 32767 (1 below 1e-10),
+//   xq = (int16)roundf(o / x_scale).
+__device__ float eng_prologue(const TmqEngAct& a, const EngLds& L, int c0, int c1) {
+    const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
+    const bool wr = a.hidden_out && blockIdx.x == 0;
+    const bool norm = (a.mode == TMQ_ACT_RESID_NORM || a.mode == TMQ_ACT_EMBED_NORM) && a.w;
+    float* sq = (float*)L.xh;  // squares, consumed before xh/xl are written
+    float m = 0.0f;
+    if (a.mode == TMQ_ACT_PRESCALED) {
+        // max given; only the workgroup's columns are needed
+        for (int i = c0 + tid; i < c1; i += nt) L.x[i] = a.x[i];
+    } else if (a.mode == TMQ_ACT_RESID_NORM && a.d1.ntiles == 0 && n <= 4 * nt) {
+        // up to 4 elements per thread: every load first, then the arithmetic
+        float xin[4], wv[4], ri[4], bi[4];
+        int64_t ac[4];
+        const float dxs = *a.d1.xs;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = tid + e * nt;
+            if (i < n) {
+                xin[e] = a.x[i];
+                ac[e] = tmq_ld_acc(a.d1.acc + i);
+                ri[e] = a.d1.row_inv[i];
+                bi[e] = a.d1.bias ? a.d1.bias[i] : 0.0f;
+                wv[e] = norm ? a.w[i] : 1.0f;
             }
-            for (; i < n; i++) sum += sq[i];
-            const float mean = sum / (float)n;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = tid + e * nt;
+            if (i < n) {
+                float d = (float)(((double)ac[e] * (double)dxs) / (double)ri[e]);
+                if (a.d1.bias) d = d + bi[e];
+                float v = xin[e] + d;
+                if (wr) a.hidden_out[i] = v;
+                if (norm) {
+                    sq[i] = v * v;
+                    v = v * wv[e];
+                }
+                L.x[i] = v;
+                m = fmaxf(m, fabsf(v));
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        if ((tid & 63) == 0) L.red[2 + (tid >> 6)] = m;
+    } else {
+        int tok = 0;
+        if (a.mode == TMQ_ACT_EMBED_NORM) tok = a.tokens[a.state->pos];
+        for (int i = tid; i < n; i += nt) {
+            float v;
+            if (a.mode == TMQ_ACT_EMBED_NORM) v = tensor_elem(a.emb, tok, i);
+            else if (a.mode == TMQ_ACT_RESID_NORM) v = a.x[i] + tmq_fin(a.d1, i);
+            else v = a.x[i];
+            if (wr) a.hidden_out[i] = v;
+            if (norm) {
+                sq[i] = v * v;
+                v = v * a.w[i];
+            }
+            L.x[i] = v;
+            m = fmaxf(m, fabsf(v));
+        }
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        if ((tid & 63) == 0) L.red[2 + (tid >> 6)] = m;
+    }
+    __syncthreads();
+    float s = 1.0f;  // the norm's scale
+    if (norm) {
+        if (tid == 0) {
+            const float mean = seq_sum_lds(sq, n) / (float)n;
             L.red[0] = 1.0f / sqrtf(mean + a.eps);
         }
         __syncthreads();
-        const float scale = L.red[0];
-        for (int i = tid; i < n; i += nt) L.x[i] = L.x[i] * a.w[i] * scale;
+        s = L.red[0];
     }
-    float m = 0.0f;
-    for (int i = tid; i < n; i += nt) m = fmaxf(m, fabsf(L.x[i]));
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    __syncthreads();  // all reads of red[0] / the squares are done
-    if ((tid & 63) == 0) L.red[1 + (tid >> 6)] = m;
-    __syncthreads();
-    float mm = 0.0f;
-    for (int i = 0; i < (int)(nt >> 6); i++) mm = fmaxf(mm, L.red[1 + i]);
-    const float s = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
-    for (int k = tid; k < n / 2; k += nt) {
-        const int p = (int)(int16_t)roundf(L.x[2 * k] / s);
-        const int q = (int)(int16_t)roundf(L.x[2 * k + 1] / s);
+    float mm;
+    if (a.mode == TMQ_ACT_PRESCALED) {
+        mm = __builtin_bit_cast(float, __hip_atomic_load(a.max_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    } else {
+        mm = 0.0f;
+        for (int i = 0; i < (int)(nt >> 6); i++) mm = fmaxf(mm, L.red[2 + i]);
+        if (norm) mm = mm * s;
+    }
+    const float xs = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
+    for (int k = (c0 >> 1) + tid; k < (c1 >> 1); k += nt) {
+        float u = L.x[2 * k], v = L.x[2 * k + 1];
+        if (norm) {
+            u = u * s;
+            v = v * s;
+        }
+        const int p = (int)(int16_t)roundf(u / xs);
+        const int q = (int)(int16_t)roundf(v / xs);
         L.xh[k] = ((uint32_t)(p >> 8) & 0xffffu) | ((uint32_t)(q >> 8) << 16);
         L.xl[k] = ((uint32_t)p & 0xffu) | (((uint32_t)q & 0xffu) << 16);
     }
     __syncthreads();
-    return s;
+    return xs;
 }
 
 __device__ __forceinline__ ActL eng_act(const EngLds& L, float xs) {
@@ -608,36 +721,53 @@ __device__ __forceinline__ ActL eng_act(const EngLds& L, float xs) {
     return A;
 }
 
+// Work unit u of a row: Q5_0 block u, or K-quant quarter block (u >> 2, u & 3).
+template <int FMT> struct UnitOf;
+template <> struct UnitOf<kQ5_0> { typedef Q5Blk T; static constexpr int per_block = 1; };
+template <> struct UnitOf<kQ4_K> { typedef Q4KQ T; static constexpr int per_block = 4; };
+template <> struct UnitOf<kQ6_K> { typedef Q6KQ T; static constexpr int per_block = 4; };
+template <int FMT>
+__device__ __forceinline__ typename UnitOf<FMT>::T unit_load(const TmqTensorDev& t, int u, int r) {
+    if constexpr (FMT == kQ5_0) return q5_load(t, u, r);
+    else if constexpr (FMT == kQ4_K) return q4kq_load(t, u >> 2, u & 3, r);
+    else return q6kq_load(t, u >> 2, u & 3, r);
+}
+template <int FMT, class AT>
+__device__ __forceinline__ void unit_mac(const typename UnitOf<FMT>::T& k, const AT& A, int u, float inv,
+                                         int& sh, int& sl) {
+    if constexpr (FMT == kQ5_0) q5_mac<false>(k, A, u, inv, sh, sl);
+    else if constexpr (FMT == kQ4_K) q4k_mac_q<false>(k.h, k.qa, k.qb, A, u >> 2, u & 3, inv, sh, sl);
+    else q6k_mac_q<false>(k.sc, h2f(k.d), k.qla, k.qlb, k.qhc, A, u >> 2, (u & 3) >> 1, u & 1, inv, sh, sl);
+}
+
+// Q5_0 / K-quant row group g, K chunk c: the workgroup's units are split
+// over its waves; each wave keeps its next unit in flight while it
+// multiplies.  With kc > 1 (or a kacc) the int64 row sums go to w.kacc.
 template <int FMT, int NW>
-__device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int g) {
-    typedef typename BlkOf<FMT>::T Blk;
+__device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int gi) {
+    typedef typename UnitOf<FMT>::T Unit;
     const TmqTensorDev& t = w.t;
+    const int kc = w.kc, g = gi / kc, c = gi - g * kc;
+    const int nu = t.nb * UnitOf<FMT>::per_block;
+    const int u0 = (int)((int64_t)c * nu / kc), u1 = (int)((int64_t)(c + 1) * nu / kc);
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
-    Blk cur{};
-    if (wave < t.nb) cur = blk_load<FMT>(t, wave, r);
+    Unit cur{};
+    if (u0 + wave < u1) cur = unit_load<FMT>(t, u0 + wave, r);
     const float inv = t.row_inv[r];
-    const ActL A = eng_act(L, eng_prologue(a, L));
+    constexpr int QK = FMT == kQ5_0 ? 32 : 256, PB = UnitOf<FMT>::per_block;
+    const float xs = eng_prologue(a, L, (u0 / PB) * QK, ((u1 + PB - 1) / PB) * QK);
+    if (w.xs_out && gi == 0 && threadIdx.x == 0) *w.xs_out = xs;
+    const ActL A = eng_act(L, xs);
     int64_t acc = 0;
-    // Q5_0 / Q4_K keep the next block in flight while multiplying; a Q6_K
-    // block (53 registers) is loaded when needed (at most a few per wave)
-    if constexpr (FMT != kQ6_K) {
-        for (int b = wave; b < t.nb; b += NW) {
-            const bool more = b + NW < t.nb;
-            Blk nxt{};
-            if (more) nxt = blk_load<FMT>(t, b + NW, r);
-            int sh = 0, sl = 0;
-            blk_mac<FMT, false>(cur, A, b, inv, sh, sl);
-            acc += (int64_t)sh * 256 + sl;
-            if (more) cur = nxt;
-        }
-    } else {
-        for (int b = wave; b < t.nb; b += NW) {
-            if (b != wave) cur = blk_load<FMT>(t, b, r);
-            int sh = 0, sl = 0;
-            blk_mac<FMT, false>(cur, A, b, inv, sh, sl);
-            acc += (int64_t)sh * 256 + sl;
-        }
+    for (int u = u0 + wave; u < u1; u += NW) {
+        const bool more = u + NW < u1;
+        Unit nxt{};
+        if (more) nxt = unit_load<FMT>(t, u + NW, r);
+        int sh = 0, sl = 0;
+        unit_mac<FMT>(cur, A, u, inv, sh, sl);
+        acc += (int64_t)sh * 256 + sl;
+        if (more) cur = nxt;
     }
     L.part[wave * 64 + lane] = acc;
     __syncthreads();
@@ -645,8 +775,46 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
         int64_t tot = 0;
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += L.part[i * 64 + lane];
-        if (w.acc) w.acc[r] = tot;
-        if (w.y) store_y(w, r, (float)(((double)tot * (double)A.xs) / (double)inv));
+        if (w.kacc) {
+            __hip_atomic_fetch_add(w.kacc + r, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            if (w.acc) w.acc[r] = tot;
+            if (w.y) store_y(w, r, (float)(((double)tot * (double)xs) / (double)inv));
+        }
+    }
+}
+
+// Q8_0 K-split (attn_v): 64-row group g, tile chunk c; each wave takes
+// tiles (two blocks) of the chunk and stores their int64 P into
+// kacc[r][tile] (one writer per slot; the consumer folds the tiles in order).
+template <int NW>
+__device__ __forceinline__ void eng_group_q8_split(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int gi) {
+    const TmqTensorDev& t = w.t;
+    const int kc = w.kc, g = gi / kc, c = gi - g * kc;
+    const int nt = (t.cols + 63) / 64;
+    const int t0 = (int)((int64_t)c * nt / kc), t1 = (int)((int64_t)(c + 1) * nt / kc);
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    Q8Blk b0{}, b1{};
+    if (t0 + wave < t1) {
+        b0 = q8_load(t, 2 * (t0 + wave), r);
+        if (2 * (t0 + wave) + 1 < t.nb) b1 = q8_load(t, 2 * (t0 + wave) + 1, r);
+    }
+    const float ri = t.row_inv[r];
+    const float xs = eng_prologue(a, L, 64 * t0, min(64 * t1, t.cols));
+    if (w.xs_out && gi == 0 && threadIdx.x == 0) *w.xs_out = xs;
+    const ActL A = eng_act(L, xs);
+    for (int tt = t0 + wave; tt < t1; tt += NW) {
+        if (tt != t0 + wave) {
+            b0 = q8_load(t, 2 * tt, r);
+            if (2 * tt + 1 < t.nb) b1 = q8_load(t, 2 * tt + 1, r);
+        }
+        int sh = 0, sl = 0;
+        q8_mac(b0, A, 2 * tt, ri, sh, sl);
+        if (2 * tt + 1 < t.nb) q8_mac(b1, A, 2 * tt + 1, ri, sh, sl);
+        if (r < t.rows)
+            __hip_atomic_store(w.kacc + (size_t)r * nt + tt, (int64_t)sh * 256 + sl, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -657,6 +825,9 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int r) {
     return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)r);
 }
 
+// Q8_0 direct (the logits): each wave owns 64 rows and walks all tiles,
+// folding in double (sim/tmac_gguf.cpp:1075-1076), and leaves its argmax
+// candidate.
 template <int NW>
 __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int g) {
     const TmqTensorDev& t = w.t;
@@ -672,7 +843,7 @@ __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L
         ri = t.row_inv[r];
         rs = t.row_scale[r];
     }
-    const ActL A = eng_act(L, eng_prologue(a, L));
+    const ActL A = eng_act(L, eng_prologue(a, L, 0, t.cols));
     if (!active) return;
     const int nt = (t.cols + 63) / 64;
     float y = 0.0f;
@@ -703,21 +874,67 @@ __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L
     }
 }
 
-template <int NW>
-__global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngAct a, const TmqWork* __restrict__ works,
-                                                          const int32_t* __restrict__ gmap) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char eng_smem[];
-    const EngLds L = eng_lds(eng_smem, a.n, NW);
-    if (a.state && a.state->err) return;
-    const TmqWork& w = works[gmap[blockIdx.x]];
+// Format codes of the engine kernel variants: the ggml types, and
+// kQ8_DIRECT for the logits (Q8_0, one wave per 64 rows, direct output).
+constexpr int kQ8_DIRECT = 108;
+
+template <int NW, int FMT>
+__device__ __forceinline__ void eng_dispatch(const TmqEngAct& a, const EngLds& L, const TmqWork& w) {
     const int g = blockIdx.x - w.first_group;
-    switch (w.t.type) {
-    case kQ5_0: eng_group_k<kQ5_0, NW>(a, L, w, g); break;
-    case kQ4_K: eng_group_k<kQ4_K, NW>(a, L, w, g); break;
-    case kQ6_K: eng_group_k<kQ6_K, NW>(a, L, w, g); break;
-    case kQ8_0: eng_group_q8<NW>(a, L, w, g); break;
-    default: break;
+    if constexpr (FMT == kQ8_0) eng_group_q8_split<NW>(a, L, w, g);
+    else if constexpr (FMT == kQ8_DIRECT) eng_group_q8<NW>(a, L, w, g);
+    else eng_group_k<FMT, NW>(a, L, w, g);
+}
+
+// The launch arrives by value (kernel arguments): no dependent loads
+// before the weight prefetch and the activation prologue start.  One
+// instantiation per format pair keeps the code small: every work uses FA
+// except the last, which uses FB.
+template <int NW, int FA, int FB>
+__global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngLaunch P) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char eng_smem[];
+    const EngLds L = eng_lds(eng_smem, P.act.n, NW);
+    const int b = blockIdx.x;
+    const int wi = (P.nworks > 2 && b >= P.w[2].first_group) ? 2 : (P.nworks > 1 && b >= P.w[1].first_group) ? 1 : 0;
+    const TmqWork w = wi == 2 ? P.w[2] : wi == 1 ? P.w[1] : P.w[0];
+    if (FA != FB && wi == P.nworks - 1) eng_dispatch<NW, FB>(P.act, L, w);
+    else eng_dispatch<NW, FA>(P.act, L, w);
+}
+
+// x = silu(g) * u (sim/tmac_gguf.cpp:434-439, :1693-1697) from two K-split
+// GEMVs, once per layer; the workgroups' max |x| meet in max_bits.
+__global__ __launch_bounds__(256) void silu_kernel(TmqDeferred g, TmqDeferred u, int n, float* x,
+                                                   uint32_t* max_bits) {
+    __shared__ float red[4];
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    float m = 0.0f;
+    if (i < n) {
+        const float gv = tmq_fin(g, i);
+        const float v = (gv / (1.0f + tmq_math::tmq_expf(-gv))) * tmq_fin(u, i);
+        x[i] = v;
+        m = fabsf(v);
     }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        __hip_atomic_fetch_max(max_bits, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// hidden + the pending deferred rows (the residual stream as the host sees
+// it), for reads from outside a step (dumps, tmq_model_hidden).
+__global__ __launch_bounds__(256) void resid_view_kernel(const float* __restrict__ x, TmqDeferred d, int n,
+                                                         float* out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = x[i] + tmq_fin(d, i);
+}
+
+// Zeroes n int64 K-split accumulators (at the device coherence point).
+__global__ __launch_bounds__(256) void zero_acc_kernel(int64_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        __hip_atomic_store(p + i, (int64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------ activation prep
@@ -951,19 +1168,53 @@ int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_
     return (int)hipLaunchKernel(k, dim3(total_groups), dim3(TMQ_WG), args, 0, s);
 }
 
+int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(resid_view_kernel, dim3((n + 255) / 256), dim3(256), 0, s, x, d, n, out);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_zero_acc(int64_t* p, size_t n, hipStream_t s) {
+    if (!n) return 0;
+    size_t g = (n + 255) / 256;
+    if (g > 1024) g = 1024;
+    hipLaunchKernelGGL(zero_acc_kernel, dim3((unsigned)g), dim3(256), 0, s, p, n);
+    return (int)hipGetLastError();
+}
+
 size_t tmq_eng_lds_bytes(int n, int waves) { return 8 * (size_t)n + 8 * 64 * (size_t)waves + 256; }
 
-int tmq_launch_eng_gemv(const TmqEngAct& act, const TmqWork* works_dev, const int32_t* group_work_dev,
-                        int total_groups, int waves, hipStream_t s) {
-    if (total_groups <= 0) return 0;
-    if (act.n <= 0 || act.n > TMQ_ENG_MAXN || act.n % 2) return (int)hipErrorInvalidValue;
-    const size_t lds = tmq_eng_lds_bytes(act.n, waves);
-    if (waves == 16)
-        hipLaunchKernelGGL(eng_gemv_kernel<16>, dim3(total_groups), dim3(1024), lds, s, act, works_dev, group_work_dev);
-    else if (waves == 4)
-        hipLaunchKernelGGL(eng_gemv_kernel<4>, dim3(total_groups), dim3(256), lds, s, act, works_dev, group_work_dev);
-    else
+template <int NW>
+static void* eng_kernel_for(int fa, int fb) {
+#define TMQ_ENG_K(A, B) (void*)eng_gemv_kernel<NW, A, B>
+    if (fa == kQ5_0 && fb == kQ5_0) return TMQ_ENG_K(kQ5_0, kQ5_0);
+    if (fa == kQ5_0 && fb == kQ8_0) return TMQ_ENG_K(kQ5_0, kQ8_0);
+    if (fa == kQ4_K && fb == kQ4_K) return TMQ_ENG_K(kQ4_K, kQ4_K);
+    if (fa == kQ6_K && fb == kQ6_K) return TMQ_ENG_K(kQ6_K, kQ6_K);
+    if (fa == kQ8_0 && fb == kQ8_0) return TMQ_ENG_K(kQ8_0, kQ8_0);
+    if (fa == kQ8_DIRECT && fb == kQ8_DIRECT) return TMQ_ENG_K(kQ8_DIRECT, kQ8_DIRECT);
+#undef TMQ_ENG_K
+    return nullptr;
+}
+
+int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
+    if (l.ngroups <= 0) return 0;
+    if (l.act.n <= 0 || l.act.n > TMQ_ENG_MAXN || l.act.n % 2 || l.nworks < 1 || l.nworks > TMQ_ENG_MAXW)
         return (int)hipErrorInvalidValue;
+    // format of the first and the last work (the others must match the first)
+    auto code = [](const TmqWork& w) { return w.t.type == kQ8_0 && !w.kacc ? kQ8_DIRECT : w.t.type; };
+    const int fa = code(l.w[0]), fb = code(l.w[l.nworks - 1]);
+    for (int i = 1; i + 1 < l.nworks; i++)
+        if (code(l.w[i]) != fa) return (int)hipErrorInvalidValue;
+    void* k = waves == 16 ? eng_kernel_for<16>(fa, fb) : waves == 4 ? eng_kernel_for<4>(fa, fb) : nullptr;
+    if (!k) return (int)hipErrorInvalidValue;
+    TmqEngLaunch arg = l;
+    void* args[] = {&arg};
+    return (int)hipLaunchKernel(k, dim3(l.ngroups), dim3(64 * waves), args, tmq_eng_lds_bytes(l.act.n, waves), s);
+}
+
+int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x, uint32_t* max_bits,
+                    hipStream_t s) {
+    hipLaunchKernelGGL(silu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, n, x, max_bits);
     return (int)hipGetLastError();
 }
 

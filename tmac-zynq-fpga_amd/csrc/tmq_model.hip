@@ -31,10 +31,10 @@ struct Entry {
     const uint8_t* data;
 };
 
-// one engine GEMV launch: activation recipe + a contiguous gmap range
+// one engine GEMV launch (passed by value) and its workgroup size
 struct Launch {
-    TmqEngAct act{};
-    int gmap_off = 0, ngroups = 0, waves = 16;
+    TmqEngLaunch P{};
+    int waves = 4;
 };
 
 struct Layer {
@@ -43,6 +43,8 @@ struct Layer {
     size_t attn_norm = 0, ffn_norm = 0;  // offsets into fvec (floats)
     long bq = -1, bk = -1, bv = -1;      // bias offsets or -1
     Launch qkv, o_l, gu, dn;
+    // K-split results of this layer's GEMVs, finalised by their consumers
+    TmqDeferred dq{}, dk{}, dv{}, dout{}, dg{}, du{}, dd{};
 };
 
 inline uint64_t rd64(const uint8_t* p) {
@@ -115,17 +117,21 @@ struct tmq_model {
     std::vector<tmq_tensor*> owned;
     // device memory (one allocation)
     void* dmem = nullptr;
-    void* tail_mem = nullptr;
-    float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ctxv = nullptr;
-    float *gate = nullptr, *up = nullptr, *logits = nullptr, *fvec = nullptr, *dump = nullptr;
+    // residual stream, double buffered: hid[1] = after the attention block's
+    // input materialisation (embedding / + down), hid[0] = after + attn_output
+    float* hid[2] = {nullptr, nullptr};
+    float *ctxv = nullptr, *logits = nullptr, *fvec = nullptr, *dump = nullptr, *view = nullptr;
+    int64_t* kacc = nullptr;  // all K-split accumulators of a step
+    size_t kacc_n = 0;
+    float* xs = nullptr;      // x_scale slots, 4 per layer
     uint64_t* cand = nullptr;  // logits argmax candidates, one per 64 rows
     int n_cand = 0;
     float *kc = nullptr, *vc = nullptr;
     float2* rope = nullptr;
     TmqEngState* state = nullptr;
     int32_t* tokens = nullptr;
-    TmqWork* works_dev = nullptr;
-    int32_t* gmap_dev = nullptr;
+    float* silu_x = nullptr;      // SiLU(gate) * up of the current layer
+    uint32_t* max_bits = nullptr; // per layer max |silu_x| (in the zeroed accumulator range)
     Launch logits_l;
     uint64_t weight_bytes = 0;
     int pos = -1;  // host mirror of state.pos
@@ -145,34 +151,33 @@ void model_release(tmq_model* m) {
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
     for (tmq_tensor* t : m->owned) tmq_tensor_free(t);
     if (m->dmem) (void)hipFree(m->dmem);
-    if (m->tail_mem) (void)hipFree(m->tail_mem);
     delete m;
 }
 
 // ---------------------------------------------------------------- launches
 int launch_gemv(tmq_model* m, const Launch& l) {
-    LAUNCH_TRY(tmq_launch_eng_gemv(l.act, m->works_dev, m->gmap_dev + l.gmap_off, l.ngroups, l.waves,
-                                   m->ctx->stream));
+    LAUNCH_TRY(tmq_launch_eng_gemv(l.P, l.waves, m->ctx->stream));
     return 0;
 }
 
 // all layers at the current position (forward_all_layers); layer 0's QKV
-// launch also performs process_embedding of tokens[pos].  With dump, the
-// hidden state after the embedding and after every layer is copied to
-// dump[(l+1)*H].
+// launch also performs process_embedding of tokens[pos].  The step's K-split
+// accumulators are zeroed first.  With dump, the residual stream after the
+// embedding and after every layer is copied to dump[(l+1)*H].
 int launch_layers(tmq_model* m, bool dump) {
     hipStream_t s = m->ctx->stream;
     const tmq_model_config& c = m->cfg;
     const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM;
+    LAUNCH_TRY(tmq_launch_zero_acc(m->kacc, m->kacc_n, s));
     for (int l = 0; l < c.n_layers; l++) {
         const Layer& L = m->layers[l];
         int rc = launch_gemv(m, L.qkv);
         if (rc) return rc;
-        if (dump && l == 0) HIP_TRY(hipMemcpyAsync(m->dump, m->hidden, sizeof(float) * H, hipMemcpyDeviceToDevice, s));
+        if (dump && l == 0) HIP_TRY(hipMemcpyAsync(m->dump, m->hid[1], sizeof(float) * H, hipMemcpyDeviceToDevice, s));
         TmqAttnArgs aa{};
-        aa.q = m->q;
-        aa.k = m->k;
-        aa.v = m->v;
+        aa.q = L.dq;
+        aa.k = L.dk;
+        aa.v = L.dv;
         aa.kc = m->kc + (size_t)l * c.max_seq * KV;
         aa.vc = m->vc + (size_t)l * c.max_seq * KV;
         aa.rope = m->rope;
@@ -184,10 +189,9 @@ int launch_layers(tmq_model* m, bool dump) {
         LAUNCH_TRY(tmq_launch_attn(aa, s));
         if ((rc = launch_gemv(m, L.o_l))) return rc;
         if ((rc = launch_gemv(m, L.gu))) return rc;
+        LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s));
         if ((rc = launch_gemv(m, L.dn))) return rc;
-        if (dump)
-            HIP_TRY(hipMemcpyAsync(m->dump + (size_t)(l + 1) * H, m->hidden, sizeof(float) * H,
-                                   hipMemcpyDeviceToDevice, s));
+        if (dump) LAUNCH_TRY(tmq_launch_resid_view(m->hid[0], L.dd, H, m->dump + (size_t)(l + 1) * H, s));
     }
     return 0;
 }
@@ -199,8 +203,8 @@ int launch_feed_impl(tmq_model* m, bool dump) {
 }
 int launch_feed(tmq_model* m) { return launch_feed_impl(m, false); }
 
-// get_logits_q8: output_norm (when present) + the Q8_0 logits GEMV, which
-// also leaves per-wave argmax candidates
+// get_logits_q8: output_norm (when present) of the residual stream + the
+// Q8_0 logits GEMV, which also leaves per-wave argmax candidates
 int launch_logits(tmq_model* m) { return launch_gemv(m, m->logits_l); }
 
 // one greedy generate() iteration: logits, argmax -> tokens[pos+1] (and
@@ -367,6 +371,18 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     }
     if ((rc = add_vec("output_norm.weight", H, false, &m->out_norm))) return rc;
 
+    // K-split accumulators per layer: q, k, v (Q8_0: rows x tiles), o, gate,
+    // up, down
+    auto acc_rows = [](const tmq_tensor* t) -> size_t {
+        return t->dev.type == TMQ_TYPE_Q8_0 ? (size_t)t->dev.rows * ((t->dev.cols + 63) / 64) : (size_t)t->dev.rows;
+    };
+    std::vector<size_t> acc_off(L);
+    size_t acc_n = 0;
+    for (int l = 0; l < L; l++) {
+        const Layer& Y = m->layers[l];
+        acc_off[l] = acc_n;
+        for (const tmq_tensor* t : {Y.q, Y.k, Y.v, Y.o, Y.gate, Y.up, Y.down}) acc_n += (acc_rows(t) + 31) & ~(size_t)31;
+    }
     // device buffer layout
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
     const int n_cand = (int)((c.vocab + 63) / 64);
@@ -378,16 +394,16 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     };
     place("state", sizeof(TmqEngState));
     place("tokens", sizeof(int32_t) * (size_t)(max_seq + 1));
-    place("hidden", 4 * (size_t)H);
-    place("q", 4 * (size_t)H);
-    place("k", 4 * (size_t)KV);
-    place("v", 4 * (size_t)KV);
+    place("hid0", 4 * (size_t)H);
+    place("hid1", 4 * (size_t)H);
+    place("view", 4 * (size_t)H);
     place("ctx", 4 * (size_t)H);
-    place("gate", 4 * (size_t)I);
-    place("up", 4 * (size_t)I);
     place("logits", 4 * (size_t)c.vocab);
     place("cand", 8 * (size_t)n_cand);
     place("dump", 4 * (size_t)H * (L + 1));
+    place("xs", 4 * 4 * (size_t)L);
+    place("kacc", 8 * (acc_n + L));
+    place("silu", 4 * (size_t)I);
     place("fvec", 4 * fv.size() + 4);
     place("rope", sizeof(float2) * 32 * (size_t)max_seq);
     place("kc", 4 * (size_t)L * max_seq * KV);
@@ -397,17 +413,19 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     uint8_t* B = (uint8_t*)m->dmem;
     m->state = (TmqEngState*)(B + lay["state"]);
     m->tokens = (int32_t*)(B + lay["tokens"]);
-    m->hidden = (float*)(B + lay["hidden"]);
-    m->q = (float*)(B + lay["q"]);
-    m->k = (float*)(B + lay["k"]);
-    m->v = (float*)(B + lay["v"]);
+    m->hid[0] = (float*)(B + lay["hid0"]);
+    m->hid[1] = (float*)(B + lay["hid1"]);
+    m->view = (float*)(B + lay["view"]);
     m->ctxv = (float*)(B + lay["ctx"]);
-    m->gate = (float*)(B + lay["gate"]);
-    m->up = (float*)(B + lay["up"]);
     m->logits = (float*)(B + lay["logits"]);
     m->cand = (uint64_t*)(B + lay["cand"]);
     m->n_cand = n_cand;
     m->dump = (float*)(B + lay["dump"]);
+    m->xs = (float*)(B + lay["xs"]);
+    m->kacc = (int64_t*)(B + lay["kacc"]);
+    m->kacc_n = acc_n + L;  // + one max slot per layer
+    m->max_bits = (uint32_t*)(m->kacc + acc_n);  // slot l at byte 8*l: every other u32
+    m->silu_x = (float*)(B + lay["silu"]);
     m->fvec = (float*)(B + lay["fvec"]);
     m->rope = (float2*)(B + lay["rope"]);
     m->kc = (float*)(B + lay["kc"]);
@@ -415,29 +433,44 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     auto fv_ptr = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
 
     // Work lists.  Every launch is one engine GEMV: per layer qkv / o /
-    // gate+up / down, then the logits.  A K-quant or Q5_0 row group is 64
-    // rows on one workgroup whose waves split the blocks; a Q8_0 wave owns 64
-    // rows, so a workgroup covers waves*64 rows.
-    std::vector<TmqWork> works;
-    std::vector<int32_t> gmap;
-    auto add_work = [&](Launch& ln, const tmq_tensor* t, float* y, const float* bias, int resid) {
-        TmqWork w = tmq_rt_make_work(t, nullptr, y, nullptr);
-        w.bias = bias;
-        w.resid = resid;
+    // gate+up / down, each split over K (kc workgroups per 64-row group) into
+    // int64 accumulators that the next launch finalises; then the logits
+    // (one Q8_0 wave per 64 rows, direct).
+    const int kc_qkv = env_int("TMQ_KC_QKV", 7), kc_o = env_int("TMQ_KC_O", 7);
+    const int kc_gu = env_int("TMQ_KC_GU", 4), kc_dn = env_int("TMQ_KC_DN", 4);
+    auto nw_env = [](const char* n, int d) { return env_int(n, d) == 4 ? 4 : env_int(n, d) == 16 ? 16 : d; };
+    const int nw_qkv = nw_env("TMQ_NW_QKV", 4), nw_o = nw_env("TMQ_NW_O", 4);
+    const int nw_gu = nw_env("TMQ_NW_GU", 4), nw_dn = nw_env("TMQ_NW_DN", 16);
+    auto add_work = [&](Launch& ln, const tmq_tensor* t, int64_t* kacc, float* xs_out, int kc) {
+        TmqWork w = tmq_rt_make_work(t, nullptr, nullptr, nullptr);
         const int g64 = t->dev.rows_pad / 64;
-        w.ngroups = t->dev.type == TMQ_TYPE_Q8_0 ? (g64 + ln.waves - 1) / ln.waves : g64;
-        w.first_group = ln.ngroups;
-        for (int g = 0; g < w.ngroups; g++) gmap.push_back((int32_t)works.size());
-        ln.ngroups += w.ngroups;
-        works.push_back(w);
-        return works.size() - 1;
+        const int units = t->dev.type == TMQ_TYPE_Q8_0 ? (t->dev.cols + 63) / 64
+                          : t->dev.nb * (t->dev.type == TMQ_TYPE_Q5_0 ? 1 : 4);
+        if (kc > units) kc = units;
+        if (kc < 1) kc = 1;
+        w.kc = kc;
+        w.kacc = kacc;
+        w.xs_out = xs_out;
+        w.ngroups = g64 * kc;
+        w.first_group = ln.P.ngroups;
+        ln.P.ngroups += w.ngroups;
+        ln.P.w[ln.P.nworks++] = w;
     };
-    auto recipe = [&](int mode, const float* x, const float* x2, const float* w, int n) {
+    auto deferred = [&](const tmq_tensor* t, int64_t* acc, float* xs, const float* bias) {
+        TmqDeferred d{};
+        d.acc = acc;
+        d.xs = xs;
+        d.row_inv = t->dev.row_inv;
+        d.row_scale = t->dev.row_scale;
+        d.bias = bias;
+        d.ntiles = t->dev.type == TMQ_TYPE_Q8_0 ? (t->dev.cols + 63) / 64 : 0;
+        return d;
+    };
+    auto recipe = [&](int mode, const float* x, const float* w, int n) {
         TmqEngAct a{};
         a.mode = mode;
         a.n = n;
         a.x = x;
-        a.x2 = x2;
         a.w = w;
         a.eps = c.norm_eps;
         a.state = m->state;
@@ -445,53 +478,67 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     };
     for (int l = 0; l < L; l++) {
         Layer& Y = m->layers[l];
+        int64_t* A = m->kacc + acc_off[l];
+        int64_t *aq = A, *ak = aq + ((acc_rows(Y.q) + 31) & ~(size_t)31), *av = ak + ((acc_rows(Y.k) + 31) & ~(size_t)31);
+        int64_t *ao = av + ((acc_rows(Y.v) + 31) & ~(size_t)31), *ag = ao + ((acc_rows(Y.o) + 31) & ~(size_t)31);
+        int64_t *au = ag + ((acc_rows(Y.gate) + 31) & ~(size_t)31), *ad = au + ((acc_rows(Y.up) + 31) & ~(size_t)31);
+        float* xs = m->xs + 4 * l;
+        Y.dq = deferred(Y.q, aq, xs + 0, fv_ptr(Y.bq));
+        Y.dk = deferred(Y.k, ak, xs + 0, fv_ptr(Y.bk));
+        Y.dv = deferred(Y.v, av, xs + 0, fv_ptr(Y.bv));
+        Y.dout = deferred(Y.o, ao, xs + 1, nullptr);
+        Y.dg = deferred(Y.gate, ag, xs + 2, nullptr);
+        Y.du = deferred(Y.up, au, xs + 2, nullptr);
+        Y.dd = deferred(Y.down, ad, xs + 3, nullptr);
         if (l == 0) {
-            Y.qkv.act = recipe(TMQ_ACT_EMBED_NORM, nullptr, nullptr, m->fvec + Y.attn_norm, H);
-            Y.qkv.act.tokens = m->tokens;
-            Y.qkv.act.hidden_out = m->hidden;
-            Y.qkv.act.emb = m->emb->dev;
+            Y.qkv.P.act = recipe(TMQ_ACT_EMBED_NORM, nullptr, m->fvec + Y.attn_norm, H);
+            Y.qkv.P.act.tokens = m->tokens;
+            Y.qkv.P.act.emb = m->emb->dev;
         } else {
-            Y.qkv.act = recipe(TMQ_ACT_NORM, m->hidden, nullptr, m->fvec + Y.attn_norm, H);
+            Y.qkv.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[0], m->fvec + Y.attn_norm, H);
+            Y.qkv.P.act.d1 = m->layers[l - 1].dd;
         }
-        add_work(Y.qkv, Y.q, m->q, fv_ptr(Y.bq), 0);
-        add_work(Y.qkv, Y.k, m->k, fv_ptr(Y.bk), 0);
-        add_work(Y.qkv, Y.v, m->v, fv_ptr(Y.bv), 0);
-        Y.o_l.act = recipe(TMQ_ACT_PLAIN, m->ctxv, nullptr, nullptr, H);
-        add_work(Y.o_l, Y.o, m->hidden, nullptr, 1);
-        Y.gu.act = recipe(TMQ_ACT_NORM, m->hidden, nullptr, m->fvec + Y.ffn_norm, H);
-        add_work(Y.gu, Y.gate, m->gate, nullptr, 0);
-        add_work(Y.gu, Y.up, m->up, nullptr, 0);
-        Y.dn.act = recipe(TMQ_ACT_SILU, m->gate, m->up, nullptr, I);
-        add_work(Y.dn, Y.down, m->hidden, nullptr, 1);
+        Y.qkv.P.act.hidden_out = m->hid[1];
+        Y.qkv.waves = nw_qkv;
+        add_work(Y.qkv, Y.q, aq, xs + 0, kc_qkv);
+        add_work(Y.qkv, Y.k, ak, nullptr, kc_qkv);
+        add_work(Y.qkv, Y.v, av, nullptr, kc_qkv);
+        Y.o_l.P.act = recipe(TMQ_ACT_PLAIN, m->ctxv, nullptr, H);
+        Y.o_l.waves = nw_o;
+        add_work(Y.o_l, Y.o, ao, xs + 1, kc_o);
+        Y.gu.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[1], m->fvec + Y.ffn_norm, H);
+        Y.gu.P.act.d1 = Y.dout;
+        Y.gu.P.act.hidden_out = m->hid[0];
+        Y.gu.waves = nw_gu;
+        add_work(Y.gu, Y.gate, ag, xs + 2, kc_gu);
+        add_work(Y.gu, Y.up, au, nullptr, kc_gu);
+        Y.dn.P.act = recipe(TMQ_ACT_PRESCALED, m->silu_x, nullptr, I);
+        Y.dn.P.act.max_bits = m->max_bits + 2 * l;
+        Y.dn.waves = nw_dn;
+        add_work(Y.dn, Y.down, ad, xs + 3, kc_dn);
     }
+    // logits: the residual stream (hid[0] + the last down projection),
+    // output_norm when present, direct Q8_0 GEMV with argmax candidates
     m->logits_l.waves = 4;
-    m->logits_l.act = m->out_norm >= 0 ? recipe(TMQ_ACT_NORM, m->hidden, nullptr, m->fvec + m->out_norm, H)
-                                       : recipe(TMQ_ACT_PLAIN, m->hidden, nullptr, nullptr, H);
-    works[add_work(m->logits_l, m->emb, m->logits, nullptr, 0)].cand = m->cand;
-    // gmap offsets of each launch, in the order add_work filled gmap
+    m->logits_l.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[0], m->out_norm >= 0 ? m->fvec + m->out_norm : nullptr, H);
+    m->logits_l.P.act.d1 = m->layers[L - 1].dd;
     {
-        int g = 0;
-        for (int l = 0; l < L; l++) {
-            Layer& Y = m->layers[l];
-            for (Launch* ln : {&Y.qkv, &Y.o_l, &Y.gu, &Y.dn}) {
-                ln->gmap_off = g;
-                g += ln->ngroups;
-            }
-        }
-        m->logits_l.gmap_off = g;
+        TmqWork w = tmq_rt_make_work(m->emb, nullptr, m->logits, nullptr);
+        const int g64 = m->emb->dev.rows_pad / 64;
+        w.kc = 1;
+        w.cand = m->cand;
+        w.ngroups = (g64 + m->logits_l.waves - 1) / m->logits_l.waves;
+        w.first_group = 0;
+        m->logits_l.P.w[0] = w;
+        m->logits_l.P.nworks = 1;
+        m->logits_l.P.ngroups = w.ngroups;
     }
-    const size_t tail = al(sizeof(TmqWork) * works.size()) + al(4 * gmap.size());
-    void* tmem = nullptr;
-    e = hipMalloc(&tmem, tail);
-    if (e != hipSuccess) return tmq_fail(TMQ_ERR_NOMEM, "model work lists (%zu B): %s", tail, hipGetErrorString(e));
-    m->tail_mem = tmem;
-    m->works_dev = (TmqWork*)tmem;
-    m->gmap_dev = (int32_t*)((uint8_t*)tmem + al(sizeof(TmqWork) * works.size()));
-
     hipStream_t s = ctx->stream;
-    HIP_TRY(hipMemcpyAsync(m->works_dev, works.data(), sizeof(TmqWork) * works.size(), hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->gmap_dev, gmap.data(), 4 * gmap.size(), hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(m->fvec, fv.data(), 4 * fv.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemsetAsync(m->xs, 0, 4 * 4 * (size_t)L, s));
+    HIP_TRY(hipMemsetAsync(m->hid[0], 0, 4 * (size_t)H, s));
+    HIP_TRY(hipMemsetAsync(m->hid[1], 0, 4 * (size_t)H, s));
+    LAUNCH_TRY(tmq_launch_zero_acc(m->kacc, m->kacc_n, s));
     HIP_TRY(hipMemsetAsync(m->kc, 0, 4 * (size_t)L * max_seq * KV, s));
     HIP_TRY(hipMemsetAsync(m->vc, 0, 4 * (size_t)L * max_seq * KV, s));
     // RoPE factors exactly as apply_rope forms them (sim/tmac_gguf.cpp:1531-1535)
@@ -674,7 +721,10 @@ int tmq_model_hidden(tmq_model* m, float* out) {
     if (!m || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
     int rc = tmq_rt_set_device(m->ctx);
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(out, m->hidden, sizeof(float) * m->cfg.hidden, hipMemcpyDeviceToHost, m->ctx->stream));
+    if (m->pos < 0) return tmq_fail(TMQ_ERR_ARG, "no position processed yet");
+    // the residual stream: hid[0] + the last layer's pending down projection
+    LAUNCH_TRY(tmq_launch_resid_view(m->hid[0], m->layers.back().dd, m->cfg.hidden, m->view, m->ctx->stream));
+    HIP_TRY(hipMemcpyAsync(out, m->view, sizeof(float) * m->cfg.hidden, hipMemcpyDeviceToHost, m->ctx->stream));
     return check_state(m);
 }
 
