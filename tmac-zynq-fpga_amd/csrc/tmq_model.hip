@@ -437,10 +437,10 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     // int64 accumulators that the next launch finalises; then the logits
     // (one Q8_0 wave per 64 rows, direct).
     const int kc_qkv = env_int("TMQ_KC_QKV", 7), kc_o = env_int("TMQ_KC_O", 7);
-    const int kc_gu = env_int("TMQ_KC_GU", 4), kc_dn = env_int("TMQ_KC_DN", 4);
+    const int kc_gu = env_int("TMQ_KC_GU", 1), kc_dn = env_int("TMQ_KC_DN", 19);
     auto nw_env = [](const char* n, int d) { return env_int(n, d) == 4 ? 4 : env_int(n, d) == 16 ? 16 : d; };
     const int nw_qkv = nw_env("TMQ_NW_QKV", 4), nw_o = nw_env("TMQ_NW_O", 4);
-    const int nw_gu = nw_env("TMQ_NW_GU", 4), nw_dn = nw_env("TMQ_NW_DN", 16);
+    const int nw_gu = nw_env("TMQ_NW_GU", 16), nw_dn = nw_env("TMQ_NW_DN", 4);
     auto add_work = [&](Launch& ln, const tmq_tensor* t, int64_t* kacc, float* xs_out, int kc) {
         TmqWork w = tmq_rt_make_work(t, nullptr, nullptr, nullptr);
         const int g64 = t->dev.rows_pad / 64;
