@@ -236,7 +236,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--sets", type=int, default=SETS)
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + ["c4"],
+                    help="c4: only the full-model greedy decode (BASELINE configs[3])")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE GEMV configs")
     args = ap.parse_args()
 
@@ -255,6 +256,19 @@ def main():
     ctx = tmq.Context(0)
     stream = torch.cuda.ExternalStream(ctx.stream)
     wl = args.workload
+    if wl == "c4":
+        dec = decode_bench(ctx, torch, stream, tokens=args.steps if args.steps <= 500 else 500)
+        ctx.close()
+        out = {"metric": "Qwen2-0.5B batch-1 greedy decode tok/s", "value": dec["tok_s"], "unit": "tok/s",
+               "n_gpus": 1, "steps": dec["tokens"], "warmup": 8, "ms_per_step": dec["ms_per_token"],
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int16",
+               "data": "synthetic Qwen2-0.5B-shaped model (tmq.model_synth seed 2024), one seeded prompt token",
+               "config": {"workload": "BASELINE configs[3]: 24-layer decode, mixed Q8_0/Q6_K and Q5_0/Q4_K "
+                          "layers, Q8_0 tied logits, greedy", "weight_bytes_per_token": dec["weight_bytes_per_token"]},
+               "extra": {"c4_decode": dec},
+               "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(args.cpu_seconds)}
+        print(json.dumps(out), flush=True)
+        return
     copies = args.sets if wl == "c2" else None
     desc_txt, wbytes, step_ms, kern_ms, ndesc = measure(ctx, torch, dev, stream, wl, args.steps, args.warmup, copies)
     value = wbytes / (step_ms * 1e-3) / 1e9

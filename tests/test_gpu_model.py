@@ -8,6 +8,8 @@ where the engine's logf (fp64 log rounded once) differs from the host libm's
 logf by one ulp, so they are checked to 1e-5 relative and the bit-exact
 fraction is reported.
 """
+import os
+
 import numpy as np
 import pytest
 from conftest import load_golden
@@ -148,3 +150,29 @@ def test_load_errors(ctx):
     emb = tmacfile.TmacTensor("token_embd.weight", 64, 64, tmacfile.Q8_0, np.zeros(64 * 2 * 34, np.uint8))
     with pytest.raises(tmq.TmqError):
         tmq.Model(ctx, tmacfile.to_bytes([emb]))
+
+
+def test_cli(golden, tmp_path):
+    """tmq_gguf (the tmac_gguf counterpart): --generate prints the greedy
+    tokens; without it, the top-10 JSON of the last prompt position"""
+    import json
+    import subprocess
+    from conftest import PKG
+    from tmq import model_synth, tmacfile
+    exe = os.path.join(PKG, "tmq", "tmq_gguf")
+    if not os.path.exists(exe):
+        pytest.fail("tmq_gguf is not built (make -C tmac-zynq-fpga_amd)")
+    path = tmp_path / "c4.tmac"
+    tmacfile.write(path, model_synth.gen_model(int(golden["model_seed"])))
+    prompt = f"{int(golden['prompt'][0])}\n"
+    r = subprocess.run([exe, str(path), "--generate", "16", "--fpga-q8", "--fpga-q5-0"], input=prompt,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    got = [int(t) for t in r.stdout.split()]
+    assert got == golden["tokens"][:16].tolist()
+    r = subprocess.run([exe, str(path), "--perf"], input=prompt, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    top = json.loads(r.stdout)
+    assert [t["id"] for t in top] == golden["top_ids"][0].tolist()
+    assert [t["logit"] for t in top] == [round(float(v), 3) for v in golden["top_vals"][0]]
+    assert "[PERF]" in r.stderr

@@ -1,0 +1,61 @@
+"""The engine's device expf (tmac-zynq-fpga_amd/csrc/tmq_mathf.h), built for the
+host from the same header, against the host libm expf that the reference
+engine calls (sim/tmac_gguf.cpp:438, :1650-1654).
+
+An exhaustive run over all 2^32 inputs (same check, stride 1) found no
+mismatch; the suite checks a strided sample plus the special values."""
+import ctypes as C
+import math
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+from conftest import ROOT
+
+HDR_DIR = os.path.join(ROOT, "tmac-zynq-fpga_amd", "csrc")
+SRC = os.path.join(ROOT, "tests", "mathf_check.cpp")
+
+
+@pytest.fixture(scope="module")
+def mathf():
+    out = os.path.join(tempfile.mkdtemp(prefix="tmq_mathf_"), "libmathf.so")
+    # plain IEEE build: no fast-math, no -march (the reference's own flags)
+    subprocess.run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-I", HDR_DIR, "-o", out, SRC],
+                   check=True)
+    L = C.CDLL(out)
+    L.tmqm_expf_mismatches.restype = C.c_uint64
+    L.tmqm_expf_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint32)]
+    L.tmqm_expf.restype = C.c_float
+    L.tmqm_expf.argtypes = [C.c_float]
+    return L
+
+
+def test_expf_sample_matches_libm(mathf):
+    first = C.c_uint32(0)
+    bad = mathf.tmqm_expf_mismatches(977, 13, C.byref(first))
+    assert bad == 0, f"{bad} mismatches, first input bits {first.value:#010x}"
+
+
+def test_expf_attention_range(mathf):
+    """[-88, 0], the arguments of the softmax and of SiLU's exp(-g) for g > 0"""
+    libm = C.CDLL("libm.so.6")
+    libm.expf.restype = C.c_float
+    libm.expf.argtypes = [C.c_float]
+    for x in np.linspace(-88.0, 0.0, 30001, dtype=np.float32):
+        a, e = mathf.tmqm_expf(float(x)), libm.expf(float(x))
+        assert np.float32(a).view(np.uint32) == np.float32(e).view(np.uint32), x
+
+
+@pytest.mark.parametrize("x", [0.0, -0.0, 1.0, -1.0, 88.0, 88.72283, 88.7229, -87.33655, -103.97208,
+                               -103.9721, -150.0, float("inf"), float("-inf"), 1e-30, -1e-30, 0.5, -0.5])
+def test_expf_special(mathf, x):
+    libm = C.CDLL("libm.so.6")
+    libm.expf.restype = C.c_float
+    libm.expf.argtypes = [C.c_float]
+    a, e = mathf.tmqm_expf(x), libm.expf(x)
+    if math.isnan(e):
+        assert math.isnan(a)
+    else:
+        assert np.float32(a).view(np.uint32) == np.float32(e).view(np.uint32)
