@@ -1,6 +1,6 @@
-// Host build of tmq_mathf.h (the engine's device expf) for the CPU tests:
-// compares tmq_expf with the host libm's expf over a strided sample of all
-// 2^32 float bit patterns.
+// Host build of tmq_mathf.h for the CPU tests: compares the engine's expf
+// with the host libm's expf over a strided sample of all 2^32 float bit
+// patterns, and exports the RoPE table the engine uploads at load.
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -27,3 +27,7 @@ extern "C" uint64_t tmqm_expf_mismatches(uint64_t stride, uint64_t offset, uint3
 }
 
 extern "C" float tmqm_expf(float x) { return tmq_math::tmq_expf(x); }
+
+extern "C" void tmqm_rope_table(float base, int head_dim, int max_pos, float* out) {
+    tmq_math::rope_table(base, head_dim, max_pos, out);
+}

@@ -3,7 +3,9 @@ host from the same header, against the host libm expf that the reference
 engine calls (sim/tmac_gguf.cpp:438, :1650-1654).
 
 An exhaustive run over all 2^32 inputs (same check, stride 1) found no
-mismatch; the suite checks a strided sample plus the special values."""
+mismatch; the suite checks a strided sample plus the special values.  The
+same header's RoPE table is checked against the compiled reference's
+apply_rope."""
 import ctypes as C
 import math
 import os
@@ -59,3 +61,29 @@ def test_expf_special(mathf, x):
         assert math.isnan(a)
     else:
         assert np.float32(a).view(np.uint32) == np.float32(e).view(np.uint32)
+
+
+def test_rope_table_matches_reference_apply_rope(mathf):
+    """The engine's RoPE table (built on the host at load, tmq_math::rope_table)
+    against the reference's apply_rope (sim/tmac_gguf.cpp:1528-1554): with q
+    and k made of (1, 0) pairs, apply_rope writes exactly (cos, sin) of each
+    pair (1*c - 0*s = c, 1*s + 0*c = s), so the whole table is compared bit
+    for bit, positions 0..255 (the reference's context)."""
+    from oracle import Reference
+    if not Reference.available():
+        pytest.skip("compiled reference (oracle/_ref) not built")
+    ref = Reference()
+    npos, H, KV = 256, 896, 128
+    tab = np.zeros(npos * 32 * 2, dtype=np.float32)
+    mathf.tmqm_rope_table.restype = None
+    mathf.tmqm_rope_table.argtypes = [C.c_float, C.c_int, C.c_int, C.c_void_p]
+    mathf.tmqm_rope_table(1000000.0, 64, npos, tab.ctypes.data)
+    tab = tab.reshape(npos, 32, 2)
+    for p in range(npos):
+        q = np.zeros(H, dtype=np.float32)
+        k = np.zeros(KV, dtype=np.float32)
+        q[0::2] = 1.0
+        k[0::2] = 1.0
+        ref.lib.ref_apply_rope(q.ctypes.data, k.ctypes.data, p)
+        for v in (q.reshape(-1, 32, 2), k.reshape(-1, 32, 2)):
+            assert np.array_equal(v.view(np.uint32), np.broadcast_to(tab[p], v.shape).view(np.uint32)), p

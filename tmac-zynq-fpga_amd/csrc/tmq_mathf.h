@@ -13,6 +13,8 @@
 // principles, so tmq_logf is the correctly rounded fp32 log (fp64 log then
 // one rounding); it differs from glibc's logf by one ulp on ~2e-4 of inputs.
 #pragma once
+#include <math.h>
+#include <stddef.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -90,6 +92,26 @@ TMQ_HD inline float tmq_expf(float x) {
     double y = __builtin_fma(C2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return (float)(y * s);
+}
+
+// RoPE factors for positions [0, max_pos), as apply_rope forms them on the
+// host (sim/tmac_gguf.cpp:1531-1535): theta = 1/powf(base, (float)d/head_dim),
+// freq = pos*theta, (cosf(freq), sinf(freq)) from the host libm.  out holds
+// max_pos x head_dim/2 (cos, sin) pairs.  base is read through a volatile so
+// that powf runs in the libm at run time, never folded at compile time.
+// Host code only.
+inline void rope_table(float base, int head_dim, int max_pos, float* out) {
+    volatile float base_v = base;
+    const float b = base_v;
+    const int half = head_dim / 2;
+    for (int d = 0; d < head_dim; d += 2) {
+        const float theta = 1.0f / powf(b, (float)d / head_dim);
+        for (int p = 0; p < max_pos; p++) {
+            const float freq = p * theta;
+            out[2 * ((size_t)p * half + d / 2)] = cosf(freq);
+            out[2 * ((size_t)p * half + d / 2) + 1] = sinf(freq);
+        }
+    }
 }
 
 }  // namespace tmq_math

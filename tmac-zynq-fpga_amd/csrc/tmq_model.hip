@@ -20,6 +20,7 @@
 #include "../../include/tmq.h"
 #include "tmq_engine.h"
 #include "tmq_internal.h"
+#include "tmq_mathf.h"
 #include "tmq_runtime.h"
 
 namespace {
@@ -543,15 +544,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     HIP_TRY(hipMemsetAsync(m->vc, 0, 4 * (size_t)L * max_seq * KV, s));
     // RoPE factors exactly as apply_rope forms them (sim/tmac_gguf.cpp:1531-1535)
     std::vector<float2> rope((size_t)max_seq * 32);
-    volatile float base_v = c.rope_base;
-    const float base = base_v;
-    for (int d = 0; d < TMQ_HEAD_DIM; d += 2) {
-        const float theta = 1.0f / powf(base, (float)d / TMQ_HEAD_DIM);
-        for (int p = 0; p < max_seq; p++) {
-            const float freq = p * theta;
-            rope[(size_t)p * 32 + d / 2] = make_float2(cosf(freq), sinf(freq));
-        }
-    }
+    tmq_math::rope_table(c.rope_base, TMQ_HEAD_DIM, max_seq, (float*)rope.data());
     HIP_TRY(hipMemcpyAsync(m->rope, rope.data(), sizeof(float2) * rope.size(), hipMemcpyHostToDevice, s));
     TmqEngState st{-1, 0, {0, 0}};
     HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
