@@ -208,6 +208,12 @@ int tmq_model_position(const tmq_model* m);
 int tmq_model_set_graphs(tmq_model* m, int enable);
 /* reset_cache + process_prompt (sim/tmac_gguf.cpp:1950-1997) */
 int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n);
+/* How tmq_model_prompt runs the prompt: chunk > 0 (default 512; env
+ * TMQ_PREFILL) pushes up to `chunk` tokens through each layer together
+ * (int8-MFMA GEMMs, the same bits as one token at a time); 0 processes one
+ * token at a time like process_prompt (:1992-1997).  Fails if the model's
+ * shapes or formats do not fit the batched kernels. */
+int tmq_model_set_prefill(tmq_model* m, int chunk);
 /* process_embedding + forward_all_layers of one more token (:1955-1967) */
 int tmq_model_feed(tmq_model* m, int32_t token);
 /* as tmq_model_feed, also returning the hidden state after the embedding

@@ -1,0 +1,85 @@
+"""GPU parity of the batched prefill (tmq_model_set_prefill > 0: every layer
+takes a chunk of prompt tokens at once, projections on int8 MFMA) against
+the engine's one-token-at-a-time prompt (tmq_model_set_prefill(0)), which
+is itself bit-exact with the compiled reference (test_gpu_model.py).
+
+The reference's process_prompt (sim/tmac_gguf.cpp:1992-1997) runs one token
+at a time, so the batched path must leave the same state bit for bit: the
+logits of the last position, the residual stream, and the KV cache (checked
+through the greedy tokens generated from it).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+MODEL_SEED = 2024
+
+
+@pytest.fixture(scope="module")
+def model(ctx):
+    import tmq
+    from tmq import model_synth, tmacfile
+    print("[prefill] generating the synthetic C4 model", flush=True)
+    blob = tmacfile.to_bytes(model_synth.gen_model(MODEL_SEED))
+    m = tmq.Model(ctx, blob, max_seq=1024)
+    del blob
+    yield m
+    m.free()
+
+
+def run(model, tokens, chunk, gen=4):
+    model.set_prefill(chunk)
+    model.prompt(tokens)
+    assert model.position == len(tokens)
+    logits = model.logits()
+    hidden = model.hidden()
+    out = model.generate(gen)
+    return logits, hidden, out
+
+
+def prompt_of(n, seed):
+    return np.random.default_rng(seed).integers(0, 151936, size=n).astype(np.int32)
+
+
+@pytest.mark.parametrize("n", [2, 37, 100, 300])
+def test_prefill_matches_sequential(model, n):
+    toks = prompt_of(n, 1000 + n)
+    print(f"[prefill] n={n} sequential", flush=True)
+    l0, h0, g0 = run(model, toks, 0)
+    print(f"[prefill] n={n} batched", flush=True)
+    l1, h1, g1 = run(model, toks, 512)
+    assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32))
+    assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32))
+    assert g1.tolist() == g0.tolist()
+    assert model.tokens(0, n).tolist() == toks.tolist()
+
+
+def test_prefill_chunks(model):
+    """chunks of 64 tokens: later chunks attend to the cache the earlier ones wrote"""
+    toks = prompt_of(150, 77)
+    print("[prefill] chunked 64 vs sequential", flush=True)
+    l0, h0, g0 = run(model, toks, 0)
+    l1, h1, g1 = run(model, toks, 64)
+    assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32))
+    assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32))
+    assert g1.tolist() == g0.tolist()
+
+
+def test_prefill_then_feed(model):
+    """a token fed after a batched prompt continues exactly as after a sequential one"""
+    toks = prompt_of(20, 5)
+    res = []
+    for chunk in (0, 512):
+        model.set_prefill(chunk)
+        model.prompt(toks)
+        model.feed(1234)
+        res.append((model.logits(), model.hidden()))
+    assert np.array_equal(res[0][0].view(np.uint32), res[1][0].view(np.uint32))
+    assert np.array_equal(res[0][1].view(np.uint32), res[1][1].view(np.uint32))
+
+
+def test_prefill_errors(model):
+    import tmq
+    with pytest.raises(tmq.TmqError):
+        model.set_prefill(-1)

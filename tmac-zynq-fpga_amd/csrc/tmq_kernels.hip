@@ -18,6 +18,7 @@
 #include "tmq_internal.h"
 #include "tmq_mathf.h"
 #include "tmq_device.h"
+#include "tmq_prefill.h"
 
 typedef short tmq_s16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 tmq_h2 __attribute__((ext_vector_type(2)));
@@ -105,9 +106,24 @@ __device__ __forceinline__ tmq_h2 lanes23(uint32_t w) {
 typedef __attribute__((address_space(3))) const uint32_t lu32;
 template <class P>
 struct ActT {
+    static constexpr bool kSink = false;
     float xs;
     P xh;
     P xl;
+};
+
+// Weight sink: takes the place of an activation in the block decoders and
+// stores each int16 weight pair as its prefill digits instead of multiplying
+// it (hi = w >> 8, lo = (w & 255) - 128; two bytes per plane per pair at
+// column 2*kx of the row).
+struct WDigits {
+    static constexpr bool kSink = true;
+    int8_t* hi;
+    int8_t* lo;
+    __device__ __forceinline__ void put(int kx, uint32_t P) const {
+        *(uint16_t*)(hi + 2 * kx) = (uint16_t)__builtin_amdgcn_perm(0u, P, 0x0c0c0301u);
+        *(uint16_t*)(lo + 2 * kx) = (uint16_t)(__builtin_amdgcn_perm(0u, P, 0x0c0c0200u) ^ 0x8080u);
+    }
 };
 typedef ActT<const cu32*> Act;
 typedef ActT<const lu32*> ActL;
@@ -133,10 +149,15 @@ __device__ __forceinline__ void mac4(float e0, float e1, float e2, float e3, flo
                                      const AT& A, int kx, int& sh, int& sl) {
     const uint32_t P0 = pk16(wq<CLAMP>(e0 * inv), wq<CLAMP>(e1 * inv));
     const uint32_t P1 = pk16(wq<CLAMP>(e2 * inv), wq<CLAMP>(e3 * inv));
-    sh = dot2(P0, A.xh[kx], sh);
-    sl = dot2(P0, A.xl[kx], sl);
-    sh = dot2(P1, A.xh[kx + 1], sh);
-    sl = dot2(P1, A.xl[kx + 1], sl);
+    if constexpr (AT::kSink) {
+        A.put(kx, P0);
+        A.put(kx + 1, P1);
+    } else {
+        sh = dot2(P0, A.xh[kx], sh);
+        sl = dot2(P0, A.xl[kx], sl);
+        sh = dot2(P1, A.xh[kx + 1], sh);
+        sl = dot2(P1, A.xl[kx + 1], sl);
+    }
 }
 
 // Each format: Blk = one block of one row in registers, blk_load() fetches
@@ -377,8 +398,12 @@ __device__ __forceinline__ void q8_mac(const Q8Blk& k, const AT& A, int b, float
         const int p0 = (int)(int8_t)byte_of(v, (2 * j) & 15) * cs;
         const int p1 = (int)(int8_t)byte_of(v, (2 * j + 1) & 15) * cs;
         const uint32_t P = __builtin_amdgcn_perm((uint32_t)p1, (uint32_t)p0, 0x06050201u);
-        sh = dot2(P, A.xh[b * 16 + j], sh);
-        sl = dot2(P, A.xl[b * 16 + j], sl);
+        if constexpr (AT::kSink) {
+            A.put(b * 16 + j, P);
+        } else {
+            sh = dot2(P, A.xh[b * 16 + j], sh);
+            sl = dot2(P, A.xl[b * 16 + j], sl);
+        }
     }
 }
 
@@ -1112,6 +1137,128 @@ __global__ void tile_q8_kernel(const uint8_t* __restrict__ W, const uint16_t* __
     out[n] = a;
 }
 
+// ------------------------------------------------------ prefill operands
+// Weight digits of one tensor (tmq_prefill.h): the int16 weights the decode
+// GEMVs multiply -- the same block decoders and normalisation -- stored as
+// two int8 planes at rows row0.. of a plane set K columns wide.  One lane
+// per row.
+template <int FMT>
+__global__ __launch_bounds__(64) void pf_wdigits_kernel(TmqTensorDev t, int8_t* hi, int8_t* lo, int K, int row0) {
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    if (r >= t.rows) return;
+    const WDigits S{hi + (size_t)(row0 + r) * K, lo + (size_t)(row0 + r) * K};
+    int sh = 0, sl = 0;
+    const float inv = t.row_inv[r];
+    for (int b = 0; b < t.nb; b++) {
+        if constexpr (FMT == kQ8_0) q8_mac(q8_load(t, b, r), S, b, inv, sh, sl);
+        else blk_mac<FMT, false>(blk_load<FMT>(t, b, r), S, b, inv, sh, sl);
+    }
+}
+
+// Per row of a digit plane set: the sums of (v - 128) = 256*hi + lo over
+// each 64-column chunk and over the row.  One wave per row.
+__global__ __launch_bounds__(64) void pf_rowsums_kernel(const int8_t* __restrict__ hi, const int8_t* __restrict__ lo,
+                                                       int K, int32_t* csum, int32_t* tsum) {
+    const int r = blockIdx.x, lane = threadIdx.x, nc = K / TMQ_PF_CHUNK;
+    int32_t tot = 0;
+    for (int c = 0; c < nc; c++) {
+        const size_t i = (size_t)r * K + c * TMQ_PF_CHUNK + lane;
+        int v = 256 * (int)hi[i] + (int)lo[i];
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        if (lane == 0) csum[(size_t)r * nc + c] = v;
+        tot += v;
+    }
+    if (lane == 0) tsum[r] = tot;
+}
+
+// Activation operands of one token (workgroup t of T_pad): the columns'
+// values, RMSNorm, x_scale and xq exactly as eng_prologue forms them, then
+// xq as digits with its (xq - 128) sums.  Tokens t >= T get zero planes.
+__global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
+    extern __shared__ float pf_lds[];
+    __shared__ float red[8];
+    const int t = blockIdx.x, n = a.n, tid = threadIdx.x, nt = blockDim.x;
+    const int wave = tid >> 6, lane = tid & 63, nc = n / TMQ_PF_CHUNK;
+    int8_t* hi = a.out.hi + (size_t)t * n;
+    int8_t* lo = a.out.lo + (size_t)t * n;
+    if (t >= a.T) {
+        for (int i = tid; i < n; i += nt) {
+            hi[i] = 0;
+            lo[i] = 0;
+        }
+        for (int c = tid; c < nc; c += nt) a.out.csum[(size_t)t * nc + c] = 0;
+        if (tid == 0) {
+            a.out.tsum[t] = 0;
+            a.xs[t] = 1.0f;
+        }
+        return;
+    }
+    float* X = pf_lds;       // values (after x*w for the norm modes)
+    float* sq = pf_lds + n;  // squares
+    const bool norm = a.mode == TMQ_PF_EMBED_NORM || a.mode == TMQ_PF_RESID_NORM || a.mode == TMQ_PF_NORM;
+    const bool wr = a.x_out && (a.mode == TMQ_PF_EMBED_NORM || a.mode == TMQ_PF_RESID_NORM);
+    const int tok = a.mode == TMQ_PF_EMBED_NORM ? a.tokens[a.p0 + t] : 0;
+    float m = 0.0f;
+    for (int i = tid; i < n; i += nt) {
+        float v;
+        if (a.mode == TMQ_PF_EMBED_NORM) v = tensor_elem(a.emb, tok, i);
+        else if (a.mode == TMQ_PF_RESID_NORM) v = a.x[(size_t)t * n + i] + tmq_pf_fin(a.d1, t, i);
+        else v = a.x[(size_t)t * n + i];
+        if (wr) a.x_out[(size_t)t * n + i] = v;
+        if (norm) {
+            sq[i] = v * v;
+            v = v * a.w[i];
+        }
+        X[i] = v;
+        m = fmaxf(m, fabsf(v));
+    }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) red[1 + wave] = m;
+    if (tid == 0 && a.zero_bits) a.zero_bits[t] = 0u;
+    __syncthreads();
+    float s = 1.0f;
+    if (norm) {
+        if (tid == 0) {
+            const float mean = seq_sum_lds(sq, n) / (float)n;
+            red[0] = 1.0f / sqrtf(mean + a.eps);
+        }
+        __syncthreads();
+        s = red[0];
+    }
+    float mm;
+    if (a.mode == TMQ_PF_SILU) {
+        mm = __builtin_bit_cast(float, a.max_bits[t]);
+    } else {
+        mm = 0.0f;
+        for (int i = 0; i < (nt >> 6); i++) mm = fmaxf(mm, red[1 + i]);
+        if (norm) mm = mm * s;
+    }
+    const float xs = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
+    // n is a multiple of 64: chunk c = columns [64c, 64c+64) is one wave's pass
+    int32_t tot = 0;
+    for (int c = wave; c < nc; c += (nt >> 6)) {
+        const int i = c * TMQ_PF_CHUNK + lane;
+        float u = X[i];
+        if (norm) u = u * s;
+        const int q = (int)(int16_t)roundf(u / xs);
+        hi[i] = (int8_t)(q >> 8);
+        lo[i] = (int8_t)((q & 255) ^ 128);
+        int v = q - 128;
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        if (lane == 0) a.out.csum[(size_t)t * nc + c] = v;
+        tot += v;
+    }
+    __syncthreads();
+    if (lane == 0) red[1 + wave] = __builtin_bit_cast(float, tot);
+    __syncthreads();
+    if (tid == 0) {
+        int32_t T = 0;
+        for (int i = 0; i < (nt >> 6); i++) T += __builtin_bit_cast(int32_t, red[1 + i]);
+        a.out.tsum[t] = T;
+        a.xs[t] = xs;
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
@@ -1221,5 +1368,31 @@ int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x,
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s) {
     hipLaunchKernelGGL(tile_q8_kernel, dim3(1), dim3(64), 0, s, W, cs, vec, out);
+    return (int)hipGetLastError();
+}
+
+// ------------------------------------------------------ prefill operands
+int tmq_launch_pf_wdigits(const TmqTensorDev& t, int8_t* hi, int8_t* lo, int K, int row0, hipStream_t s) {
+    const dim3 grid((t.rows + 63) / 64), blk(64);
+    switch (t.type) {
+    case kQ5_0: hipLaunchKernelGGL(pf_wdigits_kernel<kQ5_0>, grid, blk, 0, s, t, hi, lo, K, row0); break;
+    case kQ8_0: hipLaunchKernelGGL(pf_wdigits_kernel<kQ8_0>, grid, blk, 0, s, t, hi, lo, K, row0); break;
+    case kQ4_K: hipLaunchKernelGGL(pf_wdigits_kernel<kQ4_K>, grid, blk, 0, s, t, hi, lo, K, row0); break;
+    case kQ6_K: hipLaunchKernelGGL(pf_wdigits_kernel<kQ6_K>, grid, blk, 0, s, t, hi, lo, K, row0); break;
+    default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_pf_rowsums(const int8_t* hi, const int8_t* lo, int rows, int K, int32_t* csum, int32_t* tsum,
+                          hipStream_t s) {
+    if (rows <= 0 || K % TMQ_PF_CHUNK) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_rowsums_kernel, dim3(rows), dim3(64), 0, s, hi, lo, K, csum, tsum);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s) {
+    if (a.n % TMQ_PF_CHUNK || a.n > TMQ_ENG_MAXN || a.out.rows < a.T) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_act_kernel, dim3(a.out.rows), dim3(256), 8 * (size_t)a.n, s, a);
     return (int)hipGetLastError();
 }

@@ -9,6 +9,7 @@
 // exactly as apply_rope (:1527-1554) computes its factors.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -21,6 +22,7 @@
 #include "tmq_engine.h"
 #include "tmq_internal.h"
 #include "tmq_mathf.h"
+#include "tmq_prefill.h"
 #include "tmq_runtime.h"
 
 namespace {
@@ -109,6 +111,25 @@ int env_int(const char* name, int dflt) {
 
 }  // namespace
 
+// Batched prefill (tmq_prefill.h): weight digit planes of every layer,
+// built on first use, and the activation buffers of one chunk of tokens.
+struct PfLayer {
+    TmqPfPlanes qkv{}, o{}, gu{}, dn{};
+};
+struct Prefill {
+    bool built = false;
+    void* wmem = nullptr;  // all layers' weight planes
+    void* amem = nullptr;  // chunk buffers
+    int chunk = 0;         // tokens per chunk the buffers hold (multiple of 32)
+    std::vector<PfLayer> layers;
+    float *x0 = nullptr, *x1 = nullptr, *qb = nullptr, *ctx = nullptr, *s = nullptr;
+    TmqPfPlanes in[4]{};   // activation planes: QKV, O, GU, DN inputs
+    float* xs[4] = {nullptr, nullptr, nullptr, nullptr};
+    int64_t* part = nullptr;
+    uint32_t* max_bits = nullptr;
+    int dn_split = 4;
+};
+
 struct tmq_model {
     tmq_ctx* ctx = nullptr;
     tmq_model_config cfg{};
@@ -138,6 +159,9 @@ struct tmq_model {
     int pos = -1;  // host mirror of state.pos
     bool use_graphs = true;
     hipGraphExec_t g_feed = nullptr, g_decode = nullptr;
+    int prefill_chunk = 512;  // 0: prompts run one token at a time
+    const char* prefill_off = nullptr;  // why the model cannot use the batched prefill
+    Prefill pf;
 };
 
 namespace {
@@ -152,6 +176,8 @@ void model_release(tmq_model* m) {
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
     for (tmq_tensor* t : m->owned) tmq_tensor_free(t);
     if (m->dmem) (void)hipFree(m->dmem);
+    if (m->pf.wmem) (void)hipFree(m->pf.wmem);
+    if (m->pf.amem) (void)hipFree(m->pf.amem);
     delete m;
 }
 
@@ -263,6 +289,284 @@ int check_state(tmq_model* m) {
     HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     if (st.err) return tmq_fail(TMQ_ERR_ARG, "decode step failed on the device (token or position out of range)");
     if (st.pos != m->pos) return tmq_fail(TMQ_ERR_HIP, "device position %d != expected %d", st.pos, m->pos);
+    return 0;
+}
+
+// ---------------------------------------------------------------- prefill
+// Weight digit planes of every layer (once per model).  q, k, v share one
+// plane set (rows q | k | v), gate and up another (rows gate | up).
+int pf_build_weights(tmq_model* m) {
+    Prefill& P = m->pf;
+    const tmq_model_config& c = m->cfg;
+    const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM, I = c.inter;
+    auto bytes = [](int rows, int K) { return 2 * (size_t)rows * K + 4 * (size_t)rows * (K / TMQ_PF_CHUNK + 1); };
+    const size_t per = bytes(H + 2 * KV, H) + bytes(H, H) + bytes(2 * I, H) + bytes(H, I);
+    const size_t total = per * c.n_layers + 256 * 16 * (size_t)c.n_layers;
+    hipError_t e = hipMalloc(&P.wmem, total);
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_NOMEM, "prefill weight planes (%zu B): %s", total, hipGetErrorString(e));
+    hipStream_t s = m->ctx->stream;
+    HIP_TRY(hipMemsetAsync(P.wmem, 0, total, s));
+    uint8_t* B = (uint8_t*)P.wmem;
+    size_t off = 0;
+    auto carve = [&](int rows, int K) {
+        TmqPfPlanes pl{};
+        auto take = [&](size_t n) {
+            uint8_t* p = B + off;
+            off += (n + 255) & ~(size_t)255;
+            return p;
+        };
+        pl.hi = (int8_t*)take((size_t)rows * K);
+        pl.lo = (int8_t*)take((size_t)rows * K);
+        pl.csum = (int32_t*)take(4 * (size_t)rows * (K / TMQ_PF_CHUNK));
+        pl.tsum = (int32_t*)take(4 * (size_t)rows);
+        pl.rows = rows;
+        pl.K = K;
+        return pl;
+    };
+    P.layers.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+        const Layer& Y = m->layers[l];
+        PfLayer& Q = P.layers[l];
+        Q.qkv = carve(H + 2 * KV, H);
+        Q.o = carve(H, H);
+        Q.gu = carve(2 * I, H);
+        Q.dn = carve(H, I);
+        struct Job {
+            const tmq_tensor* t;
+            const TmqPfPlanes* pl;
+            int row0;
+        } jobs[] = {{Y.q, &Q.qkv, 0}, {Y.k, &Q.qkv, H}, {Y.v, &Q.qkv, H + KV}, {Y.o, &Q.o, 0},
+                    {Y.gate, &Q.gu, 0}, {Y.up, &Q.gu, I}, {Y.down, &Q.dn, 0}};
+        for (const Job& j : jobs) LAUNCH_TRY(tmq_launch_pf_wdigits(j.t->dev, j.pl->hi, j.pl->lo, j.pl->K, j.row0, s));
+        for (const TmqPfPlanes* pl : {&Q.qkv, &Q.o, &Q.gu, &Q.dn})
+            LAUNCH_TRY(tmq_launch_pf_rowsums(pl->hi, pl->lo, pl->rows, pl->K, pl->csum, pl->tsum, s));
+    }
+    if (off > total) return tmq_fail(TMQ_ERR_HIP, "prefill plane layout overflow");
+    P.built = true;
+    return 0;
+}
+
+// Buffers of one chunk of `chunk` tokens (a multiple of 32).
+int pf_build_buffers(tmq_model* m, int chunk) {
+    Prefill& P = m->pf;
+    if (P.amem && P.chunk == chunk) return 0;
+    if (P.amem) {
+        HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+        (void)hipFree(P.amem);
+        P.amem = nullptr;
+    }
+    const tmq_model_config& c = m->cfg;
+    const int H = c.hidden, I = c.inter, T = chunk;
+    std::vector<std::pair<void**, size_t>> parts;
+    parts.push_back({(void**)&P.x0, 4 * (size_t)T * H});
+    parts.push_back({(void**)&P.x1, 4 * (size_t)T * H});
+    parts.push_back({(void**)&P.qb, 4 * (size_t)T * H});
+    parts.push_back({(void**)&P.ctx, 4 * (size_t)T * H});
+    parts.push_back({(void**)&P.s, 4 * (size_t)T * I});
+    parts.push_back({(void**)&P.part, 8 * (size_t)P.dn_split * T * H});
+    parts.push_back({(void**)&P.max_bits, 4 * (size_t)T});
+    for (int i = 0; i < 4; i++) {
+        const int K = i == 3 ? I : H;
+        P.in[i].rows = T;
+        P.in[i].K = K;
+        parts.push_back({(void**)&P.in[i].hi, (size_t)T * K});
+        parts.push_back({(void**)&P.in[i].lo, (size_t)T * K});
+        parts.push_back({(void**)&P.in[i].csum, 4 * (size_t)T * (K / TMQ_PF_CHUNK)});
+        parts.push_back({(void**)&P.in[i].tsum, 4 * (size_t)T});
+        parts.push_back({(void**)&P.xs[i], 4 * (size_t)T});
+    }
+    size_t total = 0;
+    for (auto& pr : parts) total += (pr.second + 255) & ~(size_t)255;
+    hipError_t e = hipMalloc(&P.amem, total);
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_NOMEM, "prefill buffers (%zu B): %s", total, hipGetErrorString(e));
+    size_t off = 0;
+    for (auto& pr : parts) {
+        *pr.first = (uint8_t*)P.amem + off;
+        off += (pr.second + 255) & ~(size_t)255;
+    }
+    P.chunk = chunk;
+    return 0;
+}
+
+// Whether the model's layers fit the prefill kernels: 64-aligned widths,
+// and Q8_0 only among q/k/v (whose GEMM folds Q8_0 tiles).
+const char* pf_unsupported(const tmq_model* m) {
+    const tmq_model_config& c = m->cfg;
+    const int KV = c.n_kv_heads * TMQ_HEAD_DIM;
+    if (c.hidden % 64 || KV % 64 || c.inter % 64) return "hidden, KV and FFN widths must be multiples of 64";
+    if (c.n_heads / c.n_kv_heads > 8) return "more than 8 query heads per KV head";
+    for (const Layer& Y : m->layers)
+        for (const tmq_tensor* t : {Y.o, Y.gate, Y.up, Y.down})
+            if (t->dev.type == TMQ_TYPE_Q8_0) return "Q8_0 attn_output / FFN weights";
+    return nullptr;
+}
+
+TmqPfSeg pf_seg(const tmq_tensor* t, int row0, const float* bias) {
+    TmqPfSeg sg{};
+    sg.row0 = row0;
+    sg.rows = t->dev.rows;
+    sg.q8 = t->dev.type == TMQ_TYPE_Q8_0;
+    sg.row_inv = t->dev.row_inv;
+    sg.row_scale = t->dev.row_scale;
+    sg.bias = bias;
+    return sg;
+}
+
+// One chunk: positions [p0, p0+T) through every layer.  With `last`, the
+// decode engine's residual state is set from the chunk's last token.
+int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
+    Prefill& P = m->pf;
+    const tmq_model_config& c = m->cfg;
+    const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM, I = c.inter, L = c.n_layers;
+    const int T_pad = (T + 31) & ~31;
+    hipStream_t s = m->ctx->stream;
+    auto fv = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
+    auto act = [&](int mode, int set, const float* x, const float* w, int n) {
+        TmqPfAct a{};
+        a.mode = mode;
+        a.n = n;
+        a.T = T;
+        a.p0 = p0;
+        a.x = x;
+        a.w = w;
+        a.eps = c.norm_eps;
+        a.out = P.in[set];
+        a.out.rows = T_pad;
+        a.xs = P.xs[set];
+        return a;
+    };
+    auto gemm = [&](int mode, const TmqPfPlanes& W, int set) {
+        TmqPfGemm g{};
+        g.mode = mode;
+        g.K = W.K;
+        g.T = T;
+        g.T_pad = T_pad;
+        g.p0 = p0;
+        g.split = 1;
+        g.rows = W.rows;
+        g.wa = W.hi;
+        g.wb = W.lo;
+        g.rw_c = W.csum;
+        g.rw_t = W.tsum;
+        g.xc = P.in[set].hi;
+        g.xe = P.in[set].lo;
+        g.tx_c = P.in[set].csum;
+        g.tx_t = P.in[set].tsum;
+        g.xs = P.xs[set];
+        g.H = H;
+        g.KV = KV;
+        return g;
+    };
+    auto dn_part = [&](int l) {
+        TmqPfPart d{};
+        d.part = P.part;
+        d.rw = P.layers[l].dn.tsum;
+        d.tx = P.in[3].tsum;
+        d.xs = P.xs[3];
+        d.row_inv = m->layers[l].down->dev.row_inv;
+        d.bias = nullptr;
+        d.split = P.dn_split;
+        d.ld = H;
+        d.K = I;
+        d.T_pad = T_pad;
+        return d;
+    };
+    for (int l = 0; l < L; l++) {
+        const Layer& Y = m->layers[l];
+        const PfLayer& W = P.layers[l];
+        // attn_norm + quantisation of the layer input (embedding at layer 0)
+        TmqPfAct a0 = act(l == 0 ? TMQ_PF_EMBED_NORM : TMQ_PF_RESID_NORM, 0, P.x1, m->fvec + Y.attn_norm, H);
+        if (l == 0) {
+            a0.tokens = m->tokens;
+            a0.emb = m->emb->dev;
+        } else {
+            a0.d1 = dn_part(l - 1);
+        }
+        a0.x_out = P.x0;
+        LAUNCH_TRY(tmq_launch_pf_act(a0, s));
+        // q, k, v -> RoPE -> q buffer and this layer's caches
+        TmqPfGemm g = gemm(TMQ_PF_QKV, W.qkv, 0);
+        g.nseg = 3;
+        g.seg[0] = pf_seg(Y.q, 0, fv(Y.bq));
+        g.seg[1] = pf_seg(Y.k, H, fv(Y.bk));
+        g.seg[2] = pf_seg(Y.v, H + KV, fv(Y.bv));
+        g.q_out = P.qb;
+        g.kc = m->kc + (size_t)l * c.max_seq * KV;
+        g.vc = m->vc + (size_t)l * c.max_seq * KV;
+        g.rope = m->rope;
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, 4, s));
+        // attention over positions 0 .. p0+t
+        TmqPfAttn at{};
+        at.q = P.qb;
+        at.kc = g.kc;
+        at.vc = g.vc;
+        at.ctx = P.ctx;
+        at.T = T;
+        at.p0 = p0;
+        at.n_heads = c.n_heads;
+        at.n_kv = c.n_kv_heads;
+        LAUNCH_TRY(tmq_launch_pf_attn(at, s));
+        // attn_output + residual
+        LAUNCH_TRY(tmq_launch_pf_act(act(TMQ_PF_PLAIN, 1, P.ctx, nullptr, H), s));
+        g = gemm(TMQ_PF_O, W.o, 1);
+        g.nseg = 1;
+        g.seg[0] = pf_seg(Y.o, 0, nullptr);
+        g.x_res = P.x0;
+        g.x_out = P.x1;
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, 4, s));
+        // ffn_norm, gate/up + SwiGLU
+        TmqPfAct a2 = act(TMQ_PF_NORM, 2, P.x1, m->fvec + Y.ffn_norm, H);
+        a2.zero_bits = P.max_bits;
+        LAUNCH_TRY(tmq_launch_pf_act(a2, s));
+        g = gemm(TMQ_PF_GU, W.gu, 2);
+        g.nseg = 2;
+        g.gu_rows = I;
+        g.seg[0] = pf_seg(Y.gate, 0, nullptr);
+        g.seg[1] = pf_seg(Y.up, I, nullptr);
+        g.s_out = P.s;
+        g.max_bits = P.max_bits;
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, 8, s));
+        // down projection, split over K; finalised by the next layer's input
+        TmqPfAct a3 = act(TMQ_PF_SILU, 3, P.s, nullptr, I);
+        a3.max_bits = P.max_bits;
+        LAUNCH_TRY(tmq_launch_pf_act(a3, s));
+        g = gemm(TMQ_PF_PART, W.dn, 3);
+        g.split = P.dn_split;
+        g.part = P.part;
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, 4, s));
+    }
+    if (last) {
+        const Layer& Z = m->layers[L - 1];
+        TmqPfHandoff h{};
+        h.dn = dn_part(L - 1);
+        h.x1 = P.x1;
+        h.t = T - 1;
+        h.H = H;
+        h.hid = m->hid[0];
+        h.kacc = const_cast<int64_t*>(Z.dd.acc);
+        h.xs_slot = const_cast<float*>(Z.dd.xs);
+        LAUNCH_TRY(tmq_launch_pf_handoff(h, s));
+    }
+    return 0;
+}
+
+// Positions [0, n) of a prompt whose tokens are on the device: as many as
+// the prefill's attention can hold go through in chunks; returns how many.
+int pf_prompt(tmq_model* m, int n, int* done) {
+    *done = 0;
+    const int qpk = m->cfg.n_heads / m->cfg.n_kv_heads;
+    int lim = n;
+    while (lim > 0 && tmq_pf_attn_lds(qpk, lim) > 159 * 1024) lim--;
+    if (lim < 2) return 0;
+    int rc;
+    if (!m->pf.built && (rc = pf_build_weights(m))) return rc;
+    const int chunk = (std::min(m->prefill_chunk, lim) + 31) & ~31;
+    if ((rc = pf_build_buffers(m, chunk))) return rc;
+    for (int p0 = 0; p0 < lim; p0 += chunk) {
+        const int T = std::min(chunk, lim - p0);
+        if ((rc = pf_run_chunk(m, p0, T, p0 + T >= lim))) return rc;
+    }
+    *done = lim;
     return 0;
 }
 
@@ -550,6 +854,8 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
     HIP_TRY(hipStreamSynchronize(s));
     m->use_graphs = env_int("TMQ_GRAPHS", 1) != 0;
+    m->prefill_chunk = env_int("TMQ_PREFILL", 512);
+    m->prefill_off = pf_unsupported(m);
     return 0;
 }
 
@@ -639,11 +945,27 @@ int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n) {
     if (!rc) rc = reset(m);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(m->tokens, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, m->ctx->stream));
-    for (int i = 0; i < n; i++) {
+    int done = 0;
+    if (m->prefill_chunk > 0 && !m->prefill_off && n >= 2) {
+        if ((rc = pf_prompt(m, n, &done))) return rc;
+        if (done > 0) {
+            TmqEngState st{done - 1, 0, {0, 0}};
+            HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, m->ctx->stream));
+            m->pos = done - 1;
+        }
+    }
+    for (int i = done; i < n; i++) {
         if ((rc = run_feed(m))) return rc;
         m->pos++;
     }
     return check_state(m);
+}
+
+int tmq_model_set_prefill(tmq_model* m, int chunk) {
+    if (!m || chunk < 0) return tmq_fail(TMQ_ERR_ARG, "bad prefill arguments");
+    if (chunk > 0 && m->prefill_off) return tmq_fail(TMQ_ERR_ARG, "batched prefill unavailable: %s", m->prefill_off);
+    m->prefill_chunk = chunk;
+    return 0;
 }
 
 int tmq_model_feed(tmq_model* m, int32_t token) {

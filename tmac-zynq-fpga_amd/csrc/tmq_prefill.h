@@ -1,0 +1,171 @@
+// tmq_prefill.h -- batched prefill: the prompt's tokens pushed through each
+// layer together, with every projection as one int8 MFMA GEMM.
+//
+// The reference processes a prompt one token at a time (process_prompt,
+// sim/tmac_gguf.cpp:1992-1997).  Every per-token quantity of a layer --
+// the norms, the int16 activation, the projections' int64 row sums, RoPE,
+// the cache rows -- depends only on that token and on earlier positions'
+// cache rows, so a layer can take all the prompt's tokens at once and give
+// the same bits, provided each operation is the same.  The projections are
+// exact integer sums; attention keeps each chain's order per query.
+//
+// Exact int16 x int16 products from int8 MFMA ("digits"):
+//   w = 256*a + b + 128   a = w >> 8,  b = (w & 255) - 128,  both in [-128, 127]
+//   x = 256*c + e + 128   (same split of the activation's xq)
+//   sum_k w*x = 65536*S(a,c) + 256*(S(a,e) + S(b,c)) + S(b,e)
+//             + 128*sum_k (w-128) + 128*sum_k (x-128) + 16384*K
+// where S(.,.) are int8 dot products over K (each within int32 for
+// K <= 65536: |a*c| <= 2^14).  The weights' digit planes are a function of
+// the weights only (the int16 w of each format's normalisation), built once;
+// the per-row and per-token sums of (w-128), (x-128) are kept per 64-column
+// chunk, which is also the Q8_0 tile of the reference's fold.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tmq_internal.h"
+
+#define TMQ_PF_CHUNK 64  // columns per correction chunk (= one Q8_0 tile)
+
+// Digit operand planes of one K-wide matrix: [rows][K] int8 each, plus the
+// chunk and total sums of (v - 128) per row.
+struct TmqPfPlanes {
+    int8_t* hi;      // a / c
+    int8_t* lo;      // b / e
+    int32_t* csum;   // [rows][K/64]
+    int32_t* tsum;   // [rows]
+    int32_t rows, K;
+};
+
+// Split-K digit sums of one GEMM, finalised by the consumer:
+//   acc = sum_s part[s][t][row] + 128*(rw[row] + tx[t]) + 16384*K
+//   v   = (float)((double)acc * xs[t] / (double)row_inv[row])  (+ bias)
+struct TmqPfPart {
+    const int64_t* part;   // [split][T_pad][ld]
+    const int32_t* rw;     // per row of the plane set: sum (w - 128)
+    const int32_t* tx;     // per token: sum (x - 128)
+    const float* xs;       // per token x_scale
+    const float* row_inv;  // per row of the tensor
+    const float* bias;     // per row of the tensor, or null
+    int32_t split, ld, K, T_pad;
+};
+
+// Activation operands of a layer step for T tokens (one workgroup each):
+// the value of every column, then RMSNorm / quantisation exactly as the
+// decode engine's prologues (sim/tmac_gguf.cpp:415-422, :1225-1231).
+enum {
+    TMQ_PF_EMBED_NORM = 0,  // embedding of tokens[p0 + t], then the norm
+    TMQ_PF_RESID_NORM = 1,  // x[t] + finalise(d1), then the norm
+    TMQ_PF_NORM = 2,        // x[t], then the norm
+    TMQ_PF_PLAIN = 3,       // x[t]
+    TMQ_PF_SILU = 4         // x[t] with the max |x| given per token (max_bits)
+};
+struct TmqPfAct {
+    int32_t mode, n, T, p0;
+    const float* x;            // [T][n]
+    const float* w;            // RMSNorm weight (norm modes)
+    float eps;
+    int32_t pad_;
+    const uint32_t* max_bits;  // SILU: per token
+    TmqPfPart d1;              // RESID_NORM
+    float* x_out;              // EMBED/RESID: the value before the norm, [T][n]
+    uint32_t* zero_bits;       // NORM: per-token max slots cleared for the next GU GEMM (or null)
+    const int32_t* tokens;     // EMBED: token ids by position
+    TmqTensorDev emb;          // EMBED: quantised embedding
+    TmqPfPlanes out;           // digit planes [T_pad][n]
+    float* xs;                 // [T_pad] x_scale per token
+};
+
+// One tensor's rows inside a GEMM's plane set.
+struct TmqPfSeg {
+    int32_t row0, rows;
+    int32_t q8;                // Q8_0: fold 64-column tiles (sim/tmac_gguf.cpp:1075-1076)
+    int32_t pad_;
+    const float* row_inv;      // Q5_0/K-quants: row_inv; Q8_0: unused
+    const float* row_scale;    // Q8_0
+    const float* bias;         // may be null
+};
+
+enum {
+    TMQ_PF_QKV = 0,   // q -> RoPE -> q_out; k -> RoPE -> kc; v -> vc
+    TMQ_PF_O = 1,     // x_out = x_res + o
+    TMQ_PF_GU = 2,    // s_out = silu(gate) * up, max |s| per token
+    TMQ_PF_PART = 3   // int64 digit sums per split
+};
+struct TmqPfGemm {
+    int32_t mode, K, T, T_pad, p0, split, gu_rows, nseg;
+    int32_t rows, pad_;        // rows of the plane set (GU: 2 * gu_rows)
+    const int8_t* wa;          // weight digit planes [rows][K]
+    const int8_t* wb;
+    const int32_t* rw_c;       // [rows][K/64]
+    const int32_t* rw_t;       // [rows]
+    const int8_t* xc;          // activation digit planes [T_pad][K]
+    const int8_t* xe;
+    const int32_t* tx_c;       // [T_pad][K/64]
+    const int32_t* tx_t;       // [T_pad]
+    const float* xs;           // [T_pad]
+    TmqPfSeg seg[3];
+    // QKV
+    float* q_out;              // [T][H]
+    float* kc;                 // this layer's caches [max_pos][KV]
+    float* vc;
+    const float2* rope;        // [max_pos][32]
+    int32_t H, KV;
+    // O
+    const float* x_res;        // [T][rows]
+    float* x_out;
+    // GU
+    float* s_out;              // [T][gu_rows]
+    uint32_t* max_bits;        // [T]
+    // PART
+    int64_t* part;             // [split][T_pad][rows]
+};
+
+// Attention of T consecutive positions p0.. (one workgroup per token and KV
+// head): the sequential chains of the decode engine's attention, per query.
+struct TmqPfAttn {
+    const float* q;            // [T][H] after RoPE
+    const float* kc;           // this layer's caches, positions 0 .. p0+T-1 written
+    const float* vc;
+    float* ctx;                // [T][H]
+    int32_t T, p0, n_heads, n_kv;
+};
+
+// The decode engine's state after the last token of a prefill: the
+// residual before the last layer's down projection, that projection's int64
+// row sums and x_scale (TmqDeferred form), so logits and the next step run
+// exactly as after a sequential prompt.
+struct TmqPfHandoff {
+    TmqPfPart dn;              // last layer's down projection
+    const float* x1;           // [T][H]
+    int32_t t, H;              // token index (T-1)
+    float* hid;                // engine residual buffer
+    int64_t* kacc;             // engine K-split sums of the last down projection
+    float* xs_slot;
+};
+
+#if defined(__HIPCC__)
+// int64 row sum of row r, token t of a split-K GEMM (TmqPfPart).
+__device__ __forceinline__ int64_t tmq_pf_acc(const TmqPfPart& D, int t, int r) {
+    int64_t acc = 0;
+    for (int s = 0; s < D.split; s++) acc += D.part[((size_t)s * D.T_pad + t) * D.ld + r];
+    return acc + 128 * ((int64_t)D.rw[r] + D.tx[t]) + 16384 * (int64_t)D.K;
+}
+// ... finalised as the decode engine's K-split rows (sim/tmac_gguf.cpp:1303-1305,
+// bias :1595-1597)
+__device__ __forceinline__ float tmq_pf_fin(const TmqPfPart& D, int t, int r) {
+    float v = (float)(((double)tmq_pf_acc(D, t, r) * (double)D.xs[t]) / (double)D.row_inv[r]);
+    if (D.bias) v = v + D.bias[r];
+    return v;
+}
+#endif
+
+// Launchers: tmq_kernels.hip (operand planes) and tmq_prefill.hip.
+int tmq_launch_pf_wdigits(const TmqTensorDev& t, int8_t* hi, int8_t* lo, int K, int row0, hipStream_t s);
+int tmq_launch_pf_rowsums(const int8_t* hi, const int8_t* lo, int rows, int K, int32_t* csum, int32_t* tsum,
+                          hipStream_t s);
+int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s);
+int tmq_launch_pf_gemm(const TmqPfGemm& g, int waves, hipStream_t s);
+int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
+int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);
+size_t tmq_pf_attn_lds(int qpk, int npos);

@@ -36,7 +36,7 @@ EXPORTS = [
     "tmq_model_load", "tmq_model_load_mem", "tmq_model_free", "tmq_model_get_config",
     "tmq_model_weight_bytes", "tmq_model_position", "tmq_model_set_graphs", "tmq_model_prompt",
     "tmq_model_feed", "tmq_model_feed_dump", "tmq_model_logits", "tmq_model_generate",
-    "tmq_model_generate_async", "tmq_model_tokens", "tmq_model_hidden",
+    "tmq_model_generate_async", "tmq_model_tokens", "tmq_model_hidden", "tmq_model_set_prefill",
 ]
 
 
@@ -106,6 +106,7 @@ def lib(path: str = LIB_PATH):
         "tmq_model_weight_bytes": (U64, [P]),
         "tmq_model_position": (I, [P]),
         "tmq_model_set_graphs": (I, [P, I]),
+        "tmq_model_set_prefill": (I, [P, I]),
         "tmq_model_prompt": (I, [P, P, I]),
         "tmq_model_feed": (I, [P, C.c_int32]),
         "tmq_model_feed_dump": (I, [P, C.c_int32, P]),
@@ -307,6 +308,11 @@ class Model:
 
     def set_graphs(self, enable: bool):
         _check(lib().tmq_model_set_graphs(self.handle, int(bool(enable))))
+
+    def set_prefill(self, chunk: int):
+        """0: prompts one token at a time; > 0: batched prefill in chunks of
+        this many tokens (default 512)."""
+        _check(lib().tmq_model_set_prefill(self.handle, int(chunk)))
 
     def prompt(self, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
