@@ -186,6 +186,44 @@ def decode_bench(ctx, torch, stream, tokens=128, warmup=8):
             "first_tokens": got[:8].tolist()}
 
 
+# int8 MACs per token of the batched prefill: four digit products per
+# weight of every layer projection (q,k,v,o,gate,up,down) of the C4 model
+PF_LAYER_WEIGHTS = 24 * (1152 * 896 + 896 * 896 + 2 * 4864 * 896 + 896 * 4864)
+PF_LAYER_BYTES = 246930432  # ggml bytes of those weights
+MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8, datasheet
+
+
+def prefill_bench(ctx, n=512, reps=5):
+    """a seeded n-token prompt through the 24-layer model
+    with the batched prefill (one chunk, every projection an int8-digit MFMA
+    GEMM).  Timed per tmq_model_prompt call, wall clock (host launches and the
+    final synchronisation included); the weight digit planes are built by the
+    first, untimed call."""
+    import tmq
+    from tmq import model_synth, tmacfile
+    log("prefill: generating the synthetic C4 model")
+    blob = tmacfile.to_bytes(model_synth.gen_model(2024))
+    m = tmq.Model(ctx, blob, max_seq=max(512, n + 16))
+    del blob
+    toks = np.random.Generator(np.random.PCG64(12345)).integers(0, 151936, size=n).astype(np.int32)
+    m.set_prefill(512)
+    m.prompt(toks)
+    ctx.sync()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        m.prompt(toks)
+        times.append(time.perf_counter() - t0)
+    first = m.generate(4).tolist()
+    m.free()
+    ms = float(np.median(times)) * 1e3
+    tops = 4 * PF_LAYER_WEIGHTS * n * 2 / (ms * 1e-3) / 1e12
+    return {"prompt_tokens": n, "ms": round(ms, 4), "ms_min": round(min(times) * 1e3, 4),
+            "tok_s": round(n / (ms * 1e-3), 1), "layer_weight_gbps": round(PF_LAYER_BYTES / (ms * 1e-3) / 1e9, 1),
+            "int8_tops": round(tops, 2), "mfma_frac": round(tops / MFMA_I8_PEAK_TOPS, 4),
+            "next_tokens": first}
+
+
 def cpu_decode_baseline(seconds):
     """The reference engine (oracle/_ref: load_tmac + forward_all_layers +
     get_logits_q8 with the --fpga-* paths) on one host thread, greedy steps
@@ -236,14 +274,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--sets", type=int, default=SETS)
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + ["c4"],
-                    help="c4: only the full-model greedy decode (BASELINE configs[3])")
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + ["c4", "c5"],
+                    help="c4: only the full-model greedy decode (BASELINE configs[3]); "
+                         "c5: only the 512-token batched prefill (BASELINE configs[4])")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE GEMV configs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only; the GEMV shards by output rows with "
-              "no exchange (see DESIGN.md), multi-GPU runs are not part of it", file=sys.stderr)
+              "no exchange, and multi-GPU runs are not part of it", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -257,16 +296,38 @@ def main():
     stream = torch.cuda.ExternalStream(ctx.stream)
     wl = args.workload
     if wl == "c4":
-        dec = decode_bench(ctx, torch, stream, tokens=args.steps if args.steps <= 500 else 500)
+        dec = decode_bench(ctx, torch, stream, tokens=min(args.steps, 500), warmup=args.warmup)
         ctx.close()
         out = {"metric": "Qwen2-0.5B batch-1 greedy decode tok/s", "value": dec["tok_s"], "unit": "tok/s",
-               "n_gpus": 1, "steps": dec["tokens"], "warmup": 8, "ms_per_step": dec["ms_per_token"],
+               "n_gpus": 1, "steps": dec["tokens"], "warmup": args.warmup, "ms_per_step": dec["ms_per_token"],
                "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int16",
                "data": "synthetic Qwen2-0.5B-shaped model (tmq.model_synth seed 2024), one seeded prompt token",
                "config": {"workload": "BASELINE configs[3]: 24-layer decode, mixed Q8_0/Q6_K and Q5_0/Q4_K "
                           "layers, Q8_0 tied logits, greedy", "weight_bytes_per_token": dec["weight_bytes_per_token"]},
                "extra": {"c4_decode": dec},
                "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(args.cpu_seconds)}
+        print(json.dumps(out), flush=True)
+        return
+    if wl == "c5":
+        pf = prefill_bench(ctx, 512, max(3, min(args.steps, 20)))
+        ctx.close()
+        cpu = None
+        if not args.no_cpu:
+            dec = cpu_decode_baseline(args.cpu_seconds)
+            if dec is not None:
+                # the reference's process_prompt is the same per-token step
+                cpu = dict(dec, sample=dec["sample"] + "; process_prompt runs the same step per prompt token")
+        out = {"metric": "Qwen2-0.5B batched prefill tok/s (512-token prompt)", "value": pf["tok_s"],
+               "unit": "tok/s", "n_gpus": 1, "steps": max(3, min(args.steps, 20)), "warmup": 1,
+               "ms_per_step": pf["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+               "dtype": "int8 (exact int16 x int16 as digit products)",
+               "data": "synthetic Qwen2-0.5B-shaped model (tmq.model_synth seed 2024), 512 seeded token ids",
+               "config": {"workload": "BASELINE configs[4]: 512-token prompt, 24 layers, batched prefill "
+                          "(bit-exact with the one-token-at-a-time prompt)", "prompt_tokens": 512},
+               "roofline": {"bound": "mfma", "achieved": pf["int8_tops"], "peak": MFMA_I8_PEAK_TOPS,
+                            "unit": "TFLOP/s", "frac": pf["mfma_frac"], "traffic": None,
+                            "kernel": "whole prefill (int8 digit MACs / prompt time)"},
+               "extra": {"c5_prefill": pf}, "cpu_baseline": cpu}
         print(json.dumps(out), flush=True)
         return
     copies = args.sets if wl == "c2" else None
@@ -313,6 +374,7 @@ def main():
                            "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
         extra["c2_attn_q_single_launch_us"] = round(single_launch_us(ctx, torch, dev, stream, 50), 2)
         extra["c4_decode"] = decode_bench(ctx, torch, stream)
+        extra["c5_prefill"] = prefill_bench(ctx)
         out["extra"] = extra
     ctx.close()
     if not args.no_cpu:

@@ -114,15 +114,17 @@ struct ActT {
 
 // Weight sink: takes the place of an activation in the block decoders and
 // stores each int16 weight pair as its prefill digits instead of multiplying
-// it (hi = w >> 8, lo = (w & 255) - 128; two bytes per plane per pair at
-// column 2*kx of the row).
+// it (hi = w >> 8, lo = (w & 255) - 128), at columns 2*kx, 2*kx+1 of `row`
+// in fragment-major planes (tmq_prefill.h; the pair is two adjacent bytes
+// of one fragment per digit).
 struct WDigits {
     static constexpr bool kSink = true;
-    int8_t* hi;
-    int8_t* lo;
+    int8_t* planes;
+    int row, K;
     __device__ __forceinline__ void put(int kx, uint32_t P) const {
-        *(uint16_t*)(hi + 2 * kx) = (uint16_t)__builtin_amdgcn_perm(0u, P, 0x0c0c0301u);
-        *(uint16_t*)(lo + 2 * kx) = (uint16_t)(__builtin_amdgcn_perm(0u, P, 0x0c0c0200u) ^ 0x8080u);
+        const size_t o = tmq_pf_off(row, 2 * kx, K, 0);
+        *(uint16_t*)(planes + o) = (uint16_t)__builtin_amdgcn_perm(0u, P, 0x0c0c0301u);
+        *(uint16_t*)(planes + o + 1024) = (uint16_t)(__builtin_amdgcn_perm(0u, P, 0x0c0c0200u) ^ 0x8080u);
     }
 };
 typedef ActT<const cu32*> Act;
@@ -1143,10 +1145,10 @@ __global__ void tile_q8_kernel(const uint8_t* __restrict__ W, const uint16_t* __
 // two int8 planes at rows row0.. of a plane set K columns wide.  One lane
 // per row.
 template <int FMT>
-__global__ __launch_bounds__(64) void pf_wdigits_kernel(TmqTensorDev t, int8_t* hi, int8_t* lo, int K, int row0) {
+__global__ __launch_bounds__(64) void pf_wdigits_kernel(TmqTensorDev t, int8_t* planes, int K, int row0) {
     const int r = blockIdx.x * 64 + threadIdx.x;
     if (r >= t.rows) return;
-    const WDigits S{hi + (size_t)(row0 + r) * K, lo + (size_t)(row0 + r) * K};
+    const WDigits S{planes, row0 + r, K};
     int sh = 0, sl = 0;
     const float inv = t.row_inv[r];
     for (int b = 0; b < t.nb; b++) {
@@ -1157,34 +1159,40 @@ __global__ __launch_bounds__(64) void pf_wdigits_kernel(TmqTensorDev t, int8_t* 
 
 // Per row of a digit plane set: the sums of (v - 128) = 256*hi + lo over
 // each 64-column chunk and over the row.  One wave per row.
-__global__ __launch_bounds__(64) void pf_rowsums_kernel(const int8_t* __restrict__ hi, const int8_t* __restrict__ lo,
-                                                       int K, int32_t* csum, int32_t* tsum) {
-    const int r = blockIdx.x, lane = threadIdx.x, nc = K / TMQ_PF_CHUNK;
+__global__ __launch_bounds__(64) void pf_rowsums_kernel(TmqPfPlanes p) {
+    const int r = blockIdx.x, lane = threadIdx.x, nc = p.K / TMQ_PF_CHUNK;
     int32_t tot = 0;
     for (int c = 0; c < nc; c++) {
-        const size_t i = (size_t)r * K + c * TMQ_PF_CHUNK + lane;
-        int v = 256 * (int)hi[i] + (int)lo[i];
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-        if (lane == 0) csum[(size_t)r * nc + c] = v;
+        const size_t o = tmq_pf_off(r, c * TMQ_PF_CHUNK + lane, p.K, 0);
+        int v = 256 * (int)p.d[o] + (int)p.d[o + 1024];
+        for (int k = 32; k > 0; k >>= 1) v += __shfl_xor(v, k);
+        if (lane == 0) p.csum[(size_t)r * nc + c] = v;
         tot += v;
     }
-    if (lane == 0) tsum[r] = tot;
+    if (lane == 0) p.tsum[r] = tot;
 }
 
 // Activation operands of one token (workgroup t of T_pad): the columns'
 // values, RMSNorm, x_scale and xq exactly as eng_prologue forms them, then
-// xq as digits with its (xq - 128) sums.  Tokens t >= T get zero planes.
+// xq as digits with its (xq - 128) sums.  Each thread takes groups of four
+// consecutive columns (one dword of each digit plane).  Tokens t >= T get
+// zero planes.
+__device__ __forceinline__ float pf_value(const TmqPfAct& a, int t, int i, int tok) {
+    if (a.mode == TMQ_PF_EMBED_NORM) return tensor_elem(a.emb, tok, i);
+    if (a.mode == TMQ_PF_RESID_NORM) return a.x[(size_t)t * a.n + i] + tmq_pf_fin(a.d1, t, i);
+    return a.x[(size_t)t * a.n + i];
+}
 __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     extern __shared__ float pf_lds[];
     __shared__ float red[8];
     const int t = blockIdx.x, n = a.n, tid = threadIdx.x, nt = blockDim.x;
-    const int wave = tid >> 6, lane = tid & 63, nc = n / TMQ_PF_CHUNK;
-    int8_t* hi = a.out.hi + (size_t)t * n;
-    int8_t* lo = a.out.lo + (size_t)t * n;
+    const int wave = tid >> 6, lane = tid & 63, nc = n / TMQ_PF_CHUNK, ng = n >> 2;
+    int8_t* dp = a.out.d;
     if (t >= a.T) {
-        for (int i = tid; i < n; i += nt) {
-            hi[i] = 0;
-            lo[i] = 0;
+        for (int gi = tid; gi < ng; gi += nt) {
+            const size_t o = tmq_pf_off(t, 4 * gi, n, 0);
+            *(uint32_t*)(dp + o) = 0u;
+            *(uint32_t*)(dp + o + 1024) = 0u;
         }
         for (int c = tid; c < nc; c += nt) a.out.csum[(size_t)t * nc + c] = 0;
         if (tid == 0) {
@@ -1199,18 +1207,26 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     const bool wr = a.x_out && (a.mode == TMQ_PF_EMBED_NORM || a.mode == TMQ_PF_RESID_NORM);
     const int tok = a.mode == TMQ_PF_EMBED_NORM ? a.tokens[a.p0 + t] : 0;
     float m = 0.0f;
-    for (int i = tid; i < n; i += nt) {
-        float v;
-        if (a.mode == TMQ_PF_EMBED_NORM) v = tensor_elem(a.emb, tok, i);
-        else if (a.mode == TMQ_PF_RESID_NORM) v = a.x[(size_t)t * n + i] + tmq_pf_fin(a.d1, t, i);
-        else v = a.x[(size_t)t * n + i];
-        if (wr) a.x_out[(size_t)t * n + i] = v;
+    for (int gi = tid; gi < ng; gi += nt) {
+        const int i0 = 4 * gi;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = pf_value(a, t, i0 + j, tok);
+        if (wr) *(float4*)(a.x_out + (size_t)t * n + i0) = make_float4(v[0], v[1], v[2], v[3]);
         if (norm) {
-            sq[i] = v * v;
-            v = v * a.w[i];
+            const float4 w4 = *(const float4*)(a.w + i0);
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+            float s4[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                s4[j] = v[j] * v[j];
+                v[j] = v[j] * wv[j];
+            }
+            *(float4*)(sq + i0) = make_float4(s4[0], s4[1], s4[2], s4[3]);
         }
-        X[i] = v;
-        m = fmaxf(m, fabsf(v));
+        *(float4*)(X + i0) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) m = fmaxf(m, fabsf(v[j]));
     }
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if (lane == 0) red[1 + wave] = m;
@@ -1234,20 +1250,33 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
         if (norm) mm = mm * s;
     }
     const float xs = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
-    // n is a multiple of 64: chunk c = columns [64c, 64c+64) is one wave's pass
+    // 16 threads per 64-column chunk; n/4 groups cover whole chunks
     int32_t tot = 0;
-    for (int c = wave; c < nc; c += (nt >> 6)) {
-        const int i = c * TMQ_PF_CHUNK + lane;
-        float u = X[i];
-        if (norm) u = u * s;
-        const int q = (int)(int16_t)roundf(u / xs);
-        hi[i] = (int8_t)(q >> 8);
-        lo[i] = (int8_t)((q & 255) ^ 128);
-        int v = q - 128;
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-        if (lane == 0) a.out.csum[(size_t)t * nc + c] = v;
-        tot += v;
+    for (int g0 = 0; g0 < ng; g0 += nt) {
+        const int gi = g0 + tid;
+        int sum = 0;
+        if (gi < ng) {
+            const int i0 = 4 * gi;
+            const float4 x4 = *(const float4*)(X + i0);
+            float u[4] = {x4.x, x4.y, x4.z, x4.w};
+            uint32_t hi = 0, lo = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (norm) u[j] = u[j] * s;
+                const int q = (int)(int16_t)roundf(u[j] / xs);
+                hi |= ((uint32_t)(q >> 8) & 255u) << (8 * j);
+                lo |= (((uint32_t)q & 255u) ^ 128u) << (8 * j);
+                sum += q - 128;
+            }
+            const size_t o = tmq_pf_off(t, i0, n, 0);
+            *(uint32_t*)(dp + o) = hi;
+            *(uint32_t*)(dp + o + 1024) = lo;
+        }
+        for (int k = 1; k < 16; k <<= 1) sum += __shfl_xor(sum, k);
+        if (gi < ng && (gi & 15) == 0) a.out.csum[(size_t)t * nc + (gi >> 4)] = sum;
+        tot += ((tid & 15) == 0 && gi < ng) ? sum : 0;
     }
+    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o);
     __syncthreads();
     if (lane == 0) red[1 + wave] = __builtin_bit_cast(float, tot);
     __syncthreads();
@@ -1372,27 +1401,28 @@ int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec,
 }
 
 // ------------------------------------------------------ prefill operands
-int tmq_launch_pf_wdigits(const TmqTensorDev& t, int8_t* hi, int8_t* lo, int K, int row0, hipStream_t s) {
+int tmq_launch_pf_wdigits(const TmqTensorDev& t, int8_t* planes, int K, int row0, hipStream_t s) {
+    if (t.cols != K || K % TMQ_PF_CHUNK || row0 % 32) return (int)hipErrorInvalidValue;
     const dim3 grid((t.rows + 63) / 64), blk(64);
     switch (t.type) {
-    case kQ5_0: hipLaunchKernelGGL(pf_wdigits_kernel<kQ5_0>, grid, blk, 0, s, t, hi, lo, K, row0); break;
-    case kQ8_0: hipLaunchKernelGGL(pf_wdigits_kernel<kQ8_0>, grid, blk, 0, s, t, hi, lo, K, row0); break;
-    case kQ4_K: hipLaunchKernelGGL(pf_wdigits_kernel<kQ4_K>, grid, blk, 0, s, t, hi, lo, K, row0); break;
-    case kQ6_K: hipLaunchKernelGGL(pf_wdigits_kernel<kQ6_K>, grid, blk, 0, s, t, hi, lo, K, row0); break;
+    case kQ5_0: hipLaunchKernelGGL(pf_wdigits_kernel<kQ5_0>, grid, blk, 0, s, t, planes, K, row0); break;
+    case kQ8_0: hipLaunchKernelGGL(pf_wdigits_kernel<kQ8_0>, grid, blk, 0, s, t, planes, K, row0); break;
+    case kQ4_K: hipLaunchKernelGGL(pf_wdigits_kernel<kQ4_K>, grid, blk, 0, s, t, planes, K, row0); break;
+    case kQ6_K: hipLaunchKernelGGL(pf_wdigits_kernel<kQ6_K>, grid, blk, 0, s, t, planes, K, row0); break;
     default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();
 }
 
-int tmq_launch_pf_rowsums(const int8_t* hi, const int8_t* lo, int rows, int K, int32_t* csum, int32_t* tsum,
-                          hipStream_t s) {
-    if (rows <= 0 || K % TMQ_PF_CHUNK) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(pf_rowsums_kernel, dim3(rows), dim3(64), 0, s, hi, lo, K, csum, tsum);
+int tmq_launch_pf_rowsums(const TmqPfPlanes& p, hipStream_t s) {
+    if (p.rows <= 0 || p.rows % 32 || p.K % TMQ_PF_CHUNK) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_rowsums_kernel, dim3(p.rows), dim3(64), 0, s, p);
     return (int)hipGetLastError();
 }
 
 int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s) {
-    if (a.n % TMQ_PF_CHUNK || a.n > TMQ_ENG_MAXN || a.out.rows < a.T) return (int)hipErrorInvalidValue;
+    if (a.n % TMQ_PF_CHUNK || a.n > TMQ_ENG_MAXN || a.out.rows < a.T || a.out.rows % 32 || a.out.K != a.n)
+        return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(pf_act_kernel, dim3(a.out.rows), dim3(256), 8 * (size_t)a.n, s, a);
     return (int)hipGetLastError();
 }

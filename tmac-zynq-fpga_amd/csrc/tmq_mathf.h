@@ -67,7 +67,13 @@ TMQ_HD inline uint64_t exp2_tab(int i) {
 #endif
 }
 
-TMQ_HD inline float tmq_expf(float x) {
+// The table read through a functor, so that a kernel can keep a copy in LDS.
+struct Exp2TabConst {
+    TMQ_HD uint64_t operator()(int i) const { return exp2_tab(i); }
+};
+
+template <class Tab>
+TMQ_HD inline float tmq_expf_tab(float x, const Tab& tab) {
     const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
     const double Shift = 0x1.8p+52;
     const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -85,7 +91,7 @@ TMQ_HD inline float tmq_expf(float x) {
     const uint64_t ki = as_u64(kd);
     kd -= Shift;
     const double r = __builtin_fma(InvLn2N, xd, -kd);
-    const uint64_t t = exp2_tab((int)(ki % 32)) + (ki << 47);
+    const uint64_t t = tab((int)(ki % 32)) + (ki << 47);
     const double s = as_double(t);
     const double z = __builtin_fma(C0, r, C1);
     const double r2 = r * r;
@@ -93,6 +99,8 @@ TMQ_HD inline float tmq_expf(float x) {
     y = __builtin_fma(z, r2, y);
     return (float)(y * s);
 }
+
+TMQ_HD inline float tmq_expf(float x) { return tmq_expf_tab(x, Exp2TabConst{}); }
 
 // RoPE factors for positions [0, max_pos), as apply_rope forms them on the
 // host (sim/tmac_gguf.cpp:1531-1535): theta = 1/powf(base, (float)d/head_dim),

@@ -120,7 +120,7 @@ struct Prefill {
     bool built = false;
     void* wmem = nullptr;  // all layers' weight planes
     void* amem = nullptr;  // chunk buffers
-    int chunk = 0;         // tokens per chunk the buffers hold (multiple of 32)
+    int chunk = 0;         // tokens per chunk the buffers hold (multiple of 128)
     std::vector<PfLayer> layers;
     float *x0 = nullptr, *x1 = nullptr, *qb = nullptr, *ctx = nullptr, *s = nullptr;
     TmqPfPlanes in[4]{};   // activation planes: QKV, O, GU, DN inputs
@@ -128,6 +128,7 @@ struct Prefill {
     int64_t* part = nullptr;
     uint32_t* max_bits = nullptr;
     int dn_split = 4;
+    int tile[4] = {2, 2, 1, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
 };
 
 struct tmq_model {
@@ -297,6 +298,12 @@ int check_state(tmq_model* m) {
 // plane set (rows q | k | v), gate and up another (rows gate | up).
 int pf_build_weights(tmq_model* m) {
     Prefill& P = m->pf;
+    P.dn_split = std::max(1, env_int("TMQ_PF_SPLIT_DN", P.dn_split));
+    if (const char* e = getenv("TMQ_PF_TILES")) {
+        int t[4];
+        if (sscanf(e, "%d,%d,%d,%d", &t[0], &t[1], &t[2], &t[3]) == 4)
+            for (int i = 0; i < 4; i++) P.tile[i] = t[i];
+    }
     const tmq_model_config& c = m->cfg;
     const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM, I = c.inter;
     auto bytes = [](int rows, int K) { return 2 * (size_t)rows * K + 4 * (size_t)rows * (K / TMQ_PF_CHUNK + 1); };
@@ -315,8 +322,7 @@ int pf_build_weights(tmq_model* m) {
             off += (n + 255) & ~(size_t)255;
             return p;
         };
-        pl.hi = (int8_t*)take((size_t)rows * K);
-        pl.lo = (int8_t*)take((size_t)rows * K);
+        pl.d = (int8_t*)take(2 * (size_t)rows * K);
         pl.csum = (int32_t*)take(4 * (size_t)rows * (K / TMQ_PF_CHUNK));
         pl.tsum = (int32_t*)take(4 * (size_t)rows);
         pl.rows = rows;
@@ -337,16 +343,15 @@ int pf_build_weights(tmq_model* m) {
             int row0;
         } jobs[] = {{Y.q, &Q.qkv, 0}, {Y.k, &Q.qkv, H}, {Y.v, &Q.qkv, H + KV}, {Y.o, &Q.o, 0},
                     {Y.gate, &Q.gu, 0}, {Y.up, &Q.gu, I}, {Y.down, &Q.dn, 0}};
-        for (const Job& j : jobs) LAUNCH_TRY(tmq_launch_pf_wdigits(j.t->dev, j.pl->hi, j.pl->lo, j.pl->K, j.row0, s));
-        for (const TmqPfPlanes* pl : {&Q.qkv, &Q.o, &Q.gu, &Q.dn})
-            LAUNCH_TRY(tmq_launch_pf_rowsums(pl->hi, pl->lo, pl->rows, pl->K, pl->csum, pl->tsum, s));
+        for (const Job& j : jobs) LAUNCH_TRY(tmq_launch_pf_wdigits(j.t->dev, j.pl->d, j.pl->K, j.row0, s));
+        for (const TmqPfPlanes* pl : {&Q.qkv, &Q.o, &Q.gu, &Q.dn}) LAUNCH_TRY(tmq_launch_pf_rowsums(*pl, s));
     }
     if (off > total) return tmq_fail(TMQ_ERR_HIP, "prefill plane layout overflow");
     P.built = true;
     return 0;
 }
 
-// Buffers of one chunk of `chunk` tokens (a multiple of 32).
+// Buffers of one chunk of `chunk` tokens (a multiple of 128).
 int pf_build_buffers(tmq_model* m, int chunk) {
     Prefill& P = m->pf;
     if (P.amem && P.chunk == chunk) return 0;
@@ -363,14 +368,16 @@ int pf_build_buffers(tmq_model* m, int chunk) {
     parts.push_back({(void**)&P.qb, 4 * (size_t)T * H});
     parts.push_back({(void**)&P.ctx, 4 * (size_t)T * H});
     parts.push_back({(void**)&P.s, 4 * (size_t)T * I});
-    parts.push_back({(void**)&P.part, 8 * (size_t)P.dn_split * T * H});
+    // split-K sums of the down projection, or the Q8_0 V tiles of q/k/v
+    const int KV = c.n_kv_heads * TMQ_HEAD_DIM;
+    const size_t part_n = std::max((size_t)P.dn_split * T * H, (size_t)T * KV * (H / TMQ_PF_CHUNK));
+    parts.push_back({(void**)&P.part, 8 * part_n});
     parts.push_back({(void**)&P.max_bits, 4 * (size_t)T});
     for (int i = 0; i < 4; i++) {
         const int K = i == 3 ? I : H;
         P.in[i].rows = T;
         P.in[i].K = K;
-        parts.push_back({(void**)&P.in[i].hi, (size_t)T * K});
-        parts.push_back({(void**)&P.in[i].lo, (size_t)T * K});
+        parts.push_back({(void**)&P.in[i].d, 2 * (size_t)T * K});
         parts.push_back({(void**)&P.in[i].csum, 4 * (size_t)T * (K / TMQ_PF_CHUNK)});
         parts.push_back({(void**)&P.in[i].tsum, 4 * (size_t)T});
         parts.push_back({(void**)&P.xs[i], 4 * (size_t)T});
@@ -395,9 +402,12 @@ const char* pf_unsupported(const tmq_model* m) {
     const int KV = c.n_kv_heads * TMQ_HEAD_DIM;
     if (c.hidden % 64 || KV % 64 || c.inter % 64) return "hidden, KV and FFN widths must be multiples of 64";
     if (c.n_heads / c.n_kv_heads > 8) return "more than 8 query heads per KV head";
-    for (const Layer& Y : m->layers)
+    for (const Layer& Y : m->layers) {
         for (const tmq_tensor* t : {Y.o, Y.gate, Y.up, Y.down})
             if (t->dev.type == TMQ_TYPE_Q8_0) return "Q8_0 attn_output / FFN weights";
+        for (const tmq_tensor* t : {Y.q, Y.k})
+            if (t->dev.type == TMQ_TYPE_Q8_0) return "Q8_0 attn_q / attn_k weights";
+    }
     return nullptr;
 }
 
@@ -418,7 +428,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
     Prefill& P = m->pf;
     const tmq_model_config& c = m->cfg;
     const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM, I = c.inter, L = c.n_layers;
-    const int T_pad = (T + 31) & ~31;
+    const int T_pad = (T + 127) & ~127;  // whole 128-token GEMM tiles
     hipStream_t s = m->ctx->stream;
     auto fv = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
     auto act = [&](int mode, int set, const float* x, const float* w, int n) {
@@ -444,12 +454,10 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.p0 = p0;
         g.split = 1;
         g.rows = W.rows;
-        g.wa = W.hi;
-        g.wb = W.lo;
+        g.w = W.d;
         g.rw_c = W.csum;
         g.rw_t = W.tsum;
-        g.xc = P.in[set].hi;
-        g.xe = P.in[set].lo;
+        g.x = P.in[set].d;
         g.tx_c = P.in[set].csum;
         g.tx_t = P.in[set].tsum;
         g.xs = P.xs[set];
@@ -494,7 +502,25 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.kc = m->kc + (size_t)l * c.max_seq * KV;
         g.vc = m->vc + (size_t)l * c.max_seq * KV;
         g.rope = m->rope;
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, 4, s));
+        g.part = P.part;  // Q8_0 V tiles (the down projection's sums were consumed above)
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[0], s));
+        if (Y.v->dev.type == TMQ_TYPE_Q8_0) {
+            TmqPfVFold vf{};
+            vf.part = P.part;
+            vf.rw_c = W.qkv.csum;
+            vf.tx_c = P.in[0].csum;
+            vf.xs = P.xs[0];
+            vf.row_scale = Y.v->dev.row_scale;
+            vf.bias = fv(Y.bv);
+            vf.vc = g.vc;
+            vf.rows = KV;
+            vf.row0 = H + KV;
+            vf.nt = H / TMQ_PF_CHUNK;
+            vf.T = T;
+            vf.T_pad = T_pad;
+            vf.p0 = p0;
+            LAUNCH_TRY(tmq_launch_pf_vfold(vf, s));
+        }
         // attention over positions 0 .. p0+t
         TmqPfAttn at{};
         at.q = P.qb;
@@ -513,7 +539,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.seg[0] = pf_seg(Y.o, 0, nullptr);
         g.x_res = P.x0;
         g.x_out = P.x1;
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, 4, s));
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[1], s));
         // ffn_norm, gate/up + SwiGLU
         TmqPfAct a2 = act(TMQ_PF_NORM, 2, P.x1, m->fvec + Y.ffn_norm, H);
         a2.zero_bits = P.max_bits;
@@ -525,7 +551,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.seg[1] = pf_seg(Y.up, I, nullptr);
         g.s_out = P.s;
         g.max_bits = P.max_bits;
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, 8, s));
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[2], s));
         // down projection, split over K; finalised by the next layer's input
         TmqPfAct a3 = act(TMQ_PF_SILU, 3, P.s, nullptr, I);
         a3.max_bits = P.max_bits;
@@ -533,7 +559,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g = gemm(TMQ_PF_PART, W.dn, 3);
         g.split = P.dn_split;
         g.part = P.part;
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, 4, s));
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[3], s));
     }
     if (last) {
         const Layer& Z = m->layers[L - 1];
@@ -556,11 +582,11 @@ int pf_prompt(tmq_model* m, int n, int* done) {
     *done = 0;
     const int qpk = m->cfg.n_heads / m->cfg.n_kv_heads;
     int lim = n;
-    while (lim > 0 && tmq_pf_attn_lds(qpk, lim) > 159 * 1024) lim--;
+    while (lim > 0 && tmq_pf_attn_lds(qpk, lim) > 126 * 1024) lim--;
     if (lim < 2) return 0;
     int rc;
     if (!m->pf.built && (rc = pf_build_weights(m))) return rc;
-    const int chunk = (std::min(m->prefill_chunk, lim) + 31) & ~31;
+    const int chunk = (std::min(m->prefill_chunk, lim) + 127) & ~127;
     if ((rc = pf_build_buffers(m, chunk))) return rc;
     for (int p0 = 0; p0 < lim; p0 += chunk) {
         const int T = std::min(chunk, lim - p0);

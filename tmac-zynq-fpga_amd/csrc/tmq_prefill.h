@@ -27,15 +27,26 @@
 
 #define TMQ_PF_CHUNK 64  // columns per correction chunk (= one Q8_0 tile)
 
-// Digit operand planes of one K-wide matrix: [rows][K] int8 each, plus the
+// Digit operand planes of one matrix of `rows` rows (weight rows or
+// tokens, a multiple of 32) and K columns (a multiple of 64), stored
+// fragment-major: the MFMA operand of 32 rows x 32 columns for one digit is
+// 1 KiB contiguous, lane l's 16 bytes at l*16 holding row 32b + (l & 31),
+// columns 32s + 16*(l >> 5) .. +15.  Fragment (b, s, d) (d = 0: hi, 1: lo)
+// starts at ((b * K/32 + s) * 2 + d) * 1024, so the 2*KC fragments of
+// KC consecutive column steps of one block are contiguous.  Plus the
 // chunk and total sums of (v - 128) per row.
 struct TmqPfPlanes {
-    int8_t* hi;      // a / c
-    int8_t* lo;      // b / e
+    int8_t* d;       // rows * K * 2 bytes
     int32_t* csum;   // [rows][K/64]
     int32_t* tsum;   // [rows]
     int32_t rows, K;
 };
+#if defined(__HIPCC__)
+__host__ __device__ __forceinline__ size_t tmq_pf_off(int row, int col, int K, int digit) {
+    const int b = row >> 5, s = col >> 5, lane = (row & 31) + 32 * ((col >> 4) & 1);
+    return ((((size_t)b * (K >> 5) + s) * 2 + digit) * 64 + lane) * 16 + (col & 15);
+}
+#endif
 
 // Split-K digit sums of one GEMM, finalised by the consumer:
 //   acc = sum_s part[s][t][row] + 128*(rw[row] + tx[t]) + 16384*K
@@ -95,12 +106,10 @@ enum {
 struct TmqPfGemm {
     int32_t mode, K, T, T_pad, p0, split, gu_rows, nseg;
     int32_t rows, pad_;        // rows of the plane set (GU: 2 * gu_rows)
-    const int8_t* wa;          // weight digit planes [rows][K]
-    const int8_t* wb;
+    const int8_t* w;           // weight digit planes (fragment-major)
     const int32_t* rw_c;       // [rows][K/64]
     const int32_t* rw_t;       // [rows]
-    const int8_t* xc;          // activation digit planes [T_pad][K]
-    const int8_t* xe;
+    const int8_t* x;           // activation digit planes (fragment-major, T_pad rows)
     const int32_t* tx_c;       // [T_pad][K/64]
     const int32_t* tx_t;       // [T_pad]
     const float* xs;           // [T_pad]
@@ -117,8 +126,21 @@ struct TmqPfGemm {
     // GU
     float* s_out;              // [T][gu_rows]
     uint32_t* max_bits;        // [T]
-    // PART
+    // PART; QKV: the Q8_0 segment's per-tile sums [K/64][seg rows][T_pad]
     int64_t* part;             // [split][T_pad][rows]
+};
+
+// Q8_0 rows of a QKV GEMM (the per-tile digit sums it left in `part`)
+// folded into values (sim/tmac_gguf.cpp:1075-1076) and stored as V cache rows.
+struct TmqPfVFold {
+    const int64_t* part;       // [nt][rows][T_pad]
+    const int32_t* rw_c;       // plane-set rows (row0 + r) x nt
+    const int32_t* tx_c;       // [T_pad][nt]
+    const float* xs;           // [T_pad]
+    const float* row_scale;    // [rows]
+    const float* bias;         // [rows] or null
+    float* vc;                 // this layer's V cache [max_pos][rows]
+    int32_t rows, row0, nt, T, T_pad, p0;
 };
 
 // Attention of T consecutive positions p0.. (one workgroup per token and KV
@@ -161,11 +183,12 @@ __device__ __forceinline__ float tmq_pf_fin(const TmqPfPart& D, int t, int r) {
 #endif
 
 // Launchers: tmq_kernels.hip (operand planes) and tmq_prefill.hip.
-int tmq_launch_pf_wdigits(const TmqTensorDev& t, int8_t* hi, int8_t* lo, int K, int row0, hipStream_t s);
-int tmq_launch_pf_rowsums(const int8_t* hi, const int8_t* lo, int rows, int K, int32_t* csum, int32_t* tsum,
-                          hipStream_t s);
+int tmq_launch_pf_wdigits(const TmqTensorDev& t, int8_t* planes, int K, int row0, hipStream_t s);
+int tmq_launch_pf_rowsums(const TmqPfPlanes& p, hipStream_t s);
 int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s);
-int tmq_launch_pf_gemm(const TmqPfGemm& g, int waves, hipStream_t s);
+// tile: 0 = 128 rows x 128 tokens per workgroup, 1 = 64 x 128, 2 = 128 x 64
+int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s);
 int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);
+int tmq_launch_pf_vfold(const TmqPfVFold& f, hipStream_t s);
 size_t tmq_pf_attn_lds(int qpk, int npos);

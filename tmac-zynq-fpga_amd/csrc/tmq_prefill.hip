@@ -2,14 +2,16 @@
 // the digit GEMM on int8 MFMA with its fused epilogues, the attention of a
 // block of positions, and the hand-over to the decode engine.
 //
-// GEMM mapping (v_mfma_i32_32x32x32_i8, 32 rows x 32 tokens x 32 columns):
-// a wave owns two 32-row blocks and one 32-token block; the waves of a
-// workgroup take consecutive token blocks of the same rows.  Lane l holds,
-// for a 32x32x32 step, 16 bytes of row (l & 31) at columns 16*(l >> 5)..+15
-// of both operands (rows of the weight planes, tokens of the activation
-// planes, each K-contiguous); accumulator element v of lane l is row
-// 8*(v/4) + 4*(l/32) + v%4 of the block, token l & 31.  Per block three
-// int32 accumulators hold S(a,c), S(a,e)+S(b,c) and S(b,e).
+// GEMM (v_mfma_i32_32x32x32_i8, 32 rows x 32 tokens x 32 columns per
+// instruction): both operands are fragment-major digit planes, so every MFMA
+// operand is a contiguous 1 KiB block.  A workgroup (4 waves) owns a tile of
+// row blocks x token blocks; per stage of KC column steps it copies the
+// tile's fragments straight from global memory into LDS (one
+// global_load_lds_dwordx4 per fragment and wave, no registers), two stages
+// in flight.  Each wave multiplies two row blocks by one or two token
+// blocks; per (row block, token block) three int32 accumulators hold
+// S(a,c), S(a,e)+S(b,c) and S(b,e).  Accumulator element v of lane l is
+// row 8*(v/4) + 4*(l/32) + v%4 of its block, token l & 31.
 #include <hip/hip_runtime.h>
 
 #include "tmq_device.h"
@@ -20,188 +22,323 @@ namespace {
 
 typedef int tmq_v4i __attribute__((ext_vector_type(4)));
 typedef int tmq_v16i __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(1))) const tmq_v4i gv4i;
+typedef __attribute__((address_space(3))) int8_t lds_i8;
 
-__device__ __forceinline__ tmq_v4i ldq(const int8_t* p) { return *(const gv4i*)p; }
+// tmq_expf with its 2^(i/32) table in LDS
+struct Exp2TabLds {
+    const uint64_t* p;
+    __device__ uint64_t operator()(int i) const { return p[i]; }
+};
+
 __device__ __forceinline__ tmq_v16i mfma(tmq_v4i a, tmq_v4i b, tmq_v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+// 65536*S(a,c) + 256*(S(a,e)+S(b,c)) + S(b,e) + c, formed in fp64: every
+// term and partial sum is an integer below 2^53, so the value is exact
+__device__ __forceinline__ double digits_f64(int sac, int smid, int sbe, double c) {
+    return __builtin_fma((double)sac, 65536.0, __builtin_fma((double)smid, 256.0, (double)sbe + c));
 }
 // row (within a 32x32 block) of accumulator element v of lane l
 __device__ __forceinline__ int blk_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
-struct Frags {
-    tmq_v4i a0, b0, a1, b1, c, e;
+// Workgroup tiles: NWR x NWT waves, each wave 2 row blocks x WTB token
+// blocks; NBUF stage buffers of KC column steps in a ring, NBUF-1 stages in
+// flight (the copies' latency is hidden behind NBUF-1 stages of MFMA).
+template <int TILE> struct Tile;
+template <> struct Tile<0> { static constexpr int NWR = 2, NWT = 2, WTB = 2, NBUF = 4; };  // 128 rows x 128 tokens
+template <> struct Tile<1> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBUF = 3; };  // 64 x 128, 2 per CU
+template <> struct Tile<2> { static constexpr int NWR = 2, NWT = 2, WTB = 1, NBUF = 6; };  // 128 x 64
+constexpr int KC = 2;  // column steps (of 32) per stage
+
+template <int TILE>
+struct TileGeo {
+    static constexpr int NRB = 2 * Tile<TILE>::NWR;                    // row blocks per workgroup
+    static constexpr int NTB = Tile<TILE>::NWT * Tile<TILE>::WTB;      // token blocks per workgroup
+    static constexpr int FRAGS = (NRB + NTB) * KC * 2;                 // 1 KiB fragments per stage
+    static constexpr int FPW = FRAGS / 4;                              // per wave
+    static constexpr int STAGE = FRAGS * 1024;
+    static constexpr int NBUF = Tile<TILE>::NBUF;
+    static_assert((NBUF - 1) * FPW <= 63, "vmcnt holds 6 bits");
 };
-__device__ __forceinline__ Frags load_frags(const int8_t* pa0, const int8_t* pb0, const int8_t* pa1,
-                                            const int8_t* pb1, const int8_t* pc, const int8_t* pe, int ko) {
-    Frags f;
-    f.a0 = ldq(pa0 + ko);
-    f.b0 = ldq(pb0 + ko);
-    f.a1 = ldq(pa1 + ko);
-    f.b1 = ldq(pb1 + ko);
-    f.c = ldq(pc + ko);
-    f.e = ldq(pe + ko);
-    return f;
-}
-// one 32-column step of both row blocks: 8 MFMAs, the two that add into
-// the middle accumulators a second time issued last
-__device__ __forceinline__ void step(tmq_v16i (&acc)[2][3], const Frags& f) {
-    acc[0][0] = mfma(f.a0, f.c, acc[0][0]);
-    acc[1][0] = mfma(f.a1, f.c, acc[1][0]);
-    acc[0][1] = mfma(f.a0, f.e, acc[0][1]);
-    acc[1][1] = mfma(f.a1, f.e, acc[1][1]);
-    acc[0][2] = mfma(f.b0, f.e, acc[0][2]);
-    acc[1][2] = mfma(f.b1, f.e, acc[1][2]);
-    acc[0][1] = mfma(f.b0, f.c, acc[0][1]);
-    acc[1][1] = mfma(f.b1, f.c, acc[1][1]);
-}
-__device__ __forceinline__ int64_t digit_sum(const tmq_v16i (&acc)[2][3], int bi, int v) {
-    return 65536 * (int64_t)acc[bi][0][v] + 256 * (int64_t)acc[bi][1][v] + (int64_t)acc[bi][2][v];
+
+// s_waitcnt vmcnt(k * FPW): the copies of the k newest stages may still be
+// in flight
+template <int FPW, int NBUF>
+__device__ __forceinline__ void wait_stages(int k) {
+    static_assert(NBUF <= 6, "cases below");
+    switch (k) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FPW) : "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * FPW) : "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NBUF > 3 ? 3 * FPW : 0) : "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NBUF > 4 ? 4 * FPW : 0) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NBUF > 5 ? 5 * FPW : 0) : "memory"); break;
+    }
 }
 
-template <int MODE, int NWV>
-__global__ __launch_bounds__(64 * NWV) void pf_gemm_kernel(TmqPfGemm g) {
+template <int MODE, int TILE>
+__global__ __launch_bounds__(256, TILE == 1 ? 2 : 1) void pf_gemm_kernel(TmqPfGemm g) {
+    typedef Tile<TILE> C;
+    typedef TileGeo<TILE> G;
+    constexpr int WTB = C::WTB;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[G::NBUF][G::STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    int rb[2];
-    if (MODE == TMQ_PF_GU) {
-        rb[0] = 32 * blockIdx.x;
-        rb[1] = g.gu_rows + 32 * blockIdx.x;
-    } else {
-        rb[0] = 64 * blockIdx.x;
-        rb[1] = rb[0] + 32;
+    const int wr = wave / C::NWT, wt = wave % C::NWT;
+    // XCD-aware tile order: workgroups are dispatched to the 8 XCDs round
+    // robin (id % 8); renumber so that consecutive workgroups of one XCD
+    // share an operand in its L2 -- the token tiles of one row tile (the
+    // weight fragments), or, for the long-K down projection, the row tiles
+    // of one token tile (the activation fragments).
+    int bx, by, bz;
+    {
+        const int nx = gridDim.x, ny = gridDim.y, n = nx * ny * gridDim.z;
+        const int id = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+        const int per = n >> 3, rem = n & 7, k = id & 7, sl = id >> 3;
+        const int v = k * per + min(k, rem) + sl;
+        if (MODE == TMQ_PF_PART) {
+            bx = v % nx;
+            by = (v / nx) % ny;
+        } else {
+            by = v % ny;
+            bx = (v / ny) % nx;
+        }
+        bz = v / (ny * nx);
     }
-    const int tb = ((int)blockIdx.y * NWV + wave) * 32;
-    if (tb >= g.T_pad) return;  // wave-uniform; the kernel has no barrier
-    const int li = lane & 31, lk = (lane >> 5) * 16;
-    const int8_t* pa0 = g.wa + (size_t)(rb[0] + li) * g.K + lk;
-    const int8_t* pb0 = g.wb + (size_t)(rb[0] + li) * g.K + lk;
-    const int8_t* pa1 = g.wa + (size_t)(rb[1] + li) * g.K + lk;
-    const int8_t* pb1 = g.wb + (size_t)(rb[1] + li) * g.K + lk;
-    const int8_t* pc = g.xc + (size_t)(tb + li) * g.K + lk;
-    const int8_t* pe = g.xe + (size_t)(tb + li) * g.K + lk;
+    // row block of the workgroup's local row block i; GU: (gate j, up j)
+    // pairs, so that wave wr holds gate rows in its first block and the same
+    // up rows in its second
+    auto rblk = [&](int i) -> int {
+        return MODE == TMQ_PF_GU ? (i & 1) * (g.gu_rows >> 5) + bx * (G::NRB / 2) + (i >> 1) : bx * G::NRB + i;
+    };
+    const int tblk0 = by * G::NTB;
     const int nks = g.K >> 5;
-    const int ks0 = (int)((int64_t)blockIdx.z * nks / g.split), ks1 = (int)((int64_t)(blockIdx.z + 1) * nks / g.split);
-    const int t = tb + li;
+    const int nst_all = nks / KC;
+    const int st0 = (int)((int64_t)bz * nst_all / g.split);
+    const int st1 = (int)((int64_t)(bz + 1) * nst_all / g.split);
+    const int nst = st1 - st0;
 
-    // the tensor of this row tile (QKV: q, k or v; GU: gate for block 0)
+    // runtime segment (QKV): the tile lies inside one tensor
     int si = 0;
     if (MODE == TMQ_PF_QKV) {
-        if (g.nseg > 1 && rb[0] >= g.seg[1].row0) si = 1;
-        if (g.nseg > 2 && rb[0] >= g.seg[2].row0) si = 2;
+        const int r0 = rblk(0) * 32;
+        if (g.nseg > 1 && r0 >= g.seg[1].row0) si = 1;
+        if (g.nseg > 2 && r0 >= g.seg[2].row0) si = 2;
     }
     const TmqPfSeg S = si == 0 ? g.seg[0] : si == 1 ? g.seg[1] : g.seg[2];
+    const bool q8 = MODE == TMQ_PF_QKV && S.q8;
+    const bool hasb = MODE == TMQ_PF_QKV && S.bias != nullptr;
 
-    tmq_v16i acc[2][3];
-    for (int bi = 0; bi < 2; bi++)
-        for (int j = 0; j < 3; j++) acc[bi][j] = tmq_v16i{};
-    float y[2][16];
-
-    if (MODE == TMQ_PF_QKV && S.q8) {
-        // Q8_0: fold every 64-column tile into y in order, in double
-        // (sim/tmac_gguf.cpp:1075-1076); split is 1
-        const int nt = g.K / TMQ_PF_CHUNK;
-        for (int bi = 0; bi < 2; bi++)
-            for (int v = 0; v < 16; v++) y[bi][v] = 0.0f;
-        const double xs = (double)g.xs[t];
-        for (int tile = 0; tile < nt; tile++) {
-            step(acc, load_frags(pa0, pb0, pa1, pb1, pc, pe, tile * 64));
-            step(acc, load_frags(pa0, pb0, pa1, pb1, pc, pe, tile * 64 + 32));
-            const int32_t tx = g.tx_c[(size_t)t * nt + tile];
-            for (int bi = 0; bi < 2; bi++) {
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const int r = rb[bi] + blk_row(v, lane);
-                    const int64_t P = digit_sum(acc, bi, v) +
-                                      128 * ((int64_t)g.rw_c[(size_t)r * nt + tile] + tx) + 16384 * 64;
-                    y[bi][v] = (float)((double)y[bi][v] + ((double)P * xs) * (double)S.row_scale[r - S.row0]);
-                }
-                for (int j = 0; j < 3; j++) acc[bi][j] = tmq_v16i{};
-            }
+    // the epilogue's per-row constants of the workgroup's rows, in LDS:
+    // row_inv (Q8_0: row_scale), sum (w - 128), bias; the exp table (GU)
+    __shared__ float c_inv[G::NRB][32];
+    __shared__ int32_t c_rw[G::NRB][32];
+    __shared__ float c_bias[G::NRB][32];
+    __shared__ uint64_t c_tab[32];
+    if (MODE != TMQ_PF_PART) {
+        for (int idx = threadIdx.x; idx < G::NRB * 32; idx += 256) {
+            const int i = idx >> 5, r = idx & 31;
+            const TmqPfSeg Sg = MODE == TMQ_PF_GU ? ((i & 1) ? g.seg[1] : g.seg[0]) : S;
+            const int row = rblk(i) * 32 + r, rr = row - Sg.row0;
+            c_inv[i][r] = q8 ? Sg.row_scale[rr] : Sg.row_inv[rr];
+            c_rw[i][r] = g.rw_t[row];
+            c_bias[i][r] = hasb ? Sg.bias[rr] : 0.0f;
         }
-        for (int bi = 0; bi < 2; bi++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int rr = rb[bi] + blk_row(v, lane) - S.row0;
-                if (S.bias) y[bi][v] = y[bi][v] + S.bias[rr];
-            }
-    } else {
-        Frags cur = load_frags(pa0, pb0, pa1, pb1, pc, pe, ks0 * 32);
-        for (int ks = ks0; ks < ks1; ks++) {
-            const Frags nxt = load_frags(pa0, pb0, pa1, pb1, pc, pe, (ks + 1 < ks1 ? ks + 1 : ks) * 32);
-            step(acc, cur);
-            cur = nxt;
-        }
-        if (MODE == TMQ_PF_PART) {
-            int64_t* out = g.part + ((size_t)blockIdx.z * g.T_pad + t) * g.rows;
-            for (int bi = 0; bi < 2; bi++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) out[rb[bi] + blk_row(v, lane)] = digit_sum(acc, bi, v);
-            return;
-        }
-        // finalise (sim/tmac_gguf.cpp:1303-1305) + bias (:1595-1597)
-        const double xs = (double)g.xs[t];
-        const int64_t tc = 128 * (int64_t)g.tx_t[t] + 16384 * (int64_t)g.K;
-        for (int bi = 0; bi < 2; bi++) {
-            const TmqPfSeg Sb = (MODE == TMQ_PF_GU && bi == 1) ? g.seg[1] : S;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int r = rb[bi] + blk_row(v, lane), rr = r - Sb.row0;
-                const int64_t a = digit_sum(acc, bi, v) + 128 * (int64_t)g.rw_t[r] + tc;
-                float f = (float)(((double)a * xs) / (double)Sb.row_inv[rr]);
-                if (Sb.bias) f = f + Sb.bias[rr];
-                y[bi][v] = f;
-            }
-        }
+        if (MODE == TMQ_PF_GU && threadIdx.x < 32) c_tab[threadIdx.x] = tmq_math::exp2_tab(threadIdx.x);
     }
-    const bool live = t < g.T;
-
-    if (MODE == TMQ_PF_QKV) {
-        if (!live) return;
-        const int pos = g.p0 + t;
-        for (int bi = 0; bi < 2; bi++) {
+    // stage st -> buffer b: fragment f of FRAGS (run f / 2KC = one row or
+    // token block, KC column steps x 2 digits contiguous on both sides);
+    // wave w issues f = w, w+4, ...  K is a multiple of 32*KC.
+    auto issue = [&](int st, int b) {
+        const int ks = (st0 + st) * KC;
 #pragma unroll
-            for (int v = 0; v < 16; v += 2) {
-                const int rr = rb[bi] + blk_row(v, lane) - S.row0;  // even: (rr, rr+1) is a RoPE pair
-                const float y0 = y[bi][v], y1 = y[bi][v + 1];
-                if (si == 2) {
-                    g.vc[(size_t)pos * g.KV + rr] = y0;
-                    g.vc[(size_t)pos * g.KV + rr + 1] = y1;
-                } else {
-                    // apply_rope (sim/tmac_gguf.cpp:1537-1539)
-                    const float2 cs = g.rope[(size_t)pos * 32 + ((rr & 63) >> 1)];
-                    const float o0 = y0 * cs.x - y1 * cs.y;
-                    const float o1 = y0 * cs.y + y1 * cs.x;
-                    float* dst = si == 0 ? g.q_out + (size_t)t * g.H + rr : g.kc + (size_t)pos * g.KV + rr;
-                    dst[0] = o0;
-                    dst[1] = o1;
+        for (int k = 0; k < G::FPW; k++) {
+            const int f = wave + 4 * k;  // wave-uniform
+            const int run = f / (KC * 2), in = f % (KC * 2);
+            const bool wgt = run < G::NRB;
+            const int8_t* base = wgt ? g.w : g.x;
+            const int blk = wgt ? rblk(run) : tblk0 + run - G::NRB;
+            const int8_t* src = base + ((size_t)blk * nks + ks) * 2048 + (size_t)in * 1024;
+            __builtin_amdgcn_global_load_lds((const void*)(src + lane * 16),
+                                             (lds_i8*)(lds[b] + (size_t)f * 1024), 16, 0, 0);
+        }
+    };
+    auto frag = [&](int b, int run, int kc, int d) -> tmq_v4i {
+        return *(const tmq_v4i*)(lds[b] + ((size_t)(run * KC + kc) * 2 + d) * 1024 + lane * 16);
+    };
+
+    tmq_v16i acc[2][WTB][3];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < WTB; j++)
+#pragma unroll
+            for (int d = 0; d < 3; d++) acc[i][j][d] = tmq_v16i{};
+    const int tw0 = (tblk0 + wt * WTB) * 32;  // first token of the wave
+    double xs_t[WTB], tc_t[WTB];
+#pragma unroll
+    for (int j = 0; j < WTB; j++) {
+        const int t = tw0 + j * 32 + (lane & 31);
+        xs_t[j] = (double)g.xs[t];
+        tc_t[j] = (double)(128 * (int64_t)g.tx_t[t] + 16384 * (int64_t)g.K);
+    }
+
+    for (int st = 0; st < G::NBUF - 1 && st < nst; st++) issue(st, st);
+    for (int st = 0; st < nst; st++) {
+        const int b = st % G::NBUF;
+        // refill the buffer the previous iteration finished with
+        if (st + G::NBUF - 1 < nst) issue(st + G::NBUF - 1, (st + G::NBUF - 1) % G::NBUF);
+        wait_stages<G::FPW, G::NBUF>(min(G::NBUF - 1, nst - 1 - st));
+        // the stage's LDS copies are complete in this wave (vmcnt above);
+        // the barrier makes them complete in all.  A plain s_barrier (the
+        // workgroup fence of __syncthreads would also wait for the next
+        // stage's copies), as asm with a memory clobber so that no LDS
+        // access moves across it.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int ks = (st0 + st) * KC;
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
+            {
+                const tmq_v4i a0 = frag(b, 2 * wr, kc, 0), b0 = frag(b, 2 * wr, kc, 1);
+                const tmq_v4i a1 = frag(b, 2 * wr + 1, kc, 0), b1 = frag(b, 2 * wr + 1, kc, 1);
+#pragma unroll
+                for (int j = 0; j < WTB; j++) {
+                    const int tr = G::NRB + wt * WTB + j;
+                    const tmq_v4i c = frag(b, tr, kc, 0), e = frag(b, tr, kc, 1);
+                    acc[0][j][0] = mfma(a0, c, acc[0][j][0]);
+                    acc[1][j][0] = mfma(a1, c, acc[1][j][0]);
+                    acc[0][j][1] = mfma(a0, e, acc[0][j][1]);
+                    acc[1][j][1] = mfma(a1, e, acc[1][j][1]);
+                    acc[0][j][2] = mfma(b0, e, acc[0][j][2]);
+                    acc[1][j][2] = mfma(b1, e, acc[1][j][2]);
+                    acc[0][j][1] = mfma(b0, c, acc[0][j][1]);
+                    acc[1][j][1] = mfma(b1, c, acc[1][j][1]);
+                }
+            }
+            if (MODE == TMQ_PF_QKV && q8 && (kc & 1)) {
+                // Q8_0: the 64-column tile just completed, as an int64 digit
+                // sum per element, for pf_vfold_kernel
+                const int tile = (ks + kc) >> 1;
+#pragma unroll
+                for (int j = 0; j < WTB; j++) {
+                    const int t = tw0 + j * 32 + (lane & 31);
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        // [tile][row][token]: the 32 tokens of a row are contiguous
+                        int64_t* out = g.part + ((size_t)tile * S.rows + rblk(2 * wr + i) * 32 - S.row0) * g.T_pad + t;
+#pragma unroll
+                        for (int v = 0; v < 16; v++)
+                            out[(size_t)blk_row(v, lane) * g.T_pad] = 65536 * (int64_t)acc[i][j][0][v] +
+                                                                       256 * (int64_t)acc[i][j][1][v] +
+                                                                       (int64_t)acc[i][j][2][v];
+#pragma unroll
+                        for (int d = 0; d < 3; d++) acc[i][j][d] = tmq_v16i{};
+                    }
                 }
             }
         }
-    } else if (MODE == TMQ_PF_O) {
-        if (!live) return;
-        // residual add (sim/tmac_gguf.cpp:1663)
-        for (int bi = 0; bi < 2; bi++)
+        // every wave's reads of buffer b are done (their values fed the
+        // MFMAs above) before the next iteration copies stage st+2 into it
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+
+    if (MODE == TMQ_PF_PART) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const size_t i = (size_t)t * g.rows + rb[bi] + blk_row(v, lane);
-                g.x_out[i] = g.x_res[i] + y[bi][v];
-            }
-    } else if (MODE == TMQ_PF_GU) {
-        // SwiGLU (sim/tmac_gguf.cpp:434-439): gate rows in block 0, the same
-        // up rows in block 1
-        float m = 0.0f;
+        for (int j = 0; j < WTB; j++) {
+            const int t = tw0 + j * 32 + (lane & 31);
+            int64_t* out = g.part + ((size_t)bz * g.T_pad + t) * g.rows;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const float gv = y[0][v];
-            const float sv = (gv / (1.0f + tmq_math::tmq_expf(-gv))) * y[1][v];
-            if (live) g.s_out[(size_t)t * g.gu_rows + rb[0] + blk_row(v, lane)] = sv;
-            m = fmaxf(m, fabsf(sv));
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    out[rblk(2 * wr + i) * 32 + blk_row(v, lane)] = 65536 * (int64_t)acc[i][j][0][v] +
+                                                                    256 * (int64_t)acc[i][j][1][v] +
+                                                                    (int64_t)acc[i][j][2][v];
         }
-        m = fmaxf(m, __shfl_xor(m, 32));
-        if (live && lane < 32)
-            __hip_atomic_fetch_max(g.max_bits + t, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (MODE == TMQ_PF_QKV && q8) return;  // pf_vfold_kernel finishes these rows
+
+    // element v of block (i, j), finalised (sim/tmac_gguf.cpp:1303-1305) +
+    // bias (:1595-1597)
+    auto fin = [&](int i, int j, int v) -> float {
+        const int li = 2 * wr + i, rb = blk_row(v, lane);
+        const double a = digits_f64(acc[i][j][0][v], acc[i][j][1][v], acc[i][j][2][v],
+                                    tc_t[j] + (double)(128 * c_rw[li][rb]));
+        float f = (float)((a * xs_t[j]) / (double)c_inv[li][rb]);
+        if (hasb) f = f + c_bias[li][rb];
+        return f;
+    };
+
+    // elements v = 4q .. 4q+3 of a lane are 4 consecutive rows: one float4
+#pragma unroll
+    for (int j = 0; j < WTB; j++) {
+        const int t = tw0 + j * 32 + (lane & 31);
+        const bool live = t < g.T;
+        if (MODE == TMQ_PF_QKV) {
+            if (!live) continue;
+            const int pos = g.p0 + t;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int rr = rblk(2 * wr + i) * 32 + blk_row(4 * q, lane) - S.row0;  // pairs (rr, rr+1), (rr+2, rr+3)
+                    float o[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) o[k] = fin(i, j, 4 * q + k);
+                    if (si != 2) {
+                        // apply_rope (sim/tmac_gguf.cpp:1537-1539)
+                        const float4 cs = *(const float4*)(g.rope + (size_t)pos * 32 + ((rr & 63) >> 1));
+#pragma unroll
+                        for (int k = 0; k < 2; k++) {
+                            const float y0 = o[2 * k], y1 = o[2 * k + 1];
+                            const float c = k ? cs.z : cs.x, sn = k ? cs.w : cs.y;
+                            o[2 * k] = y0 * c - y1 * sn;
+                            o[2 * k + 1] = y0 * sn + y1 * c;
+                        }
+                    }
+                    float* dst = si == 0   ? g.q_out + (size_t)t * g.H + rr
+                                 : si == 1 ? g.kc + (size_t)pos * g.KV + rr
+                                           : g.vc + (size_t)pos * g.KV + rr;
+                    *(float4*)dst = make_float4(o[0], o[1], o[2], o[3]);
+                }
+            }
+        } else if (MODE == TMQ_PF_O) {
+            if (!live) continue;
+            // residual add (sim/tmac_gguf.cpp:1663)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const size_t o = (size_t)t * g.rows + rblk(2 * wr + i) * 32 + blk_row(4 * q, lane);
+                    const float4 xr = *(const float4*)(g.x_res + o);
+                    *(float4*)(g.x_out + o) = make_float4(xr.x + fin(i, j, 4 * q), xr.y + fin(i, j, 4 * q + 1),
+                                                          xr.z + fin(i, j, 4 * q + 2), xr.w + fin(i, j, 4 * q + 3));
+                }
+        } else if (MODE == TMQ_PF_GU) {
+            // SwiGLU (sim/tmac_gguf.cpp:434-439): gate rows in block 0, the
+            // same up rows in block 1
+            float m = 0.0f;
+            const int j0 = rblk(2 * wr) * 32;
+            const Exp2TabLds tab{c_tab};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float sv[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float gv = fin(0, j, 4 * q + k);
+                    sv[k] = (gv / (1.0f + tmq_math::tmq_expf_tab(-gv, tab))) * fin(1, j, 4 * q + k);
+                    m = fmaxf(m, fabsf(sv[k]));
+                }
+                if (live)
+                    *(float4*)(g.s_out + (size_t)t * g.gu_rows + j0 + blk_row(4 * q, lane)) =
+                        make_float4(sv[0], sv[1], sv[2], sv[3]);
+            }
+            m = fmaxf(m, __shfl_xor(m, 32));
+            if (live && lane < 32)
+                __hip_atomic_fetch_max(g.max_bits + t, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -209,28 +346,31 @@ __global__ __launch_bounds__(64 * NWV) void pf_gemm_kernel(TmqPfGemm g) {
 // head g: the decode engine's chains (attn_kernel) per query -- scores
 // summed over d in order and /8, max, exp terms summed over positions in
 // order, log via fp64, weights, the context summed over positions in order.
+// The query rows are wave-uniform and read through the scalar cache.
+typedef __attribute__((address_space(4))) const float cf32;
 __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
     extern __shared__ float lds[];
     __shared__ float stat[2][8];
-    const int t = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
+    __shared__ uint64_t tab[32];
+    __shared__ __attribute__((aligned(16))) float vb2[2][64 * 64];  // V rows, double-buffered
+    // the longest (latest) positions first
+    const int t = a.T - 1 - (int)blockIdx.x, g = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
     const int qpk = a.n_heads / a.n_kv, KV = a.n_kv * 64, H = a.n_heads * 64;
     const int np = a.p0 + t + 1, npad = (np + 3) & ~3;
     const int wv = tid >> 6, ln = tid & 63;
-    float* q = lds;                  // [qpk][64]
-    float* sc = q + qpk * 64;        // [qpk][npad]
+    float* sc = lds;                 // [qpk][npad]
     float* ex = sc + qpk * npad;     // [qpk][npad]
-    float* vb = ex + qpk * npad;     // [64][64]
     const float* kb = a.kc + g * 64;
     const float* vbase = a.vc + g * 64;
-    for (int i = tid; i < qpk * 64; i += nt) q[i] = a.q[(size_t)t * H + g * qpk * 64 + i];
-    __syncthreads();
+    const cf32* qg = (const cf32*)(a.q + (size_t)t * H + g * qpk * 64);
+    if (tid < 32) tab[tid] = tmq_math::exp2_tab(tid);
     for (int p = tid; p < np; p += nt) {
         float4 kk[16];
         const float4* kp = (const float4*)(kb + (size_t)p * KV);
 #pragma unroll
         for (int i = 0; i < 16; i++) kk[i] = kp[i];
         for (int h = 0; h < qpk; h++) {
-            const float* qh = q + h * 64;
+            const cf32* qh = qg + h * 64;
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -250,9 +390,10 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
         if (ln == 0) stat[0][wv] = m;
     }
     __syncthreads();
+    const Exp2TabLds et{tab};
     for (int i = tid; i < qpk * np; i += nt) {
         const int h = i / np, p = i - h * np;
-        ex[h * npad + p] = tmq_math::tmq_expf(sc[h * npad + p] - stat[0][h]);
+        ex[h * npad + p] = tmq_math::tmq_expf_tab(sc[h * npad + p] - stat[0][h], et);
     }
     __syncthreads();
     if (wv < qpk && ln == 0) {
@@ -277,24 +418,70 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
     __syncthreads();
     for (int i = tid; i < qpk * np; i += nt) {
         const int h = i / np, p = i - h * np;
-        ex[h * npad + p] = tmq_math::tmq_expf(sc[h * npad + p] - stat[1][h]);
+        ex[h * npad + p] = tmq_math::tmq_expf_tab(sc[h * npad + p] - stat[1][h], et);
+    }
+    // context, 64 positions per chunk; the next chunk's V rows are loaded
+    // into registers while the current one is summed (512 threads x 2 float4
+    // = one chunk)
+    {
+        const int nr = min(64, np);
+        for (int i = tid; i < nr * 16; i += nt) {
+            const int pr = i >> 4, q4 = i & 15;
+            *(float4*)&vb2[0][pr * 64 + 4 * q4] = *(const float4*)(vbase + (size_t)pr * KV + 4 * q4);
+        }
     }
     __syncthreads();
     float acc = 0.0f;
+    int buf = 0;
     for (int c0 = 0; c0 < np; c0 += 64) {
-        const int nr = min(64, np - c0);
-        for (int i = tid; i < nr * 16; i += nt) {
-            const int pr = i >> 4, q4 = i & 15;
-            *(float4*)&vb[pr * 64 + 4 * q4] = *(const float4*)(vbase + (size_t)(c0 + pr) * KV + 4 * q4);
+        const int nr = min(64, np - c0), c1 = c0 + 64, nr1 = min(64, np - c1);
+        float4 pre[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = tid + j * 512, pr = i >> 4, q4 = i & 15;
+            if (pr < nr1) pre[j] = *(const float4*)(vbase + (size_t)(c1 + pr) * KV + 4 * q4);
         }
-        __syncthreads();
         if (wv < qpk) {
             const float* e = ex + wv * npad + c0;
-            for (int pr = 0; pr < nr; pr++) acc += e[pr] * vb[pr * 64 + ln];
+            const float* vv = vb2[buf];
+            int pr = 0;
+            for (; pr + 4 <= nr; pr += 4) {
+                const float4 e4 = *(const float4*)(e + pr);
+                acc += e4.x * vv[pr * 64 + ln];
+                acc += e4.y * vv[(pr + 1) * 64 + ln];
+                acc += e4.z * vv[(pr + 2) * 64 + ln];
+                acc += e4.w * vv[(pr + 3) * 64 + ln];
+            }
+            for (; pr < nr; pr++) acc += e[pr] * vv[pr * 64 + ln];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = tid + j * 512, pr = i >> 4, q4 = i & 15;
+            if (pr < nr1) *(float4*)&vb2[buf ^ 1][pr * 64 + 4 * q4] = pre[j];
         }
         __syncthreads();
+        buf ^= 1;
     }
     if (wv < qpk) a.ctx[(size_t)t * H + (g * qpk + wv) * 64 + ln] = acc;
+}
+
+// One (token, Q8_0 row) of a QKV GEMM: the tiles' digit sums + corrections
+// folded in order in double, plus the bias, stored into the V cache.
+__global__ __launch_bounds__(256) void pf_vfold_kernel(TmqPfVFold f) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= f.T * f.rows) return;
+    const int r = i / f.T, t = i - r * f.T;
+    const int32_t* rw = f.rw_c + (size_t)(f.row0 + r) * f.nt;
+    const int32_t* tx = f.tx_c + (size_t)t * f.nt;
+    const double xs = (double)f.xs[t], rs = (double)f.row_scale[r];
+    float y = 0.0f;
+    for (int c = 0; c < f.nt; c++) {
+        const int64_t p = f.part[((size_t)c * f.rows + r) * f.T_pad + t] + 128 * ((int64_t)rw[c] + tx[c]) +
+                          16384 * TMQ_PF_CHUNK;
+        y = (float)((double)y + ((double)p * xs) * rs);
+    }
+    if (f.bias) y = y + f.bias[r];
+    f.vc[(size_t)(f.p0 + t) * f.rows + r] = y;
 }
 
 // The decode engine's residual state after the prefill's last token.
@@ -306,42 +493,54 @@ __global__ __launch_bounds__(256) void pf_handoff_kernel(TmqPfHandoff h) {
     if (threadIdx.x == 0) *h.xs_slot = h.dn.xs[h.t];
 }
 
-template <int MODE>
-int launch_gemm(const TmqPfGemm& g, int waves, hipStream_t s) {
-    const int rt = MODE == TMQ_PF_GU ? g.gu_rows / 32 : g.rows / 64;
-    const dim3 grid(rt, (g.T_pad + 32 * waves - 1) / (32 * waves), g.split);
-    if (waves == 4) hipLaunchKernelGGL((pf_gemm_kernel<MODE, 4>), grid, dim3(256), 0, s, g);
-    else if (waves == 8) hipLaunchKernelGGL((pf_gemm_kernel<MODE, 8>), grid, dim3(512), 0, s, g);
-    else return (int)hipErrorInvalidValue;
+template <int MODE, int TILE>
+int launch_gemm(const TmqPfGemm& g, hipStream_t s) {
+    typedef TileGeo<TILE> G;
+    const int rt = MODE == TMQ_PF_GU ? g.gu_rows / (16 * G::NRB) : g.rows / (32 * G::NRB);
+    const dim3 grid(rt, (g.T_pad + 32 * G::NTB - 1) / (32 * G::NTB), g.split);
+    hipLaunchKernelGGL((pf_gemm_kernel<MODE, TILE>), grid, dim3(256), 0, s, g);
     return (int)hipGetLastError();
+}
+template <int MODE>
+int launch_tile(const TmqPfGemm& g, int tile, hipStream_t s) {
+    switch (tile) {
+    case 0: return launch_gemm<MODE, 0>(g, s);
+    case 1: return launch_gemm<MODE, 1>(g, s);
+    case 2: return launch_gemm<MODE, 2>(g, s);
+    }
+    return (int)hipErrorInvalidValue;
 }
 
 }  // namespace
 
 size_t tmq_pf_attn_lds(int qpk, int npos) {
     const size_t npad = ((size_t)npos + 3) & ~(size_t)3;
-    return sizeof(float) * ((size_t)qpk * 64 + 2 * (size_t)qpk * npad + 64 * 64);
+    return sizeof(float) * 2 * (size_t)qpk * npad;
 }
 
-int tmq_launch_pf_gemm(const TmqPfGemm& g, int waves, hipStream_t s) {
-    // shapes the kernel assumes: 64-column chunks, 32-token blocks, 64-row
-    // tiles (GU: 32-row gate/up blocks), one split for fused epilogues
-    if (g.K <= 0 || g.K % TMQ_PF_CHUNK || g.T_pad % 32 || g.T > g.T_pad || g.split < 1 || g.split > g.K / 32)
+int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
+    // shapes the kernel assumes: 64-column chunks, whole token tiles of the
+    // operand planes, whole row tiles (GU: gate/up tiles of NRB/2 blocks),
+    // a split count no larger than the stages, one split for fused epilogues
+    if (tile < 0 || tile > 2) return (int)hipErrorInvalidValue;
+    const int nrb = tile == 1 ? 2 : 4, ntb = tile == 2 ? 2 : 4;
+    if (g.K <= 0 || g.K % (32 * KC) || g.T_pad % (32 * ntb) || g.T > g.T_pad || g.split < 1 ||
+        g.split > g.K / (32 * KC))
         return (int)hipErrorInvalidValue;
     if (g.mode != TMQ_PF_PART && g.split != 1) return (int)hipErrorInvalidValue;
+    if (g.mode == TMQ_PF_GU) {
+        if (g.gu_rows % (16 * nrb) || g.rows != 2 * g.gu_rows) return (int)hipErrorInvalidValue;
+    } else if (g.rows % (32 * nrb)) {
+        return (int)hipErrorInvalidValue;
+    }
+    if (g.mode == TMQ_PF_QKV)
+        for (int i = 0; i < g.nseg; i++)
+            if (g.seg[i].row0 % (32 * nrb) || (g.seg[i].q8 && !g.part)) return (int)hipErrorInvalidValue;
     switch (g.mode) {
-    case TMQ_PF_QKV:
-        if (g.rows % 64) return (int)hipErrorInvalidValue;
-        return launch_gemm<TMQ_PF_QKV>(g, waves, s);
-    case TMQ_PF_O:
-        if (g.rows % 64) return (int)hipErrorInvalidValue;
-        return launch_gemm<TMQ_PF_O>(g, waves, s);
-    case TMQ_PF_GU:
-        if (g.gu_rows % 32 || g.rows != 2 * g.gu_rows) return (int)hipErrorInvalidValue;
-        return launch_gemm<TMQ_PF_GU>(g, waves, s);
-    case TMQ_PF_PART:
-        if (g.rows % 64) return (int)hipErrorInvalidValue;
-        return launch_gemm<TMQ_PF_PART>(g, waves, s);
+    case TMQ_PF_QKV: return launch_tile<TMQ_PF_QKV>(g, tile, s);
+    case TMQ_PF_O: return launch_tile<TMQ_PF_O>(g, tile, s);
+    case TMQ_PF_GU: return launch_tile<TMQ_PF_GU>(g, tile, s);
+    case TMQ_PF_PART: return launch_tile<TMQ_PF_PART>(g, tile, s);
     }
     return (int)hipErrorInvalidValue;
 }
@@ -353,16 +552,22 @@ int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void*)pf_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           160 * 1024 - 1024);
+                                           160 * 1024 - 34 * 1024);
         if (e != hipSuccess) return (int)e;
         attr = true;
     }
-    if (lds > 160 * 1024 - 1024) return (int)hipErrorInvalidValue;
+    if (lds > 160 * 1024 - 34 * 1024) return (int)hipErrorInvalidValue;  // + 32 KiB static V buffers
     hipLaunchKernelGGL(pf_attn_kernel, dim3(a.T, a.n_kv), dim3(512), lds, s, a);
     return (int)hipGetLastError();
 }
 
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s) {
     hipLaunchKernelGGL(pf_handoff_kernel, dim3(1), dim3(256), 0, s, h);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_pf_vfold(const TmqPfVFold& f, hipStream_t s) {
+    const int n = f.T * f.rows;
+    hipLaunchKernelGGL(pf_vfold_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
     return (int)hipGetLastError();
 }
