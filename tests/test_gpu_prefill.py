@@ -83,3 +83,27 @@ def test_prefill_errors(model):
     import tmq
     with pytest.raises(tmq.TmqError):
         model.set_prefill(-1)
+
+
+@pytest.mark.parametrize("chunk", [0, 512, 8])
+def test_prompt_matches_reference(model, chunk):
+    """the compiled reference's own process_prompt over a 24-token prompt
+    (tests/golden/model_prompt.npz): hidden state, logits and greedy tokens,
+    one token at a time (0), in one batch (512) and in chunks of 8"""
+    from conftest import load_golden
+    g = load_golden("model_prompt.npz")
+    assert int(g["model_seed"]) == MODEL_SEED
+    print(f"[prefill] reference prompt, chunk {chunk}", flush=True)
+    model.set_prefill(chunk)
+    model.prompt(g["prompt"])
+    h = model.hidden()
+    exact = np.mean(h.view(np.uint32) == g["hidden"].view(np.uint32))
+    print(f"[prefill] hidden after the prompt: {exact:.4f} bit-exact", flush=True)
+    np.testing.assert_allclose(h, g["hidden"], rtol=0, atol=1e-5 * np.abs(g["hidden"]).max())
+    lg = model.logits()
+    top = np.lexsort((np.arange(lg.size), -lg))[:10]
+    assert top.tolist() == g["top_ids"][0].tolist()
+    np.testing.assert_allclose(lg[top], g["top_vals"][0], rtol=0, atol=1e-3)
+    np.testing.assert_allclose(lg[::64], g["logits_sub"], rtol=0, atol=1e-3)
+    out = model.generate(len(g["tokens"]))
+    assert out.tolist() == g["tokens"].tolist()

@@ -110,3 +110,25 @@ def test_golden_model_fixture():
     d = row[:, 0:2].copy().view(np.float16).astype(np.float32)
     q = row[:, 2:].view(np.int8).astype(np.float32)
     assert np.array_equal((q * d).reshape(-1).view(np.uint32), g["layers0"][0].view(np.uint32))
+
+
+def test_golden_prompt_fixture():
+    """tests/golden/model_prompt.npz (the reference's process_prompt over 24
+    seeded tokens): structure, the seeds it records, and self-consistency"""
+    import numpy as np
+    from conftest import load_golden
+    g = load_golden("model_prompt.npz")
+    assert int(g["model_seed"]) == 2024
+    exp = np.random.Generator(np.random.PCG64(11)).integers(0, 151936, size=24)
+    assert g["prompt"].tolist() == exp.tolist()
+    assert g["hidden"].shape == (896,) and np.isfinite(g["hidden"]).all()
+    assert g["top_ids"].shape == (9, 10) and g["top_vals"].shape == (9, 10)
+    assert g["logits_sub"].shape == (len(range(0, 151936, 64)),)
+    assert g["tokens"].shape == (8,)
+    # greedy: each generated token is the best of the step before it
+    assert g["tokens"].tolist() == g["top_ids"][:8, 0].tolist()
+    assert (np.diff(g["top_vals"], axis=1) <= 0).all()
+    # a top-10 logit at a multiple of 64 is also in the every-64th sample
+    for i, v in zip(g["top_ids"][0], g["top_vals"][0]):
+        if i % 64 == 0:
+            assert g["logits_sub"][i // 64] == v

@@ -351,7 +351,8 @@ int pf_build_weights(tmq_model* m) {
     return 0;
 }
 
-// Buffers of one chunk of `chunk` tokens (a multiple of 128).
+// Buffers of a chunk of up to `chunk` tokens (a multiple of 128: whole
+// GEMM token tiles).
 int pf_build_buffers(tmq_model* m, int chunk) {
     Prefill& P = m->pf;
     if (P.amem && P.chunk == chunk) return 0;
@@ -586,8 +587,8 @@ int pf_prompt(tmq_model* m, int n, int* done) {
     if (lim < 2) return 0;
     int rc;
     if (!m->pf.built && (rc = pf_build_weights(m))) return rc;
-    const int chunk = (std::min(m->prefill_chunk, lim) + 127) & ~127;
-    if ((rc = pf_build_buffers(m, chunk))) return rc;
+    const int chunk = std::min(m->prefill_chunk, lim);
+    if ((rc = pf_build_buffers(m, (chunk + 127) & ~127))) return rc;
     for (int p0 = 0; p0 < lim; p0 += chunk) {
         const int T = std::min(chunk, lim - p0);
         if ((rc = pf_run_chunk(m, p0, T, p0 + T >= lim))) return rc;
