@@ -231,6 +231,20 @@ int tmq_model_tokens(tmq_model* m, int first, int n, int32_t* out);
 /* current hidden state (hidden floats) */
 int tmq_model_hidden(tmq_model* m, float* out);
 
+/* The --perf pipeline profile (sim/tmac_gguf.cpp:17-134, the PROFILE_SCOPE
+ * spans of forward_layer_with_cache and get_logits_q8, :1578-1865): n greedy
+ * generate() steps launched one by one with a GPU event before and after
+ * every launch.  out[k] = one launch: its operation name (a static string:
+ * the reference's scope names, joined with '+' where one launch does
+ * several) and its start/end in ms from the first event.  *count = launches
+ * recorded (at most max).  Advances the position by n like
+ * tmq_model_generate. */
+typedef struct {
+    const char* name;
+    float start_ms, end_ms;
+} tmq_launch_time;
+int tmq_model_profile(tmq_model* m, int n, tmq_launch_time* out, int max, int* count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -170,9 +170,29 @@ def test_cli(golden, tmp_path):
     assert r.returncode == 0, r.stderr
     got = [int(t) for t in r.stdout.split()]
     assert got == golden["tokens"][:16].tolist()
-    r = subprocess.run([exe, str(path), "--perf"], input=prompt, capture_output=True, text=True, timeout=300)
+    trace = tmp_path / "trace.json"
+    r = subprocess.run([exe, str(path), "--perf", "--trace", str(trace)], input=prompt, capture_output=True,
+                       text=True, timeout=300)
     assert r.returncode == 0, r.stderr
     top = json.loads(r.stdout)
     assert [t["id"] for t in top] == golden["top_ids"][0].tolist()
     assert [t["logit"] for t in top] == [round(float(v), 3) for v in golden["top_vals"][0]]
-    assert "[PERF]" in r.stderr
+    assert "[PERF]" in r.stderr and "PIPELINE TIMING BREAKDOWN" in r.stderr and "ffn_down" in r.stderr
+    ev = json.loads(trace.read_text())["traceEvents"]
+    assert len(ev) == 2 * 8 * (3 + 6 * 24) and {e["ph"] for e in ev} == {"B", "E"}
+
+
+def test_profile(model, golden):
+    """tmq_model_profile: every launch of n decode steps, in order, with the
+    same greedy tokens as the graph-replayed generate"""
+    model.set_graphs(True)
+    model.prompt(golden["prompt"])
+    prof = model.profile(3)
+    assert len(prof) == 3 * (3 + 6 * 24)
+    names = [p[0] for p in prof]
+    assert names[:4] == ["output_norm+logits", "argmax", "zero_acc", "embedding+attn_norm+qkv"]
+    assert names.count("rope+attention") == 3 * 24 and names.count("ffn_down") == 3 * 24
+    starts = [p[1] for p in prof]
+    assert starts == sorted(starts) and all(e >= s for _, s, e in prof)
+    assert model.position == 4
+    assert model.tokens(1, 3).tolist() == golden["tokens"][:3].tolist()

@@ -1,7 +1,8 @@
 // tmq_gguf -- command-line engine over libtmq.so, the counterpart of the
 // reference's `tmac_gguf` (sim/tmac_gguf.cpp:2050-2181).
 //
-//   tmq_gguf <model.tmac> [--generate N] [--max-seq N] [--perf] [--no-graphs]
+//   tmq_gguf <model.tmac> [--generate N] [--max-seq N] [--perf] [--trace PATH]
+//            [--prefill N | --no-prefill] [--no-graphs]
 //            [--fpga-q8 --fpga-q5-0 --fpga-q4k --fpga-q6-k --fpga]
 //
 // Prompt token ids are read from stdin.  Without --generate the top-10
@@ -10,12 +11,19 @@
 // chosen ids are printed one per line (the reference samples top-k with
 // rand(); greedy is this engine's choice).  All quantized formats always run
 // on the GPU, so the --fpga-* flags are accepted and change nothing.
-// --perf prints a timing summary (prompt, per-token decode) to stderr.
+// The prompt runs through the batched prefill in chunks of --prefill N
+// tokens (default 512); --no-prefill runs it one token at a time.
+// --perf prints host timings (load, prompt, per-token decode) to stderr, then
+// profiles up to 8 more decode steps launch by launch on the GPU and prints
+// the reference's pipeline timing breakdown (:79-134) per operation, and
+// writes the launches as a Chrome trace (:55-76) to --trace PATH (default
+// /tmp/pipeline_trace.json, the reference's path).
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <string>
 #include <vector>
 
 #include "../../include/tmq.h"
@@ -32,22 +40,76 @@ int die(const char* what) {
     return 1;
 }
 
+// Per-operation totals of a GPU launch profile, in the reference's table
+// layout, and the launches as Chrome trace events.
+void perf_report(const std::vector<tmq_launch_time>& lt, int steps, const char* trace_path) {
+    struct Agg {
+        const char* name;
+        double ms;
+        long calls;
+    };
+    std::vector<Agg> agg;
+    double total = 0.0;
+    for (const tmq_launch_time& t : lt) {
+        const double ms = t.end_ms - t.start_ms;
+        total += ms;
+        auto it = std::find_if(agg.begin(), agg.end(), [&](const Agg& a) { return !strcmp(a.name, t.name); });
+        if (it == agg.end()) agg.push_back({t.name, ms, 1});
+        else {
+            it->ms += ms;
+            it->calls++;
+        }
+    }
+    std::sort(agg.begin(), agg.end(), [](const Agg& a, const Agg& b) { return a.ms > b.ms; });
+    fprintf(stderr, "\n[PERF — PIPELINE TIMING BREAKDOWN] (GPU, %d decode steps, launch by launch)\n", steps);
+    fprintf(stderr, "  %-24s %12s %8s %10s %8s\n", "Operation", "Time (ms)", "Calls", "Avg (ms)", "Share");
+    fprintf(stderr, "  %s\n", std::string(69, '-').c_str());
+    for (const Agg& a : agg)
+        fprintf(stderr, "  %-24s %10.3f %8ld %8.4f %6.1f%%\n", a.name, a.ms, a.calls, a.ms / a.calls,
+                total > 0 ? 100.0 * a.ms / total : 0.0);
+    fprintf(stderr, "  %s\n", std::string(69, '-').c_str());
+    fprintf(stderr, "  %-24s %10.3f\n", "TOTAL", total);
+    if (!agg.empty())
+        fprintf(stderr, "\n  >> Hottest: %s (%.3f ms, %.1f%%)\n\n", agg[0].name, agg[0].ms,
+                total > 0 ? 100.0 * agg[0].ms / total : 0.0);
+    FILE* f = fopen(trace_path, "w");
+    if (!f) {
+        fprintf(stderr, "[TRACE] cannot write %s\n", trace_path);
+        return;
+    }
+    fprintf(f, "{\"traceEvents\":[\n");
+    for (size_t i = 0; i < lt.size(); i++) {
+        fprintf(f, "{\"ph\":\"B\",\"name\":\"%s\",\"cat\":\"gpu\",\"ts\":%.3f,\"pid\":1,\"tid\":1},\n", lt[i].name,
+                lt[i].start_ms * 1e3);
+        fprintf(f, "{\"ph\":\"E\",\"name\":\"%s\",\"cat\":\"gpu\",\"ts\":%.3f,\"pid\":1,\"tid\":1}%s\n", lt[i].name,
+                lt[i].end_ms * 1e3, i + 1 < lt.size() ? "," : "");
+    }
+    fprintf(f, "]}\n");
+    fclose(f);
+    fprintf(stderr, "[TRACE] Wrote Chrome trace: %s\n", trace_path);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     if (argc < 2) {
         fprintf(stderr,
-                "Usage: %s <model.tmac> [--generate N] [--max-seq N] [--perf] [--no-graphs]\n"
+                "Usage: %s <model.tmac> [--generate N] [--max-seq N] [--perf] [--trace PATH]\n"
+                "       [--prefill N | --no-prefill] [--no-graphs]\n"
                 "  Prompt tokens read from stdin; top-10 logits JSON, or N greedy tokens, to stdout.\n",
                 argv[0]);
         return 1;
     }
-    int generate_n = 0, max_seq = 512;
+    int generate_n = 0, max_seq = 512, prefill = 512;
     bool perf = false, graphs = true;
+    const char* trace_path = "/tmp/pipeline_trace.json";
     for (int i = 2; i < argc; i++) {
         if (!strcmp(argv[i], "--generate") && i + 1 < argc) generate_n = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--max-seq") && i + 1 < argc) max_seq = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--perf")) perf = true;
+        else if (!strcmp(argv[i], "--trace") && i + 1 < argc) trace_path = argv[++i];
+        else if (!strcmp(argv[i], "--prefill") && i + 1 < argc) prefill = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--no-prefill")) prefill = 0;
         else if (!strcmp(argv[i], "--no-graphs")) graphs = false;
         else if (!strncmp(argv[i], "--fpga", 6)) continue;
         else {
@@ -68,6 +130,10 @@ int main(int argc, char** argv) {
     tmq_model* m = nullptr;
     if (tmq_model_load(ctx, argv[1], max_seq, &m) != TMQ_OK) return die("load");
     tmq_model_set_graphs(m, graphs ? 1 : 0);
+    if (tmq_model_set_prefill(m, prefill) != TMQ_OK) {
+        fprintf(stderr, "[WARN] %s; the prompt runs one token at a time\n", tmq_last_error());
+        tmq_model_set_prefill(m, 0);
+    }
     tmq_model_config cfg;
     tmq_model_get_config(m, &cfg);
     const double t1 = now_ms();
@@ -105,6 +171,14 @@ int main(int argc, char** argv) {
                     tmq_model_weight_bytes(m) * (double)generate_n / ((t3 - t2) * 1e-3) / 1e9);
         else
             fprintf(stderr, "[PERF] logits: %.3f ms\n", t3 - t2);
+        const int steps = std::min(8, cfg.max_seq - 1 - tmq_model_position(m));
+        if (steps > 0) {
+            std::vector<tmq_launch_time> lt((size_t)steps * (3 + 6 * (size_t)cfg.n_layers));
+            int n = 0;
+            if (tmq_model_profile(m, steps, lt.data(), (int)lt.size(), &n) != TMQ_OK) return die("profile");
+            lt.resize(n);
+            perf_report(lt, steps, trace_path);
+        }
     }
     tmq_model_free(m);
     tmq_close(ctx);

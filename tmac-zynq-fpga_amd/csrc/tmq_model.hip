@@ -160,6 +160,8 @@ struct tmq_model {
     int pos = -1;  // host mirror of state.pos
     bool use_graphs = true;
     hipGraphExec_t g_feed = nullptr, g_decode = nullptr;
+    // tmq_model_profile: an event before and after every launch
+    std::vector<std::pair<const char*, hipEvent_t>>* prof = nullptr;
     int prefill_chunk = 512;  // 0: prompts run one token at a time
     const char* prefill_off = nullptr;  // why the model cannot use the batched prefill
     Prefill pf;
@@ -183,6 +185,24 @@ void model_release(tmq_model* m) {
 }
 
 // ---------------------------------------------------------------- launches
+// Profiling (tmq_model_profile, eager launches only): an event on the
+// stream, tagged with the launch it opens (name) or closes (null).
+int prof_mark(tmq_model* m, const char* name) {
+    if (!m->prof) return 0;
+    hipEvent_t e = nullptr;
+    HIP_TRY(hipEventCreate(&e));
+    m->prof->push_back({name, e});
+    HIP_TRY(hipEventRecord(e, m->ctx->stream));
+    return 0;
+}
+#define PROF(name, call)                          \
+    do {                                          \
+        int prc_ = prof_mark(m, name);            \
+        if (prc_) return prc_;                    \
+        call;                                     \
+        if ((prc_ = prof_mark(m, nullptr))) return prc_; \
+    } while (0)
+
 int launch_gemv(tmq_model* m, const Launch& l) {
     LAUNCH_TRY(tmq_launch_eng_gemv(l.P, l.waves, m->ctx->stream));
     return 0;
@@ -196,10 +216,11 @@ int launch_layers(tmq_model* m, bool dump) {
     hipStream_t s = m->ctx->stream;
     const tmq_model_config& c = m->cfg;
     const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM;
-    LAUNCH_TRY(tmq_launch_zero_acc(m->kacc, m->kacc_n, s));
+    PROF("zero_acc", LAUNCH_TRY(tmq_launch_zero_acc(m->kacc, m->kacc_n, s)));
     for (int l = 0; l < c.n_layers; l++) {
         const Layer& L = m->layers[l];
-        int rc = launch_gemv(m, L.qkv);
+        int rc = 0;
+        PROF(l == 0 ? "embedding+attn_norm+qkv" : "attn_norm+qkv", rc = launch_gemv(m, L.qkv));
         if (rc) return rc;
         if (dump && l == 0) HIP_TRY(hipMemcpyAsync(m->dump, m->hid[1], sizeof(float) * H, hipMemcpyDeviceToDevice, s));
         TmqAttnArgs aa{};
@@ -214,11 +235,14 @@ int launch_layers(tmq_model* m, bool dump) {
         aa.n_heads = c.n_heads;
         aa.n_kv = c.n_kv_heads;
         aa.max_pos = c.max_seq;
-        LAUNCH_TRY(tmq_launch_attn(aa, s));
-        if ((rc = launch_gemv(m, L.o_l))) return rc;
-        if ((rc = launch_gemv(m, L.gu))) return rc;
-        LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s));
-        if ((rc = launch_gemv(m, L.dn))) return rc;
+        PROF("rope+attention", LAUNCH_TRY(tmq_launch_attn(aa, s)));
+        PROF("attn_output", rc = launch_gemv(m, L.o_l));
+        if (rc) return rc;
+        PROF("ffn_norm+gate+up", rc = launch_gemv(m, L.gu));
+        if (rc) return rc;
+        PROF("silu_x_up", LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s)));
+        PROF("ffn_down", rc = launch_gemv(m, L.dn));
+        if (rc) return rc;
         if (dump) LAUNCH_TRY(tmq_launch_resid_view(m->hid[0], L.dd, H, m->dump + (size_t)(l + 1) * H, s));
     }
     return 0;
@@ -238,9 +262,11 @@ int launch_logits(tmq_model* m) { return launch_gemv(m, m->logits_l); }
 // one greedy generate() iteration: logits, argmax -> tokens[pos+1] (and
 // pos+1), then all layers of that token
 int launch_decode(tmq_model* m) {
-    int rc = launch_logits(m);
+    int rc = 0;
+    PROF("output_norm+logits", rc = launch_logits(m));
     if (rc) return rc;
-    LAUNCH_TRY(tmq_launch_argmax(m->cand, m->n_cand, m->state, m->tokens, m->cfg.max_seq, m->ctx->stream));
+    PROF("argmax", LAUNCH_TRY(tmq_launch_argmax(m->cand, m->n_cand, m->state, m->tokens, m->cfg.max_seq,
+                                                m->ctx->stream)));
     return launch_layers(m, false);
 }
 
@@ -1067,6 +1093,42 @@ int tmq_model_hidden(tmq_model* m, float* out) {
     // the residual stream: hid[0] + the last layer's pending down projection
     LAUNCH_TRY(tmq_launch_resid_view(m->hid[0], m->layers.back().dd, m->cfg.hidden, m->view, m->ctx->stream));
     HIP_TRY(hipMemcpyAsync(out, m->view, sizeof(float) * m->cfg.hidden, hipMemcpyDeviceToHost, m->ctx->stream));
+    return check_state(m);
+}
+
+int tmq_model_profile(tmq_model* m, int n, tmq_launch_time* out, int max, int* count) {
+    if (!m || n <= 0 || !out || max <= 0 || !count) return tmq_fail(TMQ_ERR_ARG, "bad profile arguments");
+    if (m->pos < 0) return tmq_fail(TMQ_ERR_ARG, "no prompt processed");
+    if (m->pos + n >= m->cfg.max_seq)
+        return tmq_fail(TMQ_ERR_ARG, "%d more positions exceed max_seq %d", n, m->cfg.max_seq);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    std::vector<std::pair<const char*, hipEvent_t>> ev;
+    m->prof = &ev;
+    for (int i = 0; i < n && !rc; i++) {
+        if (!(rc = launch_decode(m))) m->pos++;
+    }
+    m->prof = nullptr;
+    hipError_t e = hipStreamSynchronize(m->ctx->stream);
+    int k = 0;
+    if (!rc && e == hipSuccess && !ev.empty()) {
+        for (size_t i = 0; i + 1 < ev.size() && k < max; i += 2) {
+            float a = 0.0f, b = 0.0f;
+            if (hipEventElapsedTime(&a, ev[0].second, ev[i].second) != hipSuccess ||
+                hipEventElapsedTime(&b, ev[0].second, ev[i + 1].second) != hipSuccess) {
+                rc = tmq_fail(TMQ_ERR_HIP, "profile events");
+                break;
+            }
+            out[k].name = ev[i].first;
+            out[k].start_ms = a;
+            out[k].end_ms = b;
+            k++;
+        }
+    }
+    for (auto& pe : ev) (void)hipEventDestroy(pe.second);
+    *count = k;
+    if (rc) return rc;
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_HIP, "profile: %s", hipGetErrorString(e));
     return check_state(m);
 }
 

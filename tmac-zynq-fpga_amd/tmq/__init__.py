@@ -37,7 +37,13 @@ EXPORTS = [
     "tmq_model_weight_bytes", "tmq_model_position", "tmq_model_set_graphs", "tmq_model_prompt",
     "tmq_model_feed", "tmq_model_feed_dump", "tmq_model_logits", "tmq_model_generate",
     "tmq_model_generate_async", "tmq_model_tokens", "tmq_model_hidden", "tmq_model_set_prefill",
+    "tmq_model_profile",
 ]
+
+
+class LaunchTime(C.Structure):
+    """tmq_launch_time"""
+    _fields_ = [("name", C.c_char_p), ("start_ms", C.c_float), ("end_ms", C.c_float)]
 
 
 class TmqError(RuntimeError):
@@ -107,6 +113,7 @@ def lib(path: str = LIB_PATH):
         "tmq_model_position": (I, [P]),
         "tmq_model_set_graphs": (I, [P, I]),
         "tmq_model_set_prefill": (I, [P, I]),
+        "tmq_model_profile": (I, [P, I, P, I, C.POINTER(C.c_int)]),
         "tmq_model_prompt": (I, [P, P, I]),
         "tmq_model_feed": (I, [P, C.c_int32]),
         "tmq_model_feed_dump": (I, [P, C.c_int32, P]),
@@ -308,6 +315,15 @@ class Model:
 
     def set_graphs(self, enable: bool):
         _check(lib().tmq_model_set_graphs(self.handle, int(bool(enable))))
+
+    def profile(self, n: int):
+        """n greedy decode steps launched one by one with GPU events:
+        [(operation, start_ms, end_ms)] per launch (tmq_model_profile)."""
+        per = 3 + 6 * self.config["n_layers"]
+        buf = (LaunchTime * (n * per))()
+        cnt = C.c_int(0)
+        _check(lib().tmq_model_profile(self.handle, n, C.cast(buf, C.c_void_p), n * per, C.byref(cnt)))
+        return [(buf[i].name.decode(), buf[i].start_ms, buf[i].end_ms) for i in range(cnt.value)]
 
     def set_prefill(self, chunk: int):
         """0: prompts one token at a time; > 0: batched prefill in chunks of
