@@ -179,7 +179,7 @@ def test_cli(golden, tmp_path):
     assert [t["logit"] for t in top] == [round(float(v), 3) for v in golden["top_vals"][0]]
     assert "[PERF]" in r.stderr and "PIPELINE TIMING BREAKDOWN" in r.stderr and "ffn_down" in r.stderr
     ev = json.loads(trace.read_text())["traceEvents"]
-    assert len(ev) == 2 * 8 * (3 + 6 * 24) and {e["ph"] for e in ev} == {"B", "E"}
+    assert len(ev) in (2 * 8 * (3 + 5 * 24), 2 * 8 * (3 + 6 * 24)) and {e["ph"] for e in ev} == {"B", "E"}
 
 
 def test_profile(model, golden):
@@ -188,8 +188,10 @@ def test_profile(model, golden):
     model.set_graphs(True)
     model.prompt(golden["prompt"])
     prof = model.profile(3)
-    assert len(prof) == 3 * (3 + 6 * 24)
     names = [p[0] for p in prof]
+    # 5 launches per layer when gate/up finish SwiGLU themselves, 6 with a separate silu_x_up
+    per_layer = 6 if "silu_x_up" in names else 5
+    assert len(prof) == 3 * (3 + per_layer * 24)
     assert names[:4] == ["output_norm+logits", "argmax", "zero_acc", "embedding+attn_norm+qkv"]
     assert names.count("rope+attention") == 3 * 24 and names.count("ffn_down") == 3 * 24
     starts = [p[1] for p in prof]

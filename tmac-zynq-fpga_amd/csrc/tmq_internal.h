@@ -68,6 +68,12 @@ struct TmqWork {
     int32_t ngroups;     // workgroups of this GEMV (row groups x kc)
     int32_t kc;          // engine K-split: workgroups per row group (>= 1)
     int32_t resid;
+    // engine, kc = 1: fused SwiGLU.  The tensor holds ffn_gate and ffn_up
+    // rows interleaved in groups of 32 (rows 64q..64q+31 = gate rows
+    // 32q..32q+31, the next 32 = the same up rows); row j of the result,
+    // silu(gate_j) * up_j, goes to silu[j] and max |silu| to *silu_max.
+    float* silu;
+    uint32_t* silu_max;
 };
 
 // Rows of a K-split engine GEMV finalised by the consumer:

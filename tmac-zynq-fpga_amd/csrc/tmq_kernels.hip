@@ -798,6 +798,29 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
     }
     L.part[wave * 64 + lane] = acc;
     __syncthreads();
+    if (w.silu) {
+        // fused SwiGLU (sim/tmac_gguf.cpp:434-439, :1686-1697): lane i < 32
+        // holds gate row 32g+i, lane i+32 the same up row; both finalised
+        // as the K-split consumers do (tmq_fin, no bias)
+        if (wave == 0) {
+            int64_t tot = 0;
+#pragma unroll
+            for (int i = 0; i < NW; i++) tot += L.part[i * 64 + lane];
+            const float f = (float)(((double)tot * (double)xs) / (double)inv);
+            const float up = __shfl_down(f, 32);
+            float m = 0.0f;
+            if (lane < 32) {
+                const float v = (f / (1.0f + tmq_math::tmq_expf(-f))) * up;
+                w.silu[g * 32 + lane] = v;
+                m = fabsf(v);
+            }
+            for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+            if (lane == 0)
+                __hip_atomic_fetch_max(w.silu_max, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
     if (wave == 0 && r < t.rows) {
         int64_t tot = 0;
 #pragma unroll

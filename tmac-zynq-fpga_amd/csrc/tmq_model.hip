@@ -43,6 +43,7 @@ struct Launch {
 struct Layer {
     tmq_tensor *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
     tmq_tensor *gate = nullptr, *up = nullptr, *down = nullptr;
+    tmq_tensor* gu_t = nullptr;  // gate and up rows interleaved by 32 (fused SwiGLU GEMV), or null
     size_t attn_norm = 0, ffn_norm = 0;  // offsets into fvec (floats)
     long bq = -1, bk = -1, bv = -1;      // bias offsets or -1
     Launch qkv, o_l, gu, dn;
@@ -238,9 +239,10 @@ int launch_layers(tmq_model* m, bool dump) {
         PROF("rope+attention", LAUNCH_TRY(tmq_launch_attn(aa, s)));
         PROF("attn_output", rc = launch_gemv(m, L.o_l));
         if (rc) return rc;
-        PROF("ffn_norm+gate+up", rc = launch_gemv(m, L.gu));
+        PROF(L.gu_t ? "ffn_norm+gate+up+silu_x_up" : "ffn_norm+gate+up", rc = launch_gemv(m, L.gu));
         if (rc) return rc;
-        PROF("silu_x_up", LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s)));
+        if (!L.gu_t)
+            PROF("silu_x_up", LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s)));
         PROF("ffn_down", rc = launch_gemv(m, L.dn));
         if (rc) return rc;
         if (dump) LAUNCH_TRY(tmq_launch_resid_view(m->hid[0], L.dd, H, m->dump + (size_t)(l + 1) * H, s));
@@ -726,6 +728,22 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
         if ((rc = upload(p + "ffn_gate.weight", I, H, &Y.gate))) return rc;
         if ((rc = upload(p + "ffn_up.weight", I, H, &Y.up))) return rc;
         if ((rc = upload(p + "ffn_down.weight", H, I, &Y.down))) return rc;
+        // the decode GEMV's copy of gate and up, rows interleaved in groups
+        // of 32, so that one workgroup finishes SwiGLU (TmqWork.silu)
+        const Entry* eg = get(p + "ffn_gate.weight");
+        const Entry* eu = get(p + "ffn_up.weight");
+        if (env_int("TMQ_FUSED_SWIGLU", 1) && eg->type == eu->type && eg->type != TMQ_TYPE_Q8_0 && I % 32 == 0) {
+            const uint64_t rb = ggml_bytes(eg->type, 1, H);
+            std::vector<uint8_t> buf(2 * (size_t)I * rb);
+            for (int q = 0; q < I / 32; q++) {
+                memcpy(buf.data() + (size_t)(64 * q) * rb, eg->data + (size_t)(32 * q) * rb, 32 * rb);
+                memcpy(buf.data() + (size_t)(64 * q + 32) * rb, eu->data + (size_t)(32 * q) * rb, 32 * rb);
+            }
+            rc = tmq_rt_tensor_create(ctx, eg->type, 2 * (uint64_t)I, H, buf.data(), false, buf.size(), nullptr, false,
+                                      &Y.gu_t);
+            if (rc) return tmq_fail(rc, "%sffn_gate/up: %s", p.c_str(), tmq_last_error());
+            m->owned.push_back(Y.gu_t);
+        }
     }
     if ((rc = add_vec("output_norm.weight", H, false, &m->out_norm))) return rc;
 
@@ -868,8 +886,14 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
         Y.gu.P.act.d1 = Y.dout;
         Y.gu.P.act.hidden_out = m->hid[0];
         Y.gu.waves = nw_gu;
-        add_work(Y.gu, Y.gate, ag, xs + 2, kc_gu);
-        add_work(Y.gu, Y.up, au, nullptr, kc_gu);
+        if (Y.gu_t) {
+            add_work(Y.gu, Y.gu_t, nullptr, nullptr, 1);
+            Y.gu.P.w[0].silu = m->silu_x;
+            Y.gu.P.w[0].silu_max = m->max_bits + 2 * l;
+        } else {
+            add_work(Y.gu, Y.gate, ag, xs + 2, kc_gu);
+            add_work(Y.gu, Y.up, au, nullptr, kc_gu);
+        }
         Y.dn.P.act = recipe(TMQ_ACT_PRESCALED, m->silu_x, nullptr, I);
         Y.dn.P.act.max_bits = m->max_bits + 2 * l;
         Y.dn.waves = nw_dn;
