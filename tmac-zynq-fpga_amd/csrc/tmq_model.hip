@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <string>
 #include <vector>
@@ -451,12 +452,25 @@ TmqPfSeg pf_seg(const tmq_tensor* t, int row0, const float* bias) {
     return sg;
 }
 
+// GEMM tile (tmq_launch_pf_gemm) for a plane set whose tensors start at the
+// given rows: the preferred one if its row tile (128 for tiles 0 and 2, 64
+// for tile 1; gate/up pairs: 64 / 32 per tensor) divides every boundary,
+// else the 64-row tile.
+int pf_tile(int want, std::initializer_list<int> bounds) {
+    const int rt = want == 1 ? 64 : 128;
+    for (int b : bounds)
+        if (b % rt) return 1;
+    return want;
+}
+
 // One chunk: positions [p0, p0+T) through every layer.  With `last`, the
 // decode engine's residual state is set from the chunk's last token.
 int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
     Prefill& P = m->pf;
     const tmq_model_config& c = m->cfg;
     const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM, I = c.inter, L = c.n_layers;
+    const int tile_qkv = pf_tile(P.tile[0], {H, KV}), tile_o = pf_tile(P.tile[1], {H});
+    const int tile_gu = pf_tile(P.tile[2], {2 * I}), tile_dn = pf_tile(P.tile[3], {H});
     const int T_pad = (T + 127) & ~127;  // whole 128-token GEMM tiles
     hipStream_t s = m->ctx->stream;
     auto fv = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
@@ -532,7 +546,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.vc = m->vc + (size_t)l * c.max_seq * KV;
         g.rope = m->rope;
         g.part = P.part;  // Q8_0 V tiles (the down projection's sums were consumed above)
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[0], s));
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_qkv, s));
         if (Y.v->dev.type == TMQ_TYPE_Q8_0) {
             TmqPfVFold vf{};
             vf.part = P.part;
@@ -568,7 +582,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.seg[0] = pf_seg(Y.o, 0, nullptr);
         g.x_res = P.x0;
         g.x_out = P.x1;
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[1], s));
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_o, s));
         // ffn_norm, gate/up + SwiGLU
         TmqPfAct a2 = act(TMQ_PF_NORM, 2, P.x1, m->fvec + Y.ffn_norm, H);
         a2.zero_bits = P.max_bits;
@@ -580,7 +594,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.seg[1] = pf_seg(Y.up, I, nullptr);
         g.s_out = P.s;
         g.max_bits = P.max_bits;
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[2], s));
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_gu, s));
         // down projection, split over K; finalised by the next layer's input
         TmqPfAct a3 = act(TMQ_PF_SILU, 3, P.s, nullptr, I);
         a3.max_bits = P.max_bits;
@@ -588,7 +602,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g = gemm(TMQ_PF_PART, W.dn, 3);
         g.split = P.dn_split;
         g.part = P.part;
-        LAUNCH_TRY(tmq_launch_pf_gemm(g, P.tile[3], s));
+        LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_dn, s));
     }
     if (last) {
         const Layer& Z = m->layers[L - 1];
