@@ -180,6 +180,16 @@ def test_cli(golden, tmp_path):
     assert "[PERF]" in r.stderr and "PIPELINE TIMING BREAKDOWN" in r.stderr and "ffn_down" in r.stderr
     ev = json.loads(trace.read_text())["traceEvents"]
     assert len(ev) in (2 * 8 * (3 + 5 * 24), 2 * 8 * (3 + 6 * 24)) and {e["ph"] for e in ev} == {"B", "E"}
+    # --dump-layers: cpp_layer_0..24.bin of the (one-token) prompt, as the reference writes them
+    r = subprocess.run([exe, str(path), "--dump-layers", "--dump-dir", str(tmp_path)], input=prompt,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert [t["id"] for t in json.loads(r.stdout)] == golden["top_ids"][0].tolist()
+    exp = golden["layers0"]
+    for l in range(exp.shape[0]):
+        d = np.fromfile(tmp_path / f"cpp_layer_{l}.bin", dtype=np.float32)
+        assert d.shape == exp[l].shape
+        assert np.abs(d - exp[l]).max() <= 1e-5 * np.abs(exp[l]).max(), f"layer {l}"
 
 
 def test_profile(model, golden):

@@ -180,6 +180,40 @@ def test_chain_matches_single_gemvs(ctx, oracle):
         t.free()
 
 
+@pytest.mark.parametrize("qt", [Q5_0, Q4_K, Q6_K])
+def test_chain_tall_tensors(ctx, oracle, qt):
+    """A chain segment of 4097 64-row groups over two tall tensors, one of
+    them with rows not a multiple of 64: every row bit-exact with the
+    oracle."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda:0")
+    cols = 64 if qt == Q5_0 else 256
+    # 2050 + 2047 groups = 4097 = 4 * 1024 + 1
+    shapes = [(131200, 11), (131000, 12)]
+    x = synth.gen_x(cols, 9)
+    x_d = torch.from_numpy(x).to(dev)
+    descs, outs, ws, ts = [], [], [], []
+    for rows, seed in shapes:
+        w = synth.gen_weights(qt, rows, cols, seed)
+        t = ctx.upload(qt, rows, cols, w)
+        y = torch.zeros(rows, dtype=torch.float32, device=dev)
+        tr = 4 if qt == Q5_0 else 8
+        descs.append((t, x_d.data_ptr(), y.data_ptr(), None, rows // tr, tr, cols // 256 if qt != Q5_0 else 1))
+        outs.append(y)
+        ws.append(w)
+        ts.append(t)
+    print(f"[chain] tall tensors, type {qt}", flush=True)
+    ch = ctx.chain(descs)
+    ch.run()
+    ctx.sync()
+    for (rows, _), w, y in zip(shapes, ws, outs):
+        ye = oracle.matmul(qt, w, x, rows, cols)
+        assert np.array_equal(bits(y.cpu().numpy()), bits(ye))
+    ch.free()
+    for t in ts:
+        t.free()
+
+
 def test_error_paths(ctx):
     import tmq
     w = synth.gen_weights(Q5_0, 8, 896, 1)

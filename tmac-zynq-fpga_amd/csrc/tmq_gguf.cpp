@@ -95,14 +95,15 @@ int main(int argc, char** argv) {
     if (argc < 2) {
         fprintf(stderr,
                 "Usage: %s <model.tmac> [--generate N] [--max-seq N] [--perf] [--trace PATH]\n"
-                "       [--prefill N | --no-prefill] [--no-graphs]\n"
+                "       [--prefill N | --no-prefill] [--no-graphs] [--dump-layers] [--dump-dir DIR]\n"
                 "  Prompt tokens read from stdin; top-10 logits JSON, or N greedy tokens, to stdout.\n",
                 argv[0]);
         return 1;
     }
     int generate_n = 0, max_seq = 512, prefill = 512;
-    bool perf = false, graphs = true;
+    bool perf = false, graphs = true, dump_layers = false;
     const char* trace_path = "/tmp/pipeline_trace.json";
+    const char* dump_dir = "/tmp";
     for (int i = 2; i < argc; i++) {
         if (!strcmp(argv[i], "--generate") && i + 1 < argc) generate_n = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--max-seq") && i + 1 < argc) max_seq = atoi(argv[++i]);
@@ -111,6 +112,8 @@ int main(int argc, char** argv) {
         else if (!strcmp(argv[i], "--prefill") && i + 1 < argc) prefill = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--no-prefill")) prefill = 0;
         else if (!strcmp(argv[i], "--no-graphs")) graphs = false;
+        else if (!strcmp(argv[i], "--dump-layers")) dump_layers = true;
+        else if (!strcmp(argv[i], "--dump-dir") && i + 1 < argc) dump_dir = argv[++i];
         else if (!strncmp(argv[i], "--fpga", 6)) continue;
         else {
             fprintf(stderr, "[ERROR] unknown option %s\n", argv[i]);
@@ -137,7 +140,29 @@ int main(int argc, char** argv) {
     tmq_model_config cfg;
     tmq_model_get_config(m, &cfg);
     const double t1 = now_ms();
-    if (tmq_model_prompt(m, tokens.data(), (int)tokens.size()) != TMQ_OK) return die("prompt");
+    if (!dump_layers) {
+        if (tmq_model_prompt(m, tokens.data(), (int)tokens.size()) != TMQ_OK) return die("prompt");
+    } else {
+        // process_prompt with dump_layers (sim/tmac_gguf.cpp:2001-2018): the
+        // embedding as cpp_layer_0.bin (the last token's, as each token
+        // overwrites it) and the hidden state after each layer of the last
+        // token as cpp_layer_<l+1>.bin, hidden fp32 values each
+        const int n = (int)tokens.size();
+        if (n > 1 && tmq_model_prompt(m, tokens.data(), n - 1) != TMQ_OK) return die("prompt");
+        std::vector<float> layers((size_t)(cfg.n_layers + 1) * cfg.hidden);
+        if (tmq_model_feed_dump(m, tokens[n - 1], layers.data()) != TMQ_OK) return die("feed_dump");
+        for (int l = 0; l <= cfg.n_layers; l++) {
+            char path[4096];
+            snprintf(path, sizeof(path), "%s/cpp_layer_%d.bin", dump_dir, l);
+            FILE* f = fopen(path, "wb");
+            if (!f || fwrite(layers.data() + (size_t)l * cfg.hidden, sizeof(float), cfg.hidden, f) != (size_t)cfg.hidden) {
+                fprintf(stderr, "[ERROR] cannot write %s\n", path);
+                if (f) fclose(f);
+                return 1;
+            }
+            fclose(f);
+        }
+    }
     const double t2 = now_ms();
     double t3 = t2;
     if (generate_n > 0) {

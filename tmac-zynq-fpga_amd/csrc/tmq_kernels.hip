@@ -366,6 +366,25 @@ __device__ __forceinline__ void blk_mac(const typename BlkOf<FMT>::T& k, const A
     else q6k_mac<CLAMP>(k, A, b, inv, sh, sl);
 }
 
+// Work unit u of a row: Q5_0 block u, or K-quant quarter block (u >> 2, u & 3).
+template <int FMT> struct UnitOf;
+template <> struct UnitOf<kQ5_0> { typedef Q5Blk T; static constexpr int per_block = 1; };
+template <> struct UnitOf<kQ4_K> { typedef Q4KQ T; static constexpr int per_block = 4; };
+template <> struct UnitOf<kQ6_K> { typedef Q6KQ T; static constexpr int per_block = 4; };
+template <int FMT>
+__device__ __forceinline__ typename UnitOf<FMT>::T unit_load(const TmqTensorDev& t, int u, int r) {
+    if constexpr (FMT == kQ5_0) return q5_load(t, u, r);
+    else if constexpr (FMT == kQ4_K) return q4kq_load(t, u >> 2, u & 3, r);
+    else return q6kq_load(t, u >> 2, u & 3, r);
+}
+template <int FMT, bool CLAMP = false, class AT>
+__device__ __forceinline__ void unit_mac(const typename UnitOf<FMT>::T& k, const AT& A, int u, float inv,
+                                         int& sh, int& sl) {
+    if constexpr (FMT == kQ5_0) q5_mac<CLAMP>(k, A, u, inv, sh, sl);
+    else if constexpr (FMT == kQ4_K) q4k_mac_q<CLAMP>(k.h, k.qa, k.qb, A, u >> 2, u & 3, inv, sh, sl);
+    else q6k_mac_q<CLAMP>(k.sc, h2f(k.d), k.qla, k.qlb, k.qhc, A, u >> 2, (u & 3) >> 1, u & 1, inv, sh, sl);
+}
+
 // ---------------------------------------------------------------- Q8_0
 // UQ8.8 combined scale of sim/tmac_gguf.cpp:1030-1037, including the x86
 // float->uint16 conversion (truncate to int32, keep the low 16 bits).
@@ -444,10 +463,22 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
             acc += (int64_t)sh * 256 + sl;
         }
     } else {
-        for (int b = b0 + wave; b < b1; b += TMQ_WAVES) {
+        // K-quants in quarter blocks: each wave keeps its next quarter in
+        // flight while it multiplies (the row sums are exact integers, so
+        // the grouping does not change them)
+        typedef typename UnitOf<FMT>::T Unit;
+        const int u1 = b1 * 4;
+        int u = b0 * 4 + wave;
+        Unit cur{};
+        if (u < u1) cur = unit_load<FMT>(t, u, r);
+        for (; u < u1; u += TMQ_WAVES) {
+            const bool more = u + TMQ_WAVES < u1;
+            Unit nxt{};
+            if (more) nxt = unit_load<FMT>(t, u + TMQ_WAVES, r);
             int sh = 0, sl = 0;
-            blk_mac<FMT, CLAMP>(blk_load<FMT>(t, b, r), A, b, inv, sh, sl);
+            unit_mac<FMT, CLAMP>(cur, A, u, inv, sh, sl);
             acc += (int64_t)sh * 256 + sl;
+            if (more) cur = nxt;
         }
     }
     part[wave][lane] = acc;
@@ -746,25 +777,6 @@ __device__ __forceinline__ ActL eng_act(const EngLds& L, float xs) {
     A.xh = (const lu32*)L.xh;
     A.xl = (const lu32*)L.xl;
     return A;
-}
-
-// Work unit u of a row: Q5_0 block u, or K-quant quarter block (u >> 2, u & 3).
-template <int FMT> struct UnitOf;
-template <> struct UnitOf<kQ5_0> { typedef Q5Blk T; static constexpr int per_block = 1; };
-template <> struct UnitOf<kQ4_K> { typedef Q4KQ T; static constexpr int per_block = 4; };
-template <> struct UnitOf<kQ6_K> { typedef Q6KQ T; static constexpr int per_block = 4; };
-template <int FMT>
-__device__ __forceinline__ typename UnitOf<FMT>::T unit_load(const TmqTensorDev& t, int u, int r) {
-    if constexpr (FMT == kQ5_0) return q5_load(t, u, r);
-    else if constexpr (FMT == kQ4_K) return q4kq_load(t, u >> 2, u & 3, r);
-    else return q6kq_load(t, u >> 2, u & 3, r);
-}
-template <int FMT, class AT>
-__device__ __forceinline__ void unit_mac(const typename UnitOf<FMT>::T& k, const AT& A, int u, float inv,
-                                         int& sh, int& sl) {
-    if constexpr (FMT == kQ5_0) q5_mac<false>(k, A, u, inv, sh, sl);
-    else if constexpr (FMT == kQ4_K) q4k_mac_q<false>(k.h, k.qa, k.qb, A, u >> 2, u & 3, inv, sh, sl);
-    else q6k_mac_q<false>(k.sc, h2f(k.d), k.qla, k.qlb, k.qhc, A, u >> 2, (u & 3) >> 1, u & 1, inv, sh, sl);
 }
 
 // Q5_0 / K-quant row group g, K chunk c: the workgroup's units are split
@@ -1348,7 +1360,6 @@ static void* kernel_for(int type, int clamp) {
 }
 template <int F, bool C> struct GemvK { static auto fn() { return gemv_kernel<F, C>; } };
 template <int F, bool C> struct ChainK { static auto fn() { return chain_kernel<F, C>; } };
-
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s) {
     if (w.ngroups <= 0) return 0;
     void* k = kernel_for<GemvK>(w.t.type, w.t.clamp);
