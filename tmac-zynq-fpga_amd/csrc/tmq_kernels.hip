@@ -15,6 +15,8 @@
 // block), folded into int64 once per block.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "tmq_internal.h"
 #include "tmq_mathf.h"
 #include "tmq_device.h"
@@ -675,50 +677,86 @@ __device__ __forceinline__ float seq_sum_lds(const float* v, int n) {
 //   s > 0, so it is the same value, without waiting for s.
 //   quantisation (:1225-1231): x_scale = max|o| / 32767 (1 below 1e-10),
 //   xq = (int16)roundf(o / x_scale).
-__device__ float eng_prologue(const TmqEngAct& a, const EngLds& L, int c0, int c1) {
+// `pre` issues the caller's weight prefetch.  It runs right after the
+// activation loads are issued and before any of them is used: loads retire
+// in order, so the activation arrives without waiting for the (cold) weights.
+// The common modes take up to EP elements per thread with every load issued
+// unconditionally (clamped indices), so no load waits for another.
+template <int EP, class Pre>
+__device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& L, int c0, int c1, Pre&& pre) {
     const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
     const bool wr = a.hidden_out && blockIdx.x == 0;
     const bool norm = (a.mode == TMQ_ACT_RESID_NORM || a.mode == TMQ_ACT_EMBED_NORM) && a.w;
     float* sq = (float*)L.xh;  // squares, consumed before xh/xl are written
     float m = 0.0f;
-    if (a.mode == TMQ_ACT_PRESCALED) {
+    uint32_t pmax = 0;
+    if (a.mode == TMQ_ACT_PRESCALED && c1 - c0 <= EP * nt) {
         // max given; only the workgroup's columns are needed
+        float xin[EP];
+#pragma unroll
+        for (int e = 0; e < EP; e++) xin[e] = a.x[min(c0 + tid + e * nt, c1 - 1)];
+        pmax = __hip_atomic_load(a.max_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_sched_barrier(0);
+        pre();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < EP; e++)
+            if (c0 + tid + e * nt < c1) L.x[c0 + tid + e * nt] = xin[e];
+    } else if (a.mode == TMQ_ACT_PRESCALED) {
+        pre();
         for (int i = c0 + tid; i < c1; i += nt) L.x[i] = a.x[i];
-    } else if (a.mode == TMQ_ACT_RESID_NORM && a.d1.ntiles == 0 && n <= 4 * nt) {
-        // up to 4 elements per thread: every load first, then the arithmetic
-        float xin[4], wv[4], ri[4], bi[4];
-        int64_t ac[4];
-        const float dxs = *a.d1.xs;
+        pmax = __hip_atomic_load(a.max_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if ((a.mode == TMQ_ACT_PLAIN || (a.mode == TMQ_ACT_RESID_NORM && a.d1.ntiles == 0)) && n <= EP * nt) {
+        // every load first (indices clamped into [0, n), pointers always
+        // valid), then the arithmetic; one straight-line path per mode
+        auto fast = [&](auto resid_tag) {
+            constexpr bool resid = decltype(resid_tag)::value;
+            float xin[EP], wv[EP], ri[EP], bi[EP];
+            int64_t ac[EP];
+            float dxs = 1.0f;
+            if constexpr (resid) dxs = *a.d1.xs;
+            const float* bp = resid && a.d1.bias ? a.d1.bias : a.x;
+            const float* wp = norm ? a.w : a.x;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int i = tid + e * nt;
-            if (i < n) {
+            for (int e = 0; e < EP; e++) {
+                const int i = min(tid + e * nt, n - 1);
                 xin[e] = a.x[i];
-                ac[e] = tmq_ld_acc(a.d1.acc + i);
-                ri[e] = a.d1.row_inv[i];
-                bi[e] = a.d1.bias ? a.d1.bias[i] : 0.0f;
-                wv[e] = norm ? a.w[i] : 1.0f;
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int i = tid + e * nt;
-            if (i < n) {
-                float d = (float)(((double)ac[e] * (double)dxs) / (double)ri[e]);
-                if (a.d1.bias) d = d + bi[e];
-                float v = xin[e] + d;
-                if (wr) a.hidden_out[i] = v;
-                if (norm) {
-                    sq[i] = v * v;
-                    v = v * wv[e];
+                wv[e] = wp[i];
+                if constexpr (resid) {
+                    ac[e] = tmq_ld_acc(a.d1.acc + i);
+                    ri[e] = a.d1.row_inv[i];
+                    bi[e] = bp[i];
                 }
-                L.x[i] = v;
-                m = fmaxf(m, fabsf(v));
             }
-        }
+            __builtin_amdgcn_sched_barrier(0);
+            pre();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int e = 0; e < EP; e++) {
+                const int i = tid + e * nt;
+                if (i < n) {
+                    float v = xin[e];
+                    if constexpr (resid) {
+                        float d = (float)(((double)ac[e] * (double)dxs) / (double)ri[e]);
+                        if (a.d1.bias) d = d + bi[e];
+                        v = v + d;
+                    }
+                    if (wr) a.hidden_out[i] = v;
+                    if (norm) {
+                        sq[i] = v * v;
+                        v = v * wv[e];
+                    }
+                    L.x[i] = v;
+                    m = fmaxf(m, fabsf(v));
+                }
+            }
+        };
+        if (a.mode == TMQ_ACT_RESID_NORM) fast(std::true_type{});
+        else fast(std::false_type{});
         for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
         if ((tid & 63) == 0) L.red[2 + (tid >> 6)] = m;
     } else {
+        pre();
         int tok = 0;
         if (a.mode == TMQ_ACT_EMBED_NORM) tok = a.tokens[a.state->pos];
         for (int i = tid; i < n; i += nt) {
@@ -749,7 +787,7 @@ __device__ float eng_prologue(const TmqEngAct& a, const EngLds& L, int c0, int c
     }
     float mm;
     if (a.mode == TMQ_ACT_PRESCALED) {
-        mm = __builtin_bit_cast(float, __hip_atomic_load(a.max_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        mm = __builtin_bit_cast(float, pmax);
     } else {
         mm = 0.0f;
         for (int i = 0; i < (int)(nt >> 6); i++) mm = fmaxf(mm, L.red[2 + i]);
@@ -788,14 +826,18 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
     const TmqTensorDev& t = w.t;
     const int kc = w.kc, g = gi / kc, c = gi - g * kc;
     const int nu = t.nb * UnitOf<FMT>::per_block;
-    const int u0 = (int)((int64_t)c * nu / kc), u1 = (int)((int64_t)(c + 1) * nu / kc);
+    const int u0 = c * nu / kc, u1 = (c + 1) * nu / kc;  // nu * kc < 2^31
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
     Unit cur{};
-    if (u0 + wave < u1) cur = unit_load<FMT>(t, u0 + wave, r);
-    const float inv = t.row_inv[r];
+    float inv = 0.0f;
     constexpr int QK = FMT == kQ5_0 ? 32 : 256, PB = UnitOf<FMT>::per_block;
-    const float xs = eng_prologue(a, L, (u0 / PB) * QK, ((u1 + PB - 1) / PB) * QK);
+    const float xs = eng_prologue<NW >= 16 ? 1 : 4>(a, L, (u0 / PB) * QK, ((u1 + PB - 1) / PB) * QK, [&] {
+        // unconditional (a clamped, valid unit): the prologue's waits then
+        // count these loads exactly and skip them
+        cur = unit_load<FMT>(t, max(0, min(u0 + wave, nu - 1)), r);
+        inv = t.row_inv[r];
+    });
     if (w.xs_out && gi == 0 && threadIdx.x == 0) *w.xs_out = xs;
     const ActL A = eng_act(L, xs);
     int64_t acc = 0;
@@ -854,16 +896,17 @@ __device__ __forceinline__ void eng_group_q8_split(const TmqEngAct& a, const Eng
     const TmqTensorDev& t = w.t;
     const int kc = w.kc, g = gi / kc, c = gi - g * kc;
     const int nt = (t.cols + 63) / 64;
-    const int t0 = (int)((int64_t)c * nt / kc), t1 = (int)((int64_t)(c + 1) * nt / kc);
+    const int t0 = c * nt / kc, t1 = (c + 1) * nt / kc;  // nt * kc < 2^31
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
     Q8Blk b0{}, b1{};
-    if (t0 + wave < t1) {
-        b0 = q8_load(t, 2 * (t0 + wave), r);
-        if (2 * (t0 + wave) + 1 < t.nb) b1 = q8_load(t, 2 * (t0 + wave) + 1, r);
-    }
-    const float ri = t.row_inv[r];
-    const float xs = eng_prologue(a, L, 64 * t0, min(64 * t1, t.cols));
+    float ri = 0.0f;
+    const float xs = eng_prologue<NW >= 16 ? 1 : 4>(a, L, 64 * t0, min(64 * t1, t.cols), [&] {
+        const int tt = max(0, min(t0 + wave, nt - 1));
+        b0 = q8_load(t, 2 * tt, r);
+        b1 = q8_load(t, min(2 * tt + 1, t.nb - 1), r);
+        ri = t.row_inv[r];
+    });
     if (w.xs_out && gi == 0 && threadIdx.x == 0) *w.xs_out = xs;
     const ActL A = eng_act(L, xs);
     for (int tt = t0 + wave; tt < t1; tt += NW) {
@@ -900,12 +943,11 @@ __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L
     const int r = active ? r0 + lane : lane;
     Q8Blk cur{};
     float ri = 0.0f, rs = 0.0f;
-    if (active) {
+    const ActL A = eng_act(L, eng_prologue<NW >= 16 ? 1 : 4>(a, L, 0, t.cols, [&] {
         cur = q8_load(t, 0, r);
         ri = t.row_inv[r];
         rs = t.row_scale[r];
-    }
-    const ActL A = eng_act(L, eng_prologue(a, L, 0, t.cols));
+    }));
     if (!active) return;
     const int nt = (t.cols + 63) / 64;
     float y = 0.0f;
@@ -952,15 +994,21 @@ __device__ __forceinline__ void eng_dispatch(const TmqEngAct& a, const EngLds& L
 // before the weight prefetch and the activation prologue start.  One
 // instantiation per format pair keeps the code small: every work uses FA
 // except the last, which uses FB.
-template <int NW, int FA, int FB>
+template <int NW, int FA, int FB, bool MULTI>
 __global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngLaunch P) {
     extern __shared__ __attribute__((aligned(16))) unsigned char eng_smem[];
     const EngLds L = eng_lds(eng_smem, P.act.n, NW);
-    const int b = blockIdx.x;
-    const int wi = (P.nworks > 2 && b >= P.w[2].first_group) ? 2 : (P.nworks > 1 && b >= P.w[1].first_group) ? 1 : 0;
-    const TmqWork w = wi == 2 ? P.w[2] : wi == 1 ? P.w[1] : P.w[0];
-    if (FA != FB && wi == P.nworks - 1) eng_dispatch<NW, FB>(P.act, L, w);
-    else eng_dispatch<NW, FA>(P.act, L, w);
+    if constexpr (!MULTI) {
+        // one work: every launch parameter sits at a fixed kernarg offset,
+        // so all of them come in the first batch of scalar loads
+        eng_dispatch<NW, FA>(P.act, L, P.w[0]);
+    } else {
+        const int b = blockIdx.x;
+        const int wi = (P.nworks > 2 && b >= P.w[2].first_group) ? 2 : (P.nworks > 1 && b >= P.w[1].first_group) ? 1 : 0;
+        const TmqWork w = wi == 2 ? P.w[2] : wi == 1 ? P.w[1] : P.w[0];
+        if (FA != FB && wi == P.nworks - 1) eng_dispatch<NW, FB>(P.act, L, w);
+        else eng_dispatch<NW, FA>(P.act, L, w);
+    }
 }
 
 // x = silu(g) * u (sim/tmac_gguf.cpp:434-439, :1693-1697) from two K-split
@@ -1393,9 +1441,9 @@ int tmq_launch_zero_acc(int64_t* p, size_t n, hipStream_t s) {
 
 size_t tmq_eng_lds_bytes(int n, int waves) { return 8 * (size_t)n + 8 * 64 * (size_t)waves + 256; }
 
-template <int NW>
+template <int NW, bool MULTI>
 static void* eng_kernel_for(int fa, int fb) {
-#define TMQ_ENG_K(A, B) (void*)eng_gemv_kernel<NW, A, B>
+#define TMQ_ENG_K(A, B) (void*)eng_gemv_kernel<NW, A, B, MULTI>
     if (fa == kQ5_0 && fb == kQ5_0) return TMQ_ENG_K(kQ5_0, kQ5_0);
     if (fa == kQ5_0 && fb == kQ8_0) return TMQ_ENG_K(kQ5_0, kQ8_0);
     if (fa == kQ4_K && fb == kQ4_K) return TMQ_ENG_K(kQ4_K, kQ4_K);
@@ -1415,7 +1463,13 @@ int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
     const int fa = code(l.w[0]), fb = code(l.w[l.nworks - 1]);
     for (int i = 1; i + 1 < l.nworks; i++)
         if (code(l.w[i]) != fa) return (int)hipErrorInvalidValue;
-    void* k = waves == 16 ? eng_kernel_for<16>(fa, fb) : waves == 4 ? eng_kernel_for<4>(fa, fb) : nullptr;
+    // the kernels split a row's units (or Q8_0 tiles) into kc chunks in int32
+    for (int i = 0; i < l.nworks; i++)
+        if ((int64_t)l.w[i].t.nb * 4 * (l.w[i].kc > 0 ? l.w[i].kc : 1) >= ((int64_t)1 << 31))
+            return (int)hipErrorInvalidValue;
+    void* k = nullptr;
+    if (l.nworks > 1) k = waves == 16 ? eng_kernel_for<16, true>(fa, fb) : waves == 4 ? eng_kernel_for<4, true>(fa, fb) : nullptr;
+    else k = waves == 16 ? eng_kernel_for<16, false>(fa, fb) : waves == 4 ? eng_kernel_for<4, false>(fa, fb) : nullptr;
     if (!k) return (int)hipErrorInvalidValue;
     TmqEngLaunch arg = l;
     void* args[] = {&arg};
