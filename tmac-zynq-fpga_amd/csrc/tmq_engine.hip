@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     for (int p = tid; p <= pos; p += blockDim.x) ex[p] = tmq_math::tmq_expf(sc[p] - mx);
     __syncthreads();
     if (tid == 0) {
-        // exp_sum in position order, 16 terms per batch of LDS reads
+        // exp_sum in position order (:1648-1649), 16 terms per batch of LDS reads
         float es = 0.0f;
         int p = 0;
         for (; p + 16 <= pos + 1; p += 16) {

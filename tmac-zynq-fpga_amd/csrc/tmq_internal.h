@@ -103,13 +103,13 @@ struct TmqEngState {
 
 // Activation recipe of an engine GEMV launch: every workgroup computes the
 // int16 activation of its launch into LDS before its row groups (the
-// reference's rms_norm / silu / matmul quantisation, sim/tmac_gguf.cpp:415-439,
+// reference's rms_norm / silu / matmul quantisation, sim/tmac_gguf.cpp:447-460,
 // :1225-1231), so no separate normalisation launch is needed.
 //   EMBED_NORM  x = embedding row of tokens[pos] (process_embedding, :1955)
 //   RESID_NORM  x = x_in + d1 (the residual adds, :1663, :1706)
 //   PLAIN       x = x_in (the attention context)
 //   PRESCALED   x = x_in with max|x| given (SiLU*up from tmq_launch_silu)
-// then, for the two NORM modes, x = rms_norm(x, w) (:415-422) when w is
+// then, for the two NORM modes, x = rms_norm(x, w) (:447-453) when w is
 // set.  x before the norm is stored to hidden_out by workgroup 0 when
 // hidden_out is set.
 enum { TMQ_ACT_RESID_NORM = 0, TMQ_ACT_PLAIN = 1, TMQ_ACT_PRESCALED = 2, TMQ_ACT_EMBED_NORM = 3 };

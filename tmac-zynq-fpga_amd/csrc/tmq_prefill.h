@@ -63,7 +63,7 @@ struct TmqPfPart {
 
 // Activation operands of a layer step for T tokens (one workgroup each):
 // the value of every column, then RMSNorm / quantisation exactly as the
-// decode engine's prologues (sim/tmac_gguf.cpp:415-422, :1225-1231).
+// decode engine's prologues (sim/tmac_gguf.cpp:447-453, :1225-1231).
 enum {
     TMQ_PF_EMBED_NORM = 0,  // embedding of tokens[p0 + t], then the norm
     TMQ_PF_RESID_NORM = 1,  // x[t] + finalise(d1), then the norm
