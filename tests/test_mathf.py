@@ -1,6 +1,6 @@
 """The engine's device expf (tmac-zynq-fpga_amd/csrc/tmq_mathf.h), built for the
 host from the same header, against the host libm expf that the reference
-engine calls (sim/tmac_gguf.cpp:438, :1650-1654).
+engine calls (sim/tmac_gguf.cpp:460, :1650-1654).
 
 An exhaustive run over all 2^32 inputs (same check, stride 1) found no
 mismatch; the suite checks a strided sample plus the special values.  The

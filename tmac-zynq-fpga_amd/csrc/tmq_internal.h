@@ -103,7 +103,7 @@ struct TmqEngState {
 
 // Activation recipe of an engine GEMV launch: every workgroup computes the
 // int16 activation of its launch into LDS before its row groups (the
-// reference's rms_norm / silu / matmul quantisation, sim/tmac_gguf.cpp:447-460,
+// reference's rms_norm / silu / matmul quantisation, sim/tmac_gguf.cpp:447-461,
 // :1225-1231), so no separate normalisation launch is needed.
 //   EMBED_NORM  x = embedding row of tokens[pos] (process_embedding, :1955)
 //   RESID_NORM  x = x_in + d1 (the residual adds, :1663, :1706)

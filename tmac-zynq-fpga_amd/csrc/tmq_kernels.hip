@@ -853,7 +853,7 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
     L.part[wave * 64 + lane] = acc;
     __syncthreads();
     if (w.silu) {
-        // fused SwiGLU (sim/tmac_gguf.cpp:458-460, :1696-1700): lane i < 32
+        // fused SwiGLU (sim/tmac_gguf.cpp:459-461, :1696-1700): lane i < 32
         // holds gate row 32g+i, lane i+32 the same up row; both finalised
         // as the K-split consumers do (tmq_fin, no bias)
         if (wave == 0) {
@@ -1011,7 +1011,7 @@ __global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngLaunch P) {
     }
 }
 
-// x = silu(g) * u (sim/tmac_gguf.cpp:458-460, :1696-1700) from two K-split
+// x = silu(g) * u (sim/tmac_gguf.cpp:459-461, :1696-1700) from two K-split
 // GEMVs, once per layer; the workgroups' max |x| meet in max_bits.
 __global__ __launch_bounds__(256) void silu_kernel(TmqDeferred g, TmqDeferred u, int n, float* x,
                                                    uint32_t* max_bits) {

@@ -1,6 +1,6 @@
 // tmq_mathf.h -- fp32 transcendental functions matching the reference host.
 //
-// The reference engine calls glibc's expf/logf (sim/tmac_gguf.cpp:438,
+// The reference engine calls glibc's expf/logf (sim/tmac_gguf.cpp:460,
 // :1650-1654).  glibc 2.35 implements expf with the table-driven method of
 // Szabolcs Nagy (Arm optimized-routines, "expf.c", MIT/Apache-2.0): with
 // N = 32, x*N/ln2 = k + r, exp(x) = 2^(k/N) * p(r) where p is a cubic

@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : 1) void pf_gemm_kernel(TmqPfGe
                                                           xr.z + fin(i, j, 4 * q + 2), xr.w + fin(i, j, 4 * q + 3));
                 }
         } else if (MODE == TMQ_PF_GU) {
-            // SwiGLU (sim/tmac_gguf.cpp:458-460): gate rows in block 0, the
+            // SwiGLU (sim/tmac_gguf.cpp:459-461): gate rows in block 0, the
             // same up rows in block 1
             float m = 0.0f;
             const int j0 = rblk(2 * wr) * 32;
