@@ -1265,6 +1265,7 @@ __device__ __forceinline__ float pf_value(const TmqPfAct& a, int t, int i, int t
     if (a.mode == TMQ_PF_RESID_NORM) return a.x[(size_t)t * a.n + i] + tmq_pf_fin(a.d1, t, i);
     return a.x[(size_t)t * a.n + i];
 }
+template <int G>
 __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     extern __shared__ float pf_lds[];
     __shared__ float red[8];
@@ -1290,14 +1291,11 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     const bool wr = a.x_out && (a.mode == TMQ_PF_EMBED_NORM || a.mode == TMQ_PF_RESID_NORM);
     const int tok = a.mode == TMQ_PF_EMBED_NORM ? a.tokens[a.p0 + t] : 0;
     float m = 0.0f;
-    for (int gi = tid; gi < ng; gi += nt) {
-        const int i0 = 4 * gi;
-        float v[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = pf_value(a, t, i0 + j, tok);
+    // one group of four columns: the value before the norm to x_out, the
+    // squares and x*w (norm modes) or x to LDS, the running max |.|
+    auto put = [&](int i0, float (&v)[4], float4 w4) {
         if (wr) *(float4*)(a.x_out + (size_t)t * n + i0) = make_float4(v[0], v[1], v[2], v[3]);
         if (norm) {
-            const float4 w4 = *(const float4*)(a.w + i0);
             const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
             float s4[4];
 #pragma unroll
@@ -1310,6 +1308,90 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
         *(float4*)(X + i0) = make_float4(v[0], v[1], v[2], v[3]);
 #pragma unroll
         for (int j = 0; j < 4; j++) m = fmaxf(m, fabsf(v[j]));
+    };
+    constexpr int SMAX = 4;  // split-K parts summed in registers (RESID_NORM)
+    // the batched paths read 16-byte groups
+    const uintptr_t al = (uintptr_t)a.x | (uintptr_t)a.w |
+                         (a.mode == TMQ_PF_RESID_NORM
+                              ? (uintptr_t)a.d1.rw | (uintptr_t)a.d1.row_inv | (uintptr_t)a.d1.bias | (uintptr_t)a.d1.part
+                              : 0);
+    // (the register-hungry RESID_NORM batch only for up to two groups a thread)
+    if (a.mode == TMQ_PF_EMBED_NORM || ng > G * nt || (al & 15) ||
+        (a.mode == TMQ_PF_RESID_NORM && (G > 2 || a.d1.split > SMAX || a.d1.ld % 4))) {
+        for (int gi = tid; gi < ng; gi += nt) {
+            const int i0 = 4 * gi;
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = pf_value(a, t, i0 + j, tok);
+            put(i0, v, norm ? *(const float4*)(a.w + i0) : make_float4(1.0f, 1.0f, 1.0f, 1.0f));
+        }
+    } else if (a.mode == TMQ_PF_RESID_NORM) {
+      if constexpr (G <= 2) {
+        // every load of the thread's groups first (indices clamped into the
+        // row), then the arithmetic: x + the finalised split-K sums
+        // (tmq_pf_fin), then the norm
+        const TmqPfPart& D = a.d1;
+        const float* bp = D.bias ? D.bias : D.row_inv;
+        const float xs_t = D.xs[t];
+        const int64_t corr = 128 * (int64_t)D.tx[t] + 16384 * (int64_t)D.K;
+        float4 xv[G], w4[G], ri4[G], bi4[G];
+        int4 rw4[G];
+        int64_t pp[G][SMAX][4];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const int i0 = 4 * min(tid + g * nt, ng - 1);
+            xv[g] = *(const float4*)(a.x + (size_t)t * n + i0);
+            w4[g] = *(const float4*)(a.w + i0);
+            ri4[g] = *(const float4*)(D.row_inv + i0);
+            bi4[g] = *(const float4*)(bp + i0);
+            rw4[g] = *(const int4*)(D.rw + i0);
+#pragma unroll
+            for (int sp = 0; sp < SMAX; sp++) {
+                const int64_t* q = D.part + ((size_t)min(sp, D.split - 1) * D.T_pad + t) * D.ld + i0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) pp[g][sp][j] = q[j];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            if (tid + g * nt < ng) {
+                const int i0 = 4 * (tid + g * nt);
+                const float xin[4] = {xv[g].x, xv[g].y, xv[g].z, xv[g].w};
+                const float riv[4] = {ri4[g].x, ri4[g].y, ri4[g].z, ri4[g].w};
+                const float biv[4] = {bi4[g].x, bi4[g].y, bi4[g].z, bi4[g].w};
+                const int rwv[4] = {rw4[g].x, rw4[g].y, rw4[g].z, rw4[g].w};
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    int64_t acc = 128 * (int64_t)rwv[j] + corr;
+#pragma unroll
+                    for (int sp = 0; sp < SMAX; sp++) acc += sp < D.split ? pp[g][sp][j] : 0;
+                    float d = (float)(((double)acc * (double)xs_t) / (double)riv[j]);
+                    if (D.bias) d = d + biv[j];
+                    v[j] = xin[j] + d;
+                }
+                put(i0, v, w4[g]);
+            }
+        }
+      }
+    } else {
+        // PLAIN, NORM, SILU: the values (and norm weights) of all the
+        // thread's groups first
+        const float* wp = norm ? a.w : a.x;
+        float4 xv[G], w4[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const int i0 = 4 * min(tid + g * nt, ng - 1);
+            xv[g] = *(const float4*)(a.x + (size_t)t * n + i0);
+            w4[g] = *(const float4*)(wp + i0);
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            if (tid + g * nt < ng) {
+                float v[4] = {xv[g].x, xv[g].y, xv[g].z, xv[g].w};
+                put(4 * (tid + g * nt), v, w4[g]);
+            }
+        }
     }
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if (lane == 0) red[1 + wave] = m;
@@ -1511,6 +1593,14 @@ int tmq_launch_pf_rowsums(const TmqPfPlanes& p, hipStream_t s) {
 int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s) {
     if (a.n % TMQ_PF_CHUNK || a.n > TMQ_ENG_MAXN || a.out.rows < a.T || a.out.rows % 32 || a.out.K != a.n)
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(pf_act_kernel, dim3(a.out.rows), dim3(256), 8 * (size_t)a.n, s, a);
+    // groups of four columns per thread: 1, 2, 5 or 8 (wider rows take the
+    // kernel's one-group-at-a-time path)
+    const int groups = (a.n / 4 + 255) / 256;
+    const dim3 grid(a.out.rows), blk(256);
+    const size_t lds = 8 * (size_t)a.n;
+    if (groups <= 1) hipLaunchKernelGGL(pf_act_kernel<1>, grid, blk, lds, s, a);
+    else if (groups <= 2) hipLaunchKernelGGL(pf_act_kernel<2>, grid, blk, lds, s, a);
+    else if (groups <= 5) hipLaunchKernelGGL(pf_act_kernel<5>, grid, blk, lds, s, a);
+    else hipLaunchKernelGGL(pf_act_kernel<8>, grid, blk, lds, s, a);
     return (int)hipGetLastError();
 }
