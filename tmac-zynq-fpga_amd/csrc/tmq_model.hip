@@ -625,7 +625,7 @@ int pf_prompt(tmq_model* m, int n, int* done) {
     *done = 0;
     const int qpk = m->cfg.n_heads / m->cfg.n_kv_heads;
     int lim = n;
-    while (lim > 0 && tmq_pf_attn_lds(qpk, lim) > 126 * 1024) lim--;
+    while (lim > 0 && tmq_pf_attn_lds(qpk, lim) > TMQ_PF_ATTN_LDS_MAX) lim--;
     if (lim < 2) return 0;
     int rc;
     if (!m->pf.built && (rc = pf_build_weights(m))) return rc;

@@ -192,3 +192,6 @@ int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);
 int tmq_launch_pf_vfold(const TmqPfVFold& f, hipStream_t s);
 size_t tmq_pf_attn_lds(int qpk, int npos);
+// dynamic LDS the attention kernel may take beside its ~35 KiB of static
+// buffers (160 KiB per workgroup in all)
+#define TMQ_PF_ATTN_LDS_MAX (124 * 1024)

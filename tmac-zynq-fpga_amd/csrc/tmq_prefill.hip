@@ -348,11 +348,14 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : 1) void pf_gemm_kernel(TmqPfGe
 // order, log via fp64, weights, the context summed over positions in order.
 // The query rows are wave-uniform and read through the scalar cache.
 typedef __attribute__((address_space(4))) const float cf32;
+constexpr int VT_LD = 68;  // floats between dimensions of a transposed V chunk
 __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
     extern __shared__ float lds[];
     __shared__ float stat[2][8];
     __shared__ uint64_t tab[32];
-    __shared__ __attribute__((aligned(16))) float vb2[2][64 * 64];  // V rows, double-buffered
+    // V chunks of 64 positions, transposed (dimension-major, VT_LD apart) so
+    // that the lane of dimension d reads four positions at once; double-buffered
+    __shared__ __attribute__((aligned(16))) float vb2[2][64 * VT_LD];
     // the longest (latest) positions first
     const int t = a.T - 1 - (int)blockIdx.x, g = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
     const int qpk = a.n_heads / a.n_kv, KV = a.n_kv * 64, H = a.n_heads * 64;
@@ -396,8 +399,9 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
         ex[h * npad + p] = tmq_math::tmq_expf_tab(sc[h * npad + p] - stat[0][h], et);
     }
     __syncthreads();
-    if (wv < qpk && ln == 0) {
-        const float* e = ex + wv * npad;
+    if (wv == 0 && ln < qpk) {
+        // lane h of wave 0 sums head h's terms
+        const float* e = ex + ln * npad;
         float es = 0.0f;
         int p = 0;
         for (; p + 16 <= np; p += 16) {
@@ -413,7 +417,7 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
             }
         }
         for (; p < np; p++) es += e[p];
-        stat[1][wv] = (float)log((double)es) + stat[0][wv];
+        stat[1][ln] = (float)log((double)es) + stat[0][ln];
     }
     __syncthreads();
     for (int i = tid; i < qpk * np; i += nt) {
@@ -423,11 +427,17 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
     // context, 64 positions per chunk; the next chunk's V rows are loaded
     // into registers while the current one is summed (512 threads x 2 float4
     // = one chunk)
+    auto put_v = [&](float* vt, int pr, int q4, float4 v) {
+        vt[(4 * q4 + 0) * VT_LD + pr] = v.x;
+        vt[(4 * q4 + 1) * VT_LD + pr] = v.y;
+        vt[(4 * q4 + 2) * VT_LD + pr] = v.z;
+        vt[(4 * q4 + 3) * VT_LD + pr] = v.w;
+    };
     {
         const int nr = min(64, np);
         for (int i = tid; i < nr * 16; i += nt) {
             const int pr = i >> 4, q4 = i & 15;
-            *(float4*)&vb2[0][pr * 64 + 4 * q4] = *(const float4*)(vbase + (size_t)pr * KV + 4 * q4);
+            put_v(vb2[0], pr, q4, *(const float4*)(vbase + (size_t)pr * KV + 4 * q4));
         }
     }
     __syncthreads();
@@ -443,21 +453,22 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
         }
         if (wv < qpk) {
             const float* e = ex + wv * npad + c0;
-            const float* vv = vb2[buf];
+            const float* vt = vb2[buf] + ln * VT_LD;
             int pr = 0;
             for (; pr + 4 <= nr; pr += 4) {
                 const float4 e4 = *(const float4*)(e + pr);
-                acc += e4.x * vv[pr * 64 + ln];
-                acc += e4.y * vv[(pr + 1) * 64 + ln];
-                acc += e4.z * vv[(pr + 2) * 64 + ln];
-                acc += e4.w * vv[(pr + 3) * 64 + ln];
+                const float4 v4 = *(const float4*)(vt + pr);
+                acc += e4.x * v4.x;
+                acc += e4.y * v4.y;
+                acc += e4.z * v4.z;
+                acc += e4.w * v4.w;
             }
-            for (; pr < nr; pr++) acc += e[pr] * vv[pr * 64 + ln];
+            for (; pr < nr; pr++) acc += e[pr] * vt[pr];
         }
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int i = tid + j * 512, pr = i >> 4, q4 = i & 15;
-            if (pr < nr1) *(float4*)&vb2[buf ^ 1][pr * 64 + 4 * q4] = pre[j];
+            if (pr < nr1) put_v(vb2[buf ^ 1], pr, q4, pre[j]);
         }
         __syncthreads();
         buf ^= 1;
@@ -552,11 +563,11 @@ int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void*)pf_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           160 * 1024 - 34 * 1024);
+                                           TMQ_PF_ATTN_LDS_MAX);
         if (e != hipSuccess) return (int)e;
         attr = true;
     }
-    if (lds > 160 * 1024 - 34 * 1024) return (int)hipErrorInvalidValue;  // + 32 KiB static V buffers
+    if (lds > TMQ_PF_ATTN_LDS_MAX) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(pf_attn_kernel, dim3(a.T, a.n_kv), dim3(512), lds, s, a);
     return (int)hipGetLastError();
 }
