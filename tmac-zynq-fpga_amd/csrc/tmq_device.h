@@ -26,3 +26,48 @@ static __device__ float tmq_fin(const TmqDeferred& D, int i) {
     if (D.bias) v = v + D.bias[i];
     return v;
 }
+
+// tmq_fin split in two, so that a kernel can issue the loads of several
+// deferred values before it waits for any of them: fin_load takes the raw
+// terms of row i (no branch on the data; Q8 selects the tiled form, up to
+// TMQ_FIN_MAXT tiles), fin_finish forms the value as tmq_fin does.
+#define TMQ_FIN_MAXT 16
+template <bool Q8>
+struct TmqFinRaw {
+    int64_t p[Q8 ? TMQ_FIN_MAXT : 1];
+    float r, b;
+};
+template <bool Q8>
+static __device__ __forceinline__ TmqFinRaw<Q8> fin_load(const TmqDeferred& D, int i) {
+    TmqFinRaw<Q8> f;
+    if constexpr (Q8) {
+        const int nt = D.ntiles;
+#pragma unroll
+        for (int t = 0; t < TMQ_FIN_MAXT; t++) f.p[t] = tmq_ld_acc(D.acc + (size_t)i * nt + min(t, nt - 1));
+        f.r = D.row_scale[i];
+    } else {
+        f.p[0] = tmq_ld_acc(D.acc + i);
+        f.r = D.row_inv[i];
+    }
+    // no bias: any valid row vector stands in (the value is not used)
+    const float* bp = D.bias ? D.bias : Q8 ? D.row_scale : D.row_inv;
+    f.b = bp[i];
+    return f;
+}
+template <bool Q8>
+static __device__ __forceinline__ float fin_finish(const TmqDeferred& D, const TmqFinRaw<Q8>& f, double xs) {
+    float v;
+    if constexpr (Q8) {
+        const double rs = (double)f.r;
+        float y = 0.0f;
+#pragma unroll
+        for (int t = 0; t < TMQ_FIN_MAXT; t++)
+            if (t < D.ntiles) y = (float)((double)y + ((double)f.p[t] * xs) * rs);
+        v = y;
+    } else {
+        v = (float)(((double)f.p[0] * xs) / (double)f.r);
+    }
+    if (D.bias) v = v + f.b;
+    return v;
+}
+

@@ -25,6 +25,7 @@ namespace {
 // (:1619-1655).  One workgroup per query head; head_dim is 64.  The cached
 // K row of each thread's first position and the first 64 V rows are read at
 // entry, so their latency overlaps the q/k/v finalisation.
+template <bool Q8, bool K8, bool V8>
 __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     extern __shared__ float lds[];
     float* sc = lds;                  // scores, max_pos
@@ -50,24 +51,32 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
             *(float4*)&vbuf[buf][pr][4 * q4] = *(const float4*)(vb + (size_t)(c0 + pr) * KV + 4 * q4);
         }
     };
+    // loads in the order they are needed (they retire in order): the q/k/v
+    // terms (every thread, indices folded into range: no branch), then the
+    // cached K row of the thread's first position, then the V rows
+    const int j = tid & 31, jv = tid & 63;
+    const float2 cs = a.rope[(size_t)pos * 32 + j];
+    const double qxs = (double)*a.q.xs, kxs = (double)*a.k.xs, vxs = (double)*a.v.xs;
+    const TmqFinRaw<Q8> fq0 = fin_load<Q8>(a.q, h * 64 + 2 * j), fq1 = fin_load<Q8>(a.q, h * 64 + 2 * j + 1);
+    const TmqFinRaw<K8> fk0 = fin_load<K8>(a.k, kv * 64 + 2 * j), fk1 = fin_load<K8>(a.k, kv * 64 + 2 * j + 1);
+    const TmqFinRaw<V8> fv = fin_load<V8>(a.v, kv * 64 + jv);
     float4 kk[16];
-    if (tid < pos) {
-        const float4* kp = (const float4*)(kb + (size_t)tid * KV);
+    {
+        const float4* kp = (const float4*)(kb + (size_t)min(tid, max(pos - 1, 0)) * KV);
 #pragma unroll
         for (int i = 0; i < 16; i++) kk[i] = kp[i];
     }
-    stage(0, 0, 0);
     if (tid < 32) {
-        const float2 cs = a.rope[(size_t)pos * 32 + tid];
-        const float q0 = tmq_fin(a.q, h * 64 + 2 * tid), q1 = tmq_fin(a.q, h * 64 + 2 * tid + 1);
+        const float q0 = fin_finish<Q8>(a.q, fq0, qxs), q1 = fin_finish<Q8>(a.q, fq1, qxs);
         qr[2 * tid] = q0 * cs.x - q1 * cs.y;
         qr[2 * tid + 1] = q0 * cs.y + q1 * cs.x;
-        const float k0 = tmq_fin(a.k, kv * 64 + 2 * tid), k1 = tmq_fin(a.k, kv * 64 + 2 * tid + 1);
+        const float k0 = fin_finish<K8>(a.k, fk0, kxs), k1 = fin_finish<K8>(a.k, fk1, kxs);
         kr[2 * tid] = k0 * cs.x - k1 * cs.y;
         kr[2 * tid + 1] = k0 * cs.y + k1 * cs.x;
     } else if (tid >= 64 && tid < 128) {
-        vn[tid - 64] = tmq_fin(a.v, kv * 64 + tid - 64);
+        vn[tid - 64] = fin_finish<V8>(a.v, fv, vxs);
     }
+    stage(0, 0, 0);
     __syncthreads();
     if (tid < 64) {
         if (h % qpk == 0) {
@@ -197,7 +206,22 @@ __global__ void advance_kernel(TmqEngState* state, int max_pos) {
 }  // namespace
 
 int tmq_launch_attn(const TmqAttnArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(attn_kernel, dim3(a.n_heads), dim3(256), sizeof(float) * 2 * a.max_pos, s, a);
+    // q, k, v: K-split sums (ntiles 0) or Q8_0 tile sums (at most TMQ_FIN_MAXT tiles)
+    if (a.q.ntiles > TMQ_FIN_MAXT || a.k.ntiles > TMQ_FIN_MAXT || a.v.ntiles > TMQ_FIN_MAXT)
+        return (int)hipErrorInvalidValue;
+    const dim3 grid(a.n_heads), blk(256);
+    const size_t lds = sizeof(float) * 2 * a.max_pos;
+    const int code = (a.q.ntiles > 0 ? 4 : 0) | (a.k.ntiles > 0 ? 2 : 0) | (a.v.ntiles > 0 ? 1 : 0);
+    switch (code) {
+    case 0: hipLaunchKernelGGL((attn_kernel<false, false, false>), grid, blk, lds, s, a); break;
+    case 1: hipLaunchKernelGGL((attn_kernel<false, false, true>), grid, blk, lds, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<false, true, false>), grid, blk, lds, s, a); break;
+    case 3: hipLaunchKernelGGL((attn_kernel<false, true, true>), grid, blk, lds, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<true, false, false>), grid, blk, lds, s, a); break;
+    case 5: hipLaunchKernelGGL((attn_kernel<true, false, true>), grid, blk, lds, s, a); break;
+    case 6: hipLaunchKernelGGL((attn_kernel<true, true, false>), grid, blk, lds, s, a); break;
+    default: hipLaunchKernelGGL((attn_kernel<true, true, true>), grid, blk, lds, s, a); break;
+    }
     return (int)hipGetLastError();
 }
 int tmq_launch_argmax(const uint64_t* cand, int n, TmqEngState* state, int32_t* tokens, int max_pos,
