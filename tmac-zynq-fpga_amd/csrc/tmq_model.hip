@@ -130,6 +130,7 @@ struct Prefill {
     int64_t* part = nullptr;
     uint32_t* max_bits = nullptr;
     int dn_split = 4;
+    int o_split = 4;   // attn_output GEMM split over K (finalised by the ffn_norm input)
     int tile[4] = {2, 2, 1, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
 };
 
@@ -328,6 +329,7 @@ int check_state(tmq_model* m) {
 int pf_build_weights(tmq_model* m) {
     Prefill& P = m->pf;
     P.dn_split = std::max(1, env_int("TMQ_PF_SPLIT_DN", P.dn_split));
+    P.o_split = std::max(1, env_int("TMQ_PF_SPLIT_O", P.o_split));
     if (const char* e = getenv("TMQ_PF_TILES")) {
         int t[4];
         if (sscanf(e, "%d,%d,%d,%d", &t[0], &t[1], &t[2], &t[3]) == 4)
@@ -400,7 +402,7 @@ int pf_build_buffers(tmq_model* m, int chunk) {
     parts.push_back({(void**)&P.s, 4 * (size_t)T * I});
     // split-K sums of the down projection, or the Q8_0 V tiles of q/k/v
     const int KV = c.n_kv_heads * TMQ_HEAD_DIM;
-    const size_t part_n = std::max((size_t)P.dn_split * T * H, (size_t)T * KV * (H / TMQ_PF_CHUNK));
+    const size_t part_n = std::max((size_t)std::max(P.dn_split, P.o_split) * T * H, (size_t)T * KV * (H / TMQ_PF_CHUNK));
     parts.push_back({(void**)&P.part, 8 * part_n});
     parts.push_back({(void**)&P.max_bits, 4 * (size_t)T});
     for (int i = 0; i < 4; i++) {
@@ -516,7 +518,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         d.xs = P.xs[3];
         d.row_inv = m->layers[l].down->dev.row_inv;
         d.bias = nullptr;
-        d.split = P.dn_split;
+        d.split = std::min(P.dn_split, I / 64);
         d.ld = H;
         d.K = I;
         d.T_pad = T_pad;
@@ -575,16 +577,27 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         at.n_heads = c.n_heads;
         at.n_kv = c.n_kv_heads;
         LAUNCH_TRY(tmq_launch_pf_attn(at, s));
-        // attn_output + residual
+        // attn_output, split over K; the residual and the finalisation go
+        // with the ffn_norm input
         LAUNCH_TRY(tmq_launch_pf_act(act(TMQ_PF_PLAIN, 1, P.ctx, nullptr, H), s));
-        g = gemm(TMQ_PF_O, W.o, 1);
-        g.nseg = 1;
-        g.seg[0] = pf_seg(Y.o, 0, nullptr);
-        g.x_res = P.x0;
-        g.x_out = P.x1;
+        const int o_split = std::min(P.o_split, H / 64);  // at most one split per 64-column stage
+        g = gemm(TMQ_PF_PART, W.o, 1);
+        g.split = o_split;
+        g.part = P.part;
         LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_o, s));
-        // ffn_norm, gate/up + SwiGLU
-        TmqPfAct a2 = act(TMQ_PF_NORM, 2, P.x1, m->fvec + Y.ffn_norm, H);
+        // residual + attn_output, ffn_norm, gate/up + SwiGLU
+        TmqPfAct a2 = act(TMQ_PF_RESID_NORM, 2, P.x0, m->fvec + Y.ffn_norm, H);
+        a2.d1.part = P.part;
+        a2.d1.rw = W.o.tsum;
+        a2.d1.tx = P.in[1].tsum;
+        a2.d1.xs = P.xs[1];
+        a2.d1.row_inv = Y.o->dev.row_inv;
+        a2.d1.bias = nullptr;
+        a2.d1.split = o_split;
+        a2.d1.ld = H;
+        a2.d1.K = H;
+        a2.d1.T_pad = T_pad;
+        a2.x_out = P.x1;
         a2.zero_bits = P.max_bits;
         LAUNCH_TRY(tmq_launch_pf_act(a2, s));
         g = gemm(TMQ_PF_GU, W.gu, 2);
@@ -600,7 +613,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         a3.max_bits = P.max_bits;
         LAUNCH_TRY(tmq_launch_pf_act(a3, s));
         g = gemm(TMQ_PF_PART, W.dn, 3);
-        g.split = P.dn_split;
+        g.split = std::min(P.dn_split, I / 64);
         g.part = P.part;
         LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_dn, s));
     }

@@ -99,7 +99,6 @@ struct TmqPfSeg {
 
 enum {
     TMQ_PF_QKV = 0,   // q -> RoPE -> q_out; k -> RoPE -> kc; v -> vc
-    TMQ_PF_O = 1,     // x_out = x_res + o
     TMQ_PF_GU = 2,    // s_out = silu(gate) * up, max |s| per token
     TMQ_PF_PART = 3   // int64 digit sums per split
 };
@@ -120,9 +119,6 @@ struct TmqPfGemm {
     float* vc;
     const float2* rope;        // [max_pos][32]
     int32_t H, KV;
-    // O
-    const float* x_res;        // [T][rows]
-    float* x_out;
     // GU
     float* s_out;              // [T][gu_rows]
     uint32_t* max_bits;        // [T]

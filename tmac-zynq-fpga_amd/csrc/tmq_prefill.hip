@@ -303,18 +303,6 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : 1) void pf_gemm_kernel(TmqPfGe
                     *(float4*)dst = make_float4(o[0], o[1], o[2], o[3]);
                 }
             }
-        } else if (MODE == TMQ_PF_O) {
-            if (!live) continue;
-            // residual add (sim/tmac_gguf.cpp:1663)
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const size_t o = (size_t)t * g.rows + rblk(2 * wr + i) * 32 + blk_row(4 * q, lane);
-                    const float4 xr = *(const float4*)(g.x_res + o);
-                    *(float4*)(g.x_out + o) = make_float4(xr.x + fin(i, j, 4 * q), xr.y + fin(i, j, 4 * q + 1),
-                                                          xr.z + fin(i, j, 4 * q + 2), xr.w + fin(i, j, 4 * q + 3));
-                }
         } else if (MODE == TMQ_PF_GU) {
             // SwiGLU (sim/tmac_gguf.cpp:459-461): gate rows in block 0, the
             // same up rows in block 1
@@ -549,7 +537,6 @@ int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
             if (g.seg[i].row0 % (32 * nrb) || (g.seg[i].q8 && !g.part)) return (int)hipErrorInvalidValue;
     switch (g.mode) {
     case TMQ_PF_QKV: return launch_tile<TMQ_PF_QKV>(g, tile, s);
-    case TMQ_PF_O: return launch_tile<TMQ_PF_O>(g, tile, s);
     case TMQ_PF_GU: return launch_tile<TMQ_PF_GU>(g, tile, s);
     case TMQ_PF_PART: return launch_tile<TMQ_PF_PART>(g, tile, s);
     }
