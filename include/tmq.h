@@ -181,7 +181,7 @@ uint64_t tmq_chain_weight_bytes(const tmq_chain* chain);
  * with --fpga-q8 --fpga-q5-0 --fpga-q4k --fpga-q6-k.  Results follow that
  * path's arithmetic (fp32 operations in the reference's order); the token
  * choice is greedy (first index of the largest logit) where the reference
- * samples top-k with rand() (:1975-1994).
+ * samples top-k with rand() (:1974-1990).
  * ------------------------------------------------------------------------ */
 typedef struct tmq_model tmq_model;
 
@@ -194,7 +194,7 @@ typedef struct {
 /* load_tmac (sim/tmac_gguf.cpp:1894-1947): the .tmac container of
  * scripts/extract_tmac.py:6-24, uploaded and checked (shapes, types, sizes).
  * Shapes are taken from the tensors (head_dim 64, RoPE base 1e6, RMSNorm eps
- * 1e-6 as the reference's constants, :136-148, :418, :1528).  max_seq <= 3072
+ * 1e-6 as the reference's constants, :136-148, :451, :1528).  max_seq <= 3072
  * positions of KV cache (0: 512); the reference fixes 256 (:148). */
 int tmq_model_load(tmq_ctx* ctx, const char* path, int max_seq, tmq_model** out);
 int tmq_model_load_mem(tmq_ctx* ctx, const void* data, uint64_t n_bytes, int max_seq, tmq_model** out);
@@ -214,14 +214,14 @@ int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n);
  * token at a time like process_prompt (:1992-1997).  Fails if the model's
  * shapes or formats do not fit the batched kernels. */
 int tmq_model_set_prefill(tmq_model* m, int chunk);
-/* process_embedding + forward_all_layers of one more token (:1955-1967) */
+/* process_embedding + forward_all_layers of one more token (:1958-1972) */
 int tmq_model_feed(tmq_model* m, int32_t token);
 /* as tmq_model_feed, also returning the hidden state after the embedding
- * and after every layer ((n_layers+1) x hidden floats; --dump-layers, :1976) */
+ * and after every layer ((n_layers+1) x hidden floats; --dump-layers, :2001-2018) */
 int tmq_model_feed_dump(tmq_model* m, int32_t token, float* layers_out);
 /* get_logits_q8 (:1820-1845) of the last processed position -> vocab floats */
 int tmq_model_logits(tmq_model* m, float* logits);
-/* generate (:2001-2025) with greedy choice: n x (logits, argmax, feed);
+/* generate (:2025-2045) with greedy choice: n x (logits, argmax, feed);
  * the chosen tokens are returned in out_tokens[n] */
 int tmq_model_generate(tmq_model* m, int n, int32_t* out_tokens);
 /* the same, queued without waiting; read the tokens with tmq_model_tokens */

@@ -47,7 +47,7 @@ static inline uint64_t tmq_act_bytes(int n) { return 16 + (uint64_t)n * 6 + 16; 
 // One GEMV of a chain.  The output epilogue of row r is
 //     v = finalize(acc_r);  if (bias) v = v + bias[r];  if (resid) v = y[r] + v;
 //     y[r] = v
-// (bias: sim/tmac_gguf.cpp:1595-1597; residual: :1663, :1706).
+// (bias: sim/tmac_gguf.cpp:1595-1597; residual: :1670, :1710).
 //
 // Engine GEMVs may instead split K over `kc` workgroups per 64-row group
 // and leave int64 row sums in `kacc` (accumulated with device-scope atomics:
@@ -106,7 +106,7 @@ struct TmqEngState {
 // reference's rms_norm / silu / matmul quantisation, sim/tmac_gguf.cpp:447-461,
 // :1225-1231), so no separate normalisation launch is needed.
 //   EMBED_NORM  x = embedding row of tokens[pos] (process_embedding, :1955)
-//   RESID_NORM  x = x_in + d1 (the residual adds, :1663, :1706)
+//   RESID_NORM  x = x_in + d1 (the residual adds, :1670, :1710)
 //   PLAIN       x = x_in (the attention context)
 //   PRESCALED   x = x_in with max|x| given (SiLU*up from tmq_launch_silu)
 // then, for the two NORM modes, x = rms_norm(x, w) (:447-453) when w is
