@@ -131,7 +131,7 @@ struct Prefill {
     uint32_t* max_bits = nullptr;
     int dn_split = 4;
     int o_split = 4;   // attn_output GEMM split over K (finalised by the ffn_norm input)
-    int tile[4] = {2, 2, 1, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
+    int tile[4] = {2, 2, 3, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
 };
 
 struct tmq_model {
@@ -459,7 +459,7 @@ TmqPfSeg pf_seg(const tmq_tensor* t, int row0, const float* bias) {
 // for tile 1; gate/up pairs: 64 / 32 per tensor) divides every boundary,
 // else the 64-row tile.
 int pf_tile(int want, std::initializer_list<int> bounds) {
-    const int rt = want == 1 ? 64 : 128;
+    const int rt = want == 1 || want == 3 ? 64 : 128;
     for (int b : bounds)
         if (b % rt) return 1;
     return want;

@@ -48,6 +48,7 @@ template <int TILE> struct Tile;
 template <> struct Tile<0> { static constexpr int NWR = 2, NWT = 2, WTB = 2, NBUF = 4; };  // 128 rows x 128 tokens
 template <> struct Tile<1> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBUF = 3; };  // 64 x 128, 2 per CU
 template <> struct Tile<2> { static constexpr int NWR = 2, NWT = 2, WTB = 1, NBUF = 6; };  // 128 x 64
+template <> struct Tile<3> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBUF = 2; };  // 64 x 128, 3 per CU
 constexpr int KC = 2;  // column steps (of 32) per stage
 
 template <int TILE>
@@ -77,7 +78,7 @@ __device__ __forceinline__ void wait_stages(int k) {
 }
 
 template <int MODE, int TILE>
-__global__ __launch_bounds__(256, TILE == 1 ? 2 : 1) void pf_gemm_kernel(TmqPfGemm g) {
+__global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gemm_kernel(TmqPfGemm g) {
     typedef Tile<TILE> C;
     typedef TileGeo<TILE> G;
     constexpr int WTB = C::WTB;
@@ -506,6 +507,7 @@ int launch_tile(const TmqPfGemm& g, int tile, hipStream_t s) {
     case 0: return launch_gemm<MODE, 0>(g, s);
     case 1: return launch_gemm<MODE, 1>(g, s);
     case 2: return launch_gemm<MODE, 2>(g, s);
+    case 3: return launch_gemm<MODE, 3>(g, s);
     }
     return (int)hipErrorInvalidValue;
 }
@@ -521,8 +523,8 @@ int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
     // shapes the kernel assumes: 64-column chunks, whole token tiles of the
     // operand planes, whole row tiles (GU: gate/up tiles of NRB/2 blocks),
     // a split count no larger than the stages, one split for fused epilogues
-    if (tile < 0 || tile > 2) return (int)hipErrorInvalidValue;
-    const int nrb = tile == 1 ? 2 : 4, ntb = tile == 2 ? 2 : 4;
+    if (tile < 0 || tile > 3) return (int)hipErrorInvalidValue;
+    const int nrb = tile == 1 || tile == 3 ? 2 : 4, ntb = tile == 2 ? 2 : 4;
     if (g.K <= 0 || g.K % (32 * KC) || g.T_pad % (32 * ntb) || g.T > g.T_pad || g.split < 1 ||
         g.split > g.K / (32 * KC))
         return (int)hipErrorInvalidValue;
