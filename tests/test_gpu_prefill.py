@@ -66,6 +66,32 @@ def test_prefill_chunks(model):
     assert g1.tolist() == g0.tolist()
 
 
+@pytest.fixture(scope="module")
+def long_model(ctx):
+    import tmq
+    from tmq import model_synth, tmacfile
+    print("[prefill] generating the synthetic C4 model (max_seq 3072)", flush=True)
+    blob = tmacfile.to_bytes(model_synth.gen_model(MODEL_SEED))
+    m = tmq.Model(ctx, blob, max_seq=3072)
+    del blob
+    yield m
+    m.free()
+
+
+@pytest.mark.parametrize("n,chunk", [(1300, 512), (3000, 1024)])
+def test_prefill_long(long_model, n, chunk):
+    """past 512 positions the attention keeps its scores in 2, 4 or 8
+    register passes of 512 (up to the engine's 3072 positions)"""
+    toks = prompt_of(n, 4000 + n)
+    print(f"[prefill] n={n} sequential", flush=True)
+    l0, h0, g0 = run(long_model, toks, 0)
+    print(f"[prefill] n={n} batched, chunks of {chunk}", flush=True)
+    l1, h1, g1 = run(long_model, toks, chunk)
+    assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32))
+    assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32))
+    assert g1.tolist() == g0.tolist()
+
+
 def test_prefill_then_feed(model):
     """a token fed after a batched prompt continues exactly as after a sequential one"""
     toks = prompt_of(20, 5)

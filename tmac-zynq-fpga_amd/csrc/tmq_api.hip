@@ -105,7 +105,7 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     size_t sa = 0, sb = 0, sc = 0, sd = 0;
     switch (type) {
     case TMQ_TYPE_Q8_0: sa = nb * 2 * R * 16; sd = nb * R * 2; break;
-    case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; break;
+    case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sc = nb * R; sd = nb * R * 2; break;
     case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; break;
     case TMQ_TYPE_Q6_K: sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; break;
     }
@@ -208,6 +208,10 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
         if (le) e = (hipError_t)le;
     }
     int badh = 0;
+    if (e == hipSuccess && type == TMQ_TYPE_Q5_0) {
+        le = tmq_launch_q5_fit(t->dev, ctx->stream);
+        if (le) e = (hipError_t)le;
+    }
     if (e == hipSuccess) e = hipMemcpyAsync(&badh, bad, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (aux_tmp) (void)hipFree(aux_tmp);

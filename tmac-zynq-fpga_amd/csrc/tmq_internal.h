@@ -159,6 +159,8 @@ struct ihipStream_t;
 typedef struct ihipStream_t* hipStream_t;
 int tmq_launch_act_prep(const TmqActJobs& jobs, hipStream_t s);
 int tmq_launch_repack(int type, const uint8_t* src, const TmqTensorDev& t, hipStream_t s);
+// Q5_0 per-block fit codes (plane pc) from the planes and row_inv
+int tmq_launch_q5_fit(const TmqTensorDev& t, hipStream_t s);
 int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux_max_abs, float* row_inv,
                        float* row_scale, int* bad_flag, hipStream_t s);
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s);

@@ -57,6 +57,13 @@ __device__ __forceinline__ int wq(float n) {
     return round_away(n);
 }
 
+// floor(x) as int32 in one instruction (LLVM emits v_floor + v_cvt)
+__device__ __forceinline__ int cvt_flr(float x) {
+    int r;
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
 // two int32 -> one dword of saturated int16 (lo = a, hi = b)
 __device__ __forceinline__ uint32_t pk16(int a, int b) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(a, b));
@@ -78,6 +85,8 @@ __device__ __forceinline__ uint4 ld16(const uint8_t* p) {
 }
 __device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *(const gu32*)p; }
 __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const gu16*)p; }
+typedef __attribute__((address_space(1))) const uint8_t gu8;
+__device__ __forceinline__ uint32_t ld1(const uint8_t* p) { return *(const gu8*)p; }
 
 // wave index, known to the compiler to be wave-uniform (an SGPR)
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
@@ -164,6 +173,22 @@ __device__ __forceinline__ void mac4(float e0, float e1, float e2, float e3, flo
     }
 }
 
+// 4 int16 weights (as int32) -> two pairs -> dot with the activation pairs
+// kx, kx+1
+template <class AT>
+__device__ __forceinline__ void mac4i(int w0, int w1, int w2, int w3, const AT& A, int kx, int& sh, int& sl) {
+    const uint32_t P0 = pk16(w0, w1), P1 = pk16(w2, w3);
+    if constexpr (AT::kSink) {
+        A.put(kx, P0);
+        A.put(kx + 1, P1);
+    } else {
+        sh = dot2(P0, A.xh[kx], sh);
+        sl = dot2(P0, A.xl[kx], sl);
+        sh = dot2(P1, A.xh[kx + 1], sh);
+        sl = dot2(P1, A.xl[kx + 1], sl);
+    }
+}
+
 // Each format: Blk = one block of one row in registers, blk_load() fetches
 // it from the planes, blk_mac() multiplies it into the pair sums.
 
@@ -173,9 +198,20 @@ __device__ __forceinline__ void mac4(float e0, float e1, float e2, float e3, flo
 // weights (elements 4g..4g+3) is decoded SWAR-style into four bytes
 // u = nibble | hb<<4, spread into f16 lanes 0x6400|u (= 1024+u) and turned
 // into E = (u-16)*d exactly by one v_fma_mix: (1024+u)*d - 1040*d.
+//
+// Fitted blocks (tensors normalised at upload): within one block of one row
+// the int16 weight is a function g(u) of the 5-bit code u alone, and
+// g(u) = floor(u*A + B) for a pair (A, B) found at upload (q5_fit_kernel)
+// and checked there against the exact g on every code the block holds.
+// A and B are d*row_inv and 0.5 - 16A (fp32, as computed here) moved by a
+// few ulps, coded in one byte per block and row: bits 0-2 dA+4, bits 3-5
+// dB+4, bit 7 set: no pair found, the block takes the exact decode.  The
+// code goes into an f16 lane as the subnormal u*2^-24, so one v_fma_mix
+// with A*2^24 forms u*A + B with a single rounding, and v_cvt_flr gives the
+// weight: 2 instructions per weight instead of 4.
 struct Q5Blk {
     uint4 qs;
-    uint32_t qh, d;
+    uint32_t qh, d, e;
 };
 __device__ __forceinline__ Q5Blk q5_load(const TmqTensorDev& t, int b, int r) {
     const size_t o = (size_t)b * t.rows_pad + r;
@@ -183,17 +219,48 @@ __device__ __forceinline__ Q5Blk q5_load(const TmqTensorDev& t, int b, int r) {
     k.qs = ld16(t.pa + o * 16);
     k.qh = ld4(t.pb + o * 4);
     k.d = ld2(t.pd + o * 2);
+    k.e = ld1(t.pc + o);
     return k;
+}
+// the 5-bit codes of elements 4g..4g+3 as bytes
+__device__ __forceinline__ uint32_t q5_codes(const Q5Blk& k, int g) {
+    const uint32_t nib = (g < 4) ? (dw_of(k.qs, g) & 0x0f0f0f0fu) : ((dw_of(k.qs, g - 4) >> 4) & 0x0f0f0f0fu);
+    const uint32_t hs = (g <= 4) ? (k.qh << (4 - g)) : (k.qh >> (g - 4));
+    return (hs & 0x10101010u) | nib;
+}
+// (A, B) of a fitted block from its code byte
+__device__ __forceinline__ float q5_fit_a(float d, float inv, int da) {
+    return __int_as_float(__float_as_int(d * inv) + da);
+}
+__device__ __forceinline__ float q5_fit_b(float a, int db) {
+    return __int_as_float(__float_as_int(__builtin_fmaf(-16.0f, a, 0.5f)) + db);
+}
+template <class AT>
+__device__ __forceinline__ void q5_mac_fit(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
+    const float a = q5_fit_a(h2f(k.d), inv, (int)(k.e & 7u) - 4);
+    const float a24 = a * 0x1p24f, bb = q5_fit_b(a, (int)((k.e >> 3) & 7u) - 4);
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        const uint32_t U = q5_codes(k, g);
+        const tmq_h2 l0 = lanes01(U), l1 = lanes23(U);
+        mac4i(cvt_flr(__builtin_fmaf((float)l0.x, a24, bb)), cvt_flr(__builtin_fmaf((float)l0.y, a24, bb)),
+              cvt_flr(__builtin_fmaf((float)l1.x, a24, bb)), cvt_flr(__builtin_fmaf((float)l1.y, a24, bb)), A,
+              b * 16 + 2 * g, sh, sl);
+    }
 }
 template <bool CLAMP, class AT>
 __device__ __forceinline__ void q5_mac(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
+    if constexpr (!CLAMP) {
+        if (!(k.e & 0x80u)) {
+            q5_mac_fit(k, A, b, inv, sh, sl);
+            return;
+        }
+    }
     const float d = h2f(k.d);
     const float c = -1040.0f * d;  // exact: 7-bit x 11-bit
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-        const uint32_t nib = (g < 4) ? (dw_of(k.qs, g) & 0x0f0f0f0fu) : ((dw_of(k.qs, g - 4) >> 4) & 0x0f0f0f0fu);
-        const uint32_t hs = (g <= 4) ? (k.qh << (4 - g)) : (k.qh >> (g - 4));
-        const uint32_t U = (hs & 0x10101010u) | nib;
+        const uint32_t U = q5_codes(k, g);
         const tmq_h2 v0 = __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0x64646464u, U, 0x04010400u));
         const tmq_h2 v1 = __builtin_bit_cast(tmq_h2, __builtin_amdgcn_perm(0x64646464u, U, 0x04030402u));
         mac4<CLAMP>(__builtin_fmaf((float)v0.x, d, c), __builtin_fmaf((float)v0.y, d, c),
@@ -1208,6 +1275,44 @@ __global__ void rowstat_kernel(TmqTensorDev t, const float* __restrict__ aux, fl
     }
 }
 
+// Q5_0 fits (see Q5Blk): for block b of row r, the smallest move (dA, dB),
+// |dA|, |dB| <= 3 ulps by growing square rings, for which
+// floor(u*A + B) = g(u) on every code u the block holds; else the exact
+// decode flag.  g(u) is the exact decode's int16: the saturated
+// round-half-away of fl(fl(d*(u-16)) * row_inv).
+__global__ __launch_bounds__(256) void q5_fit_kernel(TmqTensorDev t) {
+    const int r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (r >= t.rows_pad) return;
+    const Q5Blk k = q5_load(t, b, r);
+    const float d = h2f(k.d), inv = t.row_inv[r];
+    uint32_t held = 0;
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        const uint32_t U = q5_codes(k, g);
+#pragma unroll
+        for (int j = 0; j < 4; j++) held |= 1u << ((U >> (8 * j)) & 31u);
+    }
+    int gv[32];
+#pragma unroll
+    for (int u = 0; u < 32; u++) gv[u] = max(-32768, min(32767, round_away((d * (float)(u - 16)) * inv)));
+    uint32_t code = 0x80u;
+    for (int rad = 0; rad <= 3 && code == 0x80u; rad++)
+        for (int da = -rad; da <= rad && code == 0x80u; da++)
+            for (int db = -rad; db <= rad && code == 0x80u; db++) {
+                if (abs(da) != rad && abs(db) != rad) continue;
+                const float a = q5_fit_a(d, inv, da), bb = q5_fit_b(a, db);
+                bool ok = true;
+#pragma unroll
+                for (int u = 0; u < 32; u++)
+                    if ((held >> u) & 1u) {
+                        const int w = max(-32768, min(32767, cvt_flr(__builtin_fmaf((float)u, a, bb))));
+                        ok = ok && w == gv[u];
+                    }
+                if (ok) code = (uint32_t)(da + 4) | ((uint32_t)(db + 4) << 3);
+            }
+    *(uint8_t*)(t.pc + (size_t)b * t.rows_pad + r) = (uint8_t)code;
+}
+
 // ----------------------------------------------------------- Q8 tile
 // axi_vecmul_tile_q8: q8_W column-major [k][n], cs[n*2 + k/32] UQ8.8,
 // deq = (q8*cs) >> 8, result[n] = sum_k vec[k]*deq (sim/fpga_sim.hpp:316-349)
@@ -1475,6 +1580,12 @@ int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux, float* row_inv, 
     const int bs = 64;
     hipLaunchKernelGGL(rowstat_kernel, dim3((t.rows_pad + bs - 1) / bs), dim3(bs), 0, s, t, aux,
                        row_inv, row_scale, bad);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_q5_fit(const TmqTensorDev& t, hipStream_t s) {
+    if (t.type != kQ5_0 || !t.pc) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(q5_fit_kernel, dim3((t.rows_pad + 255) / 256, t.nb), dim3(256), 0, s, t);
     return (int)hipGetLastError();
 }
 

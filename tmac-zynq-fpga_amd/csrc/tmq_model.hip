@@ -131,7 +131,8 @@ struct Prefill {
     uint32_t* max_bits = nullptr;
     int dn_split = 4;
     int o_split = 4;   // attn_output GEMM split over K (finalised by the ffn_norm input)
-    int tile[4] = {2, 2, 3, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
+    int qkv_split = 7; // q/k/v GEMM split over K (finished by pf_qkv_fin)
+    int tile[4] = {3, 2, 3, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
 };
 
 struct tmq_model {
@@ -330,6 +331,7 @@ int pf_build_weights(tmq_model* m) {
     Prefill& P = m->pf;
     P.dn_split = std::max(1, env_int("TMQ_PF_SPLIT_DN", P.dn_split));
     P.o_split = std::max(1, env_int("TMQ_PF_SPLIT_O", P.o_split));
+    P.qkv_split = std::max(1, env_int("TMQ_PF_SPLIT_QKV", P.qkv_split));
     if (const char* e = getenv("TMQ_PF_TILES")) {
         int t[4];
         if (sscanf(e, "%d,%d,%d,%d", &t[0], &t[1], &t[2], &t[3]) == 4)
@@ -400,9 +402,11 @@ int pf_build_buffers(tmq_model* m, int chunk) {
     parts.push_back({(void**)&P.qb, 4 * (size_t)T * H});
     parts.push_back({(void**)&P.ctx, 4 * (size_t)T * H});
     parts.push_back({(void**)&P.s, 4 * (size_t)T * I});
-    // split-K sums of the down projection, or the Q8_0 V tiles of q/k/v
+    // split-K sums of the down projection and attn_output, or those of q/k/v
+    // followed by the Q8_0 V tiles
     const int KV = c.n_kv_heads * TMQ_HEAD_DIM;
-    const size_t part_n = std::max((size_t)std::max(P.dn_split, P.o_split) * T * H, (size_t)T * KV * (H / TMQ_PF_CHUNK));
+    const size_t part_n = std::max((size_t)std::max(P.dn_split, P.o_split) * T * H,
+                                   (size_t)P.qkv_split * T * (H + 2 * KV) + (size_t)T * KV * (H / TMQ_PF_CHUNK));
     parts.push_back({(void**)&P.part, 8 * part_n});
     parts.push_back({(void**)&P.max_bits, 4 * (size_t)T});
     for (int i = 0; i < 4; i++) {
@@ -537,8 +541,11 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         }
         a0.x_out = P.x0;
         LAUNCH_TRY(tmq_launch_pf_act(a0, s));
-        // q, k, v -> RoPE -> q buffer and this layer's caches
-        TmqPfGemm g = gemm(TMQ_PF_QKV, W.qkv, 0);
+        // q, k, v -> RoPE -> q buffer and this layer's caches; split over K,
+        // finished by pf_qkv_fin (which also folds Q8_0 V tiles)
+        const int qkv_split = std::min(P.qkv_split, H / 64);
+        TmqPfGemm g = gemm(qkv_split > 1 ? TMQ_PF_QKVS : TMQ_PF_QKV, W.qkv, 0);
+        g.split = qkv_split;
         g.nseg = 3;
         g.seg[0] = pf_seg(Y.q, 0, fv(Y.bq));
         g.seg[1] = pf_seg(Y.k, H, fv(Y.bk));
@@ -547,24 +554,32 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.kc = m->kc + (size_t)l * c.max_seq * KV;
         g.vc = m->vc + (size_t)l * c.max_seq * KV;
         g.rope = m->rope;
-        g.part = P.part;  // Q8_0 V tiles (the down projection's sums were consumed above)
+        // (the down projection's sums were consumed above)
+        g.part = P.part;
+        g.tpart = P.part + (qkv_split > 1 ? (size_t)qkv_split * T_pad * (H + 2 * KV) : 0);
         LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_qkv, s));
-        if (Y.v->dev.type == TMQ_TYPE_Q8_0) {
-            TmqPfVFold vf{};
-            vf.part = P.part;
-            vf.rw_c = W.qkv.csum;
-            vf.tx_c = P.in[0].csum;
-            vf.xs = P.xs[0];
-            vf.row_scale = Y.v->dev.row_scale;
-            vf.bias = fv(Y.bv);
-            vf.vc = g.vc;
-            vf.rows = KV;
-            vf.row0 = H + KV;
-            vf.nt = H / TMQ_PF_CHUNK;
-            vf.T = T;
-            vf.T_pad = T_pad;
-            vf.p0 = p0;
-            LAUNCH_TRY(tmq_launch_pf_vfold(vf, s));
+        if (qkv_split > 1 || Y.v->dev.type == TMQ_TYPE_Q8_0) {
+            TmqPfQkvFin f{};
+            f.part = qkv_split > 1 ? P.part : nullptr;
+            f.tpart = g.tpart;
+            f.rw_t = W.qkv.tsum;
+            f.rw_c = W.qkv.csum;
+            f.tx_t = P.in[0].tsum;
+            f.tx_c = P.in[0].csum;
+            f.xs = P.xs[0];
+            for (int i = 0; i < 3; i++) f.seg[i] = g.seg[i];
+            f.q_out = g.q_out;
+            f.kc = g.kc;
+            f.vc = g.vc;
+            f.rope = g.rope;
+            f.split = qkv_split;
+            f.K = H;
+            f.T = T;
+            f.T_pad = T_pad;
+            f.p0 = p0;
+            f.H = H;
+            f.KV = KV;
+            LAUNCH_TRY(tmq_launch_pf_qkv_fin(f, s));
         }
         // attention over positions 0 .. p0+t
         TmqPfAttn at{};
@@ -637,7 +652,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
 int pf_prompt(tmq_model* m, int n, int* done) {
     *done = 0;
     const int qpk = m->cfg.n_heads / m->cfg.n_kv_heads;
-    int lim = n;
+    int lim = std::min(n, TMQ_PF_ATTN_MAXPOS);
     while (lim > 0 && tmq_pf_attn_lds(qpk, lim) > TMQ_PF_ATTN_LDS_MAX) lim--;
     if (lim < 2) return 0;
     int rc;

@@ -100,7 +100,8 @@ struct TmqPfSeg {
 enum {
     TMQ_PF_QKV = 0,   // q -> RoPE -> q_out; k -> RoPE -> kc; v -> vc
     TMQ_PF_GU = 2,    // s_out = silu(gate) * up, max |s| per token
-    TMQ_PF_PART = 3   // int64 digit sums per split
+    TMQ_PF_PART = 3,  // int64 digit sums per split
+    TMQ_PF_QKVS = 4   // q, k, v split over K: int64 sums per split; pf_qkv_fin finishes
 };
 struct TmqPfGemm {
     int32_t mode, K, T, T_pad, p0, split, gu_rows, nseg;
@@ -122,21 +123,31 @@ struct TmqPfGemm {
     // GU
     float* s_out;              // [T][gu_rows]
     uint32_t* max_bits;        // [T]
-    // PART; QKV: the Q8_0 segment's per-tile sums [K/64][seg rows][T_pad]
+    // PART, QKVS (rows of the Q8_0 segment excepted)
     int64_t* part;             // [split][T_pad][rows]
+    // QKV, QKVS: the Q8_0 segment's per-tile sums
+    int64_t* tpart;            // [K/64][seg rows][T_pad]
 };
 
-// Q8_0 rows of a QKV GEMM (the per-tile digit sums it left in `part`)
-// folded into values (sim/tmac_gguf.cpp:1075-1076) and stored as V cache rows.
-struct TmqPfVFold {
-    const int64_t* part;       // [nt][rows][T_pad]
-    const int32_t* rw_c;       // plane-set rows (row0 + r) x nt
-    const int32_t* tx_c;       // [T_pad][nt]
+// q, k, v rows finished from the int64 sums a QKV / QKVS GEMM left: the split
+// sums of the Q5_0 / K-quant rows finalised (sim/tmac_gguf.cpp:1303-1305),
+// the Q8_0 V rows' tile sums folded (:1075-1076), + bias (:1595-1597), RoPE
+// on q and k (:1537-1539), stored to q_out and this layer's caches.  With
+// `part` null (a QKV GEMM, which finished the other rows) only the Q8_0 rows.
+struct TmqPfQkvFin {
+    const int64_t* part;       // [split][T_pad][H + 2 KV] or null
+    const int64_t* tpart;      // [K/64][KV][T_pad] when seg[2] is Q8_0
+    const int32_t* rw_t;       // plane-set rows: sum (w - 128)
+    const int32_t* rw_c;       // [H + 2 KV][K/64]
+    const int32_t* tx_t;       // [T_pad]
+    const int32_t* tx_c;       // [T_pad][K/64]
     const float* xs;           // [T_pad]
-    const float* row_scale;    // [rows]
-    const float* bias;         // [rows] or null
-    float* vc;                 // this layer's V cache [max_pos][rows]
-    int32_t rows, row0, nt, T, T_pad, p0;
+    TmqPfSeg seg[3];           // q, k, v
+    float* q_out;              // [T][H]
+    float* kc;                 // this layer's caches [max_pos][KV]
+    float* vc;
+    const float2* rope;        // [max_pos][32]
+    int32_t split, K, T, T_pad, p0, H, KV, pad_;
 };
 
 // Attention of T consecutive positions p0.. (one workgroup per token and KV
@@ -187,8 +198,10 @@ int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s);
 int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s);
 int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);
-int tmq_launch_pf_vfold(const TmqPfVFold& f, hipStream_t s);
+int tmq_launch_pf_qkv_fin(const TmqPfQkvFin& f, hipStream_t s);
 size_t tmq_pf_attn_lds(int qpk, int npos);
-// dynamic LDS the attention kernel may take beside its ~35 KiB of static
-// buffers (160 KiB per workgroup in all)
-#define TMQ_PF_ATTN_LDS_MAX (124 * 1024)
+// dynamic LDS the attention kernel may take beside its ~36 KiB of static
+// buffers (160 KiB per workgroup in all), and the positions it attends over
+// at most (its scores are held in registers, 512 positions per pass)
+#define TMQ_PF_ATTN_LDS_MAX (120 * 1024)
+#define TMQ_PF_ATTN_MAXPOS 4096

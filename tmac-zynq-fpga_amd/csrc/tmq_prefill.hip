@@ -82,6 +82,8 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     typedef Tile<TILE> C;
     typedef TileGeo<TILE> G;
     constexpr int WTB = C::WTB;
+    constexpr bool QKVM = MODE == TMQ_PF_QKV || MODE == TMQ_PF_QKVS;    // q|k|v segments
+    constexpr bool PARTM = MODE == TMQ_PF_PART || MODE == TMQ_PF_QKVS;  // int64 sums out
     __shared__ __attribute__((aligned(1024))) int8_t lds[G::NBUF][G::STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -119,15 +121,15 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     const int st1 = (int)((int64_t)(bz + 1) * nst_all / g.split);
     const int nst = st1 - st0;
 
-    // runtime segment (QKV): the tile lies inside one tensor
+    // runtime segment (QKV, QKVS): the tile lies inside one tensor
     int si = 0;
-    if (MODE == TMQ_PF_QKV) {
+    if (QKVM) {
         const int r0 = rblk(0) * 32;
         if (g.nseg > 1 && r0 >= g.seg[1].row0) si = 1;
         if (g.nseg > 2 && r0 >= g.seg[2].row0) si = 2;
     }
     const TmqPfSeg S = si == 0 ? g.seg[0] : si == 1 ? g.seg[1] : g.seg[2];
-    const bool q8 = MODE == TMQ_PF_QKV && S.q8;
+    const bool q8 = QKVM && S.q8;
     const bool hasb = MODE == TMQ_PF_QKV && S.bias != nullptr;
 
     // the epilogue's per-row constants of the workgroup's rows, in LDS:
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     __shared__ int32_t c_rw[G::NRB][32];
     __shared__ float c_bias[G::NRB][32];
     __shared__ uint64_t c_tab[32];
-    if (MODE != TMQ_PF_PART) {
+    if (!PARTM) {
         for (int idx = threadIdx.x; idx < G::NRB * 32; idx += 256) {
             const int i = idx >> 5, r = idx & 31;
             const TmqPfSeg Sg = MODE == TMQ_PF_GU ? ((i & 1) ? g.seg[1] : g.seg[0]) : S;
@@ -216,9 +218,9 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
                     acc[1][j][1] = mfma(b1, c, acc[1][j][1]);
                 }
             }
-            if (MODE == TMQ_PF_QKV && q8 && (kc & 1)) {
+            if (QKVM && q8 && (kc & 1)) {
                 // Q8_0: the 64-column tile just completed, as an int64 digit
-                // sum per element, for pf_vfold_kernel
+                // sum per element, for pf_qkv_fin_kernel
                 const int tile = (ks + kc) >> 1;
 #pragma unroll
                 for (int j = 0; j < WTB; j++) {
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
 #pragma unroll
                     for (int i = 0; i < 2; i++) {
                         // [tile][row][token]: the 32 tokens of a row are contiguous
-                        int64_t* out = g.part + ((size_t)tile * S.rows + rblk(2 * wr + i) * 32 - S.row0) * g.T_pad + t;
+                        int64_t* out = g.tpart + ((size_t)tile * S.rows + rblk(2 * wr + i) * 32 - S.row0) * g.T_pad + t;
 #pragma unroll
                         for (int v = 0; v < 16; v++)
                             out[(size_t)blk_row(v, lane) * g.T_pad] = 65536 * (int64_t)acc[i][j][0][v] +
@@ -243,7 +245,8 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
 
-    if (MODE == TMQ_PF_PART) {
+    if (QKVM && q8) return;  // pf_qkv_fin_kernel finishes these rows
+    if (PARTM) {
 #pragma unroll
         for (int j = 0; j < WTB; j++) {
             const int t = tw0 + j * 32 + (lane & 31);
@@ -258,7 +261,6 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         }
         return;
     }
-    if (MODE == TMQ_PF_QKV && q8) return;  // pf_vfold_kernel finishes these rows
 
     // element v of block (i, j), finalised (sim/tmac_gguf.cpp:1303-1305) +
     // bias (:1595-1597)
@@ -335,12 +337,16 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
 // head g: the decode engine's chains (attn_kernel) per query -- scores
 // summed over d in order and /8, max, exp terms summed over positions in
 // order, log via fp64, weights, the context summed over positions in order.
-// The query rows are wave-uniform and read through the scalar cache.
+// The query rows are wave-uniform and read through the scalar cache.  Each
+// thread keeps the scores of its positions (tid + 512 k, k < NPASS) in
+// registers; LDS holds the exp terms, then the weights, of every position.
 typedef __attribute__((address_space(4))) const float cf32;
 constexpr int VT_LD = 68;  // floats between dimensions of a transposed V chunk
-__global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
+template <int NPASS>
+__global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_attn_kernel(TmqPfAttn a) {
     extern __shared__ float lds[];
     __shared__ float stat[2][8];
+    __shared__ float red[8][8];  // [wave][head] maxima
     __shared__ uint64_t tab[32];
     // V chunks of 64 positions, transposed (dimension-major, VT_LD apart) so
     // that the lane of dimension d reads four positions at once; double-buffered
@@ -350,18 +356,24 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
     const int qpk = a.n_heads / a.n_kv, KV = a.n_kv * 64, H = a.n_heads * 64;
     const int np = a.p0 + t + 1, npad = (np + 3) & ~3;
     const int wv = tid >> 6, ln = tid & 63;
-    float* sc = lds;                 // [qpk][npad]
-    float* ex = sc + qpk * npad;     // [qpk][npad]
+    float* ex = lds;  // [qpk][npad]
     const float* kb = a.kc + g * 64;
     const float* vbase = a.vc + g * 64;
     const cf32* qg = (const cf32*)(a.q + (size_t)t * H + g * qpk * 64);
     if (tid < 32) tab[tid] = tmq_math::exp2_tab(tid);
-    for (int p = tid; p < np; p += nt) {
+    // scores of positions tid + 512 k
+    float scr[NPASS][8];
+#pragma unroll
+    for (int k = 0; k < NPASS; k++) {
+        if (k > 0 && k * 512 >= np) break;
+        const int p = tid + k * 512;
         float4 kk[16];
-        const float4* kp = (const float4*)(kb + (size_t)p * KV);
+        const float4* kp = (const float4*)(kb + (size_t)min(p, np - 1) * KV);
 #pragma unroll
         for (int i = 0; i < 16; i++) kk[i] = kp[i];
-        for (int h = 0; h < qpk; h++) {
+#pragma unroll
+        for (int h = 0; h < 8; h++) {
+            if (h >= qpk) break;
             const cf32* qh = qg + h * 64;
             float s = 0.0f;
 #pragma unroll
@@ -371,21 +383,44 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
                 s += qh[4 * i + 2] * kk[i].z;
                 s += qh[4 * i + 3] * kk[i].w;
             }
-            sc[h * npad + p] = s / 8.0f;
+            scr[k][h] = s / 8.0f;
         }
     }
-    __syncthreads();
-    if (wv < qpk) {
+    // max per head: the thread's, the wave's, then the workgroup's (fmaxf
+    // is exact in any order)
+    float mx[8];
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
         float m = -__builtin_inff();
-        for (int p = ln; p < np; p += 64) m = fmaxf(m, sc[wv * npad + p]);
+#pragma unroll
+        for (int k = 0; k < NPASS; k++)
+            if (h < qpk && tid + k * 512 < np) m = fmaxf(m, scr[k][h]);
         for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        if (ln == 0) stat[0][wv] = m;
+        mx[h] = m;
+    }
+    if (ln == 0)
+#pragma unroll
+        for (int h = 0; h < 8; h++) red[wv][h] = mx[h];
+    __syncthreads();
+    if (tid < 8) {
+        float m = red[0][tid];
+        for (int w = 1; w < 8; w++) m = fmaxf(m, red[w][tid]);
+        stat[0][tid] = m;
     }
     __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 8; h++) mx[h] = stat[0][h];
     const Exp2TabLds et{tab};
-    for (int i = tid; i < qpk * np; i += nt) {
-        const int h = i / np, p = i - h * np;
-        ex[h * npad + p] = tmq_math::tmq_expf_tab(sc[h * npad + p] - stat[0][h], et);
+    // exp terms (scores - max) into LDS
+#pragma unroll
+    for (int k = 0; k < NPASS; k++) {
+        const int p = tid + k * 512;
+        if (p >= np) break;
+#pragma unroll
+        for (int h = 0; h < 8; h++) {
+            if (h >= qpk) break;
+            ex[h * npad + p] = tmq_math::tmq_expf_tab(scr[k][h] - mx[h], et);
+        }
     }
     __syncthreads();
     if (wv == 0 && ln < qpk) {
@@ -393,25 +428,41 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
         const float* e = ex + ln * npad;
         float es = 0.0f;
         int p = 0;
-        for (; p + 16 <= np; p += 16) {
-            float4 v[4];
+        // 32 terms per step: eight LDS reads in flight, then the adds in order
+        for (; p + 32 <= np; p += 32) {
+            float4 v[8];
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = *(const float4*)(e + p + 4 * j);
+            for (int j = 0; j < 8; j++) v[j] = *(const float4*)(e + p + 4 * j);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < 8; j++) {
                 es += v[j].x;
                 es += v[j].y;
                 es += v[j].z;
                 es += v[j].w;
             }
         }
-        for (; p < np; p++) es += e[p];
+        if (p < np) {
+            // the last 1-31 terms: reads clamped into range, the terms past
+            // the end added as +0 (es is never -0, so x + 0 = x)
+            float v[32];
+#pragma unroll
+            for (int j = 0; j < 32; j++) v[j] = e[min(p + j, np - 1)];
+#pragma unroll
+            for (int j = 0; j < 32; j++) es += p + j < np ? v[j] : 0.0f;
+        }
         stat[1][ln] = (float)log((double)es) + stat[0][ln];
     }
     __syncthreads();
-    for (int i = tid; i < qpk * np; i += nt) {
-        const int h = i / np, p = i - h * np;
-        ex[h * npad + p] = tmq_math::tmq_expf_tab(sc[h * npad + p] - stat[1][h], et);
+    // weights (scores - log-sum) over the exp terms
+#pragma unroll
+    for (int k = 0; k < NPASS; k++) {
+        const int p = tid + k * 512;
+        if (p >= np) break;
+#pragma unroll
+        for (int h = 0; h < 8; h++) {
+            if (h >= qpk) break;
+            ex[h * npad + p] = tmq_math::tmq_expf_tab(scr[k][h] - stat[1][h], et);
+        }
     }
     // context, 64 positions per chunk; the next chunk's V rows are loaded
     // into registers while the current one is summed (512 threads x 2 float4
@@ -444,15 +495,56 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
             const float* e = ex + wv * npad + c0;
             const float* vt = vb2[buf] + ln * VT_LD;
             int pr = 0;
-            for (; pr + 4 <= nr; pr += 4) {
-                const float4 e4 = *(const float4*)(e + pr);
-                const float4 v4 = *(const float4*)(vt + pr);
-                acc += e4.x * v4.x;
-                acc += e4.y * v4.y;
-                acc += e4.z * v4.z;
-                acc += e4.w * v4.w;
+            // steps of 8 positions, each step's LDS reads issued during the
+            // previous step's adds
+            float4 ea[2], va[2], eb[2], vb[2];
+            auto ld = [&](float4* ev, float4* vv, int o) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    ev[j] = *(const float4*)(e + o + 4 * j);
+                    vv[j] = *(const float4*)(vt + o + 4 * j);
+                }
+            };
+            auto mac = [&](const float4* ev, const float4* vv) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    acc += ev[j].x * vv[j].x;
+                    acc += ev[j].y * vv[j].y;
+                    acc += ev[j].z * vv[j].z;
+                    acc += ev[j].w * vv[j].w;
+                }
+            };
+            if (nr == 64) {
+                ld(ea, va, 0);
+#pragma unroll
+                for (int o = 0; o < 64; o += 16) {
+                    ld(eb, vb, o + 8);
+                    mac(ea, va);
+                    if (o + 16 < 64) ld(ea, va, o + 16);
+                    mac(eb, vb);
+                }
+                pr = 64;
             }
-            for (; pr < nr; pr++) acc += e[pr] * vt[pr];
+            for (; pr + 8 <= nr; pr += 8) {
+                ld(ea, va, pr);
+                mac(ea, va);
+            }
+            if (pr < nr) {
+                // the last 1-7 positions: reads clamped into range, the
+                // terms past the end added as +0 (acc is never -0)
+                float ev[8], vv[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int q = min(pr + j, nr - 1);
+                    ev[j] = e[q];
+                    vv[j] = vt[q];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float m = ev[j] * vv[j];
+                    acc += pr + j < nr ? m : 0.0f;
+                }
+            }
         }
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -465,23 +557,104 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(TmqPfAttn a) {
     if (wv < qpk) a.ctx[(size_t)t * H + (g * qpk + wv) * 64 + ln] = acc;
 }
 
-// One (token, Q8_0 row) of a QKV GEMM: the tiles' digit sums + corrections
-// folded in order in double, plus the bias, stored into the V cache.
-__global__ __launch_bounds__(256) void pf_vfold_kernel(TmqPfVFold f) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= f.T * f.rows) return;
-    const int r = i / f.T, t = i - r * f.T;
-    const int32_t* rw = f.rw_c + (size_t)(f.row0 + r) * f.nt;
-    const int32_t* tx = f.tx_c + (size_t)t * f.nt;
-    const double xs = (double)f.xs[t], rs = (double)f.row_scale[r];
-    float y = 0.0f;
-    for (int c = 0; c < f.nt; c++) {
-        const int64_t p = f.part[((size_t)c * f.rows + r) * f.T_pad + t] + 128 * ((int64_t)rw[c] + tx[c]) +
-                          16384 * TMQ_PF_CHUNK;
-        y = (float)((double)y + ((double)p * xs) * rs);
+// q, k, v finished (TmqPfQkvFin).  Threads [0, nA): one token and four
+// consecutive rows of the q / k and Q5_0 / K-quant v rows, from the split
+// sums (rows fastest, one float4 store); threads of the blocks after: one
+// token and row of a Q8_0 v segment, from its tile sums (tokens fastest).
+__global__ __launch_bounds__(256) void pf_qkv_fin_kernel(TmqPfQkvFin f) {
+    const bool vq8 = f.seg[2].q8 != 0;
+    const int nr = f.part ? f.H + (vq8 ? 1 : 2) * f.KV : 0;  // rows from split sums
+    const int g4 = nr >> 2, nA = f.T * g4, nbA = (nA + 255) >> 8;
+    if ((int)blockIdx.x < nbA) {
+        const int i = blockIdx.x * 256 + threadIdx.x;
+        if (i >= nA) return;
+        const int t = i / g4, row = (i - t * g4) * 4;
+        const int si = row < f.H ? 0 : row < f.H + f.KV ? 1 : 2;
+        const int rr = row - (si == 0 ? 0 : si == 1 ? f.H : f.H + f.KV);
+        const float* inv = si == 0 ? f.seg[0].row_inv : si == 1 ? f.seg[1].row_inv : f.seg[2].row_inv;
+        const float* bias = si == 0 ? f.seg[0].bias : si == 1 ? f.seg[1].bias : f.seg[2].bias;
+        const int pos = f.p0 + t;
+        const int ld = f.H + 2 * f.KV;
+        // every load first
+        const int4 rw = *(const int4*)(f.rw_t + row);
+        const int64_t tc = 128 * (int64_t)f.tx_t[t] + 16384 * (int64_t)f.K;
+        const double xs = (double)f.xs[t];
+        float ri[4], bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 4; k++) ri[k] = inv[rr + k];
+        if (bias)
+#pragma unroll
+            for (int k = 0; k < 4; k++) bs[k] = bias[rr + k];
+        float4 cs = make_float4(1.0f, 0.0f, 1.0f, 0.0f);
+        if (si != 2) cs = *(const float4*)(f.rope + (size_t)pos * 32 + ((rr & 63) >> 1));
+        int64_t a[4] = {tc + 128 * (int64_t)rw.x, tc + 128 * (int64_t)rw.y, tc + 128 * (int64_t)rw.z,
+                        tc + 128 * (int64_t)rw.w};
+        // the split sums in batches of 8 (loads first; indices clamped, the
+        // surplus added as 0)
+        for (int s0 = 0; s0 < f.split; s0 += 8) {
+            longlong2 u[8], v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const longlong2* p =
+                    (const longlong2*)(f.part + ((size_t)min(s0 + j, f.split - 1) * f.T_pad + t) * ld + row);
+                u[j] = p[0];
+                v[j] = p[1];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const bool in = s0 + j < f.split;
+                a[0] += in ? u[j].x : 0;
+                a[1] += in ? u[j].y : 0;
+                a[2] += in ? v[j].x : 0;
+                a[3] += in ? v[j].y : 0;
+            }
+        }
+        // finalised (sim/tmac_gguf.cpp:1303-1305) + bias (:1595-1597)
+        float o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            o[k] = (float)(((double)a[k] * xs) / (double)ri[k]);
+            if (bias) o[k] = o[k] + bs[k];
+        }
+        if (si != 2) {
+            // apply_rope (sim/tmac_gguf.cpp:1537-1539): pairs (rr, rr+1), (rr+2, rr+3)
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const float y0 = o[2 * k], y1 = o[2 * k + 1];
+                const float c = k ? cs.z : cs.x, sn = k ? cs.w : cs.y;
+                o[2 * k] = y0 * c - y1 * sn;
+                o[2 * k + 1] = y0 * sn + y1 * c;
+            }
+        }
+        float* dst = si == 0   ? f.q_out + (size_t)t * f.H + rr
+                     : si == 1 ? f.kc + (size_t)pos * f.KV + rr
+                               : f.vc + (size_t)pos * f.KV + rr;
+        *(float4*)dst = make_float4(o[0], o[1], o[2], o[3]);
+        return;
     }
-    if (f.bias) y = y + f.bias[r];
-    f.vc[(size_t)(f.p0 + t) * f.rows + r] = y;
+    // Q8_0 v: the tiles folded in order (sim/tmac_gguf.cpp:1075-1076)
+    const int i = ((int)blockIdx.x - nbA) * 256 + threadIdx.x;
+    if (!vq8 || i >= f.T * f.KV) return;
+    const int r = i / f.T, t = i - r * f.T, nt = f.K / TMQ_PF_CHUNK;
+    const int32_t* rw = f.rw_c + (size_t)(f.H + f.KV + r) * nt;
+    const int32_t* tx = f.tx_c + (size_t)t * nt;
+    const double xs = (double)f.xs[t], rs = (double)f.seg[2].row_scale[r];
+    float y = 0.0f;
+    for (int c0 = 0; c0 < nt; c0 += 8) {
+        // 8 tiles' loads first (indices clamped), then the ordered fold
+        int64_t p[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int c = min(c0 + j, nt - 1);
+            p[j] = f.tpart[((size_t)c * f.KV + r) * f.T_pad + t] + 128 * ((int64_t)rw[c] + tx[c]) +
+                   16384 * TMQ_PF_CHUNK;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (c0 + j < nt) y = (float)((double)y + ((double)p[j] * xs) * rs);
+    }
+    if (f.seg[2].bias) y = y + f.seg[2].bias[r];
+    f.vc[(size_t)(f.p0 + t) * f.KV + r] = y;
 }
 
 // The decode engine's residual state after the prefill's last token.
@@ -516,7 +689,7 @@ int launch_tile(const TmqPfGemm& g, int tile, hipStream_t s) {
 
 size_t tmq_pf_attn_lds(int qpk, int npos) {
     const size_t npad = ((size_t)npos + 3) & ~(size_t)3;
-    return sizeof(float) * 2 * (size_t)qpk * npad;
+    return sizeof(float) * (size_t)qpk * npad;
 }
 
 int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
@@ -528,37 +701,51 @@ int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
     if (g.K <= 0 || g.K % (32 * KC) || g.T_pad % (32 * ntb) || g.T > g.T_pad || g.split < 1 ||
         g.split > g.K / (32 * KC))
         return (int)hipErrorInvalidValue;
-    if (g.mode != TMQ_PF_PART && g.split != 1) return (int)hipErrorInvalidValue;
+    if (g.mode != TMQ_PF_PART && g.mode != TMQ_PF_QKVS && g.split != 1) return (int)hipErrorInvalidValue;
     if (g.mode == TMQ_PF_GU) {
         if (g.gu_rows % (16 * nrb) || g.rows != 2 * g.gu_rows) return (int)hipErrorInvalidValue;
     } else if (g.rows % (32 * nrb)) {
         return (int)hipErrorInvalidValue;
     }
-    if (g.mode == TMQ_PF_QKV)
+    if (g.mode == TMQ_PF_QKV || g.mode == TMQ_PF_QKVS)
         for (int i = 0; i < g.nseg; i++)
-            if (g.seg[i].row0 % (32 * nrb) || (g.seg[i].q8 && !g.part)) return (int)hipErrorInvalidValue;
+            if (g.seg[i].row0 % (32 * nrb) || (g.seg[i].q8 && !g.tpart)) return (int)hipErrorInvalidValue;
+    if ((g.mode == TMQ_PF_PART || g.mode == TMQ_PF_QKVS) && !g.part) return (int)hipErrorInvalidValue;
     switch (g.mode) {
     case TMQ_PF_QKV: return launch_tile<TMQ_PF_QKV>(g, tile, s);
     case TMQ_PF_GU: return launch_tile<TMQ_PF_GU>(g, tile, s);
     case TMQ_PF_PART: return launch_tile<TMQ_PF_PART>(g, tile, s);
+    case TMQ_PF_QKVS: return launch_tile<TMQ_PF_QKVS>(g, tile, s);
     }
     return (int)hipErrorInvalidValue;
 }
 
-int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s) {
-    const int qpk = a.n_heads / a.n_kv;
-    if (qpk < 1 || qpk > 8 || a.n_heads % a.n_kv) return (int)hipErrorInvalidValue;
-    const size_t lds = tmq_pf_attn_lds(qpk, a.p0 + a.T);
+namespace {
+template <int NPASS>
+int launch_attn(const TmqPfAttn& a, size_t lds, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)pf_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           TMQ_PF_ATTN_LDS_MAX);
+        hipError_t e = hipFuncSetAttribute((const void*)pf_attn_kernel<NPASS>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, TMQ_PF_ATTN_LDS_MAX);
         if (e != hipSuccess) return (int)e;
         attr = true;
     }
-    if (lds > TMQ_PF_ATTN_LDS_MAX) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(pf_attn_kernel, dim3(a.T, a.n_kv), dim3(512), lds, s, a);
+    hipLaunchKernelGGL((pf_attn_kernel<NPASS>), dim3(a.T, a.n_kv), dim3(512), lds, s, a);
     return (int)hipGetLastError();
+}
+}  // namespace
+
+int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s) {
+    const int qpk = a.n_heads / a.n_kv, np = a.p0 + a.T;
+    if (qpk < 1 || qpk > 8 || a.n_heads % a.n_kv || a.T < 1 || np > TMQ_PF_ATTN_MAXPOS)
+        return (int)hipErrorInvalidValue;
+    const size_t lds = tmq_pf_attn_lds(qpk, np);
+    if (lds > TMQ_PF_ATTN_LDS_MAX) return (int)hipErrorInvalidValue;
+    // registers for the scores of np positions (512 per pass)
+    if (np <= 512) return launch_attn<1>(a, lds, s);
+    if (np <= 1024) return launch_attn<2>(a, lds, s);
+    if (np <= 2048) return launch_attn<4>(a, lds, s);
+    return launch_attn<8>(a, lds, s);
 }
 
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s) {
@@ -566,8 +753,15 @@ int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s) {
     return (int)hipGetLastError();
 }
 
-int tmq_launch_pf_vfold(const TmqPfVFold& f, hipStream_t s) {
-    const int n = f.T * f.rows;
-    hipLaunchKernelGGL(pf_vfold_kernel, dim3((n + 255) / 256), dim3(256), 0, s, f);
+int tmq_launch_pf_qkv_fin(const TmqPfQkvFin& f, hipStream_t s) {
+    // rows in groups of four inside one segment; split sums of whole rows
+    if (f.H % 64 || f.KV % 64 || f.K % TMQ_PF_CHUNK || f.T < 1 || f.T > f.T_pad || f.split < 1 ||
+        (f.seg[2].q8 && !f.tpart))
+        return (int)hipErrorInvalidValue;
+    const int nr = f.part ? f.H + (f.seg[2].q8 ? 1 : 2) * f.KV : 0;
+    const int nA = f.T * (nr / 4), nB = f.seg[2].q8 ? f.T * f.KV : 0;
+    const int nb = (nA + 255) / 256 + (nB + 255) / 256;
+    if (nb == 0) return 0;
+    hipLaunchKernelGGL(pf_qkv_fin_kernel, dim3(nb), dim3(256), 0, s, f);
     return (int)hipGetLastError();
 }
