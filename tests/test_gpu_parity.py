@@ -55,6 +55,37 @@ def test_gemv_bitexact(ctx, oracle, qt, rows, cols):
     t.free()
 
 
+FIT_SUB = {Q5_0: 32, Q4_K: 32, Q6_K: 16}  # weights per fitted sub-block
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(Q5_0, 4864, 896), (Q4_K, 896, 4864), (Q6_K, 896, 4864)])
+def test_fit_stats_and_exact_decode(ctx, oracle, qt, rows, cols, monkeypatch):
+    """Every sub-block is fitted or flagged; the flagged ones (present in the
+    Q5_0 and Q6_K tensors: the linear form has no pair for them) and a
+    tensor uploaded with TMQ_NOFIT=1 (every sub-block on the exact decode)
+    give the oracle's int64 sums exactly."""
+    print(f"[fit] type={qt} {rows}x{cols}", flush=True)
+    w = synth.gen_weights(qt, rows, cols, 900 + rows)
+    x = synth.gen_x(cols, 901)
+    xq, _ = oracle.quantize_act(x)
+    ae = oracle.acc(qt, w, rows, cols, xq, oracle.row_inv(qt, w, rows, cols))
+    t = ctx.upload(qt, rows, cols, w)
+    fitted, exact = t.fit_stats()
+    assert fitted + exact == rows * cols // FIT_SUB[qt]
+    assert exact < fitted // 1000
+    if qt != Q4_K:
+        assert exact > 0, "no sub-block on the exact decode: the mixed case is not covered"
+    acc, _ = ctx.partials(t, x)
+    assert np.array_equal(acc, ae), report("acc", acc, ae)
+    t.free()
+    monkeypatch.setenv("TMQ_NOFIT", "1")
+    t = ctx.upload(qt, rows, cols, w)
+    assert t.fit_stats() == (0, rows * cols // FIT_SUB[qt])
+    acc, _ = ctx.partials(t, x)
+    assert np.array_equal(acc, ae), report("acc (exact decode)", acc, ae)
+    t.free()
+
+
 def test_q8_logits_full_size(ctx, oracle):
     """151936 x 896 Q8_0 logits matvec, with and without
     the row_max_abs aux tensor."""

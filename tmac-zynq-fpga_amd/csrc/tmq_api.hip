@@ -102,15 +102,15 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     d.rows_pad = (int)((rows + 63) / 64 * 64);
     d.nb = (int)(cols / qk);
     const size_t R = d.rows_pad, nb = d.nb;
-    size_t sa = 0, sb = 0, sc = 0, sd = 0;
+    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0;
     switch (type) {
     case TMQ_TYPE_Q8_0: sa = nb * 2 * R * 16; sd = nb * R * 2; break;
-    case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sc = nb * R; sd = nb * R * 2; break;
-    case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; break;
-    case TMQ_TYPE_Q6_K: sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; break;
+    case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; se = nb * R; break;
+    case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; se = nb * R * 8; break;
+    case TMQ_TYPE_Q6_K: sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; se = nb * R * 16; break;
     }
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(R * 4) * 2;
+    const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(se) + al(R * 4) * 2;
     hipError_t e = hipMalloc(&t->alloc, total);
     if (e != hipSuccess) {
         delete t;
@@ -127,6 +127,7 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     d.pb = sb ? p : nullptr; p += al(sb);
     d.pc = sc ? p : nullptr; p += al(sc);
     d.pd = sd ? p : nullptr; p += al(sd);
+    d.pe = se ? p : nullptr; p += al(se);
     d.row_inv = (const float*)p; p += al(R * 4);
     d.row_scale = (const float*)p;
     t->weight_bytes = rows * (cols / qk) * (uint64_t)block_bytes(type);
@@ -208,8 +209,10 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
         if (le) e = (hipError_t)le;
     }
     int badh = 0;
-    if (e == hipSuccess && type == TMQ_TYPE_Q5_0) {
-        le = tmq_launch_q5_fit(t->dev, ctx->stream);
+    if (e == hipSuccess && t->dev.pe) {
+        // TMQ_NOFIT=1: every sub-block takes the exact decode (testing)
+        const char* nf = getenv("TMQ_NOFIT");
+        le = tmq_launch_fit(t->dev, nf && atoi(nf) != 0, ctx->stream);
         if (le) e = (hipError_t)le;
     }
     if (e == hipSuccess) e = hipMemcpyAsync(&badh, bad, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
@@ -404,6 +407,23 @@ int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out) {
     const float* src = t->dev.type == TMQ_TYPE_Q8_0 ? t->dev.row_scale : t->dev.row_inv;
     HIP_TRY(hipMemcpyAsync(out, src, sizeof(float) * t->dev.rows, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_tensor_fit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* fitted, uint64_t* exact) {
+    if (!ctx || !t || !fitted || !exact) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    *fitted = *exact = 0;
+    const int n = tmq_fit_codes(t->dev.type);
+    if (!n || !t->dev.pe || t->dev.clamp) return 0;
+    int rc = tmq_rt_set_device(ctx);
+    if (rc) return rc;
+    const size_t R = t->dev.rows_pad, nb = t->dev.nb;
+    std::vector<uint8_t> h(nb * R * n);
+    HIP_TRY(hipMemcpyAsync(h.data(), t->dev.pe, h.size(), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    for (size_t b = 0; b < nb; b++)
+        for (size_t r = 0; r < (size_t)t->dev.rows; r++)
+            for (int i = 0; i < n; i++) (h[(b * R + r) * n + i] & 0x80u ? *exact : *fitted) += 1;
     return 0;
 }
 

@@ -33,6 +33,7 @@ struct TmqTensorDev {
     const uint8_t* pb;
     const uint8_t* pc;
     const uint8_t* pd;
+    const uint8_t* pe;       // fit codes (Q5_0: 1 B, Q4_K: 8 B, Q6_K: 16 B per block and row)
     const float* row_inv;    // Q5_0/K-quants: row_inv; Q8_0: 1/row_scale (guarded)
     const float* row_scale;  // Q8_0 only
 };
@@ -159,8 +160,11 @@ struct ihipStream_t;
 typedef struct ihipStream_t* hipStream_t;
 int tmq_launch_act_prep(const TmqActJobs& jobs, hipStream_t s);
 int tmq_launch_repack(int type, const uint8_t* src, const TmqTensorDev& t, hipStream_t s);
-// Q5_0 per-block fit codes (plane pc) from the planes and row_inv
-int tmq_launch_q5_fit(const TmqTensorDev& t, hipStream_t s);
+// fit codes (plane pe) of a Q5_0 / Q4_K / Q6_K tensor from its planes and
+// row_inv; all_exact: every sub-block flagged for the exact decode
+int tmq_launch_fit(const TmqTensorDev& t, int all_exact, hipStream_t s);
+// bytes of fit codes per block and row (0: no fitted decode)
+static inline int tmq_fit_codes(int type) { return type == 6 ? 1 : type == 12 ? 8 : type == 14 ? 16 : 0; }
 int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux_max_abs, float* row_inv,
                        float* row_scale, int* bad_flag, hipStream_t s);
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s);

@@ -141,6 +141,24 @@ struct WDigits {
 typedef ActT<const cu32*> Act;
 typedef ActT<const lu32*> ActL;
 
+// N activation pairs in registers (element kx of the view is pair
+// base + kx of the activation), read before a decoder branches.
+template <int N>
+struct ActN {
+    static constexpr bool kSink = false;
+    uint32_t xh[N], xl[N];
+};
+template <int N, class AT>
+__device__ __forceinline__ ActN<N> act_n(const AT& A, int base) {
+    ActN<N> r;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        r.xh[i] = A.xh[base + i];
+        r.xl[i] = A.xl[base + i];
+    }
+    return r;
+}
+
 __device__ __forceinline__ Act act_view(const uint8_t* a) {
     const cu32* p = (const cu32*)a;
     Act r;
@@ -201,14 +219,14 @@ __device__ __forceinline__ void mac4i(int w0, int w1, int w2, int w3, const AT& 
 //
 // Fitted blocks (tensors normalised at upload): within one block of one row
 // the int16 weight is a function g(u) of the 5-bit code u alone, and
-// g(u) = floor(u*A + B) for a pair (A, B) found at upload (q5_fit_kernel)
+// g(u) = floor(u*A + B) for a pair (A, B) found at upload (fit_kernel)
 // and checked there against the exact g on every code the block holds.
 // A and B are d*row_inv and 0.5 - 16A (fp32, as computed here) moved by a
-// few ulps, coded in one byte per block and row: bits 0-2 dA+4, bits 3-5
-// dB+4, bit 7 set: no pair found, the block takes the exact decode.  The
-// code goes into an f16 lane as the subnormal u*2^-24, so one v_fma_mix
-// with A*2^24 forms u*A + B with a single rounding, and v_cvt_flr gives the
-// weight: 2 instructions per weight instead of 4.
+// few ulps, coded in one byte per block and row (plane pe, fit_a/fit_b).
+// The code goes into an f16 lane as the subnormal u*2^-24, so one
+// v_fma_mix with A*2^24 forms u*A + B with a single rounding, and v_cvt_flr
+// gives the weight: 2 instructions per weight instead of 4.  The K-quants
+// fit each 32-weight (Q4_K) or 16-weight (Q6_K) sub-block the same way.
 struct Q5Blk {
     uint4 qs;
     uint32_t qh, d, e;
@@ -219,7 +237,7 @@ __device__ __forceinline__ Q5Blk q5_load(const TmqTensorDev& t, int b, int r) {
     k.qs = ld16(t.pa + o * 16);
     k.qh = ld4(t.pb + o * 4);
     k.d = ld2(t.pd + o * 2);
-    k.e = ld1(t.pc + o);
+    k.e = ld1(t.pe + o);
     return k;
 }
 // the 5-bit codes of elements 4g..4g+3 as bytes
@@ -228,17 +246,16 @@ __device__ __forceinline__ uint32_t q5_codes(const Q5Blk& k, int g) {
     const uint32_t hs = (g <= 4) ? (k.qh << (4 - g)) : (k.qh >> (g - 4));
     return (hs & 0x10101010u) | nib;
 }
-// (A, B) of a fitted block from its code byte
-__device__ __forceinline__ float q5_fit_a(float d, float inv, int da) {
-    return __int_as_float(__float_as_int(d * inv) + da);
-}
-__device__ __forceinline__ float q5_fit_b(float a, int db) {
-    return __int_as_float(__float_as_int(__builtin_fmaf(-16.0f, a, 0.5f)) + db);
-}
+// Fit code byte: bits 0-2 dA+4, bits 3-5 dB+4 (ulps), bit 7 set: no pair
+// found, the (sub-)block takes the exact decode.  A = a0 moved by dA ulps;
+// B = b0, computed from that A where it depends on it, moved by dB ulps.
+__device__ __forceinline__ float fit_mv(float x, int k) { return __int_as_float(__float_as_int(x) + k); }
+__device__ __forceinline__ float fit_a(float a0, uint32_t e) { return fit_mv(a0, (int)(e & 7u) - 4); }
+__device__ __forceinline__ float fit_b(float b0, uint32_t e) { return fit_mv(b0, (int)((e >> 3) & 7u) - 4); }
 template <class AT>
 __device__ __forceinline__ void q5_mac_fit(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
-    const float a = q5_fit_a(h2f(k.d), inv, (int)(k.e & 7u) - 4);
-    const float a24 = a * 0x1p24f, bb = q5_fit_b(a, (int)((k.e >> 3) & 7u) - 4);
+    const float a = fit_a(h2f(k.d) * inv, k.e);
+    const float a24 = a * 0x1p24f, bb = fit_b(__builtin_fmaf(-16.0f, a, 0.5f), k.e);
 #pragma unroll
     for (int g = 0; g < 8; g++) {
         const uint32_t U = q5_codes(k, g);
@@ -249,13 +266,7 @@ __device__ __forceinline__ void q5_mac_fit(const Q5Blk& k, const AT& A, int b, f
     }
 }
 template <bool CLAMP, class AT>
-__device__ __forceinline__ void q5_mac(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
-    if constexpr (!CLAMP) {
-        if (!(k.e & 0x80u)) {
-            q5_mac_fit(k, A, b, inv, sh, sl);
-            return;
-        }
-    }
+__device__ __forceinline__ void q5_mac_exact(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
     const float d = h2f(k.d);
     const float c = -1040.0f * d;  // exact: 7-bit x 11-bit
 #pragma unroll
@@ -266,6 +277,22 @@ __device__ __forceinline__ void q5_mac(const Q5Blk& k, const AT& A, int b, float
         mac4<CLAMP>(__builtin_fmaf((float)v0.x, d, c), __builtin_fmaf((float)v0.y, d, c),
                     __builtin_fmaf((float)v1.x, d, c), __builtin_fmaf((float)v1.y, d, c), inv, A,
                     b * 16 + 2 * g, sh, sl);
+    }
+}
+// Fitted blocks take the two-instruction decode, the others (and every
+// block of a clamped tensor) the exact one.  The block's activation pairs
+// are read before the branch.
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q5_mac(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
+    if constexpr (CLAMP) {
+        q5_mac_exact<CLAMP>(k, A, b, inv, sh, sl);
+    } else if constexpr (AT::kSink) {
+        if (!(k.e & 0x80u)) q5_mac_fit(k, A, b, inv, sh, sl);
+        else q5_mac_exact<CLAMP>(k, A, b, inv, sh, sl);
+    } else {
+        const ActN<16> X = act_n<16>(A, b * 16);
+        if (!(k.e & 0x80u)) q5_mac_fit(k, X, 0, inv, sh, sl);
+        else q5_mac_exact<CLAMP>(k, X, 0, inv, sh, sl);
     }
 }
 
@@ -289,6 +316,7 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& h, int s, int& sc, in
 struct Q4KBlk {
     uint4 h;
     uint4 qs[8];
+    uint2 e;  // fit codes of the 8 sub-blocks
 };
 __device__ __forceinline__ Q4KBlk q4k_load(const TmqTensorDev& t, int b, int r) {
     const size_t R = t.rows_pad;
@@ -296,40 +324,80 @@ __device__ __forceinline__ Q4KBlk q4k_load(const TmqTensorDev& t, int b, int r) 
     k.h = ld16(t.pb + p16(b, 0, 1, R, r));
 #pragma unroll
     for (int i = 0; i < 8; i++) k.qs[i] = ld16(t.pa + p16(b, i, 8, R, r));
+    k.e.x = ld4(t.pe + ((size_t)b * R + r) * 8);
+    k.e.y = ld4(t.pe + ((size_t)b * R + r) * 8 + 4);
     return k;
 }
-// one quarter (sub-blocks 2sp, 2sp+1: 64 weights) of a Q4_K block
-template <bool CLAMP, class AT>
-__device__ __forceinline__ void q4k_mac_q(const uint4& h, const uint4& qsa, const uint4& qsb, const AT& A, int b,
-                                          int sp, float inv, int& sh, int& sl) {
-    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
-    int sc0, m0, sc1, m1;
-    q4k_scale_min(h, 2 * sp, sc0, m0);
-    q4k_scale_min(h, 2 * sp + 1, sc1, m1);
-    const float A0 = (d * (float)sc0) * 0x1p24f, B0 = -(dmin * (float)m0);
-    const float A1 = (d * (float)sc1) * 0x1p20f, B1 = -(dmin * (float)m1);
+// sub-block s = 2sp + hi of a quarter fitted: A = (d*sc)*row_inv and
+// B = 0.5 - (dmin*m)*row_inv (one fma), both moved by its code; the high
+// nibbles sit in their lanes as 16u*2^-24, hence A*2^20.  Pair kx of
+// dwords (hf, i) is kx0 + 8hf + 2i (+1).
+template <class AT>
+__device__ __forceinline__ void q4k_sub_fit(float Ad, float Bm, uint32_t e, const uint4& qsa, const uint4& qsb, int hi,
+                                            const AT& A, int kx0, float inv, int& sh, int& sl) {
+    const float a = fit_a(Ad * inv, e) * (hi ? 0x1p20f : 0x1p24f), bb = fit_b(__builtin_fmaf(-Bm, inv, 0.5f), e);
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
         const uint4& qs = hf ? qsb : qsa;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t w = dw_of(qs, i);
-            const uint32_t lo = w & 0x0f0f0f0fu, hi = w & 0xf0f0f0f0u;
-            const tmq_h2 l0 = lanes01(lo), l1 = lanes23(lo), h0 = lanes01(hi), h1 = lanes23(hi);
-            const int kx = (b * 256 + 64 * sp + 16 * hf + 4 * i) / 2;
-            mac4<CLAMP>(__builtin_fmaf((float)l0.x, A0, B0), __builtin_fmaf((float)l0.y, A0, B0),
-                        __builtin_fmaf((float)l1.x, A0, B0), __builtin_fmaf((float)l1.y, A0, B0),
-                        inv, A, kx, sh, sl);
-            mac4<CLAMP>(__builtin_fmaf((float)h0.x, A1, B1), __builtin_fmaf((float)h0.y, A1, B1),
-                        __builtin_fmaf((float)h1.x, A1, B1), __builtin_fmaf((float)h1.y, A1, B1),
-                        inv, A, kx + 16, sh, sl);
+            const uint32_t w = dw_of(qs, i) & (hi ? 0xf0f0f0f0u : 0x0f0f0f0fu);
+            const tmq_h2 l0 = lanes01(w), l1 = lanes23(w);
+            mac4i(cvt_flr(__builtin_fmaf((float)l0.x, a, bb)), cvt_flr(__builtin_fmaf((float)l0.y, a, bb)),
+                  cvt_flr(__builtin_fmaf((float)l1.x, a, bb)), cvt_flr(__builtin_fmaf((float)l1.y, a, bb)), A,
+                  kx0 + 8 * hf + 2 * i, sh, sl);
+        }
+    }
+}
+// the same sub-block, exact: E = fma_mix(lane, Ad*2^24 or Ad*2^20, -Bm)
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q4k_sub_exact(float Ad, float Bm, const uint4& qsa, const uint4& qsb, int hi,
+                                              const AT& A, int kx0, float inv, int& sh, int& sl) {
+    const float a = Ad * (hi ? 0x1p20f : 0x1p24f), nb = -Bm;
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        const uint4& qs = hf ? qsb : qsa;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = dw_of(qs, i) & (hi ? 0xf0f0f0f0u : 0x0f0f0f0fu);
+            const tmq_h2 l0 = lanes01(w), l1 = lanes23(w);
+            mac4<CLAMP>(__builtin_fmaf((float)l0.x, a, nb), __builtin_fmaf((float)l0.y, a, nb),
+                        __builtin_fmaf((float)l1.x, a, nb), __builtin_fmaf((float)l1.y, a, nb), inv, A,
+                        kx0 + 8 * hf + 2 * i, sh, sl);
+        }
+    }
+}
+// one quarter (sub-blocks 2sp, 2sp+1: 64 weights, pairs 128b + 32sp + 0..31;
+// the low nibbles are sub-block 2sp, pairs 0..15 of the quarter)
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q4k_mac_q(const uint4& h, const uint4& qsa, const uint4& qsb, uint32_t e2, const AT& A,
+                                          int b, int sp, float inv, int& sh, int& sl) {
+    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+#pragma unroll
+    for (int hi = 0; hi < 2; hi++) {
+        int sc, m;
+        q4k_scale_min(h, 2 * sp + hi, sc, m);
+        const float Ad = d * (float)sc, Bm = dmin * (float)m;
+        const uint32_t e = (e2 >> (8 * hi)) & 0xffu;
+        const int kx = 128 * b + 32 * sp + 16 * hi;
+        if constexpr (CLAMP) {
+            q4k_sub_exact<CLAMP>(Ad, Bm, qsa, qsb, hi, A, kx, inv, sh, sl);
+        } else if constexpr (AT::kSink) {
+            if (!(e & 0x80u)) q4k_sub_fit(Ad, Bm, e, qsa, qsb, hi, A, kx, inv, sh, sl);
+            else q4k_sub_exact<CLAMP>(Ad, Bm, qsa, qsb, hi, A, kx, inv, sh, sl);
+        } else {
+            const ActN<16> X = act_n<16>(A, kx);
+            if (!(e & 0x80u)) q4k_sub_fit(Ad, Bm, e, qsa, qsb, hi, X, 0, inv, sh, sl);
+            else q4k_sub_exact<CLAMP>(Ad, Bm, qsa, qsb, hi, X, 0, inv, sh, sl);
         }
     }
 }
 template <bool CLAMP, class AT>
 __device__ __forceinline__ void q4k_mac(const Q4KBlk& k, const AT& A, int b, float inv, int& sh, int& sl) {
 #pragma unroll
-    for (int sp = 0; sp < 4; sp++) q4k_mac_q<CLAMP>(k.h, k.qs[2 * sp], k.qs[2 * sp + 1], A, b, sp, inv, sh, sl);
+    for (int sp = 0; sp < 4; sp++)
+        q4k_mac_q<CLAMP>(k.h, k.qs[2 * sp], k.qs[2 * sp + 1], ((sp < 2 ? k.e.x : k.e.y) >> (16 * (sp & 1))) & 0xffffu,
+                         A, b, sp, inv, sh, sl);
 }
 
 // ---------------------------------------------------------------- Q6_K
@@ -339,6 +407,7 @@ struct Q6KBlk {
     uint4 ql[8];
     uint4 qh[4];
     uint4 sc;
+    uint4 e;  // fit codes of the 16 sub-blocks (byte j: scale j)
     uint32_t d;
 };
 __device__ __forceinline__ Q6KBlk q6k_load(const TmqTensorDev& t, int b, int r) {
@@ -349,31 +418,68 @@ __device__ __forceinline__ Q6KBlk q6k_load(const TmqTensorDev& t, int b, int r) 
 #pragma unroll
     for (int i = 0; i < 4; i++) k.qh[i] = ld16(t.pb + p16(b, i, 4, R, r));
     k.sc = ld16(t.pc + p16(b, 0, 1, R, r));
+    k.e = ld16(t.pe + ((size_t)b * R + r) * 16);
     k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
     return k;
 }
-// one quarter (half, lc: 64 weights) of a Q6_K block
+// the four 6-bit codes of quarter (half, lc), sub-block sub, dword i
+__device__ __forceinline__ uint32_t q6_codes(const uint4& qla, const uint4& qlb, const uint4& qhc, int sub, int i) {
+    const uint32_t ql = dw_of((sub & 1) ? qlb : qla, i), qh = dw_of(qhc, i);
+    const uint32_t nib = (sub < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+    const uint32_t hs = (sub == 0) ? (qh << 4) : (sub == 1) ? (qh << 2) : (sub == 2) ? qh : (qh >> 2);
+    return (hs & 0x30303030u) | nib;
+}
+// sub-block sub of quarter (half, lc) of a Q6_K block (16 weights, scale S);
+// pair kx of dword i is kx0 + 2i (+1)
 template <bool CLAMP, class AT>
-__device__ __forceinline__ void q6k_mac_q(const uint4& sc, float ss, const uint4& qla, const uint4& qlb,
-                                          const uint4& qhc, const AT& A, int b, int half, int lc, float inv,
-                                          int& sh, int& sl) {
+__device__ __forceinline__ void q6k_sub_exact(float S, const uint4& qla, const uint4& qlb, const uint4& qhc, int sub,
+                                              const AT& A, int kx0, float inv, int& sh, int& sl) {
+    const float nS = -32.0f * S, S24 = S * 0x1p24f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // E = S*(u-32) = fma_mix(u*2^-24, S*2^24, -32*S), exact
+        const tmq_h2 u0 = lanes01(q6_codes(qla, qlb, qhc, sub, i)), u1 = lanes23(q6_codes(qla, qlb, qhc, sub, i));
+        mac4<CLAMP>(__builtin_fmaf((float)u0.x, S24, nS), __builtin_fmaf((float)u0.y, S24, nS),
+                    __builtin_fmaf((float)u1.x, S24, nS), __builtin_fmaf((float)u1.y, S24, nS), inv, A, kx0 + 2 * i,
+                    sh, sl);
+    }
+}
+// the same sub-block fitted: A = S*row_inv and B = 0.5 - 32A, both moved by
+// its code byte
+template <class AT>
+__device__ __forceinline__ void q6k_sub_fit(float S, uint32_t e, const uint4& qla, const uint4& qlb, const uint4& qhc,
+                                            int sub, const AT& A, int kx0, float inv, int& sh, int& sl) {
+    const float a = fit_a(S * inv, e);
+    const float a24 = a * 0x1p24f, bb = fit_b(__builtin_fmaf(-32.0f, a, 0.5f), e);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t U = q6_codes(qla, qlb, qhc, sub, i);
+        const tmq_h2 u0 = lanes01(U), u1 = lanes23(U);
+        mac4i(cvt_flr(__builtin_fmaf((float)u0.x, a24, bb)), cvt_flr(__builtin_fmaf((float)u0.y, a24, bb)),
+              cvt_flr(__builtin_fmaf((float)u1.x, a24, bb)), cvt_flr(__builtin_fmaf((float)u1.y, a24, bb)), A,
+              kx0 + 2 * i, sh, sl);
+    }
+}
+// one quarter (half, lc: 64 weights) of a Q6_K block: sub-blocks
+// j = half*8 + lc + 2*sub, pairs 128b + 64half + 8lc + 16sub + 0..7
+template <bool CLAMP, class AT>
+__device__ __forceinline__ void q6k_mac_q(const uint4& sc, const uint4& e, float ss, const uint4& qla,
+                                          const uint4& qlb, const uint4& qhc, const AT& A, int b, int half, int lc,
+                                          float inv, int& sh, int& sl) {
 #pragma unroll
     for (int sub = 0; sub < 4; sub++) {
-        const float S = ss * (float)(int8_t)byte_of(sc, half * 8 + lc + 2 * sub);
-        const float nS = -32.0f * S, S24 = S * 0x1p24f;
-        const uint4& src = (sub & 1) ? qlb : qla;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t ql = dw_of(src, i), qh = dw_of(qhc, i);
-            const uint32_t nib = (sub < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
-            const uint32_t hs = (sub == 0) ? (qh << 4) : (sub == 1) ? (qh << 2) : (sub == 2) ? qh : (qh >> 2);
-            const uint32_t U = (hs & 0x30303030u) | nib;
-            const int kx = (b * 256 + half * 128 + sub * 32 + 16 * lc + 4 * i) / 2;
-            // E = S*(u-32) = fma_mix(u*2^-24, S*2^24, -32*S), exact
-            const tmq_h2 u0 = lanes01(U), u1 = lanes23(U);
-            mac4<CLAMP>(__builtin_fmaf((float)u0.x, S24, nS), __builtin_fmaf((float)u0.y, S24, nS),
-                        __builtin_fmaf((float)u1.x, S24, nS), __builtin_fmaf((float)u1.y, S24, nS),
-                        inv, A, kx, sh, sl);
+        const int j = half * 8 + lc + 2 * sub, kx = 128 * b + 64 * half + 8 * lc + 16 * sub;
+        const float S = ss * (float)(int8_t)byte_of(sc, j);
+        const uint32_t ej = byte_of(e, j);
+        if constexpr (CLAMP) {
+            q6k_sub_exact<CLAMP>(S, qla, qlb, qhc, sub, A, kx, inv, sh, sl);
+        } else if constexpr (AT::kSink) {
+            if (!(ej & 0x80u)) q6k_sub_fit(S, ej, qla, qlb, qhc, sub, A, kx, inv, sh, sl);
+            else q6k_sub_exact<CLAMP>(S, qla, qlb, qhc, sub, A, kx, inv, sh, sl);
+        } else {
+            const ActN<8> X = act_n<8>(A, kx);
+            if (!(ej & 0x80u)) q6k_sub_fit(S, ej, qla, qlb, qhc, sub, X, 0, inv, sh, sl);
+            else q6k_sub_exact<CLAMP>(S, qla, qlb, qhc, sub, X, 0, inv, sh, sl);
         }
     }
 }
@@ -384,13 +490,14 @@ __device__ __forceinline__ void q6k_mac(const Q6KBlk& k, const AT& A, int b, flo
     for (int half = 0; half < 2; half++)
 #pragma unroll
         for (int lc = 0; lc < 2; lc++)
-            q6k_mac_q<CLAMP>(k.sc, ss, k.ql[half * 4 + lc], k.ql[half * 4 + 2 + lc], k.qh[half * 2 + lc], A, b,
+            q6k_mac_q<CLAMP>(k.sc, k.e, ss, k.ql[half * 4 + lc], k.ql[half * 4 + 2 + lc], k.qh[half * 2 + lc], A, b,
                              half, lc, inv, sh, sl);
 }
 
 // Quarter-block units (64 weights) of the K-quants, for the engine's K split.
 struct Q4KQ {
     uint4 h, qa, qb;
+    uint32_t e;  // fit codes of sub-blocks 2q, 2q+1
 };
 __device__ __forceinline__ Q4KQ q4kq_load(const TmqTensorDev& t, int b, int q, int r) {
     const size_t R = t.rows_pad;
@@ -398,10 +505,11 @@ __device__ __forceinline__ Q4KQ q4kq_load(const TmqTensorDev& t, int b, int q, i
     k.h = ld16(t.pb + p16(b, 0, 1, R, r));
     k.qa = ld16(t.pa + p16(b, 2 * q, 8, R, r));
     k.qb = ld16(t.pa + p16(b, 2 * q + 1, 8, R, r));
+    k.e = ld2(t.pe + ((size_t)b * R + r) * 8 + 2 * q);
     return k;
 }
 struct Q6KQ {
-    uint4 qla, qlb, qhc, sc;
+    uint4 qla, qlb, qhc, sc, e;
     uint32_t d;
 };
 __device__ __forceinline__ Q6KQ q6kq_load(const TmqTensorDev& t, int b, int q, int r) {
@@ -412,6 +520,7 @@ __device__ __forceinline__ Q6KQ q6kq_load(const TmqTensorDev& t, int b, int q, i
     k.qlb = ld16(t.pa + p16(b, half * 4 + 2 + lc, 8, R, r));
     k.qhc = ld16(t.pb + p16(b, half * 2 + lc, 4, R, r));
     k.sc = ld16(t.pc + p16(b, 0, 1, R, r));
+    k.e = ld16(t.pe + ((size_t)b * R + r) * 16);
     k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
     return k;
 }
@@ -450,8 +559,8 @@ template <int FMT, bool CLAMP = false, class AT>
 __device__ __forceinline__ void unit_mac(const typename UnitOf<FMT>::T& k, const AT& A, int u, float inv,
                                          int& sh, int& sl) {
     if constexpr (FMT == kQ5_0) q5_mac<CLAMP>(k, A, u, inv, sh, sl);
-    else if constexpr (FMT == kQ4_K) q4k_mac_q<CLAMP>(k.h, k.qa, k.qb, A, u >> 2, u & 3, inv, sh, sl);
-    else q6k_mac_q<CLAMP>(k.sc, h2f(k.d), k.qla, k.qlb, k.qhc, A, u >> 2, (u & 3) >> 1, u & 1, inv, sh, sl);
+    else if constexpr (FMT == kQ4_K) q4k_mac_q<CLAMP>(k.h, k.qa, k.qb, k.e, A, u >> 2, u & 3, inv, sh, sl);
+    else q6k_mac_q<CLAMP>(k.sc, k.e, h2f(k.d), k.qla, k.qlb, k.qhc, A, u >> 2, (u & 3) >> 1, u & 1, inv, sh, sl);
 }
 
 // ---------------------------------------------------------------- Q8_0
@@ -519,17 +628,42 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
     const Act A = act_view(w.act);
     int64_t acc = 0;
     if (FMT == kQ5_0) {
-        int b = b0 + wave;
-        for (; b + TMQ_WAVES < b1; b += 2 * TMQ_WAVES) {
+        // two blocks per step, the next step's two in flight (indices
+        // clamped into the row, so every load is unconditional)
+        constexpr int S = TMQ_WAVES;
+        if (b1 - b0 == 7 * S) {
+            // 896 columns (7 blocks per wave): every load of the wave is
+            // issued at once, the blocks are multiplied as they arrive
+            Q5Blk kk[7];
+#pragma unroll
+            for (int i = 0; i < 7; i++) kk[i] = q5_load(t, b0 + wave + S * i, r);
             int sh = 0, sl = 0;
-            q5_mac<CLAMP>(q5_load(t, b, r), A, b, inv, sh, sl);
-            q5_mac<CLAMP>(q5_load(t, b + TMQ_WAVES, r), A, b + TMQ_WAVES, inv, sh, sl);
-            acc += (int64_t)sh * 256 + sl;
+#pragma unroll
+            for (int i = 0; i < 7; i++) {
+                q5_mac<CLAMP>(kk[i], A, b0 + wave + S * i, inv, sh, sl);
+                if (i & 1 || i == 6) {
+                    acc += (int64_t)sh * 256 + sl;
+                    sh = sl = 0;
+                }
+            }
+            goto reduce;
         }
-        if (b < b1) {
+        auto ld = [&](int bb) { return q5_load(t, min(bb, b1 - 1), r); };
+        auto pair = [&](const Q5Blk& x0, const Q5Blk& x1, int bb) {
             int sh = 0, sl = 0;
-            q5_mac<CLAMP>(q5_load(t, b, r), A, b, inv, sh, sl);
+            q5_mac<CLAMP>(x0, A, bb, inv, sh, sl);
+            if (bb + S < b1) q5_mac<CLAMP>(x1, A, bb + S, inv, sh, sl);
             acc += (int64_t)sh * 256 + sl;
+        };
+        // two register sets in turn, so that no copy waits on a load
+        Q5Blk k0 = ld(b0 + wave), k1 = ld(b0 + wave + S);
+        for (int b = b0 + wave; b < b1; b += 4 * S) {
+            const Q5Blk n0 = ld(b + 2 * S), n1 = ld(b + 3 * S);
+            pair(k0, k1, b);
+            if (b + 2 * S >= b1) break;
+            k0 = ld(b + 4 * S);
+            k1 = ld(b + 5 * S);
+            pair(n0, n1, b + 2 * S);
         }
     } else {
         // K-quants in quarter blocks: each wave keeps its next quarter in
@@ -550,6 +684,7 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
             if (more) cur = nxt;
         }
     }
+reduce:
     part[wave][lane] = acc;
     __syncthreads();
     int64_t tot = 0;
@@ -1275,42 +1410,100 @@ __global__ void rowstat_kernel(TmqTensorDev t, const float* __restrict__ aux, fl
     }
 }
 
-// Q5_0 fits (see Q5Blk): for block b of row r, the smallest move (dA, dB),
-// |dA|, |dB| <= 3 ulps by growing square rings, for which
-// floor(u*A + B) = g(u) on every code u the block holds; else the exact
-// decode flag.  g(u) is the exact decode's int16: the saturated
-// round-half-away of fl(fl(d*(u-16)) * row_inv).
-__global__ __launch_bounds__(256) void q5_fit_kernel(TmqTensorDev t) {
-    const int r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-    if (r >= t.rows_pad) return;
-    const Q5Blk k = q5_load(t, b, r);
-    const float d = h2f(k.d), inv = t.row_inv[r];
-    uint32_t held = 0;
+// Fit codes (see Q5Blk): for each sub-block of block b of row r, the
+// smallest move (dA, dB), |dA|, |dB| <= 3 ulps by growing square rings, for
+// which floor(u*A + B) = g(u) on every code u the sub-block holds; else the
+// exact-decode flag.  g(u) is the exact decode's int16: the saturated
+// round-half-away of fl(E * row_inv), E the decoder's exact value of u.
+// n codes u[] with exact values E = gu(u) and A0, B0(A) as the decoders form them.
+template <int N, class GE, class B0>
+__device__ __forceinline__ uint32_t fit_search(const int (&u)[N], float a0, float inv, GE&& gu, B0&& b0) {
+    int g[N];
 #pragma unroll
-    for (int g = 0; g < 8; g++) {
-        const uint32_t U = q5_codes(k, g);
-#pragma unroll
-        for (int j = 0; j < 4; j++) held |= 1u << ((U >> (8 * j)) & 31u);
-    }
-    int gv[32];
-#pragma unroll
-    for (int u = 0; u < 32; u++) gv[u] = max(-32768, min(32767, round_away((d * (float)(u - 16)) * inv)));
-    uint32_t code = 0x80u;
-    for (int rad = 0; rad <= 3 && code == 0x80u; rad++)
-        for (int da = -rad; da <= rad && code == 0x80u; da++)
-            for (int db = -rad; db <= rad && code == 0x80u; db++) {
+    for (int i = 0; i < N; i++) g[i] = max(-32768, min(32767, round_away(gu(u[i]) * inv)));
+    for (int rad = 0; rad <= 3; rad++)
+        for (int da = -rad; da <= rad; da++)
+            for (int db = -rad; db <= rad; db++) {
                 if (abs(da) != rad && abs(db) != rad) continue;
-                const float a = q5_fit_a(d, inv, da), bb = q5_fit_b(a, db);
+                const uint32_t code = (uint32_t)(da + 4) | ((uint32_t)(db + 4) << 3);
+                const float a = fit_a(a0, code), bb = fit_b(b0(a), code);
                 bool ok = true;
 #pragma unroll
-                for (int u = 0; u < 32; u++)
-                    if ((held >> u) & 1u) {
-                        const int w = max(-32768, min(32767, cvt_flr(__builtin_fmaf((float)u, a, bb))));
-                        ok = ok && w == gv[u];
-                    }
-                if (ok) code = (uint32_t)(da + 4) | ((uint32_t)(db + 4) << 3);
+                for (int i = 0; i < N; i++)
+                    ok = ok && max(-32768, min(32767, cvt_flr(__builtin_fmaf((float)u[i], a, bb)))) == g[i];
+                if (ok) return code;
             }
-    *(uint8_t*)(t.pc + (size_t)b * t.rows_pad + r) = (uint8_t)code;
+    return 0x80u;
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void fit_kernel(TmqTensorDev t, int all_exact) {
+    const int r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (r >= t.rows_pad) return;
+    const size_t R = t.rows_pad, o = (size_t)b * R + r;
+    const float inv = t.row_inv[r];
+    uint8_t* pe = (uint8_t*)t.pe;
+    if (all_exact) {
+        const int n = FMT == kQ5_0 ? 1 : FMT == kQ4_K ? 8 : 16;
+        for (int i = 0; i < n; i++) pe[o * n + i] = 0x80u;
+        return;
+    }
+    if constexpr (FMT == kQ5_0) {
+        const Q5Blk k = q5_load(t, b, r);
+        const float d = h2f(k.d);
+        int u[32];
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const uint32_t U = q5_codes(k, g);
+#pragma unroll
+            for (int j = 0; j < 4; j++) u[4 * g + j] = (int)((U >> (8 * j)) & 31u);
+        }
+        pe[o] = (uint8_t)fit_search(
+            u, d * inv, inv, [&](int c) { return d * (float)(c - 16); },
+            [](float a) { return __builtin_fmaf(-16.0f, a, 0.5f); });
+    } else if constexpr (FMT == kQ4_K) {
+        const Q4KBlk k = q4k_load(t, b, r);
+        const float d = h2f(k.h.x), dmin = h2f(k.h.x >> 16);
+#pragma unroll 1
+        for (int s = 0; s < 8; s++) {
+            int sc, m;
+            q4k_scale_min(k.h, s, sc, m);
+            const float Ad = d * (float)sc, Bm = dmin * (float)m;
+            int u[32];
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                const uint32_t by = byte_of(k.qs[(s >> 1) * 2 + (i >> 4)], i & 15);
+                u[i] = (int)((s & 1) ? (by >> 4) : (by & 15u));
+            }
+            const float b0 = __builtin_fmaf(-Bm, inv, 0.5f);
+            pe[o * 8 + s] = (uint8_t)fit_search(
+                u, Ad * inv, inv, [&](int c) { return __builtin_fmaf((float)c, Ad, -Bm); },
+                [&](float) { return b0; });
+        }
+    } else {
+        const Q6KBlk k = q6k_load(t, b, r);
+        const float ss = h2f(k.d);
+#pragma unroll 1
+        for (int q = 0; q < 4; q++) {
+            const int half = q >> 1, lc = q & 1;
+            const uint4 qla = k.ql[half * 4 + lc], qlb = k.ql[half * 4 + 2 + lc], qhc = k.qh[half * 2 + lc];
+#pragma unroll 1
+            for (int sub = 0; sub < 4; sub++) {
+                const int j = half * 8 + lc + 2 * sub;
+                const float S = ss * (float)(int8_t)byte_of(k.sc, j);
+                int u[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t U = q6_codes(qla, qlb, qhc, sub, i);
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) u[4 * i + jj] = (int)((U >> (8 * jj)) & 63u);
+                }
+                pe[o * 16 + j] = (uint8_t)fit_search(
+                    u, S * inv, inv, [&](int c) { return S * (float)(c - 32); },
+                    [](float a) { return __builtin_fmaf(-32.0f, a, 0.5f); });
+            }
+        }
+    }
 }
 
 // ----------------------------------------------------------- Q8 tile
@@ -1583,9 +1776,15 @@ int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux, float* row_inv, 
     return (int)hipGetLastError();
 }
 
-int tmq_launch_q5_fit(const TmqTensorDev& t, hipStream_t s) {
-    if (t.type != kQ5_0 || !t.pc) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(q5_fit_kernel, dim3((t.rows_pad + 255) / 256, t.nb), dim3(256), 0, s, t);
+int tmq_launch_fit(const TmqTensorDev& t, int all_exact, hipStream_t s) {
+    if (!t.pe || t.clamp) return (int)hipErrorInvalidValue;
+    const dim3 grid((t.rows_pad + 255) / 256, t.nb);
+    switch (t.type) {
+    case kQ5_0: hipLaunchKernelGGL(fit_kernel<kQ5_0>, grid, dim3(256), 0, s, t, all_exact); break;
+    case kQ4_K: hipLaunchKernelGGL(fit_kernel<kQ4_K>, grid, dim3(256), 0, s, t, all_exact); break;
+    case kQ6_K: hipLaunchKernelGGL(fit_kernel<kQ6_K>, grid, dim3(256), 0, s, t, all_exact); break;
+    default: return (int)hipErrorInvalidValue;
+    }
     return (int)hipGetLastError();
 }
 

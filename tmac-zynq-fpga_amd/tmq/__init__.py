@@ -28,7 +28,7 @@ BLOCK_BYTES = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210}
 EXPORTS = [
     "tmq_last_error", "tmq_version", "tmq_open", "tmq_close", "tmq_stream", "tmq_sync",
     "tmq_tensor_upload", "tmq_tensor_upload_dev", "tmq_tensor_free", "tmq_tensor_info",
-    "tmq_tensor_row_norm", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_partials",
+    "tmq_tensor_row_norm", "tmq_tensor_fit_stats", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_partials",
     "tmq_vecmul_tile_q8", "tmq_vecmul_tile_q5_0_8x896", "tmq_vecmul_tile_q6_k",
     "tmq_vecmul_tile_q4k", "tmq_phaseb_run", "tmq_chain_create", "tmq_chain_run",
     "tmq_chain_prepare", "tmq_chain_launch",
@@ -91,6 +91,7 @@ def lib(path: str = LIB_PATH):
         "tmq_tensor_free": (I, [P]),
         "tmq_tensor_info": (I, [P, P, P, P, P]),
         "tmq_tensor_row_norm": (I, [P, P, P]),
+        "tmq_tensor_fit_stats": (I, [P, P, C.POINTER(U64), C.POINTER(U64)]),
         "tmq_matmul": (I, [P, P, P, P, I, I]),
         "tmq_gemv_dev": (I, [P, P, P, P, P]),
         "tmq_gemv_partials": (I, [P, P, P, P, U64, P]),
@@ -156,6 +157,12 @@ class Tensor:
         out = np.empty(self.rows, dtype=np.float32)
         _check(lib().tmq_tensor_row_norm(self.ctx.handle, self.handle, _p(out)))
         return out
+
+    def fit_stats(self):
+        """(fitted, exact) sub-block counts of the upload-time decode fits"""
+        f, e = C.c_uint64(), C.c_uint64()
+        _check(lib().tmq_tensor_fit_stats(self.ctx.handle, self.handle, C.byref(f), C.byref(e)))
+        return f.value, e.value
 
     def free(self):
         if self.handle:
