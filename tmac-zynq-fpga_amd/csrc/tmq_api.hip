@@ -241,6 +241,8 @@ void act_from_int16(const int16_t* xq, int n, std::vector<uint8_t>& buf) {
         xl[k] = ((uint32_t)a & 0xffu) | (((uint32_t)c & 0xffu) << 16);
     }
     memcpy(q, xq, sizeof(int16_t) * n);
+    int32_t* q32 = (int32_t*)(q + n);
+    for (int k = 0; k < n; k++) q32[k] = xq[k];
 }
 
 TmqWork make_work(const tmq_tensor* t, const uint8_t* act, float* y, int64_t* acc) {

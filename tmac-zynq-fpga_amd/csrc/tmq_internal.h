@@ -40,10 +40,10 @@ struct TmqTensorDev {
 
 // Prepared activation, written by act_prep (or by the host for int16 input):
 //   +0  float x_scale   +4 int32 n   +16 u32 XH[n/2]   +16+2n u32 XL[n/2]
-//   +16+4n int16 xq[n]
+//   +16+4n int16 xq[n]   +16+6n int32 xq[n] (the fitted decoders' int64 sums)
 // XH/XL hold (xq >> 8, xq & 255) as int16 pairs (elements 2k, 2k+1), so that
 // sum w*xq = 256*sum w*xh + sum w*xl with every partial inside int32.
-static inline uint64_t tmq_act_bytes(int n) { return 16 + (uint64_t)n * 6 + 16; }
+static inline uint64_t tmq_act_bytes(int n) { return 16 + (uint64_t)n * 10 + 16; }
 
 // One GEMV of a chain.  The output epilogue of row r is
 //     v = finalize(acc_r);  if (bias) v = v + bias[r];  if (resid) v = y[r] + v;

@@ -121,6 +121,7 @@ struct ActT {
     float xs;
     P xh;
     P xl;
+    P x32;  // xq as int32 (scalar-cache view only)
 };
 
 // Weight sink: takes the place of an activation in the block decoders and
@@ -166,6 +167,7 @@ __device__ __forceinline__ Act act_view(const uint8_t* a) {
     const int n = (int)p[1];
     r.xh = p + 4;
     r.xl = r.xh + n / 2;
+    r.x32 = r.xh + 3 * (n / 2);
     return r;
 }
 
@@ -263,6 +265,23 @@ __device__ __forceinline__ void q5_mac_fit(const Q5Blk& k, const AT& A, int b, f
         mac4i(cvt_flr(__builtin_fmaf((float)l0.x, a24, bb)), cvt_flr(__builtin_fmaf((float)l0.y, a24, bb)),
               cvt_flr(__builtin_fmaf((float)l1.x, a24, bb)), cvt_flr(__builtin_fmaf((float)l1.y, a24, bb)), A,
               b * 16 + 2 * g, sh, sl);
+    }
+}
+// a fitted block summed straight into int64 (v_mad_i64_i32 per weight, the
+// activation as int32 through the scalar cache; x holds elements 32b..32b+31)
+__device__ __forceinline__ void q5_fit64(const Q5Blk& k, const int32_t (&x)[32], float inv, int64_t& acc0,
+                                         int64_t& acc1) {
+    const float a = fit_a(h2f(k.d) * inv, k.e);
+    const float a24 = a * 0x1p24f, bb = fit_b(__builtin_fmaf(-16.0f, a, 0.5f), k.e);
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        const uint32_t U = q5_codes(k, g);
+        const tmq_h2 l0 = lanes01(U), l1 = lanes23(U);
+        int64_t& c = (g & 1) ? acc1 : acc0;
+        c += (int64_t)cvt_flr(__builtin_fmaf((float)l0.x, a24, bb)) * x[4 * g];
+        c += (int64_t)cvt_flr(__builtin_fmaf((float)l0.y, a24, bb)) * x[4 * g + 1];
+        c += (int64_t)cvt_flr(__builtin_fmaf((float)l1.x, a24, bb)) * x[4 * g + 2];
+        c += (int64_t)cvt_flr(__builtin_fmaf((float)l1.y, a24, bb)) * x[4 * g + 3];
     }
 }
 template <bool CLAMP, class AT>
@@ -637,14 +656,34 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
             Q5Blk kk[7];
 #pragma unroll
             for (int i = 0; i < 7; i++) kk[i] = q5_load(t, b0 + wave + S * i, r);
-            int sh = 0, sl = 0;
+            if constexpr (CLAMP) {
+                int sh = 0, sl = 0;
 #pragma unroll
-            for (int i = 0; i < 7; i++) {
-                q5_mac<CLAMP>(kk[i], A, b0 + wave + S * i, inv, sh, sl);
-                if (i & 1 || i == 6) {
-                    acc += (int64_t)sh * 256 + sl;
-                    sh = sl = 0;
+                for (int i = 0; i < 7; i++) {
+                    q5_mac<CLAMP>(kk[i], A, b0 + wave + S * i, inv, sh, sl);
+                    if (i & 1 || i == 6) {
+                        acc += (int64_t)sh * 256 + sl;
+                        sh = sl = 0;
+                    }
                 }
+            } else {
+                // fitted blocks into int64 directly, the others exact
+                int64_t acc1 = 0;
+#pragma unroll
+                for (int i = 0; i < 7; i++) {
+                    const int b = b0 + wave + S * i;
+                    int32_t x[32];
+#pragma unroll
+                    for (int j = 0; j < 32; j++) x[j] = (int32_t)A.x32[32 * b + j];
+                    if (!(kk[i].e & 0x80u)) {
+                        q5_fit64(kk[i], x, inv, acc, acc1);
+                    } else {
+                        int sh = 0, sl = 0;
+                        q5_mac_exact<CLAMP>(kk[i], A, b, inv, sh, sl);
+                        acc += (int64_t)sh * 256 + sl;
+                    }
+                }
+                acc += acc1;
             }
             goto reduce;
         }
@@ -1274,11 +1313,14 @@ __global__ __launch_bounds__(1024) void act_prep_kernel(TmqActJobs jobs) {
     uint32_t* xh = (uint32_t*)(J.act + 16);
     uint32_t* xl = xh + n / 2;
     int16_t* xq = (int16_t*)(xl + n / 2);
+    int32_t* x32 = (int32_t*)(xq + n);
     for (int k = threadIdx.x; k < n / 2; k += blockDim.x) {
         int a = (int)(int16_t)roundf(J.x[2 * k] / s);
         int c = (int)(int16_t)roundf(J.x[2 * k + 1] / s);
         xq[2 * k] = (int16_t)a;
         xq[2 * k + 1] = (int16_t)c;
+        x32[2 * k] = a;
+        x32[2 * k + 1] = c;
         xh[k] = ((uint32_t)(a >> 8) & 0xffffu) | ((uint32_t)(c >> 8) << 16);
         xl[k] = ((uint32_t)a & 0xffu) | (((uint32_t)c & 0xffu) << 16);
     }
