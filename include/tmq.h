@@ -92,10 +92,10 @@ int tmq_tensor_info(const tmq_tensor* t, uint32_t* type, uint64_t* rows, uint64_
 int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out);
 /* Decode fits made at upload (no counterpart in the reference; diagnostics
  * for tests and profiling).  Within one sub-block (Q5_0: a block, Q4_K: 32
- * weights, Q6_K: 16 weights) of a row the int16 weight of code u is
- * floor(u*A + B) for a pair (A, B) checked against the exact decode on
- * every code the sub-block holds; sub-blocks without such a pair take the
- * exact decode.  Counts over the tensor's rows; both 0 for Q8_0 and for
+ * weights, Q6_K: 16 weights) of a row the int16 weight of code u is the
+ * integer nearest to fl(u*A + B) for a pair (A, B) checked against the
+ * exact decode on every code the sub-block holds; sub-blocks without such
+ * a pair take the exact decode.  Counts over the tensor's rows; both 0 for Q8_0 and for
  * tensors uploaded with an external row_inv.  TMQ_NOFIT=1 in the
  * environment at upload sends every sub-block to the exact decode. */
 int tmq_tensor_fit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* fitted, uint64_t* exact);

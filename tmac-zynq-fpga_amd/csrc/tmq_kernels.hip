@@ -57,11 +57,15 @@ __device__ __forceinline__ int wq(float n) {
     return round_away(n);
 }
 
-// floor(x) as int32 in one instruction (LLVM emits v_floor + v_cvt)
-__device__ __forceinline__ int cvt_flr(float x) {
-    int r;
-    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
-    return r;
+// A fitted weight is the integer nearest (ties to even) to fl(u*A + B):
+// adding 1.5*2^23 rounds that value to an integer in the low mantissa bits,
+// the bit pattern being kFitM + w (|w| < 2^22).
+constexpr uint32_t kFitM = 0x4B400000u;
+__device__ __forceinline__ float fit_rne(float x) { return x + 0x1.8p23f; }
+__device__ __forceinline__ int32_t fit_biased(float r) { return (int32_t)__float_as_uint(r); }
+// two of them (fit_rne values) as one int16 pair: the low halves
+__device__ __forceinline__ uint32_t pk_rne(float r0, float r1) {
+    return __builtin_amdgcn_perm(__float_as_uint(r1), __float_as_uint(r0), 0x05040100u);
 }
 
 // two int32 -> one dword of saturated int16 (lo = a, hi = b)
@@ -193,11 +197,11 @@ __device__ __forceinline__ void mac4(float e0, float e1, float e2, float e3, flo
     }
 }
 
-// 4 int16 weights (as int32) -> two pairs -> dot with the activation pairs
-// kx, kx+1
+// 4 fitted weights (fit_rne values) -> two int16 pairs -> dot with the
+// activation pairs kx, kx+1
 template <class AT>
-__device__ __forceinline__ void mac4i(int w0, int w1, int w2, int w3, const AT& A, int kx, int& sh, int& sl) {
-    const uint32_t P0 = pk16(w0, w1), P1 = pk16(w2, w3);
+__device__ __forceinline__ void mac4r(float r0, float r1, float r2, float r3, const AT& A, int kx, int& sh, int& sl) {
+    const uint32_t P0 = pk_rne(r0, r1), P1 = pk_rne(r2, r3);
     if constexpr (AT::kSink) {
         A.put(kx, P0);
         A.put(kx + 1, P1);
@@ -221,14 +225,15 @@ __device__ __forceinline__ void mac4i(int w0, int w1, int w2, int w3, const AT& 
 //
 // Fitted blocks (tensors normalised at upload): within one block of one row
 // the int16 weight is a function g(u) of the 5-bit code u alone, and
-// g(u) = floor(u*A + B) for a pair (A, B) found at upload (fit_kernel)
-// and checked there against the exact g on every code the block holds.
-// A and B are d*row_inv and 0.5 - 16A (fp32, as computed here) moved by a
-// few ulps, coded in one byte per block and row (plane pe, fit_a/fit_b).
-// The code goes into an f16 lane as the subnormal u*2^-24, so one
-// v_fma_mix with A*2^24 forms u*A + B with a single rounding, and v_cvt_flr
-// gives the weight: 2 instructions per weight instead of 4.  The K-quants
-// fit each 32-weight (Q4_K) or 16-weight (Q6_K) sub-block the same way.
+// g(u) = rne(fl(u*A + B)) (nearest integer, ties to even) for a pair
+// (A, B) found at upload (fit_kernel) and checked there against the exact
+// g on every code the block holds.  A and B are d*row_inv and -16A (fp32,
+// as computed here) moved by a few ulps, coded in one byte per block and
+// row (plane pe, fit_a/fit_b).  The code goes into an f16 lane as the
+// subnormal u*2^-24, so one v_fma_mix with A*2^24 forms u*A + B with a
+// single rounding, and one add of 1.5*2^23 (fit_rne) leaves the weight in
+// the low bits: 2 instructions per weight instead of 4.  The K-quants fit
+// each 32-weight (Q4_K) or 16-weight (Q6_K) sub-block the same way.
 struct Q5Blk {
     uint4 qs;
     uint32_t qh, d, e;
@@ -257,13 +262,13 @@ __device__ __forceinline__ float fit_b(float b0, uint32_t e) { return fit_mv(b0,
 template <class AT>
 __device__ __forceinline__ void q5_mac_fit(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
     const float a = fit_a(h2f(k.d) * inv, k.e);
-    const float a24 = a * 0x1p24f, bb = fit_b(__builtin_fmaf(-16.0f, a, 0.5f), k.e);
+    const float a24 = a * 0x1p24f, bb = fit_b(-16.0f * a, k.e);
 #pragma unroll
     for (int g = 0; g < 8; g++) {
         const uint32_t U = q5_codes(k, g);
         const tmq_h2 l0 = lanes01(U), l1 = lanes23(U);
-        mac4i(cvt_flr(__builtin_fmaf((float)l0.x, a24, bb)), cvt_flr(__builtin_fmaf((float)l0.y, a24, bb)),
-              cvt_flr(__builtin_fmaf((float)l1.x, a24, bb)), cvt_flr(__builtin_fmaf((float)l1.y, a24, bb)), A,
+        mac4r(fit_rne(__builtin_fmaf((float)l0.x, a24, bb)), fit_rne(__builtin_fmaf((float)l0.y, a24, bb)),
+              fit_rne(__builtin_fmaf((float)l1.x, a24, bb)), fit_rne(__builtin_fmaf((float)l1.y, a24, bb)), A,
               b * 16 + 2 * g, sh, sl);
     }
 }
@@ -272,17 +277,22 @@ __device__ __forceinline__ void q5_mac_fit(const Q5Blk& k, const AT& A, int b, f
 __device__ __forceinline__ void q5_fit64(const Q5Blk& k, const int32_t (&x)[32], float inv, int64_t& acc0,
                                          int64_t& acc1) {
     const float a = fit_a(h2f(k.d) * inv, k.e);
-    const float a24 = a * 0x1p24f, bb = fit_b(__builtin_fmaf(-16.0f, a, 0.5f), k.e);
+    const float a24 = a * 0x1p24f, bb = fit_b(-16.0f * a, k.e);
 #pragma unroll
     for (int g = 0; g < 8; g++) {
         const uint32_t U = q5_codes(k, g);
         const tmq_h2 l0 = lanes01(U), l1 = lanes23(U);
         int64_t& c = (g & 1) ? acc1 : acc0;
-        c += (int64_t)cvt_flr(__builtin_fmaf((float)l0.x, a24, bb)) * x[4 * g];
-        c += (int64_t)cvt_flr(__builtin_fmaf((float)l0.y, a24, bb)) * x[4 * g + 1];
-        c += (int64_t)cvt_flr(__builtin_fmaf((float)l1.x, a24, bb)) * x[4 * g + 2];
-        c += (int64_t)cvt_flr(__builtin_fmaf((float)l1.y, a24, bb)) * x[4 * g + 3];
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l0.x, a24, bb))) * x[4 * g];
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l0.y, a24, bb))) * x[4 * g + 1];
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l1.x, a24, bb))) * x[4 * g + 2];
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l1.y, a24, bb))) * x[4 * g + 3];
     }
+    // every term carried kFitM: take kFitM * sum(x) off (a wave-uniform sum)
+    int32_t xs = 0;
+#pragma unroll
+    for (int i = 0; i < 32; i++) xs += x[i];
+    acc1 -= (int64_t)kFitM * xs;
 }
 template <bool CLAMP, class AT>
 __device__ __forceinline__ void q5_mac_exact(const Q5Blk& k, const AT& A, int b, float inv, int& sh, int& sl) {
@@ -348,13 +358,13 @@ __device__ __forceinline__ Q4KBlk q4k_load(const TmqTensorDev& t, int b, int r) 
     return k;
 }
 // sub-block s = 2sp + hi of a quarter fitted: A = (d*sc)*row_inv and
-// B = 0.5 - (dmin*m)*row_inv (one fma), both moved by its code; the high
+// B = -(dmin*m)*row_inv, both moved by its code; the high
 // nibbles sit in their lanes as 16u*2^-24, hence A*2^20.  Pair kx of
 // dwords (hf, i) is kx0 + 8hf + 2i (+1).
 template <class AT>
 __device__ __forceinline__ void q4k_sub_fit(float Ad, float Bm, uint32_t e, const uint4& qsa, const uint4& qsb, int hi,
                                             const AT& A, int kx0, float inv, int& sh, int& sl) {
-    const float a = fit_a(Ad * inv, e) * (hi ? 0x1p20f : 0x1p24f), bb = fit_b(__builtin_fmaf(-Bm, inv, 0.5f), e);
+    const float a = fit_a(Ad * inv, e) * (hi ? 0x1p20f : 0x1p24f), bb = fit_b(-Bm * inv, e);
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
         const uint4& qs = hf ? qsb : qsa;
@@ -362,11 +372,38 @@ __device__ __forceinline__ void q4k_sub_fit(float Ad, float Bm, uint32_t e, cons
         for (int i = 0; i < 4; i++) {
             const uint32_t w = dw_of(qs, i) & (hi ? 0xf0f0f0f0u : 0x0f0f0f0fu);
             const tmq_h2 l0 = lanes01(w), l1 = lanes23(w);
-            mac4i(cvt_flr(__builtin_fmaf((float)l0.x, a, bb)), cvt_flr(__builtin_fmaf((float)l0.y, a, bb)),
-                  cvt_flr(__builtin_fmaf((float)l1.x, a, bb)), cvt_flr(__builtin_fmaf((float)l1.y, a, bb)), A,
+            mac4r(fit_rne(__builtin_fmaf((float)l0.x, a, bb)), fit_rne(__builtin_fmaf((float)l0.y, a, bb)),
+                  fit_rne(__builtin_fmaf((float)l1.x, a, bb)), fit_rne(__builtin_fmaf((float)l1.y, a, bb)), A,
                   kx0 + 8 * hf + 2 * i, sh, sl);
         }
     }
+}
+// the same sub-block fitted, summed into int64 against the int32
+// activation x of its 32 elements (element 16hf + 4i + k: byte k of dword i
+// of qs[hf])
+__device__ __forceinline__ void q4k_sub_fit64(float Ad, float Bm, uint32_t e, const uint4& qsa, const uint4& qsb,
+                                              int hi, const int32_t (&x)[32], float inv, int64_t& acc0,
+                                              int64_t& acc1) {
+    const float a = fit_a(Ad * inv, e) * (hi ? 0x1p20f : 0x1p24f), bb = fit_b(-Bm * inv, e);
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        const uint4& qs = hf ? qsb : qsa;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = dw_of(qs, i) & (hi ? 0xf0f0f0f0u : 0x0f0f0f0fu);
+            const tmq_h2 l0 = lanes01(w), l1 = lanes23(w);
+            const int o = 16 * hf + 4 * i;
+            int64_t& c = (i & 1) ? acc1 : acc0;
+            c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l0.x, a, bb))) * x[o];
+            c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l0.y, a, bb))) * x[o + 1];
+            c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l1.x, a, bb))) * x[o + 2];
+            c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)l1.y, a, bb))) * x[o + 3];
+        }
+    }
+    int32_t xs = 0;
+#pragma unroll
+    for (int i = 0; i < 32; i++) xs += x[i];
+    acc1 -= (int64_t)kFitM * xs;
 }
 // the same sub-block, exact: E = fma_mix(lane, Ad*2^24 or Ad*2^20, -Bm)
 template <bool CLAMP, class AT>
@@ -463,21 +500,43 @@ __device__ __forceinline__ void q6k_sub_exact(float S, const uint4& qla, const u
                     sh, sl);
     }
 }
-// the same sub-block fitted: A = S*row_inv and B = 0.5 - 32A, both moved by
+// the same sub-block fitted: A = S*row_inv and B = -32A, both moved by
 // its code byte
 template <class AT>
 __device__ __forceinline__ void q6k_sub_fit(float S, uint32_t e, const uint4& qla, const uint4& qlb, const uint4& qhc,
                                             int sub, const AT& A, int kx0, float inv, int& sh, int& sl) {
     const float a = fit_a(S * inv, e);
-    const float a24 = a * 0x1p24f, bb = fit_b(__builtin_fmaf(-32.0f, a, 0.5f), e);
+    const float a24 = a * 0x1p24f, bb = fit_b(-32.0f * a, e);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t U = q6_codes(qla, qlb, qhc, sub, i);
         const tmq_h2 u0 = lanes01(U), u1 = lanes23(U);
-        mac4i(cvt_flr(__builtin_fmaf((float)u0.x, a24, bb)), cvt_flr(__builtin_fmaf((float)u0.y, a24, bb)),
-              cvt_flr(__builtin_fmaf((float)u1.x, a24, bb)), cvt_flr(__builtin_fmaf((float)u1.y, a24, bb)), A,
+        mac4r(fit_rne(__builtin_fmaf((float)u0.x, a24, bb)), fit_rne(__builtin_fmaf((float)u0.y, a24, bb)),
+              fit_rne(__builtin_fmaf((float)u1.x, a24, bb)), fit_rne(__builtin_fmaf((float)u1.y, a24, bb)), A,
               kx0 + 2 * i, sh, sl);
     }
+}
+// the same sub-block fitted, summed into int64 against the int32 activation
+// x of its 16 elements (element 4i + k: byte k of code dword i)
+__device__ __forceinline__ void q6k_sub_fit64(float S, uint32_t e, const uint4& qla, const uint4& qlb,
+                                              const uint4& qhc, int sub, const int32_t (&x)[16], float inv,
+                                              int64_t& acc0, int64_t& acc1) {
+    const float a = fit_a(S * inv, e);
+    const float a24 = a * 0x1p24f, bb = fit_b(-32.0f * a, e);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t U = q6_codes(qla, qlb, qhc, sub, i);
+        const tmq_h2 u0 = lanes01(U), u1 = lanes23(U);
+        int64_t& c = (i & 1) ? acc1 : acc0;
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)u0.x, a24, bb))) * x[4 * i];
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)u0.y, a24, bb))) * x[4 * i + 1];
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)u1.x, a24, bb))) * x[4 * i + 2];
+        c += (int64_t)fit_biased(fit_rne(__builtin_fmaf((float)u1.y, a24, bb))) * x[4 * i + 3];
+    }
+    int32_t xs = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) xs += x[i];
+    acc1 -= (int64_t)kFitM * xs;
 }
 // one quarter (half, lc: 64 weights) of a Q6_K block: sub-blocks
 // j = half*8 + lc + 2*sub, pairs 128b + 64half + 8lc + 16sub + 0..7
@@ -582,6 +641,56 @@ __device__ __forceinline__ void unit_mac(const typename UnitOf<FMT>::T& k, const
     else q6k_mac_q<CLAMP>(k.sc, k.e, h2f(k.d), k.qla, k.qlb, k.qhc, A, u >> 2, (u & 3) >> 1, u & 1, inv, sh, sl);
 }
 
+// A quarter unit with fitted sub-blocks summed into int64 (against the
+// int32 activation of the scalar-cache view) and the others exact.
+template <int FMT>
+__device__ __forceinline__ void unit_mac64(const typename UnitOf<FMT>::T& k, const Act& A, int u, float inv,
+                                           int64_t& acc0, int64_t& acc1) {
+    const int b = u >> 2, q = u & 3;
+    if constexpr (FMT == kQ4_K) {
+        const float d = h2f(k.h.x), dmin = h2f(k.h.x >> 16);
+#pragma unroll
+        for (int hi = 0; hi < 2; hi++) {
+            int sc, m;
+            q4k_scale_min(k.h, 2 * q + hi, sc, m);
+            const float Ad = d * (float)sc, Bm = dmin * (float)m;
+            const uint32_t e = (k.e >> (8 * hi)) & 0xffu;
+            const int e0 = 256 * b + 64 * q + 32 * hi;
+            int32_t x[32];
+#pragma unroll
+            for (int j = 0; j < 32; j++) x[j] = (int32_t)A.x32[e0 + j];
+            if (!(e & 0x80u)) {
+                q4k_sub_fit64(Ad, Bm, e, k.qa, k.qb, hi, x, inv, acc0, acc1);
+            } else {
+                int sh = 0, sl = 0;
+                q4k_sub_exact<false>(Ad, Bm, k.qa, k.qb, hi, A, 128 * b + 32 * q + 16 * hi, inv, sh, sl);
+                acc0 += (int64_t)sh * 256 + sl;
+            }
+        }
+    } else {
+        const int half = q >> 1, lc = q & 1;
+        const float ss = h2f(k.d);
+#pragma unroll
+        for (int sub = 0; sub < 4; sub++) {
+            const int j = half * 8 + lc + 2 * sub;
+            const float S = ss * (float)(int8_t)byte_of(k.sc, j);
+            const uint32_t ej = byte_of(k.e, j);
+            const int e0 = 256 * b + 128 * half + 32 * sub + 16 * lc;
+            int32_t x[16];
+#pragma unroll
+            for (int jj = 0; jj < 16; jj++) x[jj] = (int32_t)A.x32[e0 + jj];
+            if (!(ej & 0x80u)) {
+                q6k_sub_fit64(S, ej, k.qla, k.qlb, k.qhc, sub, x, inv, acc0, acc1);
+            } else {
+                int sh = 0, sl = 0;
+                q6k_sub_exact<false>(S, k.qla, k.qlb, k.qhc, sub, A, 128 * b + 64 * half + 8 * lc + 16 * sub, inv,
+                                     sh, sl);
+                acc0 += (int64_t)sh * 256 + sl;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- Q8_0
 // UQ8.8 combined scale of sim/tmac_gguf.cpp:1030-1037, including the x86
 // float->uint16 conversion (truncate to int32, keep the low 16 bits).
@@ -646,7 +755,7 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
     const float inv = t.row_inv[r];
     const Act A = act_view(w.act);
     int64_t acc = 0;
-    if (FMT == kQ5_0) {
+    if constexpr (FMT == kQ5_0) {
         // two blocks per step, the next step's two in flight (indices
         // clamped into the row, so every load is unconditional)
         constexpr int S = TMQ_WAVES;
@@ -709,19 +818,30 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
         // flight while it multiplies (the row sums are exact integers, so
         // the grouping does not change them)
         typedef typename UnitOf<FMT>::T Unit;
+        constexpr int S = TMQ_WAVES;
         const int u1 = b1 * 4;
-        int u = b0 * 4 + wave;
-        Unit cur{};
-        if (u < u1) cur = unit_load<FMT>(t, u, r);
-        for (; u < u1; u += TMQ_WAVES) {
-            const bool more = u + TMQ_WAVES < u1;
-            Unit nxt{};
-            if (more) nxt = unit_load<FMT>(t, u + TMQ_WAVES, r);
-            int sh = 0, sl = 0;
-            unit_mac<FMT, CLAMP>(cur, A, u, inv, sh, sl);
-            acc += (int64_t)sh * 256 + sl;
-            if (more) cur = nxt;
+        int64_t acc1 = 0;
+        auto ld = [&](int uu) { return unit_load<FMT>(t, min(uu, u1 - 1), r); };
+        auto mac = [&](const Unit& k, int uu) {
+            if constexpr (CLAMP) {
+                int sh = 0, sl = 0;
+                unit_mac<FMT, CLAMP>(k, A, uu, inv, sh, sl);
+                acc += (int64_t)sh * 256 + sl;
+            } else {
+                unit_mac64<FMT>(k, A, uu, inv, acc, acc1);
+            }
+        };
+        // two register sets in turn (clamped, unconditional loads), so that
+        // no copy waits on a load
+        Unit c0 = ld(b0 * 4 + wave);
+        for (int u = b0 * 4 + wave; u < u1; u += 2 * S) {
+            const Unit c1 = ld(u + S);
+            mac(c0, u);
+            if (u + S >= u1) break;
+            c0 = ld(u + 2 * S);
+            mac(c1, u + S);
         }
+        acc += acc1;
     }
 reduce:
     part[wave][lane] = acc;
@@ -1454,7 +1574,7 @@ __global__ void rowstat_kernel(TmqTensorDev t, const float* __restrict__ aux, fl
 
 // Fit codes (see Q5Blk): for each sub-block of block b of row r, the
 // smallest move (dA, dB), |dA|, |dB| <= 3 ulps by growing square rings, for
-// which floor(u*A + B) = g(u) on every code u the sub-block holds; else the
+// which rne(fl(u*A + B)) = g(u) on every code u the sub-block holds; else the
 // exact-decode flag.  g(u) is the exact decode's int16: the saturated
 // round-half-away of fl(E * row_inv), E the decoder's exact value of u.
 // n codes u[] with exact values E = gu(u) and A0, B0(A) as the decoders form them.
@@ -1472,7 +1592,7 @@ __device__ __forceinline__ uint32_t fit_search(const int (&u)[N], float a0, floa
                 bool ok = true;
 #pragma unroll
                 for (int i = 0; i < N; i++)
-                    ok = ok && max(-32768, min(32767, cvt_flr(__builtin_fmaf((float)u[i], a, bb)))) == g[i];
+                    ok = ok && fit_biased(fit_rne(__builtin_fmaf((float)u[i], a, bb))) - (int32_t)kFitM == g[i];
                 if (ok) return code;
             }
     return 0x80u;
@@ -1502,7 +1622,7 @@ __global__ __launch_bounds__(256) void fit_kernel(TmqTensorDev t, int all_exact)
         }
         pe[o] = (uint8_t)fit_search(
             u, d * inv, inv, [&](int c) { return d * (float)(c - 16); },
-            [](float a) { return __builtin_fmaf(-16.0f, a, 0.5f); });
+            [](float a) { return -16.0f * a; });
     } else if constexpr (FMT == kQ4_K) {
         const Q4KBlk k = q4k_load(t, b, r);
         const float d = h2f(k.h.x), dmin = h2f(k.h.x >> 16);
@@ -1517,7 +1637,7 @@ __global__ __launch_bounds__(256) void fit_kernel(TmqTensorDev t, int all_exact)
                 const uint32_t by = byte_of(k.qs[(s >> 1) * 2 + (i >> 4)], i & 15);
                 u[i] = (int)((s & 1) ? (by >> 4) : (by & 15u));
             }
-            const float b0 = __builtin_fmaf(-Bm, inv, 0.5f);
+            const float b0 = -Bm * inv;
             pe[o * 8 + s] = (uint8_t)fit_search(
                 u, Ad * inv, inv, [&](int c) { return __builtin_fmaf((float)c, Ad, -Bm); },
                 [&](float) { return b0; });
@@ -1542,7 +1662,7 @@ __global__ __launch_bounds__(256) void fit_kernel(TmqTensorDev t, int all_exact)
                 }
                 pe[o * 16 + j] = (uint8_t)fit_search(
                     u, S * inv, inv, [&](int c) { return S * (float)(c - 32); },
-                    [](float a) { return __builtin_fmaf(-32.0f, a, 0.5f); });
+                    [](float a) { return -32.0f * a; });
             }
         }
     }
