@@ -742,12 +742,14 @@ __device__ __forceinline__ void store_y(const TmqWork& w, int r, float v) {
     w.y[r] = v;
 }
 
-// K-split group (Q5_0 / K-quants): 4 waves share 64 rows, wave w takes
-// blocks w, w+4, ...; the int32 pair sums are folded into int64 every 256
+// K-split group (Q5_0 / K-quants): NWV waves share 64 rows (4 for Q5_0, 8
+// for the K-quants, whose rows are long: shorter waves balance the CUs),
+// wave w takes blocks w, w+NWV, ...; the int32 pair sums are folded into int64 every 256
 // weights at most (|sum| < 2^31), then the waves meet in LDS.
 template <int FMT, bool CLAMP>
 __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
-    __shared__ int64_t part[TMQ_WAVES][64];
+    constexpr int NWV = gemv_waves(FMT);
+    __shared__ int64_t part[NWV][64];
     const TmqTensorDev& t = w.t;
     const int b0 = 0, b1 = t.nb;
     const int lane = threadIdx.x & 63, wave = wave_id();
@@ -758,7 +760,7 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
     if constexpr (FMT == kQ5_0) {
         // two blocks per step, the next step's two in flight (indices
         // clamped into the row, so every load is unconditional)
-        constexpr int S = TMQ_WAVES;
+        constexpr int S = NWV;
         if (b1 - b0 == 7 * S) {
             // 896 columns (7 blocks per wave): every load of the wave is
             // issued at once, the blocks are multiplied as they arrive
@@ -818,7 +820,7 @@ __device__ __forceinline__ void group_ksplit(const TmqWork& w, int g) {
         // flight while it multiplies (the row sums are exact integers, so
         // the grouping does not change them)
         typedef typename UnitOf<FMT>::T Unit;
-        constexpr int S = TMQ_WAVES;
+        constexpr int S = NWV;
         const int u1 = b1 * 4;
         int64_t acc1 = 0;
         auto ld = [&](int uu) { return unit_load<FMT>(t, min(uu, u1 - 1), r); };
@@ -847,7 +849,9 @@ reduce:
     part[wave][lane] = acc;
     __syncthreads();
     int64_t tot = 0;
-    if (wave == 0) tot = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
+    if (wave == 0)
+#pragma unroll
+        for (int i = 0; i < NWV; i++) tot += part[i][lane];
     if (wave == 0 && r < t.rows) {
         if (w.acc) w.acc[r] = tot;
         // sim/tmac_gguf.cpp:1303-1305: y = 0.0f; y += (double)acc*x_scale/(double)row_inv
@@ -898,14 +902,14 @@ __device__ __forceinline__ void run_group(const TmqWork& w, int g) {
 
 // one GEMV
 template <int FMT, bool CLAMP>
-__global__ __launch_bounds__(TMQ_WG) void gemv_kernel(TmqWork w) {
+__global__ __launch_bounds__(64 * gemv_waves(FMT)) void gemv_kernel(TmqWork w) {
     run_group<FMT, CLAMP>(w, blockIdx.x);
 }
 
 // A chain segment: every descriptor of one format in one launch,
 // workgroup -> (descriptor, group) through the group map.
 template <int FMT, bool CLAMP>
-__global__ __launch_bounds__(TMQ_WG) void chain_kernel(const TmqWork* __restrict__ works,
+__global__ __launch_bounds__(64 * gemv_waves(FMT)) void chain_kernel(const TmqWork* __restrict__ works,
                                                        const int32_t* __restrict__ group_work) {
     const TmqWork& w = works[group_work[blockIdx.x]];
     run_group<FMT, CLAMP>(w, blockIdx.x - w.first_group);
@@ -1968,7 +1972,7 @@ int tmq_launch_gemv(const TmqWork& w, hipStream_t s) {
     if (!k) return (int)hipErrorInvalidValue;
     TmqWork arg = w;
     void* args[] = {&arg};
-    return (int)hipLaunchKernel(k, dim3(w.ngroups), dim3(TMQ_WG), args, 0, s);
+    return (int)hipLaunchKernel(k, dim3(w.ngroups), dim3(64 * gemv_waves(w.t.type)), args, 0, s);
 }
 
 int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_t* group_work_dev,
@@ -1977,7 +1981,7 @@ int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_
     void* k = kernel_for<ChainK>(type, clamp);
     if (!k) return (int)hipErrorInvalidValue;
     void* args[] = {&works_dev, &group_work_dev};
-    return (int)hipLaunchKernel(k, dim3(total_groups), dim3(TMQ_WG), args, 0, s);
+    return (int)hipLaunchKernel(k, dim3(total_groups), dim3(64 * gemv_waves(type)), args, 0, s);
 }
 
 int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* out, hipStream_t s) {
