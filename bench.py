@@ -138,6 +138,8 @@ def measure(ctx, torch, dev, stream, name, steps, warmup, copies=None):
     ctx.sync()
     chain.prepare()
     ctx.sync()
+    for _ in range(warmup // 4):
+        chain.launch()
     kern_ms = time_events(torch, stream, chain.launch, steps)
     ctx.sync()
     torch.cuda.synchronize()
@@ -268,8 +270,12 @@ def copy_calibration(torch, dev, nbytes=1 << 30):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # GEMV chains: the GPU's clock dips for a few hundred launches after a burst
+    # and then settles, so the default warm-up runs into the settled state
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 200 GEMV chain launches, 128 decode tokens, 20 prefills)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default: 400 chain launches, 8 tokens, 1 prefill)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--sets", type=int, default=SETS)
@@ -279,6 +285,11 @@ def main():
                          "c5: only the 512-token batched prefill (BASELINE configs[4])")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE GEMV configs")
     args = ap.parse_args()
+    dflt = {"c4": (128, 8), "c5": (20, 1)}.get(args.workload, (200, 400))
+    if args.steps is None:
+        args.steps = dflt[0]
+    if args.warmup is None:
+        args.warmup = dflt[1]
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only; the GEMV shards by output rows with "
@@ -368,7 +379,7 @@ def main():
     if not args.no_extra and wl == "c2":
         extra = {}
         for name in ("c1", "c3q4k", "c3q6k"):
-            _, wb, sm, km, nd = measure(ctx, torch, dev, stream, name, max(10, args.steps // 2), 2)
+            _, wb, sm, km, nd = measure(ctx, torch, dev, stream, name, max(10, args.steps // 2), args.warmup)
             extra[name] = {"weight_bytes": wb, "descriptors": nd, "ms_per_launch": round(km, 5),
                            "gbps": round(wb / (km * 1e-3) / 1e9, 2),
                            "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
