@@ -22,9 +22,10 @@
 #define TMQ_ROWS_PER_GROUP 64
 #define TMQ_WAVES 4
 #define TMQ_WG (64 * TMQ_WAVES)
-// waves per workgroup of the standalone / chain GEMVs of a type (Q4_K,
-// Q6_K: 8, so that their long rows split into shorter waves)
-constexpr int gemv_waves(int type) { return type == 12 || type == 14 ? 8 : TMQ_WAVES; }
+// waves per workgroup of the standalone / chain GEMVs of a type (Q6_K: 8,
+// its long rows split into shorter waves; measured 4 % faster for Q6_K and
+// 4 % slower for Q4_K on the 896x4864 BASELINE shapes)
+constexpr int gemv_waves(int type) { return type == 14 ? 8 : TMQ_WAVES; }
 #define TMQ_Q8_MAX_TILES 256  // cols <= 16384 for Q8_0
 
 struct TmqTensorDev {

@@ -742,8 +742,7 @@ __device__ __forceinline__ void store_y(const TmqWork& w, int r, float v) {
     w.y[r] = v;
 }
 
-// K-split group (Q5_0 / K-quants): NWV waves share 64 rows (4 for Q5_0, 8
-// for the K-quants, whose rows are long: shorter waves balance the CUs),
+// K-split group (Q5_0 / K-quants): NWV waves (gemv_waves) share 64 rows,
 // wave w takes blocks w, w+NWV, ...; the int32 pair sums are folded into int64 every 256
 // weights at most (|sum| < 2^31), then the waves meet in LDS.
 template <int FMT, bool CLAMP>
