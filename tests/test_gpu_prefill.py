@@ -111,6 +111,32 @@ def test_prefill_errors(model):
         model.set_prefill(-1)
 
 
+def test_norm_sum_fallback(ctx, model, monkeypatch):
+    """RMSNorm's sequential sum of squares runs in segments from speculated
+    starting values, each checked against the exact end of the segment
+    before it.  With TMQ_SPEC_MISS=1 at load every speculation is rejected
+    and every segment re-run from its exact start: the same bits, one token
+    at a time, batched, and in the decode steps after the prompt."""
+    import tmq
+    from tmq import model_synth, tmacfile
+    toks = prompt_of(40, 4040)
+    exp = {c: run(model, toks, c, gen=3) for c in (0, 512)}
+    monkeypatch.setenv("TMQ_SPEC_MISS", "1")
+    print("[prefill] model with every norm segment re-run", flush=True)
+    blob = tmacfile.to_bytes(model_synth.gen_model(MODEL_SEED))
+    m = tmq.Model(ctx, blob, max_seq=64)
+    del blob
+    try:
+        for c in (0, 512):
+            l1, h1, g1 = run(m, toks, c, gen=3)
+            l0, h0, g0 = exp[c]
+            assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32)), f"chunk {c}"
+            assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32)), f"chunk {c}"
+            assert g1.tolist() == g0.tolist()
+    finally:
+        m.free()
+
+
 @pytest.mark.parametrize("chunk", [0, 512, 8])
 def test_prompt_matches_reference(model, chunk):
     """the compiled reference's own process_prompt over a 24-token prompt

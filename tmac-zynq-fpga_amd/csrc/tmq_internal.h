@@ -126,7 +126,7 @@ struct TmqEngAct {
     const float* w;            // NORM modes: RMSNorm weight (null: no norm)
     const uint32_t* max_bits;  // PRESCALED: bits of max|x| (atomic max of non-negative floats)
     float eps;
-    int32_t pad_;
+    int32_t spec_miss;         // nonzero: the norm's segmented sum re-runs every segment (testing)
     TmqDeferred d1;            // RESID_NORM: the residual term
     float* hidden_out;
     TmqEngState* state;        // EMBED_NORM: token = tokens[state->pos]

@@ -993,14 +993,14 @@ __device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw) {
     return L;
 }
 
-// Sequential fp32 sum of v[0..n) in index order (the reference's loops),
-// by the calling lane, from LDS.  A dependent fp32 add issues every ~8
-// cycles; the reads of the next 32 values overlap the current 32 adds
-// (two register batches used in turn, no copies between them).
-__device__ __forceinline__ float seq_sum_lds(const float* v, int n) {
-    float sum = 0.0f;
-    const int n64 = n & ~63;
-    const float4* q = (const float4*)v;
+// Sequential fp32 sum of v[i0..i1) in index order from `sum` (the
+// reference's loops), by the calling lane, from LDS (i0 a multiple of 4).  A
+// dependent fp32 add issues every ~8 cycles; the reads of the next 32 values
+// overlap the current 32 adds (two register batches used in turn, no copies
+// between them).
+__device__ __forceinline__ float seq_chain_lds(const float* v, int i0, int i1, float sum) {
+    const int n64 = (i1 - i0) & ~63;
+    const float4* q = (const float4*)(v + i0);
     float4 A[8], B[8];
     if (n64) {
 #pragma unroll
@@ -1028,7 +1028,70 @@ __device__ __forceinline__ float seq_sum_lds(const float* v, int n) {
             sum += B[j].w;
         }
     }
-    for (int i = n64; i < n; i++) sum += v[i];
+    for (int i = i0 + n64; i < i1; i++) sum += v[i];
+    return sum;
+}
+
+// The same sequential sum of v[0..n) (0 + v[0] + v[1] + ..., each add
+// rounded), by S waves of the workgroup at once; every thread calls it, and
+// the result is returned to the lanes of wave 0.  The column range is cut
+// into S segments of L values; wave j runs segment j from 64 starting
+// values, lane l from the float whose bits are those of c_j plus l - 32,
+// c_j being the fp64 sum of v[0 .. jL) rounded to float (wave 0 from the
+// exact start, 0).  Wave 0 then walks the segments in order: the exact
+// start of segment j is the result of segment j-1, and the lane that
+// started from those very bits performed exactly the sequential adds of
+// that segment, so its result is taken.  When no lane did (the fp32 chain
+// drifted more than 32 ulps from the fp64 sum, as over long runs of equal
+// values), wave 0 runs the segment from the exact start.  For v >= 0 the
+// float bits order the values, so the 64 starts are 64 consecutive floats.
+// miss != 0 moves every window away (each segment then runs again: a test
+// of that path).  scr: 2*S*64 words of LDS, scr_c: S words.
+template <int S>
+__device__ __forceinline__ float seq_sum_spec(const float* v, int n, float* scr, int* scr_c, int miss) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int L = ((n + S - 1) / S + 63) & ~63;  // whole batches of 64 adds
+    int* st = (int*)(scr + S * 64);
+    if (wave < S) {
+        const int j0 = min(n, wave * L), j1 = min(n, j0 + L);
+        double p = 0.0;
+        for (int i = lane; i < j0; i += 64) p += (double)v[i];
+        for (int o = 32; o > 0; o >>= 1) p += __shfl_xor(p, o);
+        // one centre for the wave (the lanes' butterfly sums may differ in
+        // their last bits)
+        const int cb = __shfl((int)__float_as_uint((float)p), 0) + (miss ? (1 << 20) : 0);
+        const int sb = wave == 0 ? 0 : max(0, cb + lane - 32);
+        scr[wave * 64 + lane] = seq_chain_lds(v, j0, j1, __uint_as_float((uint32_t)sb));
+        st[wave * 64 + lane] = sb;
+        if (lane == 0) scr_c[wave] = cb;
+    }
+    __syncthreads();
+    float sum = 0.0f;
+    if (wave == 0) {
+        // every segment's results and starts into registers (lane l holds
+        // lane l's), then the walk reads them across lanes with uniform
+        // indices: no LDS round trip per segment
+        float o[S];
+        int t[S], c[S];
+#pragma unroll
+        for (int j = 0; j < S; j++) {
+            o[j] = scr[j * 64 + lane];
+            t[j] = st[j * 64 + lane];
+            c[j] = scr_c[j];
+        }
+        sum = o[0];  // wave 0 ran from the exact start in every lane
+#pragma unroll
+        for (int j = 1; j < S; j++) {
+            const int j0 = min(n, j * L), j1 = min(n, j0 + L);
+            if (j0 >= j1) break;
+            const int sb = __builtin_amdgcn_readfirstlane((int)__float_as_uint(sum));
+            const int idx = sb - __builtin_amdgcn_readfirstlane(c[j]) + 32;
+            const int li = idx & 63;
+            const bool hit = idx == li && __builtin_amdgcn_readlane(t[j], li) == sb;
+            sum = hit ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(o[j]), li))
+                      : seq_chain_lds(v, j0, j1, sum);
+        }
+    }
     return sum;
 }
 
@@ -1046,8 +1109,9 @@ __device__ __forceinline__ float seq_sum_lds(const float* v, int n) {
 // in order, so the activation arrives without waiting for the (cold) weights.
 // The common modes take up to EP elements per thread with every load issued
 // unconditionally (clamped indices), so no load waits for another.
-template <int EP, class Pre>
+template <int NW, class Pre>
 __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& L, int c0, int c1, Pre&& pre) {
+    constexpr int EP = NW >= 16 ? 1 : 4;
     const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
     const bool wr = a.hidden_out && blockIdx.x == 0;
     const bool norm = (a.mode == TMQ_ACT_RESID_NORM || a.mode == TMQ_ACT_EMBED_NORM) && a.w;
@@ -1142,10 +1206,10 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
     __syncthreads();
     float s = 1.0f;  // the norm's scale
     if (norm) {
-        if (tid == 0) {
-            const float mean = seq_sum_lds(sq, n) / (float)n;
-            L.red[0] = 1.0f / sqrtf(mean + a.eps);
-        }
+        // L.part is free until the row sums; red[32..48) is unused
+        constexpr int S = NW >= 8 ? 8 : NW;
+        const float ss = seq_sum_spec<S>(sq, n, (float*)L.part, (int*)(L.red + 32), a.spec_miss);
+        if (tid == 0) L.red[0] = 1.0f / sqrtf(ss / (float)n + a.eps);
         __syncthreads();
         s = L.red[0];
     }
@@ -1196,7 +1260,7 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
     Unit cur{};
     float inv = 0.0f;
     constexpr int QK = FMT == kQ5_0 ? 32 : 256, PB = UnitOf<FMT>::per_block;
-    const float xs = eng_prologue<NW >= 16 ? 1 : 4>(a, L, (u0 / PB) * QK, ((u1 + PB - 1) / PB) * QK, [&] {
+    const float xs = eng_prologue<NW>(a, L, (u0 / PB) * QK, ((u1 + PB - 1) / PB) * QK, [&] {
         // unconditional (a clamped, valid unit): the prologue's waits then
         // count these loads exactly and skip them
         cur = unit_load<FMT>(t, max(0, min(u0 + wave, nu - 1)), r);
@@ -1265,7 +1329,7 @@ __device__ __forceinline__ void eng_group_q8_split(const TmqEngAct& a, const Eng
     const int r = g * 64 + lane;
     Q8Blk b0{}, b1{};
     float ri = 0.0f;
-    const float xs = eng_prologue<NW >= 16 ? 1 : 4>(a, L, 64 * t0, min(64 * t1, t.cols), [&] {
+    const float xs = eng_prologue<NW>(a, L, 64 * t0, min(64 * t1, t.cols), [&] {
         const int tt = max(0, min(t0 + wave, nt - 1));
         b0 = q8_load(t, 2 * tt, r);
         b1 = q8_load(t, min(2 * tt + 1, t.nb - 1), r);
@@ -1307,7 +1371,7 @@ __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L
     const int r = active ? r0 + lane : lane;
     Q8Blk cur{};
     float ri = 0.0f, rs = 0.0f;
-    const ActL A = eng_act(L, eng_prologue<NW >= 16 ? 1 : 4>(a, L, 0, t.cols, [&] {
+    const ActL A = eng_act(L, eng_prologue<NW>(a, L, 0, t.cols, [&] {
         cur = q8_load(t, 0, r);
         ri = t.row_inv[r];
         rs = t.row_scale[r];
@@ -1732,6 +1796,8 @@ template <int G>
 __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     extern __shared__ float pf_lds[];
     __shared__ float red[8];
+    __shared__ __attribute__((aligned(16))) float spec[2 * 4 * 64];  // seq_sum_spec<4>
+    __shared__ int spec_c[4];
     const int t = blockIdx.x, n = a.n, tid = threadIdx.x, nt = blockDim.x;
     const int wave = tid >> 6, lane = tid & 63, nc = n / TMQ_PF_CHUNK, ng = n >> 2;
     int8_t* dp = a.out.d;
@@ -1862,10 +1928,8 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     __syncthreads();
     float s = 1.0f;
     if (norm) {
-        if (tid == 0) {
-            const float mean = seq_sum_lds(sq, n) / (float)n;
-            red[0] = 1.0f / sqrtf(mean + a.eps);
-        }
+        const float ss = seq_sum_spec<4>(sq, n, spec, spec_c, a.spec_miss);
+        if (tid == 0) red[0] = 1.0f / sqrtf(ss / (float)n + a.eps);
         __syncthreads();
         s = red[0];
     }

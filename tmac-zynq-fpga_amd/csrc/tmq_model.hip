@@ -167,6 +167,7 @@ struct tmq_model {
     // tmq_model_profile: an event before and after every launch
     std::vector<std::pair<const char*, hipEvent_t>>* prof = nullptr;
     int prefill_chunk = 512;  // 0: prompts run one token at a time
+    int spec_miss = 0;        // TMQ_SPEC_MISS=1: every RMSNorm sum segment re-runs (testing)
     const char* prefill_off = nullptr;  // why the model cannot use the batched prefill
     Prefill pf;
 };
@@ -489,6 +490,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         a.x = x;
         a.w = w;
         a.eps = c.norm_eps;
+        a.spec_miss = m->spec_miss;
         a.out = P.in[set];
         a.out.rows = T_pad;
         a.xs = P.xs[set];
@@ -891,6 +893,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
         a.x = x;
         a.w = w;
         a.eps = c.norm_eps;
+        a.spec_miss = m->spec_miss;
         a.state = m->state;
         return a;
     };
@@ -973,6 +976,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
     HIP_TRY(hipStreamSynchronize(s));
     m->use_graphs = env_int("TMQ_GRAPHS", 1) != 0;
+    m->spec_miss = env_int("TMQ_SPEC_MISS", 0) != 0;
     m->prefill_chunk = env_int("TMQ_PREFILL", 512);
     m->prefill_off = pf_unsupported(m);
     return 0;

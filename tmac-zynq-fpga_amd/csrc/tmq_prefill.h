@@ -76,7 +76,7 @@ struct TmqPfAct {
     const float* x;            // [T][n]
     const float* w;            // RMSNorm weight (norm modes)
     float eps;
-    int32_t pad_;
+    int32_t spec_miss;         // as TmqEngAct::spec_miss
     const uint32_t* max_bits;  // SILU: per token
     TmqPfPart d1;              // RESID_NORM
     float* x_out;              // EMBED/RESID: the value before the norm, [T][n]
