@@ -975,13 +975,15 @@ __device__ float tensor_elem(const TmqTensorDev& t, int r, int j) {
 
 // LDS carve-up of an engine workgroup: x[n] fp32 | xh[n/2] xl[n/2] (the
 // squares of RMSNorm alias xh/xl before the quantisation) | part[NW*64] int64
-// | red[64]
+// | red[64] | spec[16*64] spec_c[16] (the norm's segmented sum)
 struct EngLds {
     float* x;
     uint32_t* xh;
     uint32_t* xl;
     int64_t* part;
     float* red;
+    float* spec;
+    int* spec_c;
 };
 __device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw) {
     EngLds L;
@@ -990,6 +992,8 @@ __device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw) {
     L.xl = L.xh + n / 2;
     L.part = (int64_t*)(base + 8 * (size_t)n);
     L.red = (float*)(L.part + nw * 64);
+    L.spec = L.red + 64;
+    L.spec_c = (int*)(L.spec + 16 * 64);
     return L;
 }
 
@@ -1032,64 +1036,102 @@ __device__ __forceinline__ float seq_chain_lds(const float* v, int i0, int i1, f
     return sum;
 }
 
+// One DPP move of a double across lanes (lanes the control leaves without a
+// source, or outside ROW_MASK, read 0.0).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, 0xf, false);
+    return __hiloint2double(hi, lo);
+}
+// Sum of x over the wave's 64 lanes, complete in lane 63: pairs and quads
+// (quad permutations), rows of 8 and 16 (half-row and row mirrors), then
+// row 0 into row 1 and row 2 into row 3 (row_bcast15), rows 0-1 into row 3
+// (row_bcast31).  VALU lane moves only, no LDS round trips.
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    x += dpp_f64<0xb1>(x);       // quad_perm [1,0,3,2]
+    x += dpp_f64<0x4e>(x);       // quad_perm [2,3,0,1]
+    x += dpp_f64<0x141>(x);      // row_half_mirror
+    x += dpp_f64<0x140>(x);      // row_mirror
+    x += dpp_f64<0x142, 0xa>(x);  // row_bcast15
+    x += dpp_f64<0x143, 0xc>(x);  // row_bcast31
+    return x;
+}
+
 // The same sequential sum of v[0..n) (0 + v[0] + v[1] + ..., each add
-// rounded), by S waves of the workgroup at once; every thread calls it, and
-// the result is returned to the lanes of wave 0.  The column range is cut
-// into S segments of L values; wave j runs segment j from 64 starting
-// values, lane l from the float whose bits are those of c_j plus l - 32,
-// c_j being the fp64 sum of v[0 .. jL) rounded to float (wave 0 from the
-// exact start, 0).  Wave 0 then walks the segments in order: the exact
-// start of segment j is the result of segment j-1, and the lane that
-// started from those very bits performed exactly the sequential adds of
-// that segment, so its result is taken.  When no lane did (the fp32 chain
-// drifted more than 32 ulps from the fp64 sum, as over long runs of equal
-// values), wave 0 runs the segment from the exact start.  For v >= 0 the
-// float bits order the values, so the 64 starts are 64 consecutive floats.
-// miss != 0 moves every window away (each segment then runs again: a test
-// of that path).  scr: 2*S*64 words of LDS, scr_c: S words.
+// rounded; n a multiple of 4), by S waves of the workgroup at once (S at
+// most the workgroup's waves); every thread calls it, and the result is
+// returned to the lanes of wave 0.  The range is cut into S segments of L
+// values (whole batches of 64); wave j runs segment j from 64 starting
+// values, lane l from the float whose bits are those of c_j plus l - 32, c_j
+// being the fp64 sum of v[0 .. jL) rounded to float (wave 0 from the exact
+// start, 0).  Wave 0 then walks the segments in order: the exact start of
+// segment j is the result of segment j-1, and the lane that started from
+// those very bits performed exactly the sequential adds of that segment, so
+// its result is taken.  When no lane did (the fp32 chain drifted more than
+// 32 ulps from the fp64 sum, as over long runs of equal values), wave 0 runs
+// the segment again from the exact start.  For v >= 0 the float bits order
+// the values, so the 64 starts are 64 consecutive floats; lane l started
+// from max(0, c_j + l - 32), which for the index l = b - c_j + 32 in
+// [0, 64) of an exact start with bits b is b itself whenever b >= 0 as an
+// integer (a float without its sign bit).  miss != 0 moves every window
+// away (each segment then runs again: a test of that path).  scr: S*64
+// words of LDS, scr_c: S words.
 template <int S>
 __device__ __forceinline__ float seq_sum_spec(const float* v, int n, float* scr, int* scr_c, int miss) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int L = ((n + S - 1) / S + 63) & ~63;  // whole batches of 64 adds
-    int* st = (int*)(scr + S * 64);
+    const int L = ((n + S - 1) / S + 63) & ~63;
     if (wave < S) {
         const int j0 = min(n, wave * L), j1 = min(n, j0 + L);
+        // centre: lane l adds the runs of 16 values at 16 l + 1024 i
         double p = 0.0;
-        for (int i = lane; i < j0; i += 64) p += (double)v[i];
-        for (int o = 32; o > 0; o >>= 1) p += __shfl_xor(p, o);
-        // one centre for the wave (the lanes' butterfly sums may differ in
-        // their last bits)
-        const int cb = __shfl((int)__float_as_uint((float)p), 0) + (miss ? (1 << 20) : 0);
-        const int sb = wave == 0 ? 0 : max(0, cb + lane - 32);
-        scr[wave * 64 + lane] = seq_chain_lds(v, j0, j1, __uint_as_float((uint32_t)sb));
-        st[wave * 64 + lane] = sb;
+        for (int base = 16 * lane; base < j0; base += 1024) {
+            float4 q4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) q4[e] = *(const float4*)(v + min(base + 4 * e, n - 4));
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x[4] = {q4[e].x, q4[e].y, q4[e].z, q4[e].w};
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (base + 4 * e + u < j0) p += (double)x[u];
+            }
+        }
+        const int cb = min(__builtin_amdgcn_readlane((int)__float_as_uint((float)wave_sum_f64(p)), 63), 0x7f800000) +
+                       (miss ? (1 << 20) : 0);
+        const float s0 = __uint_as_float((uint32_t)(wave == 0 ? 0 : max(0, cb + lane - 32)));
+        scr[wave * 64 + lane] = seq_chain_lds(v, j0, j1, s0);
         if (lane == 0) scr_c[wave] = cb;
     }
     __syncthreads();
     float sum = 0.0f;
     if (wave == 0) {
-        // every segment's results and starts into registers (lane l holds
-        // lane l's), then the walk reads them across lanes with uniform
-        // indices: no LDS round trip per segment
+        // the segments' results (lane l holds lane l's) and centres into
+        // registers, all read at once (the empty asm keeps the compiler from
+        // moving each read down to its step), then the walk reads them across
+        // lanes with uniform indices
         float o[S];
-        int t[S], c[S];
+        int c[S];
 #pragma unroll
         for (int j = 0; j < S; j++) {
             o[j] = scr[j * 64 + lane];
-            t[j] = st[j * 64 + lane];
             c[j] = scr_c[j];
         }
-        sum = o[0];  // wave 0 ran from the exact start in every lane
+#pragma unroll
+        for (int j = 0; j < S; j++) {
+            c[j] = __builtin_amdgcn_readfirstlane(c[j]);
+            asm volatile("" : "+v"(o[j]), "+s"(c[j]));
+        }
+        sum = o[0];  // segment 0 ran from the exact start in every lane
 #pragma unroll
         for (int j = 1; j < S; j++) {
             const int j0 = min(n, j * L), j1 = min(n, j0 + L);
             if (j0 >= j1) break;
             const int sb = __builtin_amdgcn_readfirstlane((int)__float_as_uint(sum));
-            const int idx = sb - __builtin_amdgcn_readfirstlane(c[j]) + 32;
+            const int idx = sb - c[j] + 32;
             const int li = idx & 63;
-            const bool hit = idx == li && __builtin_amdgcn_readlane(t[j], li) == sb;
-            sum = hit ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(o[j]), li))
-                      : seq_chain_lds(v, j0, j1, sum);
+            sum = idx == li && sb >= 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(o[j]), li))
+                                       : seq_chain_lds(v, j0, j1, sum);
         }
     }
     return sum;
@@ -1109,7 +1151,14 @@ __device__ __forceinline__ float seq_sum_spec(const float* v, int n, float* scr,
 // in order, so the activation arrives without waiting for the (cold) weights.
 // The common modes take up to EP elements per thread with every load issued
 // unconditionally (clamped indices), so no load waits for another.
-template <int NW, class Pre>
+// Segments of the norm's sum (seq_sum_spec), one a wave: 8 of a 16-wave
+// workgroup (4 where the format's units, or several works in one launch,
+// leave fewer of the 128 registers), or the four waves.  (16 segments of 64
+// measured slower: the walk's 13 steps cost more than the shorter chains
+// save.)
+template <int NW, int FMT, bool MULTI = false>
+constexpr int eng_norm_segs() { return NW < 16 || MULTI || FMT == kQ6_K ? 4 : 8; }
+template <int NW, int SEGS, class Pre>
 __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& L, int c0, int c1, Pre&& pre) {
     constexpr int EP = NW >= 16 ? 1 : 4;
     const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
@@ -1206,9 +1255,8 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
     __syncthreads();
     float s = 1.0f;  // the norm's scale
     if (norm) {
-        // L.part is free until the row sums; red[32..48) is unused
-        constexpr int S = NW >= 8 ? 8 : NW;
-        const float ss = seq_sum_spec<S>(sq, n, (float*)L.part, (int*)(L.red + 32), a.spec_miss);
+        static_assert(SEGS <= NW && SEGS <= 16, "a segment per wave");
+        const float ss = seq_sum_spec<SEGS>(sq, n, L.spec, L.spec_c, a.spec_miss);
         if (tid == 0) L.red[0] = 1.0f / sqrtf(ss / (float)n + a.eps);
         __syncthreads();
         s = L.red[0];
@@ -1248,7 +1296,7 @@ __device__ __forceinline__ ActL eng_act(const EngLds& L, float xs) {
 // Q5_0 / K-quant row group g, K chunk c: the workgroup's units are split
 // over its waves; each wave keeps its next unit in flight while it
 // multiplies.  With kc > 1 (or a kacc) the int64 row sums go to w.kacc.
-template <int FMT, int NW>
+template <int FMT, int NW, bool MULTI>
 __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int gi) {
     typedef typename UnitOf<FMT>::T Unit;
     const TmqTensorDev& t = w.t;
@@ -1260,7 +1308,7 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
     Unit cur{};
     float inv = 0.0f;
     constexpr int QK = FMT == kQ5_0 ? 32 : 256, PB = UnitOf<FMT>::per_block;
-    const float xs = eng_prologue<NW>(a, L, (u0 / PB) * QK, ((u1 + PB - 1) / PB) * QK, [&] {
+    const float xs = eng_prologue<NW, eng_norm_segs<NW, FMT, MULTI>()>(a, L, (u0 / PB) * QK, ((u1 + PB - 1) / PB) * QK, [&] {
         // unconditional (a clamped, valid unit): the prologue's waits then
         // count these loads exactly and skip them
         cur = unit_load<FMT>(t, max(0, min(u0 + wave, nu - 1)), r);
@@ -1319,7 +1367,7 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
 // Q8_0 K-split (attn_v): 64-row group g, tile chunk c; each wave takes
 // tiles (two blocks) of the chunk and stores their int64 P into
 // kacc[r][tile] (one writer per slot; the consumer folds the tiles in order).
-template <int NW>
+template <int NW, bool MULTI>
 __device__ __forceinline__ void eng_group_q8_split(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int gi) {
     const TmqTensorDev& t = w.t;
     const int kc = w.kc, g = gi / kc, c = gi - g * kc;
@@ -1329,7 +1377,7 @@ __device__ __forceinline__ void eng_group_q8_split(const TmqEngAct& a, const Eng
     const int r = g * 64 + lane;
     Q8Blk b0{}, b1{};
     float ri = 0.0f;
-    const float xs = eng_prologue<NW>(a, L, 64 * t0, min(64 * t1, t.cols), [&] {
+    const float xs = eng_prologue<NW, eng_norm_segs<NW, kQ8_0, MULTI>()>(a, L, 64 * t0, min(64 * t1, t.cols), [&] {
         const int tt = max(0, min(t0 + wave, nt - 1));
         b0 = q8_load(t, 2 * tt, r);
         b1 = q8_load(t, min(2 * tt + 1, t.nb - 1), r);
@@ -1371,7 +1419,7 @@ __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L
     const int r = active ? r0 + lane : lane;
     Q8Blk cur{};
     float ri = 0.0f, rs = 0.0f;
-    const ActL A = eng_act(L, eng_prologue<NW>(a, L, 0, t.cols, [&] {
+    const ActL A = eng_act(L, eng_prologue<NW, eng_norm_segs<NW, kQ8_0>()>(a, L, 0, t.cols, [&] {
         cur = q8_load(t, 0, r);
         ri = t.row_inv[r];
         rs = t.row_scale[r];
@@ -1410,12 +1458,12 @@ __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L
 // kQ8_DIRECT for the logits (Q8_0, one wave per 64 rows, direct output).
 constexpr int kQ8_DIRECT = 108;
 
-template <int NW, int FMT>
+template <int NW, int FMT, bool MULTI>
 __device__ __forceinline__ void eng_dispatch(const TmqEngAct& a, const EngLds& L, const TmqWork& w) {
     const int g = blockIdx.x - w.first_group;
-    if constexpr (FMT == kQ8_0) eng_group_q8_split<NW>(a, L, w, g);
+    if constexpr (FMT == kQ8_0) eng_group_q8_split<NW, MULTI>(a, L, w, g);
     else if constexpr (FMT == kQ8_DIRECT) eng_group_q8<NW>(a, L, w, g);
-    else eng_group_k<FMT, NW>(a, L, w, g);
+    else eng_group_k<FMT, NW, MULTI>(a, L, w, g);
 }
 
 // The launch arrives by value (kernel arguments): no dependent loads
@@ -1429,13 +1477,13 @@ __global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngLaunch P) {
     if constexpr (!MULTI) {
         // one work: every launch parameter sits at a fixed kernarg offset,
         // so all of them come in the first batch of scalar loads
-        eng_dispatch<NW, FA>(P.act, L, P.w[0]);
+        eng_dispatch<NW, FA, MULTI>(P.act, L, P.w[0]);
     } else {
         const int b = blockIdx.x;
         const int wi = (P.nworks > 2 && b >= P.w[2].first_group) ? 2 : (P.nworks > 1 && b >= P.w[1].first_group) ? 1 : 0;
         const TmqWork w = wi == 2 ? P.w[2] : wi == 1 ? P.w[1] : P.w[0];
-        if (FA != FB && wi == P.nworks - 1) eng_dispatch<NW, FB>(P.act, L, w);
-        else eng_dispatch<NW, FA>(P.act, L, w);
+        if (FA != FB && wi == P.nworks - 1) eng_dispatch<NW, FB, MULTI>(P.act, L, w);
+        else eng_dispatch<NW, FA, MULTI>(P.act, L, w);
     }
 }
 
@@ -1796,7 +1844,7 @@ template <int G>
 __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     extern __shared__ float pf_lds[];
     __shared__ float red[8];
-    __shared__ __attribute__((aligned(16))) float spec[2 * 4 * 64];  // seq_sum_spec<4>
+    __shared__ float spec[4 * 64];  // seq_sum_spec<4>
     __shared__ int spec_c[4];
     const int t = blockIdx.x, n = a.n, tid = threadIdx.x, nt = blockDim.x;
     const int wave = tid >> 6, lane = tid & 63, nc = n / TMQ_PF_CHUNK, ng = n >> 2;
@@ -2060,7 +2108,7 @@ int tmq_launch_zero_acc(int64_t* p, size_t n, hipStream_t s) {
     return (int)hipGetLastError();
 }
 
-size_t tmq_eng_lds_bytes(int n, int waves) { return 8 * (size_t)n + 8 * 64 * (size_t)waves + 256; }
+size_t tmq_eng_lds_bytes(int n, int waves) { return 8 * (size_t)n + 8 * 64 * (size_t)waves + 256 + 4 * (16 * 64 + 16); }
 
 template <int NW, bool MULTI>
 static void* eng_kernel_for(int fa, int fb) {
