@@ -38,6 +38,13 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     const int qpk = a.n_heads / a.n_kv;
     const int kv = h / qpk;
     const int KV = a.n_kv * 64;
+    // the q/k/v terms do not depend on the position: their loads are issued
+    // before the position arrives (valid addresses whatever it is)
+    const int j = tid & 31, jv = tid & 63;
+    const double qxs = (double)*a.q.xs, kxs = (double)*a.k.xs, vxs = (double)*a.v.xs;
+    const TmqFinRaw<Q8> fq0 = fin_load<Q8>(a.q, h * 64 + 2 * j), fq1 = fin_load<Q8>(a.q, h * 64 + 2 * j + 1);
+    const TmqFinRaw<K8> fk0 = fin_load<K8>(a.k, kv * 64 + 2 * j), fk1 = fin_load<K8>(a.k, kv * 64 + 2 * j + 1);
+    const TmqFinRaw<V8> fv = fin_load<V8>(a.v, kv * 64 + jv);
     const int pos = a.state->pos;
     if (a.state->err || pos < 0 || pos >= a.max_pos) return;
     const float* kb = a.kc + kv * 64;
@@ -51,15 +58,9 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
             *(float4*)&vbuf[buf][pr][4 * q4] = *(const float4*)(vb + (size_t)(c0 + pr) * KV + 4 * q4);
         }
     };
-    // loads in the order they are needed (they retire in order): the q/k/v
-    // terms (every thread, indices folded into range: no branch), then the
-    // cached K row of the thread's first position, then the V rows
-    const int j = tid & 31, jv = tid & 63;
+    // then, in the order they are needed (loads retire in order): the RoPE
+    // factors, the cached K row of the thread's first position, the V rows
     const float2 cs = a.rope[(size_t)pos * 32 + j];
-    const double qxs = (double)*a.q.xs, kxs = (double)*a.k.xs, vxs = (double)*a.v.xs;
-    const TmqFinRaw<Q8> fq0 = fin_load<Q8>(a.q, h * 64 + 2 * j), fq1 = fin_load<Q8>(a.q, h * 64 + 2 * j + 1);
-    const TmqFinRaw<K8> fk0 = fin_load<K8>(a.k, kv * 64 + 2 * j), fk1 = fin_load<K8>(a.k, kv * 64 + 2 * j + 1);
-    const TmqFinRaw<V8> fv = fin_load<V8>(a.v, kv * 64 + jv);
     float4 kk[16];
     {
         const float4* kp = (const float4*)(kb + (size_t)min(tid, max(pos - 1, 0)) * KV);
