@@ -1141,9 +1141,10 @@ __device__ __forceinline__ float seq_sum_spec(const float* v, int n, float* scr,
 // the columns [c0, c1) the workgroup reads (all of them for the modes that
 // need the whole vector); returns x_scale.
 //   rms_norm (sim/tmac_gguf.cpp:447-453): o = fl(fl(x*w)*s), s from the
-//   sequential sum of squares (one lane, from LDS).  The max of |o| is taken
-//   as fl(max|fl(x*w)| * s) while that lane sums: rounding is monotone and
-//   s > 0, so it is the same value, without waiting for s.
+//   sequential sum of squares (seq_sum_spec over the squares in LDS).  The
+//   max of |o| is taken as fl(max|fl(x*w)| * s), the wave maxima gathered
+//   before the sum: rounding is monotone and s > 0, so it is the same value,
+//   without waiting for s.
 //   quantisation (:1225-1231): x_scale = max|o| / 32767 (1 below 1e-10),
 //   xq = (int16)roundf(o / x_scale).
 // `pre` issues the caller's weight prefetch.  It runs right after the
