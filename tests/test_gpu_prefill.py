@@ -137,6 +137,56 @@ def test_norm_sum_fallback(ctx, model, monkeypatch):
         m.free()
 
 
+def test_norm_sum_mixed(ctx, monkeypatch):
+    """a prompt token whose embedding row is constant (every Q8_0 block d =
+    0x2e66, q = 13: 1.2997 in all 896 columns): the fp32 chain of its
+    attn_norm sum of squares drifts past the 64-float window at some segment
+    starts and not at others (the 4 segments of that norm, in the QKV
+    prologue and the prefill act kernel: taken, re-run, taken -- checked on
+    the host below), so the walk mixes taken and re-run segments.  The result must equal the
+    all-re-run path (TMQ_SPEC_MISS=1) bit for bit, one token at a time and
+    batched."""
+    import tmq
+    from tmq import model_synth, tmacfile
+    tens = model_synth.gen_model(MODEL_SEED)
+    emb = tens[0]
+    assert emb.name == "token_embd.weight" and emb.cols == 896
+    tok = 1234
+    rb = (emb.cols // 32) * 34
+    row = emb.data[tok * rb:(tok + 1) * rb].reshape(-1, 34)
+    row[:, 0], row[:, 1] = 0x66, 0x2E
+    row[:, 2:] = 13
+    blob = tmacfile.to_bytes(tens)
+    del tens
+    # the premise, on the host: the chain's distance (in floats) from the
+    # rounded fp64 prefix at each segment start is within the window for
+    # some segments and outside it for others
+    v = np.float32(np.float16(np.frombuffer(bytes([0x66, 0x2E]), np.float16)[0])) * np.float32(13)
+    sq = np.full(896, np.float32(v) * np.float32(v), np.float32)
+    chain = np.zeros(897, np.float32)
+    for i in range(896):
+        chain[i + 1] = np.float32(chain[i] + sq[i])
+    pref = np.concatenate([[0.0], np.cumsum(sq.astype(np.float64))]).astype(np.float32)
+    d = [int(chain[j].view(np.int32)) - int(pref[j].view(np.int32)) for j in (256, 512, 768)]
+    inside = [-32 <= x <= 31 for x in d]
+    assert any(inside) and not all(inside), d
+    toks = np.array([tok, 17, 99000, 4242], dtype=np.int32)
+    res = []
+    for miss in ("0", "1"):
+        monkeypatch.setenv("TMQ_SPEC_MISS", miss)
+        print(f"[prefill] constant-embedding model, TMQ_SPEC_MISS={miss}", flush=True)
+        m = tmq.Model(ctx, blob, max_seq=64)
+        try:
+            res.append({c: run(m, toks, c, gen=3) for c in (0, 512)})
+        finally:
+            m.free()
+    for c in (0, 512):
+        (l0, h0, g0), (l1, h1, g1) = res[0][c], res[1][c]
+        assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32)), f"chunk {c}"
+        assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32)), f"chunk {c}"
+        assert g0.tolist() == g1.tolist()
+
+
 @pytest.mark.parametrize("chunk", [0, 512, 8])
 def test_prompt_matches_reference(model, chunk):
     """the compiled reference's own process_prompt over a 24-token prompt
