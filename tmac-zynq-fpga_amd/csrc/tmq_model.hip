@@ -856,7 +856,8 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     // gate+up / down, each split over K (kc workgroups per 64-row group) into
     // int64 accumulators that the next launch finalises; then the logits
     // (one Q8_0 wave per 64 rows, direct).
-    const int kc_qkv = env_int("TMQ_KC_QKV", 7), kc_o = env_int("TMQ_KC_O", 7);
+    // (attn_output over 14 K chunks: 196 workgroups, 0.45 % faster per step than 7)
+    const int kc_qkv = env_int("TMQ_KC_QKV", 7), kc_o = env_int("TMQ_KC_O", 14);
     const int kc_gu = env_int("TMQ_KC_GU", 1), kc_dn = env_int("TMQ_KC_DN", 19);
     auto nw_env = [](const char* n, int d) { return env_int(n, d) == 4 ? 4 : env_int(n, d) == 16 ? 16 : d; };
     const int nw_qkv = nw_env("TMQ_NW_QKV", 4), nw_o = nw_env("TMQ_NW_O", 4);
