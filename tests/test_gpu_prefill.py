@@ -185,6 +185,63 @@ def test_norm_sum_mixed(ctx, monkeypatch):
         assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32)), f"chunk {c}"
         assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32)), f"chunk {c}"
         assert g0.tolist() == g1.tolist()
+    # one token at a time and batched leave the same bits as well
+    (l0, h0, g0), (l1, h1, g1) = res[0][0], res[0][512]
+    assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32))
+    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
+    assert g0.tolist() == g1.tolist()
+
+
+def chain_drift(v, seg, n=896):
+    """distance in floats between the sequential fp32 sum of n squares of
+    v and the fp64 prefix rounded to float, at every segment start"""
+    sq = np.full(n, np.float32(v) * np.float32(v), np.float32)
+    chain = np.zeros(n + 1, np.float32)
+    for i in range(n):
+        chain[i + 1] = np.float32(chain[i] + sq[i])
+    pref = np.concatenate([[0.0], np.cumsum(sq.astype(np.float64))]).astype(np.float32)
+    return [int(chain[j].view(np.int32)) - int(pref[j].view(np.int32)) for j in range(seg, n, seg)]
+
+
+def test_norm_sum_mixed_ffn(ctx, monkeypatch):
+    """the same constant embedding row, and layer 0's attn_output weights
+    all zero (every block d = 0: the projection adds exactly 0), so the
+    ffn_norm input of that token is the constant row too.  The decode
+    engine sums it in the 16-wave gate/up launch as 8 segments of 128; the
+    walk there mixes taken and re-run segments (premise checked on the
+    host), and must leave the bits of the all-re-run path and of the batched
+    prefill."""
+    import tmq
+    from tmq import model_synth, tmacfile
+    tens = model_synth.gen_model(MODEL_SEED)
+    emb = tens[0]
+    tok = 1234
+    rb = (emb.cols // 32) * 34
+    row = emb.data[tok * rb:(tok + 1) * rb].reshape(-1, 34)
+    row[:, 0], row[:, 1] = 0x66, 0x2E
+    row[:, 2:] = 13
+    o0 = [t for t in tens if t.name == "blk.0.attn_output.weight"][0]
+    o0.data[:] = 0
+    blob = tmacfile.to_bytes(tens)
+    del tens
+    v = np.float32(np.float16(np.frombuffer(bytes([0x66, 0x2E]), np.float16)[0])) * np.float32(13)
+    inside = [-32 <= x <= 31 for x in chain_drift(v, 128)]
+    assert any(inside) and not all(inside), inside
+    toks = np.array([tok, 5, 151000], dtype=np.int32)
+    res = []
+    for miss in ("0", "1"):
+        monkeypatch.setenv("TMQ_SPEC_MISS", miss)
+        print(f"[prefill] zero attn_output model, TMQ_SPEC_MISS={miss}", flush=True)
+        m = tmq.Model(ctx, blob, max_seq=64)
+        try:
+            res.append({c: run(m, toks, c, gen=3) for c in (0, 512)})
+        finally:
+            m.free()
+    ref = res[1][0]
+    for r in (res[0][0], res[0][512], res[1][512]):
+        assert np.array_equal(r[1].view(np.uint32), ref[1].view(np.uint32))
+        assert np.array_equal(r[0].view(np.uint32), ref[0].view(np.uint32))
+        assert r[2].tolist() == ref[2].tolist()
 
 
 @pytest.mark.parametrize("chunk", [0, 512, 8])

@@ -852,6 +852,8 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     m->vc = (float*)(B + lay["vc"]);
     auto fv_ptr = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
 
+    // read before the work lists: every launch's recipe copies it
+    m->spec_miss = env_int("TMQ_SPEC_MISS", 0) != 0;
     // Work lists.  Every launch is one engine GEMV: per layer qkv / o /
     // gate+up / down, each split over K (kc workgroups per 64-row group) into
     // int64 accumulators that the next launch finalises; then the logits
@@ -977,7 +979,6 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
     HIP_TRY(hipStreamSynchronize(s));
     m->use_graphs = env_int("TMQ_GRAPHS", 1) != 0;
-    m->spec_miss = env_int("TMQ_SPEC_MISS", 0) != 0;
     m->prefill_chunk = env_int("TMQ_PREFILL", 512);
     m->prefill_off = pf_unsupported(m);
     return 0;
