@@ -115,6 +115,20 @@ int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int 
 int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev,
                  int64_t* acc_dev);
 
+/* tmq_gemv_dev without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as tmq_gemv_dev; the
+ * prepared activation lives in a fixed per-device scratch array of the
+ * library (about 160 KiB, held until the process ends) instead of a buffer
+ * the context allocates on first use.  Tensors wider than
+ * TMQ_NOALLOC_MAX_COLS columns are rejected with TMQ_ERR_ARG.  Every call
+ * on one device shares that array: calls that overlap on one device (two
+ * streams, two contexts) race and must be ordered by the caller. */
+#define TMQ_NOALLOC_MAX_COLS 16384
+int tmq_gemv_dev_noalloc(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev,
+                         int64_t* acc_dev);
+
 /* Host form returning the integer partials (layout as acc_dev above) and
  * x_scale; used by parity tests. */
 int tmq_gemv_partials(tmq_ctx* ctx, const tmq_tensor* t, const float* x, int64_t* acc,

@@ -11,6 +11,7 @@
 #include <cstring>
 #include <algorithm>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -20,6 +21,39 @@
 
 namespace {
 thread_local std::string g_err;
+}  // namespace
+
+// Scratch of tmq_gemv_dev_noalloc: the prepared activation of one GEMV
+// (tmq_act_bytes(cols) bytes, cols <= TMQ_NOALLOC_MAX_COLS), in a
+// file-scope device array that lives until the process ends.  Host code
+// never uses the array's name as an address: tmq_open looks up each
+// device's copy once (hipGetSymbolAddress, with that device current) and
+// the entry point passes that pointer to the kernels.  Every call on one
+// device shares its copy; calls that overlap on one device race on it.
+#define TMQ_NOALLOC_SCRATCH_BYTES ((16 + 10 * (size_t)TMQ_NOALLOC_MAX_COLS + 16 + 255) & ~(size_t)255)
+static __device__ __align__(256) uint8_t scratch[TMQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// the device's copy of `scratch` (the device is current); once per device
+int scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) return tmq_fail(TMQ_ERR_ARG, "device %d >= %d", device, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return 0;
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return tmq_fail(TMQ_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+    return 0;
+}
+void* scratch_of(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return device >= 0 && device < kMaxDevices ? g_scratch_ptr[device] : nullptr;
+}
 }  // namespace
 
 int tmq_fail(int code, const char* fmt, ...) {
@@ -348,6 +382,12 @@ int tmq_open(int device, tmq_ctx** out) {
         delete c;
         return tmq_fail(TMQ_ERR_HIP, "stream create: %s", hipGetErrorString(e));
     }
+    int rc = scratch_init(device);
+    if (rc) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return rc;
+    }
     *out = c;
     return 0;
 }
@@ -441,6 +481,26 @@ int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y
     jobs.j[0].n = t->dev.cols;
     LAUNCH_TRY(tmq_launch_act_prep(jobs, ctx->stream));
     TmqWork w = make_work(t, (const uint8_t*)ctx->act.p, y_dev, acc_dev);
+    LAUNCH_TRY(tmq_launch_gemv(w, ctx->stream));
+    return 0;
+}
+
+int tmq_gemv_dev_noalloc(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev, int64_t* acc_dev) {
+    if (!ctx || !t || !x_dev) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (t->dev.cols > TMQ_NOALLOC_MAX_COLS)
+        return tmq_fail(TMQ_ERR_ARG, "tmq_gemv_dev_noalloc: cols %d above its scratch limit of %d columns",
+                        t->dev.cols, TMQ_NOALLOC_MAX_COLS);
+    int rc = tmq_rt_set_device(ctx);
+    if (rc) return rc;
+    uint8_t* act = (uint8_t*)scratch_of(ctx->device);
+    if (!act) return tmq_fail(TMQ_ERR_HIP, "tmq_gemv_dev_noalloc: no scratch for device %d", ctx->device);
+    TmqActJobs jobs{};
+    jobs.count = 1;
+    jobs.j[0].x = x_dev;
+    jobs.j[0].act = act;
+    jobs.j[0].n = t->dev.cols;
+    LAUNCH_TRY(tmq_launch_act_prep(jobs, ctx->stream));
+    TmqWork w = make_work(t, act, y_dev, acc_dev);
     LAUNCH_TRY(tmq_launch_gemv(w, ctx->stream));
     return 0;
 }

@@ -24,11 +24,13 @@ LIB_PATH = os.path.join(HERE, "libtmq.so")
 Q5_0, Q8_0, Q4_K, Q6_K, CPU_OP = 6, 8, 12, 14, 15
 QK = {Q8_0: 32, Q5_0: 32, Q4_K: 256, Q6_K: 256}
 BLOCK_BYTES = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210}
+NOALLOC_MAX_COLS = 16384  # TMQ_NOALLOC_MAX_COLS
 
 EXPORTS = [
     "tmq_last_error", "tmq_version", "tmq_open", "tmq_close", "tmq_stream", "tmq_sync",
     "tmq_tensor_upload", "tmq_tensor_upload_dev", "tmq_tensor_free", "tmq_tensor_info",
-    "tmq_tensor_row_norm", "tmq_tensor_fit_stats", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_partials",
+    "tmq_tensor_row_norm", "tmq_tensor_fit_stats", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_dev_noalloc",
+    "tmq_gemv_partials",
     "tmq_vecmul_tile_q8", "tmq_vecmul_tile_q5_0_8x896", "tmq_vecmul_tile_q6_k",
     "tmq_vecmul_tile_q4k", "tmq_phaseb_run", "tmq_chain_create", "tmq_chain_run",
     "tmq_chain_prepare", "tmq_chain_launch",
@@ -94,6 +96,7 @@ def lib(path: str = LIB_PATH):
         "tmq_tensor_fit_stats": (I, [P, P, C.POINTER(U64), C.POINTER(U64)]),
         "tmq_matmul": (I, [P, P, P, P, I, I]),
         "tmq_gemv_dev": (I, [P, P, P, P, P]),
+        "tmq_gemv_dev_noalloc": (I, [P, P, P, P, P]),
         "tmq_gemv_partials": (I, [P, P, P, P, U64, P]),
         "tmq_vecmul_tile_q8": (I, [P, P, P, P, P]),
         "tmq_vecmul_tile_q5_0_8x896": (I, [P, P, P, P, P, I]),
@@ -264,6 +267,10 @@ class Context:
 
     def gemv_dev(self, t: Tensor, x_ptr: int, y_ptr: int | None, acc_ptr: int | None = None):
         _check(lib().tmq_gemv_dev(self.handle, t.handle, x_ptr, y_ptr, acc_ptr))
+
+    def gemv_dev_noalloc(self, t: Tensor, x_ptr: int, y_ptr: int | None, acc_ptr: int | None = None):
+        """tmq_gemv_dev from the library's fixed scratch (no device allocation)"""
+        _check(lib().tmq_gemv_dev_noalloc(self.handle, t.handle, x_ptr, y_ptr, acc_ptr))
 
     # -- tiles -----------------------------------------------------------
     def tile_q8(self, W, cs, vec) -> np.ndarray:
