@@ -36,7 +36,11 @@ extern "C" {
 #define TMQ_ERR_NODEV (-6)     /* no usable gfx950 device                     */
 
 /* ggml tensor types, same codes as sim/tmac_gguf.cpp:154-159 and the PhaseB
- * DESC_TYPE_* constants of sim/fpga_sim.hpp:1272-1279 */
+ * DESC_TYPE_* constants of sim/fpga_sim.hpp:1272-1279.  F32 and F16 tensors
+ * have no matmul_fpga_* of their own: the reference's `matmul` sends them to
+ * matmul_fpga_int16 or the FP32 loop (TMQ_PATH_INT16 / TMQ_PATH_FP32). */
+#define TMQ_TYPE_F32 0
+#define TMQ_TYPE_F16 1
 #define TMQ_TYPE_Q5_0 6
 #define TMQ_TYPE_Q8_0 8
 #define TMQ_TYPE_Q4_K 12
@@ -75,7 +79,9 @@ int tmq_sync(tmq_ctx* ctx);
  * (sim/matmul_q8.cpp:24-30); NULL computes it from the weights (the two are
  * identical, scripts/extract_tmac.py:231-259).  Requires cols % QK == 0
  * (QK = 32 for Q8_0/Q5_0, 256 for K-quants) and, for Q8_0, cols <= 16384.
- * Returns TMQ_ERR_NONFINITE if any fp16 scale is Inf/NaN. */
+ * Returns TMQ_ERR_NONFINITE if any fp16 scale is Inf/NaN.  F32 / F16
+ * tensors (row-major elements, cols % 32 == 0, every element finite) are
+ * accepted for the INT16 and FP32 paths. */
 int tmq_tensor_upload(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols,
                       const void* data, uint64_t n_bytes, const float* row_max_abs,
                       tmq_tensor** out);
@@ -107,6 +113,48 @@ int tmq_tensor_fit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* fitted, ui
  * matmul_fpga_q6_k (:1367).  Host x[cols] in, host y[rows] overwritten,
  * synchronous.  rows/cols must equal the tensor's. */
 int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int rows, int cols);
+
+/* ---- the three branches of `matmul` (sim/tmac_gguf.cpp:473-493) --------
+ * TMQ_PATH_FPGA   the tensor type's own matmul_fpga_* (tmq_matmul above)
+ * TMQ_PATH_INT16  matmul_fpga_int16 (:887-940): exact element values
+ *                 (read_tensor, :398-411), per row row_scale = max|E|/32767,
+ *                 w = (int16)roundf(E/row_scale), 64x64 int16 tiles whose
+ *                 int64 results fold as y += (double)P*x_scale*row_scale in
+ *                 column-tile order.  The rounded weights depend on the
+ *                 weights only and are built once per tensor
+ *                 (tmq_tensor_prepare_int16, 2 bytes per weight).
+ * TMQ_PATH_FP32   the loop without any --fpga flag (:488-492):
+ *                 y_r = sum_j read_tensor(r,j)*x[j] in fp32, j ascending.
+ * Flags mirror the reference globals set by its command line (:2085-2091):
+ * TMQ_FLAG_FPGA = g_use_fpga (--fpga, --fpga-int16, or any --fpga-<type>),
+ * TMQ_FLAG_<type> = g_fpga_<type>. */
+#define TMQ_PATH_FPGA 0
+#define TMQ_PATH_INT16 1
+#define TMQ_PATH_FP32 2
+#define TMQ_FLAG_FPGA 1u
+#define TMQ_FLAG_Q8_0 2u
+#define TMQ_FLAG_Q5_0 4u
+#define TMQ_FLAG_Q4_K 8u
+#define TMQ_FLAG_Q6_K 16u
+#define TMQ_FLAGS_ALL (TMQ_FLAG_FPGA | TMQ_FLAG_Q8_0 | TMQ_FLAG_Q5_0 | TMQ_FLAG_Q4_K | TMQ_FLAG_Q6_K)
+/* The branch `matmul` takes for a tensor type under flags (:474-492):
+ * TMQ_PATH_* or a negative status for an unknown type. */
+int tmq_route(uint32_t type, uint32_t flags);
+/* `matmul` itself: routes by type and flags, host x/y, synchronous. */
+int tmq_matmul_flags(tmq_ctx* ctx, const tmq_tensor* t, uint32_t flags, const float* x, float* y,
+                     int rows, int cols);
+/* one branch, chosen by the caller (host x/y, synchronous) */
+int tmq_matmul_path(tmq_ctx* ctx, const tmq_tensor* t, int path, const float* x, float* y, int rows,
+                    int cols);
+/* device-pointer form; acc_dev (INT16: int64 [rows][ceil(cols/64)] tile
+ * results, FP32: must be NULL) may be NULL */
+int tmq_gemv_dev_path(tmq_ctx* ctx, const tmq_tensor* t, int path, const float* x_dev, float* y_dev,
+                      int64_t* acc_dev);
+/* host form returning the integer partials of TMQ_PATH_FPGA / _INT16 */
+int tmq_gemv_partials_path(tmq_ctx* ctx, const tmq_tensor* t, int path, const float* x, int64_t* acc,
+                           uint64_t acc_len, float* x_scale);
+/* builds the INT16 path's rounded weights now (otherwise on first use) */
+int tmq_tensor_prepare_int16(tmq_ctx* ctx, tmq_tensor* t);
 
 /* Device-pointer, stream-ordered form of tmq_matmul: x_dev fp32[cols],
  * y_dev fp32[rows] (may be NULL), acc_dev optional int64 partials: per row

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libtmacref.so")
 
-Q8_0, Q5_0, Q4_K, Q6_K = 8, 6, 12, 14
+F32, F16, Q8_0, Q5_0, Q4_K, Q6_K = 0, 1, 8, 6, 12, 14
 
 _P = C.c_void_p
 _i = C.c_int
@@ -61,6 +61,9 @@ class Oracle:
         _setup(L, "tmqo_tile_q4_k", None, [_P, _i, _P, _i, _P, _P, _i])
         _setup(L, "tmqo_tile_q5_0_4x896", None, [_P, _P, _P, _P, _i])
         _setup(L, "tmqo_phaseb_run", _i, [_P, _u32, _u32, _P])
+        _setup(L, "tmqo_read_tensor", C.c_float, [_u32, _P, _i, _i, _i])
+        _setup(L, "tmqo_matmul_int16", None, [_u32, _P, _P, _P, _i, _i, _P, _P])
+        _setup(L, "tmqo_matmul_fp32", None, [_u32, _P, _P, _P, _i, _i])
 
     # -- activation / row stats -------------------------------------------
     def quantize_act(self, x: np.ndarray):
@@ -107,6 +110,26 @@ class Oracle:
             getattr(self.lib, f"tmqo_matmul_{name}")(_ptr(w), _ptr(x), _ptr(y), rows, cols)
         return y
 
+    def read_tensor(self, qtype, w, cols, r, j) -> np.float32:
+        return np.float32(self.lib.tmqo_read_tensor(qtype, _ptr(w), cols, r, j))
+
+    def matmul_int16(self, qtype, w, x, rows, cols):
+        """matmul_fpga_int16: (y, int64 tiles [rows][ceil(cols/64)], row_scale)"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w).view(np.uint8)
+        y = np.empty(rows, dtype=np.float32)
+        tiles = np.empty((rows, (cols + 63) // 64), dtype=np.int64)
+        rs = np.empty(rows, dtype=np.float32)
+        self.lib.tmqo_matmul_int16(qtype, _ptr(w), _ptr(x), _ptr(y), rows, cols, _ptr(tiles), _ptr(rs))
+        return y, tiles, rs
+
+    def matmul_fp32(self, qtype, w, x, rows, cols) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w).view(np.uint8)
+        y = np.empty(rows, dtype=np.float32)
+        self.lib.tmqo_matmul_fp32(qtype, _ptr(w), _ptr(x), _ptr(y), rows, cols)
+        return y
+
     # -- tiles ----------------------------------------------------------------
     def tile_q8(self, W, cs, vec):
         r = np.zeros(64, dtype=np.int64)
@@ -141,6 +164,9 @@ class Reference:
         _setup(L, "ref_f16_to_f32", C.c_float, [C.c_uint16])
         _setup(L, "ref_matmul", _i, [_u32, _P, _u64, _i, _i, _P, _P, _P])
         _setup(L, "ref_matmul_fp32", None, [_u32, _P, _u64, _i, _i, _P, _P])
+        _setup(L, "ref_matmul_int16", None, [_u32, _P, _u64, _i, _i, _P, _P])
+        _setup(L, "ref_model_set_flags", None, [C.c_uint])
+        _setup(L, "ref_model_logits_auto", None, [_P, _P])
         _setup(L, "ref_tile_q8", None, [_P, _P, _P, _P])
         _setup(L, "ref_tile_q5_0_8x896", None, [_P, _P, _P, _P, _i])
         _setup(L, "ref_tile_q6_k", None, [_P, _i, _P, _i, _P, _P, _i])
@@ -206,6 +232,22 @@ class Reference:
         y = np.empty(rows, dtype=np.float32)
         self.lib.ref_matmul_fp32(qtype, _ptr(w), w.size, rows, cols, _ptr(x), _ptr(y))
         return y
+
+    def matmul_int16(self, qtype, w, x, rows, cols) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w).view(np.uint8)
+        y = np.empty(rows, dtype=np.float32)
+        self.lib.ref_matmul_int16(qtype, _ptr(w), w.size, rows, cols, _ptr(x), _ptr(y))
+        return y
+
+    def model_set_flags(self, flags: int):
+        self.lib.ref_model_set_flags(int(flags))
+
+    def model_logits_auto(self, hidden) -> np.ndarray:
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        out = np.empty(self.VOCAB, dtype=np.float32)
+        self.lib.ref_model_logits_auto(_ptr(h), _ptr(out))
+        return out
 
     def tile_q8(self, W, cs, vec):
         r = np.zeros(64, dtype=np.int64)

@@ -58,6 +58,13 @@ void ref_matmul_fp32(uint32_t type, const uint8_t* data, uint64_t n_bytes, int r
     g_use_fpga = saved;
 }
 
+// matmul_fpga_int16 (sim/tmac_gguf.cpp:887-940), any tensor type
+void ref_matmul_int16(uint32_t type, const uint8_t* data, uint64_t n_bytes, int rows, int cols,
+                      const float* x, float* y) {
+    Tensor t = ref_make_tensor(type, (uint64_t)rows, (uint64_t)cols, data, n_bytes);
+    matmul_fpga_int16(&t, x, y, rows, cols);
+}
+
 // fpga_sim tile primitives
 void ref_tile_q8(const uint8_t* q8_W, const uint16_t* cs, const int16_t* vec, int64_t* result) {
     fpga_sim::axi_vecmul_tile_q8(q8_W, cs, vec, result);
@@ -117,6 +124,20 @@ int ref_model_load(const char* path) {
     if (load_tmac(path) != 0) return -1;
     g_use_fpga = g_fpga_q8 = g_fpga_q4k = g_fpga_q5_0 = g_fpga_q6_k = true;
     return 0;
+}
+// the command line's flag globals (sim/tmac_gguf.cpp:2085-2091): bit 0
+// g_use_fpga, 1 g_fpga_q8, 2 g_fpga_q5_0, 3 g_fpga_q4k, 4 g_fpga_q6_k
+void ref_model_set_flags(unsigned flags) {
+    g_use_fpga = (flags & 1u) != 0;
+    g_fpga_q8 = (flags & 2u) != 0;
+    g_fpga_q5_0 = (flags & 4u) != 0;
+    g_fpga_q4k = (flags & 8u) != 0;
+    g_fpga_q6_k = (flags & 16u) != 0;
+}
+// the logits as generate() / main() choose them (:2033-2037, :2151-2155)
+void ref_model_logits_auto(const float* hidden, float* logits) {
+    if (g_fpga_q8) get_logits_q8(logits, hidden);
+    else get_logits(logits, hidden);
 }
 int ref_model_prompt(const int* tokens, int n, float* hidden) {
     std::vector<int> v(tokens, tokens + n);

@@ -357,6 +357,89 @@ void tmqo_matmul_q8_0(const uint8_t* w, const float* x, float* y, int rows, int 
     free(xq); free(mx); free(rs); free(P);
 }
 
+/* ------------------------------------ the other branches of `matmul` */
+
+/* read_tensor (sim/tmac_gguf.cpp:398-411): element (r, j) of a row-major
+ * tensor as the reference's decoders give it -- F32 as stored, F16 half to
+ * float (:216-228), Q8_0 val*scale (:238-248), Q5_0 d*q (:305-323), Q6_K
+ * d*scale*q (:325-361), Q4_K d*sc*q4 - dmin*m (:363-393). */
+float tmqo_read_tensor(uint32_t type, const uint8_t* w, int cols, int r, int j) {
+    uint64_t idx = (uint64_t)j + (uint64_t)r * (uint64_t)cols;
+    if (type == TMQO_F32) {
+        float v;
+        memcpy(&v, w + idx * 4, 4);
+        return v;
+    }
+    if (type == TMQO_F16) return tmqo_f16_to_f32(rd16(w + idx * 2));
+    if (type == TMQO_Q8_0) {
+        const uint8_t* blk = w + (idx / 32) * 34;
+        float d = tmqo_f16_to_f32(rd16(blk));
+        return (float)(int8_t)blk[2 + idx % 32] * d;
+    }
+    if (type == TMQO_Q5_0) {
+        const uint8_t* blk = w + (idx / 32) * 22;
+        float d = tmqo_f16_to_f32(rd16(blk));
+        return d * (float)q5_0_q(blk, (int)(idx % 32));
+    }
+    if (type == TMQO_Q6_K) return q6k_E(w + (idx / 256) * 210, (int)(idx % 256));
+    if (type == TMQO_Q4_K) return q4k_E(w + (idx / 256) * 144, (int)(idx % 256));
+    return 0.0f;
+}
+
+/* matmul_fpga_int16 (sim/tmac_gguf.cpp:887-940): activation quantised as in
+ * every path (:893-899); per group of 64 rows the exact values, per row
+ * row_scale = max|E|/32767 (1 below 1e-10, :908-913), and per 64-column tile
+ * W_q = (int16)roundf(E / row_scale) (:915-921) times the int16 activation
+ * summed in int64 (axi_vecmul_tile_int16 -> vecmul_1x64_int16,
+ * sim/fpga_sim.hpp:437-446, :45-54), folded y += (double)P*x_scale*row_scale
+ * tile by tile (:930-931).  Optional outputs: the int64 tile results P
+ * [rows][ceil(cols/64)] and the row scales. */
+void tmqo_matmul_int16(uint32_t type, const uint8_t* w, const float* x, float* y, int rows, int cols,
+                       int64_t* tiles, float* row_scale_out) {
+    const int N = 64, nt = (cols + N - 1) / N;
+    int16_t* xq = (int16_t*)malloc(sizeof(int16_t) * (size_t)cols);
+    float* W = (float*)malloc(sizeof(float) * (size_t)N * cols);
+    float xs = tmqo_quantize_act(x, cols, xq);
+    for (int r = 0; r < rows; r++) y[r] = 0.0f;
+    for (int r0 = 0; r0 < rows; r0 += N) {
+        int rn = rows - r0 < N ? rows - r0 : N;
+        float rs[64];
+        for (int i = 0; i < rn; i++)
+            for (int j = 0; j < cols; j++) W[(size_t)i * cols + j] = tmqo_read_tensor(type, w, cols, r0 + i, j);
+        for (int i = 0; i < rn; i++) {
+            float m = 0.0f;
+            for (int j = 0; j < cols; j++) m = fmaxf(m, fabsf(W[(size_t)i * cols + j]));
+            rs[i] = (m < 1e-10f) ? 1.0f : m / 32767.0f;
+            if (row_scale_out) row_scale_out[r0 + i] = rs[i];
+        }
+        for (int t = 0; t < nt; t++) {
+            int c = t * N, cn = cols - c < N ? cols - c : N;
+            for (int i = 0; i < rn; i++) {
+                int64_t P = 0;
+                for (int k = 0; k < cn; k++) {
+                    int16_t wq = (int16_t)roundf(W[(size_t)i * cols + c + k] / rs[i]);
+                    P += (int64_t)xq[c + k] * (int64_t)wq;
+                }
+                if (tiles) tiles[(size_t)(r0 + i) * nt + t] = P;
+                y[r0 + i] += (double)P * xs * rs[i];
+            }
+        }
+    }
+    free(xq);
+    free(W);
+}
+
+/* The FP32 loop of `matmul` without any --fpga flag (sim/tmac_gguf.cpp:
+ * 488-492): y_r = 0 + E(r,0)*x_0 + E(r,1)*x_1 + ..., each product and sum
+ * rounded to float, columns ascending. */
+void tmqo_matmul_fp32(uint32_t type, const uint8_t* w, const float* x, float* y, int rows, int cols) {
+    for (int r = 0; r < rows; r++) {
+        float sum = 0.0f;
+        for (int j = 0; j < cols; j++) sum += tmqo_read_tensor(type, w, cols, r, j) * x[j];
+        y[r] = sum;
+    }
+}
+
 /* ------------------------------------------------------ tile primitives */
 
 void tmqo_tile_q8(const uint8_t* q8_W, const uint16_t* cs, const int16_t* vec, int64_t* result) {

@@ -19,6 +19,7 @@ extern "C" {
 
 /* ggml tensor type codes, sim/tmac_gguf.cpp:154-159 */
 #define TMQO_F32 0
+#define TMQO_F16 1
 #define TMQO_Q5_0 6
 #define TMQO_Q8_0 8
 #define TMQO_Q4_K 12
@@ -75,7 +76,18 @@ void tmqo_matmul_q5_0(const uint8_t* w, const float* x, float* y, int rows, int 
 void tmqo_matmul_q4_k(const uint8_t* w, const float* x, float* y, int rows, int cols);
 void tmqo_matmul_q6_k(const uint8_t* w, const float* x, float* y, int rows, int cols);
 
-/* fpga_sim tile primitives.
+/* read_tensor (sim/tmac_gguf.cpp:398-411): exact element (r, j), F32/F16/
+ * Q8_0/Q5_0/Q4_K/Q6_K. */
+float tmqo_read_tensor(uint32_t type, const uint8_t* w, int cols, int r, int j);
+/* matmul_fpga_int16 (sim/tmac_gguf.cpp:887-940), the branch of `matmul`
+ * for a type whose --fpga-* flag is off.  tiles (int64 [rows][ceil(cols/64)])
+ * and row_scale ([rows]) may be NULL. */
+void tmqo_matmul_int16(uint32_t type, const uint8_t* w, const float* x, float* y, int rows, int cols,
+                       int64_t* tiles, float* row_scale);
+/* the FP32 loop of `matmul` without any --fpga flag (sim/tmac_gguf.cpp:488-492) */
+void tmqo_matmul_fp32(uint32_t type, const uint8_t* w, const float* x, float* y, int rows, int cols);
+
+/* fpga_sim tile primitives./* fpga_sim tile primitives.
  * axi_vecmul_tile_q8              sim/fpga_sim.hpp:466-491 (+ :316-349, :45-54)
  * axi_vecmul_tile_q5_0_8x896      sim/fpga_sim.hpp:1004-1052  (accumulates)
  * axi_vecmul_tile_q6_k_axilite    sim/fpga_sim.hpp:1058-1115  (accumulates)

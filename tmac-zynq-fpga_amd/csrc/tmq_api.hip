@@ -70,7 +70,7 @@ namespace {
 
 int qk_of(uint32_t type) {
     switch (type) {
-    case TMQ_TYPE_Q8_0: case TMQ_TYPE_Q5_0: return 32;
+    case TMQ_TYPE_Q8_0: case TMQ_TYPE_Q5_0: case TMQ_TYPE_F32: case TMQ_TYPE_F16: return 32;
     case TMQ_TYPE_Q4_K: case TMQ_TYPE_Q6_K: return 256;
     default: return 0;
     }
@@ -81,7 +81,21 @@ int block_bytes(uint32_t type) {
     case TMQ_TYPE_Q5_0: return 22;
     case TMQ_TYPE_Q4_K: return 144;
     case TMQ_TYPE_Q6_K: return 210;
+    case TMQ_TYPE_F32: return 128;  // 32 elements
+    case TMQ_TYPE_F16: return 64;
     default: return 0;
+    }
+}
+bool is_float_type(uint32_t type) { return type == TMQ_TYPE_F32 || type == TMQ_TYPE_F16; }
+const char* type_name(uint32_t type) {
+    switch (type) {
+    case TMQ_TYPE_F32: return "F32";
+    case TMQ_TYPE_F16: return "F16";
+    case TMQ_TYPE_Q5_0: return "Q5_0";
+    case TMQ_TYPE_Q8_0: return "Q8_0";
+    case TMQ_TYPE_Q4_K: return "Q4_K";
+    case TMQ_TYPE_Q6_K: return "Q6_K";
+    default: return "?";
     }
 }
 
@@ -142,6 +156,8 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; se = nb * R; break;
     case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; se = nb * R * 8; break;
     case TMQ_TYPE_Q6_K: sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; se = nb * R * 16; break;
+    case TMQ_TYPE_F32: sa = nb * 8 * R * 16; break;
+    case TMQ_TYPE_F16: sa = nb * 4 * R * 16; break;
     }
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
     const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(se) + al(R * 4) * 2;
@@ -212,6 +228,27 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
                                       hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "row_inv copy: %s", hipGetErrorString(e)));
+        cleanup(0);
+        *out = t;
+        return 0;
+    }
+    if (is_float_type(type)) {
+        // no normaliser of their own (they only take the INT16 / FP32
+        // paths); every element must be finite
+        int rcm = ctx->misc.ensure(256);
+        if (rcm) return cleanup(rcm);
+        int* bad = (int*)ctx->misc.p;
+        int badh = 0;
+        hipError_t e = hipMemsetAsync(bad, 0, sizeof(int), ctx->stream);
+        if (e == hipSuccess) {
+            le = tmq_launch_check_finite(t->dev, bad, ctx->stream);
+            if (le) e = (hipError_t)le;
+        }
+        if (e == hipSuccess) e = hipMemcpyAsync(&badh, bad, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "finite check: %s", hipGetErrorString(e)));
+        if (badh) return cleanup(tmq_fail(TMQ_ERR_NONFINITE, "non-finite element in %llux%llu %s tensor",
+                                          (unsigned long long)rows, (unsigned long long)cols, type_name(type)));
         cleanup(0);
         *out = t;
         return 0;
@@ -347,6 +384,27 @@ inline uint32_t rd32(const uint8_t* p) {
 
 int tmq_rt_groups_of(const TmqTensorDev& t) { return groups_of(t); }
 
+int tmq_rt_prepare_int16(tmq_ctx* ctx, tmq_tensor* t) {
+    if (t->i16_alloc) return 0;
+    const size_t R = t->dev.rows_pad;
+    const size_t wb = ((size_t)t->dev.cols / 8) * R * 16, total = ((wb + 255) & ~(size_t)255) + R * 4;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, total);
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_NOMEM, "hipMalloc(%zu) for INT16 planes: %s", total, hipGetErrorString(e));
+    TmqTensorDev d = t->dev;
+    d.pw = (const uint8_t*)p;
+    d.rs16 = (const float*)((uint8_t*)p + ((wb + 255) & ~(size_t)255));
+    int le = tmq_launch_i16_prep(d, ctx->stream);
+    if (le == 0) le = (int)hipStreamSynchronize(ctx->stream);
+    if (le) {
+        (void)hipFree(p);
+        return tmq_fail(TMQ_ERR_HIP, "INT16 weight preparation: %s", hipGetErrorString((hipError_t)le));
+    }
+    t->i16_alloc = p;
+    t->dev = d;
+    return 0;
+}
+
 int tmq_rt_tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
                          bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
                          tmq_tensor** out) {
@@ -423,10 +481,11 @@ int tmq_tensor_upload_dev(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t c
 
 int tmq_tensor_free(tmq_tensor* t) {
     if (!t) return 0;
-    if (t->alloc) {
+    if (t->alloc || t->i16_alloc) {
         (void)hipSetDevice(t->ctx->device);
         (void)hipStreamSynchronize(t->ctx->stream);
-        (void)hipFree(t->alloc);
+        if (t->alloc) (void)hipFree(t->alloc);
+        if (t->i16_alloc) (void)hipFree(t->i16_alloc);
     }
     delete t;
     return 0;
@@ -471,6 +530,9 @@ int tmq_tensor_fit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* fitted, ui
 
 int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev, int64_t* acc_dev) {
     if (!ctx || !t || !x_dev) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (is_float_type((uint32_t)t->dev.type))
+        return tmq_fail(TMQ_ERR_ARG, "%s tensor: no matmul_fpga_* of its own (the reference sends it to "
+                        "matmul_fpga_int16 or the FP32 loop: tmq_gemv_dev_path)", type_name((uint32_t)t->dev.type));
     int rc = tmq_rt_set_device(ctx);
     if (!rc) rc = ctx->act.ensure(tmq_act_bytes(t->dev.cols));
     if (rc) return rc;
@@ -487,6 +549,8 @@ int tmq_gemv_dev(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y
 
 int tmq_gemv_dev_noalloc(tmq_ctx* ctx, const tmq_tensor* t, const float* x_dev, float* y_dev, int64_t* acc_dev) {
     if (!ctx || !t || !x_dev) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (is_float_type((uint32_t)t->dev.type))
+        return tmq_fail(TMQ_ERR_ARG, "%s tensor: no matmul_fpga_* of its own", type_name((uint32_t)t->dev.type));
     if (t->dev.cols > TMQ_NOALLOC_MAX_COLS)
         return tmq_fail(TMQ_ERR_ARG, "tmq_gemv_dev_noalloc: cols %d above its scratch limit of %d columns",
                         t->dev.cols, TMQ_NOALLOC_MAX_COLS);
@@ -517,6 +581,98 @@ int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int 
     rc = tmq_gemv_dev(ctx, t, (const float*)ctx->x.p, (float*)ctx->y.p, nullptr);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(y, ctx->y.p, sizeof(float) * rows, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_route(uint32_t type, uint32_t flags) {
+    if (!qk_of(type)) return tmq_fail(TMQ_ERR_ARG, "unsupported tensor type %u", type);
+    if (!(flags & TMQ_FLAG_FPGA)) return TMQ_PATH_FP32;
+    const bool own = (type == TMQ_TYPE_Q5_0 && (flags & TMQ_FLAG_Q5_0)) ||
+                     (type == TMQ_TYPE_Q6_K && (flags & TMQ_FLAG_Q6_K)) ||
+                     (type == TMQ_TYPE_Q4_K && (flags & TMQ_FLAG_Q4_K)) ||
+                     (type == TMQ_TYPE_Q8_0 && (flags & TMQ_FLAG_Q8_0));
+    return own ? TMQ_PATH_FPGA : TMQ_PATH_INT16;
+}
+
+int tmq_tensor_prepare_int16(tmq_ctx* ctx, tmq_tensor* t) {
+    if (!ctx || !t) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    int rc = tmq_rt_set_device(ctx);
+    return rc ? rc : tmq_rt_prepare_int16(ctx, t);
+}
+
+int tmq_gemv_dev_path(tmq_ctx* ctx, const tmq_tensor* t, int path, const float* x_dev, float* y_dev,
+                      int64_t* acc_dev) {
+    if (path == TMQ_PATH_FPGA) return tmq_gemv_dev(ctx, t, x_dev, y_dev, acc_dev);
+    if (!ctx || !t || !x_dev) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (path != TMQ_PATH_INT16 && path != TMQ_PATH_FP32) return tmq_fail(TMQ_ERR_ARG, "unknown matmul path %d", path);
+    int rc = tmq_rt_set_device(ctx);
+    if (rc) return rc;
+    TmqWork w = make_work(t, nullptr, y_dev, nullptr);
+    if (path == TMQ_PATH_FP32) {
+        if (acc_dev) return tmq_fail(TMQ_ERR_ARG, "the FP32 path has no integer partials (acc_dev must be NULL)");
+        w.path = TMQ_WPATH_FP32;
+        w.xf = x_dev;
+        LAUNCH_TRY(tmq_launch_gemv(w, ctx->stream));
+        return 0;
+    }
+    // INT16: weights quantised once per tensor, activation as every path does
+    rc = tmq_rt_prepare_int16(ctx, const_cast<tmq_tensor*>(t));
+    if (!rc) rc = ctx->act.ensure(tmq_act_bytes(t->dev.cols));
+    if (rc) return rc;
+    TmqActJobs jobs{};
+    jobs.count = 1;
+    jobs.j[0].x = x_dev;
+    jobs.j[0].act = (uint8_t*)ctx->act.p;
+    jobs.j[0].n = t->dev.cols;
+    LAUNCH_TRY(tmq_launch_act_prep(jobs, ctx->stream));
+    w = make_work(t, (const uint8_t*)ctx->act.p, y_dev, acc_dev);
+    w.path = TMQ_WPATH_INT16;
+    LAUNCH_TRY(tmq_launch_gemv(w, ctx->stream));
+    return 0;
+}
+
+int tmq_matmul_path(tmq_ctx* ctx, const tmq_tensor* t, int path, const float* x, float* y, int rows, int cols) {
+    if (!ctx || !t || !x || !y) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (rows != t->dev.rows || cols != t->dev.cols)
+        return tmq_fail(TMQ_ERR_ARG, "shape %dx%d does not match tensor %dx%d", rows, cols, t->dev.rows, t->dev.cols);
+    int rc = tmq_rt_set_device(ctx);
+    if (!rc) rc = ctx->x.ensure(sizeof(float) * cols);
+    if (!rc) rc = ctx->y.ensure(sizeof(float) * rows);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->x.p, x, sizeof(float) * cols, hipMemcpyHostToDevice, ctx->stream));
+    rc = tmq_gemv_dev_path(ctx, t, path, (const float*)ctx->x.p, (float*)ctx->y.p, nullptr);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(y, ctx->y.p, sizeof(float) * rows, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_matmul_flags(tmq_ctx* ctx, const tmq_tensor* t, uint32_t flags, const float* x, float* y, int rows,
+                     int cols) {
+    if (!t) return tmq_fail(TMQ_ERR_ARG, "null tensor");
+    const int path = tmq_route((uint32_t)t->dev.type, flags);
+    if (path < 0) return path;
+    return tmq_matmul_path(ctx, t, path, x, y, rows, cols);
+}
+
+int tmq_gemv_partials_path(tmq_ctx* ctx, const tmq_tensor* t, int path, const float* x, int64_t* acc,
+                           uint64_t acc_len, float* x_scale) {
+    if (path == TMQ_PATH_FPGA) return tmq_gemv_partials(ctx, t, x, acc, acc_len, x_scale);
+    if (path != TMQ_PATH_INT16) return tmq_fail(TMQ_ERR_ARG, "path %d has no integer partials", path);
+    if (!ctx || !t || !x || !acc) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    const uint64_t need = (uint64_t)t->dev.rows * ((t->dev.cols + 63) / 64);
+    if (acc_len < need) return tmq_fail(TMQ_ERR_ARG, "acc_len %llu < %llu", (unsigned long long)acc_len,
+                                        (unsigned long long)need);
+    int rc = tmq_rt_set_device(ctx);
+    if (!rc) rc = ctx->x.ensure(sizeof(float) * t->dev.cols);
+    if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * need);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->x.p, x, sizeof(float) * t->dev.cols, hipMemcpyHostToDevice, ctx->stream));
+    rc = tmq_gemv_dev_path(ctx, t, TMQ_PATH_INT16, (const float*)ctx->x.p, nullptr, (int64_t*)ctx->acc.p);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(acc, ctx->acc.p, sizeof(int64_t) * need, hipMemcpyDeviceToHost, ctx->stream));
+    if (x_scale) HIP_TRY(hipMemcpyAsync(x_scale, ctx->act.p, sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     return 0;
 }
@@ -623,6 +779,10 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
             return tmq_fail(TMQ_ERR_DESC, "descriptor %d: null weight or x", i);
         }
         const TmqTensorDev& td = t->dev;
+        if (is_float_type((uint32_t)td.type)) {
+            delete ch;
+            return tmq_fail(TMQ_ERR_DESC, "descriptor %d: %s tensors have no descriptor type", i, type_name((uint32_t)td.type));
+        }
         long rows;
         if (td.type == TMQ_TYPE_Q4_K || td.type == TMQ_TYPE_Q6_K) {
             if (d.num_col_groups == 0 || d.num_tiles % d.num_col_groups || d.num_col_groups * 256 != td.cols) {

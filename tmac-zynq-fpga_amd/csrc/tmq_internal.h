@@ -14,8 +14,15 @@
 //   Q4_K  A: qs   [b][8][r] x16B     B: hdr (d,dmin,scales[12]) [b][r] x16B
 //   Q6_K  A: ql   [b][8][r] x16B     B: qh [b][4][r] x16B   C: sc [b][r] x16B
 //         D: d [b][r] u16
+//   F32   A: 32 floats [b][8][r] x16B        (b = 32-column block)
+//   F16   A: 32 halves [b][4][r] x16B
 //
 // rows_pad = rows rounded up to 64; padding rows are zero (they compute 0).
+//
+// INT16 path (matmul_fpga_int16, sim/tmac_gguf.cpp:887-940), built on first
+// use by tmq_tensor_prepare_int16: the rounded int16 weights of every row,
+// W: [c/8][r] x16B (8 consecutive columns per chunk), and the per-row
+// row_scale max|E|/32767 (rs16).
 #pragma once
 #include <stdint.h>
 
@@ -40,7 +47,12 @@ struct TmqTensorDev {
     const uint8_t* pe;       // fit codes (Q5_0: 1 B, Q4_K: 8 B, Q6_K: 16 B per block and row)
     const float* row_inv;    // Q5_0/K-quants: row_inv; Q8_0: 1/row_scale (guarded)
     const float* row_scale;  // Q8_0 only
+    const uint8_t* pw;       // INT16 path weights (null until prepared)
+    const float* rs16;       // INT16 path row scales
 };
+
+// matmul branch a work takes (sim/tmac_gguf.cpp:473-493)
+enum { TMQ_WPATH_FPGA = 0, TMQ_WPATH_INT16 = 1, TMQ_WPATH_FP32 = 2 };
 
 // Prepared activation, written by act_prep (or by the host for int16 input):
 //   +0  float x_scale   +4 int32 n   +16 u32 XH[n/2]   +16+2n u32 XL[n/2]
@@ -73,6 +85,8 @@ struct TmqWork {
     int32_t ngroups;     // workgroups of this GEMV (row groups x kc)
     int32_t kc;          // engine K-split: workgroups per row group (>= 1)
     int32_t resid;
+    int32_t path;        // TMQ_WPATH_*: the type's own kernel, INT16 or FP32
+    const float* xf;     // FP32 path: the fp32 activation (act unused)
     // engine, kc = 1: fused SwiGLU.  The tensor holds ffn_gate and ffn_up
     // rows interleaved in groups of 32 (rows 64q..64q+31 = gate rows
     // 32q..32q+31, the next 32 = the same up rows); row j of the result,
@@ -188,3 +202,7 @@ int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* ou
 int tmq_launch_zero_acc(int64_t* p, size_t n, hipStream_t s);
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s);
+// INT16 path weights and row scales of a tensor (t.pw, t.rs16 allocated)
+int tmq_launch_i16_prep(const TmqTensorDev& t, hipStream_t s);
+// F32 / F16 tensors: flags non-finite elements
+int tmq_launch_check_finite(const TmqTensorDev& t, int* bad, hipStream_t s);

@@ -31,6 +31,7 @@ typedef __attribute__((address_space(4))) const uint32_t cu32;
 namespace {
 
 constexpr int kQ5_0 = 6, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14;
+constexpr int kF32 = 0, kF16 = 1;  // element types of the INT16 / FP32 paths
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xffffu));
@@ -914,6 +915,211 @@ __global__ __launch_bounds__(64 * gemv_waves(FMT)) void chain_kernel(const TmqWo
     run_group<FMT, CLAMP>(w, blockIdx.x - w.first_group);
 }
 
+// ------------------------------------------------- INT16 and FP32 paths
+// The two other branches of the reference's `matmul` (sim/tmac_gguf.cpp:
+// 473-493): matmul_fpga_int16 (:887-940), taken when --fpga is on but the
+// tensor type's own flag is off, and the FP32 loop (:488-492) of a run
+// without any --fpga flag.  Both start from the exact element values of
+// read_tensor (:398-411, the decoders :236-393).
+
+// 32 exact elements of row r, columns j0..j0+31 (j0 % 32 == 0), evaluated as
+// read_tensor does: Q8_0 val*scale (:247), Q5_0 d*q (:322), Q6_K d*sc*q
+// (:360), Q4_K d*sc*q4 - dmin*m (:392), F32 as stored, F16 half->float.
+__device__ __forceinline__ void elems32(const TmqTensorDev& t, int r, int j0, float (&E)[32]) {
+    const size_t R = t.rows_pad;
+    if (t.type == kQ8_0) {
+        const int b = j0 >> 5;
+        const uint4 v0 = ld16(t.pa + p16(b, 0, 2, R, r)), v1 = ld16(t.pa + p16(b, 1, 2, R, r));
+        const float d = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            E[i] = (float)(int8_t)byte_of(v0, i) * d;
+            E[16 + i] = (float)(int8_t)byte_of(v1, i) * d;
+        }
+    } else if (t.type == kQ5_0) {
+        const int b = j0 >> 5;
+        const size_t o = (size_t)b * R + r;
+        const uint4 qs = ld16(t.pa + o * 16);
+        const uint32_t qhp = ld4(t.pb + o * 4);
+        const float d = h2f(ld2(t.pd + o * 2));
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            const uint32_t by = byte_of(qs, e & 15);
+            const int nib = (e < 16) ? (int)(by & 15u) : (int)(by >> 4);
+            const int hb = (int)((qhp >> (8 * (e & 3) + (e >> 2))) & 1u);
+            E[e] = d * (float)((hb << 4) + nib - 16);
+        }
+    } else if (t.type == kQ4_K) {
+        const int b = j0 >> 8, s = (j0 & 255) >> 5;
+        const uint4 h = ld16(t.pb + p16(b, 0, 1, R, r));
+        const uint4 qa = ld16(t.pa + p16(b, (s >> 1) * 2, 8, R, r)), qb = ld16(t.pa + p16(b, (s >> 1) * 2 + 1, 8, R, r));
+        const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+        int sc, m;
+        q4k_scale_min(h, s, sc, m);
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t by = byte_of(i < 16 ? qa : qb, i & 15);
+            const int q4 = (s & 1) ? (int)(by >> 4) : (int)(by & 15u);
+            E[i] = d * (float)sc * (float)q4 - dmin * (float)m;
+        }
+    } else if (t.type == kQ6_K) {
+        const int b = j0 >> 8, off = j0 & 255, half = off >> 7, sub = (off & 127) >> 5;
+        const int cl = half * 4 + (sub & 1) * 2, ch = half * 2;
+        const uint4 l0 = ld16(t.pa + p16(b, cl, 8, R, r)), l1 = ld16(t.pa + p16(b, cl + 1, 8, R, r));
+        const uint4 h0 = ld16(t.pb + p16(b, ch, 4, R, r)), h1 = ld16(t.pb + p16(b, ch + 1, 4, R, r));
+        const uint4 scv = ld16(t.pc + p16(b, 0, 1, R, r));
+        const float d = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const uint32_t qlb = byte_of(l < 16 ? l0 : l1, l & 15), qhb = byte_of(l < 16 ? h0 : h1, l & 15);
+            const uint32_t nib = (sub < 2) ? (qlb & 15u) : (qlb >> 4);
+            const int q = (int)(nib | (((qhb >> (2 * sub)) & 3u) << 4)) - 32;
+            const int sc = (int)(int8_t)byte_of(scv, half * 8 + (l >> 4) + sub * 2);
+            E[l] = d * (float)sc * (float)q;
+        }
+    } else if (t.type == kF32) {
+        const int b = j0 >> 5;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const uint4 v = ld16(t.pa + p16(b, c, 8, R, r));
+            E[4 * c] = __uint_as_float(v.x);
+            E[4 * c + 1] = __uint_as_float(v.y);
+            E[4 * c + 2] = __uint_as_float(v.z);
+            E[4 * c + 3] = __uint_as_float(v.w);
+        }
+    } else {  // F16
+        const int b = j0 >> 5;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint4 v = ld16(t.pa + p16(b, c, 4, R, r));
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t w = dw_of(v, k);
+                E[8 * c + 2 * k] = h2f(w);
+                E[8 * c + 2 * k + 1] = h2f(w >> 16);
+            }
+        }
+    }
+}
+
+// matmul_fpga_int16's weight quantisation (sim/tmac_gguf.cpp:905-925), a
+// function of the weights alone, done once per tensor: per row
+// row_scale = max|E|/32767 (1 below 1e-10), w = (int16)roundf(E/row_scale)
+// with the IEEE division; 8 weights per 16-byte chunk of plane pw.
+// (|E/row_scale| <= 32767*(1+2^-24), so the cast never overflows.)
+__global__ __launch_bounds__(64) void i16_prep_kernel(TmqTensorDev t) {
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    if (r >= t.rows_pad) return;
+    const size_t R = t.rows_pad;
+    float m = 0.0f;
+    for (int j0 = 0; j0 < t.cols; j0 += 32) {
+        float E[32];
+        elems32(t, r, j0, E);
+#pragma unroll
+        for (int i = 0; i < 32; i++) m = fmaxf(m, fabsf(E[i]));
+    }
+    const float rs = (m < 1e-10f) ? 1.0f : m / 32767.0f;
+    ((float*)t.rs16)[r] = rs;
+    uint8_t* pw = (uint8_t*)t.pw;
+    for (int j0 = 0; j0 < t.cols; j0 += 32) {
+        float E[32];
+        elems32(t, r, j0, E);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint32_t d[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int a = (int)(int16_t)roundf(E[8 * c + 2 * k] / rs);
+                const int b = (int)(int16_t)roundf(E[8 * c + 2 * k + 1] / rs);
+                d[k] = ((uint32_t)a & 0xffffu) | ((uint32_t)b << 16);
+            }
+            *(uint4*)(pw + p16(j0 / 8 + c, 0, 1, R, r)) = make_uint4(d[0], d[1], d[2], d[3]);
+        }
+    }
+}
+
+// F32 / F16 tensors: every element finite (the quantized types check their
+// fp16 scales in rowstat_kernel).
+__global__ __launch_bounds__(64) void check_finite_kernel(TmqTensorDev t, int* bad) {
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    if (r >= t.rows) return;
+    bool ok = true;
+    for (int j0 = 0; j0 < t.cols; j0 += 32) {
+        float E[32];
+        elems32(t, r, j0, E);
+#pragma unroll
+        for (int i = 0; i < 32; i++) ok = ok && __builtin_isfinite(E[i]);
+    }
+    if (!ok) atomicOr(bad, 1);
+}
+
+// INT16 64-column tile tt of row r: result = sum_k xq[c+k] * w[r][c+k]
+// (axi_vecmul_tile_int16 -> vecmul_1x64_int16, sim/fpga_sim.hpp:437-446,
+// :45-54) from the xh/xl pairs: |sum w*xh|, |sum w*xl| < 2^30 over 64
+// columns, so both stay inside int32.
+template <class AT>
+__device__ __forceinline__ int64_t i16_tile(const TmqTensorDev& t, const AT& A, int r, int tt) {
+    const size_t R = t.rows_pad;
+    const int c0 = 8 * tt, c1 = min(c0 + 8, t.cols >> 3);
+    uint4 v[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) v[c] = ld16(t.pw + p16(min(c0 + c, c1 - 1), 0, 1, R, r));
+    int sh = 0, sl = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        if (c0 + c >= c1) break;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int kx = 4 * (c0 + c) + k;
+            sh = dot2(dw_of(v[c], k), A.xh[kx], sh);
+            sl = dot2(dw_of(v[c], k), A.xl[kx], sl);
+        }
+    }
+    return (int64_t)sh * 256 + sl;
+}
+
+// matmul_fpga_int16 (sim/tmac_gguf.cpp:887-940): 4 waves, each owning 64
+// rows, walk the 64-column tiles in order and fold every tile's result as
+// y += (double)result * x_scale * row_scale (:930-931).
+__global__ __launch_bounds__(64 * TMQ_WAVES) void i16_gemv_kernel(TmqWork w) {
+    const TmqTensorDev& t = w.t;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r0 = (blockIdx.x * TMQ_WAVES + wave) * 64;
+    if (r0 >= t.rows_pad) return;
+    const int r = r0 + lane;
+    const float rs = t.rs16[r];
+    const Act A = act_view(w.act);
+    const int nt = (t.cols + 63) / 64;
+    float y = 0.0f;
+    for (int tt = 0; tt < nt; tt++) {
+        const int64_t P = i16_tile(t, A, r, tt);
+        if (w.acc && r < t.rows) w.acc[(size_t)r * nt + tt] = P;
+        y = (float)((double)y + ((double)P * (double)A.xs) * (double)rs);
+    }
+    if (w.y && r < t.rows) store_y(w, r, y);
+}
+
+// The FP32 loop of `matmul` (sim/tmac_gguf.cpp:488-492): y_r = sum over
+// j in order of read_tensor(r, j) * x[j], every product and sum rounded to
+// fp32 (no fma: the library is built with -ffp-contract=off).  One lane per
+// row, 4 waves of 64 rows; x is read through the scalar cache.
+__global__ __launch_bounds__(64 * TMQ_WAVES) void f32_gemv_kernel(TmqWork w) {
+    const TmqTensorDev& t = w.t;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r0 = (blockIdx.x * TMQ_WAVES + wave) * 64;
+    if (r0 >= t.rows_pad) return;
+    const int r = r0 + lane;
+    const cu32* xp = (const cu32*)w.xf;
+    float sum = 0.0f;
+    for (int j0 = 0; j0 < t.cols; j0 += 32) {
+        float E[32];
+        elems32(t, r, j0, E);
+#pragma unroll
+        for (int i = 0; i < 32; i++) sum = sum + E[i] * __uint_as_float(xp[j0 + i]);
+    }
+    if (w.y && r < t.rows) store_y(w, r, sum);
+}
+
 // ------------------------------------------------------------ engine GEMV
 // One launch = one activation recipe (TmqEngAct) + row groups of works of
 // any formats.  Every workgroup first issues the loads of its first weight
@@ -1592,6 +1798,11 @@ __global__ void repack_kernel(int type, const uint8_t* __restrict__ src, TmqTens
         const uint8_t* s = src + idx * 144;
         for (int i = 0; i < 16; i++) pb[p16(b, 0, 1, R, r) + i] = s[i];
         for (int i = 0; i < 128; i++) pa[p16(b, i >> 4, 8, R, r) + (i & 15)] = s[16 + i];
+    } else if (type == kF32 || type == kF16) {
+        // row-major elements: block b of row r is 32 contiguous values
+        const int nbytes = type == kF32 ? 128 : 64, C = nbytes / 16;
+        const uint8_t* s = src + idx * nbytes;
+        for (int i = 0; i < nbytes; i++) pa[p16(b, i >> 4, C, R, r) + (i & 15)] = s[i];
     } else if (type == kQ6_K) {
         const uint8_t* s = src + idx * 210;
         for (int i = 0; i < 128; i++) pa[p16(b, i >> 4, 8, R, r) + (i & 15)] = s[i];
@@ -2080,6 +2291,15 @@ template <int F, bool C> struct GemvK { static auto fn() { return gemv_kernel<F,
 template <int F, bool C> struct ChainK { static auto fn() { return chain_kernel<F, C>; } };
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s) {
     if (w.ngroups <= 0) return 0;
+    if (w.path != TMQ_WPATH_FPGA) {
+        // INT16 / FP32 paths: 4 waves of 64 rows per workgroup
+        if (w.path == TMQ_WPATH_INT16 && (!w.t.pw || !w.t.rs16 || !w.act)) return (int)hipErrorInvalidValue;
+        if (w.path == TMQ_WPATH_FP32 && !w.xf) return (int)hipErrorInvalidValue;
+        const int g = (w.t.rows_pad / 64 + TMQ_WAVES - 1) / TMQ_WAVES;
+        if (w.path == TMQ_WPATH_INT16) hipLaunchKernelGGL(i16_gemv_kernel, dim3(g), dim3(64 * TMQ_WAVES), 0, s, w);
+        else hipLaunchKernelGGL(f32_gemv_kernel, dim3(g), dim3(64 * TMQ_WAVES), 0, s, w);
+        return (int)hipGetLastError();
+    }
     void* k = kernel_for<GemvK>(w.t.type, w.t.clamp);
     if (!k) return (int)hipErrorInvalidValue;
     TmqWork arg = w;
@@ -2155,6 +2375,17 @@ int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x,
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s) {
     hipLaunchKernelGGL(tile_q8_kernel, dim3(1), dim3(64), 0, s, W, cs, vec, out);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_i16_prep(const TmqTensorDev& t, hipStream_t s) {
+    if (!t.pw || !t.rs16) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(i16_prep_kernel, dim3(t.rows_pad / 64), dim3(64), 0, s, t);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_check_finite(const TmqTensorDev& t, int* bad, hipStream_t s) {
+    hipLaunchKernelGGL(check_finite_kernel, dim3(t.rows_pad / 64), dim3(64), 0, s, t, bad);
     return (int)hipGetLastError();
 }
 

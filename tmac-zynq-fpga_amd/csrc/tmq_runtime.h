@@ -56,6 +56,7 @@ struct tmq_tensor {
     tmq_ctx* ctx = nullptr;
     TmqTensorDev dev{};
     void* alloc = nullptr;  // planes + row_inv + row_scale
+    void* i16_alloc = nullptr;  // INT16 path weights + row scales (tmq_tensor_prepare_int16)
     uint64_t weight_bytes = 0;
 };
 
@@ -68,3 +69,5 @@ int tmq_rt_tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t co
                          bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
                          tmq_tensor** out);
 TmqWork tmq_rt_make_work(const tmq_tensor* t, const uint8_t* act, float* y, int64_t* acc);
+// builds the INT16 path planes of t once (matmul_fpga_int16's weights)
+int tmq_rt_prepare_int16(tmq_ctx* ctx, tmq_tensor* t);

@@ -21,16 +21,21 @@ from . import synth  # noqa: F401  (re-export)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmq.so")
 
-Q5_0, Q8_0, Q4_K, Q6_K, CPU_OP = 6, 8, 12, 14, 15
-QK = {Q8_0: 32, Q5_0: 32, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210}
+F32, F16, Q5_0, Q8_0, Q4_K, Q6_K, CPU_OP = 0, 1, 6, 8, 12, 14, 15
+QK = {Q8_0: 32, Q5_0: 32, Q4_K: 256, Q6_K: 256, F32: 32, F16: 32}
+BLOCK_BYTES = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210, F32: 128, F16: 64}
+# matmul branches and the reference's --fpga* flags (include/tmq.h)
+PATH_FPGA, PATH_INT16, PATH_FP32 = 0, 1, 2
+FLAG_FPGA, FLAG_Q8_0, FLAG_Q5_0, FLAG_Q4_K, FLAG_Q6_K = 1, 2, 4, 8, 16
+FLAGS_ALL = 31
 NOALLOC_MAX_COLS = 16384  # TMQ_NOALLOC_MAX_COLS
 
 EXPORTS = [
     "tmq_last_error", "tmq_version", "tmq_open", "tmq_close", "tmq_stream", "tmq_sync",
     "tmq_tensor_upload", "tmq_tensor_upload_dev", "tmq_tensor_free", "tmq_tensor_info",
     "tmq_tensor_row_norm", "tmq_tensor_fit_stats", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_dev_noalloc",
-    "tmq_gemv_partials",
+    "tmq_gemv_partials", "tmq_route", "tmq_matmul_flags", "tmq_matmul_path", "tmq_gemv_dev_path",
+    "tmq_gemv_partials_path", "tmq_tensor_prepare_int16",
     "tmq_vecmul_tile_q8", "tmq_vecmul_tile_q5_0_8x896", "tmq_vecmul_tile_q6_k",
     "tmq_vecmul_tile_q4k", "tmq_phaseb_run", "tmq_chain_create", "tmq_chain_run",
     "tmq_chain_prepare", "tmq_chain_launch",
@@ -46,6 +51,11 @@ EXPORTS = [
 class LaunchTime(C.Structure):
     """tmq_launch_time"""
     _fields_ = [("name", C.c_char_p), ("start_ms", C.c_float), ("end_ms", C.c_float)]
+
+
+def route(qtype: int, flags: int) -> int:
+    """the matmul branch (PATH_*) the reference takes for a type under flags"""
+    return _check(lib().tmq_route(qtype, flags))
 
 
 class TmqError(RuntimeError):
@@ -98,6 +108,12 @@ def lib(path: str = LIB_PATH):
         "tmq_gemv_dev": (I, [P, P, P, P, P]),
         "tmq_gemv_dev_noalloc": (I, [P, P, P, P, P]),
         "tmq_gemv_partials": (I, [P, P, P, P, U64, P]),
+        "tmq_route": (I, [U32, U32]),
+        "tmq_matmul_flags": (I, [P, P, U32, P, P, I, I]),
+        "tmq_matmul_path": (I, [P, P, I, P, P, I, I]),
+        "tmq_gemv_dev_path": (I, [P, P, I, P, P, P]),
+        "tmq_gemv_partials_path": (I, [P, P, I, P, P, U64, P]),
+        "tmq_tensor_prepare_int16": (I, [P, P]),
         "tmq_vecmul_tile_q8": (I, [P, P, P, P, P]),
         "tmq_vecmul_tile_q5_0_8x896": (I, [P, P, P, P, P, I]),
         "tmq_vecmul_tile_q6_k": (I, [P, P, I, P, I, P, P, I]),
@@ -254,6 +270,31 @@ class Context:
         y = np.empty(t.rows, dtype=np.float32)
         _check(lib().tmq_matmul(self.handle, t.handle, _p(x), _p(y), t.rows, t.cols))
         return y
+
+    def matmul_path(self, t: Tensor, x: np.ndarray, path: int) -> np.ndarray:
+        """one branch of the reference's matmul (PATH_FPGA / PATH_INT16 / PATH_FP32)"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(t.rows, dtype=np.float32)
+        _check(lib().tmq_matmul_path(self.handle, t.handle, path, _p(x), _p(y), t.rows, t.cols))
+        return y
+
+    def matmul_flags(self, t: Tensor, x: np.ndarray, flags: int) -> np.ndarray:
+        """the reference's matmul under its --fpga* flags (FLAG_*)"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(t.rows, dtype=np.float32)
+        _check(lib().tmq_matmul_flags(self.handle, t.handle, flags, _p(x), _p(y), t.rows, t.cols))
+        return y
+
+    def partials_int16(self, t: Tensor, x: np.ndarray):
+        """INT16 path: int64 [rows][ceil(cols/64)] tile results and x_scale"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        acc = np.empty((t.rows, (t.cols + 63) // 64), dtype=np.int64)
+        xs = np.zeros(1, dtype=np.float32)
+        _check(lib().tmq_gemv_partials_path(self.handle, t.handle, PATH_INT16, _p(x), _p(acc), acc.size, _p(xs)))
+        return acc, xs[0]
+
+    def gemv_dev_path(self, t: Tensor, path: int, x_ptr: int, y_ptr: int | None, acc_ptr: int | None = None):
+        _check(lib().tmq_gemv_dev_path(self.handle, t.handle, path, x_ptr, y_ptr, acc_ptr))
 
     def partials(self, t: Tensor, x: np.ndarray):
         x = np.ascontiguousarray(x, dtype=np.float32)

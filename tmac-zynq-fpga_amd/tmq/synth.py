@@ -9,6 +9,8 @@ distributions are the ones BASELINE.json fixes per format:
   Q4_K  d, dmin = fp16(|N| * 0.01), random 12-byte scales,
         random nibbles                                         144 B / 256 weights
   Q6_K  random ql/qh, sc ~ U{-32..31} int8, d = fp16(|N|*0.01)  210 B / 256 weights
+  F32   N(0,1) * 0.05 (row-major fp32)                          4 B / weight
+  F16   the same rounded to fp16                                2 B / weight
   x     fp32 N(0,1)
 
 Block layouts follow ggml as read by the reference decoders
@@ -19,10 +21,10 @@ from __future__ import annotations
 
 import numpy as np
 
-Q8_0, Q5_0, Q4_K, Q6_K = 8, 6, 12, 14
+F32, F16, Q8_0, Q5_0, Q4_K, Q6_K = 0, 1, 8, 6, 12, 14
 # type -> (weights per block, bytes per block)
-BLOCK = {Q8_0: (32, 34), Q5_0: (32, 22), Q4_K: (256, 144), Q6_K: (256, 210)}
-NAMES = {Q8_0: "q8_0", Q5_0: "q5_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+BLOCK = {Q8_0: (32, 34), Q5_0: (32, 22), Q4_K: (256, 144), Q6_K: (256, 210), F32: (32, 128), F16: (32, 64)}
+NAMES = {Q8_0: "q8_0", Q5_0: "q5_0", Q4_K: "q4_k", Q6_K: "q6_k", F32: "f32", F16: "f16"}
 
 
 def nbytes(qtype: int, rows: int, cols: int) -> int:
@@ -60,6 +62,9 @@ def gen_weights(qtype: int, rows: int, cols: int, seed: int) -> np.ndarray:
         out[:, 192:208] = rng.integers(-32, 32, size=(nblk, 16), dtype=np.int8).view(np.uint8)
         d = _f16_bits(np.abs(rng.standard_normal(nblk, dtype=np.float32)) * np.float32(0.01))
         out[:, 208:210] = d.view(np.uint8).reshape(nblk, 2)
+    elif qtype in (F32, F16):
+        v = rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.05)
+        return (v if qtype == F32 else v.astype(np.float16)).view(np.uint8).copy()
     else:
         raise ValueError(f"unsupported type {qtype}")
     return out.reshape(-1)
