@@ -279,6 +279,17 @@ int tmq_model_position(const tmq_model* m);
 int tmq_model_set_graphs(tmq_model* m, int enable);
 /* reset_cache + process_prompt (sim/tmac_gguf.cpp:1950-1997) */
 int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n);
+/* The reference's --fpga* flags (TMQ_FLAG_*, default TMQ_FLAGS_ALL = the
+ * four --fpga-<type> paths): every projection then takes the branch that
+ * `matmul` takes for its type under these flags (sim/tmac_gguf.cpp:473-493:
+ * its own quantized kernel, matmul_fpga_int16, or the FP32 loop without
+ * any flag), and the logits are get_logits_q8 under TMQ_FLAG_Q8_0, else
+ * get_logits (:1852-1866, :2033-2037).  Tensors routed to INT16 get their
+ * rounded weights built here (2 bytes per weight).  The batched prefill
+ * covers the all-flags arithmetic only: other flag sets run prompts one
+ * token at a time.  Captured step graphs are rebuilt. */
+int tmq_model_set_flags(tmq_model* m, uint32_t flags);
+uint32_t tmq_model_get_flags(const tmq_model* m);
 /* How tmq_model_prompt runs the prompt: chunk > 0 (default 512; env
  * TMQ_PREFILL) pushes up to `chunk` tokens through each layer together
  * (int8-MFMA GEMMs, the same bits as one token at a time); 0 processes one

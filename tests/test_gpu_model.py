@@ -165,13 +165,24 @@ def test_cli(golden, tmp_path):
     path = tmp_path / "c4.tmac"
     tmacfile.write(path, model_synth.gen_model(int(golden["model_seed"])))
     prompt = f"{int(golden['prompt'][0])}\n"
-    r = subprocess.run([exe, str(path), "--generate", "16", "--fpga-q8", "--fpga-q5-0"], input=prompt,
+    allf = ["--fpga-q8", "--fpga-q5-0", "--fpga-q4k", "--fpga-q6-k"]  # the flags of model_c4.npz
+    r = subprocess.run([exe, str(path), "--generate", "16"] + allf, input=prompt,
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr
     got = [int(t) for t in r.stdout.split()]
     assert got == golden["tokens"][:16].tolist()
+    # the reference's other flag sets (tests/golden/model_flags.npz): Q4_K/Q6_K
+    # through matmul_fpga_int16, and no flag at all (the FP32 loop)
+    gf = load_golden("model_flags.npz")
+    r = subprocess.run([exe, str(path), "--generate", "8", "--fpga-q8", "--fpga-q5-0"], input=prompt,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert [int(t) for t in r.stdout.split()] == gf["q8q5_tokens"][:8].tolist()
+    r = subprocess.run([exe, str(path)], input=prompt, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert [t["id"] for t in json.loads(r.stdout)] == gf["fp32_top_ids"][0].tolist()
     trace = tmp_path / "trace.json"
-    r = subprocess.run([exe, str(path), "--perf", "--trace", str(trace)], input=prompt, capture_output=True,
+    r = subprocess.run([exe, str(path), "--perf", "--trace", str(trace)] + allf, input=prompt, capture_output=True,
                        text=True, timeout=300)
     assert r.returncode == 0, r.stderr
     top = json.loads(r.stdout)
@@ -181,7 +192,7 @@ def test_cli(golden, tmp_path):
     ev = json.loads(trace.read_text())["traceEvents"]
     assert len(ev) in (2 * 8 * (3 + 5 * 24), 2 * 8 * (3 + 6 * 24)) and {e["ph"] for e in ev} == {"B", "E"}
     # --dump-layers: cpp_layer_0..24.bin of the (one-token) prompt, as the reference writes them
-    r = subprocess.run([exe, str(path), "--dump-layers", "--dump-dir", str(tmp_path)], input=prompt,
+    r = subprocess.run([exe, str(path), "--dump-layers", "--dump-dir", str(tmp_path)] + allf, input=prompt,
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr
     assert [t["id"] for t in json.loads(r.stdout)] == golden["top_ids"][0].tolist()

@@ -14,7 +14,9 @@ static __device__ __forceinline__ int64_t tmq_ld_acc(const int64_t* p) {
 static __device__ float tmq_fin(const TmqDeferred& D, int i) {
     const double xs = (double)*D.xs;
     float v;
-    if (D.ntiles == 0) {
+    if (D.val) {
+        v = __hip_atomic_load(D.val + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (D.ntiles == 0) {
         v = (float)(((double)tmq_ld_acc(D.acc + i) * xs) / (double)D.row_inv[i]);
     } else {
         const double rs = (double)D.row_scale[i];
@@ -40,7 +42,13 @@ struct TmqFinRaw {
 template <bool Q8>
 static __device__ __forceinline__ TmqFinRaw<Q8> fin_load(const TmqDeferred& D, int i) {
     TmqFinRaw<Q8> f;
-    if constexpr (Q8) {
+    if (D.val) {
+        // FP32 path: the value itself (its bits in p[0])
+#pragma unroll
+        for (int t = 0; t < (Q8 ? TMQ_FIN_MAXT : 1); t++) f.p[t] = 0;
+        f.p[0] = (int64_t)__float_as_uint(__hip_atomic_load(D.val + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        f.r = 1.0f;
+    } else if constexpr (Q8) {
         const int nt = D.ntiles;
 #pragma unroll
         for (int t = 0; t < TMQ_FIN_MAXT; t++) f.p[t] = tmq_ld_acc(D.acc + (size_t)i * nt + min(t, nt - 1));
@@ -50,14 +58,16 @@ static __device__ __forceinline__ TmqFinRaw<Q8> fin_load(const TmqDeferred& D, i
         f.r = D.row_inv[i];
     }
     // no bias: any valid row vector stands in (the value is not used)
-    const float* bp = D.bias ? D.bias : Q8 ? D.row_scale : D.row_inv;
+    const float* bp = D.bias ? D.bias : D.val ? D.val : Q8 ? D.row_scale : D.row_inv;
     f.b = bp[i];
     return f;
 }
 template <bool Q8>
 static __device__ __forceinline__ float fin_finish(const TmqDeferred& D, const TmqFinRaw<Q8>& f, double xs) {
     float v;
-    if constexpr (Q8) {
+    if (D.val) {
+        v = __uint_as_float((uint32_t)f.p[0]);
+    } else if constexpr (Q8) {
         const double rs = (double)f.r;
         float y = 0.0f;
 #pragma unroll

@@ -3,14 +3,18 @@
 //
 //   tmq_gguf <model.tmac> [--generate N] [--max-seq N] [--perf] [--trace PATH]
 //            [--prefill N | --no-prefill] [--no-graphs]
-//            [--fpga-q8 --fpga-q5-0 --fpga-q4k --fpga-q6-k --fpga]
+//            [--fpga] [--fpga-int16] [--fpga-q8] [--fpga-q4k] [--fpga-q5-0] [--fpga-q6-k]
 //
 // Prompt token ids are read from stdin.  Without --generate the top-10
 // logits of the last prompt position are printed as JSON,
 // [{"id":…,"logit":%.3f},…] (:2156-2165); with --generate N the N greedily
 // chosen ids are printed one per line (the reference samples top-k with
-// rand(); greedy is this engine's choice).  All quantized formats always run
-// on the GPU, so the --fpga-* flags are accepted and change nothing.
+// rand(); greedy is this engine's choice).  The --fpga* flags set what the
+// reference's flags set (:2085-2091) and route every matmul the way its
+// `matmul` does (:473-493), all on the GPU: a type whose --fpga-<type> flag
+// is given takes its quantized kernel, the others matmul_fpga_int16 when
+// any --fpga flag is given, and without any flag every matmul is the FP32
+// loop; the logits are get_logits_q8 only under --fpga-q8 (:2151-2155).
 // The prompt runs through the batched prefill in chunks of --prefill N
 // tokens (default 512); --no-prefill runs it one token at a time.
 // --perf prints host timings (load, prompt, per-token decode) to stderr, then
@@ -96,12 +100,14 @@ int main(int argc, char** argv) {
         fprintf(stderr,
                 "Usage: %s <model.tmac> [--generate N] [--max-seq N] [--perf] [--trace PATH]\n"
                 "       [--prefill N | --no-prefill] [--no-graphs] [--dump-layers] [--dump-dir DIR]\n"
+                "       [--fpga] [--fpga-int16] [--fpga-q8] [--fpga-q4k] [--fpga-q5-0] [--fpga-q6-k]\n"
                 "  Prompt tokens read from stdin; top-10 logits JSON, or N greedy tokens, to stdout.\n",
                 argv[0]);
         return 1;
     }
     int generate_n = 0, max_seq = 512, prefill = 512;
     bool perf = false, graphs = true, dump_layers = false;
+    uint32_t flags = 0;  // the reference's g_use_fpga / g_fpga_* (all off by default)
     const char* trace_path = "/tmp/pipeline_trace.json";
     const char* dump_dir = "/tmp";
     for (int i = 2; i < argc; i++) {
@@ -114,7 +120,11 @@ int main(int argc, char** argv) {
         else if (!strcmp(argv[i], "--no-graphs")) graphs = false;
         else if (!strcmp(argv[i], "--dump-layers")) dump_layers = true;
         else if (!strcmp(argv[i], "--dump-dir") && i + 1 < argc) dump_dir = argv[++i];
-        else if (!strncmp(argv[i], "--fpga", 6)) continue;
+        else if (!strcmp(argv[i], "--fpga") || !strcmp(argv[i], "--fpga-int16")) flags |= TMQ_FLAG_FPGA;
+        else if (!strcmp(argv[i], "--fpga-q8")) flags |= TMQ_FLAG_FPGA | TMQ_FLAG_Q8_0;
+        else if (!strcmp(argv[i], "--fpga-q4k")) flags |= TMQ_FLAG_FPGA | TMQ_FLAG_Q4_K;
+        else if (!strcmp(argv[i], "--fpga-q5-0")) flags |= TMQ_FLAG_FPGA | TMQ_FLAG_Q5_0;
+        else if (!strcmp(argv[i], "--fpga-q6-k")) flags |= TMQ_FLAG_FPGA | TMQ_FLAG_Q6_K;
         else {
             fprintf(stderr, "[ERROR] unknown option %s\n", argv[i]);
             return 1;
@@ -133,6 +143,8 @@ int main(int argc, char** argv) {
     tmq_model* m = nullptr;
     if (tmq_model_load(ctx, argv[1], max_seq, &m) != TMQ_OK) return die("load");
     tmq_model_set_graphs(m, graphs ? 1 : 0);
+    if (tmq_model_set_flags(m, flags) != TMQ_OK) return die("flags");
+    if (prefill > 0 && flags != TMQ_FLAGS_ALL) prefill = 0;  // batched prefill: the all-flags arithmetic only
     if (tmq_model_set_prefill(m, prefill) != TMQ_OK) {
         fprintf(stderr, "[WARN] %s; the prompt runs one token at a time\n", tmq_last_error());
         tmq_model_set_prefill(m, 0);

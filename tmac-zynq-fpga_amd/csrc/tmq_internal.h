@@ -101,13 +101,17 @@ struct TmqWork {
 //   Q8_0             v = fold over tiles t of (float)((double)v + (double)P*xs*row_scale[i])
 //                    (:1075-1076)
 //   then v = v + bias[i] when a bias is given (:1595-1597).
+//   FP32 path        v = val[i], the rows as the FP32 loop left them
+//   INT16 path       as Q8_0, the tiles of matmul_fpga_int16 with its row
+//                    scales (:930-931)
 struct TmqDeferred {
     const int64_t* acc;
     const float* xs;
     const float* row_inv;
     const float* row_scale;
     const float* bias;
-    int32_t ntiles;        // 0: Q5_0 / K-quants; > 0: Q8_0 tiles per row
+    const float* val;      // FP32 path: final row values (acc, row_* unused)
+    int32_t ntiles;        // 0: Q5_0 / K-quants; > 0: Q8_0 / INT16 tiles per row
     int32_t pad_;
 };
 

@@ -1390,7 +1390,8 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
         pre();
         for (int i = c0 + tid; i < c1; i += nt) L.x[i] = a.x[i];
         pmax = __hip_atomic_load(a.max_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else if ((a.mode == TMQ_ACT_PLAIN || (a.mode == TMQ_ACT_RESID_NORM && a.d1.ntiles == 0)) && n <= EP * nt) {
+    } else if ((a.mode == TMQ_ACT_PLAIN || (a.mode == TMQ_ACT_RESID_NORM && a.d1.ntiles == 0 && !a.d1.val)) &&
+               n <= EP * nt) {
         // every load first (indices clamped into [0, n), pointers always
         // valid), then the arithmetic; one straight-line path per mode
         auto fast = [&](auto resid_tag) {
@@ -1468,6 +1469,8 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
         __syncthreads();
         s = L.red[0];
     }
+    // the FP32 path reads the activation itself: o = L.x * red[1]
+    if (tid == 0) L.red[1] = s;
     float mm;
     if (a.mode == TMQ_ACT_PRESCALED) {
         mm = __builtin_bit_cast(float, pmax);
@@ -1661,15 +1664,99 @@ __device__ __forceinline__ void eng_group_q8(const TmqEngAct& a, const EngLds& L
     }
 }
 
+// INT16 path in the engine (matmul_fpga_int16, sim/tmac_gguf.cpp:887-940),
+// K split over 64-column tiles as the Q8_0 split is: each wave takes tiles of
+// its chunk and stores their int64 results into kacc[r][tile] (one writer
+// per slot); the consumer folds them in order with the INT16 row scales.
+template <int NW, bool MULTI>
+__device__ __forceinline__ void eng_group_i16_split(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int gi) {
+    const TmqTensorDev& t = w.t;
+    const int kc = w.kc, g = gi / kc, c = gi - g * kc;
+    const int nt = (t.cols + 63) / 64;
+    const int t0 = c * nt / kc, t1 = (c + 1) * nt / kc;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    const float xs = eng_prologue<NW, eng_norm_segs<NW, kQ8_0, MULTI>()>(a, L, 64 * t0, min(64 * t1, t.cols), [] {});
+    if (w.xs_out && gi == 0 && threadIdx.x == 0) *w.xs_out = xs;
+    const ActL A = eng_act(L, xs);
+    for (int tt = t0 + wave; tt < t1; tt += NW) {
+        const int64_t P = i16_tile(t, A, r, tt);
+        if (r < t.rows)
+            __hip_atomic_store(w.kacc + (size_t)r * nt + tt, P, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// argmax candidate of a wave's 64 rows (y of row r, rows past t.rows excluded)
+__device__ __forceinline__ void wave_cand(const TmqWork& w, int r, float y, int grp) {
+    uint64_t k = (r < w.t.rows) ? argmax_key(y, r) : 0ull;
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t ok = __shfl_xor(k, o);
+        k = ok > k ? ok : k;
+    }
+    if ((threadIdx.x & 63) == 0) w.cand[grp] = k;
+}
+
+// INT16 path, direct (the logits through get_logits, :1852-1866): each
+// wave owns 64 rows and folds all its tiles; argmax candidates as the
+// Q8_0 logits leave them.
+template <int NW>
+__device__ __forceinline__ void eng_group_i16(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int g) {
+    const TmqTensorDev& t = w.t;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int grp = g * NW + wave, r0 = grp * 64;
+    const bool active = r0 < t.rows_pad;
+    const int r = active ? r0 + lane : lane;
+    const ActL A = eng_act(L, eng_prologue<NW, eng_norm_segs<NW, kQ8_0>()>(a, L, 0, t.cols, [] {}));
+    if (!active) return;
+    const float rs = t.rs16[r];
+    const int nt = (t.cols + 63) / 64;
+    float y = 0.0f;
+    for (int tt = 0; tt < nt; tt++)
+        y = (float)((double)y + ((double)i16_tile(t, A, r, tt) * (double)A.xs) * (double)rs);
+    if (w.y && r < t.rows) w.y[r] = y;
+    if (w.cand) wave_cand(w, r, y, grp);
+}
+
+// FP32 path in the engine (the loop of :488-492): each wave owns 64 rows,
+// one lane per row, and sums read_tensor(r, j) * o_j in column order from
+// the launch's fp32 activation o = L.x * red[1] (the rms_norm output
+// fl(fl(x*w)*scale), :447-453, or the input itself).  The rows are final
+// values (TmqDeferred.val); the logits also leave argmax candidates.
+template <int NW, bool MULTI>
+__device__ __forceinline__ void eng_group_f32(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int g) {
+    const TmqTensorDev& t = w.t;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int grp = g * NW + wave, r0 = grp * 64;
+    const bool active = r0 < t.rows_pad;
+    const int r = active ? r0 + lane : lane;
+    (void)eng_prologue<NW, eng_norm_segs<NW, kQ8_0, MULTI>()>(a, L, 0, t.cols, [] {});
+    if (!active) return;
+    const float sc = L.red[1];
+    float sum = 0.0f;
+    for (int j0 = 0; j0 < t.cols; j0 += 32) {
+        float E[32];
+        elems32(t, r, j0, E);
+#pragma unroll
+        for (int i = 0; i < 32; i++) sum = sum + E[i] * (L.x[j0 + i] * sc);
+    }
+    if (w.y && r < t.rows) __hip_atomic_store(w.y + r, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (w.cand) wave_cand(w, r, sum, grp);
+}
+
 // Format codes of the engine kernel variants: the ggml types, and
 // kQ8_DIRECT for the logits (Q8_0, one wave per 64 rows, direct output).
 constexpr int kQ8_DIRECT = 108;
+// the other branches of matmul: INT16 K-split / direct, FP32
+constexpr int kI16 = 116, kI16_DIRECT = 117, kF32P = 200;
 
 template <int NW, int FMT, bool MULTI>
 __device__ __forceinline__ void eng_dispatch(const TmqEngAct& a, const EngLds& L, const TmqWork& w) {
     const int g = blockIdx.x - w.first_group;
     if constexpr (FMT == kQ8_0) eng_group_q8_split<NW, MULTI>(a, L, w, g);
     else if constexpr (FMT == kQ8_DIRECT) eng_group_q8<NW>(a, L, w, g);
+    else if constexpr (FMT == kI16) eng_group_i16_split<NW, MULTI>(a, L, w, g);
+    else if constexpr (FMT == kI16_DIRECT) eng_group_i16<NW>(a, L, w, g);
+    else if constexpr (FMT == kF32P) eng_group_f32<NW, MULTI>(a, L, w, g);
     else eng_group_k<FMT, NW, MULTI>(a, L, w, g);
 }
 
@@ -2340,6 +2427,17 @@ static void* eng_kernel_for(int fa, int fb) {
     if (fa == kQ6_K && fb == kQ6_K) return TMQ_ENG_K(kQ6_K, kQ6_K);
     if (fa == kQ8_0 && fb == kQ8_0) return TMQ_ENG_K(kQ8_0, kQ8_0);
     if (fa == kQ8_DIRECT && fb == kQ8_DIRECT) return TMQ_ENG_K(kQ8_DIRECT, kQ8_DIRECT);
+    if constexpr (NW == 4) {
+        // the INT16 / FP32 branches (4-wave launches only)
+        if (fa == kI16 && fb == kI16) return TMQ_ENG_K(kI16, kI16);
+        if (fa == kF32P && fb == kF32P) return TMQ_ENG_K(kF32P, kF32P);
+        if constexpr (MULTI) {
+            if (fa == kQ5_0 && fb == kI16) return TMQ_ENG_K(kQ5_0, kI16);
+            if (fa == kI16 && fb == kQ8_0) return TMQ_ENG_K(kI16, kQ8_0);
+        } else {
+            if (fa == kI16_DIRECT && fb == kI16_DIRECT) return TMQ_ENG_K(kI16_DIRECT, kI16_DIRECT);
+        }
+    }
 #undef TMQ_ENG_K
     return nullptr;
 }
@@ -2349,14 +2447,21 @@ int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
     if (l.act.n <= 0 || l.act.n > TMQ_ENG_MAXN || l.act.n % 2 || l.nworks < 1 || l.nworks > TMQ_ENG_MAXW)
         return (int)hipErrorInvalidValue;
     // format of the first and the last work (the others must match the first)
-    auto code = [](const TmqWork& w) { return w.t.type == kQ8_0 && !w.kacc ? kQ8_DIRECT : w.t.type; };
+    auto code = [](const TmqWork& w) {
+        if (w.path == TMQ_WPATH_INT16) return w.kacc ? kI16 : kI16_DIRECT;
+        if (w.path == TMQ_WPATH_FP32) return kF32P;
+        return w.t.type == kQ8_0 && !w.kacc ? kQ8_DIRECT : w.t.type;
+    };
     const int fa = code(l.w[0]), fb = code(l.w[l.nworks - 1]);
     for (int i = 1; i + 1 < l.nworks; i++)
         if (code(l.w[i]) != fa) return (int)hipErrorInvalidValue;
     // the kernels split a row's units (or Q8_0 tiles) into kc chunks in int32
-    for (int i = 0; i < l.nworks; i++)
+    for (int i = 0; i < l.nworks; i++) {
         if ((int64_t)l.w[i].t.nb * 4 * (l.w[i].kc > 0 ? l.w[i].kc : 1) >= ((int64_t)1 << 31))
             return (int)hipErrorInvalidValue;
+        if (l.w[i].path == TMQ_WPATH_INT16 && (!l.w[i].t.pw || !l.w[i].t.rs16)) return (int)hipErrorInvalidValue;
+        if (l.w[i].path == TMQ_WPATH_FP32 && l.w[i].t.cols != l.act.n) return (int)hipErrorInvalidValue;
+    }
     void* k = nullptr;
     if (l.nworks > 1) k = waves == 16 ? eng_kernel_for<16, true>(fa, fb) : waves == 4 ? eng_kernel_for<4, true>(fa, fb) : nullptr;
     else k = waves == 16 ? eng_kernel_for<16, false>(fa, fb) : waves == 4 ? eng_kernel_for<4, false>(fa, fb) : nullptr;

@@ -48,6 +48,7 @@ struct Layer {
     size_t attn_norm = 0, ffn_norm = 0;  // offsets into fvec (floats)
     long bq = -1, bk = -1, bv = -1;      // bias offsets or -1
     Launch qkv, o_l, gu, dn;
+    bool fused_gu = false;  // gate+up+SwiGLU in one launch (gu_t) under the current flags
     // K-split results of this layer's GEMVs, finalised by their consumers
     TmqDeferred dq{}, dk{}, dv{}, dout{}, dg{}, du{}, dd{};
 };
@@ -149,7 +150,9 @@ struct tmq_model {
     float* hid[2] = {nullptr, nullptr};
     float *ctxv = nullptr, *logits = nullptr, *fvec = nullptr, *dump = nullptr, *view = nullptr;
     int64_t* kacc = nullptr;  // all K-split accumulators of a step
-    size_t kacc_n = 0;
+    size_t kacc_n = 0;        // used by the current flags (zeroed per step)
+    size_t kacc_cap = 0;      // allocated
+    uint32_t flags = TMQ_FLAGS_ALL;  // the reference's --fpga* globals (TMQ_FLAG_*)
     float* xs = nullptr;      // x_scale slots, 4 per layer
     uint64_t* cand = nullptr;  // logits argmax candidates, one per 64 rows
     int n_cand = 0;
@@ -243,9 +246,9 @@ int launch_layers(tmq_model* m, bool dump) {
         PROF("rope+attention", LAUNCH_TRY(tmq_launch_attn(aa, s)));
         PROF("attn_output", rc = launch_gemv(m, L.o_l));
         if (rc) return rc;
-        PROF(L.gu_t ? "ffn_norm+gate+up+silu_x_up" : "ffn_norm+gate+up", rc = launch_gemv(m, L.gu));
+        PROF(L.fused_gu ? "ffn_norm+gate+up+silu_x_up" : "ffn_norm+gate+up", rc = launch_gemv(m, L.gu));
         if (rc) return rc;
-        if (!L.gu_t)
+        if (!L.fused_gu)
             PROF("silu_x_up", LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s)));
         PROF("ffn_down", rc = launch_gemv(m, L.dn));
         if (rc) return rc;
@@ -670,6 +673,194 @@ int pf_prompt(tmq_model* m, int n, int* done) {
 }
 
 // ------------------------------------------------------------------ build
+// The launch lists of one decode step under the model's flags (the
+// reference's command-line globals, sim/tmac_gguf.cpp:2085-2091): every
+// projection takes the branch `matmul` takes for its tensor type
+// (:473-493, tmq_route) -- its own quantized kernel, the INT16 fallback or
+// the FP32 loop -- and the logits are get_logits_q8 under --fpga-q8, else
+// get_logits, i.e. `matmul` of token_embd (:1852-1866, :2033-2037).
+int build_launches(tmq_model* m) {
+    const tmq_model_config& c = m->cfg;
+    const int L = c.n_layers, H = c.hidden, I = c.inter;
+    const uint32_t flags = m->flags;
+    auto path_of = [&](const tmq_tensor* t) {
+        const int p = tmq_route((uint32_t)t->dev.type, flags);
+        return p == TMQ_PATH_INT16 ? (int)TMQ_WPATH_INT16 : p == TMQ_PATH_FP32 ? (int)TMQ_WPATH_FP32 : (int)TMQ_WPATH_FPGA;
+    };
+    const int logits_path = (flags & TMQ_FLAG_Q8_0) ? (int)TMQ_WPATH_FPGA : path_of(m->emb);
+    // INT16 weights of every tensor routed there, built once per tensor
+    int rc = 0;
+    for (Layer& Y : m->layers)
+        for (tmq_tensor* t : {Y.q, Y.k, Y.v, Y.o, Y.gate, Y.up, Y.down})
+            if (path_of(t) == TMQ_WPATH_INT16 && (rc = tmq_rt_prepare_int16(m->ctx, t))) return rc;
+    if (logits_path == TMQ_WPATH_INT16 && (rc = tmq_rt_prepare_int16(m->ctx, m->emb))) return rc;
+
+    // accumulator slots of this flag set (FP32 rows hold final floats)
+    auto slot = [&](const tmq_tensor* t) -> size_t {
+        const int p = path_of(t);
+        const size_t n = (p == TMQ_WPATH_FPGA && t->dev.type != TMQ_TYPE_Q8_0) || p == TMQ_WPATH_FP32
+                             ? (size_t)t->dev.rows
+                             : (size_t)t->dev.rows * ((t->dev.cols + 63) / 64);
+        return (n + 31) & ~(size_t)31;
+    };
+    std::vector<size_t> acc_off(L);
+    size_t acc_n = 0;
+    for (int l = 0; l < L; l++) {
+        const Layer& Y = m->layers[l];
+        acc_off[l] = acc_n;
+        for (const tmq_tensor* t : {Y.q, Y.k, Y.v, Y.o, Y.gate, Y.up, Y.down}) acc_n += slot(t);
+    }
+    if (acc_n + L > m->kacc_cap) return tmq_fail(TMQ_ERR_HIP, "accumulator layout exceeds its buffer");
+    m->kacc_n = acc_n + L;  // + one max slot per layer
+    m->max_bits = (uint32_t*)(m->kacc + acc_n);  // slot l at byte 8*l: every other u32
+    auto fv_ptr = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
+
+    // Work lists.  Every launch is one engine GEMV: per layer qkv / o /
+    // gate+up / down, each split over K (kc workgroups per 64-row group) into
+    // int64 accumulators that the next launch finalises; then the logits
+    // (one wave per 64 rows, direct).  The INT16 and FP32 branches run in
+    // 4-wave launches; FP32 rows are not split (their sums are sequential).
+    // (attn_output over 14 K chunks: 196 workgroups, 0.45 % faster per step than 7)
+    const int kc_qkv = env_int("TMQ_KC_QKV", 7), kc_o = env_int("TMQ_KC_O", 14);
+    const int kc_gu = env_int("TMQ_KC_GU", 1), kc_dn = env_int("TMQ_KC_DN", 19);
+    auto nw_env = [](const char* n, int d) { return env_int(n, d) == 4 ? 4 : env_int(n, d) == 16 ? 16 : d; };
+    const int nw_qkv = nw_env("TMQ_NW_QKV", 4), nw_o = nw_env("TMQ_NW_O", 4);
+    const int nw_gu = nw_env("TMQ_NW_GU", 16), nw_dn = nw_env("TMQ_NW_DN", 4);
+    auto add_work = [&](Launch& ln, const tmq_tensor* t, int64_t* kacc, float* xs_out, int kc) {
+        TmqWork w = tmq_rt_make_work(t, nullptr, nullptr, nullptr);
+        w.path = path_of(t);
+        const int g64 = t->dev.rows_pad / 64;
+        if (w.path == TMQ_WPATH_FP32) {
+            w.kc = 1;
+            w.y = (float*)kacc;
+            w.ngroups = (g64 + ln.waves - 1) / ln.waves;
+        } else {
+            const int units = (t->dev.type == TMQ_TYPE_Q8_0 || w.path == TMQ_WPATH_INT16)
+                                  ? (t->dev.cols + 63) / 64
+                                  : t->dev.nb * (t->dev.type == TMQ_TYPE_Q5_0 ? 1 : 4);
+            if (kc > units) kc = units;
+            if (kc < 1) kc = 1;
+            w.kc = kc;
+            w.kacc = kacc;
+            w.xs_out = xs_out;
+            w.ngroups = g64 * kc;
+        }
+        w.first_group = ln.P.ngroups;
+        ln.P.ngroups += w.ngroups;
+        ln.P.w[ln.P.nworks++] = w;
+    };
+    auto deferred = [&](const tmq_tensor* t, int64_t* acc, float* xs, const float* bias) {
+        TmqDeferred d{};
+        const int p = path_of(t);
+        d.acc = acc;
+        d.xs = xs;
+        d.bias = bias;
+        if (p == TMQ_WPATH_FP32) {
+            d.val = (const float*)acc;
+            d.row_inv = d.row_scale = (const float*)acc;
+        } else if (p == TMQ_WPATH_INT16) {
+            d.row_inv = d.row_scale = t->dev.rs16;
+            d.ntiles = (t->dev.cols + 63) / 64;
+        } else {
+            d.row_inv = t->dev.row_inv;
+            d.row_scale = t->dev.row_scale;
+            d.ntiles = t->dev.type == TMQ_TYPE_Q8_0 ? (t->dev.cols + 63) / 64 : 0;
+        }
+        return d;
+    };
+    auto recipe = [&](int mode, const float* x, const float* w, int n) {
+        TmqEngAct a{};
+        a.mode = mode;
+        a.n = n;
+        a.x = x;
+        a.w = w;
+        a.eps = c.norm_eps;
+        a.spec_miss = m->spec_miss;
+        a.state = m->state;
+        return a;
+    };
+    auto all_fpga = [&](std::initializer_list<const tmq_tensor*> ts) {
+        for (const tmq_tensor* t : ts)
+            if (path_of(t) != TMQ_WPATH_FPGA) return false;
+        return true;
+    };
+    for (int l = 0; l < L; l++) {
+        Layer& Y = m->layers[l];
+        Y.qkv = Launch{};
+        Y.o_l = Launch{};
+        Y.gu = Launch{};
+        Y.dn = Launch{};
+        int64_t* A = m->kacc + acc_off[l];
+        int64_t *aq = A, *ak = aq + slot(Y.q), *av = ak + slot(Y.k);
+        int64_t *ao = av + slot(Y.v), *ag = ao + slot(Y.o);
+        int64_t *au = ag + slot(Y.gate), *ad = au + slot(Y.up);
+        float* xs = m->xs + 4 * l;
+        Y.dq = deferred(Y.q, aq, xs + 0, fv_ptr(Y.bq));
+        Y.dk = deferred(Y.k, ak, xs + 0, fv_ptr(Y.bk));
+        Y.dv = deferred(Y.v, av, xs + 0, fv_ptr(Y.bv));
+        Y.dout = deferred(Y.o, ao, xs + 1, nullptr);
+        Y.dg = deferred(Y.gate, ag, xs + 2, nullptr);
+        Y.du = deferred(Y.up, au, xs + 2, nullptr);
+        Y.dd = deferred(Y.down, ad, xs + 3, nullptr);
+        if (l == 0) {
+            Y.qkv.P.act = recipe(TMQ_ACT_EMBED_NORM, nullptr, m->fvec + Y.attn_norm, H);
+            Y.qkv.P.act.tokens = m->tokens;
+            Y.qkv.P.act.emb = m->emb->dev;
+        } else {
+            Y.qkv.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[0], m->fvec + Y.attn_norm, H);
+            Y.qkv.P.act.d1 = m->layers[l - 1].dd;
+        }
+        Y.qkv.P.act.hidden_out = m->hid[1];
+        Y.qkv.waves = all_fpga({Y.q, Y.k, Y.v}) ? nw_qkv : 4;
+        add_work(Y.qkv, Y.q, aq, xs + 0, kc_qkv);
+        add_work(Y.qkv, Y.k, ak, nullptr, kc_qkv);
+        add_work(Y.qkv, Y.v, av, nullptr, kc_qkv);
+        Y.o_l.P.act = recipe(TMQ_ACT_PLAIN, m->ctxv, nullptr, H);
+        Y.o_l.waves = all_fpga({Y.o}) ? nw_o : 4;
+        add_work(Y.o_l, Y.o, ao, xs + 1, kc_o);
+        Y.gu.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[1], m->fvec + Y.ffn_norm, H);
+        Y.gu.P.act.d1 = Y.dout;
+        Y.gu.P.act.hidden_out = m->hid[0];
+        Y.fused_gu = Y.gu_t && all_fpga({Y.gate, Y.up});
+        Y.gu.waves = all_fpga({Y.gate, Y.up}) ? nw_gu : 4;
+        if (Y.fused_gu) {
+            add_work(Y.gu, Y.gu_t, nullptr, nullptr, 1);
+            Y.gu.P.w[0].silu = m->silu_x;
+            Y.gu.P.w[0].silu_max = m->max_bits + 2 * l;
+        } else {
+            add_work(Y.gu, Y.gate, ag, xs + 2, kc_gu);
+            add_work(Y.gu, Y.up, au, nullptr, kc_gu);
+        }
+        Y.dn.P.act = recipe(TMQ_ACT_PRESCALED, m->silu_x, nullptr, I);
+        Y.dn.P.act.max_bits = m->max_bits + 2 * l;
+        Y.dn.waves = all_fpga({Y.down}) ? nw_dn : 4;
+        add_work(Y.dn, Y.down, ad, xs + 3, kc_dn);
+    }
+    // logits: the residual stream (hid[0] + the last down projection),
+    // output_norm when present, direct GEMV with argmax candidates
+    m->logits_l = Launch{};
+    m->logits_l.waves = 4;
+    m->logits_l.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[0], m->out_norm >= 0 ? m->fvec + m->out_norm : nullptr, H);
+    m->logits_l.P.act.d1 = m->layers[L - 1].dd;
+    {
+        TmqWork w = tmq_rt_make_work(m->emb, nullptr, m->logits, nullptr);
+        const int g64 = m->emb->dev.rows_pad / 64;
+        w.path = logits_path;
+        w.kc = 1;
+        w.cand = m->cand;
+        w.ngroups = (g64 + m->logits_l.waves - 1) / m->logits_l.waves;
+        w.first_group = 0;
+        m->logits_l.P.w[0] = w;
+        m->logits_l.P.nworks = 1;
+        m->logits_l.P.ngroups = w.ngroups;
+    }
+    // captured step graphs hold the old launches
+    if (m->g_feed) (void)hipGraphExecDestroy(m->g_feed);
+    if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
+    m->g_feed = m->g_decode = nullptr;
+    return 0;
+}
+
 int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     tmq_ctx* ctx = m->ctx;
     std::map<std::string, const Entry*> by;
@@ -791,17 +982,17 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     }
     if ((rc = add_vec("output_norm.weight", H, false, &m->out_norm))) return rc;
 
-    // K-split accumulators per layer: q, k, v (Q8_0: rows x tiles), o, gate,
-    // up, down
-    auto acc_rows = [](const tmq_tensor* t) -> size_t {
-        return t->dev.type == TMQ_TYPE_Q8_0 ? (size_t)t->dev.rows * ((t->dev.cols + 63) / 64) : (size_t)t->dev.rows;
+    // K-split accumulators: per layer q, k, v, o, gate, up, down, each
+    // sized for its largest use (INT16 / Q8_0: rows x 64-column tiles), plus
+    // one max slot per layer; build_launches lays out the slots the current
+    // flags use at the front
+    auto acc_cap = [](const tmq_tensor* t) -> size_t {
+        return (((size_t)t->dev.rows * ((t->dev.cols + 63) / 64)) + 31) & ~(size_t)31;
     };
-    std::vector<size_t> acc_off(L);
-    size_t acc_n = 0;
+    size_t acc_cap_n = 0;
     for (int l = 0; l < L; l++) {
         const Layer& Y = m->layers[l];
-        acc_off[l] = acc_n;
-        for (const tmq_tensor* t : {Y.q, Y.k, Y.v, Y.o, Y.gate, Y.up, Y.down}) acc_n += (acc_rows(t) + 31) & ~(size_t)31;
+        for (const tmq_tensor* t : {Y.q, Y.k, Y.v, Y.o, Y.gate, Y.up, Y.down}) acc_cap_n += acc_cap(t);
     }
     // device buffer layout
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
@@ -822,7 +1013,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     place("cand", 8 * (size_t)n_cand);
     place("dump", 4 * (size_t)H * (L + 1));
     place("xs", 4 * 4 * (size_t)L);
-    place("kacc", 8 * (acc_n + L));
+    place("kacc", 8 * (acc_cap_n + L));
     place("silu", 4 * (size_t)I);
     place("fvec", 4 * fv.size() + 4);
     place("rope", sizeof(float2) * 32 * (size_t)max_seq);
@@ -843,132 +1034,19 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     m->dump = (float*)(B + lay["dump"]);
     m->xs = (float*)(B + lay["xs"]);
     m->kacc = (int64_t*)(B + lay["kacc"]);
-    m->kacc_n = acc_n + L;  // + one max slot per layer
-    m->max_bits = (uint32_t*)(m->kacc + acc_n);  // slot l at byte 8*l: every other u32
+    m->kacc_cap = acc_cap_n + L;
     m->silu_x = (float*)(B + lay["silu"]);
     m->fvec = (float*)(B + lay["fvec"]);
     m->rope = (float2*)(B + lay["rope"]);
     m->kc = (float*)(B + lay["kc"]);
     m->vc = (float*)(B + lay["vc"]);
-    auto fv_ptr = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
 
-    // read before the work lists: every launch's recipe copies it
-    m->spec_miss = env_int("TMQ_SPEC_MISS", 0) != 0;
-    // Work lists.  Every launch is one engine GEMV: per layer qkv / o /
-    // gate+up / down, each split over K (kc workgroups per 64-row group) into
-    // int64 accumulators that the next launch finalises; then the logits
-    // (one Q8_0 wave per 64 rows, direct).
-    // (attn_output over 14 K chunks: 196 workgroups, 0.45 % faster per step than 7)
-    const int kc_qkv = env_int("TMQ_KC_QKV", 7), kc_o = env_int("TMQ_KC_O", 14);
-    const int kc_gu = env_int("TMQ_KC_GU", 1), kc_dn = env_int("TMQ_KC_DN", 19);
-    auto nw_env = [](const char* n, int d) { return env_int(n, d) == 4 ? 4 : env_int(n, d) == 16 ? 16 : d; };
-    const int nw_qkv = nw_env("TMQ_NW_QKV", 4), nw_o = nw_env("TMQ_NW_O", 4);
-    const int nw_gu = nw_env("TMQ_NW_GU", 16), nw_dn = nw_env("TMQ_NW_DN", 4);
-    auto add_work = [&](Launch& ln, const tmq_tensor* t, int64_t* kacc, float* xs_out, int kc) {
-        TmqWork w = tmq_rt_make_work(t, nullptr, nullptr, nullptr);
-        const int g64 = t->dev.rows_pad / 64;
-        const int units = t->dev.type == TMQ_TYPE_Q8_0 ? (t->dev.cols + 63) / 64
-                          : t->dev.nb * (t->dev.type == TMQ_TYPE_Q5_0 ? 1 : 4);
-        if (kc > units) kc = units;
-        if (kc < 1) kc = 1;
-        w.kc = kc;
-        w.kacc = kacc;
-        w.xs_out = xs_out;
-        w.ngroups = g64 * kc;
-        w.first_group = ln.P.ngroups;
-        ln.P.ngroups += w.ngroups;
-        ln.P.w[ln.P.nworks++] = w;
-    };
-    auto deferred = [&](const tmq_tensor* t, int64_t* acc, float* xs, const float* bias) {
-        TmqDeferred d{};
-        d.acc = acc;
-        d.xs = xs;
-        d.row_inv = t->dev.row_inv;
-        d.row_scale = t->dev.row_scale;
-        d.bias = bias;
-        d.ntiles = t->dev.type == TMQ_TYPE_Q8_0 ? (t->dev.cols + 63) / 64 : 0;
-        return d;
-    };
-    auto recipe = [&](int mode, const float* x, const float* w, int n) {
-        TmqEngAct a{};
-        a.mode = mode;
-        a.n = n;
-        a.x = x;
-        a.w = w;
-        a.eps = c.norm_eps;
-        a.spec_miss = m->spec_miss;
-        a.state = m->state;
-        return a;
-    };
-    for (int l = 0; l < L; l++) {
-        Layer& Y = m->layers[l];
-        int64_t* A = m->kacc + acc_off[l];
-        int64_t *aq = A, *ak = aq + ((acc_rows(Y.q) + 31) & ~(size_t)31), *av = ak + ((acc_rows(Y.k) + 31) & ~(size_t)31);
-        int64_t *ao = av + ((acc_rows(Y.v) + 31) & ~(size_t)31), *ag = ao + ((acc_rows(Y.o) + 31) & ~(size_t)31);
-        int64_t *au = ag + ((acc_rows(Y.gate) + 31) & ~(size_t)31), *ad = au + ((acc_rows(Y.up) + 31) & ~(size_t)31);
-        float* xs = m->xs + 4 * l;
-        Y.dq = deferred(Y.q, aq, xs + 0, fv_ptr(Y.bq));
-        Y.dk = deferred(Y.k, ak, xs + 0, fv_ptr(Y.bk));
-        Y.dv = deferred(Y.v, av, xs + 0, fv_ptr(Y.bv));
-        Y.dout = deferred(Y.o, ao, xs + 1, nullptr);
-        Y.dg = deferred(Y.gate, ag, xs + 2, nullptr);
-        Y.du = deferred(Y.up, au, xs + 2, nullptr);
-        Y.dd = deferred(Y.down, ad, xs + 3, nullptr);
-        if (l == 0) {
-            Y.qkv.P.act = recipe(TMQ_ACT_EMBED_NORM, nullptr, m->fvec + Y.attn_norm, H);
-            Y.qkv.P.act.tokens = m->tokens;
-            Y.qkv.P.act.emb = m->emb->dev;
-        } else {
-            Y.qkv.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[0], m->fvec + Y.attn_norm, H);
-            Y.qkv.P.act.d1 = m->layers[l - 1].dd;
-        }
-        Y.qkv.P.act.hidden_out = m->hid[1];
-        Y.qkv.waves = nw_qkv;
-        add_work(Y.qkv, Y.q, aq, xs + 0, kc_qkv);
-        add_work(Y.qkv, Y.k, ak, nullptr, kc_qkv);
-        add_work(Y.qkv, Y.v, av, nullptr, kc_qkv);
-        Y.o_l.P.act = recipe(TMQ_ACT_PLAIN, m->ctxv, nullptr, H);
-        Y.o_l.waves = nw_o;
-        add_work(Y.o_l, Y.o, ao, xs + 1, kc_o);
-        Y.gu.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[1], m->fvec + Y.ffn_norm, H);
-        Y.gu.P.act.d1 = Y.dout;
-        Y.gu.P.act.hidden_out = m->hid[0];
-        Y.gu.waves = nw_gu;
-        if (Y.gu_t) {
-            add_work(Y.gu, Y.gu_t, nullptr, nullptr, 1);
-            Y.gu.P.w[0].silu = m->silu_x;
-            Y.gu.P.w[0].silu_max = m->max_bits + 2 * l;
-        } else {
-            add_work(Y.gu, Y.gate, ag, xs + 2, kc_gu);
-            add_work(Y.gu, Y.up, au, nullptr, kc_gu);
-        }
-        Y.dn.P.act = recipe(TMQ_ACT_PRESCALED, m->silu_x, nullptr, I);
-        Y.dn.P.act.max_bits = m->max_bits + 2 * l;
-        Y.dn.waves = nw_dn;
-        add_work(Y.dn, Y.down, ad, xs + 3, kc_dn);
-    }
-    // logits: the residual stream (hid[0] + the last down projection),
-    // output_norm when present, direct Q8_0 GEMV with argmax candidates
-    m->logits_l.waves = 4;
-    m->logits_l.P.act = recipe(TMQ_ACT_RESID_NORM, m->hid[0], m->out_norm >= 0 ? m->fvec + m->out_norm : nullptr, H);
-    m->logits_l.P.act.d1 = m->layers[L - 1].dd;
-    {
-        TmqWork w = tmq_rt_make_work(m->emb, nullptr, m->logits, nullptr);
-        const int g64 = m->emb->dev.rows_pad / 64;
-        w.kc = 1;
-        w.cand = m->cand;
-        w.ngroups = (g64 + m->logits_l.waves - 1) / m->logits_l.waves;
-        w.first_group = 0;
-        m->logits_l.P.w[0] = w;
-        m->logits_l.P.nworks = 1;
-        m->logits_l.P.ngroups = w.ngroups;
-    }
     hipStream_t s = ctx->stream;
     HIP_TRY(hipMemcpyAsync(m->fvec, fv.data(), 4 * fv.size(), hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemsetAsync(m->xs, 0, 4 * 4 * (size_t)L, s));
     HIP_TRY(hipMemsetAsync(m->hid[0], 0, 4 * (size_t)H, s));
     HIP_TRY(hipMemsetAsync(m->hid[1], 0, 4 * (size_t)H, s));
-    LAUNCH_TRY(tmq_launch_zero_acc(m->kacc, m->kacc_n, s));
+    LAUNCH_TRY(tmq_launch_zero_acc(m->kacc, m->kacc_cap, s));
     HIP_TRY(hipMemsetAsync(m->kc, 0, 4 * (size_t)L * max_seq * KV, s));
     HIP_TRY(hipMemsetAsync(m->vc, 0, 4 * (size_t)L * max_seq * KV, s));
     // RoPE factors exactly as apply_rope forms them (sim/tmac_gguf.cpp:1531-1535)
@@ -979,9 +1057,12 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
     HIP_TRY(hipStreamSynchronize(s));
     m->use_graphs = env_int("TMQ_GRAPHS", 1) != 0;
+    // read before the work lists: every launch's recipe copies it
+    m->spec_miss = env_int("TMQ_SPEC_MISS", 0) != 0;
     m->prefill_chunk = env_int("TMQ_PREFILL", 512);
     m->prefill_off = pf_unsupported(m);
-    return 0;
+    m->flags = TMQ_FLAGS_ALL;
+    return build_launches(m);
 }
 
 int reset(tmq_model* m) {
@@ -1071,7 +1152,8 @@ int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n) {
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(m->tokens, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, m->ctx->stream));
     int done = 0;
-    if (m->prefill_chunk > 0 && !m->prefill_off && n >= 2) {
+    // the batched prefill reproduces the all-flags arithmetic only
+    if (m->prefill_chunk > 0 && !m->prefill_off && m->flags == TMQ_FLAGS_ALL && n >= 2) {
         if ((rc = pf_prompt(m, n, &done))) return rc;
         if (done > 0) {
             TmqEngState st{done - 1, 0, {0, 0}};
@@ -1085,6 +1167,24 @@ int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n) {
     }
     return check_state(m);
 }
+
+int tmq_model_set_flags(tmq_model* m, uint32_t flags) {
+    if (!m) return tmq_fail(TMQ_ERR_ARG, "null model");
+    if (flags & ~TMQ_FLAGS_ALL) return tmq_fail(TMQ_ERR_ARG, "unknown flag bits 0x%x", flags & ~TMQ_FLAGS_ALL);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    const uint32_t old = m->flags;
+    m->flags = flags;
+    rc = build_launches(m);
+    if (rc) {
+        m->flags = old;
+        (void)build_launches(m);
+    }
+    return rc;
+}
+
+uint32_t tmq_model_get_flags(const tmq_model* m) { return m ? m->flags : 0u; }
 
 int tmq_model_set_prefill(tmq_model* m, int chunk) {
     if (!m || chunk < 0) return tmq_fail(TMQ_ERR_ARG, "bad prefill arguments");

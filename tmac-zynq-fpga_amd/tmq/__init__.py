@@ -44,7 +44,7 @@ EXPORTS = [
     "tmq_model_weight_bytes", "tmq_model_position", "tmq_model_set_graphs", "tmq_model_prompt",
     "tmq_model_feed", "tmq_model_feed_dump", "tmq_model_logits", "tmq_model_generate",
     "tmq_model_generate_async", "tmq_model_tokens", "tmq_model_hidden", "tmq_model_set_prefill",
-    "tmq_model_profile",
+    "tmq_model_profile", "tmq_model_set_flags", "tmq_model_get_flags",
 ]
 
 
@@ -133,6 +133,8 @@ def lib(path: str = LIB_PATH):
         "tmq_model_position": (I, [P]),
         "tmq_model_set_graphs": (I, [P, I]),
         "tmq_model_set_prefill": (I, [P, I]),
+        "tmq_model_set_flags": (I, [P, U32]),
+        "tmq_model_get_flags": (U32, [P]),
         "tmq_model_profile": (I, [P, I, P, I, C.POINTER(C.c_int)]),
         "tmq_model_prompt": (I, [P, P, I]),
         "tmq_model_feed": (I, [P, C.c_int32]),
@@ -379,6 +381,15 @@ class Model:
         cnt = C.c_int(0)
         _check(lib().tmq_model_profile(self.handle, n, C.cast(buf, C.c_void_p), n * per, C.byref(cnt)))
         return [(buf[i].name.decode(), buf[i].start_ms, buf[i].end_ms) for i in range(cnt.value)]
+
+    def set_flags(self, flags: int):
+        """the reference's --fpga* flags (FLAG_*): per-type matmul routing and
+        get_logits_q8 vs get_logits"""
+        _check(lib().tmq_model_set_flags(self.handle, int(flags)))
+
+    @property
+    def flags(self) -> int:
+        return lib().tmq_model_get_flags(self.handle)
 
     def set_prefill(self, chunk: int):
         """0: prompts one token at a time; > 0: batched prefill in chunks of
