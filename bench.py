@@ -5,16 +5,21 @@ Workload: the Q5_0 batch-1 projections of
 Qwen2-0.5B -- attn_q 896x896 run as one descriptor with num_tiles=224 and
 tile_res_rows=4, ffn_gate and ffn_up 4864x896 -- on a seeded N(0,1) fp32
 activation.  The three tensors are replicated over enough distinct weight
-sets that one step streams more than the 256 MiB Infinity Cache (42 sets,
-275 MB); a step is one pass of the descriptor chain over all of them: one
+sets that one step streams twice the 256 MiB Infinity Cache (84 sets,
+550 MB); a step is one pass of the descriptor chain over all of them: one
 activation-quantisation launch plus one launch of every GEMV.
 
 value  = ggml weight bytes streamed per step / step time  (GB/s)
-roofline.achieved = the same bytes / average duration of the GEMV launch
-         alone (HIP events on the library's stream), against 8 TB/s.
+roofline.achieved = the same bytes / average duration of the GEMV launch,
+         bracketed by HIP events on the library's stream inside the timed
+         steps themselves (so kernel_ms <= ms_per_step), against 8 TB/s.
 cpu_baseline = the reference's own matmul_fpga_q5_0 (sim/tmac_gguf.cpp:1221,
          compiled in place into oracle/_ref) or, where that was not built, its
-         C restatement, on one host core over the same shapes.
+         C restatement, on one host core over the same shapes; beside it the
+         reference's no-flag FP32 loop (:488-492) on the same shapes, the
+         host's core count and CPU model.
+Weight sets are cycled to twice the 256 MiB Infinity Cache by default
+(--sets-sweep measures 1x, 2x and 4x).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -34,7 +39,8 @@ sys.path.insert(0, PKG)
 
 PEAK_GBPS = 8000.0  # MI355X HBM3E, datasheet
 METRIC = "quant GEMV weight GB/s (% HBM peak); Qwen2-0.5B batch-1 decode tok/s"
-SETS = 42           # 42 x (551936 + 2 x 2996224) B = 274.9 MB > 256 MiB
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+MALL_FACTOR = 2.0       # default working set: twice the Infinity Cache
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chain_q5_0_c2_traffic.txt")
 
 
@@ -42,24 +48,34 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-# name -> (description, [(qtype, rows, cols, num_tiles, tile_res_rows, num_col_groups)], copies, x len)
+# name -> (description, [(qtype, rows, cols, num_tiles, tile_res_rows, num_col_groups)], x len)
 WORKLOADS = {
     "c2": ("BASELINE configs[1]: Q5_0 attn_q 896x896 (1 descriptor, num_tiles=224, tile_res_rows=4) "
            "+ ffn_gate/ffn_up 4864x896, batch 1",
-           [(6, 896, 896, 224, 4, 1), (6, 4864, 896, 1216, 4, 1), (6, 4864, 896, 1216, 4, 1)], SETS, 896),
+           [(6, 896, 896, 224, 4, 1), (6, 4864, 896, 1216, 4, 1), (6, 4864, 896, 1216, 4, 1)], 896),
     "c1": ("BASELINE configs[0]: Q8_0 logits 151936x896 (num_tiles=2374 64-row tiles), batch 1",
-           [(8, 151936, 896, 2374, 64, 14)], 3, 896),
+           [(8, 151936, 896, 2374, 64, 14)], 896),
     "c3q4k": ("BASELINE configs[2]: Q4_K ffn_down 896x4864 (56-row tiles, 19 column groups), batch 1",
-              [(12, 896, 4864, 304, 56, 19)], 111, 4864),
+              [(12, 896, 4864, 304, 56, 19)], 4864),
     "c3q6k": ("BASELINE configs[2]: Q6_K ffn_down 896x4864 (32-row tiles, 19 column groups), batch 1",
-              [(14, 896, 4864, 532, 32, 19)], 77, 4864),
+              [(14, 896, 4864, 532, 32, 19)], 4864),
 }
+BLOCK = {6: (32, 22), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+
+
+def set_bytes(name):
+    return sum(r * (c // BLOCK[qt][0]) * BLOCK[qt][1] for qt, r, c, *_ in WORKLOADS[name][1])
+
+
+def copies_for(name, factor=MALL_FACTOR):
+    """distinct weight sets whose total exceeds factor x the Infinity Cache"""
+    return int(factor * MALL_BYTES // set_bytes(name)) + 1
 
 
 def build_workload(ctx, torch, dev, name, copies=None):
     from tmq import synth
-    desc_txt, shapes, ncopies, n = WORKLOADS[name]
-    copies = copies or ncopies
+    desc_txt, shapes, n = WORKLOADS[name]
+    copies = copies or copies_for(name)
     x = synth.gen_x(n, 12345)
     x_d = torch.from_numpy(x).to(dev)
     tensors, descs, ys = [], [], []
@@ -98,8 +114,22 @@ def read_traffic():
     return None
 
 
+def host_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
 def cpu_baseline(seconds):
-    """Reference CPU path on one core, bounded sample of the same workload."""
+    """Reference CPU path on one core, bounded sample of the same workload:
+    (i) the --fpga-q5-0 integer path (matmul_fpga_q5_0) and (ii) the no-flag
+    FP32 loop of matmul (sim/tmac_gguf.cpp:488-492), each ~seconds."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, Reference
     from tmq import synth
@@ -108,45 +138,65 @@ def cpu_baseline(seconds):
     x = synth.gen_x(896, 12345)
     ws = [(synth.gen_weights(qt, r, c, seed=k), r, c) for k, (qt, r, c, *_) in enumerate(WORKLOADS["c2"][1])]
     nbytes = sum(w.size for w, _, _ in ws)
-    done, t0 = 0, time.perf_counter()
-    while True:
-        for w, r, c in ws:
-            impl.matmul(6, w, x, r, c)
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+
+    def run(fn):
+        done, t0 = 0, time.perf_counter()
+        while True:
+            for w, r, c in ws:
+                fn(6, w, x, r, c)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return done, el
+
+    done, el = run(impl.matmul)
+    done32, el32 = run(impl.matmul_fp32)
     gbps = done * nbytes / el / 1e9
     name = "sim matmul_fpga_q5_0 (compiled reference)" if kind == "reference" else "C restatement of matmul_fpga_q5_0"
-    return {"value": round(gbps, 5), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{name} over attn_q 896x896 + ffn_gate/ffn_up 4864x896 "
-                      f"({nbytes} weight bytes) x {done} passes = {el:.1f} s on one host thread, "
-                      f"per-call row scan included as in the reference"}
+    out = {"value": round(gbps, 5), "unit": "GB/s", "cores": 1, "kind": kind,
+           "sample": f"{name} over attn_q 896x896 + ffn_gate/ffn_up 4864x896 "
+                     f"({nbytes} weight bytes) x {done} passes = {el:.1f} s on one host thread, "
+                     f"per-call row scan included as in the reference",
+           "fp32_path": {"value": round(done32 * nbytes / el32 / 1e9, 5), "unit": "GB/s", "cores": 1,
+                         "sample": f"the no-flag FP32 loop of matmul (sim/tmac_gguf.cpp:488-492) on the same "
+                                   f"shapes x {done32} passes = {el32:.1f} s on one host thread"}}
+    out.update(host_info())
+    return out
 
 
 def measure(ctx, torch, dev, stream, name, steps, warmup, copies=None):
-    """Returns (desc, weight bytes, step ms, kernel-only ms, n descriptors)."""
+    """Returns (desc, weight bytes, step ms, kernel ms, n descriptors, copies).
+    A step = the activation-quantisation launch + the chain's GEMV launch;
+    the GEMV launch of every timed step is bracketed by its own HIP events,
+    so the kernel time is measured in the same warmed state as the step."""
+    copies = copies or copies_for(name)
     desc_txt, x_d, tensors, descs, ys = build_workload(ctx, torch, dev, name, copies)
     chain = ctx.chain(descs)
     wbytes = chain.weight_bytes
-    log(f"{name}: {len(descs)} descriptors, {wbytes} weight bytes per step")
+    log(f"{name}: {len(descs)} descriptors ({copies} weight sets), {wbytes} weight bytes per step")
     for _ in range(warmup):
         chain.run()
     ctx.sync()
     torch.cuda.synchronize()
-    step_ms = time_events(torch, stream, chain.run, steps)
-    ctx.sync()
-    chain.prepare()
-    ctx.sync()
-    for _ in range(warmup // 4):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for a, b in ev:
+        chain.prepare()
+        a.record(stream)
         chain.launch()
-    kern_ms = time_events(torch, stream, chain.launch, steps)
+        b.record(stream)
+    e1.record(stream)
+    e1.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
     ctx.sync()
     torch.cuda.synchronize()
     chain.free()
     for t in tensors:
         t.free()
-    return desc_txt, wbytes, step_ms, kern_ms, len(descs)
+    return desc_txt, wbytes, step_ms, kern_ms, len(descs), copies
 
 
 def single_launch_us(ctx, torch, dev, stream, steps):
@@ -278,7 +328,9 @@ def main():
                     help="untimed steps first (default: 400 chain launches, 8 tokens, 1 prefill)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--sets", type=int, default=SETS)
+    ap.add_argument("--sets", type=int, default=None, help="weight sets of the c2 chain (default: 2x the MALL)")
+    ap.add_argument("--sets-sweep", action="store_true",
+                    help="GEMV GB/s at working sets of 1x, 2x and 4x the Infinity Cache (c2, c3q4k, c3q6k, c1)")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + ["c4", "c5"],
                     help="c4: only the full-model greedy decode (BASELINE configs[3]); "
@@ -341,8 +393,20 @@ def main():
                "extra": {"c5_prefill": pf}, "cpu_baseline": cpu}
         print(json.dumps(out), flush=True)
         return
+    if args.sets_sweep:
+        for name in ("c2", "c3q4k", "c3q6k", "c1"):
+            for f in (1.0, 2.0, 4.0):
+                n = copies_for(name, f)
+                _, wb, sm, km, nd, _ = measure(ctx, torch, dev, stream, name, args.steps, args.warmup, n)
+                print(json.dumps({"sweep": name, "mall_factor": f, "sets": n, "weight_bytes": wb,
+                                  "ms_per_step": round(sm, 5), "kernel_ms": round(km, 5),
+                                  "step_gbps": round(wb / (sm * 1e-3) / 1e9, 2),
+                                  "kernel_gbps": round(wb / (km * 1e-3) / 1e9, 2)}), flush=True)
+        ctx.close()
+        return
     copies = args.sets if wl == "c2" else None
-    desc_txt, wbytes, step_ms, kern_ms, ndesc = measure(ctx, torch, dev, stream, wl, args.steps, args.warmup, copies)
+    desc_txt, wbytes, step_ms, kern_ms, ndesc, copies = measure(ctx, torch, dev, stream, wl, args.steps,
+                                                                args.warmup, copies)
     value = wbytes / (step_ms * 1e-3) / 1e9
     achieved = wbytes / (kern_ms * 1e-3) / 1e9
     traffic = read_traffic() if wl == "c2" else None
@@ -360,7 +424,8 @@ def main():
         "dtype": "int16",
         "data": "synthetic (seeded ggml blocks as BASELINE.json specifies per format; x ~ N(0,1))",
         "config": {
-            "workload": f"{desc_txt}; weight sets cycled ({wbytes} B > 256 MiB), one chain launch per step",
+            "workload": f"{desc_txt}; {copies} weight sets cycled ({wbytes} B, "
+                        f"{wbytes / MALL_BYTES:.2f}x the 256 MiB Infinity Cache), one chain launch per step",
             "descriptors_per_step": ndesc,
             "weight_bytes_per_step": wbytes,
             "pct_hbm_peak": round(100.0 * value / PEAK_GBPS, 2),
@@ -379,9 +444,9 @@ def main():
     if not args.no_extra and wl == "c2":
         extra = {}
         for name in ("c1", "c3q4k", "c3q6k"):
-            _, wb, sm, km, nd = measure(ctx, torch, dev, stream, name, max(10, args.steps // 2), args.warmup)
-            extra[name] = {"weight_bytes": wb, "descriptors": nd, "ms_per_launch": round(km, 5),
-                           "gbps": round(wb / (km * 1e-3) / 1e9, 2),
+            _, wb, sm, km, nd, nc = measure(ctx, torch, dev, stream, name, max(10, args.steps // 2), args.warmup)
+            extra[name] = {"weight_bytes": wb, "descriptors": nd, "weight_sets": nc, "ms_per_launch": round(km, 5),
+                           "ms_per_step": round(sm, 5), "gbps": round(wb / (km * 1e-3) / 1e9, 2),
                            "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
         extra["c2_attn_q_single_launch_us"] = round(single_launch_us(ctx, torch, dev, stream, 50), 2)
         extra["c4_decode"] = decode_bench(ctx, torch, stream)

@@ -156,6 +156,15 @@ int tmq_gemv_partials_path(tmq_ctx* ctx, const tmq_tensor* t, int path, const fl
 /* builds the INT16 path's rounded weights now (otherwise on first use) */
 int tmq_tensor_prepare_int16(tmq_ctx* ctx, tmq_tensor* t);
 
+/* The activation quantisation every matmul_fpga_* performs first
+ * (sim/tmac_gguf.cpp:955-961, :1101-1107, :1225-1231, :1371-1377), on the
+ * GPU: host x[n] in, host xq[n] and *x_scale out (either may be NULL). */
+int tmq_quantize_act(tmq_ctx* ctx, const float* x, int n, int16_t* xq, float* x_scale);
+/* The UQ8.8 combined scale matmul_fpga_q8 forms for every (row, 32-column
+ * block) of a Q8_0 tensor (sim/tmac_gguf.cpp:1022-1039), on the GPU:
+ * out[r * (cols/32) + b]. */
+int tmq_tensor_q8_scales(tmq_ctx* ctx, const tmq_tensor* t, uint16_t* out);
+
 /* Device-pointer, stream-ordered form of tmq_matmul: x_dev fp32[cols],
  * y_dev fp32[rows] (may be NULL), acc_dev optional int64 partials: per row
  * (Q5_0/K-quants) or per row and 64-column tile, [rows][ceil(cols/64)]
@@ -296,11 +305,27 @@ uint32_t tmq_model_get_flags(const tmq_model* m);
  * token at a time like process_prompt (:1992-1997).  Fails if the model's
  * shapes or formats do not fit the batched kernels. */
 int tmq_model_set_prefill(tmq_model* m, int chunk);
+/* reset_cache (:1951-1955): the next fed token is position 0 */
+int tmq_model_reset(tmq_model* m);
 /* process_embedding + forward_all_layers of one more token (:1958-1972) */
 int tmq_model_feed(tmq_model* m, int32_t token);
 /* as tmq_model_feed, also returning the hidden state after the embedding
  * and after every layer ((n_layers+1) x hidden floats; --dump-layers, :2001-2018) */
 int tmq_model_feed_dump(tmq_model* m, int32_t token, float* layers_out);
+/* as tmq_model_feed, also returning the fp32 input of every matmul of the
+ * position, per layer l at acts_out + l*(3*hidden + ffn): the attn_norm
+ * output (attn_q/k/v), the attention context (attn_output), the ffn_norm
+ * output (ffn_gate/up) and SiLU(gate)*up (ffn_down) -- what the reference's
+ * matmul calls of forward_layer_with_cache receive (:1583-1707).  Used to
+ * rebuild the reference's per-matmul artefacts (PhaseB chains, tile dumps). */
+int tmq_model_feed_capture(tmq_model* m, int32_t token, float* acts_out);
+/* get_logits_q8 / get_logits of the last processed position as
+ * tmq_model_logits (logits may be NULL), also returning the fp32 input of
+ * the logits matmul (the output_norm of the residual stream, hidden floats) */
+int tmq_model_logits_capture(tmq_model* m, float* logits, float* x_out);
+/* the uploaded tensor of a matmul weight by its .tmac name
+ * ("token_embd.weight", "blk.N.attn_q.weight", ...); NULL if absent */
+const tmq_tensor* tmq_model_tensor(const tmq_model* m, const char* name);
 /* get_logits_q8 (:1820-1845) of the last processed position -> vocab floats */
 int tmq_model_logits(tmq_model* m, float* logits);
 /* generate (:2025-2045) with greedy choice: n x (logits, argmax, feed);

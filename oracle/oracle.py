@@ -166,6 +166,10 @@ class Reference:
         _setup(L, "ref_matmul_fp32", None, [_u32, _P, _u64, _i, _i, _P, _P])
         _setup(L, "ref_matmul_int16", None, [_u32, _P, _u64, _i, _i, _P, _P])
         _setup(L, "ref_model_set_flags", None, [C.c_uint])
+        _setup(L, "ref_dump_tiles_open", _i, [_i, _i, C.c_char_p])
+        _setup(L, "ref_dump_tiles_close", None, [])
+        _setup(L, "ref_phaseb_verify", _i, [])
+        _setup(L, "ref_phaseb_dump_files", None, [])
         _setup(L, "ref_model_logits_auto", None, [_P, _P])
         _setup(L, "ref_tile_q8", None, [_P, _P, _P, _P])
         _setup(L, "ref_tile_q5_0_8x896", None, [_P, _P, _P, _P, _i])
@@ -181,6 +185,9 @@ class Reference:
         _setup(L, "ref_phaseb_count", _i, [])
         _setup(L, "ref_ddr", _P, [])
         _setup(L, "ref_phaseb_run", _i, [_u32, _P])
+        _setup(L, "ref_phaseb_alloc", _u32, [_u32])
+        _setup(L, "ref_phaseb_add_descriptor", _u32,
+               [_u32, _u32, _u32, C.c_uint16, C.c_uint16, C.c_uint8, C.c_uint8, C.c_uint8, C.c_uint16, C.c_uint8])
         _setup(L, "ref_model_load", _i, [C.c_char_p])
         _setup(L, "ref_model_prompt", _i, [_P, _i, _P])
         _setup(L, "ref_model_reset", None, [])

@@ -107,11 +107,34 @@ uint32_t ref_phaseb_next_off(void) { return g_phaseb.next_off; }
 int ref_phaseb_count(void) { return (int)g_phaseb.slots.size(); }
 const uint8_t* ref_ddr(void) { return g_ddr; }
 int ref_phaseb_run(uint32_t desc_off, int64_t* acc) { return phaseb_run_descriptor(desc_off, acc); }
+uint32_t ref_phaseb_alloc(uint32_t bytes) { return phaseb_alloc(bytes); }
 uint32_t ref_phaseb_add_descriptor(uint32_t w, uint32_t a, uint32_t r, uint16_t nt, uint16_t tb,
                                    uint8_t type, uint8_t trr, uint8_t flags, uint16_t atb,
                                    uint8_t ncg) {
     return phaseb_add_descriptor(w, a, r, nt, tb, type, trr, flags, atb, ncg);
 }
+
+// Cosimulation tile dumps as main() opens them (sim/tmac_gguf.cpp:2095-2130):
+// which 0 = --dump-tiles (Q8), 1 = --dump-tiles-q5-0, 2 = --dump-tiles-q6-k
+int ref_dump_tiles_open(int which, int n, const char* path) {
+    FILE* f = fopen(path, "wb");
+    if (!f) return -1;
+    uint32_t header[4] = {(uint32_t)n, 0, 0, 0};
+    fwrite(header, 4, 4, f);
+    if (which == 0) { g_dump_file = f; g_dump_tiles_remaining = n; }
+    else if (which == 1) { g_dump_q5_0_file = f; g_dump_q5_0_tiles_remaining = n; }
+    else { g_dump_q6k_file = f; g_dump_q6k_tiles_remaining = n; }
+    return 0;
+}
+void ref_dump_tiles_close(void) {
+    for (FILE** f : {&g_dump_file, &g_dump_q5_0_file, &g_dump_q6k_file})
+        if (*f) { fclose(*f); *f = nullptr; }
+    g_dump_tiles_remaining = g_dump_q5_0_tiles_remaining = g_dump_q6k_tiles_remaining = 0;
+}
+// phaseb_verify (:834-880) and phaseb_dump_files (:609-708, writes
+// /tmp/tb_phaseb.bin and /tmp/tb_phaseb.hdr)
+int ref_phaseb_verify(void) { return phaseb_verify(); }
+void ref_phaseb_dump_files(void) { phaseb_dump_files(); }
 
 // Whole-model engine, run as `tmac_gguf model.tmac --fpga-q8 --fpga-q5-0
 // --fpga-q4k --fpga-q6-k` would (sim/tmac_gguf.cpp:2066-2091): load_tmac

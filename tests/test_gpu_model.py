@@ -8,6 +8,7 @@ where the engine's logf (fp64 log rounded once) differs from the host libm's
 logf by one ulp, so they are checked to 1e-5 relative and the bit-exact
 fraction is reported.
 """
+import json
 import os
 
 import numpy as np
@@ -201,6 +202,49 @@ def test_cli(golden, tmp_path):
         d = np.fromfile(tmp_path / f"cpp_layer_{l}.bin", dtype=np.float32)
         assert d.shape == exp[l].shape
         assert np.abs(d - exp[l]).max() <= 1e-5 * np.abs(exp[l]).max(), f"layer {l}"
+
+
+def test_cli_cosim(golden, tmp_path):
+    """tmq_gguf --fpga-phaseb --dump-phaseb --dump-tiles 4 --dump-tiles-q5-0 3
+    --dump-tiles-q6-k 3 on a one-token prompt against the compiled
+    reference's run (tests/golden/cosim.npz): the Q8_0 dump byte for byte;
+    the Q5_0 and Q6_K dumps byte for byte in every field but the results of
+    the tiles after the first, which carry the values the reference's
+    overflowing result array loses (q5_fixed, q6_fixed); tb_phaseb.bin and
+    .hdr identical (sha256); the same verification outcome."""
+    import hashlib
+    import subprocess
+    from conftest import PKG
+    from tmq import model_synth, tmacfile
+    gc = load_golden("cosim.npz")
+    exe = os.path.join(PKG, "tmq", "tmq_gguf")
+    path = tmp_path / "c4.tmac"
+    tmacfile.write(path, model_synth.gen_model(int(gc["model_seed"])))
+    out = tmp_path / "cosim"
+    out.mkdir()
+    print("[model] CLI with --fpga-phaseb and the tile dumps", flush=True)
+    r = subprocess.run([exe, str(path), "--fpga-phaseb", "--dump-phaseb", "--dump-tiles", "4", "--dump-tiles-q5-0", "3",
+                        "--dump-tiles-q6-k", "3", "--cosim-dir", str(out)], input=f"{int(gc['prompt'][0])}\n",
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-3000:]
+    assert [t["id"] for t in json.loads(r.stdout)] == golden["top_ids"][0].tolist()
+    assert f"156 descriptors verified, {int(gc['phaseb_errors'])} errors" in r.stderr
+    q8 = np.fromfile(out / "cosim_tiles.bin", dtype=np.uint8)
+    assert np.array_equal(q8, gc["q8"])
+    for k, rec, res_off, fixed in (("q5", 6816, 6752, gc["q5_fixed"]), ("q6", 7616, 7360, gc["q6_fixed"])):
+        fn = "cosim_tiles_q5_0.bin" if k == "q5" else "cosim_tiles_q6_k.bin"
+        got, exp = np.fromfile(out / fn, dtype=np.uint8), gc[k]
+        assert got.size == exp.size and np.array_equal(got[:16 + rec], exp[:16 + rec])
+        for t in range(1, 3):
+            a, b = got[16 + t * rec: 16 + (t + 1) * rec], exp[16 + t * rec: 16 + (t + 1) * rec]
+            assert np.array_equal(a[:res_off], b[:res_off]), f"{k} tile {t}"
+            assert np.array_equal(a[res_off:].view(np.int64), fixed[t]), f"{k} tile {t} results"
+    for name, key in (("tb_phaseb.bin", "bin"), ("tb_phaseb.hdr", "hdr")):
+        data = (out / name).read_bytes()
+        assert len(data) == int(gc[f"{key}_size"])
+        if key == "hdr":
+            assert np.array_equal(np.frombuffer(data[:gc["hdr_head"].size], np.uint8), gc["hdr_head"])
+        assert hashlib.sha256(data).hexdigest() == str(gc[f"{key}_sha256"]), name
 
 
 def test_profile(model, golden):

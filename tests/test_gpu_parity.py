@@ -179,6 +179,20 @@ def test_golden_phaseb(ctx):
     assert np.array_equal(np.concatenate(got), g["acc"])
 
 
+def test_golden_phaseb_chain(ctx):
+    """the compiled reference's in-order replay of a chain with matmul, OP->OP
+    (activation = the previous result slot), CPU_OP, Q8_0 and mixed-row_inv
+    Q6_K descriptors (tests/golden/phaseb_chain.npz): the arena after
+    tmq_phaseb_run equals the reference's byte for byte"""
+    g = load_golden("phaseb_chain.npz")
+    arena = g["arena"].copy()
+    print("[phaseb] chain with OP->OP / CPU_OP / Q8_0 / mixed row_inv", flush=True)
+    n, rows = ctx.phaseb_run(arena, int(g["base"]), int(g["head"]))
+    assert n == len(g["rows"]) and list(rows) == g["rows"].tolist()
+    bad = np.flatnonzero(arena != g["arena_after"])
+    assert bad.size == 0, f"{bad.size} bytes differ, first at offset {bad[:4]}"
+
+
 def test_chain_matches_single_gemvs(ctx, oracle):
     """A device chain (one launch) over mixed formats equals per-GEMV results."""
     torch = pytest.importorskip("torch")

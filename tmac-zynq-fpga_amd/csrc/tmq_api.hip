@@ -585,6 +585,41 @@ int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int 
     return 0;
 }
 
+int tmq_quantize_act(tmq_ctx* ctx, const float* x, int n, int16_t* xq, float* x_scale) {
+    if (!ctx || !x || n <= 0 || n % 2) return tmq_fail(TMQ_ERR_ARG, "bad activation arguments");
+    int rc = tmq_rt_set_device(ctx);
+    if (!rc) rc = ctx->x.ensure(sizeof(float) * n);
+    if (!rc) rc = ctx->act.ensure(tmq_act_bytes(n));
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->x.p, x, sizeof(float) * n, hipMemcpyHostToDevice, ctx->stream));
+    TmqActJobs jobs{};
+    jobs.count = 1;
+    jobs.j[0].x = (const float*)ctx->x.p;
+    jobs.j[0].act = (uint8_t*)ctx->act.p;
+    jobs.j[0].n = n;
+    LAUNCH_TRY(tmq_launch_act_prep(jobs, ctx->stream));
+    // layout of the prepared activation: x_scale at 0, int16 values at 16 + 4n
+    if (x_scale) HIP_TRY(hipMemcpyAsync(x_scale, ctx->act.p, sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    if (xq)
+        HIP_TRY(hipMemcpyAsync(xq, (const uint8_t*)ctx->act.p + 16 + 4 * (size_t)n, sizeof(int16_t) * n,
+                               hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int tmq_tensor_q8_scales(tmq_ctx* ctx, const tmq_tensor* t, uint16_t* out) {
+    if (!ctx || !t || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (t->dev.type != TMQ_TYPE_Q8_0) return tmq_fail(TMQ_ERR_ARG, "not a Q8_0 tensor");
+    int rc = tmq_rt_set_device(ctx);
+    const size_t n = (size_t)t->dev.rows * t->dev.nb;
+    if (!rc) rc = ctx->misc.ensure(sizeof(uint16_t) * n);
+    if (rc) return rc;
+    LAUNCH_TRY(tmq_launch_q8_scales(t->dev, (uint16_t*)ctx->misc.p, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(out, ctx->misc.p, sizeof(uint16_t) * n, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
 int tmq_route(uint32_t type, uint32_t flags) {
     if (!qk_of(type)) return tmq_fail(TMQ_ERR_ARG, "unsupported tensor type %u", type);
     if (!(flags & TMQ_FLAG_FPGA)) return TMQ_PATH_FP32;
@@ -890,8 +925,85 @@ uint64_t tmq_chain_weight_bytes(const tmq_chain* ch) { return ch ? ch->weight_by
 
 // ---------------------------------------------------------------- PhaseB
 // Walks the chain on the host (descriptors are 32 bytes each), rebuilds
-// each matmul descriptor's weights as a device tensor and runs all of them
-// in one chain launch; results land in the arena at result_addr.
+// each matmul descriptor's weights as device tensors and runs them in chain
+// launches; results land in the arena at result_addr, as phaseb_verify
+// writes them (sim/tmac_gguf.cpp:851-852).  Descriptors run in chain order
+// as far as the hardware would see: one whose activation or weights read a
+// result range still pending (an OP->OP chain, :551-561) first waits for
+// the pending ones to land in the arena.
+namespace {
+struct PbPart {
+    tmq_tensor* t = nullptr;
+    std::vector<uint8_t> act;
+};
+struct PbItem {
+    std::vector<PbPart> parts;  // one tensor, or one per column group
+    uint32_t result_addr = 0;
+    int nrows = 0;
+    bool kquant = false;
+};
+void pb_free(std::vector<PbItem>& items) {
+    for (PbItem& it : items)
+        for (PbPart& p : it.parts) tmq_tensor_free(p.t);
+    items.clear();
+}
+// every pending descriptor in one launch per format, results into the arena
+int pb_flush(tmq_ctx* ctx, std::vector<PbItem>& items, uint8_t* arena, uint32_t arena_base) {
+    if (items.empty()) return 0;
+    size_t act_total = 0, acc_total = 0;
+    std::vector<size_t> aoff, coff;
+    for (PbItem& it : items)
+        for (PbPart& p : it.parts) {
+            aoff.push_back(act_total);
+            act_total += (p.act.size() + 255) & ~(size_t)255;
+            coff.push_back(acc_total);
+            acc_total += (size_t)p.t->dev.rows;
+        }
+    int rc = ctx->act.ensure(act_total);
+    if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * acc_total);
+    if (rc) return rc;
+    std::vector<TmqWork> works;
+    std::vector<int32_t> gmap;
+    std::vector<Segment> segs;
+    size_t k = 0;
+    for (PbItem& it : items)
+        for (PbPart& p : it.parts) {
+            HIP_TRY(hipMemcpyAsync((uint8_t*)ctx->act.p + aoff[k], p.act.data(), p.act.size(), hipMemcpyHostToDevice,
+                                   ctx->stream));
+            works.push_back(make_work(p.t, (const uint8_t*)ctx->act.p + aoff[k], nullptr, (int64_t*)ctx->acc.p + coff[k]));
+            k++;
+        }
+    plan_segments(works, gmap, segs);
+    rc = ctx->works.ensure(sizeof(TmqWork) * works.size());
+    if (!rc) rc = ctx->gmap.ensure(sizeof(int32_t) * gmap.size());
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->works.p, works.data(), sizeof(TmqWork) * works.size(), hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(ctx->gmap.p, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice, ctx->stream));
+    rc = launch_segments(segs, ctx->works.p, ctx->gmap.p, ctx->stream);
+    if (rc) return rc;
+    std::vector<int64_t> acc(acc_total);
+    HIP_TRY(hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc_total, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    k = 0;
+    for (PbItem& it : items) {
+        // column-group parts add up per row, as the tiles accumulate (:815-817)
+        std::vector<int64_t> rows(it.nrows, 0);
+        for (PbPart& p : it.parts) {
+            for (int r = 0; r < it.nrows && r < p.t->dev.rows; r++) rows[r] += acc[coff[k] + r];
+            k++;
+        }
+        uint8_t* dst = arena + (it.result_addr - arena_base);
+        for (int r = 0; r < it.nrows; r++) {
+            // K-quant tiles only accumulate rows < 896 (sim/fpga_sim.hpp:1112, :779)
+            const int64_t v = (it.kquant && r >= 896) ? 0 : rows[r];
+            memcpy(dst + (size_t)r * 8, &v, 8);
+        }
+    }
+    pb_free(items);
+    return 0;
+}
+}  // namespace
+
 int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t arena_base,
                    uint32_t head_off, uint32_t* rows_out, int max_desc) {
     if (!ctx || !arena) return tmq_fail(TMQ_ERR_ARG, "null argument");
@@ -900,18 +1012,17 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
     auto in_arena = [&](uint64_t off, uint64_t len) {
         return off >= arena_base && off - arena_base + len <= arena_bytes;
     };
-    struct Item {
-        tmq_tensor* t;
-        uint32_t result_addr;
-        int nrows;
-        std::vector<uint8_t> act;
-        int kquant_rows_lt896;
-    };
-    std::vector<Item> items;
+    std::vector<PbItem> items;  // pending
     std::vector<uint32_t> rows_list;
     auto cleanup = [&](int code) {
-        for (Item& it : items) tmq_tensor_free(it.t);
+        pb_free(items);
         return code;
+    };
+    // does [a, a+len) read a result range that is still pending?
+    auto reads_pending = [&](uint64_t a, uint64_t len) {
+        for (const PbItem& it : items)
+            if (a < (uint64_t)it.result_addr + 8ull * it.nrows && (uint64_t)it.result_addr < a + len) return true;
+        return false;
     };
     uint32_t off = head_off;
     int walked = 0;
@@ -931,18 +1042,20 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
             nrows = nt * tr;
             if (!in_arena(wa, (uint64_t)nt * tb) || !in_arena(aa, 896 * 2) || !in_arena(ra, (uint64_t)nrows * 8))
                 return cleanup(tmq_fail(TMQ_ERR_DESC, "Q5_0 descriptor at 0x%x: address out of arena", off));
+            if (reads_pending(wa, (uint64_t)nt * tb) || reads_pending(aa, 896 * 2))
+                if ((rc = pb_flush(ctx, items, arena, arena_base))) return cleanup(rc);
             std::vector<uint8_t> w((size_t)nt * 224 * 22);
             for (int ti = 0; ti < nt; ti++)
                 memcpy(w.data() + (size_t)ti * 224 * 22, arena + (wa - arena_base) + (size_t)ti * tb, 224 * 22);
-            Item it{};
-            int rc2 = tensor_create(ctx, TMQ_TYPE_Q5_0, (uint64_t)nrows, 896, w.data(), false, w.size(),
-                                    nullptr, false, nullptr, &it.t);
+            PbItem it;
+            it.parts.resize(1);
+            int rc2 = tensor_create(ctx, TMQ_TYPE_Q5_0, (uint64_t)nrows, 896, w.data(), false, w.size(), nullptr,
+                                    false, nullptr, &it.parts[0].t);
             if (rc2) return cleanup(rc2);
-            it.t->dev.clamp = 1;
-            act_from_int16((const int16_t*)(arena + (aa - arena_base)), 896, it.act);
+            it.parts[0].t->dev.clamp = 1;
+            act_from_int16((const int16_t*)(arena + (aa - arena_base)), 896, it.parts[0].act);
             it.result_addr = ra;
             it.nrows = nrows;
-            it.kquant_rows_lt896 = 0;
             items.push_back(std::move(it));
         } else if (type == TMQ_TYPE_Q6_K || type == TMQ_TYPE_Q4_K) {
             const bool k6 = type == TMQ_TYPE_Q6_K;
@@ -955,29 +1068,47 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
             const int cols = cg * 256;
             if (!in_arena(wa, (uint64_t)nt * tb) || !in_arena(aa, (uint64_t)cols * 2) || !in_arena(ra, (uint64_t)nrows * 8))
                 return cleanup(tmq_fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: address out of arena", off));
-            std::vector<uint8_t> w((size_t)nrows * cg * bb);
-            std::vector<float> ri(nrows, 0.0f);
-            std::vector<char> seen(nrows, 0);
+            if (reads_pending(wa, (uint64_t)nt * tb) || reads_pending(aa, (uint64_t)cols * 2))
+                if ((rc = pb_flush(ctx, items, arena, arena_base))) return cleanup(rc);
+            // row_inv of every (row, column group): the tile's UQ24.8 value (:791-795)
+            std::vector<float> ri((size_t)nrows * cg, 0.0f);
+            bool uniform = true;
             for (int ti = 0; ti < nt; ti++) {
-                const int cgi = ti % cg, rg = ti / cg, row0 = rg * tr;
+                const int cgi = ti % cg, row0 = (ti / cg) * tr;
                 const uint8_t* tile = arena + (wa - arena_base) + (size_t)ti * tb;
                 for (int i = 0; i < tr; i++) {
-                    memcpy(w.data() + ((size_t)(row0 + i) * cg + cgi) * bb, tile + (size_t)i * bb, bb);
-                    float v = (float)rd32(tile + blk_bytes + i * 4) / 256.0f;  // UQ24.8 (:791-795)
-                    if (seen[row0 + i] && ri[row0 + i] != v)
-                        return cleanup(tmq_fail(TMQ_ERR_DESC, "K-quant descriptor at 0x%x: row %d has differing row_inv across tiles", off, row0 + i));
-                    ri[row0 + i] = v;
-                    seen[row0 + i] = 1;
+                    ri[(size_t)(row0 + i) * cg + cgi] = (float)rd32(tile + blk_bytes + i * 4) / 256.0f;
+                    if (cgi > 0 && ri[(size_t)(row0 + i) * cg + cgi] != ri[(size_t)(row0 + i) * cg]) uniform = false;
                 }
             }
-            Item it{};
-            int rc2 = tensor_create(ctx, (uint32_t)type, (uint64_t)nrows, (uint64_t)cols, w.data(), false,
-                                    w.size(), nullptr, false, ri.data(), &it.t);
-            if (rc2) return cleanup(rc2);
-            act_from_int16((const int16_t*)(arena + (aa - arena_base)), cols, it.act);
+            // one tensor when every row has one row_inv, else one per column
+            // group (each tile's own value applies to its columns)
+            const int np = uniform ? 1 : cg, pcols = uniform ? cols : 256;
+            PbItem it;
+            it.parts.resize(np);
+            const int16_t* act = (const int16_t*)(arena + (aa - arena_base));
+            for (int p = 0; p < np; p++) {
+                const int ncg = uniform ? cg : 1;
+                std::vector<uint8_t> w((size_t)nrows * ncg * bb);
+                std::vector<float> pri(nrows);
+                for (int ti = 0; ti < nt; ti++) {
+                    const int cgi = ti % cg, row0 = (ti / cg) * tr;
+                    if (!uniform && cgi != p) continue;
+                    const int dcol = uniform ? cgi : 0;
+                    const uint8_t* tile = arena + (wa - arena_base) + (size_t)ti * tb;
+                    for (int i = 0; i < tr; i++) {
+                        memcpy(w.data() + ((size_t)(row0 + i) * ncg + dcol) * bb, tile + (size_t)i * bb, bb);
+                        pri[row0 + i] = ri[(size_t)(row0 + i) * cg + (uniform ? 0 : p)];
+                    }
+                }
+                int rc2 = tensor_create(ctx, (uint32_t)type, (uint64_t)nrows, (uint64_t)pcols, w.data(), false,
+                                        w.size(), nullptr, false, pri.data(), &it.parts[p].t);
+                if (rc2) return cleanup(rc2);
+                act_from_int16(act + (uniform ? 0 : 256 * p), pcols, it.parts[p].act);
+            }
             it.result_addr = ra;
             it.nrows = nrows;
-            it.kquant_rows_lt896 = 1;
+            it.kquant = true;
             items.push_back(std::move(it));
         } else {
             nrows = 0;  // CPU_OP and unsupported types: no matmul rows (:823-829)
@@ -986,56 +1117,9 @@ int tmq_phaseb_run(tmq_ctx* ctx, uint8_t* arena, uint64_t arena_bytes, uint32_t 
         walked++;
         off = next;
     }
-    // one launch over all matmul descriptors
-    if (!items.empty()) {
-        size_t act_total = 0, acc_total = 0;
-        std::vector<size_t> aoff, coff;
-        for (Item& it : items) {
-            aoff.push_back(act_total);
-            act_total += (it.act.size() + 255) & ~(size_t)255;
-            coff.push_back(acc_total);
-            acc_total += (size_t)it.t->dev.rows;
-        }
-        rc = ctx->act.ensure(act_total);
-        if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * acc_total);
-        if (rc) return cleanup(rc);
-        std::vector<TmqWork> works;
-        std::vector<int32_t> gmap;
-        std::vector<Segment> segs;
-        for (size_t i = 0; i < items.size(); i++) {
-            hipError_t e = hipMemcpyAsync((uint8_t*)ctx->act.p + aoff[i], items[i].act.data(), items[i].act.size(),
-                                          hipMemcpyHostToDevice, ctx->stream);
-            if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "act copy: %s", hipGetErrorString(e)));
-            works.push_back(make_work(items[i].t, (const uint8_t*)ctx->act.p + aoff[i], nullptr,
-                                      (int64_t*)ctx->acc.p + coff[i]));
-        }
-        plan_segments(works, gmap, segs);
-        rc = ctx->works.ensure(sizeof(TmqWork) * works.size());
-        if (!rc) rc = ctx->gmap.ensure(sizeof(int32_t) * gmap.size());
-        if (rc) return cleanup(rc);
-        hipError_t e = hipMemcpyAsync(ctx->works.p, works.data(), sizeof(TmqWork) * works.size(),
-                                      hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(ctx->gmap.p, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice, ctx->stream);
-        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "chain upload: %s", hipGetErrorString(e)));
-        int le = launch_segments(segs, ctx->works.p, ctx->gmap.p, ctx->stream);
-        if (le) return cleanup(le);
-        std::vector<int64_t> acc(acc_total);
-        e = hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc_total, hipMemcpyDeviceToHost, ctx->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "chain results: %s", hipGetErrorString(e)));
-        for (size_t i = 0; i < items.size(); i++) {
-            uint8_t* dst = arena + (items[i].result_addr - arena_base);
-            for (int r = 0; r < items[i].nrows; r++) {
-                // K-quant tiles only accumulate rows < 896 (sim/fpga_sim.hpp:1112, :779)
-                int64_t v = (items[i].kquant_rows_lt896 && r >= 896) ? 0 : acc[coff[i] + r];
-                memcpy(dst + (size_t)r * 8, &v, 8);
-            }
-        }
-    }
+    if ((rc = pb_flush(ctx, items, arena, arena_base))) return cleanup(rc);
     if (rows_out)
         for (int i = 0; i < (int)rows_list.size() && i < max_desc; i++) rows_out[i] = rows_list[i];
-    cleanup(0);
     return walked;
 }
 

@@ -17,6 +17,15 @@
 // loop; the logits are get_logits_q8 only under --fpga-q8 (:2151-2155).
 // The prompt runs through the batched prefill in chunks of --prefill N
 // tokens (default 512); --no-prefill runs it one token at a time.
+// --dump-tiles N, --dump-tiles-q5-0 N, --dump-tiles-q6-k N write the first N
+// Q8_0 / Q5_0 / Q6_K tiles of the run's matmuls in the reference's
+// cosimulation layouts (:1046-1065, :1282-1298, :1478-1495) to
+// <cosim-dir>/cosim_tiles{,_q5_0,_q6_k}.bin (default /tmp); --fpga-phaseb
+// sets every --fpga flag and records the PhaseB descriptor chain of the
+// run's Q5_0/Q4_K/Q6_K matmuls until the reference's 1 GiB DDR is full,
+// replays it on the GPU and verifies it (:834-880); --dump-phaseb writes
+// tb_phaseb.bin/.hdr (:609-708) to the same directory.  While any of these
+// records, positions run one at a time with their matmul inputs captured.
 // --perf prints host timings (load, prompt, per-token decode) to stderr, then
 // profiles up to 8 more decode steps launch by launch on the GPU and prints
 // the reference's pipeline timing breakdown (:79-134) per operation, and
@@ -27,10 +36,12 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
 #include "../../include/tmq.h"
+#include "tmq_cosim.h"
 
 namespace {
 
@@ -108,6 +119,9 @@ int main(int argc, char** argv) {
     int generate_n = 0, max_seq = 512, prefill = 512;
     bool perf = false, graphs = true, dump_layers = false;
     uint32_t flags = 0;  // the reference's g_use_fpga / g_fpga_* (all off by default)
+    bool phaseb = false, dump_phaseb = false;
+    int dump_tiles[3] = {0, 0, 0};  // Q8_0, Q5_0, Q6_K
+    std::string cosim_dir = "/tmp";
     const char* trace_path = "/tmp/pipeline_trace.json";
     const char* dump_dir = "/tmp";
     for (int i = 2; i < argc; i++) {
@@ -125,6 +139,14 @@ int main(int argc, char** argv) {
         else if (!strcmp(argv[i], "--fpga-q4k")) flags |= TMQ_FLAG_FPGA | TMQ_FLAG_Q4_K;
         else if (!strcmp(argv[i], "--fpga-q5-0")) flags |= TMQ_FLAG_FPGA | TMQ_FLAG_Q5_0;
         else if (!strcmp(argv[i], "--fpga-q6-k")) flags |= TMQ_FLAG_FPGA | TMQ_FLAG_Q6_K;
+        else if (!strcmp(argv[i], "--fpga-phaseb")) {
+            phaseb = true;
+            flags = TMQ_FLAGS_ALL;
+        } else if (!strcmp(argv[i], "--dump-phaseb")) dump_phaseb = true;
+        else if (!strcmp(argv[i], "--dump-tiles") && i + 1 < argc) dump_tiles[0] = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--dump-tiles-q5-0") && i + 1 < argc) dump_tiles[1] = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--dump-tiles-q6-k") && i + 1 < argc) dump_tiles[2] = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--cosim-dir") && i + 1 < argc) cosim_dir = argv[++i];
         else {
             fprintf(stderr, "[ERROR] unknown option %s\n", argv[i]);
             return 1;
@@ -151,8 +173,53 @@ int main(int argc, char** argv) {
     }
     tmq_model_config cfg;
     tmq_model_get_config(m, &cfg);
+    // per-matmul recorders (tile dumps, PhaseB): the .tmac bytes of every
+    // weight, and the inputs of every matmul captured position by position
+    tmq_cli::TmacFile tf;
+    std::unique_ptr<tmq_cli::Recorder> rec;
+    if (phaseb || dump_tiles[0] > 0 || dump_tiles[1] > 0 || dump_tiles[2] > 0) {
+        std::string err;
+        if (!tf.load(argv[1], &err)) {
+            fprintf(stderr, "[ERROR] %s\n", err.c_str());
+            return 1;
+        }
+        rec.reset(new tmq_cli::Recorder(ctx, m, &tf, flags));
+        static const char* names[3] = {"/cosim_tiles.bin", "/cosim_tiles_q5_0.bin", "/cosim_tiles_q6_k.bin"};
+        for (int k = 0; k < 3; k++)
+            if (!rec->open_tiles(k, dump_tiles[k], cosim_dir + names[k])) {
+                fprintf(stderr, "[ERROR] cannot write %s%s\n", cosim_dir.c_str(), names[k]);
+                return 1;
+            }
+        if (phaseb) {
+            rec->enable_phaseb();
+            fprintf(stderr, "[PHASEB] Descriptor chain mode enabled\n");
+        }
+    }
+    const size_t cap_n = (size_t)cfg.n_layers * (3 * (size_t)cfg.hidden + cfg.inter);
+    std::vector<float> acts;
+    // one position with its matmul inputs offered to the recorders
+    auto feed_rec = [&](int32_t t) -> int {
+        acts.resize(cap_n);
+        if (tmq_model_feed_capture(m, t, acts.data()) != TMQ_OK) return die("feed_capture");
+        return rec->offer_position(acts.data(), cfg.n_layers, cfg.hidden, cfg.inter) ? 1 : 0;
+    };
+    // the logits (get_logits_q8 / get_logits) with their input offered
+    auto logits_rec = [&](std::vector<float>& lg) -> int {
+        std::vector<float> x(cfg.hidden);
+        if (tmq_model_logits_capture(m, lg.data(), x.data()) != TMQ_OK) return die("logits_capture");
+        if (flags & TMQ_FLAG_Q8_0) return rec->offer({"token_embd.weight", x.data()}) ? 1 : 0;
+        return 0;
+    };
     const double t1 = now_ms();
-    if (!dump_layers) {
+    if (rec && rec->active() && !dump_layers) {
+        // process_prompt one token at a time while the recorders take calls
+        if (tmq_model_reset(m) != TMQ_OK) return die("reset");
+        size_t i = 0;
+        for (; i < tokens.size() && rec->active(); i++)
+            if (feed_rec(tokens[i])) return 1;
+        for (; i < tokens.size(); i++)
+            if (tmq_model_feed(m, tokens[i]) != TMQ_OK) return die("feed");
+    } else if (!dump_layers) {
         if (tmq_model_prompt(m, tokens.data(), (int)tokens.size()) != TMQ_OK) return die("prompt");
     } else {
         // process_prompt with dump_layers (sim/tmac_gguf.cpp:2001-2018): the
@@ -177,14 +244,28 @@ int main(int argc, char** argv) {
     }
     const double t2 = now_ms();
     double t3 = t2;
+    // greedy choice of generate: the first index of the largest logit
+    auto argmax = [](const std::vector<float>& lg) {
+        return (int32_t)(std::max_element(lg.begin(), lg.end()) - lg.begin());
+    };
     if (generate_n > 0) {
         std::vector<int32_t> out(generate_n);
-        if (tmq_model_generate(m, generate_n, out.data()) != TMQ_OK) return die("generate");
+        int g = 0;
+        std::vector<float> lg(cfg.vocab);
+        // generate (:2025-2045): logits, choice, then the chosen token fed
+        for (; g < generate_n && rec && rec->active(); g++) {
+            if (logits_rec(lg)) return 1;
+            out[g] = argmax(lg);
+            if (feed_rec(out[g])) return 1;
+        }
+        if (g < generate_n && tmq_model_generate(m, generate_n - g, out.data() + g) != TMQ_OK) return die("generate");
         t3 = now_ms();
         for (int v : out) printf("%d\n", v);
     } else {
         std::vector<float> logits(cfg.vocab);
-        if (tmq_model_logits(m, logits.data()) != TMQ_OK) return die("logits");
+        if (rec && rec->active()) {
+            if (logits_rec(logits)) return 1;
+        } else if (tmq_model_logits(m, logits.data()) != TMQ_OK) return die("logits");
         t3 = now_ms();
         std::vector<int> idx(cfg.vocab);
         for (int i = 0; i < cfg.vocab; i++) idx[i] = i;
@@ -217,7 +298,14 @@ int main(int argc, char** argv) {
             perf_report(lt, steps, trace_path);
         }
     }
+    int rc = 0;
+    if (rec && phaseb) {
+        // phaseb_verify (:834-880), then phaseb_dump_files (:609-708)
+        if (rec->phaseb_verify() < 0) rc = 1;
+        if (!rc && dump_phaseb && rec->phaseb_dump(cosim_dir) < 0) rc = 1;
+    }
+    rec.reset();
     tmq_model_free(m);
     tmq_close(ctx);
-    return 0;
+    return rc;
 }

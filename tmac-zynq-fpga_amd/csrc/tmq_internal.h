@@ -147,6 +147,7 @@ struct TmqEngAct {
     int32_t spec_miss;         // nonzero: the norm's segmented sum re-runs every segment (testing)
     TmqDeferred d1;            // RESID_NORM: the residual term
     float* hidden_out;
+    float* act_out;            // NORM modes: workgroup 0 stores the fp32 norm output (capture)
     TmqEngState* state;        // EMBED_NORM: token = tokens[state->pos]
     const int32_t* tokens;
     TmqTensorDev emb;          // EMBED_NORM: quantized embedding
@@ -206,6 +207,8 @@ int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* ou
 int tmq_launch_zero_acc(int64_t* p, size_t n, hipStream_t s);
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s);
+// UQ8.8 combined scales of a Q8_0 tensor, out[r * nb + b]
+int tmq_launch_q8_scales(const TmqTensorDev& t, uint16_t* out, hipStream_t s);
 // INT16 path weights and row scales of a tensor (t.pw, t.rs16 allocated)
 int tmq_launch_i16_prep(const TmqTensorDev& t, hipStream_t s);
 // F32 / F16 tensors: flags non-finite elements

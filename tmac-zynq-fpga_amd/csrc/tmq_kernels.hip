@@ -1471,6 +1471,9 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
     }
     // the FP32 path reads the activation itself: o = L.x * red[1]
     if (tid == 0) L.red[1] = s;
+    // capture of the norm output (the matmuls' fp32 input, rms_norm's o)
+    if (norm && a.act_out && blockIdx.x == 0)
+        for (int i = tid; i < n; i += nt) a.act_out[i] = L.x[i] * s;
     float mm;
     if (a.mode == TMQ_ACT_PRESCALED) {
         mm = __builtin_bit_cast(float, pmax);
@@ -2082,6 +2085,16 @@ __global__ __launch_bounds__(256) void fit_kernel(TmqTensorDev t, int all_exact)
     }
 }
 
+// UQ8.8 combined scale of every (row, block) of a Q8_0 tensor, as
+// matmul_fpga_q8 forms them for its tiles (sim/tmac_gguf.cpp:1022-1039);
+// out[r * nb + b]
+__global__ __launch_bounds__(256) void q8_scales_kernel(TmqTensorDev t, uint16_t* out) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)t.rows * t.nb) return;
+    const int r = (int)(i / t.nb), b = (int)(i % t.nb);
+    out[i] = (uint16_t)q8_cs(h2f(ld2(t.pd + ((size_t)b * t.rows_pad + r) * 2)), t.row_inv[r]);
+}
+
 // ----------------------------------------------------------- Q8 tile
 // axi_vecmul_tile_q8: q8_W column-major [k][n], cs[n*2 + k/32] UQ8.8,
 // deq = (q8*cs) >> 8, result[n] = sum_k vec[k]*deq (sim/fpga_sim.hpp:316-349)
@@ -2480,6 +2493,13 @@ int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x,
 int tmq_launch_tile_q8(const uint8_t* W, const uint16_t* cs, const int16_t* vec, int64_t* out,
                        hipStream_t s) {
     hipLaunchKernelGGL(tile_q8_kernel, dim3(1), dim3(64), 0, s, W, cs, vec, out);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_q8_scales(const TmqTensorDev& t, uint16_t* out, hipStream_t s) {
+    if (t.type != kQ8_0) return (int)hipErrorInvalidValue;
+    const size_t n = (size_t)t.rows * t.nb;
+    hipLaunchKernelGGL(q8_scales_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, t, out);
     return (int)hipGetLastError();
 }
 

@@ -220,13 +220,25 @@ int launch_gemv(tmq_model* m, const Launch& l) {
 // launch also performs process_embedding of tokens[pos].  The step's K-split
 // accumulators are zeroed first.  With dump, the residual stream after the
 // embedding and after every layer is copied to dump[(l+1)*H].
-int launch_layers(tmq_model* m, bool dump) {
+// With cap (eager launches only), the fp32 input of every matmul is stored
+// per layer at cap + l*(3*hidden + ffn): the attn_norm output (q, k, v),
+// the attention context (attn_output), the ffn_norm output (gate, up) and
+// SiLU(gate)*up (ffn_down).
+int launch_layers(tmq_model* m, bool dump, float* cap = nullptr) {
     hipStream_t s = m->ctx->stream;
     const tmq_model_config& c = m->cfg;
     const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM;
+    const size_t per = 3 * (size_t)H + c.inter;
     PROF("zero_acc", LAUNCH_TRY(tmq_launch_zero_acc(m->kacc, m->kacc_n, s)));
     for (int l = 0; l < c.n_layers; l++) {
-        const Layer& L = m->layers[l];
+        const Layer& L0 = m->layers[l];
+        Layer Lc;
+        if (cap) {
+            Lc = L0;
+            Lc.qkv.P.act.act_out = cap + l * per;
+            Lc.gu.P.act.act_out = cap + l * per + 2 * (size_t)H;
+        }
+        const Layer& L = cap ? Lc : L0;
         int rc = 0;
         PROF(l == 0 ? "embedding+attn_norm+qkv" : "attn_norm+qkv", rc = launch_gemv(m, L.qkv));
         if (rc) return rc;
@@ -244,12 +256,16 @@ int launch_layers(tmq_model* m, bool dump) {
         aa.n_kv = c.n_kv_heads;
         aa.max_pos = c.max_seq;
         PROF("rope+attention", LAUNCH_TRY(tmq_launch_attn(aa, s)));
+        if (cap) HIP_TRY(hipMemcpyAsync(cap + l * per + H, m->ctxv, sizeof(float) * H, hipMemcpyDeviceToDevice, s));
         PROF("attn_output", rc = launch_gemv(m, L.o_l));
         if (rc) return rc;
         PROF(L.fused_gu ? "ffn_norm+gate+up+silu_x_up" : "ffn_norm+gate+up", rc = launch_gemv(m, L.gu));
         if (rc) return rc;
         if (!L.fused_gu)
             PROF("silu_x_up", LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s)));
+        if (cap)
+            HIP_TRY(hipMemcpyAsync(cap + l * per + 3 * (size_t)H, m->silu_x, sizeof(float) * c.inter,
+                                   hipMemcpyDeviceToDevice, s));
         PROF("ffn_down", rc = launch_gemv(m, L.dn));
         if (rc) return rc;
         if (dump) LAUNCH_TRY(tmq_launch_resid_view(m->hid[0], L.dd, H, m->dump + (size_t)(l + 1) * H, s));
@@ -258,9 +274,9 @@ int launch_layers(tmq_model* m, bool dump) {
 }
 
 // one position whose token the host stored at tokens[pos+1]
-int launch_feed_impl(tmq_model* m, bool dump) {
+int launch_feed_impl(tmq_model* m, bool dump, float* cap = nullptr) {
     LAUNCH_TRY(tmq_launch_advance(m->state, m->cfg.max_seq, m->ctx->stream));
-    return launch_layers(m, dump);
+    return launch_layers(m, dump, cap);
 }
 int launch_feed(tmq_model* m) { return launch_feed_impl(m, false); }
 
@@ -1186,6 +1202,14 @@ int tmq_model_set_flags(tmq_model* m, uint32_t flags) {
 
 uint32_t tmq_model_get_flags(const tmq_model* m) { return m ? m->flags : 0u; }
 
+int tmq_model_reset(tmq_model* m) {
+    if (!m) return tmq_fail(TMQ_ERR_ARG, "null model");
+    int rc = tmq_rt_set_device(m->ctx);
+    if (!rc) rc = reset(m);
+    if (!rc) HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return rc;
+}
+
 int tmq_model_set_prefill(tmq_model* m, int chunk) {
     if (!m || chunk < 0) return tmq_fail(TMQ_ERR_ARG, "bad prefill arguments");
     if (chunk > 0 && m->prefill_off) return tmq_fail(TMQ_ERR_ARG, "batched prefill unavailable: %s", m->prefill_off);
@@ -1316,6 +1340,79 @@ int tmq_model_feed_dump(tmq_model* m, int32_t token, float* layers_out) {
     const size_t nb = sizeof(float) * m->cfg.hidden * (size_t)(m->cfg.n_layers + 1);
     HIP_TRY(hipMemcpyAsync(layers_out, m->dump, nb, hipMemcpyDeviceToHost, m->ctx->stream));
     return check_state(m);
+}
+
+int tmq_model_feed_capture(tmq_model* m, int32_t token, float* acts_out) {
+    if (!m || !acts_out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (token < 0 || token >= m->cfg.vocab) return tmq_fail(TMQ_ERR_ARG, "token %d outside [0, %d)", token, m->cfg.vocab);
+    if (m->pos + 1 >= m->cfg.max_seq) return tmq_fail(TMQ_ERR_ARG, "context full (max_seq %d)", m->cfg.max_seq);
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    const size_t n = (size_t)m->cfg.n_layers * (3 * (size_t)m->cfg.hidden + m->cfg.inter);
+    void* cap = nullptr;
+    HIP_TRY(hipMalloc(&cap, sizeof(float) * n));
+    hipStream_t s = m->ctx->stream;
+    hipError_t e = hipMemcpyAsync(m->tokens + m->pos + 1, &token, 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && (rc = launch_feed_impl(m, false, (float*)cap)) == 0)
+        e = hipMemcpyAsync(acts_out, cap, sizeof(float) * n, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(cap);
+    if (rc) return rc;
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_HIP, "feed_capture: %s", hipGetErrorString(e));
+    m->pos++;
+    return check_state(m);
+}
+
+int tmq_model_logits_capture(tmq_model* m, float* logits, float* x_out) {
+    if (!m || !x_out) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    if (m->pos < 0) return tmq_fail(TMQ_ERR_ARG, "no position processed yet");
+    int rc = tmq_rt_set_device(m->ctx);
+    if (rc) return rc;
+    hipStream_t s = m->ctx->stream;
+    const int H = m->cfg.hidden;
+    void* cap = nullptr;
+    HIP_TRY(hipMalloc(&cap, sizeof(float) * H));
+    Launch l = m->logits_l;
+    l.P.act.act_out = (float*)cap;
+    rc = launch_gemv(m, l);
+    hipError_t e = hipSuccess;
+    if (!rc && m->out_norm < 0) {
+        // no output_norm: the logits read the residual stream itself
+        int le = tmq_launch_resid_view(m->hid[0], m->layers.back().dd, H, (float*)cap, s);
+        if (le) e = (hipError_t)le;
+    }
+    if (!rc && e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, m->logits, sizeof(float) * m->cfg.vocab, hipMemcpyDeviceToHost, s);
+    if (!rc && e == hipSuccess) e = hipMemcpyAsync(x_out, cap, sizeof(float) * H, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(cap);
+    if (rc) return rc;
+    if (e != hipSuccess) return tmq_fail(TMQ_ERR_HIP, "logits_capture: %s", hipGetErrorString(e));
+    return 0;
+}
+
+const tmq_tensor* tmq_model_tensor(const tmq_model* m, const char* name) {
+    if (!m || !name) {
+        tmq_fail(TMQ_ERR_ARG, "null argument");
+        return nullptr;
+    }
+    const std::string n(name);
+    if (n == "token_embd.weight") return m->emb;
+    for (int l = 0; l < (int)m->layers.size(); l++) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        if (n.compare(0, p.size(), p) != 0) continue;
+        const std::string r = n.substr(p.size());
+        const Layer& Y = m->layers[l];
+        if (r == "attn_q.weight") return Y.q;
+        if (r == "attn_k.weight") return Y.k;
+        if (r == "attn_v.weight") return Y.v;
+        if (r == "attn_output.weight") return Y.o;
+        if (r == "ffn_gate.weight") return Y.gate;
+        if (r == "ffn_up.weight") return Y.up;
+        if (r == "ffn_down.weight") return Y.down;
+    }
+    tmq_fail(TMQ_ERR_ARG, "model has no matmul tensor %s", name);
+    return nullptr;
 }
 
 }  // extern "C"

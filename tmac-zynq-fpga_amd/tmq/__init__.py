@@ -44,7 +44,9 @@ EXPORTS = [
     "tmq_model_weight_bytes", "tmq_model_position", "tmq_model_set_graphs", "tmq_model_prompt",
     "tmq_model_feed", "tmq_model_feed_dump", "tmq_model_logits", "tmq_model_generate",
     "tmq_model_generate_async", "tmq_model_tokens", "tmq_model_hidden", "tmq_model_set_prefill",
-    "tmq_model_profile", "tmq_model_set_flags", "tmq_model_get_flags",
+    "tmq_model_profile", "tmq_model_set_flags", "tmq_model_get_flags", "tmq_quantize_act",
+    "tmq_tensor_q8_scales", "tmq_model_feed_capture", "tmq_model_tensor", "tmq_model_logits_capture",
+    "tmq_model_reset",
 ]
 
 
@@ -134,6 +136,12 @@ def lib(path: str = LIB_PATH):
         "tmq_model_set_graphs": (I, [P, I]),
         "tmq_model_set_prefill": (I, [P, I]),
         "tmq_model_set_flags": (I, [P, U32]),
+        "tmq_quantize_act": (I, [P, P, I, P, P]),
+        "tmq_tensor_q8_scales": (I, [P, P, P]),
+        "tmq_model_feed_capture": (I, [P, C.c_int32, P]),
+        "tmq_model_tensor": (P, [P, C.c_char_p]),
+        "tmq_model_logits_capture": (I, [P, P, P]),
+        "tmq_model_reset": (I, [P]),
         "tmq_model_get_flags": (U32, [P]),
         "tmq_model_profile": (I, [P, I, P, I, C.POINTER(C.c_int)]),
         "tmq_model_prompt": (I, [P, P, I]),
@@ -315,6 +323,19 @@ class Context:
         """tmq_gemv_dev from the library's fixed scratch (no device allocation)"""
         _check(lib().tmq_gemv_dev_noalloc(self.handle, t.handle, x_ptr, y_ptr, acc_ptr))
 
+    def quantize_act(self, x: np.ndarray):
+        """(int16 xq, x_scale) as every matmul_fpga_* quantises x, on the GPU"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        xq = np.empty(x.size, dtype=np.int16)
+        xs = np.zeros(1, dtype=np.float32)
+        _check(lib().tmq_quantize_act(self.handle, _p(x), x.size, _p(xq), _p(xs)))
+        return xq, xs[0]
+
+    def q8_scales(self, t: Tensor) -> np.ndarray:
+        out = np.empty((t.rows, t.cols // 32), dtype=np.uint16)
+        _check(lib().tmq_tensor_q8_scales(self.handle, t.handle, _p(out)))
+        return out
+
     # -- tiles -----------------------------------------------------------
     def tile_q8(self, W, cs, vec) -> np.ndarray:
         out = np.zeros(64, dtype=np.int64)
@@ -399,6 +420,14 @@ class Model:
     def prompt(self, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         _check(lib().tmq_model_prompt(self.handle, _p(t), t.size))
+
+    def feed_capture(self, token: int) -> np.ndarray:
+        """one more position; the fp32 input of every matmul per layer:
+        [attn_norm out (H) | context (H) | ffn_norm out (H) | silu*up (I)]"""
+        c = self.config
+        out = np.empty((c["n_layers"], 3 * c["hidden"] + c["inter"]), dtype=np.float32)
+        _check(lib().tmq_model_feed_capture(self.handle, int(token), _p(out)))
+        return out
 
     def feed(self, token: int, dump: bool = False):
         if dump:
