@@ -105,6 +105,17 @@ int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out);
  * tensors uploaded with an external row_inv.  TMQ_NOFIT=1 in the
  * environment at upload sends every sub-block to the exact decode. */
 int tmq_tensor_fit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* fitted, uint64_t* exact);
+/* Integer fit of the MFMA decoders (no counterpart in the reference;
+ * diagnostics).  Q5_0 tensors of at most 8192 columns: within each block
+ * of a row the int16 weight of code u
+ * is floor((AN*u + BN)/256) for integers AN, BN fixed at upload; the codes
+ * no such pair reproduces are listed as corrections, applied exactly after
+ * the fitted sums.  *blocks = (row, block) pairs with a code (0: the tensor
+ * takes the fitted-float decoders), *corrections = listed codes.
+ * TMQ_NOMFMA=1 at upload keeps the tensor on the fitted-float decoders;
+ * TMQ_IFIT_FORCE=1 gives every block one fixed, mostly wrong pair (testing
+ * the corrections). */
+int tmq_tensor_ifit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* blocks, uint64_t* corrections);
 
 /* ---- GEMV (boundary 1) -------------------------------------------------
  * Drop-in for the --fpga-* dispatch of `matmul` (sim/tmac_gguf.cpp:473-493):

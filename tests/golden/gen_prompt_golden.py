@@ -16,9 +16,12 @@ Stored (model_prompt.npz, no pickle):
   tokens[S]          greedy tokens (first index of the largest logit)
 
     make -C oracle && python tests/golden/gen_prompt_golden.py
+    # the reference's longest context (MAX_SEQ_LEN 256, sim/tmac_gguf.cpp:148):
+    python tests/golden/gen_prompt_golden.py --len 250 --steps 5 --seed 13 --out model_prompt_long.npz
 """
 from __future__ import annotations
 
+import argparse
 import os
 import sys
 import tempfile
@@ -46,13 +49,20 @@ def top10(logits: np.ndarray):
 
 
 def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--len", type=int, default=PROMPT_LEN)
+    ap.add_argument("--steps", type=int, default=STEPS)
+    ap.add_argument("--seed", type=int, default=PROMPT_SEED)
+    ap.add_argument("--out", default="model_prompt.npz")
+    args = ap.parse_args()
+    assert args.len + args.steps <= 256, "the reference's KV cache holds 256 positions"
     R = Reference()
     t0 = time.time()
     with tempfile.TemporaryDirectory() as td:
         path = os.path.join(td, "model.tmac")
         tmacfile.write(path, model_synth.gen_model(MODEL_SEED))
         R.model_load(path)
-    prompt = np.random.Generator(np.random.PCG64(PROMPT_SEED)).integers(0, 151936, size=PROMPT_LEN).astype(np.int32)
+    prompt = np.random.Generator(np.random.PCG64(args.seed)).integers(0, 151936, size=args.len).astype(np.int32)
     R.model_reset()
     hidden = R.model_prompt(prompt)
     prompt_hidden = hidden.copy()
@@ -60,21 +70,21 @@ def main():
     logits_sub = logits[::64].copy()
     ids, vals = [], []
     tokens = []
-    for s in range(STEPS + 1):
+    for s in range(args.steps + 1):
         i, v = top10(logits)
         ids.append(i)
         vals.append(v)
-        if s == STEPS:
+        if s == args.steps:
             break
         tok = int(np.argmax(logits))
         tokens.append(tok)
-        R.model_step(hidden, tok, PROMPT_LEN + s)
+        R.model_step(hidden, tok, args.len + s)
         logits = R.model_logits(hidden)
         print(f"step {s}: token {tok} ({time.time() - t0:.0f} s)", flush=True)
-    np.savez(os.path.join(OUT, "model_prompt.npz"), model_seed=np.int64(MODEL_SEED), prompt=prompt,
+    np.savez(os.path.join(OUT, args.out), model_seed=np.int64(MODEL_SEED), prompt=prompt,
              hidden=prompt_hidden, top_ids=np.array(ids), top_vals=np.array(vals), logits_sub=logits_sub,
              tokens=np.array(tokens, dtype=np.int32))
-    print(f"wrote model_prompt.npz in {time.time() - t0:.0f} s")
+    print(f"wrote {args.out} in {time.time() - t0:.0f} s")
 
 
 if __name__ == "__main__":

@@ -79,6 +79,7 @@ def test_fit_stats_and_exact_decode(ctx, oracle, qt, rows, cols, monkeypatch):
     assert np.array_equal(acc, ae), report("acc", acc, ae)
     t.free()
     monkeypatch.setenv("TMQ_NOFIT", "1")
+    monkeypatch.setenv("TMQ_NOMFMA", "1")  # Q5_0: the standalone GEMV's exact decode, not the MFMA one
     t = ctx.upload(qt, rows, cols, w)
     assert t.fit_stats() == (0, rows * cols // FIT_SUB[qt])
     acc, _ = ctx.partials(t, x)

@@ -30,7 +30,7 @@ thread_local std::string g_err;
 // device's copy once (hipGetSymbolAddress, with that device current) and
 // the entry point passes that pointer to the kernels.  Every call on one
 // device shares its copy; calls that overlap on one device race on it.
-#define TMQ_NOALLOC_SCRATCH_BYTES ((16 + 10 * (size_t)TMQ_NOALLOC_MAX_COLS + 16 + 255) & ~(size_t)255)
+#define TMQ_NOALLOC_SCRATCH_BYTES ((tmq_act_bytes(TMQ_NOALLOC_MAX_COLS) + 255) & ~(size_t)255)
 static __device__ __align__(256) uint8_t scratch[TMQ_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -100,7 +100,7 @@ const char* type_name(uint32_t type) {
 }
 
 struct Segment {
-    int type, clamp, gmap_off, ngroups;
+    int type, clamp, gmap_off, ngroups, max_cols;  // type: kernel format (tmq_kernel_fmt)
 };
 
 }  // namespace
@@ -150,7 +150,7 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     d.rows_pad = (int)((rows + 63) / 64 * 64);
     d.nb = (int)(cols / qk);
     const size_t R = d.rows_pad, nb = d.nb;
-    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0;
+    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0, si = nb * R * tmq_ifit_codes((int)type);
     switch (type) {
     case TMQ_TYPE_Q8_0: sa = nb * 2 * R * 16; sd = nb * R * 2; break;
     case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; se = nb * R; break;
@@ -160,7 +160,7 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     case TMQ_TYPE_F16: sa = nb * 4 * R * 16; break;
     }
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(se) + al(R * 4) * 2;
+    const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(se) + al(si) + al(R * 4) * 2;
     hipError_t e = hipMalloc(&t->alloc, total);
     if (e != hipSuccess) {
         delete t;
@@ -178,11 +178,71 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     d.pc = sc ? p : nullptr; p += al(sc);
     d.pd = sd ? p : nullptr; p += al(sd);
     d.pe = se ? p : nullptr; p += al(se);
+    d.pi = si ? p : nullptr; p += al(si);
     d.row_inv = (const float*)p; p += al(R * 4);
     d.row_scale = (const float*)p;
     t->weight_bytes = rows * (cols / qk) * (uint64_t)block_bytes(type);
     *out = t;
     return 0;
+}
+
+// Integer fit codes and corrections of the MFMA decoders (t->dev.pi):
+// codes and per-(row, block) correction counts on the device, the offsets
+// of the corrections (rows in order, so each 64-row group's are contiguous)
+// on the host, then the corrections themselves.  Tensors with more than
+// TMQ_MFMA_MAX_COLS columns, and any uploaded under TMQ_NOMFMA=1 (testing),
+// stay on the fitted-float decoders.
+int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
+    TmqTensorDev& d = t->dev;
+    const char* nm = getenv("TMQ_NOMFMA");
+    if (!d.pi || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS) {
+        d.pi = nullptr;
+        return 0;
+    }
+    const size_t n = (size_t)d.rows_pad * d.nb;
+    uint8_t* cnt = nullptr;
+    int32_t* offd = nullptr;
+    auto done = [&](int code) {
+        if (cnt) (void)hipFree(cnt);
+        if (offd) (void)hipFree(offd);
+        return code;
+    };
+    hipError_t e = hipMalloc(&cnt, n);
+    if (e != hipSuccess) return done(tmq_fail(TMQ_ERR_NOMEM, "ifit counts: %s", hipGetErrorString(e)));
+    int le = tmq_launch_ifit(d, 0, cnt, nullptr, nullptr, ctx->stream);
+    if (le) return done(tmq_fail(TMQ_ERR_HIP, "ifit launch: %s", hipGetErrorString((hipError_t)le)));
+    std::vector<uint8_t> c(n);
+    e = hipMemcpyAsync(c.data(), cnt, n, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return done(tmq_fail(TMQ_ERR_HIP, "ifit counts: %s", hipGetErrorString(e)));
+    std::vector<int32_t> off(n);
+    const int ng = d.rows_pad / 64;
+    std::vector<int32_t> goff(ng + 1);
+    int64_t total = 0;
+    for (size_t i = 0; i < n; i++) {
+        if (i % ((size_t)64 * d.nb) == 0) goff[i / ((size_t)64 * d.nb)] = (int32_t)total;
+        off[i] = (int32_t)total;
+        total += c[i];
+    }
+    goff[ng] = (int32_t)total;
+    if (total == 0) return done(0);
+    if (total > (1 << 30)) return done(tmq_fail(TMQ_ERR_ARG, "ifit: %lld corrections", (long long)total));
+    const size_t cb = ((size_t)total * 16 + 255) & ~(size_t)255;
+    e = hipMalloc(&t->corr_alloc, cb + sizeof(int32_t) * (ng + 1));
+    if (e == hipSuccess) e = hipMalloc(&offd, sizeof(int32_t) * n);
+    if (e != hipSuccess) return done(tmq_fail(TMQ_ERR_NOMEM, "ifit corrections: %s", hipGetErrorString(e)));
+    uint4* corr = (uint4*)t->corr_alloc;
+    int32_t* go = (int32_t*)((uint8_t*)t->corr_alloc + cb);
+    e = hipMemcpyAsync(offd, off.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(go, goff.data(), sizeof(int32_t) * (ng + 1), hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return done(tmq_fail(TMQ_ERR_HIP, "ifit offsets: %s", hipGetErrorString(e)));
+    le = tmq_launch_ifit(d, 1, nullptr, offd, corr, ctx->stream);
+    if (le) return done(tmq_fail(TMQ_ERR_HIP, "ifit launch: %s", hipGetErrorString((hipError_t)le)));
+    e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return done(tmq_fail(TMQ_ERR_HIP, "ifit: %s", hipGetErrorString(e)));
+    d.corr = corr;
+    d.corr_off = go;
+    return done(0);
 }
 
 // Upload ggml bytes (host or device) into a freshly allocated tensor and
@@ -222,6 +282,7 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
     if (le) return cleanup(tmq_fail(TMQ_ERR_HIP, "repack launch: %s", hipGetErrorString((hipError_t)le)));
     if (ext_row_inv) {
         t->dev.clamp = 1;
+        t->dev.pi = nullptr;
         std::vector<float> ri(t->dev.rows_pad, 1.0f);
         memcpy(ri.data(), ext_row_inv, sizeof(float) * rows);
         hipError_t e = hipMemcpyAsync((void*)t->dev.row_inv, ri.data(), sizeof(float) * ri.size(),
@@ -292,6 +353,8 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
     if (e != hipSuccess) return cleanup(tmq_fail(TMQ_ERR_HIP, "rowstat: %s", hipGetErrorString(e)));
     if (badh) return cleanup(tmq_fail(TMQ_ERR_NONFINITE, "non-finite fp16 block scale in %llux%llu type %u tensor",
                                   (unsigned long long)rows, (unsigned long long)cols, type));
+    rc = ifit_build(ctx, t);
+    if (rc) return cleanup(rc);
     cleanup(0);
     *out = t;
     return 0;
@@ -314,6 +377,16 @@ void act_from_int16(const int16_t* xq, int n, std::vector<uint8_t>& buf) {
     memcpy(q, xq, sizeof(int16_t) * n);
     int32_t* q32 = (int32_t*)(q + n);
     for (int k = 0; k < n; k++) q32[k] = xq[k];
+    // MFMA decoders' operand bytes and block sums (tmq_internal.h)
+    uint8_t* xa = buf.data() + tmq_act_xa(n);
+    int32_t* xs = (int32_t*)(buf.data() + tmq_act_xs(n));
+    for (int k = 0; k < (int)tmq_act_nbx(n) * 32; k++) {
+        const int v = k < n ? xq[k] : 0, b = k >> 5, i = k & 31;
+        xa[64 * b + 32 * (i >> 4) + (i & 15)] = (uint8_t)(v >> 8);
+        xa[64 * b + 32 * (i >> 4) + 16 + (i & 15)] = (uint8_t)((v & 255) ^ 0x80);
+        xs[b] += v;
+    }
+    memset(xa + 64 * tmq_act_nbx(n) + 16, 1, 16);
 }
 
 TmqWork make_work(const tmq_tensor* t, const uint8_t* act, float* y, int64_t* acc) {
@@ -350,15 +423,18 @@ int run_int16(tmq_ctx* ctx, const tmq_tensor* t, const int16_t* xq, std::vector<
 // first_group made relative to the segment's first workgroup.
 void plan_segments(std::vector<TmqWork>& works, std::vector<int32_t>& gmap, std::vector<Segment>& segs) {
     std::stable_sort(works.begin(), works.end(), [](const TmqWork& a, const TmqWork& b) {
-        return a.t.type != b.t.type ? a.t.type < b.t.type : a.t.clamp < b.t.clamp;
+        const int fa = tmq_kernel_fmt(a.t), fb = tmq_kernel_fmt(b.t);
+        return fa != fb ? fa < fb : a.t.clamp < b.t.clamp;
     });
     gmap.clear();
     segs.clear();
     for (size_t i = 0; i < works.size(); i++) {
         TmqWork& w = works[i];
-        if (segs.empty() || segs.back().type != w.t.type || segs.back().clamp != w.t.clamp)
-            segs.push_back(Segment{w.t.type, w.t.clamp, (int)gmap.size(), 0});
+        const int fmt = tmq_kernel_fmt(w.t);
+        if (segs.empty() || segs.back().type != fmt || segs.back().clamp != w.t.clamp)
+            segs.push_back(Segment{fmt, w.t.clamp, (int)gmap.size(), 0, 0});
         Segment& sg = segs.back();
+        sg.max_cols = std::max(sg.max_cols, w.t.cols);
         w.first_group = sg.ngroups;
         for (int g = 0; g < w.ngroups; g++) gmap.push_back((int32_t)i);
         sg.ngroups += w.ngroups;
@@ -368,7 +444,7 @@ void plan_segments(std::vector<TmqWork>& works, std::vector<int32_t>& gmap, std:
 int launch_segments(const std::vector<Segment>& segs, const void* works_dev, const void* gmap_dev,
                     hipStream_t s) {
     for (const Segment& sg : segs) {
-        int e = tmq_launch_chain(sg.type, sg.clamp, (const TmqWork*)works_dev,
+        int e = tmq_launch_chain(sg.type, sg.clamp, sg.max_cols, (const TmqWork*)works_dev,
                                  (const int32_t*)gmap_dev + sg.gmap_off, sg.ngroups, s);
         if (e) return tmq_fail(TMQ_ERR_HIP, "chain segment launch: %s", hipGetErrorString((hipError_t)e));
     }
@@ -481,11 +557,12 @@ int tmq_tensor_upload_dev(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t c
 
 int tmq_tensor_free(tmq_tensor* t) {
     if (!t) return 0;
-    if (t->alloc || t->i16_alloc) {
+    if (t->alloc || t->i16_alloc || t->corr_alloc) {
         (void)hipSetDevice(t->ctx->device);
         (void)hipStreamSynchronize(t->ctx->stream);
         if (t->alloc) (void)hipFree(t->alloc);
         if (t->i16_alloc) (void)hipFree(t->i16_alloc);
+        if (t->corr_alloc) (void)hipFree(t->corr_alloc);
     }
     delete t;
     return 0;
@@ -525,6 +602,22 @@ int tmq_tensor_fit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* fitted, ui
     for (size_t b = 0; b < nb; b++)
         for (size_t r = 0; r < (size_t)t->dev.rows; r++)
             for (int i = 0; i < n; i++) (h[(b * R + r) * n + i] & 0x80u ? *exact : *fitted) += 1;
+    return 0;
+}
+
+int tmq_tensor_ifit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* blocks, uint64_t* corrections) {
+    if (!ctx || !t || !blocks || !corrections) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    *blocks = *corrections = 0;
+    if (!t->dev.pi) return 0;
+    *blocks = (uint64_t)t->dev.rows * t->dev.nb;
+    if (!t->dev.corr_off) return 0;
+    int rc = tmq_rt_set_device(ctx);
+    if (rc) return rc;
+    int32_t last = 0;
+    HIP_TRY(hipMemcpyAsync(&last, t->dev.corr_off + t->dev.rows_pad / 64, sizeof(int32_t), hipMemcpyDeviceToHost,
+                           ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    *corrections = (uint64_t)last;
     return 0;
 }
 

@@ -9,8 +9,9 @@
 //   so the 64 lanes of a wave (one row each) read 1 KiB contiguous per load.
 //
 //   Q8_0  A: q    [b][2][r] x16B     D: d [b][r] u16
-//   Q5_0  A: qs   [b][r]    x16B     B: qh' [b][r] u32     D: d [b][r] u16
-//         (qh' = qh with bit 8k+g holding the high bit of element 4g+k)
+//   Q5_0  A: D0-D3 [b][r]   x16B     B: D4  [b][r] u32     D: d [b][r] u16
+//         (the 32 5-bit codes repacked into five dwords, tmq_kernels.hip
+//         q5_codes; fit codes E: pe [b][r], integer fit codes pi [b][r])
 //   Q4_K  A: qs   [b][8][r] x16B     B: hdr (d,dmin,scales[12]) [b][r] x16B
 //   Q6_K  A: ql   [b][8][r] x16B     B: qh [b][4][r] x16B   C: sc [b][r] x16B
 //         D: d [b][r] u16
@@ -32,7 +33,11 @@
 // waves per workgroup of the standalone / chain GEMVs of a type (Q6_K: 8,
 // its long rows split into shorter waves; measured 4 % faster for Q6_K and
 // 4 % slower for Q4_K on the 896x4864 BASELINE shapes)
-constexpr int gemv_waves(int type) { return type == 14 ? 8 : TMQ_WAVES; }
+// Kernel format of a standalone / chain GEMV: the tensor's type, or
+// TMQ_FMT_Q5_0_MFMA for a Q5_0 tensor on the MFMA decoders (its integer fit
+// built at upload).
+#define TMQ_FMT_Q5_0_MFMA 106
+constexpr int gemv_waves(int fmt) { return fmt == 14 ? 8 : TMQ_WAVES; }
 #define TMQ_Q8_MAX_TILES 256  // cols <= 16384 for Q8_0
 
 struct TmqTensorDev {
@@ -45,11 +50,18 @@ struct TmqTensorDev {
     const uint8_t* pc;
     const uint8_t* pd;
     const uint8_t* pe;       // fit codes (Q5_0: 1 B, Q4_K: 8 B, Q6_K: 16 B per block and row)
+    const uint8_t* pi;       // integer fit codes of the MFMA decoders (Q5_0: 1 B per block and row)
+    const uint4* corr;       // their corrections (TmqCorr), grouped by 64-row group
+    const int32_t* corr_off; // [rows_pad/64 + 1] first correction of each group (null: none)
     const float* row_inv;    // Q5_0/K-quants: row_inv; Q8_0: 1/row_scale (guarded)
     const float* row_scale;  // Q8_0 only
     const uint8_t* pw;       // INT16 path weights (null until prepared)
     const float* rs16;       // INT16 path row scales
 };
+
+static inline int tmq_kernel_fmt(const TmqTensorDev& t) {
+    return t.type == 6 && t.pi && !t.clamp ? TMQ_FMT_Q5_0_MFMA : t.type;
+}
 
 // matmul branch a work takes (sim/tmac_gguf.cpp:473-493)
 enum { TMQ_WPATH_FPGA = 0, TMQ_WPATH_INT16 = 1, TMQ_WPATH_FP32 = 2 };
@@ -57,9 +69,21 @@ enum { TMQ_WPATH_FPGA = 0, TMQ_WPATH_INT16 = 1, TMQ_WPATH_FP32 = 2 };
 // Prepared activation, written by act_prep (or by the host for int16 input):
 //   +0  float x_scale   +4 int32 n   +16 u32 XH[n/2]   +16+2n u32 XL[n/2]
 //   +16+4n int16 xq[n]   +16+6n int32 xq[n] (the fitted decoders' int64 sums)
+//   +XA  (tmq_act_xa) the MFMA decoders' operand bytes, 64 B per 32-element
+//        block b: int8 xh of elements 0-15, int8 xl-128 of 0-15, xh of
+//        16-31, xl-128 of 16-31; then 16 zero bytes and 16 bytes of 1
+//   +XS  (XA + 64*nbx + 32) int32 sum of xq over each block, padded to 16 B
 // XH/XL hold (xq >> 8, xq & 255) as int16 pairs (elements 2k, 2k+1), so that
 // sum w*xq = 256*sum w*xh + sum w*xl with every partial inside int32.
-static inline uint64_t tmq_act_bytes(int n) { return 16 + (uint64_t)n * 10 + 16; }
+constexpr uint64_t tmq_act_nbx(int n) { return ((uint64_t)n + 31) / 32; }
+constexpr uint64_t tmq_act_xa(int n) { return (16 + (uint64_t)n * 10 + 15) & ~(uint64_t)15; }
+constexpr uint64_t tmq_act_xs(int n) { return tmq_act_xa(n) + 64 * tmq_act_nbx(n) + 32; }
+constexpr uint64_t tmq_act_bytes(int n) { return tmq_act_xs(n) + ((4 * tmq_act_nbx(n) + 15) & ~(uint64_t)15) + 16; }
+
+// One correction of the MFMA decoders' integer fit (uint4): the block's
+// fitted weights differ from the exact ones by `delta` on the elements
+// col0 + i, i in `mask` (all holding one code), so the row sum takes
+// delta * sum of xq over them.  x = row, y = col0, z = mask, w = delta.
 
 // One GEMV of a chain.  The output epilogue of row r is
 //     v = finalize(acc_r);  if (bias) v = v + bias[r];  if (resid) v = y[r] + v;
@@ -188,12 +212,25 @@ int tmq_launch_repack(int type, const uint8_t* src, const TmqTensorDev& t, hipSt
 int tmq_launch_fit(const TmqTensorDev& t, int all_exact, hipStream_t s);
 // bytes of fit codes per block and row (0: no fitted decode)
 static inline int tmq_fit_codes(int type) { return type == 6 ? 1 : type == 12 ? 8 : type == 14 ? 16 : 0; }
+// integer fit codes (plane pi) of the MFMA decoders.  pass 0: the codes and
+// the number of corrections of each (row, block) into cnt[r * nb + b];
+// pass 1: the corrections of (row, block) from corr[off[r * nb + b]] on.
+int tmq_launch_ifit(const TmqTensorDev& t, int pass, uint8_t* cnt, const int32_t* off, uint4* corr,
+                    hipStream_t s);
+// bytes of integer fit codes per block and row (0: type without the MFMA decoder)
+static inline int tmq_ifit_codes(int type) { return type == 6 ? 1 : 0; }
+// widest activation the MFMA decoders keep in LDS (wider rows take the
+// fitted-float decoders)
+#define TMQ_MFMA_MAX_COLS 8192
 int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux_max_abs, float* row_inv,
                        float* row_scale, int* bad_flag, hipStream_t s);
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s);
-// one launch per chain segment (descriptors of one format / clamp mode)
-int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_t* group_work_dev,
+// one launch per chain segment (descriptors of one kernel format
+// (tmq_kernel_fmt) and clamp mode, max_cols = the widest of them)
+int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const int32_t* group_work_dev,
                      int total_groups, hipStream_t s);
+// dynamic LDS of a standalone / chain GEMV launch of a kernel format
+size_t tmq_gemv_lds_bytes(int fmt, int max_cols);
 // engine GEMV: activation recipe + works of any formats; waves = 16 or 4
 int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s);
 // x = silu(g) * u over n rows of two K-split GEMVs; *max_bits = max over

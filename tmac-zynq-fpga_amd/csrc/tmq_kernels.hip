@@ -15,6 +15,7 @@
 // block), folded into int64 once per block.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <type_traits>
 
 #include "tmq_internal.h"
@@ -30,7 +31,7 @@ typedef __attribute__((address_space(4))) const uint32_t cu32;
 
 namespace {
 
-constexpr int kQ5_0 = 6, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14;
+constexpr int kQ5_0 = 6, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kQ5_0M = TMQ_FMT_Q5_0_MFMA;
 constexpr int kF32 = 0, kF16 = 1;  // element types of the INT16 / FP32 paths
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
@@ -218,10 +219,14 @@ __device__ __forceinline__ void mac4r(float r0, float r1, float r2, float r3, co
 // it from the planes, blk_mac() multiplies it into the pair sums.
 
 // ---------------------------------------------------------------- Q5_0
-// Planes: qs[16] as in ggml; qh' = qh with its bits transposed so that bit
-// (8k + g) holds the high bit of element 4g + k; d f16.  Group g of four
-// weights (elements 4g..4g+3) is decoded SWAR-style into four bytes
-// u = nibble | hb<<4, spread into f16 lanes 0x6400|u (= 1024+u) and turned
+// Planes: the 32 5-bit codes in five dwords D0..D4 (A: D0-D3, B: D4), d f16.
+// Byte k of D_g holds in bits 0-4 the code of element 4g + k (elements
+// 0-19); bits 5-7 of the twenty bytes hold elements 20-31: element 20+k
+// bits 0-2 in D0 byte k, bits 3-4 in D1 byte k bits 5-6; 24+k likewise in
+// D2, D3; 28+k bits 0-2 in D4 byte k, bit 3 in D1 byte k bit 7, bit 4 in D3
+// byte k bit 7.  Group g of four weights (elements 4g..4g+3) is then one
+// mask (g < 5) or a few shifts and masks away as four code bytes u; the
+// decoders spread them into f16 lanes 0x6400|u (= 1024+u) and turn them
 // into E = (u-16)*d exactly by one v_fma_mix: (1024+u)*d - 1040*d.
 //
 // Fitted blocks (tensors normalised at upload): within one block of one row
@@ -236,8 +241,8 @@ __device__ __forceinline__ void mac4r(float r0, float r1, float r2, float r3, co
 // the low bits: 2 instructions per weight instead of 4.  The K-quants fit
 // each 32-weight (Q4_K) or 16-weight (Q6_K) sub-block the same way.
 struct Q5Blk {
-    uint4 qs;
-    uint32_t qh, d, e;
+    uint4 qs;           // D0..D3
+    uint32_t qh, d, e;  // D4, d, fit code
 };
 __device__ __forceinline__ Q5Blk q5_load(const TmqTensorDev& t, int b, int r) {
     const size_t o = (size_t)b * t.rows_pad + r;
@@ -250,9 +255,28 @@ __device__ __forceinline__ Q5Blk q5_load(const TmqTensorDev& t, int b, int r) {
 }
 // the 5-bit codes of elements 4g..4g+3 as bytes
 __device__ __forceinline__ uint32_t q5_codes(const Q5Blk& k, int g) {
-    const uint32_t nib = (g < 4) ? (dw_of(k.qs, g) & 0x0f0f0f0fu) : ((dw_of(k.qs, g - 4) >> 4) & 0x0f0f0f0fu);
-    const uint32_t hs = (g <= 4) ? (k.qh << (4 - g)) : (k.qh >> (g - 4));
-    return (hs & 0x10101010u) | nib;
+    const uint32_t d0 = k.qs.x, d1 = k.qs.y, d2 = k.qs.z, d3 = k.qs.w, d4 = k.qh;
+    switch (g) {
+    case 0: return d0 & 0x1f1f1f1fu;
+    case 1: return d1 & 0x1f1f1f1fu;
+    case 2: return d2 & 0x1f1f1f1fu;
+    case 3: return d3 & 0x1f1f1f1fu;
+    case 4: return d4 & 0x1f1f1f1fu;
+    case 5: return ((d0 >> 5) & 0x07070707u) | ((d1 >> 2) & 0x18181818u);
+    case 6: return ((d2 >> 5) & 0x07070707u) | ((d3 >> 2) & 0x18181818u);
+    default: return ((d4 >> 5) & 0x07070707u) | ((d1 >> 4) & 0x08080808u) | ((d3 >> 3) & 0x10101010u);
+    }
+}
+// the code of element e (0..31) from the five dwords
+__device__ __forceinline__ int q5_code(const uint4& qs, uint32_t d4, int e) {
+    const int g = e >> 2, k = e & 3, sh = 8 * k + 5;
+    if (e < 20) {
+        const uint32_t v = g == 0 ? qs.x : g == 1 ? qs.y : g == 2 ? qs.z : g == 3 ? qs.w : d4;
+        return (int)((v >> (8 * k)) & 31u);
+    }
+    if (e < 24) return (int)(((qs.x >> sh) & 7u) | (((qs.y >> sh) & 3u) << 3));
+    if (e < 28) return (int)(((qs.z >> sh) & 7u) | (((qs.w >> sh) & 3u) << 3));
+    return (int)(((d4 >> sh) & 7u) | (((qs.y >> (sh + 2)) & 1u) << 3) | (((qs.w >> (sh + 2)) & 1u) << 4));
 }
 // Fit code byte: bits 0-2 dA+4, bits 3-5 dB+4 (ulps), bit 7 set: no pair
 // found, the (sub-)block takes the exact decode.  A = a0 moved by dA ulps;
@@ -894,10 +918,292 @@ __device__ __forceinline__ void group_q8(const TmqWork& w, int g) {
     if (w.y && r < t.rows) store_y(w, r, y);
 }
 
+// --------------------------------------------- MFMA decoders (Q5_0)
+// Integer fit.  Within one block of one row the int16 weight of code u is
+// g(u) = clamp16(roundf(fl(E(u) * row_inv))); ifit_kernel picks integers
+// AN = 256*alpha + a, BN = 256*beta + bb (0 <= a, bb < 256) with
+//     g(u) = floor((AN*u + BN) / 256) = alpha*u + beta + t(u),
+//     t(u) = (a*u + bb) >> 8  (0 <= t < 32)
+// for every code the block holds, AN and BN being the nominal slope
+// trunc(d*row_inv*256) and intercept 128 - 16*AN moved by the fit code
+// (plane pi: bits 0-2 dA + 4, bits 3-6 dB + 8).  Blocks it cannot fit keep
+// the closest pair and list the differing codes as corrections (TmqCorr).
+// t(u) is the high byte of the 16-bit a*u + bb, two codes per v_pk_mad_u16.
+//
+// The row sums go to v_mfma_i32_32x32x32_i8.  A wave owns 32 rows; lane
+// (j, h) = (l & 31, l >> 5) decodes block 2p + h of row j into the code
+// bytes U and the t bytes T: as B operands (32 columns = rows, K = the two
+// blocks' 16-code halves) they meet an A operand whose rows 4h, 4h+1, 4h+2
+// hold, over K half h only, xh, xl - 128 and ones of block 2p + h, so that
+// accumulator elements 0, 1, 2 of lane (j, h) are
+//     sum u*xh, sum u*(xl-128), sum u     over block 2p + h of row j
+// (element v of lane l: A row 8*(v/4) + 4*(l/32) + v%4, B column l & 31).
+// With xq = 256*xh + (xl - 128) + 128:
+//     sum_k w_k xq_k = alpha * S(u) + S(t) + beta * sum_k xq_k,
+//     S(v) = 256*sum v*xh + sum v*(xl-128) + 128*sum v.
+// S(u) is read out per block (its alpha differs); S(t) has coefficient 1
+// and stays in a second accumulator for the whole row.  Every partial is
+// an exact integer: the MFMA sums stay below 2^31, the row sum is int64.
+typedef int tmq_v4i __attribute__((ext_vector_type(4)));
+typedef int tmq_v16i __attribute__((ext_vector_type(16)));
+typedef unsigned short tmq_u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ tmq_v16i mfma_i8(tmq_v4i a, tmq_v4i b, tmq_v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+// two 16-bit lanes x*a + b (v_pk_mad_u16)
+__device__ __forceinline__ uint32_t pk_mad_u16(uint32_t x, uint32_t a, uint32_t b) {
+    const tmq_u16x2 r = __builtin_bit_cast(tmq_u16x2, x) * __builtin_bit_cast(tmq_u16x2, a) +
+                        __builtin_bit_cast(tmq_u16x2, b);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+struct IFit {
+    int alpha, beta;
+    uint32_t a2, b2;  // a and bb in both 16-bit lanes
+};
+// nominal slope: trunc(d * row_inv * 256), the float held inside +-(2^23 - 8)
+// (no real block comes near: |g| <= 32767 bounds it for any code but 16)
+__device__ __forceinline__ int ifit_an0(float d, float ri256) {
+    return (int)__builtin_amdgcn_fmed3f(d * ri256, -8388600.0f, 8388600.0f);
+}
+__device__ __forceinline__ IFit ifit_q5(uint32_t dbits, float ri256, uint32_t e) {
+    const int AN = ifit_an0(h2f(dbits), ri256) + (int)(e & 7u) - 4;
+    const int BN = 120 - 16 * AN + (int)((e >> 3) & 15u);
+    IFit f;
+    f.alpha = AN >> 8;
+    f.beta = BN >> 8;
+    f.a2 = ((uint32_t)AN & 255u) * 0x10001u;
+    f.b2 = ((uint32_t)BN & 255u) * 0x10001u;
+    return f;
+}
+// the fitted weight of code u (what the MFMA sums amount to)
+__device__ __forceinline__ int ifit_w(const IFit& f, int u) {
+    return f.alpha * u + f.beta + (int)(((f.a2 & 0xffffu) * (uint32_t)u + (f.b2 & 0xffffu)) >> 8);
+}
+// t bytes of four code bytes
+__device__ __forceinline__ uint32_t ifit_t4(uint32_t U, uint32_t a2, uint32_t b2) {
+    const uint32_t PE = pk_mad_u16(U & 0x00ff00ffu, a2, b2);
+    const uint32_t PO = pk_mad_u16(__builtin_amdgcn_perm(0u, U, 0x0c030c01u), a2, b2);
+    return __builtin_amdgcn_perm(PO, PE, 0x07030501u);
+}
+__device__ __forceinline__ Q5Blk q5i_load(const TmqTensorDev& t, int b, int r) {
+    const size_t o = (size_t)b * t.rows_pad + r;
+    Q5Blk k;
+    k.qs = ld16(t.pa + o * 16);
+    k.qh = ld4(t.pb + o * 4);
+    k.d = ld2(t.pd + o * 2);
+    k.e = ld1(t.pi + o);
+    return k;
+}
+
+// block pairs in flight per lane
+#ifndef TMQ_MFMA_DEPTH
+#define TMQ_MFMA_DEPTH 2
+#endif
+
+typedef __attribute__((address_space(3))) const tmq_v4i lv4i;
+typedef __attribute__((address_space(3))) const int32_t li32;
+typedef __attribute__((address_space(3))) const uint32_t lu32c;
+typedef __attribute__((address_space(3))) const uint16_t lu16;
+typedef __attribute__((address_space(3))) const uint8_t lu8;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Dynamic LDS of the MFMA decoders (mfma_lds_bytes): per wave a ring of
+// TMQ_MFMA_DEPTH stages, each one block of the wave's 64 rows as the LDS DMA
+// lays it down (lane l at 16*l of the qs part, 4*l of the others): qs
+// 1024 B, qh' 256 B, d 256 B, fit code 256 B; then the activation's operand
+// bytes (XA with the zero and ones chunks), the block sums, the waves' row
+// sums and the 64 rows' corrections.
+constexpr int kMfmaStage = 1792;
+constexpr int kMfmaWaves = gemv_waves(kQ5_0M);
+__host__ __device__ constexpr int mfma_xa_off() { return kMfmaWaves * TMQ_MFMA_DEPTH * kMfmaStage; }
+__host__ __device__ constexpr int mfma_xs_off(int nb) { return mfma_xa_off() + ((nb * 64 + 32 + 15) & ~15); }
+__host__ __device__ constexpr int mfma_part_off(int nb) { return mfma_xs_off(nb) + ((nb * 4 + 15) & ~15); }
+__host__ __device__ constexpr int mfma_lds_bytes(int nb) { return mfma_part_off(nb) + (kMfmaWaves + 1) * 64 * 8; }
+
+// s_waitcnt vmcnt(n) for the ring (n = loads issued after the awaited stage)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N <= 63, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ tmq_v4i mfma16(tmq_v4i a, tmq_v4i b, tmq_v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// 64 rows (group g), one per lane, the row's blocks split over the waves
+// (wave w: blocks w, w + 4, ...; any block count).  v_mfma_i32_16x16x64_i8 sees lane
+// l = 16q + n as B column n, K group q (16 codes) and A row n, K group q,
+// so lane l's codes of a block pair with A rows 4q .. 4q+2 only where those
+// hold the block's xh, xl - 128 and ones for K group q and zero elsewhere;
+// accumulator element v of lane l is then A row 4q + v, column n = lane l's
+// row: elements 0, 1, 2 are that row's S(u) parts.  Two MFMAs per block
+// take codes 0-15 and 16-31 (u), two more the t bytes.  The weights
+// stream global -> LDS through each wave's ring (LDS DMA: no registers hold
+// data in flight, and each wait is for the oldest stage alone); the
+// activation's operand bytes are copied into LDS once per workgroup.
+__device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
+    constexpr int NW = kMfmaWaves, D = TMQ_MFMA_DEPTH;
+    const TmqTensorDev& t = w.t;
+    const int nb = t.nb;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    const int nbw = (nb - wave + NW - 1) / NW;  // this wave's blocks (wave-uniform, >= 0)
+    // corrections of the group (uniform), fetched first
+    const int c0 = t.corr_off ? t.corr_off[g] : 0, c1 = t.corr_off ? t.corr_off[g + 1] : 0;
+    const float inv = t.row_inv[r], ri256 = inv * 256.0f;
+    const int n = t.cols;
+    uint8_t* xa = mfma_lds + mfma_xa_off();
+    int32_t* xsl = (int32_t*)(mfma_lds + mfma_xs_off(nb));
+    int64_t* part = (int64_t*)(mfma_lds + mfma_part_off(nb));
+    int64_t* fix = part + NW * 64;
+
+    // the activation copy first (global -> LDS), so that waiting for it does
+    // not wait for the ring's stages
+    {
+        const uint8_t* src = w.act + tmq_act_xa(n);
+        const int n16 = nb * 4 + 2;
+        for (int i0 = wave * 64; i0 < n16; i0 += NW * 64)
+            if (i0 + lane < n16)
+                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
+                                                 16, 0, 0);
+        const uint8_t* xs = w.act + tmq_act_xs(n);
+        for (int i0 = wave * 64; i0 < nb; i0 += NW * 64)
+            if (i0 + lane < nb)
+                __builtin_amdgcn_global_load_lds((const void*)(xs + (size_t)(i0 + lane) * 4),
+                                                 (lds_u8*)((uint8_t*)xsl + i0 * 4), 4, 0, 0);
+    }
+
+    uint8_t* ring = mfma_lds + wave * D * kMfmaStage;
+    const int ilast = max(nbw - 1, 0);
+    const size_t R = t.rows_pad;
+    // stage `slot` <- the wave's block i (clamped: the refills past the end
+    // reload the last block, so every step waits for the same count; a wave
+    // with no block of its own (nb < NW) loads block nb - 1 and uses none)
+    auto issue = [&](int i, int slot) {
+        const size_t o = (size_t)min(wave + NW * min(i, ilast), nb - 1) * R + r;
+        uint8_t* st = ring + slot * kMfmaStage;
+        __builtin_amdgcn_global_load_lds((const void*)(t.pa + o * 16), (lds_u8*)st, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(t.pb + o * 4), (lds_u8*)(st + 1024), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(t.pd + o * 2), (lds_u8*)(st + 1280), 2, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(t.pi + o), (lds_u8*)(st + 1536), 1, 0, 0);
+    };
+#pragma unroll
+    for (int i = 0; i < D; i++) issue(i, i);
+    // this wave's part of the activation copy has landed; the barrier makes
+    // every part visible (a plain s_barrier: the workgroup fence of
+    // __syncthreads would also wait for the ring's stages)
+    wait_vm<4 * D>();
+    asm volatile("s_barrier" ::: "memory");
+
+    // this lane's A operand: rows 4q, 4q+1 the block's xh and xl - 128 over
+    // K group q, row 4q+2 ones, the rest zero
+    uint32_t abase, astride, acoff;
+    {
+        const int q = lane >> 4, m = lane & 15, dg = m & 3;
+        const bool own = (m >> 2) == q;
+        const uint32_t zero = (uint32_t)nb * 64u;
+        abase = own && dg < 2 ? (uint32_t)(dg * 16) : own && dg == 2 ? zero + 16u : zero;
+        astride = own && dg < 2 ? 64u : 0u;
+        acoff = own && dg < 2 ? 32u : 0u;
+    }
+
+    int64_t acc = 0;
+    tmq_v4i Ct = {}, Cu = {};
+    int ap = 0, bp = 0, xp = 0;  // previous block: alpha, beta, block sum
+    const tmq_v4i Z = {};
+    // the wave's block i from stage `slot`: decode, read out the previous
+    // block's u sums (their MFMAs have long finished), then this block's
+    // MFMAs into the same accumulator; the stage is refilled D blocks ahead
+    auto step = [&](int i, int slot) {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<4 * (D - 1)>();
+        const int b = wave + NW * i;
+        const uint8_t* st = ring + slot * kMfmaStage;
+        Q5Blk k;
+        {
+            const tmq_v4i v = *(lv4i*)(st + lane * 16);
+            k.qs = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+        }
+        k.qh = *(lu32c*)(st + 1024 + lane * 4);
+        k.d = *(lu16*)(st + 1280 + lane * 4);
+        k.e = *(lu8*)(st + 1536 + lane * 4);
+        const uint32_t ao = abase + (uint32_t)b * astride;
+        const tmq_v4i A0 = *(lv4i*)(xa + ao), A1 = *(lv4i*)(xa + ao + acoff);
+        const int xsv = *(li32*)(xsl + b);
+        // the stage's reads are in registers before its refill overwrites it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i + D, slot);
+        const IFit f = ifit_q5(k.d, ri256, k.e);
+        uint32_t U[8], T[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            U[e] = q5_codes(k, e);
+            T[e] = ifit_t4(U[e], f.a2, f.b2);
+        }
+        const tmq_v4i U0 = {(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
+        const tmq_v4i U1 = {(int)U[4], (int)U[5], (int)U[6], (int)U[7]};
+        const tmq_v4i T0 = {(int)T[0], (int)T[1], (int)T[2], (int)T[3]};
+        const tmq_v4i T1 = {(int)T[4], (int)T[5], (int)T[6], (int)T[7]};
+        acc += (int64_t)ap * (Cu[0] * 256 + Cu[1] + Cu[2] * 128) + (int64_t)bp * xp;
+        __builtin_amdgcn_sched_barrier(0);  // the read-out before the overwrite: one accumulator
+        Cu = mfma16(A0, U0, Z);
+        Cu = mfma16(A1, U1, Cu);
+        Ct = mfma16(A0, T0, Ct);
+        Ct = mfma16(A1, T1, Ct);
+        ap = f.alpha;
+        bp = f.beta;
+        xp = xsv;
+    };
+    int ib = 0;
+    for (; ib + D <= nbw; ib += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) step(ib + i, i);
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++)
+        if (ib + i < nbw) step(ib + i, i);
+    acc += (int64_t)ap * (Cu[0] * 256 + Cu[1] + Cu[2] * 128) + (int64_t)bp * xp;
+    acc += (int64_t)Ct[0] * 256 + Ct[1] + (int64_t)Ct[2] * 128;
+    // no DMA into the ring may still run past this point
+    wait_vm<0>();
+    part[wave * 64 + lane] = acc;
+    if (threadIdx.x < 64) fix[threadIdx.x] = 0;
+    __syncthreads();
+    if (c1 > c0) {
+        // corrections (uniform branch): delta * sum of xq over their elements
+        const int32_t* x32 = (const int32_t*)(w.act + 16 + 6 * (size_t)n);
+        for (int c = c0 + (int)threadIdx.x; c < c1; c += 64 * NW) {
+            const uint4 e = t.corr[c];
+            int64_t s = 0;
+            for (uint32_t m = e.z; m; m &= m - 1) s += x32[e.y + __builtin_ctz(m)];
+            atomicAdd((unsigned long long*)&fix[(int)e.x - g * 64], (unsigned long long)((int64_t)(int32_t)e.w * s));
+        }
+        __syncthreads();
+    }
+    if (wave == 0 && r < t.rows) {
+        int64_t tot = fix[lane];
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += part[i * 64 + lane];
+        if (w.acc) w.acc[r] = tot;
+        // sim/tmac_gguf.cpp:1303-1305: y = 0.0f; y += (double)acc*x_scale/(double)row_inv
+        const float xs = *(const float*)w.act;
+        if (w.y) store_y(w, r, (float)(((double)tot * (double)xs) / (double)inv));
+    }
+}
+
 template <int FMT, bool CLAMP>
 __device__ __forceinline__ void run_group(const TmqWork& w, int g) {
-    if constexpr (FMT == kQ8_0) group_q8(w, g);
-    else group_ksplit<FMT, CLAMP>(w, g);
+    if constexpr (FMT == kQ8_0) {
+        group_q8(w, g);
+    } else if constexpr (FMT == kQ5_0M) {
+        group_mfma_q5(w, g);
+    } else {
+        group_ksplit<FMT, CLAMP>(w, g);
+    }
 }
 
 // one GEMV
@@ -940,15 +1246,10 @@ __device__ __forceinline__ void elems32(const TmqTensorDev& t, int r, int j0, fl
         const int b = j0 >> 5;
         const size_t o = (size_t)b * R + r;
         const uint4 qs = ld16(t.pa + o * 16);
-        const uint32_t qhp = ld4(t.pb + o * 4);
+        const uint32_t d4 = ld4(t.pb + o * 4);
         const float d = h2f(ld2(t.pd + o * 2));
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            const uint32_t by = byte_of(qs, e & 15);
-            const int nib = (e < 16) ? (int)(by & 15u) : (int)(by >> 4);
-            const int hb = (int)((qhp >> (8 * (e & 3) + (e >> 2))) & 1u);
-            E[e] = d * (float)((hb << 4) + nib - 16);
-        }
+        for (int e = 0; e < 32; e++) E[e] = d * (float)(q5_code(qs, d4, e) - 16);
     } else if (t.type == kQ4_K) {
         const int b = j0 >> 8, s = (j0 & 255) >> 5;
         const uint4 h = ld16(t.pb + p16(b, 0, 1, R, r));
@@ -1139,12 +1440,9 @@ __device__ float tensor_elem(const TmqTensorDev& t, int r, int j) {
     }
     if (t.type == kQ5_0) {
         const int b = j >> 5, e = j & 31;
-        const float d = h2f(ld2(t.pd + ((size_t)b * R + r) * 2));
-        const uint32_t by = t.pa[p16(b, 0, 1, R, r) + (e & 15)];
-        const uint32_t qhp = ld4(t.pb + ((size_t)b * R + r) * 4);
-        const int nib = (e < 16) ? (int)(by & 15u) : (int)(by >> 4);
-        const int hb = (int)((qhp >> (8 * (e & 3) + (e >> 2))) & 1u);
-        return d * (float)((hb << 4) + nib - 16);  // :307-322
+        const size_t o = (size_t)b * R + r;
+        const float d = h2f(ld2(t.pd + o * 2));
+        return d * (float)(q5_code(ld16(t.pa + o * 16), ld4(t.pb + o * 4), e) - 16);  // :307-322
     }
     if (t.type == kQ4_K) {
         const int b = j >> 8, off = j & 255, s = off >> 5, qp = off & 31;
@@ -1856,6 +2154,29 @@ __global__ __launch_bounds__(1024) void act_prep_kernel(TmqActJobs jobs) {
         xh[k] = ((uint32_t)(a >> 8) & 0xffffu) | ((uint32_t)(c >> 8) << 16);
         xl[k] = ((uint32_t)a & 0xffu) | (((uint32_t)c & 0xffu) << 16);
     }
+    // the MFMA decoders' operand bytes and block sums: four lanes per
+    // 32-element block, eight elements each (xq recomputed, as above)
+    const int nbx = (n + 31) / 32;
+    uint8_t* XA = J.act + tmq_act_xa(n);
+    int32_t* XS = (int32_t*)(J.act + tmq_act_xs(n));
+    for (int q = threadIdx.x; q < nbx * 4; q += blockDim.x) {
+        const int b = q >> 2, e0 = 32 * b + 8 * (q & 3);
+        uint32_t hi[2] = {0, 0}, lo[2] = {0x80808080u, 0x80808080u};
+        int sum = 0;
+        for (int i = 0; i < 8; i++) {
+            const int a = e0 + i < n ? (int)(int16_t)roundf(J.x[e0 + i] / s) : 0;
+            sum += a;
+            hi[i >> 2] = (hi[i >> 2] & ~(0xffu << (8 * (i & 3)))) | (((uint32_t)(a >> 8) & 0xffu) << (8 * (i & 3)));
+            lo[i >> 2] = (lo[i >> 2] & ~(0xffu << (8 * (i & 3)))) | ((((uint32_t)a & 0xffu) ^ 0x80u) << (8 * (i & 3)));
+        }
+        const int c = (q >> 1) & 1, pos = 8 * (q & 1);
+        *(uint2*)(XA + 64 * b + 32 * c + pos) = make_uint2(hi[0], hi[1]);
+        *(uint2*)(XA + 64 * b + 32 * c + 16 + pos) = make_uint2(lo[0], lo[1]);
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        if ((q & 3) == 0) XS[b] = sum;
+    }
+    if (threadIdx.x < 8) ((uint32_t*)(XA + 64 * nbx))[threadIdx.x] = threadIdx.x < 4 ? 0u : 0x01010101u;
 }
 
 // ------------------------------------------------------------- repack
@@ -1879,11 +2200,26 @@ __global__ void repack_kernel(int type, const uint8_t* __restrict__ src, TmqTens
         const uint8_t* s = src + idx * 22;
         pd[((size_t)b * R + r) * 2 + 0] = s[0];
         pd[((size_t)b * R + r) * 2 + 1] = s[1];
+        // ggml: code(e) = nibble e of qs (low nibbles 0-15, high 16-31) | bit e of qh << 4
         const uint32_t qh = (uint32_t)s[2] | ((uint32_t)s[3] << 8) | ((uint32_t)s[4] << 16) | ((uint32_t)s[5] << 24);
-        uint32_t qhp = 0;  // bit 8k+g <- bit 4g+k
-        for (int e = 0; e < 32; e++) qhp |= ((qh >> e) & 1u) << (8 * (e & 3) + (e >> 2));
-        *(uint32_t*)(pb + ((size_t)b * R + r) * 4) = qhp;
-        for (int i = 0; i < 16; i++) pa[p16(b, 0, 1, R, r) + i] = s[6 + i];
+        uint32_t D[5] = {0, 0, 0, 0, 0};
+        for (int e = 0; e < 32; e++) {
+            const uint32_t c = (uint32_t)((e < 16 ? s[6 + e] & 15 : s[6 + e - 16] >> 4) | (((qh >> e) & 1u) << 4));
+            const int k = e & 3, sh = 8 * k + 5;
+            if (e < 20) {
+                D[e >> 2] |= c << (8 * k);
+            } else if (e < 28) {
+                const int lo = e < 24 ? 0 : 2;  // D0/D1 or D2/D3
+                D[lo] |= (c & 7u) << sh;
+                D[lo + 1] |= (c >> 3) << sh;
+            } else {
+                D[4] |= (c & 7u) << sh;
+                D[1] |= ((c >> 3) & 1u) << (sh + 2);
+                D[3] |= (c >> 4) << (sh + 2);
+            }
+        }
+        for (int i = 0; i < 4; i++) *(uint32_t*)(pa + p16(b, 0, 1, R, r) + 4 * i) = D[i];
+        *(uint32_t*)(pb + ((size_t)b * R + r) * 4) = D[4];
     } else if (type == kQ4_K) {
         const uint8_t* s = src + idx * 144;
         for (int i = 0; i < 16; i++) pb[p16(b, 0, 1, R, r) + i] = s[i];
@@ -1922,12 +2258,9 @@ __global__ void rowstat_kernel(TmqTensorDev t, const float* __restrict__ aux, fl
             ok &= finite_h(db);
             const float d = h2f(db);
             const uint4 qs = ld16(t.pa + p16(b, 0, 1, R, r));
-            const uint32_t qhp = *(const uint32_t*)(t.pb + ((size_t)b * R + r) * 4);
+            const uint32_t d4 = *(const uint32_t*)(t.pb + ((size_t)b * R + r) * 4);
             for (int e = 0; e < 32; e++) {
-                uint32_t by = byte_of(qs, e & 15);
-                int nib = (e < 16) ? (int)(by & 15u) : (int)(by >> 4);
-                int hb = (int)((qhp >> (8 * (e & 3) + (e >> 2))) & 1u);
-                int q = (hb << 4) + nib - 16;
+                int q = q5_code(qs, d4, e) - 16;
                 float ab = fabsf(d * (float)q);
                 if (ab > mx) mx = ab;
             }
@@ -2082,6 +2415,76 @@ __global__ __launch_bounds__(256) void fit_kernel(TmqTensorDev t, int all_exact)
                     [](float a) { return -32.0f * a; });
             }
         }
+    }
+}
+
+// Integer fit codes of the MFMA decoders (see IFit): for block b of row r
+// the first (dA, dB) by growing |dA| then |dB| (dA in [-4, 3], dB in
+// [-8, 7]) whose fitted weights equal g(u) on every code the block holds,
+// else the pair with the fewest differing elements.  Pass 0 writes the code
+// and the number of differing codes; pass 1 writes one correction per
+// differing code from corr[off[r * nb + b]] on.  force: every block takes
+// the code dA = 3, dB = 7 (testing the corrections).
+__global__ __launch_bounds__(256) void ifit_kernel(TmqTensorDev t, int pass, int force, uint8_t* cnt,
+                                                   const int32_t* off, uint4* corr) {
+    const int r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (r >= t.rows_pad) return;
+    const size_t R = t.rows_pad, o = (size_t)b * R + r;
+    const float inv = t.row_inv[r], ri256 = inv * 256.0f;
+    const Q5Blk k = q5_load(t, b, r);
+    const float d = h2f(k.d);
+    int u[32], gv[32];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const uint32_t U = q5_codes(k, q);
+#pragma unroll
+        for (int i = 0; i < 4; i++) u[4 * q + i] = (int)((U >> (8 * i)) & 31u);
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++)
+        gv[i] = max(-32768, min(32767, round_away(d * (float)(u[i] - 16) * inv)));
+    uint32_t best = 0x7fu;
+    if (!force) {
+        int best_mis = 33;
+        for (int ia = 0; ia < 8 && best_mis; ia++) {
+            const int da = (ia & 1) ? -((ia + 1) >> 1) : (ia >> 1);  // 0, -1, 1, -2, 2, -3, 3, -4
+            for (int ib = 0; ib < 16 && best_mis; ib++) {
+                const int db = (ib & 1) ? -((ib + 1) >> 1) : (ib >> 1);  // 0, -1, 1, ..., 7, -8
+                const uint32_t e = (uint32_t)(da + 4) | ((uint32_t)(db + 8) << 3);
+                const IFit f = ifit_q5(k.d, ri256, e);
+                int mis = 0;
+#pragma unroll
+                for (int i = 0; i < 32; i++) mis += ifit_w(f, u[i]) != gv[i];
+                if (mis < best_mis) {
+                    best_mis = mis;
+                    best = e;
+                }
+            }
+        }
+    }
+    const IFit f = ifit_q5(k.d, ri256, best);
+    uint32_t bad = 0;  // codes whose fitted weight differs
+#pragma unroll
+    for (int i = 0; i < 32; i++)
+        if (ifit_w(f, u[i]) != gv[i]) bad |= 1u << u[i];
+    if (pass == 0) {
+        ((uint8_t*)t.pi)[o] = (uint8_t)best;
+        cnt[(size_t)r * t.nb + b] = (uint8_t)__builtin_popcount(bad);
+        return;
+    }
+    if (!bad) return;
+    int slot = off[(size_t)r * t.nb + b];
+    for (; bad; bad &= bad - 1) {
+        const int c = __builtin_ctz(bad);
+        uint32_t m = 0;
+        int delta = 0;
+#pragma unroll
+        for (int i = 0; i < 32; i++)
+            if (u[i] == c) {
+                m |= 1u << i;
+                delta = gv[i] - ifit_w(f, c);
+            }
+        corr[slot++] = make_uint4((uint32_t)r, (uint32_t)(32 * b), m, (uint32_t)delta);
     }
 }
 
@@ -2377,9 +2780,20 @@ int tmq_launch_fit(const TmqTensorDev& t, int all_exact, hipStream_t s) {
     return (int)hipGetLastError();
 }
 
+int tmq_launch_ifit(const TmqTensorDev& t, int pass, uint8_t* cnt, const int32_t* off, uint4* corr,
+                    hipStream_t s) {
+    if (t.type != kQ5_0 || !t.pi || t.clamp) return (int)hipErrorInvalidValue;
+    const char* fe = getenv("TMQ_IFIT_FORCE");
+    const int force = fe && atoi(fe) != 0;
+    const dim3 grid((t.rows_pad + 255) / 256, t.nb);
+    hipLaunchKernelGGL(ifit_kernel, grid, dim3(256), 0, s, t, pass, force, cnt, off, corr);
+    return (int)hipGetLastError();
+}
+
 template <template <int, bool> class K>
 static void* kernel_for(int type, int clamp) {
     switch (type) {
+    case kQ5_0M: return clamp ? nullptr : (void*)K<kQ5_0M, false>::fn();
     case kQ5_0: return clamp ? (void*)K<kQ5_0, true>::fn() : (void*)K<kQ5_0, false>::fn();
     case kQ4_K: return clamp ? (void*)K<kQ4_K, true>::fn() : (void*)K<kQ4_K, false>::fn();
     case kQ6_K: return clamp ? (void*)K<kQ6_K, true>::fn() : (void*)K<kQ6_K, false>::fn();
@@ -2400,20 +2814,28 @@ int tmq_launch_gemv(const TmqWork& w, hipStream_t s) {
         else hipLaunchKernelGGL(f32_gemv_kernel, dim3(g), dim3(64 * TMQ_WAVES), 0, s, w);
         return (int)hipGetLastError();
     }
-    void* k = kernel_for<GemvK>(w.t.type, w.t.clamp);
+    const int fmt = tmq_kernel_fmt(w.t);
+    void* k = kernel_for<GemvK>(fmt, w.t.clamp);
     if (!k) return (int)hipErrorInvalidValue;
     TmqWork arg = w;
     void* args[] = {&arg};
-    return (int)hipLaunchKernel(k, dim3(w.ngroups), dim3(64 * gemv_waves(w.t.type)), args, 0, s);
+    return (int)hipLaunchKernel(k, dim3(w.ngroups), dim3(64 * gemv_waves(fmt)), args,
+                                tmq_gemv_lds_bytes(fmt, w.t.cols), s);
 }
 
-int tmq_launch_chain(int type, int clamp, const TmqWork* works_dev, const int32_t* group_work_dev,
+size_t tmq_gemv_lds_bytes(int fmt, int max_cols) {
+    if (fmt != kQ5_0M) return 0;
+    return (size_t)mfma_lds_bytes(min(max_cols, TMQ_MFMA_MAX_COLS) / 32);
+}
+
+int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const int32_t* group_work_dev,
                      int total_groups, hipStream_t s) {
     if (total_groups <= 0) return 0;
-    void* k = kernel_for<ChainK>(type, clamp);
+    void* k = kernel_for<ChainK>(fmt, clamp);
     if (!k) return (int)hipErrorInvalidValue;
     void* args[] = {&works_dev, &group_work_dev};
-    return (int)hipLaunchKernel(k, dim3(total_groups), dim3(64 * gemv_waves(type)), args, 0, s);
+    return (int)hipLaunchKernel(k, dim3(total_groups), dim3(64 * gemv_waves(fmt)), args,
+                                tmq_gemv_lds_bytes(fmt, max_cols), s);
 }
 
 int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* out, hipStream_t s) {

@@ -57,6 +57,7 @@ struct tmq_tensor {
     TmqTensorDev dev{};
     void* alloc = nullptr;  // planes + row_inv + row_scale
     void* i16_alloc = nullptr;  // INT16 path weights + row scales (tmq_tensor_prepare_int16)
+    void* corr_alloc = nullptr;  // integer-fit corrections + their group offsets (MFMA decoders)
     uint64_t weight_bytes = 0;
 };
 

@@ -33,7 +33,7 @@ NOALLOC_MAX_COLS = 16384  # TMQ_NOALLOC_MAX_COLS
 EXPORTS = [
     "tmq_last_error", "tmq_version", "tmq_open", "tmq_close", "tmq_stream", "tmq_sync",
     "tmq_tensor_upload", "tmq_tensor_upload_dev", "tmq_tensor_free", "tmq_tensor_info",
-    "tmq_tensor_row_norm", "tmq_tensor_fit_stats", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_dev_noalloc",
+    "tmq_tensor_row_norm", "tmq_tensor_fit_stats", "tmq_tensor_ifit_stats", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_dev_noalloc",
     "tmq_gemv_partials", "tmq_route", "tmq_matmul_flags", "tmq_matmul_path", "tmq_gemv_dev_path",
     "tmq_gemv_partials_path", "tmq_tensor_prepare_int16",
     "tmq_vecmul_tile_q8", "tmq_vecmul_tile_q5_0_8x896", "tmq_vecmul_tile_q6_k",
@@ -106,6 +106,7 @@ def lib(path: str = LIB_PATH):
         "tmq_tensor_info": (I, [P, P, P, P, P]),
         "tmq_tensor_row_norm": (I, [P, P, P]),
         "tmq_tensor_fit_stats": (I, [P, P, C.POINTER(U64), C.POINTER(U64)]),
+        "tmq_tensor_ifit_stats": (I, [P, P, C.POINTER(U64), C.POINTER(U64)]),
         "tmq_matmul": (I, [P, P, P, P, I, I]),
         "tmq_gemv_dev": (I, [P, P, P, P, P]),
         "tmq_gemv_dev_noalloc": (I, [P, P, P, P, P]),
@@ -192,6 +193,13 @@ class Tensor:
         f, e = C.c_uint64(), C.c_uint64()
         _check(lib().tmq_tensor_fit_stats(self.ctx.handle, self.handle, C.byref(f), C.byref(e)))
         return f.value, e.value
+
+    def ifit_stats(self):
+        """(blocks, corrections) of the MFMA decoders' integer fit (0, 0:
+        the tensor takes the fitted-float decoders)"""
+        b, c = C.c_uint64(), C.c_uint64()
+        _check(lib().tmq_tensor_ifit_stats(self.ctx.handle, self.handle, C.byref(b), C.byref(c)))
+        return b.value, c.value
 
     def free(self):
         if self.handle:
