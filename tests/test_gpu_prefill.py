@@ -244,15 +244,19 @@ def test_norm_sum_mixed_ffn(ctx, monkeypatch):
         assert r[2].tolist() == ref[2].tolist()
 
 
-@pytest.mark.parametrize("chunk", [0, 512, 8])
-def test_prompt_matches_reference(model, chunk):
-    """the compiled reference's own process_prompt over a 24-token prompt
-    (tests/golden/model_prompt.npz): hidden state, logits and greedy tokens,
-    one token at a time (0), in one batch (512) and in chunks of 8"""
+@pytest.mark.parametrize("golden,chunk", [("model_prompt.npz", 0), ("model_prompt.npz", 512), ("model_prompt.npz", 8),
+                                          ("model_prompt_long.npz", 512), ("model_prompt_long.npz", 64),
+                                          ("model_prompt_long.npz", 0)])
+def test_prompt_matches_reference(model, golden, chunk):
+    """the compiled reference's own process_prompt (sim/tmac_gguf.cpp:
+    1992-1997) over a 24-token prompt (tests/golden/model_prompt.npz) and a
+    250-token one, close to its 256-position KV cache (MAX_SEQ_LEN,
+    :148; model_prompt_long.npz): hidden state, logits and greedy tokens,
+    one token at a time (0), in one batch (512) and in chunks (8, 64)"""
     from conftest import load_golden
-    g = load_golden("model_prompt.npz")
+    g = load_golden(golden)
     assert int(g["model_seed"]) == MODEL_SEED
-    print(f"[prefill] reference prompt, chunk {chunk}", flush=True)
+    print(f"[prefill] reference prompt {golden} ({g['prompt'].size} tokens), chunk {chunk}", flush=True)
     model.set_prefill(chunk)
     model.prompt(g["prompt"])
     h = model.hidden()
