@@ -1,9 +1,10 @@
-"""The engine's device expf (tmac-zynq-fpga_amd/csrc/tmq_mathf.h), built for the
-host from the same header, against the host libm expf that the reference
-engine calls (sim/tmac_gguf.cpp:460, :1650-1654).
+"""The engine's device expf and logf (tmac-zynq-fpga_amd/csrc/tmq_mathf.h),
+built for the host from the same header, against the host libm expf and logf
+that the reference engine calls (sim/tmac_gguf.cpp:460, :1650-1654).
 
-An exhaustive run over all 2^32 inputs (same check, stride 1) found no
-mismatch; the suite checks a strided sample plus the special values.  The
+Exhaustive runs over all 2^32 inputs (same checks, stride 1) found no
+mismatch for either; the suite checks a strided sample plus the special
+values.  The
 same header's RoPE table is checked against the compiled reference's
 apply_rope."""
 import ctypes as C
@@ -31,7 +32,19 @@ def mathf():
     L.tmqm_expf_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint32)]
     L.tmqm_expf.restype = C.c_float
     L.tmqm_expf.argtypes = [C.c_float]
+    L.tmqm_logf_mismatches.restype = C.c_uint64
+    L.tmqm_logf_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint32)]
+    L.tmqm_logf.restype = C.c_float
+    L.tmqm_logf.argtypes = [C.c_float]
     return L
+
+
+def _libm(name):
+    libm = C.CDLL("libm.so.6")
+    f = getattr(libm, name)
+    f.restype = C.c_float
+    f.argtypes = [C.c_float]
+    return f
 
 
 def test_expf_sample_matches_libm(mathf):
@@ -87,3 +100,30 @@ def test_rope_table_matches_reference_apply_rope(mathf):
         ref.lib.ref_apply_rope(q.ctypes.data, k.ctypes.data, p)
         for v in (q.reshape(-1, 32, 2), k.reshape(-1, 32, 2)):
             assert np.array_equal(v.view(np.uint32), np.broadcast_to(tab[p], v.shape).view(np.uint32)), p
+
+
+def test_logf_sample_matches_libm(mathf):
+    first = C.c_uint32(0)
+    bad = mathf.tmqm_logf_mismatches(977, 29, C.byref(first))
+    assert bad == 0, f"{bad} mismatches, first input bits {first.value:#010x}"
+
+
+def test_logf_softmax_range(mathf):
+    """[1, 4096]: the softmax denominators (the largest term is exp(0) = 1),
+    every float of [1, 2) and a dense sample above"""
+    libm_logf = _libm("logf")
+    xs = np.concatenate([np.arange(0x3F800000, 0x40000000, 7, dtype=np.uint32).view(np.float32),
+                         np.geomspace(2.0, 4096.0, 20001, dtype=np.float32)])
+    for x in xs[::97]:
+        a, e = mathf.tmqm_logf(float(x)), libm_logf(float(x))
+        assert np.float32(a).view(np.uint32) == np.float32(e).view(np.uint32), x
+
+
+@pytest.mark.parametrize("x", [0.0, -0.0, 1.0, -1.0, 2.0, 0.5, 1e-45, 1e-40, 1.1754942e-38, 3.4028235e38,
+                               float("inf"), float("-inf"), float("nan"), 0.6999999, 1.4142135, 1.0000001])
+def test_logf_special(mathf, x):
+    a, e = mathf.tmqm_logf(x), _libm("logf")(x)
+    if math.isnan(e):
+        assert math.isnan(a)
+    else:
+        assert np.float32(a).view(np.uint32) == np.float32(e).view(np.uint32)

@@ -6,8 +6,8 @@
 // Every fp32 operation follows sim/tmac_gguf.cpp's order: sums the reference
 // forms sequentially (attention scores, the softmax denominator, the context
 // accumulation) are formed sequentially here too, by one lane per sum, from
-// values staged in LDS.  Maxima are order free.  expf is tmq_expf (identical
-// to the host libm's expf); logf is the fp32 rounding of the fp64 log.
+// values staged in LDS.  Maxima are order free.  expf and logf are tmq_expf
+// and tmq_logf (identical to the host libm's expf and logf).
 //
 // The current position lives in device memory (TmqEngState.pos); the first
 // kernel of a step advances it, so a captured step replays without host
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
             }
         }
         for (; p <= pos; p++) es += ex[p];
-        s_stat[0] = (float)log((double)es) + mx;
+        s_stat[0] = tmq_math::tmq_logf(es) + mx;
     }
     __syncthreads();
     const float ls = s_stat[0];

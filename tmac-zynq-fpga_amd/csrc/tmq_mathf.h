@@ -9,9 +9,14 @@
 // is the correctly rounded 2^(i/32) minus (i << 47) (derivable from first
 // principles).  It agrees with the host's expf on all 2^32 inputs.
 //
-// logf: glibc's table of (1/c, log c) pairs is not derivable from first
-// principles, so tmq_logf is the correctly rounded fp32 log (fp64 log then
-// one rounding); it differs from glibc's logf by one ulp on ~2e-4 of inputs.
+// logf: glibc 2.35 implements logf with the same author's method (Arm
+// optimized-routines "logf.c"): x = 2^k z with z in [0x3f330000, 2x that),
+// the top 4 mantissa bits of z - 0x3f330000 pick a pair (1/c, log c) with c
+// near the centre of the subinterval, r = z/c - 1 exactly in double, and
+// log x = k ln2 + log c + r + A0 r^4 + (A1 r + A2) r^2 in double, rounded
+// once to float (0.82 ulp at most).  tmq_logf restates it with that
+// published table and polynomial; it agrees with the host's logf on all
+// 2^32 inputs, in the fma form used here and in the separate form alike.
 #pragma once
 #include <math.h>
 #include <stddef.h>
@@ -101,6 +106,56 @@ TMQ_HD inline float tmq_expf_tab(float x, const Tab& tab) {
 }
 
 TMQ_HD inline float tmq_expf(float x) { return tmq_expf_tab(x, Exp2TabConst{}); }
+
+// (1/c, log c) of the 16 subintervals of logf's reduced argument
+#define TMQ_LOGF_TAB                                                                                   \
+    {0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2, 0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2,     \
+     0x1.49539f0f010bp+0,  -0x1.01eae7f513a67p-2, 0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3,     \
+     0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3, 0x1.25e227b0b8eap+0,  -0x1.1aa2bc79c81p-3,       \
+     0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4, 0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4,     \
+     0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5, 0x1p+0,               0x0p+0,                    \
+     0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5,  0x1.ca4b31f026aap-1,  0x1.c5e53aa362eb4p-4,      \
+     0x1.b2036576afce6p-1, 0x1.526e57720db08p-3,  0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3,       \
+     0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2,  0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}
+#if defined(__HIPCC__)
+static __constant__ double tmq_logf_tab_dev[32] = TMQ_LOGF_TAB;
+#endif
+static const double tmq_logf_tab_host[32] = TMQ_LOGF_TAB;
+
+TMQ_HD inline double logf_tab(int j) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return tmq_logf_tab_dev[j];
+#else
+    return tmq_logf_tab_host[j];
+#endif
+}
+
+TMQ_HD inline float tmq_logf(float x) {
+    const double Ln2 = 0x1.62e42fefa39efp-1;
+    const double A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2, A2 = -0x1.ffffef20a4123p-2;
+    uint32_t ix = as_u32(x);
+    if (ix == 0x3f800000u) return 0.0f;
+    if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+        if (ix * 2 == 0) return -__builtin_inff();                           // log(+-0)
+        if (ix == 0x7f800000u) return x;                                     // log(inf)
+        if ((ix & 0x80000000u) || ix * 2 >= 0xff000000u) return __builtin_nanf("");
+        ix = as_u32(x * 0x1p23f) - (23u << 23);                              // subnormal
+    }
+    const uint32_t tmp = ix - 0x3f330000u;
+    const int i = (int)((tmp >> 19) % 16);
+    const int k = (int32_t)tmp >> 23;
+    const uint32_t iz = ix - (tmp & 0xff800000u);
+    float zf;
+    memcpy(&zf, &iz, 4);
+    const double invc = logf_tab(2 * i), logc = logf_tab(2 * i + 1);
+    const double r = __builtin_fma((double)zf, invc, -1.0);
+    const double y0 = __builtin_fma((double)k, Ln2, logc);
+    const double r2 = r * r;
+    double y = __builtin_fma(A1, r, A2);
+    y = __builtin_fma(A0, r2, y);
+    y = __builtin_fma(y, r2, y0 + r);
+    return (float)y;
+}
 
 // RoPE factors for positions [0, max_pos), as apply_rope forms them on the
 // host (sim/tmac_gguf.cpp:1531-1535): theta = 1/powf(base, (float)d/head_dim),

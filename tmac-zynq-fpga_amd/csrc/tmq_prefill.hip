@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
 // Attention of token t (position P = p0 + t) for the query heads of KV
 // head g: the decode engine's chains (attn_kernel) per query -- scores
 // summed over d in order and /8, max, exp terms summed over positions in
-// order, log via fp64, weights, the context summed over positions in order.
+// order, tmq_logf, weights, the context summed over positions in order.
 // The query rows are wave-uniform and read through the scalar cache.  Each
 // thread keeps the scores of its positions (tid + 512 k, k < NPASS) in
 // registers; LDS holds the exp terms, then the weights, of every position.
@@ -450,7 +450,7 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
 #pragma unroll
             for (int j = 0; j < 32; j++) es += p + j < np ? v[j] : 0.0f;
         }
-        stat[1][ln] = (float)log((double)es) + stat[0][ln];
+        stat[1][ln] = tmq_math::tmq_logf(es) + stat[0][ln];
     }
     __syncthreads();
     // weights (scores - log-sum) over the exp terms
