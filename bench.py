@@ -9,10 +9,17 @@ sets that one step streams twice the 256 MiB Infinity Cache (84 sets,
 550 MB); a step is one pass of the descriptor chain over all of them: one
 activation-quantisation launch plus one launch of every GEMV.
 
-value  = ggml weight bytes streamed per step / step time  (GB/s)
-roofline.achieved = the same bytes / average duration of the GEMV launch,
-         bracketed by HIP events on the library's stream inside the timed
-         steps themselves (so kernel_ms <= ms_per_step), against 8 TB/s.
+value  = ggml weight bytes streamed per step / step time  (GB/s).  A step is
+         one tmq_chain_run: the activation-quantisation launch plus the GEMV
+         launch; K steps back to back between two HIP events on the
+         library's stream.
+roofline.achieved = the same bytes / average duration of the GEMV launch:
+         K launches back to back on the prepared activation, timed the same
+         way right after the steps (same warmed clock), against 8 TB/s.
+warm-up: after a burst of launches the GPU's clock dips for a few hundred
+         launches before it settles, so GEMV chain workloads run at least
+         MIN_WARMUP untimed steps whatever --warmup asks; the line reports
+         the count run ("warmup") and the count asked ("warmup_requested").
 cpu_baseline = the reference's own matmul_fpga_q5_0 (sim/tmac_gguf.cpp:1221,
          compiled in place into oracle/_ref) or, where that was not built, its
          C restatement, on one host core over the same shapes; beside it the
@@ -42,6 +49,7 @@ METRIC = "quant GEMV weight GB/s (% HBM peak); Qwen2-0.5B batch-1 decode tok/s"
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 MALL_FACTOR = 2.0       # default working set: twice the Infinity Cache
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chain_q5_0_c2_traffic.txt")
+MIN_WARMUP = 300  # untimed chain steps before any GEMV measurement (clock settle)
 
 
 def log(msg):
@@ -166,31 +174,21 @@ def cpu_baseline(seconds):
 
 def measure(ctx, torch, dev, stream, name, steps, warmup, copies=None):
     """Returns (desc, weight bytes, step ms, kernel ms, n descriptors, copies).
-    A step = the activation-quantisation launch + the chain's GEMV launch;
-    the GEMV launch of every timed step is bracketed by its own HIP events,
-    so the kernel time is measured in the same warmed state as the step."""
+    A step = the activation-quantisation launch + the chain's GEMV launch.
+    The steps are timed as one run of K back to back (events only at the
+    ends: an event between launches costs the step a few microseconds);
+    the GEMV launch alone is timed right after in the same way."""
     copies = copies or copies_for(name)
     desc_txt, x_d, tensors, descs, ys = build_workload(ctx, torch, dev, name, copies)
     chain = ctx.chain(descs)
     wbytes = chain.weight_bytes
     log(f"{name}: {len(descs)} descriptors ({copies} weight sets), {wbytes} weight bytes per step")
-    for _ in range(warmup):
+    for _ in range(max(warmup, MIN_WARMUP)):
         chain.run()
     ctx.sync()
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for a, b in ev:
-        chain.prepare()
-        a.record(stream)
-        chain.launch()
-        b.record(stream)
-    e1.record(stream)
-    e1.synchronize()
-    step_ms = e0.elapsed_time(e1) / steps
-    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    step_ms = time_events(torch, stream, chain.run, steps)
+    kern_ms = time_events(torch, stream, chain.launch, steps)
     ctx.sync()
     torch.cuda.synchronize()
     chain.free()
@@ -416,7 +414,8 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": max(args.warmup, MIN_WARMUP),
+        "warmup_requested": args.warmup,
         "ms_per_step": round(step_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",

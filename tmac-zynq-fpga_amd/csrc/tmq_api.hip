@@ -190,12 +190,14 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
 // codes and per-(row, block) correction counts on the device, the offsets
 // of the corrections (rows in order, so each 64-row group's are contiguous)
 // on the host, then the corrections themselves.  Tensors with more than
-// TMQ_MFMA_MAX_COLS columns, and any uploaded under TMQ_NOMFMA=1 (testing),
-// stay on the fitted-float decoders.
+// TMQ_MFMA_MAX_COLS columns or a code plane of 2 GiB or more (the decoders
+// address the planes with 32-bit buffer offsets), and any uploaded under
+// TMQ_NOMFMA=1 (testing), stay on the fitted-float decoders.
 int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
     TmqTensorDev& d = t->dev;
     const char* nm = getenv("TMQ_NOMFMA");
-    if (!d.pi || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS) {
+    if (!d.pi || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS ||
+        (uint64_t)d.rows_pad * (uint64_t)d.nb * 16 >= (1ull << 31)) {
         d.pi = nullptr;
         return 0;
     }

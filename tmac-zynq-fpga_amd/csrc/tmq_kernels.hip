@@ -94,6 +94,44 @@ __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const gu16*
 typedef __attribute__((address_space(1))) const uint8_t gu8;
 __device__ __forceinline__ uint32_t ld1(const uint8_t* p) { return *(const gu8*)p; }
 
+// Weight-stream loads: every weight byte is read once per GEMV, so they
+// carry the nontemporal cache policy (gfx950 "nt": streamed through the
+// caches without displacing reused lines), worth ~10 % of read bandwidth
+// on a plain stream.  TMQ_CPOL_NT is the same bit for the LDS-DMA loads.
+#ifndef TMQ_WEIGHT_NT
+#define TMQ_WEIGHT_NT 1
+#endif
+#define TMQ_CPOL_NT (TMQ_WEIGHT_NT ? 2 : 0)
+__device__ __forceinline__ uint4 ldw16(const uint8_t* p) {
+#if TMQ_WEIGHT_NT
+    const tmq_u32x4 v = __builtin_nontemporal_load((const gu4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return ld16(p);
+#endif
+}
+__device__ __forceinline__ uint32_t ldw4(const uint8_t* p) {
+#if TMQ_WEIGHT_NT
+    return __builtin_nontemporal_load((const gu32*)p);
+#else
+    return ld4(p);
+#endif
+}
+__device__ __forceinline__ uint32_t ldw2(const uint8_t* p) {
+#if TMQ_WEIGHT_NT
+    return __builtin_nontemporal_load((const gu16*)p);
+#else
+    return ld2(p);
+#endif
+}
+__device__ __forceinline__ uint32_t ldw1(const uint8_t* p) {
+#if TMQ_WEIGHT_NT
+    return __builtin_nontemporal_load((const gu8*)p);
+#else
+    return ld1(p);
+#endif
+}
+
 // wave index, known to the compiler to be wave-uniform (an SGPR)
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
@@ -247,10 +285,10 @@ struct Q5Blk {
 __device__ __forceinline__ Q5Blk q5_load(const TmqTensorDev& t, int b, int r) {
     const size_t o = (size_t)b * t.rows_pad + r;
     Q5Blk k;
-    k.qs = ld16(t.pa + o * 16);
-    k.qh = ld4(t.pb + o * 4);
-    k.d = ld2(t.pd + o * 2);
-    k.e = ld1(t.pe + o);
+    k.qs = ldw16(t.pa + o * 16);
+    k.qh = ldw4(t.pb + o * 4);
+    k.d = ldw2(t.pd + o * 2);
+    k.e = ldw1(t.pe + o);
     return k;
 }
 // the 5-bit codes of elements 4g..4g+3 as bytes
@@ -605,10 +643,10 @@ struct Q4KQ {
 __device__ __forceinline__ Q4KQ q4kq_load(const TmqTensorDev& t, int b, int q, int r) {
     const size_t R = t.rows_pad;
     Q4KQ k;
-    k.h = ld16(t.pb + p16(b, 0, 1, R, r));
-    k.qa = ld16(t.pa + p16(b, 2 * q, 8, R, r));
-    k.qb = ld16(t.pa + p16(b, 2 * q + 1, 8, R, r));
-    k.e = ld2(t.pe + ((size_t)b * R + r) * 8 + 2 * q);
+    k.h = ldw16(t.pb + p16(b, 0, 1, R, r));
+    k.qa = ldw16(t.pa + p16(b, 2 * q, 8, R, r));
+    k.qb = ldw16(t.pa + p16(b, 2 * q + 1, 8, R, r));
+    k.e = ldw2(t.pe + ((size_t)b * R + r) * 8 + 2 * q);
     return k;
 }
 struct Q6KQ {
@@ -619,12 +657,12 @@ __device__ __forceinline__ Q6KQ q6kq_load(const TmqTensorDev& t, int b, int q, i
     const size_t R = t.rows_pad;
     const int half = q >> 1, lc = q & 1;
     Q6KQ k;
-    k.qla = ld16(t.pa + p16(b, half * 4 + lc, 8, R, r));
-    k.qlb = ld16(t.pa + p16(b, half * 4 + 2 + lc, 8, R, r));
-    k.qhc = ld16(t.pb + p16(b, half * 2 + lc, 4, R, r));
-    k.sc = ld16(t.pc + p16(b, 0, 1, R, r));
-    k.e = ld16(t.pe + ((size_t)b * R + r) * 16);
-    k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
+    k.qla = ldw16(t.pa + p16(b, half * 4 + lc, 8, R, r));
+    k.qlb = ldw16(t.pa + p16(b, half * 4 + 2 + lc, 8, R, r));
+    k.qhc = ldw16(t.pb + p16(b, half * 2 + lc, 4, R, r));
+    k.sc = ldw16(t.pc + p16(b, 0, 1, R, r));
+    k.e = ldw16(t.pe + ((size_t)b * R + r) * 16);
+    k.d = ldw2(t.pd + ((size_t)b * R + r) * 2);
     return k;
 }
 
@@ -736,9 +774,9 @@ struct Q8Blk {
 __device__ __forceinline__ Q8Blk q8_load(const TmqTensorDev& t, int b, int r) {
     const size_t R = t.rows_pad;
     Q8Blk k;
-    k.v0 = ld16(t.pa + p16(b, 0, 2, R, r));
-    k.v1 = ld16(t.pa + p16(b, 1, 2, R, r));
-    k.d = ld2(t.pd + ((size_t)b * R + r) * 2);
+    k.v0 = ldw16(t.pa + p16(b, 0, 2, R, r));
+    k.v1 = ldw16(t.pa + p16(b, 1, 2, R, r));
+    k.d = ldw2(t.pd + ((size_t)b * R + r) * 2);
     return k;
 }
 template <class AT>
@@ -1022,6 +1060,12 @@ __host__ __device__ constexpr int mfma_xs_off(int nb) { return mfma_xa_off() + (
 __host__ __device__ constexpr int mfma_part_off(int nb) { return mfma_xs_off(nb) + ((nb * 4 + 15) & ~15); }
 __host__ __device__ constexpr int mfma_lds_bytes(int nb) { return mfma_part_off(nb) + (kMfmaWaves + 1) * 64 * 8; }
 
+// raw buffer resource over `bytes` bytes at p (gfx9 word 3: 32-bit data
+// format, no stride / swizzle); out-of-range reads return 0
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // s_waitcnt vmcnt(n) for the ring (n = loads issued after the awaited stage)
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -1083,13 +1127,22 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     // stage `slot` <- the wave's block i (clamped: the refills past the end
     // reload the last block, so every step waits for the same count; a wave
     // with no block of its own (nb < NW) loads block nb - 1 and uses none)
+    // Buffer loads: the planes' base addresses and sizes in scalar resources,
+    // the block's element offset (wave-uniform) in a scalar register and
+    // the lane's in a constant vector register, so no vector instruction
+    // forms an address (the host keeps every plane below 2^31 bytes).
+    const uint32_t pl = (uint32_t)(R * (size_t)nb);  // elements per plane
+    const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(t.pa, 16 * pl), rsb = buf_rsrc(t.pb, 4 * pl);
+    const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(t.pd, 2 * pl), rsi = buf_rsrc(t.pi, pl);
+    const int la16 = lane * 16, la4 = lane * 4, la2 = lane * 2;
     auto issue = [&](int i, int slot) {
-        const size_t o = (size_t)min(wave + NW * min(i, ilast), nb - 1) * R + r;
+        const int blk = __builtin_amdgcn_readfirstlane(min(wave + NW * min(i, ilast), nb - 1));
+        const int ob = blk * (int)R + g * 64;
         uint8_t* st = ring + slot * kMfmaStage;
-        __builtin_amdgcn_global_load_lds((const void*)(t.pa + o * 16), (lds_u8*)st, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(t.pb + o * 4), (lds_u8*)(st + 1024), 4, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(t.pd + o * 2), (lds_u8*)(st + 1280), 2, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(t.pi + o), (lds_u8*)(st + 1536), 1, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)st, 16, la16, 16 * ob, 0, TMQ_CPOL_NT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_u8*)(st + 1024), 4, la4, 4 * ob, 0, TMQ_CPOL_NT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsd, (lds_u8*)(st + 1280), 2, la2, 2 * ob, 0, TMQ_CPOL_NT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 1536), 1, lane, ob, 0, TMQ_CPOL_NT);
     };
 #pragma unroll
     for (int i = 0; i < D; i++) issue(i, i);
