@@ -1,6 +1,7 @@
-"""GPU parity of the MFMA decoders: Q5_0 GEMVs whose blocks are decoded by
-the upload-time integer fit and summed on the int8 MFMA, with the codes the
-fit cannot reproduce applied as corrections.
+"""GPU parity of the MFMA decoders: Q5_0, Q4_K and Q6_K GEMVs whose blocks
+(K-quants: sub-blocks) are decoded by the upload-time integer fit and summed
+on the int8 MFMA, with the codes the fit cannot reproduce applied as
+corrections.
 
 Bar: bit-exact int64 row sums and fp32 outputs against the CPU oracle
 (oracle/tmq_oracle.c: tmqo_matmul_q5_0, the restatement of
@@ -12,7 +13,7 @@ through the corrections and must give the same sums.
 """
 import numpy as np
 import pytest
-from oracle import Q5_0
+from oracle import Q4_K, Q5_0, Q6_K
 from tmq import synth
 
 pytestmark = pytest.mark.gpu
@@ -33,17 +34,17 @@ def eligible(cols):
     return cols <= MFMA_MAX_COLS
 
 
-def check(ctx, oracle, rows, cols, seed):
-    w = synth.gen_weights(Q5_0, rows, cols, seed)
+def check(ctx, oracle, rows, cols, seed, qt=Q5_0):
+    w = synth.gen_weights(qt, rows, cols, seed)
     x = synth.gen_x(cols, seed + 1)
-    t = ctx.upload(Q5_0, rows, cols, w)
+    t = ctx.upload(qt, rows, cols, w)
     blocks, corr = t.ifit_stats()
     y = ctx.matmul(t, x)
     acc, xs = ctx.partials(t, x)
     t.free()
-    ye = oracle.matmul(Q5_0, w, x, rows, cols)
+    ye = oracle.matmul(qt, w, x, rows, cols)
     xq, _ = oracle.quantize_act(x)
-    ae = oracle.acc(Q5_0, w, rows, cols, xq, oracle.row_inv(Q5_0, w, rows, cols))
+    ae = oracle.acc(qt, w, rows, cols, xq, oracle.row_inv(qt, w, rows, cols))
     assert np.array_equal(acc, ae), report("acc", acc, ae)
     assert np.array_equal(bits(y), bits(ye)), report("y", bits(y), bits(ye))
     return blocks, corr
@@ -86,3 +87,53 @@ def test_mfma_q5_off(ctx, oracle, monkeypatch):
     monkeypatch.setenv("TMQ_NOMFMA", "1")
     print("[mfma] Q5_0 896x896 without the MFMA decoders", flush=True)
     assert check(ctx, oracle, 896, 896, 1803) == (0, 0)
+
+
+# K-quant sub-blocks per 256-column super-block
+SUBS = {Q4_K: 8, Q6_K: 16}
+
+
+@pytest.mark.parametrize("qt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows,cols", [(896, 4864), (64, 256), (100, 512), (130, 768), (200, 1024),
+                                       (64, MFMA_MAX_COLS), (64, MFMA_MAX_COLS + 256)])
+def test_mfma_kquant_bitexact(ctx, oracle, qt, rows, cols):
+    """K-quants on the MFMA decoders: every row's int64 sum and fp32 output
+    bit-exact; one to 32 super-blocks per row (quarters per wave 1 to 32),
+    rows not a multiple of 64; wider than 8192 columns stays on the
+    fitted-float decoders."""
+    print(f"[mfma] type {qt} {rows}x{cols}", flush=True)
+    blocks, corr = check(ctx, oracle, rows, cols, 2300 + rows + cols + qt, qt)
+    if eligible(cols):
+        assert blocks == rows * cols // 256 * SUBS[qt]
+        # the fit misses about one Q6_K sub-block in 200 (a few per cent on
+        # small tensors) and almost no Q4_K one
+        assert corr <= max(32, blocks // 25)
+    else:
+        assert (blocks, corr) == (0, 0)
+
+
+@pytest.mark.parametrize("qt", [Q4_K, Q6_K])
+def test_mfma_kquant_corrections(ctx, oracle, monkeypatch, qt):
+    """Every sub-block on one fixed wrong fit (TMQ_IFIT_FORCE=1): most codes
+    become corrections, the sums stay exact."""
+    monkeypatch.setenv("TMQ_IFIT_FORCE", "1")
+    print(f"[mfma] type {qt} 256x4864 forced fit", flush=True)
+    blocks, corr = check(ctx, oracle, 256, 4864, 2401 + qt, qt)
+    assert blocks == 256 * 19 * SUBS[qt]
+    assert corr > blocks // 2  # most sub-blocks carry corrections
+
+
+def test_mfma_q6k_misfits_present(ctx, oracle):
+    """The BASELINE Q6_K shape holds sub-blocks the integer fit cannot
+    reproduce, so the natural corrections are exercised."""
+    print("[mfma] Q6_K 896x4864 natural corrections", flush=True)
+    blocks, corr = check(ctx, oracle, 896, 4864, 2402, Q6_K)
+    assert corr > 0
+
+
+@pytest.mark.parametrize("qt", [Q4_K, Q6_K])
+def test_mfma_kquant_off(ctx, oracle, monkeypatch, qt):
+    """TMQ_NOMFMA=1 keeps a K-quant tensor on the fitted-float decoders."""
+    monkeypatch.setenv("TMQ_NOMFMA", "1")
+    print(f"[mfma] type {qt} without the MFMA decoders", flush=True)
+    assert check(ctx, oracle, 128, 1024, 2403 + qt, qt) == (0, 0)

@@ -63,8 +63,11 @@ def test_fit_stats_and_exact_decode(ctx, oracle, qt, rows, cols, monkeypatch):
     """Every sub-block is fitted or flagged; the flagged ones (present in the
     Q5_0 and Q6_K tensors: the linear form has no pair for them) and a
     tensor uploaded with TMQ_NOFIT=1 (every sub-block on the exact decode)
-    give the oracle's int64 sums exactly."""
+    give the oracle's int64 sums exactly.  The fitted-float decoders are the
+    ones the decode engine runs; TMQ_NOMFMA=1 keeps the standalone GEMV on
+    them (every tensor here would otherwise take the MFMA decoders)."""
     print(f"[fit] type={qt} {rows}x{cols}", flush=True)
+    monkeypatch.setenv("TMQ_NOMFMA", "1")
     w = synth.gen_weights(qt, rows, cols, 900 + rows)
     x = synth.gen_x(cols, 901)
     xq, _ = oracle.quantize_act(x)
@@ -79,7 +82,6 @@ def test_fit_stats_and_exact_decode(ctx, oracle, qt, rows, cols, monkeypatch):
     assert np.array_equal(acc, ae), report("acc", acc, ae)
     t.free()
     monkeypatch.setenv("TMQ_NOFIT", "1")
-    monkeypatch.setenv("TMQ_NOMFMA", "1")  # Q5_0: the standalone GEMV's exact decode, not the MFMA one
     t = ctx.upload(qt, rows, cols, w)
     assert t.fit_stats() == (0, rows * cols // FIT_SUB[qt])
     acc, _ = ctx.partials(t, x)

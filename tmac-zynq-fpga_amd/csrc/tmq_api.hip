@@ -187,21 +187,23 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
 }
 
 // Integer fit codes and corrections of the MFMA decoders (t->dev.pi):
-// codes and per-(row, block) correction counts on the device, the offsets
-// of the corrections (rows in order, so each 64-row group's are contiguous)
-// on the host, then the corrections themselves.  Tensors with more than
-// TMQ_MFMA_MAX_COLS columns or a code plane of 2 GiB or more (the decoders
-// address the planes with 32-bit buffer offsets), and any uploaded under
-// TMQ_NOMFMA=1 (testing), stay on the fitted-float decoders.
+// codes and per-(row, block, fitted unit) correction counts on the device,
+// the offsets of the corrections (rows in order, so each 64-row group's are
+// contiguous) on the host, then the corrections themselves.  Tensors with
+// more than TMQ_MFMA_MAX_COLS columns or a weight plane of 2 GiB or more (the
+// decoders address the planes with 32-bit buffer offsets), tensors with an
+// external row_inv (clamped), and any uploaded under TMQ_NOMFMA=1 (testing)
+// stay on the fitted-float decoders.
 int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
     TmqTensorDev& d = t->dev;
     const char* nm = getenv("TMQ_NOMFMA");
-    if (!d.pi || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS ||
-        (uint64_t)d.rows_pad * (uint64_t)d.nb * 16 >= (1ull << 31)) {
+    const uint64_t plane = (uint64_t)d.rows_pad * (uint64_t)d.nb * (d.type == TMQ_TYPE_Q5_0 ? 16 : 128);
+    if (!d.pi || d.clamp || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS || plane >= (1ull << 31)) {
         d.pi = nullptr;
         return 0;
     }
-    const size_t n = (size_t)d.rows_pad * d.nb;
+    const int subs = tmq_ifit_subs(d.type);
+    const size_t n = (size_t)d.rows_pad * d.nb * subs;
     uint8_t* cnt = nullptr;
     int32_t* offd = nullptr;
     auto done = [&](int code) {
@@ -221,8 +223,9 @@ int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
     const int ng = d.rows_pad / 64;
     std::vector<int32_t> goff(ng + 1);
     int64_t total = 0;
+    const size_t per_group = (size_t)64 * d.nb * subs;
     for (size_t i = 0; i < n; i++) {
-        if (i % ((size_t)64 * d.nb) == 0) goff[i / ((size_t)64 * d.nb)] = (int32_t)total;
+        if (i % per_group == 0) goff[i / per_group] = (int32_t)total;
         off[i] = (int32_t)total;
         total += c[i];
     }
@@ -382,11 +385,13 @@ void act_from_int16(const int16_t* xq, int n, std::vector<uint8_t>& buf) {
     // MFMA decoders' operand bytes and block sums (tmq_internal.h)
     uint8_t* xa = buf.data() + tmq_act_xa(n);
     int32_t* xs = (int32_t*)(buf.data() + tmq_act_xs(n));
+    int32_t* xs16 = (int32_t*)(buf.data() + tmq_act_xs16(n));
     for (int k = 0; k < (int)tmq_act_nbx(n) * 32; k++) {
         const int v = k < n ? xq[k] : 0, b = k >> 5, i = k & 31;
         xa[64 * b + 32 * (i >> 4) + (i & 15)] = (uint8_t)(v >> 8);
         xa[64 * b + 32 * (i >> 4) + 16 + (i & 15)] = (uint8_t)((v & 255) ^ 0x80);
         xs[b] += v;
+        xs16[k >> 4] += v;
     }
     memset(xa + 64 * tmq_act_nbx(n) + 16, 1, 16);
 }
@@ -611,7 +616,7 @@ int tmq_tensor_ifit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* blocks, u
     if (!ctx || !t || !blocks || !corrections) return tmq_fail(TMQ_ERR_ARG, "null argument");
     *blocks = *corrections = 0;
     if (!t->dev.pi) return 0;
-    *blocks = (uint64_t)t->dev.rows * t->dev.nb;
+    *blocks = (uint64_t)t->dev.rows * t->dev.nb * tmq_ifit_subs(t->dev.type);
     if (!t->dev.corr_off) return 0;
     int rc = tmq_rt_set_device(ctx);
     if (rc) return rc;

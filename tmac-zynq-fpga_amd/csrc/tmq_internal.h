@@ -34,9 +34,11 @@
 // its long rows split into shorter waves; measured 4 % faster for Q6_K and
 // 4 % slower for Q4_K on the 896x4864 BASELINE shapes)
 // Kernel format of a standalone / chain GEMV: the tensor's type, or
-// TMQ_FMT_Q5_0_MFMA for a Q5_0 tensor on the MFMA decoders (its integer fit
-// built at upload).
+// TMQ_FMT_*_MFMA for a Q5_0 / Q4_K / Q6_K tensor on the MFMA decoders (its
+// integer fit built at upload).
 #define TMQ_FMT_Q5_0_MFMA 106
+#define TMQ_FMT_Q4_K_MFMA 112
+#define TMQ_FMT_Q6_K_MFMA 114
 constexpr int gemv_waves(int fmt) { return fmt == 14 ? 8 : TMQ_WAVES; }
 #define TMQ_Q8_MAX_TILES 256  // cols <= 16384 for Q8_0
 
@@ -50,7 +52,8 @@ struct TmqTensorDev {
     const uint8_t* pc;
     const uint8_t* pd;
     const uint8_t* pe;       // fit codes (Q5_0: 1 B, Q4_K: 8 B, Q6_K: 16 B per block and row)
-    const uint8_t* pi;       // integer fit codes of the MFMA decoders (Q5_0: 1 B per block and row)
+    const uint8_t* pi;       // integer fit codes of the MFMA decoders: Q5_0 [b][r] 1 B; Q4_K [b][q][r] 2 B
+                             // (sub-blocks 2q, 2q+1); Q6_K [b][q][r] 4 B (the quarter's four sub-blocks)
     const uint4* corr;       // their corrections (TmqCorr), grouped by 64-row group
     const int32_t* corr_off; // [rows_pad/64 + 1] first correction of each group (null: none)
     const float* row_inv;    // Q5_0/K-quants: row_inv; Q8_0: 1/row_scale (guarded)
@@ -60,7 +63,9 @@ struct TmqTensorDev {
 };
 
 static inline int tmq_kernel_fmt(const TmqTensorDev& t) {
-    return t.type == 6 && t.pi && !t.clamp ? TMQ_FMT_Q5_0_MFMA : t.type;
+    if (!t.pi || t.clamp) return t.type;
+    return t.type == 6 ? TMQ_FMT_Q5_0_MFMA : t.type == 12 ? TMQ_FMT_Q4_K_MFMA : t.type == 14 ? TMQ_FMT_Q6_K_MFMA
+                                                                                       : t.type;
 }
 
 // matmul branch a work takes (sim/tmac_gguf.cpp:473-493)
@@ -73,12 +78,14 @@ enum { TMQ_WPATH_FPGA = 0, TMQ_WPATH_INT16 = 1, TMQ_WPATH_FP32 = 2 };
 //        block b: int8 xh of elements 0-15, int8 xl-128 of 0-15, xh of
 //        16-31, xl-128 of 16-31; then 16 zero bytes and 16 bytes of 1
 //   +XS  (XA + 64*nbx + 32) int32 sum of xq over each block, padded to 16 B
+//   +XS16 (tmq_act_xs16) int32 sum of xq over each 16 elements, padded to 16 B
 // XH/XL hold (xq >> 8, xq & 255) as int16 pairs (elements 2k, 2k+1), so that
 // sum w*xq = 256*sum w*xh + sum w*xl with every partial inside int32.
 constexpr uint64_t tmq_act_nbx(int n) { return ((uint64_t)n + 31) / 32; }
 constexpr uint64_t tmq_act_xa(int n) { return (16 + (uint64_t)n * 10 + 15) & ~(uint64_t)15; }
 constexpr uint64_t tmq_act_xs(int n) { return tmq_act_xa(n) + 64 * tmq_act_nbx(n) + 32; }
-constexpr uint64_t tmq_act_bytes(int n) { return tmq_act_xs(n) + ((4 * tmq_act_nbx(n) + 15) & ~(uint64_t)15) + 16; }
+constexpr uint64_t tmq_act_xs16(int n) { return tmq_act_xs(n) + ((4 * tmq_act_nbx(n) + 15) & ~(uint64_t)15); }
+constexpr uint64_t tmq_act_bytes(int n) { return tmq_act_xs16(n) + ((8 * tmq_act_nbx(n) + 15) & ~(uint64_t)15) + 16; }
 
 // One correction of the MFMA decoders' integer fit (uint4): the block's
 // fitted weights differ from the exact ones by `delta` on the elements
@@ -213,12 +220,15 @@ int tmq_launch_fit(const TmqTensorDev& t, int all_exact, hipStream_t s);
 // bytes of fit codes per block and row (0: no fitted decode)
 static inline int tmq_fit_codes(int type) { return type == 6 ? 1 : type == 12 ? 8 : type == 14 ? 16 : 0; }
 // integer fit codes (plane pi) of the MFMA decoders.  pass 0: the codes and
-// the number of corrections of each (row, block) into cnt[r * nb + b];
-// pass 1: the corrections of (row, block) from corr[off[r * nb + b]] on.
+// the number of corrections of each (row, block, fitted unit) into
+// cnt[(r * nb + b) * subs + k] (subs = tmq_ifit_subs); pass 1: the
+// corrections of each from corr[off[...]] on.
 int tmq_launch_ifit(const TmqTensorDev& t, int pass, uint8_t* cnt, const int32_t* off, uint4* corr,
                     hipStream_t s);
 // bytes of integer fit codes per block and row (0: type without the MFMA decoder)
-static inline int tmq_ifit_codes(int type) { return type == 6 ? 1 : 0; }
+static inline int tmq_ifit_codes(int type) { return type == 6 ? 1 : type == 12 ? 8 : type == 14 ? 16 : 0; }
+// fitted units per block of the MFMA decoders (Q5_0 block, K-quant sub-block)
+static inline int tmq_ifit_subs(int type) { return type == 6 ? 1 : type == 12 ? 8 : type == 14 ? 16 : 0; }
 // widest activation the MFMA decoders keep in LDS (wider rows take the
 // fitted-float decoders)
 #define TMQ_MFMA_MAX_COLS 8192

@@ -32,6 +32,7 @@ typedef __attribute__((address_space(4))) const uint32_t cu32;
 namespace {
 
 constexpr int kQ5_0 = 6, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kQ5_0M = TMQ_FMT_Q5_0_MFMA;
+constexpr int kQ4_KM = TMQ_FMT_Q4_K_MFMA, kQ6_KM = TMQ_FMT_Q6_K_MFMA;
 constexpr int kF32 = 0, kF16 = 1;  // element types of the INT16 / FP32 paths
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
@@ -1025,6 +1026,26 @@ __device__ __forceinline__ uint32_t ifit_t4(uint32_t U, uint32_t a2, uint32_t b2
     const uint32_t PO = pk_mad_u16(__builtin_amdgcn_perm(0u, U, 0x0c030c01u), a2, b2);
     return __builtin_amdgcn_perm(PO, PE, 0x07030501u);
 }
+// Integer fit of a K-quant sub-block (the same form as IFit): nominal
+// slope AN = floor(an) with an = A*row_inv*256 for the per-code step A
+// (Q4_K d*sc, Q6_K d*sc), and the value at the pivot code p (Q4_K 8, Q6_K
+// 32, the middle of the codes) BN(p) = floor(bn), bn = E(p)*row_inv*256 +
+// 128; the fit code moves AN by dA = (code & 7) - 4 and the pivot value by
+// dB = (code >> 3) - 16, the intercept following from the pivot:
+//     BN = BN(p) - p*AN,   g(u) = floor((AN*u + BN) / 256).
+// an and bn are held inside +-(2^23 - 8) (|AN*u + BN| < 2^30 for u < 64).
+__device__ __forceinline__ IFit kfit(float an, float bn, int p, uint32_t code) {
+    const int AN = (int)floorf(__builtin_amdgcn_fmed3f(an, -8388600.0f, 8388600.0f)) + (int)(code & 7u) - 4;
+    const int BN = (int)floorf(__builtin_amdgcn_fmed3f(bn, -8388600.0f, 8388600.0f)) - p * AN +
+                   (int)((code >> 3) & 31u) - 16;
+    IFit f;
+    f.alpha = AN >> 8;
+    f.beta = BN >> 8;
+    f.a2 = ((uint32_t)AN & 255u) * 0x10001u;
+    f.b2 = ((uint32_t)BN & 255u) * 0x10001u;
+    return f;
+}
+
 __device__ __forceinline__ Q5Blk q5i_load(const TmqTensorDev& t, int b, int r) {
     const size_t o = (size_t)b * t.rows_pad + r;
     Q5Blk k;
@@ -1248,12 +1269,305 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     }
 }
 
+// --------------------------------------- MFMA decoders (Q4_K, Q6_K)
+// The K-quant blocks on the same int8 MFMA form as group_mfma_q5, per
+// sub-block (Q4_K 32 weights, Q6_K 16 weights) with its own kfit pair:
+//     sum_k w_k xq_k = alpha*S(u) + beta*sum_k xq_k + S(t),
+// S(u) read out per sub-block, S(t) summed in one accumulator for the row.
+// A workgroup owns 64 rows (one per lane) and splits their quarter blocks
+// (64 weights: Q4_K sub-blocks 2q, 2q+1; Q6_K quarter (h, lc) = the four
+// 16-weight sub-blocks 128h + 32sub + 16lc + (0..15)) over its 4 waves:
+// wave w takes quarters w, w + 4, ..., i.e. quarter w of every super-block,
+// so a 4864-column row gives each wave 19.  Each wave streams its quarters
+// global -> LDS through a ring of TMQ_MFMA_DEPTH stages (buffer loads with
+// scalar offsets; the per-block header / scales / d, which the four waves
+// of the workgroup all read, keep the default cache policy).  The LDS DMA
+// puts lane l's data at 16*l for 16-byte loads and at 4*l for the 1-, 2-
+// and 4-byte ones:
+//   Q4_K stage: qs chunks 2q, 2q+1 (1024 B each), header (1024 B), the two
+//               fit codes (256 B);
+//   Q6_K stage: ql chunks 4h+lc, 4h+2+lc, qh chunk 2h+lc, scales (1024 B
+//               each), d (256 B), the four fit codes (256 B).
+// The activation's operand bytes, 32- and 16-element sums are copied into
+// LDS once per workgroup.
+constexpr int kKqWaves = 4;
+template <int FMT> __host__ __device__ constexpr int kq_stage() { return FMT == kQ4_K ? 3328 : 4608; }
+template <int FMT> __host__ __device__ constexpr int kq_ndma() { return FMT == kQ4_K ? 4 : 6; }
+template <int FMT> __host__ __device__ constexpr int kq_xa_off() { return kKqWaves * TMQ_MFMA_DEPTH * kq_stage<FMT>(); }
+template <int FMT> __host__ __device__ constexpr int kq_xs_off(int nbx) {
+    return kq_xa_off<FMT>() + ((nbx * 64 + 32 + 15) & ~15);
+}
+template <int FMT> __host__ __device__ constexpr int kq_xs16_off(int nbx) { return kq_xs_off<FMT>(nbx) + ((nbx * 4 + 15) & ~15); }
+template <int FMT> __host__ __device__ constexpr int kq_part_off(int nbx) {
+    return kq_xs16_off<FMT>(nbx) + (FMT == kQ6_K ? ((nbx * 8 + 15) & ~15) : 0);
+}
+template <int FMT> __host__ __device__ constexpr int kq_lds_bytes(int nbx) {
+    return kq_part_off<FMT>(nbx) + (kKqWaves + 1) * 64 * 8;
+}
+
+template <int FMT>
+__device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
+    constexpr int NW = kKqWaves, D = TMQ_MFMA_DEPTH, ST = kq_stage<FMT>(), ND = kq_ndma<FMT>();
+    constexpr int NS = FMT == kQ4_K ? 2 : 4;  // sub-blocks per quarter
+    const TmqTensorDev& t = w.t;
+    const int nb = t.nb, nbx = nb * 8, n = t.cols;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    const int nu = 4 * nb;                      // quarters of a row
+    const int nuw = (nu - wave + NW - 1) / NW;  // this wave's quarters (wave-uniform, >= 1)
+    const int c0 = t.corr_off ? t.corr_off[g] : 0, c1 = t.corr_off ? t.corr_off[g + 1] : 0;
+    const float inv = t.row_inv[r], ri256 = inv * 256.0f;
+    uint8_t* xa = mfma_lds + kq_xa_off<FMT>();
+    int32_t* xsl = (int32_t*)(mfma_lds + kq_xs_off<FMT>(nbx));
+    int32_t* xs16l = (int32_t*)(mfma_lds + kq_xs16_off<FMT>(nbx));
+    int64_t* part = (int64_t*)(mfma_lds + kq_part_off<FMT>(nbx));
+    int64_t* fix = part + NW * 64;
+
+    // the activation copy first (global -> LDS), so that waiting for it does
+    // not wait for the ring's stages
+    {
+        const uint8_t* src = w.act + tmq_act_xa(n);
+        const int n16 = nbx * 4 + 2;
+        for (int i0 = wave * 64; i0 < n16; i0 += NW * 64)
+            if (i0 + lane < n16)
+                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
+                                                 16, 0, 0);
+        const uint8_t* xs = w.act + tmq_act_xs(n);
+        for (int i0 = wave * 64; i0 < nbx; i0 += NW * 64)
+            if (i0 + lane < nbx)
+                __builtin_amdgcn_global_load_lds((const void*)(xs + (size_t)(i0 + lane) * 4),
+                                                 (lds_u8*)((uint8_t*)xsl + i0 * 4), 4, 0, 0);
+        if constexpr (FMT == kQ6_K) {
+            const uint8_t* x16 = w.act + tmq_act_xs16(n);
+            for (int i0 = wave * 64; i0 < 2 * nbx; i0 += NW * 64)
+                if (i0 + lane < 2 * nbx)
+                    __builtin_amdgcn_global_load_lds((const void*)(x16 + (size_t)(i0 + lane) * 4),
+                                                     (lds_u8*)((uint8_t*)xs16l + i0 * 4), 4, 0, 0);
+        }
+    }
+
+    uint8_t* ring = mfma_lds + wave * D * ST;
+    const int ilast = max(nuw - 1, 0);
+    const int R = t.rows_pad, g64 = g * 64;
+    // planes (the host keeps each below 2^31 bytes)
+    const uint32_t pb = (uint32_t)R * (uint32_t)nb;  // (row, block) pairs
+    const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(t.pa, 128 * pb), rsi = buf_rsrc(t.pi, (FMT == kQ4_K ? 8 : 16) * pb);
+    const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(t.pb, (FMT == kQ4_K ? 16 : 64) * pb);
+    const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(FMT == kQ6_K ? t.pc : t.pb, 16 * pb);
+    const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(FMT == kQ6_K ? t.pd : t.pb, 2 * pb);
+    const int l16 = lane * 16;
+    // stage `slot` <- the wave's quarter i (clamped: refills past the end
+    // reload the last quarter, so every step waits for the same count)
+    auto issue = [&](int i, int slot) {
+        const int u = __builtin_amdgcn_readfirstlane(wave + NW * min(i, ilast));
+        const int b = u >> 2, q = u & 3;
+        uint8_t* st = ring + slot * ST;
+        if constexpr (FMT == kQ4_K) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)st, 16, l16, ((b * 8 + 2 * q) * R + g64) * 16, 0,
+                                                     TMQ_CPOL_NT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)(st + 1024), 16, l16,
+                                                     ((b * 8 + 2 * q + 1) * R + g64) * 16, 0, TMQ_CPOL_NT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_u8*)(st + 2048), 16, l16, (b * R + g64) * 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 3072), 2, lane * 2, ((b * 4 + q) * R + g64) * 2,
+                                                     0, TMQ_CPOL_NT);
+        } else {
+            const int h = q >> 1, lc = q & 1;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)st, 16, l16, ((b * 8 + 4 * h + lc) * R + g64) * 16,
+                                                     0, TMQ_CPOL_NT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)(st + 1024), 16, l16,
+                                                     ((b * 8 + 4 * h + 2 + lc) * R + g64) * 16, 0, TMQ_CPOL_NT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_u8*)(st + 2048), 16, l16,
+                                                     ((b * 4 + 2 * h + lc) * R + g64) * 16, 0, TMQ_CPOL_NT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_u8*)(st + 3072), 16, l16, (b * R + g64) * 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsd, (lds_u8*)(st + 4096), 2, lane * 2, (b * R + g64) * 2, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 4352), 4, lane * 4, ((b * 4 + q) * R + g64) * 4,
+                                                     0, TMQ_CPOL_NT);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D; i++) issue(i, i);
+    // this wave's part of the activation copy has landed; the barrier makes
+    // every part visible (a plain s_barrier: the workgroup fence of
+    // __syncthreads would also wait for the ring's stages)
+    wait_vm<ND * D>();
+    asm volatile("s_barrier" ::: "memory");
+
+    // this lane's A operand: rows 4q', 4q'+1 the sub-block's xh and
+    // xl - 128 over K group q' (lane >> 4), row 4q'+2 ones, the rest zero;
+    // the 16 elements of (32-element block xb, half hf) at abase +
+    // astride*(64*xb + 32*hf)
+    uint32_t abase, astride;
+    {
+        const int qg = lane >> 4, m = lane & 15, dg = m & 3;
+        const bool own = (m >> 2) == qg;
+        const uint32_t zero = (uint32_t)nbx * 64u;
+        abase = own && dg < 2 ? (uint32_t)(dg * 16) : own && dg == 2 ? zero + 16u : zero;
+        astride = own && dg < 2 ? 1u : 0u;
+    }
+    auto aop = [&](int xb, int hf) { return *(lv4i*)(xa + abase + astride * (uint32_t)(64 * xb + 32 * hf)); };
+
+    int64_t acc = 0;
+    tmq_v4i Ct = {};
+    tmq_v4i Cu[NS];
+    int ap[NS], bp[NS], xp[NS];  // the previous quarter's sub-blocks: alpha, beta, activation sum
+#pragma unroll
+    for (int k = 0; k < NS; k++) {
+        Cu[k] = tmq_v4i{};
+        ap[k] = bp[k] = xp[k] = 0;
+    }
+    const tmq_v4i Z = {};
+    auto step = [&](int i, int slot) {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<ND * (D - 1)>();
+        const int u = wave + NW * i, b = u >> 2, q = u & 3;
+        const uint8_t* st = ring + slot * ST;
+        IFit f[NS];
+        tmq_v4i UA[NS][2], TA[NS][2], AA[NS][2];
+        int xsv[NS];
+        if constexpr (FMT == kQ4_K) {
+            const tmq_v4i qa = *(lv4i*)(st + lane * 16), qb = *(lv4i*)(st + 1024 + lane * 16);
+            const tmq_v4i hv = *(lv4i*)(st + 2048 + lane * 16);
+            const uint32_t codes = *(lu16*)(st + 3072 + lane * 4);
+#pragma unroll
+            for (int k = 0; k < NS; k++) {
+                const int xb = 8 * b + 2 * q + k;
+                AA[k][0] = aop(xb, 0);
+                AA[k][1] = aop(xb, 1);
+                xsv[k] = xsl[xb];
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(i + D, slot);
+            const uint4 h = make_uint4((uint32_t)hv.x, (uint32_t)hv.y, (uint32_t)hv.z, (uint32_t)hv.w);
+            const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+#pragma unroll
+            for (int k = 0; k < NS; k++) {
+                int sc, m;
+                q4k_scale_min(h, 2 * q + k, sc, m);
+                const float Ad = d * (float)sc, Bm = dmin * (float)m;
+                f[k] = kfit(Ad * ri256, __builtin_fmaf(__builtin_fmaf(8.0f, Ad, -Bm), ri256, 128.0f), 8,
+                            (codes >> (8 * k)) & 255u);
+                const tmq_v4i src[2] = {qa, qb};
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    uint32_t U[4], T[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t v = (uint32_t)src[hf][e];
+                        U[e] = (k ? (v >> 4) : v) & 0x0f0f0f0fu;
+                        T[e] = ifit_t4(U[e], f[k].a2, f[k].b2);
+                    }
+                    UA[k][hf] = tmq_v4i{(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
+                    TA[k][hf] = tmq_v4i{(int)T[0], (int)T[1], (int)T[2], (int)T[3]};
+                }
+            }
+        } else {
+            const int h = q >> 1, lc = q & 1;
+            const tmq_v4i va = *(lv4i*)(st + lane * 16), vb = *(lv4i*)(st + 1024 + lane * 16);
+            const tmq_v4i vh = *(lv4i*)(st + 2048 + lane * 16);
+            const uint32_t sc0 = *(lu32c*)(st + 3072 + lane * 16 + 8 * h);
+            const uint32_t sc1 = *(lu32c*)(st + 3072 + lane * 16 + 8 * h + 4);
+            const uint32_t dbits = *(lu16*)(st + 4096 + lane * 4);
+            const uint32_t codes = *(lu32c*)(st + 4352 + lane * 4);
+#pragma unroll
+            for (int k = 0; k < NS; k++) {
+                const int xb = 8 * b + 4 * h + k;
+                AA[k][0] = aop(xb, lc);
+                xsv[k] = xs16l[2 * xb + lc];
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(i + D, slot);
+            const uint4 qla = make_uint4((uint32_t)va.x, (uint32_t)va.y, (uint32_t)va.z, (uint32_t)va.w);
+            const uint4 qlb = make_uint4((uint32_t)vb.x, (uint32_t)vb.y, (uint32_t)vb.z, (uint32_t)vb.w);
+            const uint4 qhc = make_uint4((uint32_t)vh.x, (uint32_t)vh.y, (uint32_t)vh.z, (uint32_t)vh.w);
+            const float ssri = h2f(dbits) * ri256;
+#pragma unroll
+            for (int k = 0; k < NS; k++) {
+                // scale 8h + lc + 2k: byte lc + 2k of the 8 bytes at 8h
+                const uint32_t sw = (k < 2) ? sc0 : sc1;
+                const int sc = (int)(int8_t)(uint8_t)(sw >> (8 * (lc + 2 * (k & 1))));
+                f[k] = kfit(ssri * (float)sc, 128.0f, 32, (codes >> (8 * k)) & 255u);
+                uint32_t U[4], T[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    U[e] = q6_codes(qla, qlb, qhc, k, e);
+                    T[e] = ifit_t4(U[e], f[k].a2, f[k].b2);
+                }
+                UA[k][0] = tmq_v4i{(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
+                TA[k][0] = tmq_v4i{(int)T[0], (int)T[1], (int)T[2], (int)T[3]};
+            }
+        }
+        // the previous quarter's u sums (their MFMAs have long finished)
+#pragma unroll
+        for (int k = 0; k < NS; k++)
+            acc += (int64_t)ap[k] * (Cu[k][0] * 256 + Cu[k][1] + Cu[k][2] * 128) + (int64_t)bp[k] * xp[k];
+        __builtin_amdgcn_sched_barrier(0);  // the read-out before the overwrite
+#pragma unroll
+        for (int k = 0; k < NS; k++) {
+            if constexpr (FMT == kQ4_K) {
+                Cu[k] = mfma16(AA[k][0], UA[k][0], Z);
+                Cu[k] = mfma16(AA[k][1], UA[k][1], Cu[k]);
+                Ct = mfma16(AA[k][0], TA[k][0], Ct);
+                Ct = mfma16(AA[k][1], TA[k][1], Ct);
+            } else {
+                Cu[k] = mfma16(AA[k][0], UA[k][0], Z);
+                Ct = mfma16(AA[k][0], TA[k][0], Ct);
+            }
+            ap[k] = f[k].alpha;
+            bp[k] = f[k].beta;
+            xp[k] = xsv[k];
+        }
+    };
+    int ib = 0;
+    for (; ib + D <= nuw; ib += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) step(ib + i, i);
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++)
+        if (ib + i < nuw) step(ib + i, i);
+#pragma unroll
+    for (int k = 0; k < NS; k++)
+        acc += (int64_t)ap[k] * (Cu[k][0] * 256 + Cu[k][1] + Cu[k][2] * 128) + (int64_t)bp[k] * xp[k];
+    acc += (int64_t)Ct[0] * 256 + Ct[1] + (int64_t)Ct[2] * 128;
+    // no DMA into the ring may still run past this point
+    wait_vm<0>();
+    part[wave * 64 + lane] = acc;
+    if (threadIdx.x < 64) fix[threadIdx.x] = 0;
+    __syncthreads();
+    if (c1 > c0) {
+        // corrections (uniform branch): delta * sum of xq over their elements
+        const int32_t* x32 = (const int32_t*)(w.act + 16 + 6 * (size_t)n);
+        for (int c = c0 + (int)threadIdx.x; c < c1; c += 64 * NW) {
+            const uint4 e = t.corr[c];
+            int64_t s = 0;
+            for (uint32_t m = e.z; m; m &= m - 1) s += x32[e.y + __builtin_ctz(m)];
+            atomicAdd((unsigned long long*)&fix[(int)e.x - g * 64], (unsigned long long)((int64_t)(int32_t)e.w * s));
+        }
+        __syncthreads();
+    }
+    if (wave == 0 && r < t.rows) {
+        int64_t tot = fix[lane];
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += part[i * 64 + lane];
+        if (w.acc) w.acc[r] = tot;
+        // sim/tmac_gguf.cpp:1192-1194 (Q4_K), :1501-1503 (Q6_K):
+        // y = (float)((double)acc*x_scale/(double)row_inv)
+        const float xs = *(const float*)w.act;
+        if (w.y) store_y(w, r, (float)(((double)tot * (double)xs) / (double)inv));
+    }
+}
+
 template <int FMT, bool CLAMP>
 __device__ __forceinline__ void run_group(const TmqWork& w, int g) {
     if constexpr (FMT == kQ8_0) {
         group_q8(w, g);
     } else if constexpr (FMT == kQ5_0M) {
         group_mfma_q5(w, g);
+    } else if constexpr (FMT == kQ4_KM) {
+        group_mfma_kq<kQ4_K>(w, g);
+    } else if constexpr (FMT == kQ6_KM) {
+        group_mfma_kq<kQ6_K>(w, g);
     } else {
         group_ksplit<FMT, CLAMP>(w, g);
     }
@@ -2212,6 +2526,7 @@ __global__ __launch_bounds__(1024) void act_prep_kernel(TmqActJobs jobs) {
     const int nbx = (n + 31) / 32;
     uint8_t* XA = J.act + tmq_act_xa(n);
     int32_t* XS = (int32_t*)(J.act + tmq_act_xs(n));
+    int32_t* XS16 = (int32_t*)(J.act + tmq_act_xs16(n));
     for (int q = threadIdx.x; q < nbx * 4; q += blockDim.x) {
         const int b = q >> 2, e0 = 32 * b + 8 * (q & 3);
         uint32_t hi[2] = {0, 0}, lo[2] = {0x80808080u, 0x80808080u};
@@ -2226,6 +2541,7 @@ __global__ __launch_bounds__(1024) void act_prep_kernel(TmqActJobs jobs) {
         *(uint2*)(XA + 64 * b + 32 * c + pos) = make_uint2(hi[0], hi[1]);
         *(uint2*)(XA + 64 * b + 32 * c + 16 + pos) = make_uint2(lo[0], lo[1]);
         sum += __shfl_xor(sum, 1);
+        if ((q & 1) == 0) XS16[2 * b + ((q >> 1) & 1)] = sum;
         sum += __shfl_xor(sum, 2);
         if ((q & 3) == 0) XS[b] = sum;
     }
@@ -2541,6 +2857,117 @@ __global__ __launch_bounds__(256) void ifit_kernel(TmqTensorDev t, int pass, int
     }
 }
 
+// Integer fit codes of the K-quant MFMA decoders (kfit): one thread per
+// (row, sub-block).  The sub-block's exact weights g(u) are those of the
+// fitted-float decoders' fit (fit_kernel: clamp16(roundf(fl(E(u)*row_inv))),
+// E as the reference dequantises); the first (dA, dB) by growing |dA| then
+// |dB| (dA in [-4, 3], dB in [-16, 15]) that gives g on every code the
+// sub-block holds is kept, else the pair with the fewest differing codes.
+// Sub-block k of block b: Q4_K k = s (32 weights, columns 256b + 32s + i),
+// quarter q = s >> 1; Q6_K k = 4q + sub for quarter q = 2h + lc (16 weights,
+// columns 256b + 128h + 32sub + 16lc + i, scale 8h + lc + 2sub).  Pass 0
+// writes the code (plane pi, quarter-major) and the number of differing
+// codes at cnt[(r*nb + b)*NSUB + k]; pass 1 writes one correction per
+// differing code from corr[off[...]] on.  force: every sub-block takes the
+// code dA = 3, dB = 15 (testing the corrections).
+template <int FMT>
+__global__ __launch_bounds__(256) void ikfit_kernel(TmqTensorDev t, int pass, int force, uint8_t* cnt,
+                                                    const int32_t* off, uint4* corr) {
+    constexpr int NSUB = FMT == kQ4_K ? 8 : 16, N = FMT == kQ4_K ? 32 : 16, P = FMT == kQ4_K ? 8 : 32;
+    const int r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y / NSUB, k = blockIdx.y % NSUB;
+    if (r >= t.rows_pad) return;
+    const size_t R = t.rows_pad;
+    const float inv = t.row_inv[r], ri256 = inv * 256.0f;
+    int u[N], gv[N];
+    float an, bn;
+    int q, col0;
+    size_t po;  // byte of the fit code in plane pi
+    if constexpr (FMT == kQ4_K) {
+        const Q4KBlk kb = q4k_load(t, b, r);
+        const int sidx = k;
+        q = sidx >> 1;
+        const float d = h2f(kb.h.x), dmin = h2f(kb.h.x >> 16);
+        int sc, m;
+        q4k_scale_min(kb.h, sidx, sc, m);
+        const float Ad = d * (float)sc, Bm = dmin * (float)m;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t by = byte_of(kb.qs[(sidx >> 1) * 2 + (i >> 4)], i & 15);
+            u[i] = (int)((sidx & 1) ? (by >> 4) : (by & 15u));
+            gv[i] = max(-32768, min(32767, round_away(__builtin_fmaf((float)u[i], Ad, -Bm) * inv)));
+        }
+        an = Ad * ri256;
+        bn = __builtin_fmaf(__builtin_fmaf(8.0f, Ad, -Bm), ri256, 128.0f);
+        col0 = 256 * b + 32 * sidx;
+        po = (((size_t)b * 4 + q) * R + r) * 2 + (sidx & 1);
+    } else {
+        const Q6KBlk kb = q6k_load(t, b, r);
+        q = k >> 2;
+        const int sub = k & 3, h = q >> 1, lc = q & 1;
+        const float ss = h2f(kb.d);
+        const int sc = (int)(int8_t)byte_of(kb.sc, 8 * h + lc + 2 * sub);
+        const float S = ss * (float)sc;
+        const uint4 qla = kb.ql[h * 4 + lc], qlb = kb.ql[h * 4 + 2 + lc], qhc = kb.qh[h * 2 + lc];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t U = q6_codes(qla, qlb, qhc, sub, i);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                u[4 * i + j] = (int)((U >> (8 * j)) & 63u);
+                gv[4 * i + j] = max(-32768, min(32767, round_away(S * (float)(u[4 * i + j] - 32) * inv)));
+            }
+        }
+        an = (ss * ri256) * (float)sc;
+        bn = 128.0f;
+        col0 = 256 * b + 128 * h + 32 * sub + 16 * lc;
+        po = (((size_t)b * 4 + q) * R + r) * 4 + sub;
+    }
+    uint32_t best = 255u;
+    if (!force) {
+        int best_mis = N + 1;
+        for (int ia = 0; ia < 8 && best_mis; ia++) {
+            const int da = (ia & 1) ? -((ia + 1) >> 1) : (ia >> 1);  // 0, -1, 1, -2, 2, -3, 3, -4
+            for (int ib = 0; ib < 32 && best_mis; ib++) {
+                const int db = (ib & 1) ? -((ib + 1) >> 1) : (ib >> 1);  // 0, -1, 1, ..., 15, -16
+                const uint32_t e = (uint32_t)(da + 4) | ((uint32_t)(db + 16) << 3);
+                const IFit f = kfit(an, bn, P, e);
+                int mis = 0;
+#pragma unroll
+                for (int i = 0; i < N; i++) mis += ifit_w(f, u[i]) != gv[i];
+                if (mis < best_mis) {
+                    best_mis = mis;
+                    best = e;
+                }
+            }
+        }
+    }
+    const IFit f = kfit(an, bn, P, best);
+    uint64_t bad = 0;  // codes whose fitted weight differs
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        if (ifit_w(f, u[i]) != gv[i]) bad |= 1ull << u[i];
+    const size_t ci = ((size_t)r * t.nb + b) * NSUB + k;
+    if (pass == 0) {
+        ((uint8_t*)t.pi)[po] = (uint8_t)best;
+        cnt[ci] = (uint8_t)__builtin_popcountll(bad);
+        return;
+    }
+    if (!bad) return;
+    int slot = off[ci];
+    for (; bad; bad &= bad - 1) {
+        const int c = __builtin_ctzll(bad);
+        uint32_t m = 0;
+        int delta = 0;
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if (u[i] == c) {
+                m |= 1u << i;
+                delta = gv[i] - ifit_w(f, c);
+            }
+        corr[slot++] = make_uint4((uint32_t)r, (uint32_t)col0, m, (uint32_t)delta);
+    }
+}
+
 // UQ8.8 combined scale of every (row, block) of a Q8_0 tensor, as
 // matmul_fpga_q8 forms them for its tiles (sim/tmac_gguf.cpp:1022-1039);
 // out[r * nb + b]
@@ -2835,11 +3262,15 @@ int tmq_launch_fit(const TmqTensorDev& t, int all_exact, hipStream_t s) {
 
 int tmq_launch_ifit(const TmqTensorDev& t, int pass, uint8_t* cnt, const int32_t* off, uint4* corr,
                     hipStream_t s) {
-    if (t.type != kQ5_0 || !t.pi || t.clamp) return (int)hipErrorInvalidValue;
+    if (!t.pi || t.clamp) return (int)hipErrorInvalidValue;
     const char* fe = getenv("TMQ_IFIT_FORCE");
     const int force = fe && atoi(fe) != 0;
-    const dim3 grid((t.rows_pad + 255) / 256, t.nb);
-    hipLaunchKernelGGL(ifit_kernel, grid, dim3(256), 0, s, t, pass, force, cnt, off, corr);
+    const int ns = tmq_ifit_subs(t.type);
+    if (!ns) return (int)hipErrorInvalidValue;
+    const dim3 grid((t.rows_pad + 255) / 256, t.nb * ns);
+    if (t.type == kQ5_0) hipLaunchKernelGGL(ifit_kernel, grid, dim3(256), 0, s, t, pass, force, cnt, off, corr);
+    else if (t.type == kQ4_K) hipLaunchKernelGGL(ikfit_kernel<kQ4_K>, grid, dim3(256), 0, s, t, pass, force, cnt, off, corr);
+    else hipLaunchKernelGGL(ikfit_kernel<kQ6_K>, grid, dim3(256), 0, s, t, pass, force, cnt, off, corr);
     return (int)hipGetLastError();
 }
 
@@ -2847,6 +3278,8 @@ template <template <int, bool> class K>
 static void* kernel_for(int type, int clamp) {
     switch (type) {
     case kQ5_0M: return clamp ? nullptr : (void*)K<kQ5_0M, false>::fn();
+    case kQ4_KM: return clamp ? nullptr : (void*)K<kQ4_KM, false>::fn();
+    case kQ6_KM: return clamp ? nullptr : (void*)K<kQ6_KM, false>::fn();
     case kQ5_0: return clamp ? (void*)K<kQ5_0, true>::fn() : (void*)K<kQ5_0, false>::fn();
     case kQ4_K: return clamp ? (void*)K<kQ4_K, true>::fn() : (void*)K<kQ4_K, false>::fn();
     case kQ6_K: return clamp ? (void*)K<kQ6_K, true>::fn() : (void*)K<kQ6_K, false>::fn();
@@ -2877,8 +3310,11 @@ int tmq_launch_gemv(const TmqWork& w, hipStream_t s) {
 }
 
 size_t tmq_gemv_lds_bytes(int fmt, int max_cols) {
-    if (fmt != kQ5_0M) return 0;
-    return (size_t)mfma_lds_bytes(min(max_cols, TMQ_MFMA_MAX_COLS) / 32);
+    const int nbx = min(max_cols, TMQ_MFMA_MAX_COLS) / 32;
+    if (fmt == kQ5_0M) return (size_t)mfma_lds_bytes(nbx);
+    if (fmt == kQ4_KM) return (size_t)kq_lds_bytes<kQ4_K>(nbx);
+    if (fmt == kQ6_KM) return (size_t)kq_lds_bytes<kQ6_K>(nbx);
+    return 0;
 }
 
 int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const int32_t* group_work_dev,

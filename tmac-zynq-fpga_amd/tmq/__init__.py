@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 
 import numpy as np
 
@@ -179,6 +180,7 @@ def _p(a):
 class Tensor:
     def __init__(self, ctx: "Context", handle, qtype: int, rows: int, cols: int):
         self.ctx, self.handle, self.qtype, self.rows, self.cols = ctx, handle, qtype, rows, cols
+        ctx._adopt(self)
         wb = C.c_uint64()
         _check(lib().tmq_tensor_info(handle, None, None, None, C.byref(wb)))
         self.weight_bytes = wb.value
@@ -225,6 +227,7 @@ class Chain:
         h = C.c_void_p()
         _check(lib().tmq_chain_create(ctx.handle, arr, len(descs), C.byref(h)))
         self.handle = h
+        ctx._adopt(self)
         self.weight_bytes = lib().tmq_chain_weight_bytes(h)
 
     def run(self):
@@ -249,10 +252,19 @@ class Chain:
 
 
 class Context:
+    """A device and stream (tmq_open).  Tensors, chains and models made from
+    it are freed at the latest by close(): the library needs its context
+    alive to free them, so anything still alive then is freed first and
+    their own free() becomes a no-op."""
+
     def __init__(self, device: int = 0):
         h = C.c_void_p()
         _check(lib().tmq_open(device, C.byref(h)))
         self.handle = h
+        self._children = weakref.WeakSet()
+
+    def _adopt(self, obj):
+        self._children.add(obj)
 
     @property
     def stream(self) -> int:
@@ -263,8 +275,16 @@ class Context:
 
     def close(self):
         if self.handle:
+            for obj in list(self._children):
+                obj.free()
             lib().tmq_close(self.handle)
             self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     # -- tensors ---------------------------------------------------------
     def upload(self, qtype: int, rows: int, cols: int, data: np.ndarray, row_max_abs=None) -> Tensor:
@@ -390,6 +410,7 @@ class Model:
             buf = np.ascontiguousarray(buf, dtype=np.uint8)
             _check(lib().tmq_model_load_mem(ctx.handle, _p(buf), buf.size, max_seq, C.byref(h)))
         self.ctx, self.handle = ctx, h
+        ctx._adopt(self)
         cfg = ModelConfig()
         _check(lib().tmq_model_get_config(h, C.byref(cfg)))
         self.config = {f: getattr(cfg, f) for f, _ in ModelConfig._fields_}
