@@ -1027,16 +1027,17 @@ __device__ __forceinline__ uint32_t ifit_t4(uint32_t U, uint32_t a2, uint32_t b2
     return __builtin_amdgcn_perm(PO, PE, 0x07030501u);
 }
 // Integer fit of a K-quant sub-block (the same form as IFit): nominal
-// slope AN = floor(an) with an = A*row_inv*256 for the per-code step A
-// (Q4_K d*sc, Q6_K d*sc), and the value at the pivot code p (Q4_K 8, Q6_K
-// 32, the middle of the codes) BN(p) = floor(bn), bn = E(p)*row_inv*256 +
-// 128; the fit code moves AN by dA = (code & 7) - 4 and the pivot value by
-// dB = (code >> 3) - 16, the intercept following from the pivot:
+// slope AN = (int)an with an ~ A*row_inv*256 for the per-code step A (Q4_K
+// d*sc, Q6_K d*sc), and the value at the pivot code p (Q4_K 8, Q6_K 32, the
+// middle of the codes) BN(p) = (int)bn, bn ~ E(p)*row_inv*256 + 128 (kq_nom:
+// any fixed rounding of these serves, the fit code absorbs it); the code
+// moves AN by dA = (code & 7) - 4 and the pivot value by dB = (code >> 3) -
+// 16, the intercept following from the pivot:
 //     BN = BN(p) - p*AN,   g(u) = floor((AN*u + BN) / 256).
 // an and bn are held inside +-(2^23 - 8) (|AN*u + BN| < 2^30 for u < 64).
 __device__ __forceinline__ IFit kfit(float an, float bn, int p, uint32_t code) {
-    const int AN = (int)floorf(__builtin_amdgcn_fmed3f(an, -8388600.0f, 8388600.0f)) + (int)(code & 7u) - 4;
-    const int BN = (int)floorf(__builtin_amdgcn_fmed3f(bn, -8388600.0f, 8388600.0f)) - p * AN +
+    const int AN = (int)__builtin_amdgcn_fmed3f(an, -8388600.0f, 8388600.0f) + (int)(code & 7u) - 4;
+    const int BN = (int)__builtin_amdgcn_fmed3f(bn, -8388600.0f, 8388600.0f) - p * AN +
                    (int)((code >> 3) & 31u) - 16;
     IFit f;
     f.alpha = AN >> 8;
@@ -1044,6 +1045,15 @@ __device__ __forceinline__ IFit kfit(float an, float bn, int p, uint32_t code) {
     f.a2 = ((uint32_t)AN & 255u) * 0x10001u;
     f.b2 = ((uint32_t)BN & 255u) * 0x10001u;
     return f;
+}
+
+// Nominal fit values of a Q4_K sub-block from dri = d*row_inv*256 and
+// mri = dmin*row_inv*256 (per block): an = dri*sc, bn = 8*an - mri*m + 128
+// (E(8)*row_inv*256 + 128 up to rounding).  The upload fit and the decoder
+// both use this function.
+__device__ __forceinline__ void q4k_nom(float dri, float mri, int sc, int m, float& an, float& bn) {
+    an = dri * (float)sc;
+    bn = __builtin_fmaf(an, 8.0f, __builtin_fmaf(-mri, (float)m, 128.0f));
 }
 
 __device__ __forceinline__ Q5Blk q5i_load(const TmqTensorDev& t, int b, int r) {
@@ -1397,15 +1407,19 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
     // xl - 128 over K group q' (lane >> 4), row 4q'+2 ones, the rest zero;
     // the 16 elements of (32-element block xb, half hf) at abase +
     // astride*(64*xb + 32*hf)
-    uint32_t abase, astride;
+    // (the offset is a multiple of 32 and abase < 32 where amask is set, so
+    // (offset & amask) | abase is one v_and_or)
+    uint32_t abase, amask;
     {
         const int qg = lane >> 4, m = lane & 15, dg = m & 3;
         const bool own = (m >> 2) == qg;
         const uint32_t zero = (uint32_t)nbx * 64u;
         abase = own && dg < 2 ? (uint32_t)(dg * 16) : own && dg == 2 ? zero + 16u : zero;
-        astride = own && dg < 2 ? 1u : 0u;
+        amask = own && dg < 2 ? 0xffffffffu : 0u;
     }
-    auto aop = [&](int xb, int hf) { return *(lv4i*)(xa + abase + astride * (uint32_t)(64 * xb + 32 * hf)); };
+    auto aop = [&](int xb, int hf) {
+        return *(lv4i*)(xa + ((((uint32_t)(64 * xb + 32 * hf)) & amask) | abase));
+    };
 
     int64_t acc = 0;
     tmq_v4i Ct = {};
@@ -1439,14 +1453,14 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             issue(i + D, slot);
             const uint4 h = make_uint4((uint32_t)hv.x, (uint32_t)hv.y, (uint32_t)hv.z, (uint32_t)hv.w);
-            const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+            const float dri = h2f(h.x) * ri256, mri = h2f(h.x >> 16) * ri256;
 #pragma unroll
             for (int k = 0; k < NS; k++) {
                 int sc, m;
                 q4k_scale_min(h, 2 * q + k, sc, m);
-                const float Ad = d * (float)sc, Bm = dmin * (float)m;
-                f[k] = kfit(Ad * ri256, __builtin_fmaf(__builtin_fmaf(8.0f, Ad, -Bm), ri256, 128.0f), 8,
-                            (codes >> (8 * k)) & 255u);
+                float an, bn;
+                q4k_nom(dri, mri, sc, m, an, bn);
+                f[k] = kfit(an, bn, 8, (codes >> (8 * k)) & 255u);
                 const tmq_v4i src[2] = {qa, qb};
 #pragma unroll
                 for (int hf = 0; hf < 2; hf++) {
@@ -2896,8 +2910,7 @@ __global__ __launch_bounds__(256) void ikfit_kernel(TmqTensorDev t, int pass, in
             u[i] = (int)((sidx & 1) ? (by >> 4) : (by & 15u));
             gv[i] = max(-32768, min(32767, round_away(__builtin_fmaf((float)u[i], Ad, -Bm) * inv)));
         }
-        an = Ad * ri256;
-        bn = __builtin_fmaf(__builtin_fmaf(8.0f, Ad, -Bm), ri256, 128.0f);
+        q4k_nom(d * ri256, dmin * ri256, sc, m, an, bn);
         col0 = 256 * b + 32 * sidx;
         po = (((size_t)b * 4 + q) * R + r) * 2 + (sidx & 1);
     } else {
