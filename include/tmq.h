@@ -106,15 +106,15 @@ int tmq_tensor_row_norm(tmq_ctx* ctx, const tmq_tensor* t, float* out);
  * environment at upload sends every sub-block to the exact decode. */
 int tmq_tensor_fit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* fitted, uint64_t* exact);
 /* Integer fit of the MFMA decoders (no counterpart in the reference;
- * diagnostics).  Q5_0 tensors of at most 8192 columns: within each block
- * of a row the int16 weight of code u
- * is floor((AN*u + BN)/256) for integers AN, BN fixed at upload; the codes
- * no such pair reproduces are listed as corrections, applied exactly after
- * the fitted sums.  *blocks = (row, block) pairs with a code (0: the tensor
- * takes the fitted-float decoders), *corrections = listed codes.
- * TMQ_NOMFMA=1 at upload keeps the tensor on the fitted-float decoders;
- * TMQ_IFIT_FORCE=1 gives every block one fixed, mostly wrong pair (testing
- * the corrections). */
+ * diagnostics).  Q5_0, Q4_K and Q6_K tensors of at most 8192 columns: within
+ * each fitted unit of a row (Q5_0 block, Q4_K 32-weight sub-block, Q6_K
+ * 16-weight sub-block) the int16 weight of code u is floor((AN*u + BN)/256)
+ * for integers AN, BN fixed at upload; the codes no such pair reproduces
+ * are listed as corrections, applied exactly after the fitted sums.
+ * *blocks = fitted units with a code (0: the tensor takes the fitted-float
+ * decoders), *corrections = listed codes.  TMQ_NOMFMA=1 at upload keeps the
+ * tensor on the fitted-float decoders; TMQ_IFIT_FORCE=1 gives every unit
+ * one fixed, mostly wrong pair (testing the corrections). */
 int tmq_tensor_ifit_stats(tmq_ctx* ctx, const tmq_tensor* t, uint64_t* blocks, uint64_t* corrections);
 
 /* ---- GEMV (boundary 1) -------------------------------------------------
