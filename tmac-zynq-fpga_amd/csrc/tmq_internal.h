@@ -173,7 +173,8 @@ struct TmqEngAct {
     int32_t n;
     const float* x;            // RESID_NORM / PLAIN / PRESCALED input
     const float* w;            // NORM modes: RMSNorm weight (null: no norm)
-    const uint32_t* max_bits;  // PRESCALED: bits of max|x| (atomic max of non-negative floats)
+    const uint32_t* max_bits;  // PRESCALED: max|x| as the largest of max_n slots (bits of non-negative floats)
+    int32_t max_n;             // PRESCALED: slots in max_bits (1 .. TMQ_MAX_SLOTS)
     float eps;
     int32_t spec_miss;         // nonzero: the norm's segmented sum re-runs every segment (testing)
     TmqDeferred d1;            // RESID_NORM: the residual term
@@ -183,6 +184,10 @@ struct TmqEngAct {
     const int32_t* tokens;
     TmqTensorDev emb;          // EMBED_NORM: quantized embedding
 };
+
+// max |x| slots of a PRESCALED activation: each producing workgroup stores
+// its own (no contended atomic); the consumer's prologue takes the largest
+#define TMQ_MAX_SLOTS 256
 
 // One engine GEMV launch, passed by value: the activation recipe and up to
 // TMQ_ENG_MAXW works whose workgroups follow each other (first_group).

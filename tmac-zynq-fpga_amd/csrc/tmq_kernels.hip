@@ -2052,23 +2052,29 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
     const bool norm = (a.mode == TMQ_ACT_RESID_NORM || a.mode == TMQ_ACT_EMBED_NORM) && a.w;
     float* sq = (float*)L.xh;  // squares, consumed before xh/xl are written
     float m = 0.0f;
-    uint32_t pmax = 0;
-    if (a.mode == TMQ_ACT_PRESCALED && c1 - c0 <= EP * nt) {
-        // max given; only the workgroup's columns are needed
-        float xin[EP];
+    if (a.mode == TMQ_ACT_PRESCALED) {
+        // max given as a_max_n slots (one per producing workgroup, bits of
+        // non-negative floats); only the workgroup's columns are needed
+        uint32_t mv = 0;
+        if (c1 - c0 <= EP * nt) {
+            float xin[EP];
 #pragma unroll
-        for (int e = 0; e < EP; e++) xin[e] = a.x[min(c0 + tid + e * nt, c1 - 1)];
-        pmax = __hip_atomic_load(a.max_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_sched_barrier(0);
-        pre();
-        __builtin_amdgcn_sched_barrier(0);
+            for (int e = 0; e < EP; e++) xin[e] = a.x[min(c0 + tid + e * nt, c1 - 1)];
+            if (tid < a.max_n) mv = __hip_atomic_load(a.max_bits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_sched_barrier(0);
+            pre();
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int e = 0; e < EP; e++)
-            if (c0 + tid + e * nt < c1) L.x[c0 + tid + e * nt] = xin[e];
-    } else if (a.mode == TMQ_ACT_PRESCALED) {
-        pre();
-        for (int i = c0 + tid; i < c1; i += nt) L.x[i] = a.x[i];
-        pmax = __hip_atomic_load(a.max_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int e = 0; e < EP; e++)
+                if (c0 + tid + e * nt < c1) L.x[c0 + tid + e * nt] = xin[e];
+        } else {
+            pre();
+            for (int i = c0 + tid; i < c1; i += nt) L.x[i] = a.x[i];
+            if (tid < a.max_n) mv = __hip_atomic_load(a.max_bits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        m = __builtin_bit_cast(float, mv);
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        if ((tid & 63) == 0) L.red[2 + (tid >> 6)] = m;
     } else if ((a.mode == TMQ_ACT_PLAIN || (a.mode == TMQ_ACT_RESID_NORM && a.d1.ntiles == 0 && !a.d1.val)) &&
                n <= EP * nt) {
         // every load first (indices clamped into [0, n), pointers always
@@ -2153,14 +2159,9 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
     // capture of the norm output (the matmuls' fp32 input, rms_norm's o)
     if (norm && a.act_out && blockIdx.x == 0)
         for (int i = tid; i < n; i += nt) a.act_out[i] = L.x[i] * s;
-    float mm;
-    if (a.mode == TMQ_ACT_PRESCALED) {
-        mm = __builtin_bit_cast(float, pmax);
-    } else {
-        mm = 0.0f;
-        for (int i = 0; i < (int)(nt >> 6); i++) mm = fmaxf(mm, L.red[2 + i]);
-        if (norm) mm = mm * s;
-    }
+    float mm = 0.0f;
+    for (int i = 0; i < (int)(nt >> 6); i++) mm = fmaxf(mm, L.red[2 + i]);
+    if (norm) mm = mm * s;
     const float xs = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
     for (int k = (c0 >> 1) + tid; k < (c1 >> 1); k += nt) {
         float u = L.x[2 * k], v = L.x[2 * k + 1];
@@ -2237,9 +2238,10 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
                 m = fabsf(v);
             }
             for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+            // this group's max in its own slot (the consumer takes the largest)
             if (lane == 0)
-                __hip_atomic_fetch_max(w.silu_max, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(w.silu_max + g, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }

@@ -161,7 +161,7 @@ struct tmq_model {
     TmqEngState* state = nullptr;
     int32_t* tokens = nullptr;
     float* silu_x = nullptr;      // SiLU(gate) * up of the current layer
-    uint32_t* max_bits = nullptr; // per layer max |silu_x| (in the zeroed accumulator range)
+    uint32_t* max_bits = nullptr; // per layer TMQ_MAX_SLOTS slots of max |silu_x| (in the zeroed accumulator range)
     Launch logits_l;
     uint64_t weight_bytes = 0;
     int pos = -1;  // host mirror of state.pos
@@ -262,7 +262,8 @@ int launch_layers(tmq_model* m, bool dump, float* cap = nullptr) {
         PROF(L.fused_gu ? "ffn_norm+gate+up+silu_x_up" : "ffn_norm+gate+up", rc = launch_gemv(m, L.gu));
         if (rc) return rc;
         if (!L.fused_gu)
-            PROF("silu_x_up", LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x, m->max_bits + 2 * l, s)));
+            PROF("silu_x_up", LAUNCH_TRY(tmq_launch_silu(L.dg, L.du, c.inter, m->silu_x,
+                                                         m->max_bits + TMQ_MAX_SLOTS * l, s)));
         if (cap)
             HIP_TRY(hipMemcpyAsync(cap + l * per + 3 * (size_t)H, m->silu_x, sizeof(float) * c.inter,
                                    hipMemcpyDeviceToDevice, s));
@@ -726,9 +727,10 @@ int build_launches(tmq_model* m) {
         acc_off[l] = acc_n;
         for (const tmq_tensor* t : {Y.q, Y.k, Y.v, Y.o, Y.gate, Y.up, Y.down}) acc_n += slot(t);
     }
-    if (acc_n + L > m->kacc_cap) return tmq_fail(TMQ_ERR_HIP, "accumulator layout exceeds its buffer");
-    m->kacc_n = acc_n + L;  // + one max slot per layer
-    m->max_bits = (uint32_t*)(m->kacc + acc_n);  // slot l at byte 8*l: every other u32
+    const size_t slots64 = TMQ_MAX_SLOTS / 2;  // int64 words holding a layer's max slots
+    if (acc_n + slots64 * L > m->kacc_cap) return tmq_fail(TMQ_ERR_HIP, "accumulator layout exceeds its buffer");
+    m->kacc_n = acc_n + slots64 * L;  // + the max slots of every layer
+    m->max_bits = (uint32_t*)(m->kacc + acc_n);  // layer l's slots at max_bits + TMQ_MAX_SLOTS * l
     auto fv_ptr = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
 
     // Work lists.  Every launch is one engine GEMV: per layer qkv / o /
@@ -842,13 +844,17 @@ int build_launches(tmq_model* m) {
         if (Y.fused_gu) {
             add_work(Y.gu, Y.gu_t, nullptr, nullptr, 1);
             Y.gu.P.w[0].silu = m->silu_x;
-            Y.gu.P.w[0].silu_max = m->max_bits + 2 * l;
+            Y.gu.P.w[0].silu_max = m->max_bits + TMQ_MAX_SLOTS * l;
+            if (Y.gu.P.w[0].ngroups > TMQ_MAX_SLOTS) return tmq_fail(TMQ_ERR_ARG, "ffn too wide for the max slots");
         } else {
             add_work(Y.gu, Y.gate, ag, xs + 2, kc_gu);
             add_work(Y.gu, Y.up, au, nullptr, kc_gu);
         }
         Y.dn.P.act = recipe(TMQ_ACT_PRESCALED, m->silu_x, nullptr, I);
-        Y.dn.P.act.max_bits = m->max_bits + 2 * l;
+        Y.dn.P.act.max_bits = m->max_bits + TMQ_MAX_SLOTS * l;
+        // fused gate/up: one slot per workgroup; silu_kernel: one atomic slot
+        Y.dn.P.act.max_n = Y.fused_gu ? Y.gu.P.w[0].ngroups : 1;
+        if (Y.dn.P.act.max_n > 64 * Y.dn.waves) return tmq_fail(TMQ_ERR_ARG, "more max slots than down threads");
         Y.dn.waves = all_fpga({Y.down}) ? nw_dn : 4;
         add_work(Y.dn, Y.down, ad, xs + 3, kc_dn);
     }
@@ -1029,7 +1035,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     place("cand", 8 * (size_t)n_cand);
     place("dump", 4 * (size_t)H * (L + 1));
     place("xs", 4 * 4 * (size_t)L);
-    place("kacc", 8 * (acc_cap_n + L));
+    place("kacc", 8 * (acc_cap_n + (size_t)(TMQ_MAX_SLOTS / 2) * L));
     place("silu", 4 * (size_t)I);
     place("fvec", 4 * fv.size() + 4);
     place("rope", sizeof(float2) * 32 * (size_t)max_seq);
@@ -1050,7 +1056,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     m->dump = (float*)(B + lay["dump"]);
     m->xs = (float*)(B + lay["xs"]);
     m->kacc = (int64_t*)(B + lay["kacc"]);
-    m->kacc_cap = acc_cap_n + L;
+    m->kacc_cap = acc_cap_n + (size_t)(TMQ_MAX_SLOTS / 2) * L;
     m->silu_x = (float*)(B + lay["silu"]);
     m->fvec = (float*)(B + lay["fvec"]);
     m->rope = (float2*)(B + lay["rope"]);
