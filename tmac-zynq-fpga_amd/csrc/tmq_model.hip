@@ -131,9 +131,9 @@ struct Prefill {
     int64_t* part = nullptr;
     uint32_t* max_bits = nullptr;
     int dn_split = 4;
-    int o_split = 4;   // attn_output GEMM split over K (finalised by the ffn_norm input)
-    int qkv_split = 7; // q/k/v GEMM split over K (finished by pf_qkv_fin)
-    int tile[4] = {3, 2, 3, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
+    int o_split = 2;   // attn_output GEMM split over K (finalised by the ffn_norm input)
+    int qkv_split = 1; // q/k/v GEMM split over K (finished by pf_qkv_fin)
+    int tile[4] = {4, 4, 3, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
 };
 
 struct tmq_model {
@@ -479,12 +479,17 @@ TmqPfSeg pf_seg(const tmq_tensor* t, int row0, const float* bias) {
     return sg;
 }
 
-// GEMM tile (tmq_launch_pf_gemm) for a plane set whose tensors start at the
-// given rows: the preferred one if its row tile (128 for tiles 0 and 2, 64
-// for tile 1; gate/up pairs: 64 / 32 per tensor) divides every boundary,
-// else the 64-row tile.
-int pf_tile(int want, std::initializer_list<int> bounds) {
-    const int rt = want == 1 || want == 3 ? 64 : 128;
+// GEMM tile (tmq_launch_pf_gemm) for a plane set of K columns whose tensors
+// start at the given rows: the preferred one if its row tile (128 for tiles
+// 0 and 2, 64 for tiles 1, 3 and 4; gate/up pairs: 64 / 32 per tensor)
+// divides every boundary and its stage (128 columns for tile 4, else 64)
+// divides K, else the 64-row tile.
+// columns per stage of a GEMM tile: the most splits over K it takes is K / this
+int pf_stage_cols(int tile) { return tile == 4 ? 128 : 64; }
+
+int pf_tile(int want, int K, std::initializer_list<int> bounds) {
+    const int rt = want == 1 || want == 3 || want == 4 ? 64 : 128;
+    if (K % pf_stage_cols(want)) return 1;
     for (int b : bounds)
         if (b % rt) return 1;
     return want;
@@ -496,8 +501,8 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
     Prefill& P = m->pf;
     const tmq_model_config& c = m->cfg;
     const int H = c.hidden, KV = c.n_kv_heads * TMQ_HEAD_DIM, I = c.inter, L = c.n_layers;
-    const int tile_qkv = pf_tile(P.tile[0], {H, KV}), tile_o = pf_tile(P.tile[1], {H});
-    const int tile_gu = pf_tile(P.tile[2], {2 * I}), tile_dn = pf_tile(P.tile[3], {H});
+    const int tile_qkv = pf_tile(P.tile[0], H, {H, KV}), tile_o = pf_tile(P.tile[1], H, {H});
+    const int tile_gu = pf_tile(P.tile[2], H, {2 * I}), tile_dn = pf_tile(P.tile[3], I, {H});
     const int T_pad = (T + 127) & ~127;  // whole 128-token GEMM tiles
     hipStream_t s = m->ctx->stream;
     auto fv = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
@@ -544,7 +549,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         d.xs = P.xs[3];
         d.row_inv = m->layers[l].down->dev.row_inv;
         d.bias = nullptr;
-        d.split = std::min(P.dn_split, I / 64);
+        d.split = std::min(P.dn_split, I / pf_stage_cols(tile_dn));
         d.ld = H;
         d.K = I;
         d.T_pad = T_pad;
@@ -565,7 +570,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         LAUNCH_TRY(tmq_launch_pf_act(a0, s));
         // q, k, v -> RoPE -> q buffer and this layer's caches; split over K,
         // finished by pf_qkv_fin (which also folds Q8_0 V tiles)
-        const int qkv_split = std::min(P.qkv_split, H / 64);
+        const int qkv_split = std::min(P.qkv_split, H / pf_stage_cols(tile_qkv));
         TmqPfGemm g = gemm(qkv_split > 1 ? TMQ_PF_QKVS : TMQ_PF_QKV, W.qkv, 0);
         g.split = qkv_split;
         g.nseg = 3;
@@ -617,7 +622,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         // attn_output, split over K; the residual and the finalisation go
         // with the ffn_norm input
         LAUNCH_TRY(tmq_launch_pf_act(act(TMQ_PF_PLAIN, 1, P.ctx, nullptr, H), s));
-        const int o_split = std::min(P.o_split, H / 64);  // at most one split per 64-column stage
+        const int o_split = std::min(P.o_split, H / pf_stage_cols(tile_o));  // at most one split per stage
         g = gemm(TMQ_PF_PART, W.o, 1);
         g.split = o_split;
         g.part = P.part;
@@ -650,7 +655,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         a3.max_bits = P.max_bits;
         LAUNCH_TRY(tmq_launch_pf_act(a3, s));
         g = gemm(TMQ_PF_PART, W.dn, 3);
-        g.split = std::min(P.dn_split, I / 64);
+        g.split = std::min(P.dn_split, I / pf_stage_cols(tile_dn));
         g.part = P.part;
         LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_dn, s));
     }

@@ -194,7 +194,8 @@ int tmq_launch_pf_wdigits(const TmqTensorDev& t, int8_t* planes, int K, int row0
 int tmq_launch_pf_rowsums(const TmqPfPlanes& p, hipStream_t s);
 int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s);
 // tile: 0 = 128 rows x 128 tokens per workgroup, 1 = 64 x 128, 2 = 128 x 64,
-// 3 = 64 x 128 with two stage buffers (three workgroups per CU)
+// 3 = 64 x 128 with two stage buffers (three workgroups per CU), 4 = 64 x 64
+// with K split in halves between the workgroup's waves (K a multiple of 128)
 int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s);
 int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);

@@ -38,28 +38,54 @@ __device__ __forceinline__ tmq_v16i mfma(tmq_v4i a, tmq_v4i b, tmq_v16i c) {
 __device__ __forceinline__ double digits_f64(int sac, int smid, int sbe, double c) {
     return __builtin_fma((double)sac, 65536.0, __builtin_fma((double)smid, 256.0, (double)sbe + c));
 }
+// (float)(t / (double)ri) for ri > 0, given rr = 1.0 / (double)ri
+// (correctly rounded).  q = t * rr is within 2.5 units in the last place of
+// the correctly rounded double quotient (two roundings of relative 2^-53
+// each, and that quotient's own half unit), so q and it round to the same
+// float unless a midpoint between two floats -- low 29 mantissa bits
+// 0x10000000 -- lies within 4 units of q, or q is outside the normal float
+// range; those take the division.
+__device__ __forceinline__ float div_f32_rr(double t, float ri, double rr) {
+    const double q = t * rr;
+    const uint64_t b = (uint64_t)__double_as_longlong(q);
+    const uint32_t lo = (uint32_t)b & 0x1fffffffu, e = (uint32_t)(b >> 52) & 0x7ffu;
+    if (lo - 0x0ffffffcu <= 8u || e - 897u > 253u) return (float)(t / (double)ri);
+    return (float)q;
+}
 // row (within a 32x32 block) of accumulator element v of lane l
 __device__ __forceinline__ int blk_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
-// Workgroup tiles: NWR x NWT waves, each wave 2 row blocks x WTB token
-// blocks; NBUF stage buffers of KC column steps in a ring, NBUF-1 stages in
-// flight (the copies' latency is hidden behind NBUF-1 stages of MFMA).
+// Workgroup tiles: KG groups of NWR x NWT waves, each wave 2 row blocks x
+// WTB token blocks; NBUF stage buffers of KG*KC column steps in a ring,
+// NBUF-1 stages in flight (the copies' latency is hidden behind NBUF-1
+// stages of MFMA).  With KG > 1 the groups take KC column steps each of
+// every stage (a split over K inside the workgroup) and add their integer
+// sums in LDS after the loop.
 template <int TILE> struct Tile;
-template <> struct Tile<0> { static constexpr int NWR = 2, NWT = 2, WTB = 2, NBUF = 4; };  // 128 rows x 128 tokens
-template <> struct Tile<1> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBUF = 3; };  // 64 x 128, 2 per CU
-template <> struct Tile<2> { static constexpr int NWR = 2, NWT = 2, WTB = 1, NBUF = 6; };  // 128 x 64
-template <> struct Tile<3> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBUF = 2; };  // 64 x 128, 3 per CU
-constexpr int KC = 2;  // column steps (of 32) per stage
+template <> struct Tile<0> { static constexpr int NWR = 2, NWT = 2, WTB = 2, NBUF = 4, KG = 1; };  // 128 rows x 128 tokens
+template <> struct Tile<1> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBUF = 3, KG = 1; };  // 64 x 128, 2 per CU
+template <> struct Tile<2> { static constexpr int NWR = 2, NWT = 2, WTB = 1, NBUF = 6, KG = 1; };  // 128 x 64
+template <> struct Tile<3> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBUF = 2, KG = 1; };  // 64 x 128, 3 per CU
+template <> struct Tile<4> { static constexpr int NWR = 1, NWT = 2, WTB = 1, NBUF = 3, KG = 2; };  // 64 x 64, K in halves
+constexpr int KC = 2;  // column steps (of 32) per stage and K group
 
 template <int TILE>
 struct TileGeo {
+    static constexpr int KG = Tile<TILE>::KG;
+    static constexpr int KS = KC * KG;                                 // column steps per stage
     static constexpr int NRB = 2 * Tile<TILE>::NWR;                    // row blocks per workgroup
     static constexpr int NTB = Tile<TILE>::NWT * Tile<TILE>::WTB;      // token blocks per workgroup
-    static constexpr int FRAGS = (NRB + NTB) * KC * 2;                 // 1 KiB fragments per stage
+    static constexpr int FRAGS = (NRB + NTB) * KS * 2;                 // 1 KiB fragments per stage
     static constexpr int FPW = FRAGS / 4;                              // per wave
     static constexpr int STAGE = FRAGS * 1024;
     static constexpr int NBUF = Tile<TILE>::NBUF;
+    static constexpr int GW = Tile<TILE>::NWR * Tile<TILE>::NWT;       // waves per K group
+    // int32 digit sums a wave holds: 2 x WTB blocks x 3 accumulators x 16
+    static constexpr int ACCW = 2 * Tile<TILE>::WTB * 3 * 16;
+    static_assert(GW * KG == 4 && KG <= 2, "four waves, K in one or two groups");
     static_assert((NBUF - 1) * FPW <= 63, "vmcnt holds 6 bits");
+    static_assert(KG * GW * (ACCW / 2) * 64 * 4 <= NBUF * STAGE, "the K groups' exchanged sums fit the stage ring");
+    static_assert(NBUF * STAGE >= 4 * 32 * 34 * 8, "the epilogue's transpose slices fit the stage ring");
 };
 
 // s_waitcnt vmcnt(k * FPW): the copies of the k newest stages may still be
@@ -87,7 +113,8 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     __shared__ __attribute__((aligned(1024))) int8_t lds[G::NBUF][G::STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int wr = wave / C::NWT, wt = wave % C::NWT;
+    const int kg = wave / G::GW, wq = wave % G::GW;  // K group, wave within it
+    const int wr = wq / C::NWT, wt = wq % C::NWT;
     // XCD-aware tile order: workgroups are dispatched to the 8 XCDs round
     // robin (id % 8); renumber so that consecutive workgroups of one XCD
     // share an operand in its L2 -- the token tiles of one row tile (the
@@ -116,9 +143,9 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     };
     const int tblk0 = by * G::NTB;
     const int nks = g.K >> 5;
-    const int nst_all = nks / KC;
-    const int st0 = (int)((int64_t)bz * nst_all / g.split);
-    const int st1 = (int)((int64_t)(bz + 1) * nst_all / g.split);
+    const int nst_all = nks / G::KS;
+    const int st0 = bz * nst_all / g.split;  // (nst_all * split < 2^31)
+    const int st1 = (bz + 1) * nst_all / g.split;
     const int nst = st1 - st0;
 
     // runtime segment (QKV, QKVS): the tile lies inside one tensor
@@ -132,32 +159,35 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     const bool q8 = QKVM && S.q8;
     const bool hasb = MODE == TMQ_PF_QKV && S.bias != nullptr;
 
-    // the epilogue's per-row constants of the workgroup's rows, in LDS:
-    // row_inv (Q8_0: row_scale), sum (w - 128), bias; the exp table (GU)
+    // the epilogue's per-row constants of the workgroup's rows -- row_inv
+    // (Q8_0: row_scale), sum (w - 128), bias -- one a thread, loaded here
+    // (they arrive during the K loop) and put into LDS after it, with the
+    // exp table (GU)
+    static_assert(G::NRB * 32 <= 256, "one row constant a thread");
     __shared__ float c_inv[G::NRB][32];
     __shared__ int32_t c_rw[G::NRB][32];
     __shared__ float c_bias[G::NRB][32];
+    __shared__ double c_rr[G::NRB][32];  // 1 / (double)c_inv
     __shared__ uint64_t c_tab[32];
-    if (!PARTM) {
-        for (int idx = threadIdx.x; idx < G::NRB * 32; idx += 256) {
-            const int i = idx >> 5, r = idx & 31;
-            const TmqPfSeg Sg = MODE == TMQ_PF_GU ? ((i & 1) ? g.seg[1] : g.seg[0]) : S;
-            const int row = rblk(i) * 32 + r, rr = row - Sg.row0;
-            c_inv[i][r] = q8 ? Sg.row_scale[rr] : Sg.row_inv[rr];
-            c_rw[i][r] = g.rw_t[row];
-            c_bias[i][r] = hasb ? Sg.bias[rr] : 0.0f;
-        }
-        if (MODE == TMQ_PF_GU && threadIdx.x < 32) c_tab[threadIdx.x] = tmq_math::exp2_tab(threadIdx.x);
+    float pre_inv = 0.0f, pre_bias = 0.0f;
+    int32_t pre_rw = 0;
+    if (!PARTM && (int)threadIdx.x < G::NRB * 32) {
+        const int i = threadIdx.x >> 5, r = threadIdx.x & 31;
+        const TmqPfSeg Sg = MODE == TMQ_PF_GU ? ((i & 1) ? g.seg[1] : g.seg[0]) : S;
+        const int row = rblk(i) * 32 + r, rr = row - Sg.row0;
+        pre_inv = q8 ? Sg.row_scale[rr] : Sg.row_inv[rr];
+        pre_rw = g.rw_t[row];
+        pre_bias = hasb ? Sg.bias[rr] : 0.0f;
     }
     // stage st -> buffer b: fragment f of FRAGS (run f / 2KC = one row or
     // token block, KC column steps x 2 digits contiguous on both sides);
     // wave w issues f = w, w+4, ...  K is a multiple of 32*KC.
     auto issue = [&](int st, int b) {
-        const int ks = (st0 + st) * KC;
+        const int ks = (st0 + st) * G::KS;
 #pragma unroll
         for (int k = 0; k < G::FPW; k++) {
             const int f = wave + 4 * k;  // wave-uniform
-            const int run = f / (KC * 2), in = f % (KC * 2);
+            const int run = f / (G::KS * 2), in = f % (G::KS * 2);
             const bool wgt = run < G::NRB;
             const int8_t* base = wgt ? g.w : g.x;
             const int blk = wgt ? rblk(run) : tblk0 + run - G::NRB;
@@ -166,8 +196,9 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
                                              (lds_i8*)(lds[b] + (size_t)f * 1024), 16, 0, 0);
         }
     };
+    // (column step kc of the wave's K group)
     auto frag = [&](int b, int run, int kc, int d) -> tmq_v4i {
-        return *(const tmq_v4i*)(lds[b] + ((size_t)(run * KC + kc) * 2 + d) * 1024 + lane * 16);
+        return *(const tmq_v4i*)(lds[b] + ((size_t)(run * G::KS + kg * KC + kc) * 2 + d) * 1024 + lane * 16);
     };
 
     tmq_v16i acc[2][WTB][3];
@@ -178,15 +209,40 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
 #pragma unroll
             for (int d = 0; d < 3; d++) acc[i][j][d] = tmq_v16i{};
     const int tw0 = (tblk0 + wt * WTB) * 32;  // first token of the wave
-    double xs_t[WTB], tc_t[WTB];
+    // the tokens' x_scale and sum (x - 128): loaded now, converted after the
+    // K loop (a conversion here would wait for the loads before the first
+    // copies are issued)
+    float xs_raw[WTB];
+    int32_t tx_raw[WTB];
 #pragma unroll
     for (int j = 0; j < WTB; j++) {
         const int t = tw0 + j * 32 + (lane & 31);
-        xs_t[j] = (double)g.xs[t];
-        tc_t[j] = (double)(128 * (int64_t)g.tx_t[t] + 16384 * (int64_t)g.K);
+        xs_raw[j] = g.xs[t];
+        tx_raw[j] = g.tx_t[t];
+    }
+
+    // RoPE pairs of the wave's q / k rows (QKV), loaded now: they arrive
+    // during the K loop
+    float4 rope_cs[WTB][2][4];
+    if (MODE == TMQ_PF_QKV && si != 2) {
+#pragma unroll
+        for (int j = 0; j < WTB; j++) {
+            const int pos = g.p0 + min(tw0 + j * 32 + (lane & 31), g.T - 1);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int rr = rblk(2 * wr + i) * 32 + blk_row(4 * q, lane) - S.row0;
+                    rope_cs[j][i][q] = *(const float4*)(g.rope + (size_t)pos * 32 + ((rr & 63) >> 1));
+                }
+        }
     }
 
     for (int st = 0; st < G::NBUF - 1 && st < nst; st++) issue(st, st);
+    // the K loop, compiled twice: with the Q8_0 tile sums (Q8 true) and
+    // without them, so that the common loop carries none of their registers
+    auto kloop = [&](auto q8c) {
+    constexpr bool Q8 = decltype(q8c)::value;
     for (int st = 0; st < nst; st++) {
         const int b = st % G::NBUF;
         // refill the buffer the previous iteration finished with
@@ -198,7 +254,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         // stage's copies), as asm with a memory clobber so that no LDS
         // access moves across it.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const int ks = (st0 + st) * KC;
+        const int ks = (st0 + st) * G::KS + kg * KC;  // the group's first column step
 #pragma unroll
         for (int kc = 0; kc < KC; kc++) {
             {
@@ -218,7 +274,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
                     acc[1][j][1] = mfma(b1, c, acc[1][j][1]);
                 }
             }
-            if (QKVM && q8 && (kc & 1)) {
+            if (Q8 && (kc & 1)) {
                 // Q8_0: the 64-column tile just completed, as an int64 digit
                 // sum per element, for pf_qkv_fin_kernel
                 const int tile = (ks + kc) >> 1;
@@ -244,20 +300,88 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         // MFMAs above) before the next iteration copies stage st+2 into it
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
+    };
+    if (QKVM && q8) kloop(std::integral_constant<bool, true>{});
+    else kloop(std::integral_constant<bool, false>{});
 
     if (QKVM && q8) return;  // pf_qkv_fin_kernel finishes these rows
+    double xs_t[WTB], tc_t[WTB];
+#pragma unroll
+    for (int j = 0; j < WTB; j++) {
+        xs_t[j] = (double)xs_raw[j];
+        tc_t[j] = (double)(128 * (int64_t)tx_raw[j] + 16384 * (int64_t)g.K);
+    }
+    if (!PARTM) {
+        if ((int)threadIdx.x < G::NRB * 32) {
+            const int i = threadIdx.x >> 5, r = threadIdx.x & 31;
+            c_inv[i][r] = pre_inv;
+            c_rr[i][r] = 1.0 / (double)pre_inv;
+            c_rw[i][r] = pre_rw;
+            c_bias[i][r] = pre_bias;
+        }
+        if (MODE == TMQ_PF_GU && threadIdx.x < 32) c_tab[threadIdx.x] = tmq_math::exp2_tab(threadIdx.x);
+        __syncthreads();
+    }
+    // K groups (KG = 2): group g keeps row block g of its waves' two and
+    // finishes it; the other block's digit sums go to the wave of the other
+    // group that holds the same tile, through the stage ring (free since the
+    // loop's last barrier)
+    auto mine = [&](int i) { return G::KG == 1 || i == kg; };
+    if (G::KG == 2) {
+        int* red = (int*)&lds[0][0];
+        int* dst = red + (kg * G::GW + wq) * (WTB * 3 * 16) * 64 + lane;
+        const int* src = red + ((1 - kg) * G::GW + wq) * (WTB * 3 * 16) * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            if (mine(i)) continue;
+#pragma unroll
+            for (int j = 0; j < WTB; j++)
+#pragma unroll
+                for (int d = 0; d < 3; d++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) dst[((j * 3 + d) * 16 + v) * 64] = acc[i][j][d][v];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            if (!mine(i)) continue;
+#pragma unroll
+            for (int j = 0; j < WTB; j++)
+#pragma unroll
+                for (int d = 0; d < 3; d++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[i][j][d][v] += src[((j * 3 + d) * 16 + v) * 64];
+        }
+        // (the epilogue's transposes reuse the ring)
+        __syncthreads();
+    }
+    // the stage ring is free now (the last iteration's barrier): each wave
+    // turns its 32x32 blocks to [token][row] in its own slice of it, so that
+    // the global stores are whole rows of a token (every wave's LDS accesses
+    // execute in order, so no barrier between its writes and reads)
     if (PARTM) {
+        // int64 sums, 34 per token (16-byte aligned rows; two lanes a bank
+        // at most); stored 256 contiguous bytes a token, four tokens an
+        // instruction
+        int64_t* tp = (int64_t*)&lds[0][0] + wave * (32 * 34);
 #pragma unroll
         for (int j = 0; j < WTB; j++) {
-            const int t = tw0 + j * 32 + (lane & 31);
-            int64_t* out = g.part + ((size_t)bz * g.T_pad + t) * g.rows;
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 2; i++) {
+                if (!mine(i)) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++)
-                    out[rblk(2 * wr + i) * 32 + blk_row(v, lane)] = 65536 * (int64_t)acc[i][j][0][v] +
-                                                                    256 * (int64_t)acc[i][j][1][v] +
-                                                                    (int64_t)acc[i][j][2][v];
+                    tp[(lane & 31) * 34 + blk_row(v, lane)] = 65536 * (int64_t)acc[i][j][0][v] +
+                                                               256 * (int64_t)acc[i][j][1][v] +
+                                                               (int64_t)acc[i][j][2][v];
+                const int r0 = rblk(2 * wr + i) * 32, c = lane & 15;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int tt = (lane >> 4) + 4 * k;
+                    const longlong2 val = *(const longlong2*)(tp + tt * 34 + 2 * c);
+                    *(longlong2*)(g.part + ((size_t)bz * g.T_pad + tw0 + j * 32 + tt) * g.rows + r0 + 2 * c) = val;
+                }
+            }
         }
         return;
     }
@@ -268,7 +392,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         const int li = 2 * wr + i, rb = blk_row(v, lane);
         const double a = digits_f64(acc[i][j][0][v], acc[i][j][1][v], acc[i][j][2][v],
                                     tc_t[j] + (double)(128 * c_rw[li][rb]));
-        float f = (float)((a * xs_t[j]) / (double)c_inv[li][rb]);
+        float f = div_f32_rr(a * xs_t[j], c_inv[li][rb], c_rr[li][rb]);
         if (hasb) f = f + c_bias[li][rb];
         return f;
     };
@@ -283,6 +407,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
             const int pos = g.p0 + t;
 #pragma unroll
             for (int i = 0; i < 2; i++) {
+                if (!mine(i)) continue;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const int rr = rblk(2 * wr + i) * 32 + blk_row(4 * q, lane) - S.row0;  // pairs (rr, rr+1), (rr+2, rr+3)
@@ -291,7 +416,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
                     for (int k = 0; k < 4; k++) o[k] = fin(i, j, 4 * q + k);
                     if (si != 2) {
                         // apply_rope (sim/tmac_gguf.cpp:1537-1539)
-                        const float4 cs = *(const float4*)(g.rope + (size_t)pos * 32 + ((rr & 63) >> 1));
+                        const float4 cs = rope_cs[j][i][q];
 #pragma unroll
                         for (int k = 0; k < 2; k++) {
                             const float y0 = o[2 * k], y1 = o[2 * k + 1];
@@ -309,9 +434,13 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         } else if (MODE == TMQ_PF_GU) {
             // SwiGLU (sim/tmac_gguf.cpp:459-461): gate rows in block 0, the
             // same up rows in block 1
+            // (the SwiGLU values through the wave's LDS slice, 36 floats a
+            // token; stored 128 contiguous bytes a token, eight tokens an
+            // instruction)
             float m = 0.0f;
             const int j0 = rblk(2 * wr) * 32;
             const Exp2TabLds tab{c_tab};
+            float* tp = (float*)&lds[0][0] + wave * (32 * 36);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 float sv[4];
@@ -321,9 +450,13 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
                     sv[k] = (gv / (1.0f + tmq_math::tmq_expf_tab(-gv, tab))) * fin(1, j, 4 * q + k);
                     m = fmaxf(m, fabsf(sv[k]));
                 }
-                if (live)
-                    *(float4*)(g.s_out + (size_t)t * g.gu_rows + j0 + blk_row(4 * q, lane)) =
-                        make_float4(sv[0], sv[1], sv[2], sv[3]);
+                *(float4*)(tp + (lane & 31) * 36 + blk_row(4 * q, lane)) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int tt = (lane >> 3) + 8 * k, c = lane & 7, ts = tw0 + j * 32 + tt;
+                const float4 val = *(const float4*)(tp + tt * 36 + 4 * c);
+                if (ts < g.T) *(float4*)(g.s_out + (size_t)ts * g.gu_rows + j0 + 4 * c) = val;
             }
             m = fmaxf(m, __shfl_xor(m, 32));
             if (live && lane < 32)
@@ -355,17 +488,20 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
     const int t = a.T - 1 - (int)blockIdx.x, g = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
     const int qpk = a.n_heads / a.n_kv, KV = a.n_kv * 64, H = a.n_heads * 64;
     const int np = a.p0 + t + 1, npad = (np + 3) & ~3;
-    const int wv = tid >> 6, ln = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
     float* ex = lds;  // [qpk][npad]
     const float* kb = a.kc + g * 64;
     const float* vbase = a.vc + g * 64;
     const cf32* qg = (const cf32*)(a.q + (size_t)t * H + g * qpk * 64);
     if (tid < 32) tab[tid] = tmq_math::exp2_tab(tid);
-    // scores of positions tid + 512 k
+    // scores of positions tid + 512 k; a wave whose 64 positions all lie
+    // past the last one computes none (its entries are never read: every
+    // later use is guarded by p < np)
     float scr[NPASS][8];
 #pragma unroll
     for (int k = 0; k < NPASS; k++) {
         if (k > 0 && k * 512 >= np) break;
+        if (k * 512 + wv * 64 >= np) continue;
         const int p = tid + k * 512;
         float4 kk[16];
         const float4* kp = (const float4*)(kb + (size_t)min(p, np - 1) * KV);
@@ -681,6 +817,7 @@ int launch_tile(const TmqPfGemm& g, int tile, hipStream_t s) {
     case 1: return launch_gemm<MODE, 1>(g, s);
     case 2: return launch_gemm<MODE, 2>(g, s);
     case 3: return launch_gemm<MODE, 3>(g, s);
+    case 4: return launch_gemm<MODE, 4>(g, s);
     }
     return (int)hipErrorInvalidValue;
 }
@@ -696,14 +833,16 @@ int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
     // shapes the kernel assumes: 64-column chunks, whole token tiles of the
     // operand planes, whole row tiles (GU: gate/up tiles of NRB/2 blocks),
     // a split count no larger than the stages, one split for fused epilogues
-    if (tile < 0 || tile > 3) return (int)hipErrorInvalidValue;
-    const int nrb = tile == 1 || tile == 3 ? 2 : 4, ntb = tile == 2 ? 2 : 4;
-    if (g.K <= 0 || g.K % (32 * KC) || g.T_pad % (32 * ntb) || g.T > g.T_pad || g.split < 1 ||
-        g.split > g.K / (32 * KC))
+    if (tile < 0 || tile > 4) return (int)hipErrorInvalidValue;
+    const int nrb = tile == 1 || tile == 3 || tile == 4 ? 2 : 4, ntb = tile == 2 || tile == 4 ? 2 : 4;
+    const int ks = KC * (tile == 4 ? Tile<4>::KG : 1);  // column steps per stage
+    if (g.K <= 0 || g.K % (32 * ks) || g.T_pad % (32 * ntb) || g.T > g.T_pad || g.split < 1 ||
+        g.split > g.K / (32 * ks))
         return (int)hipErrorInvalidValue;
     if (g.mode != TMQ_PF_PART && g.mode != TMQ_PF_QKVS && g.split != 1) return (int)hipErrorInvalidValue;
     if (g.mode == TMQ_PF_GU) {
-        if (g.gu_rows % (16 * nrb) || g.rows != 2 * g.gu_rows) return (int)hipErrorInvalidValue;
+        // (the SwiGLU epilogue needs both blocks of a wave: no K groups)
+        if (tile == 4 || g.gu_rows % (16 * nrb) || g.rows != 2 * g.gu_rows) return (int)hipErrorInvalidValue;
     } else if (g.rows % (32 * nrb)) {
         return (int)hipErrorInvalidValue;
     }
