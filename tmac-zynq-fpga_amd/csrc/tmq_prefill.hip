@@ -602,7 +602,8 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
     }
     // context, 64 positions per chunk; the next chunk's V rows are loaded
     // into registers while the current one is summed (512 threads x 2 float4
-    // = one chunk)
+    // = one chunk; a wave's lanes take 64 positions of one group of four
+    // dimensions, so that their transposed stores hit 64 banks)
     auto put_v = [&](float* vt, int pr, int q4, float4 v) {
         vt[(4 * q4 + 0) * VT_LD + pr] = v.x;
         vt[(4 * q4 + 1) * VT_LD + pr] = v.y;
@@ -611,9 +612,9 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
     };
     {
         const int nr = min(64, np);
-        for (int i = tid; i < nr * 16; i += nt) {
-            const int pr = i >> 4, q4 = i & 15;
-            put_v(vb2[0], pr, q4, *(const float4*)(vbase + (size_t)pr * KV + 4 * q4));
+        for (int i = tid; i < 64 * 16; i += nt) {
+            const int pr = i & 63, q4 = i >> 6;
+            if (pr < nr) put_v(vb2[0], pr, q4, *(const float4*)(vbase + (size_t)pr * KV + 4 * q4));
         }
     }
     __syncthreads();
@@ -624,7 +625,7 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
         float4 pre[2];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int i = tid + j * 512, pr = i >> 4, q4 = i & 15;
+            const int i = tid + j * 512, pr = i & 63, q4 = i >> 6;
             if (pr < nr1) pre[j] = *(const float4*)(vbase + (size_t)(c1 + pr) * KV + 4 * q4);
         }
         if (wv < qpk) {
@@ -684,7 +685,7 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
         }
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int i = tid + j * 512, pr = i >> 4, q4 = i & 15;
+            const int i = tid + j * 512, pr = i & 63, q4 = i >> 6;
             if (pr < nr1) put_v(vb2[buf ^ 1], pr, q4, pre[j]);
         }
         __syncthreads();
