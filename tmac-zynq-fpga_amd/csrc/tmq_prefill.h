@@ -201,7 +201,7 @@ int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);
 int tmq_launch_pf_qkv_fin(const TmqPfQkvFin& f, hipStream_t s);
 size_t tmq_pf_attn_lds(int qpk, int npos);
-// dynamic LDS the attention kernel may take beside its ~36 KiB of static
+// dynamic LDS the attention kernel may take beside its ~19 KiB of static
 // buffers (160 KiB per workgroup in all), and the positions it attends over
 // at most (its scores are held in registers, 512 positions per pass)
 #define TMQ_PF_ATTN_LDS_MAX (120 * 1024)

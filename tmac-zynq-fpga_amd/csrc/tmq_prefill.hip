@@ -474,18 +474,22 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
 // thread keeps the scores of its positions (tid + 512 k, k < NPASS) in
 // registers; LDS holds the exp terms, then the weights, of every position.
 typedef __attribute__((address_space(4))) const float cf32;
-constexpr int VT_LD = 68;  // floats between dimensions of a transposed V chunk
+constexpr int VCH = 32;    // positions per V chunk
+constexpr int VT_LD = 36;  // floats between dimensions of a transposed V chunk
 template <int NPASS>
-__global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_attn_kernel(TmqPfAttn a) {
+__global__ __launch_bounds__(512, NPASS <= 2 ? 4 : 2) void pf_attn_kernel(TmqPfAttn a) {
     extern __shared__ float lds[];
     __shared__ float stat[2][8];
     __shared__ float red[8][8];  // [wave][head] maxima
     __shared__ uint64_t tab[32];
-    // V chunks of 64 positions, transposed (dimension-major, VT_LD apart) so
-    // that the lane of dimension d reads four positions at once; double-buffered
+    // V chunks of VCH positions, transposed (dimension-major, VT_LD apart)
+    // so that the lane of dimension d reads four positions at once;
+    // double-buffered.  (About 34 KiB of LDS a workgroup with the exp terms
+    // of 512 positions, and at most 64 registers: four workgroups a CU, so
+    // that the launch's 2 x T workgroups run in one round.)
     __shared__ __attribute__((aligned(16))) float vb2[2][64 * VT_LD];
     // the longest (latest) positions first
-    const int t = a.T - 1 - (int)blockIdx.x, g = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
+    const int t = a.T - 1 - (int)blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int qpk = a.n_heads / a.n_kv, KV = a.n_kv * 64, H = a.n_heads * 64;
     const int np = a.p0 + t + 1, npad = (np + 3) & ~3;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
@@ -503,24 +507,33 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
         if (k > 0 && k * 512 >= np) break;
         if (k * 512 + wv * 64 >= np) continue;
         const int p = tid + k * 512;
-        float4 kk[16];
         const float4* kp = (const float4*)(kb + (size_t)min(p, np - 1) * KV);
+        // the key row in two halves of 32 dimensions (each head's sum runs
+        // over the first half, then on over the second: the same order)
+        float s[8];
 #pragma unroll
-        for (int i = 0; i < 16; i++) kk[i] = kp[i];
+        for (int h = 0; h < 8; h++) s[h] = 0.0f;
 #pragma unroll
-        for (int h = 0; h < 8; h++) {
-            if (h >= qpk) break;
-            const cf32* qh = qg + h * 64;
-            float s = 0.0f;
+        for (int half = 0; half < 2; half++) {
+            float4 kk[8];
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                s += qh[4 * i + 0] * kk[i].x;
-                s += qh[4 * i + 1] * kk[i].y;
-                s += qh[4 * i + 2] * kk[i].z;
-                s += qh[4 * i + 3] * kk[i].w;
+            for (int i = 0; i < 8; i++) kk[i] = kp[8 * half + i];
+#pragma unroll
+            for (int h = 0; h < 8; h++) {
+                if (h >= qpk) break;
+                const cf32* qh = qg + h * 64 + 32 * half;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    s[h] += qh[4 * i + 0] * kk[i].x;
+                    s[h] += qh[4 * i + 1] * kk[i].y;
+                    s[h] += qh[4 * i + 2] * kk[i].z;
+                    s[h] += qh[4 * i + 3] * kk[i].w;
+                }
             }
-            scr[k][h] = s / 8.0f;
         }
+#pragma unroll
+        for (int h = 0; h < 8; h++)
+            if (h < qpk) scr[k][h] = s[h] / 8.0f;
     }
     // max per head: the thread's, the wave's, then the workgroup's (fmaxf
     // is exact in any order)
@@ -600,34 +613,29 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
             ex[h * npad + p] = tmq_math::tmq_expf_tab(scr[k][h] - stat[1][h], et);
         }
     }
-    // context, 64 positions per chunk; the next chunk's V rows are loaded
-    // into registers while the current one is summed (512 threads x 2 float4
-    // = one chunk; a wave's lanes take 64 positions of one group of four
-    // dimensions, so that their transposed stores hit 64 banks)
+    // context, VCH positions per chunk; the next chunk's V rows are loaded
+    // into registers while the current one is summed (512 threads x one
+    // float4 = one chunk; a wave's lanes take the chunk's 32 positions of two
+    // groups of four dimensions)
     auto put_v = [&](float* vt, int pr, int q4, float4 v) {
         vt[(4 * q4 + 0) * VT_LD + pr] = v.x;
         vt[(4 * q4 + 1) * VT_LD + pr] = v.y;
         vt[(4 * q4 + 2) * VT_LD + pr] = v.z;
         vt[(4 * q4 + 3) * VT_LD + pr] = v.w;
     };
+    static_assert(VCH * 16 == 512, "one float4 a thread per chunk");
     {
-        const int nr = min(64, np);
-        for (int i = tid; i < 64 * 16; i += nt) {
-            const int pr = i & 63, q4 = i >> 6;
-            if (pr < nr) put_v(vb2[0], pr, q4, *(const float4*)(vbase + (size_t)pr * KV + 4 * q4));
-        }
+        const int nr = min(VCH, np), pr = tid & (VCH - 1), q4 = tid / VCH;
+        if (pr < nr) put_v(vb2[0], pr, q4, *(const float4*)(vbase + (size_t)pr * KV + 4 * q4));
     }
     __syncthreads();
     float acc = 0.0f;
     int buf = 0;
-    for (int c0 = 0; c0 < np; c0 += 64) {
-        const int nr = min(64, np - c0), c1 = c0 + 64, nr1 = min(64, np - c1);
-        float4 pre[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int i = tid + j * 512, pr = i & 63, q4 = i >> 6;
-            if (pr < nr1) pre[j] = *(const float4*)(vbase + (size_t)(c1 + pr) * KV + 4 * q4);
-        }
+    for (int c0 = 0; c0 < np; c0 += VCH) {
+        const int nr = min(VCH, np - c0), c1 = c0 + VCH, nr1 = min(VCH, np - c1);
+        const int ppr = tid & (VCH - 1), pq4 = tid / VCH;
+        float4 pre;
+        if (ppr < nr1) pre = *(const float4*)(vbase + (size_t)(c1 + ppr) * KV + 4 * pq4);
         if (wv < qpk) {
             const float* e = ex + wv * npad + c0;
             const float* vt = vb2[buf] + ln * VT_LD;
@@ -651,16 +659,16 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
                     acc += ev[j].w * vv[j].w;
                 }
             };
-            if (nr == 64) {
+            if (nr == VCH) {
                 ld(ea, va, 0);
 #pragma unroll
-                for (int o = 0; o < 64; o += 16) {
+                for (int o = 0; o < VCH; o += 16) {
                     ld(eb, vb, o + 8);
                     mac(ea, va);
-                    if (o + 16 < 64) ld(ea, va, o + 16);
+                    if (o + 16 < VCH) ld(ea, va, o + 16);
                     mac(eb, vb);
                 }
-                pr = 64;
+                pr = VCH;
             }
             for (; pr + 8 <= nr; pr += 8) {
                 ld(ea, va, pr);
@@ -683,11 +691,7 @@ __global__ __launch_bounds__(512, NPASS == 1 ? 6 : NPASS == 2 ? 4 : 2) void pf_a
                 }
             }
         }
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int i = tid + j * 512, pr = i & 63, q4 = i >> 6;
-            if (pr < nr1) put_v(vb2[buf ^ 1], pr, q4, pre[j]);
-        }
+        if (ppr < nr1) put_v(vb2[buf ^ 1], ppr, pq4, pre);
         __syncthreads();
         buf ^= 1;
     }
