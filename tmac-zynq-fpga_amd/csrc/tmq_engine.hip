@@ -27,6 +27,7 @@ namespace {
 // entry, so their latency overlaps the q/k/v finalisation.
 template <bool Q8, bool K8, bool V8>
 __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
+    tmq_warm_kernargs<sizeof(TmqAttnArgs)>();
     extern __shared__ float lds[];
     float* sc = lds;                  // scores, max_pos
     float* ex = lds + a.max_pos;      // exp terms / weights, max_pos

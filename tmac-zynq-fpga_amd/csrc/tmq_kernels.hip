@@ -2450,6 +2450,7 @@ __device__ __forceinline__ void eng_dispatch(const TmqEngAct& a, const EngLds& L
 // except the last, which uses FB.
 template <int NW, int FA, int FB, bool MULTI>
 __global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngLaunch P) {
+    tmq_warm_kernargs<sizeof(TmqEngLaunch)>();
     extern __shared__ __attribute__((aligned(16))) unsigned char eng_smem[];
     const EngLds L = eng_lds(eng_smem, P.act.n, NW);
     if constexpr (!MULTI) {
@@ -2505,6 +2506,7 @@ __global__ __launch_bounds__(256) void zero_acc_kernel(int64_t* p, size_t n) {
 // sim/tmac_gguf.cpp:1225-1231: x_scale = max|x| (sequential fmaxf; the max
 // is order independent), /32767 unless < 1e-10; xq = (int16)roundf(x/x_scale)
 __global__ __launch_bounds__(1024) void act_prep_kernel(TmqActJobs jobs) {
+    tmq_warm_kernargs<sizeof(TmqActJobs)>();
     const TmqActJob& J = jobs.j[blockIdx.x];
     __shared__ float red[16];
     __shared__ float s_scale;
@@ -3052,6 +3054,7 @@ __device__ __forceinline__ float pf_value(const TmqPfAct& a, int t, int i, int t
 }
 template <int G>
 __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
+    tmq_warm_kernargs<sizeof(TmqPfAct)>();
     extern __shared__ float pf_lds[];
     __shared__ float red[8];
     __shared__ float spec[4 * 64];  // seq_sum_spec<4>

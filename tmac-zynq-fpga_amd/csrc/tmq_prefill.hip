@@ -105,6 +105,7 @@ __device__ __forceinline__ void wait_stages(int k) {
 
 template <int MODE, int TILE>
 __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gemm_kernel(TmqPfGemm g) {
+    tmq_warm_kernargs<sizeof(TmqPfGemm)>();
     typedef Tile<TILE> C;
     typedef TileGeo<TILE> G;
     constexpr int WTB = C::WTB;
@@ -478,6 +479,7 @@ constexpr int VCH = 32;    // positions per V chunk
 constexpr int VT_LD = 36;  // floats between dimensions of a transposed V chunk
 template <int NPASS>
 __global__ __launch_bounds__(512, NPASS <= 2 ? 4 : 2) void pf_attn_kernel(TmqPfAttn a) {
+    tmq_warm_kernargs<sizeof(TmqPfAttn)>();
     extern __shared__ float lds[];
     __shared__ float stat[2][8];
     __shared__ float red[8][8];  // [wave][head] maxima
@@ -703,6 +705,7 @@ __global__ __launch_bounds__(512, NPASS <= 2 ? 4 : 2) void pf_attn_kernel(TmqPfA
 // sums (rows fastest, one float4 store); threads of the blocks after: one
 // token and row of a Q8_0 v segment, from its tile sums (tokens fastest).
 __global__ __launch_bounds__(256) void pf_qkv_fin_kernel(TmqPfQkvFin f) {
+    tmq_warm_kernargs<sizeof(TmqPfQkvFin)>();
     const bool vq8 = f.seg[2].q8 != 0;
     const int nr = f.part ? f.H + (vq8 ? 1 : 2) * f.KV : 0;  // rows from split sums
     const int g4 = nr >> 2, nA = f.T * g4, nbA = (nA + 255) >> 8;
