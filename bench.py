@@ -134,6 +134,29 @@ def host_info():
     return {"nproc": os.cpu_count(), "cpu_model": model}
 
 
+def _stdout_to_stderr(fn):
+    """Runs fn with file descriptor 1 pointed at stderr: the compiled
+    reference prints its progress (model loading) on stdout, which carries
+    only the bench's JSON line.  The C library's buffer is flushed before the
+    descriptor is restored."""
+    import ctypes
+    import functools
+
+    @functools.wraps(fn)
+    def run(*a, **k):
+        sys.stdout.flush()
+        saved = os.dup(1)
+        os.dup2(2, 1)
+        try:
+            return fn(*a, **k)
+        finally:
+            ctypes.CDLL(None).fflush(None)
+            os.dup2(saved, 1)
+            os.close(saved)
+    return run
+
+
+@_stdout_to_stderr
 def cpu_baseline(seconds):
     """Reference CPU path on one core, bounded sample of the same workload:
     (i) the --fpga-q5-0 integer path (matmul_fpga_q5_0) and (ii) the no-flag
@@ -274,6 +297,7 @@ def prefill_bench(ctx, n=512, reps=5):
             "next_tokens": first}
 
 
+@_stdout_to_stderr
 def cpu_decode_baseline(seconds):
     """The reference engine (oracle/_ref: load_tmac + forward_all_layers +
     get_logits_q8 with the --fpga-* paths) on one host thread, greedy steps
