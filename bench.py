@@ -462,6 +462,11 @@ def main():
             "traffic": traffic,
             "kernel": "chain_kernel",
             "kernel_ms": round(kern_ms, 5),
+            # a step is the activation preparation plus the chain launch, so
+            # the launch alone cannot take longer; if it did, the two timed
+            # legs ran in different clock or cache states and frac is not to
+            # be trusted
+            "kernel_within_step": bool(kern_ms <= step_ms),
         },
     }
     if not args.no_extra and wl == "c2":
