@@ -1882,42 +1882,53 @@ __device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw) {
     return L;
 }
 
-// Sequential fp32 sum of v[i0..i1) in index order from `sum` (the
-// reference's loops), by the calling lane, from LDS (i0 a multiple of 4).  A
-// dependent fp32 add issues every ~8 cycles; the reads of the next 32 values
-// overlap the current 32 adds (two register batches used in turn, no copies
-// between them).
+// sum += the 64 values of a group, in order, in every lane: each lane of a
+// 16-lane row holds four of them (lane i: values 4i .. 4i+3, the same in the
+// four rows), and v_add_f32_dpp row_newbcast:i adds lane i's value of the
+// lane's own row as src0 (src0 + src1 = v + sum, the same rounded value as
+// sum + v).  No LDS traffic inside the chain; a dependent DPP add issues
+// about every 7 cycles.  s_nop 1: the two wait states a DPP read of a VGPR
+// needs after a VALU write of it.
+__device__ __forceinline__ float add64_rowbcast(float4 x, float sum) {
+#define TMQ_RB4(N)                                                                 \
+    "v_add_f32_dpp %0, %1, %0 row_newbcast:" #N " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_add_f32_dpp %0, %2, %0 row_newbcast:" #N " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_add_f32_dpp %0, %3, %0 row_newbcast:" #N " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_add_f32_dpp %0, %4, %0 row_newbcast:" #N " row_mask:0xf bank_mask:0xf\n\t"
+    asm volatile("s_nop 1\n\t" TMQ_RB4(0) TMQ_RB4(1) TMQ_RB4(2) TMQ_RB4(3) TMQ_RB4(4) TMQ_RB4(5) TMQ_RB4(6)
+                     TMQ_RB4(7) TMQ_RB4(8) TMQ_RB4(9) TMQ_RB4(10) TMQ_RB4(11) TMQ_RB4(12) TMQ_RB4(13)
+                         TMQ_RB4(14) TMQ_RB4(15)
+                 : "+v"(sum)
+                 : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w));
+#undef TMQ_RB4
+    return sum;
+}
+// Lane i's four values of group g of [i0, i1) (v[i0 + 64g + 4i ..]), +0.0
+// past i1.
+__device__ __forceinline__ float4 seq_group(const float* v, int i0, int i1, int g, int i) {
+    const int b = i0 + 64 * g + 4 * i;
+    if (b + 4 <= i1) return *(const float4*)(v + b);
+    float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (b + 0 < i1) r.x = v[b + 0];
+    if (b + 1 < i1) r.y = v[b + 1];
+    if (b + 2 < i1) r.z = v[b + 2];
+    return r;
+}
+// Sequential fp32 sum of v[i0..i1) in index order from each lane's `sum`
+// (the reference's loops), by a whole wave (the same i0, i1 in every lane;
+// i0 a multiple of 4), from LDS, in groups of 64 (add64_rowbcast), the next
+// group's values read during the current one's adds.  The values past i1 in
+// the last group are +0.0: adding +0.0 leaves any sum whose sign bit is
+// clear unchanged, which the callers guarantee (v >= 0, starts of
+// non-negative bits).
 __device__ __forceinline__ float seq_chain_lds(const float* v, int i0, int i1, float sum) {
-    const int n64 = (i1 - i0) & ~63;
-    const float4* q = (const float4*)(v + i0);
-    float4 A[8], B[8];
-    if (n64) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) A[j] = q[j];
+    const int i = threadIdx.x & 15, ng = (i1 - i0 + 63) >> 6;
+    float4 x = ng > 0 ? seq_group(v, i0, i1, 0, i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int g = 0; g < ng; g++) {
+        const float4 cur = x;
+        if (g + 1 < ng) x = seq_group(v, i0, i1, g + 1, i);
+        sum = add64_rowbcast(cur, sum);
     }
-    for (int i = 0; i < n64; i += 64) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) B[j] = q[i / 4 + 8 + j];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            sum += A[j].x;
-            sum += A[j].y;
-            sum += A[j].z;
-            sum += A[j].w;
-        }
-        if (i + 64 < n64) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) A[j] = q[i / 4 + 16 + j];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            sum += B[j].x;
-            sum += B[j].y;
-            sum += B[j].z;
-            sum += B[j].w;
-        }
-    }
-    for (int i = i0 + n64; i < i1; i++) sum += v[i];
     return sum;
 }
 
