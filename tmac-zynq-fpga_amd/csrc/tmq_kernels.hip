@@ -2018,17 +2018,32 @@ __device__ __forceinline__ float seq_sum_spec(const float* v, int n, float* scr,
             c[j] = __builtin_amdgcn_readfirstlane(c[j]);
             asm volatile("" : "+v"(o[j]), "+s"(c[j]));
         }
-        sum = o[0];  // segment 0 ran from the exact start in every lane
+        // the exact running sum as bits in a scalar register: a step is a
+        // few scalar instructions and one lane read
+        int sb = __builtin_amdgcn_readfirstlane(__float_as_int(o[0]));  // segment 0: exact in every lane
 #pragma unroll
         for (int j = 1; j < S; j++) {
             const int j0 = min(n, j * L), j1 = min(n, j0 + L);
             if (j0 >= j1) break;
-            const int sb = __builtin_amdgcn_readfirstlane((int)__float_as_uint(sum));
-            const int idx = sb - c[j] + 32;
-            const int li = idx & 63;
-            sum = idx == li && sb >= 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(o[j]), li))
-                                       : seq_chain_lds(v, j0, j1, sum);
+            // idx = sb - c_j + 32; a hit when idx is in [0, 64) and sb >= 0
+            int nsb, miss, idx;
+            asm volatile(
+                "s_sub_i32 %[i], %[sb], %[c]\n\t"
+                "s_add_i32 %[i], %[i], 32\n\t"
+                "s_cmp_lt_u32 %[i], 64\n\t"
+                "s_cselect_b32 %[m], 0, 1\n\t"
+                "s_cmp_lt_i32 %[sb], 0\n\t"
+                "s_cselect_b32 %[m], 1, %[m]\n\t"
+                "s_and_b32 %[i], %[i], 63\n\t"
+                "v_readlane_b32 %[r], %[o], %[i]"
+                : [r] "=s"(nsb), [m] "=&s"(miss), [i] "=&s"(idx)
+                : [sb] "s"(sb), [c] "s"(c[j]), [o] "v"(o[j])
+                : "scc");
+            sb = __builtin_expect(miss, 0)
+                     ? __builtin_amdgcn_readfirstlane(__float_as_int(seq_chain_lds(v, j0, j1, __int_as_float(sb))))
+                     : nsb;
         }
+        sum = __int_as_float(sb);
     }
     return sum;
 }
