@@ -12,7 +12,7 @@
 template <int BYTES>
 static __device__ __forceinline__ void tmq_warm_kernargs() {
     constexpr int N = (BYTES + 63) / 64;
-    static_assert(N >= 1 && N <= 15, "one to fifteen lines");
+    static_assert(N >= 1 && N <= 16, "one to sixteen lines");
     const auto p = __builtin_amdgcn_kernarg_segment_ptr();
     if constexpr (N == 1)
         asm volatile("s_load_dword s80, %0, 0x0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "memory");
@@ -44,6 +44,8 @@ static __device__ __forceinline__ void tmq_warm_kernargs() {
         asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_load_dword s93, %0, 0x340\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "memory");
     else if constexpr (N == 15)
         asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_load_dword s93, %0, 0x340\n" "s_load_dword s94, %0, 0x380\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "memory");
+    else if constexpr (N == 16)
+        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_load_dword s93, %0, 0x340\n" "s_load_dword s94, %0, 0x380\n" "s_load_dword s95, %0, 0x3c0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95", "memory");
 }
 
 // int64 row sums of a K-split GEMV live at the device coherence point

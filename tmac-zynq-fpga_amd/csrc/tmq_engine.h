@@ -14,7 +14,7 @@ struct TmqAttnArgs {
     TmqDeferred q, k, v;     // the QKV projections (K-split, with bias)
     float* kc;               // this layer's caches [max_pos][n_kv*64]
     float* vc;
-    const float2* rope;      // [max_pos][32] (cos, sin)
+    const float2* rope_cur;  // [32] (cos, sin) of the current position (the qkv launch's copy)
     TmqEngState* state;
     float* ctx;              // out [n_heads*64]
     int32_t n_heads, n_kv, max_pos, pad_;

@@ -22,9 +22,12 @@ namespace {
 
 // RoPE (sim/tmac_gguf.cpp:1527-1554, adjacent pairs, cos/sin table from the
 // host) + KV cache append (:1616-1617) + attention of one query head
-// (:1619-1655).  One workgroup per query head; head_dim is 64.  The cached
-// K row of each thread's first position and the first 64 V rows are read at
-// entry, so their latency overlaps the q/k/v finalisation.
+// (:1619-1655).  One workgroup per query head; head_dim is 64.  The q/k/v
+// terms and the RoPE row of this step (copied by the qkv launch) are read at
+// entry, before the position arrives, so the q/k/v finalisation waits for one
+// memory round trip; then the cached K row of each thread's first position
+// and the first 64 V rows (rows below the position: reading the rows not yet
+// written, as a position-free read would, measured 3 % slower per step).
 template <bool Q8, bool K8, bool V8>
 __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     tmq_warm_kernargs<sizeof(TmqAttnArgs)>();
@@ -46,10 +49,25 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     const TmqFinRaw<Q8> fq0 = fin_load<Q8>(a.q, h * 64 + 2 * j), fq1 = fin_load<Q8>(a.q, h * 64 + 2 * j + 1);
     const TmqFinRaw<K8> fk0 = fin_load<K8>(a.k, kv * 64 + 2 * j), fk1 = fin_load<K8>(a.k, kv * 64 + 2 * j + 1);
     const TmqFinRaw<V8> fv = fin_load<V8>(a.v, kv * 64 + jv);
-    const int pos = a.state->pos;
-    if (a.state->err || pos < 0 || pos >= a.max_pos) return;
+    const float2 cs = a.rope_cur[j];
     const float* kb = a.kc + kv * 64;
     const float* vb = a.vc + kv * 64;
+    const int pos = a.state->pos;
+    if (a.state->err || pos < 0 || pos >= a.max_pos) return;
+    float4 kk[16];
+    {
+        const float4* kp = (const float4*)(kb + (size_t)min(tid, max(pos - 1, 0)) * KV);
+#pragma unroll
+        for (int i = 0; i < 16; i++) kk[i] = kp[i];
+    }
+    // V rows 0..63 below pos (thread: rows tid/16 + 16 u, 16-byte column tid % 16)
+    float4 v0[4];
+    const int nv0 = max(min(64, pos), 1);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int pr = (tid >> 4) + 16 * u;
+        v0[u] = *(const float4*)(vb + (size_t)min(pr, nv0 - 1) * KV + 4 * (tid & 15));
+    }
     // V rows [c0, c0+64) of cached positions (< pos) into vbuf[buf], by the
     // threads from `first` on
     auto stage = [&](int c0, int buf, int first) {
@@ -59,15 +77,6 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
             *(float4*)&vbuf[buf][pr][4 * q4] = *(const float4*)(vb + (size_t)(c0 + pr) * KV + 4 * q4);
         }
     };
-    // then, in the order they are needed (loads retire in order): the RoPE
-    // factors, the cached K row of the thread's first position, the V rows
-    const float2 cs = a.rope[(size_t)pos * 32 + j];
-    float4 kk[16];
-    {
-        const float4* kp = (const float4*)(kb + (size_t)min(tid, max(pos - 1, 0)) * KV);
-#pragma unroll
-        for (int i = 0; i < 16; i++) kk[i] = kp[i];
-    }
     if (tid < 32) {
         const float q0 = fin_finish<Q8>(a.q, fq0, qxs), q1 = fin_finish<Q8>(a.q, fq1, qxs);
         qr[2 * tid] = q0 * cs.x - q1 * cs.y;
@@ -78,7 +87,8 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     } else if (tid >= 64 && tid < 128) {
         vn[tid - 64] = fin_finish<V8>(a.v, fv, vxs);
     }
-    stage(0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; u++) *(float4*)&vbuf[0][(tid >> 4) + 16 * u][4 * (tid & 15)] = v0[u];
     __syncthreads();
     if (tid < 64) {
         if (h % qpk == 0) {

@@ -197,6 +197,15 @@ struct TmqEngLaunch {
     TmqWork w[TMQ_ENG_MAXW];
     int32_t nworks;
     int32_t ngroups;   // total workgroups
+    // qkv launches (rope_out set): one more workgroup copies the RoPE row of
+    // the current position (rope_src[state->pos], 32 (cos, sin) pairs) to
+    // rope_out, so that the attention after the launch reads it without
+    // waiting for the position first
+    const float2* rope_src;
+    float2* rope_out;
+    const TmqEngState* rope_state;
+    int32_t rope_max_pos;
+    int32_t pad_;
 };
 
 // Activation-quantisation jobs: one workgroup each, at most TMQ_MAX_ACT per launch.

@@ -2477,6 +2477,13 @@ __device__ __forceinline__ void eng_dispatch(const TmqEngAct& a, const EngLds& L
 template <int NW, int FA, int FB, bool MULTI>
 __global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngLaunch P) {
     tmq_warm_kernargs<sizeof(TmqEngLaunch)>();
+    if ((int)blockIdx.x >= P.ngroups) {
+        // the RoPE-row workgroup (launched only with rope_out set)
+        const int pos = P.rope_state->pos;
+        if (threadIdx.x < 32 && pos >= 0 && pos < P.rope_max_pos)
+            P.rope_out[threadIdx.x] = P.rope_src[(size_t)pos * 32 + threadIdx.x];
+        return;
+    }
     extern __shared__ __attribute__((aligned(16))) unsigned char eng_smem[];
     const EngLds L = eng_lds(eng_smem, P.act.n, NW);
     if constexpr (!MULTI) {
@@ -3436,7 +3443,9 @@ int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
     if (!k) return (int)hipErrorInvalidValue;
     TmqEngLaunch arg = l;
     void* args[] = {&arg};
-    return (int)hipLaunchKernel(k, dim3(l.ngroups), dim3(64 * waves), args, tmq_eng_lds_bytes(l.act.n, waves), s);
+    if (l.rope_out && (!l.rope_src || !l.rope_state || l.rope_max_pos < 1)) return (int)hipErrorInvalidValue;
+    return (int)hipLaunchKernel(k, dim3(l.ngroups + (l.rope_out ? 1 : 0)), dim3(64 * waves), args,
+                                tmq_eng_lds_bytes(l.act.n, waves), s);
 }
 
 int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x, uint32_t* max_bits,

@@ -158,6 +158,7 @@ struct tmq_model {
     int n_cand = 0;
     float *kc = nullptr, *vc = nullptr;
     float2* rope = nullptr;
+    float2* rope_cur = nullptr;  // the current position's RoPE row (written by every qkv launch)
     TmqEngState* state = nullptr;
     int32_t* tokens = nullptr;
     float* silu_x = nullptr;      // SiLU(gate) * up of the current layer
@@ -249,7 +250,7 @@ int launch_layers(tmq_model* m, bool dump, float* cap = nullptr) {
         aa.v = L.dv;
         aa.kc = m->kc + (size_t)l * c.max_seq * KV;
         aa.vc = m->vc + (size_t)l * c.max_seq * KV;
-        aa.rope = m->rope;
+        aa.rope_cur = m->rope_cur;
         aa.state = m->state;
         aa.ctx = m->ctxv;
         aa.n_heads = c.n_heads;
@@ -838,6 +839,10 @@ int build_launches(tmq_model* m) {
         add_work(Y.qkv, Y.q, aq, xs + 0, kc_qkv);
         add_work(Y.qkv, Y.k, ak, nullptr, kc_qkv);
         add_work(Y.qkv, Y.v, av, nullptr, kc_qkv);
+        Y.qkv.P.rope_src = m->rope;
+        Y.qkv.P.rope_out = m->rope_cur;
+        Y.qkv.P.rope_state = m->state;
+        Y.qkv.P.rope_max_pos = c.max_seq;
         Y.o_l.P.act = recipe(TMQ_ACT_PLAIN, m->ctxv, nullptr, H);
         Y.o_l.waves = all_fpga({Y.o}) ? nw_o : 4;
         add_work(Y.o_l, Y.o, ao, xs + 1, kc_o);
@@ -1044,6 +1049,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     place("silu", 4 * (size_t)I);
     place("fvec", 4 * fv.size() + 4);
     place("rope", sizeof(float2) * 32 * (size_t)max_seq);
+    place("rope_cur", sizeof(float2) * 32);
     place("kc", 4 * (size_t)L * max_seq * KV);
     place("vc", 4 * (size_t)L * max_seq * KV);
     hipError_t e = hipMalloc(&m->dmem, off);
@@ -1065,6 +1071,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     m->silu_x = (float*)(B + lay["silu"]);
     m->fvec = (float*)(B + lay["fvec"]);
     m->rope = (float2*)(B + lay["rope"]);
+    m->rope_cur = (float2*)(B + lay["rope_cur"]);
     m->kc = (float*)(B + lay["kc"]);
     m->vc = (float*)(B + lay["vc"]);
 
