@@ -214,6 +214,12 @@ int tmq_vecmul_tile_q8(tmq_ctx* ctx, const uint8_t* q8_W, const uint16_t* cs,
  * (8 rows x 896), act int16[896], row_inv[8]; result[row_base+i] += acc_i. */
 int tmq_vecmul_tile_q5_0_8x896(tmq_ctx* ctx, const uint8_t* blocks, const int16_t* act,
                                const float* row_inv, int64_t* result, int row_base);
+/* axi_vecmul_tile_q5_0_4x896_axilite (sim/fpga_sim.hpp:1194): the hp_fsm
+ * 4x896 tile, 56 interleaved 48-byte pairs (core 0 block, core 1 block, 4
+ * bytes of padding; pair bi: column block bi % 28 of rows bi / 28 and
+ * 2 + bi / 28), act int16[896], row_norm[4]; result[row_base+i] += acc_i. */
+int tmq_vecmul_tile_q5_0_4x896(tmq_ctx* ctx, const uint8_t* blocks56, const int16_t* act,
+                               const float* row_norm, int64_t* result, int row_base);
 /* axi_vecmul_tile_q6_k_axilite (sim/fpga_sim.hpp:1058) and
  * axi_vecmul_tile_q4k_axilite (sim/fpga_sim.hpp:821): nblocks one-row blocks,
  * act int16[ncols] (ncols <= 256 columns of each block are used), row_inv

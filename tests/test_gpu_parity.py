@@ -164,6 +164,28 @@ def test_tiles_vs_oracle_clamp(ctx, oracle):
         assert np.array_equal(a, b)
 
 
+def test_tile_q5_0_4x896_vs_oracle(ctx, oracle):
+    """The hp_fsm 4x896 tile (56 interleaved 48-byte block pairs, UQ8.8-sized
+    row_norm, and large ones that saturate) against the oracle, which
+    test_oracle_ref pins to the compiled reference's
+    axi_vecmul_tile_q5_0_4x896_axilite."""
+    rng = np.random.Generator(np.random.PCG64(11))
+    for scale in (np.float32(4.0), np.float32(4000.0), np.float32(1e7)):
+        b56 = rng.integers(0, 256, size=56 * 48, dtype=np.uint8)
+        for i in range(56):  # finite fp16 scales of both cores
+            b56[i * 48: i * 48 + 2] = np.array([np.float16(0.01 * (1 + i % 5))], np.float16).view(np.uint8)
+            b56[i * 48 + 22: i * 48 + 24] = np.array([np.float16(-0.02 * (1 + i % 3))], np.float16).view(np.uint8)
+        act = rng.integers(-32767, 32768, size=896, dtype=np.int16)
+        rn = (rng.random(4, dtype=np.float32) * scale).astype(np.float32)
+        a = rng.integers(-1000, 1000, size=10).astype(np.int64)
+        b = a.copy()
+        ctx.tile_q5_0_4x896(b56, act, rn, a, 5)
+        oracle.tile_q5_0_4x896(b56, act, rn, b, 5)
+        assert np.array_equal(a, b), f"row_norm scale {scale}"
+    with pytest.raises(ValueError):
+        ctx.tile_q5_0_4x896(b56, act, rn, np.zeros(6, np.int64), 3)
+
+
 def test_golden_phaseb(ctx):
     g = load_golden("phaseb.npz")
     arena = g["arena"].copy()

@@ -865,6 +865,31 @@ int tmq_vecmul_tile_q5_0_8x896(tmq_ctx* ctx, const uint8_t* blocks, const int16_
     return 0;
 }
 
+int tmq_vecmul_tile_q5_0_4x896(tmq_ctx* ctx, const uint8_t* blocks56, const int16_t* act,
+                               const float* row_norm, int64_t* result, int row_base) {
+    if (!ctx || !blocks56 || !act || !row_norm || !result) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    // the 56 interleaved 48-byte pairs (core 0 block, core 1 block, 4 bytes
+    // of padding) as 4 rows of 28 ggml blocks: pair bi holds column block
+    // bi % 28 of row bi / 28 (core 0) and of row 2 + bi / 28 (core 1)
+    // (sim/fpga_sim.hpp:1215-1222); the weight is the same (d*q)*row_norm
+    // rounded and clamped to int16 as the 8-row tile's (d*q)*row_inv
+    std::vector<uint8_t> rows((size_t)4 * 28 * 22);
+    for (int bi = 0; bi < 56; bi++) {
+        const int r = bi / 28, cb = bi % 28;
+        memcpy(&rows[((size_t)r * 28 + cb) * 22], blocks56 + (size_t)bi * 48, 22);
+        memcpy(&rows[((size_t)(r + 2) * 28 + cb) * 22], blocks56 + (size_t)bi * 48 + 22, 22);
+    }
+    tmq_tensor* t = nullptr;
+    int rc = tensor_create(ctx, TMQ_TYPE_Q5_0, 4, 896, rows.data(), false, rows.size(), nullptr, false, row_norm, &t);
+    if (rc) return rc;
+    std::vector<int64_t> acc;
+    rc = run_int16(ctx, t, act, acc);
+    tmq_tensor_free(t);
+    if (rc) return rc;
+    for (int i = 0; i < 4; i++) result[row_base + i] += acc[i];
+    return 0;
+}
+
 static int tile_kquant(tmq_ctx* ctx, uint32_t type, const uint8_t* blocks, int nblocks,
                        const int16_t* act, int ncols, const float* row_inv, int64_t* result,
                        int row_base) {

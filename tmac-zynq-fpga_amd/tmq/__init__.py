@@ -37,7 +37,7 @@ EXPORTS = [
     "tmq_tensor_row_norm", "tmq_tensor_fit_stats", "tmq_tensor_ifit_stats", "tmq_matmul", "tmq_gemv_dev", "tmq_gemv_dev_noalloc",
     "tmq_gemv_partials", "tmq_route", "tmq_matmul_flags", "tmq_matmul_path", "tmq_gemv_dev_path",
     "tmq_gemv_partials_path", "tmq_tensor_prepare_int16",
-    "tmq_vecmul_tile_q8", "tmq_vecmul_tile_q5_0_8x896", "tmq_vecmul_tile_q6_k",
+    "tmq_vecmul_tile_q8", "tmq_vecmul_tile_q5_0_8x896", "tmq_vecmul_tile_q5_0_4x896", "tmq_vecmul_tile_q6_k",
     "tmq_vecmul_tile_q4k", "tmq_phaseb_run", "tmq_chain_create", "tmq_chain_run",
     "tmq_chain_prepare", "tmq_chain_launch",
     "tmq_chain_free", "tmq_chain_weight_bytes",
@@ -120,6 +120,7 @@ def lib(path: str = LIB_PATH):
         "tmq_tensor_prepare_int16": (I, [P, P]),
         "tmq_vecmul_tile_q8": (I, [P, P, P, P, P]),
         "tmq_vecmul_tile_q5_0_8x896": (I, [P, P, P, P, P, I]),
+        "tmq_vecmul_tile_q5_0_4x896": (I, [P, P, P, P, P, I]),
         "tmq_vecmul_tile_q6_k": (I, [P, P, I, P, I, P, P, I]),
         "tmq_vecmul_tile_q4k": (I, [P, P, I, P, I, P, P, I]),
         "tmq_phaseb_run": (I, [P, P, U64, U32, U32, P, I]),
@@ -372,6 +373,17 @@ class Context:
 
     def tile_q5_0_8x896(self, blocks, act, row_inv, result, row_base):
         _check(lib().tmq_vecmul_tile_q5_0_8x896(self.handle, _p(blocks), _p(act), _p(row_inv),
+                                                _p(result), row_base))
+
+    def tile_q5_0_4x896(self, blocks56, act, row_norm, result, row_base):
+        """axi_vecmul_tile_q5_0_4x896_axilite: 56 interleaved 48-byte block
+        pairs, act int16[896], row_norm float32[4]; result[row_base+i] += acc_i"""
+        if (blocks56.dtype != np.uint8 or blocks56.size < 56 * 48 or act.dtype != np.int16 or act.size < 896
+                or row_norm.dtype != np.float32 or row_norm.size < 4 or result.dtype != np.int64
+                or not 0 <= row_base <= result.size - 4):
+            raise ValueError("tile_q5_0_4x896: uint8[2688], int16[896], float32[4], int64 result with 4 rows "
+                             "from row_base")
+        _check(lib().tmq_vecmul_tile_q5_0_4x896(self.handle, _p(blocks56), _p(act), _p(row_norm),
                                                 _p(result), row_base))
 
     def tile_kquant(self, qtype, blocks, nblocks, act, ncols, row_inv, result, row_base):
