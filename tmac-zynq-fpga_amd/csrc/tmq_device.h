@@ -48,6 +48,45 @@ static __device__ __forceinline__ void tmq_warm_kernargs() {
         asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_load_dword s93, %0, 0x340\n" "s_load_dword s94, %0, 0x380\n" "s_load_dword s95, %0, 0x3c0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95", "memory");
 }
 
+// Wave reductions by DPP lane moves (VALU only; __shfl_xor is a chain of six
+// LDS round trips): pairs and quads (quad permutations), rows of 8 and 16
+// (half-row and row mirrors), row 0 into row 1 and row 2 into row 3
+// (row_bcast15), rows 0-1 into rows 2-3 (row_bcast31); lane 63 then holds
+// the whole wave's value.  `old` is what a lane that a move leaves without a
+// source reads: the identity of the operation.
+template <int CTRL, int ROW_MASK = 0xf>
+static __device__ __forceinline__ int tmq_dpp_i32(int v, int old) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+// fmaxf over the wave, the same value in every lane (a quiet NaN is fmaxf's
+// identity; fmaxf picks the same value in any order for the inputs used
+// here, which hold no -0)
+static __device__ __forceinline__ float tmq_wave_max(float x) {
+    const int q = 0x7fc00000;
+    x = fmaxf(x, __int_as_float(tmq_dpp_i32<0xb1>(__float_as_int(x), q)));
+    x = fmaxf(x, __int_as_float(tmq_dpp_i32<0x4e>(__float_as_int(x), q)));
+    x = fmaxf(x, __int_as_float(tmq_dpp_i32<0x141>(__float_as_int(x), q)));
+    x = fmaxf(x, __int_as_float(tmq_dpp_i32<0x140>(__float_as_int(x), q)));
+    x = fmaxf(x, __int_as_float(tmq_dpp_i32<0x142, 0xa>(__float_as_int(x), q)));
+    x = fmaxf(x, __int_as_float(tmq_dpp_i32<0x143, 0xc>(__float_as_int(x), q)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+// integer sum over each 16-lane row, in every lane of the row
+static __device__ __forceinline__ int tmq_row_sum(int x) {
+    x += tmq_dpp_i32<0xb1>(x, 0);
+    x += tmq_dpp_i32<0x4e>(x, 0);
+    x += tmq_dpp_i32<0x141>(x, 0);
+    x += tmq_dpp_i32<0x140>(x, 0);
+    return x;
+}
+// integer sum over the wave, the same value in every lane
+static __device__ __forceinline__ int tmq_wave_sum(int x) {
+    x = tmq_row_sum(x);
+    x += tmq_dpp_i32<0x142, 0xa>(x, 0);
+    x += tmq_dpp_i32<0x143, 0xc>(x, 0);
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
 // int64 row sums of a K-split GEMV live at the device coherence point
 // (device-scope atomics); reads go there too.
 static __device__ __forceinline__ int64_t tmq_ld_acc(const int64_t* p) {

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     __syncthreads();
     float m = -__builtin_inff();
     for (int p = tid; p <= pos; p += blockDim.x) m = fmaxf(m, sc[p]);
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = tmq_wave_max(m);
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

@@ -2099,7 +2099,7 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
             if (tid < a.max_n) mv = __hip_atomic_load(a.max_bits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         m = __builtin_bit_cast(float, mv);
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = tmq_wave_max(m);
         if ((tid & 63) == 0) L.red[2 + (tid >> 6)] = m;
     } else if ((a.mode == TMQ_ACT_PLAIN || (a.mode == TMQ_ACT_RESID_NORM && a.d1.ntiles == 0 && !a.d1.val)) &&
                n <= EP * nt) {
@@ -2149,7 +2149,7 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
         };
         if (a.mode == TMQ_ACT_RESID_NORM) fast(std::true_type{});
         else fast(std::false_type{});
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = tmq_wave_max(m);
         if ((tid & 63) == 0) L.red[2 + (tid >> 6)] = m;
     } else {
         pre();
@@ -2168,7 +2168,7 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
             L.x[i] = v;
             m = fmaxf(m, fabsf(v));
         }
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = tmq_wave_max(m);
         if ((tid & 63) == 0) L.red[2 + (tid >> 6)] = m;
     }
     __syncthreads();
@@ -2257,13 +2257,13 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
             for (int i = 0; i < NW; i++) tot += L.part[i * 64 + lane];
             const float f = (float)(((double)tot * (double)xs) / (double)inv);
             const float up = __shfl_down(f, 32);
-            float m = 0.0f;
+            float m = __int_as_float(0x7fc00000);  // lanes 32-63: fmaxf's identity
             if (lane < 32) {
                 const float v = (f / (1.0f + tmq_math::tmq_expf(-f))) * up;
                 w.silu[g * 32 + lane] = v;
                 m = fabsf(v);
             }
-            for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+            m = tmq_wave_max(m);
             // this group's max in its own slot (the consumer takes the largest)
             if (lane == 0)
                 __hip_atomic_store(w.silu_max + g, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
@@ -2512,7 +2512,7 @@ __global__ __launch_bounds__(256) void silu_kernel(TmqDeferred g, TmqDeferred u,
         x[i] = v;
         m = fabsf(v);
     }
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = tmq_wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -2546,7 +2546,7 @@ __global__ __launch_bounds__(1024) void act_prep_kernel(TmqActJobs jobs) {
     const int n = J.n;
     float m = 0.0f;
     for (int j = threadIdx.x; j < n; j += blockDim.x) m = fmaxf(m, fabsf(J.x[j]));
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = tmq_wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -3216,7 +3216,7 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
             }
         }
     }
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = tmq_wave_max(m);
     if (lane == 0) red[1 + wave] = m;
     if (tid == 0 && a.zero_bits) a.zero_bits[t] = 0u;
     __syncthreads();
@@ -3258,11 +3258,11 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
             *(uint32_t*)(dp + o) = hi;
             *(uint32_t*)(dp + o + 1024) = lo;
         }
-        for (int k = 1; k < 16; k <<= 1) sum += __shfl_xor(sum, k);
+        sum = tmq_row_sum(sum);
         if (gi < ng && (gi & 15) == 0) a.out.csum[(size_t)t * nc + (gi >> 4)] = sum;
         tot += ((tid & 15) == 0 && gi < ng) ? sum : 0;
     }
-    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o);
+    tot = tmq_wave_sum(tot);
     __syncthreads();
     if (lane == 0) red[1 + wave] = __builtin_bit_cast(float, tot);
     __syncthreads();

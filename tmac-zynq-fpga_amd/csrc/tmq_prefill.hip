@@ -546,7 +546,7 @@ __global__ __launch_bounds__(512, NPASS <= 2 ? 4 : 2) void pf_attn_kernel(TmqPfA
 #pragma unroll
         for (int k = 0; k < NPASS; k++)
             if (h < qpk && tid + k * 512 < np) m = fmaxf(m, scr[k][h]);
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = tmq_wave_max(m);
         mx[h] = m;
     }
     if (ln == 0)
