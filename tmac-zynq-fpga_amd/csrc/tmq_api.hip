@@ -150,17 +150,20 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     d.rows_pad = (int)((rows + 63) / 64 * 64);
     d.nb = (int)(cols / qk);
     const size_t R = d.rows_pad, nb = d.nb;
-    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0, si = nb * R * tmq_ifit_codes((int)type);
+    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0, si = nb * R * tmq_ifit_codes((int)type), sq = 0;
     switch (type) {
     case TMQ_TYPE_Q8_0: sa = nb * 2 * R * 16; sd = nb * R * 2; break;
     case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; se = nb * R; break;
     case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; se = nb * R * 8; break;
-    case TMQ_TYPE_Q6_K: sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; se = nb * R * 16; break;
+    case TMQ_TYPE_Q6_K:
+        sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; se = nb * R * 16;
+        sq = nb * 12 * R * 16;
+        break;
     case TMQ_TYPE_F32: sa = nb * 8 * R * 16; break;
     case TMQ_TYPE_F16: sa = nb * 4 * R * 16; break;
     }
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(se) + al(si) + al(R * 4) * 2;
+    const size_t total = al(sa) + al(sb) + al(sc) + al(sd) + al(se) + al(si) + al(sq) + al(R * 4) * 2;
     hipError_t e = hipMalloc(&t->alloc, total);
     if (e != hipSuccess) {
         delete t;
@@ -179,6 +182,7 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     d.pd = sd ? p : nullptr; p += al(sd);
     d.pe = se ? p : nullptr; p += al(se);
     d.pi = si ? p : nullptr; p += al(si);
+    d.pq = sq ? p : nullptr; p += al(sq);
     d.row_inv = (const float*)p; p += al(R * 4);
     d.row_scale = (const float*)p;
     t->weight_bytes = rows * (cols / qk) * (uint64_t)block_bytes(type);
@@ -197,7 +201,8 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
 int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
     TmqTensorDev& d = t->dev;
     const char* nm = getenv("TMQ_NOMFMA");
-    const uint64_t plane = (uint64_t)d.rows_pad * (uint64_t)d.nb * (d.type == TMQ_TYPE_Q5_0 ? 16 : 128);
+    const uint64_t plane = (uint64_t)d.rows_pad * (uint64_t)d.nb *
+                           (d.type == TMQ_TYPE_Q5_0 ? 16 : d.type == TMQ_TYPE_Q6_K ? 192 : 128);
     if (!d.pi || d.clamp || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS || plane >= (1ull << 31)) {
         d.pi = nullptr;
         return 0;
@@ -360,6 +365,10 @@ int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, con
                                   (unsigned long long)rows, (unsigned long long)cols, type));
     rc = ifit_build(ctx, t);
     if (rc) return cleanup(rc);
+    if (t->dev.pi && t->dev.pq) {
+        le = tmq_launch_q6_pack(t->dev, ctx->stream);
+        if (le) return cleanup(tmq_fail(TMQ_ERR_HIP, "q6 pack launch: %s", hipGetErrorString((hipError_t)le)));
+    }
     cleanup(0);
     *out = t;
     return 0;

@@ -54,6 +54,9 @@ struct TmqTensorDev {
     const uint8_t* pe;       // fit codes (Q5_0: 1 B, Q4_K: 8 B, Q6_K: 16 B per block and row)
     const uint8_t* pi;       // integer fit codes of the MFMA decoders: Q5_0 [b][r] 1 B; Q4_K [b][q][r] 2 B
                              // (sub-blocks 2q, 2q+1); Q6_K [b][q][r] 4 B (the quarter's four sub-blocks)
+    const uint8_t* pq;       // Q6_K codes for the MFMA decoder: chunk 3q+k (k < 3) of block b, [b][12][r] 16 B,
+                             // holds sub-block k of quarter q (a code in the low 6 bits of each byte) and, in
+                             // the top 2 bits, bits 2k, 2k+1 of sub-block 3's codes
     const uint4* corr;       // their corrections (TmqCorr), grouped by 64-row group
     const int32_t* corr_off; // [rows_pad/64 + 1] first correction of each group (null: none)
     const float* row_inv;    // Q5_0/K-quants: row_inv; Q8_0: 1/row_scale (guarded)
@@ -228,6 +231,8 @@ struct ihipStream_t;
 typedef struct ihipStream_t* hipStream_t;
 int tmq_launch_act_prep(const TmqActJobs& jobs, hipStream_t s);
 int tmq_launch_repack(int type, const uint8_t* src, const TmqTensorDev& t, hipStream_t s);
+// Q6_K: the MFMA decoder's code plane (TmqTensorDev.pq) from the ql / qh planes
+int tmq_launch_q6_pack(const TmqTensorDev& t, hipStream_t s);
 // fit codes (plane pe) of a Q5_0 / Q4_K / Q6_K tensor from its planes and
 // row_inv; all_exact: every sub-block flagged for the exact decode
 int tmq_launch_fit(const TmqTensorDev& t, int all_exact, hipStream_t s);

@@ -1296,8 +1296,9 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
 // and 4-byte ones:
 //   Q4_K stage: qs chunks 2q, 2q+1 (1024 B each), header (1024 B), the two
 //               fit codes (256 B);
-//   Q6_K stage: ql chunks 4h+lc, 4h+2+lc, qh chunk 2h+lc, scales (1024 B
-//               each), d (256 B), the four fit codes (256 B).
+//   Q6_K stage: the quarter's three chunks of the packed code plane
+//               (q6_pack_kernel), scales (1024 B each), d (256 B), the four
+//               fit codes (256 B).
 // The activation's operand bytes, 32- and 16-element sums are copied into
 // LDS once per workgroup.
 constexpr int kKqWaves = 4;
@@ -1366,6 +1367,7 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
     const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(t.pb, (FMT == kQ4_K ? 16 : 64) * pb);
     const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(FMT == kQ6_K ? t.pc : t.pb, 16 * pb);
     const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(FMT == kQ6_K ? t.pd : t.pb, 2 * pb);
+    const __amdgpu_buffer_rsrc_t rsq = buf_rsrc(FMT == kQ6_K ? t.pq : t.pb, 192 * pb);
     const int l16 = lane * 16;
     // stage `slot` <- the wave's quarter i (clamped: refills past the end
     // reload the last quarter, so every step waits for the same count)
@@ -1382,13 +1384,11 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 3072), 2, lane * 2, ((b * 4 + q) * R + g64) * 2,
                                                      0, TMQ_CPOL_NT);
         } else {
-            const int h = q >> 1, lc = q & 1;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)st, 16, l16, ((b * 8 + 4 * h + lc) * R + g64) * 16,
-                                                     0, TMQ_CPOL_NT);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)(st + 1024), 16, l16,
-                                                     ((b * 8 + 4 * h + 2 + lc) * R + g64) * 16, 0, TMQ_CPOL_NT);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_u8*)(st + 2048), 16, l16,
-                                                     ((b * 4 + 2 * h + lc) * R + g64) * 16, 0, TMQ_CPOL_NT);
+            // the quarter's three code chunks of the packed plane
+#pragma unroll
+            for (int k = 0; k < 3; k++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsq, (lds_u8*)(st + 1024 * k), 16, l16,
+                                                         ((b * 12 + 3 * q + k) * R + g64) * 16, 0, TMQ_CPOL_NT);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_u8*)(st + 3072), 16, l16, (b * R + g64) * 16, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsd, (lds_u8*)(st + 4096), 2, lane * 2, (b * R + g64) * 2, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 4352), 4, lane * 4, ((b * 4 + q) * R + g64) * 4,
@@ -1491,9 +1491,6 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             issue(i + D, slot);
-            const uint4 qla = make_uint4((uint32_t)va.x, (uint32_t)va.y, (uint32_t)va.z, (uint32_t)va.w);
-            const uint4 qlb = make_uint4((uint32_t)vb.x, (uint32_t)vb.y, (uint32_t)vb.z, (uint32_t)vb.w);
-            const uint4 qhc = make_uint4((uint32_t)vh.x, (uint32_t)vh.y, (uint32_t)vh.z, (uint32_t)vh.w);
             const float ssri = h2f(dbits) * ri256;
 #pragma unroll
             for (int k = 0; k < NS; k++) {
@@ -1504,7 +1501,13 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
                 uint32_t U[4], T[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    U[e] = q6_codes(qla, qlb, qhc, k, e);
+                    // sub-blocks 0-2: the low 6 bits of chunk k; sub-block 3:
+                    // the top 2 bits of chunks 0, 1, 2 as its bits 0-1, 2-3, 4-5
+                    const uint32_t d0 = (uint32_t)va[e], d1 = (uint32_t)vb[e], d2 = (uint32_t)vh[e];
+                    U[e] = k == 0   ? d0 & 0x3f3f3f3fu
+                           : k == 1 ? d1 & 0x3f3f3f3fu
+                           : k == 2 ? d2 & 0x3f3f3f3fu
+                                    : ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0c0c0c0cu) | ((d2 >> 2) & 0x30303030u);
                     T[e] = ifit_t4(U[e], f[k].a2, f[k].b2);
                 }
                 UA[k][0] = tmq_v4i{(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
@@ -3276,10 +3279,44 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
 
 }  // namespace
 
+// The Q6_K code plane of the MFMA decoder (TmqTensorDev.pq): one thread per
+// (row, block, quarter) reads the quarter's ql / qh chunks as the decoder
+// read them and stores sub-blocks 0-2 of its codes a byte each, sub-block 3's
+// six bits spread over the top two bits of the three (48 bytes for 64
+// codes, as ql + qh): the decoder then takes 48 of every 64 codes with one
+// mask a dword.
+__global__ __launch_bounds__(256) void q6_pack_kernel(TmqTensorDev t) {
+    const size_t R = t.rows_pad, total = R * t.nb * 4;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int r = (int)(idx % R);
+    const int bq = (int)(idx / R), q = bq & 3, b = bq >> 2;
+    const int h = q >> 1, lc = q & 1;
+    const uint4 qla = *(const uint4*)(t.pa + (((size_t)b * 8 + 4 * h + lc) * R + r) * 16);
+    const uint4 qlb = *(const uint4*)(t.pa + (((size_t)b * 8 + 4 * h + 2 + lc) * R + r) * 16);
+    const uint4 qhc = *(const uint4*)(t.pb + (((size_t)b * 4 + 2 * h + lc) * R + r) * 16);
+    uint8_t* pq = (uint8_t*)t.pq;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        uint32_t D[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            D[e] = q6_codes(qla, qlb, qhc, k, e) | (((q6_codes(qla, qlb, qhc, 3, e) >> (2 * k)) & 0x03030303u) << 6);
+        *(uint4*)(pq + (((size_t)b * 12 + 3 * q + k) * R + r) * 16) = make_uint4(D[0], D[1], D[2], D[3]);
+    }
+}
+
 // ---------------------------------------------------------------- launchers
 int tmq_launch_act_prep(const TmqActJobs& jobs, hipStream_t s) {
     if (jobs.count <= 0) return 0;
     hipLaunchKernelGGL(act_prep_kernel, dim3(jobs.count), dim3(1024), 0, s, jobs);
+    return (int)hipGetLastError();
+}
+
+int tmq_launch_q6_pack(const TmqTensorDev& t, hipStream_t s) {
+    if (t.type != kQ6_K || !t.pq) return (int)hipErrorInvalidValue;
+    const size_t total = (size_t)t.rows_pad * t.nb * 4;
+    hipLaunchKernelGGL(q6_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, t);
     return (int)hipGetLastError();
 }
 
