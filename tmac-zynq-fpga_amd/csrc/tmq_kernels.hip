@@ -1431,6 +1431,17 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
         ap[k] = bp[k] = xp[k] = 0;
     }
     const tmq_v4i Z = {};
+    // Q4_K: a wave's quarter is the same in every super-block (wave & 3, as
+    // NW is 4), so sub-blocks s = 2q + k unpack from the header with
+    // wave-uniform fields (q4k_scale_min's cases):
+    //   q < 2:  sc = bits 8s..+5 of dword 1,  m = bits 8s..+5 of dword 2
+    //   q >= 2: s' = s - 4, sc = bits 8s'..+3 of dword 3 | bits 8s'+6, +7 of dword 1 << 4,
+    //           m = bits 8s'+4..+7 of dword 3 | bits 8s'+6, +7 of dword 2 << 4
+    // (a field of width 0 reads as 0)
+    static_assert(NW == 4, "the quarter of a wave is wave & 3");
+    const int qw = wave & 3, lo2 = qw < 2;
+    const uint32_t ko1 = lo2 ? 16 * qw : 16 * qw - 32, ko3 = lo2 ? ko1 : ko1 + 4, ko2 = ko1 + 6;
+    const uint32_t kw1 = lo2 ? 6 : 4, kw2 = lo2 ? 0 : 2;
     auto step = [&](int i, int slot) {
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<ND * (D - 1)>();
@@ -1454,10 +1465,13 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             issue(i + D, slot);
             const uint4 h = make_uint4((uint32_t)hv.x, (uint32_t)hv.y, (uint32_t)hv.z, (uint32_t)hv.w);
             const float dri = h2f(h.x) * ri256, mri = h2f(h.x >> 16) * ri256;
+            const uint32_t hp = lo2 ? h.y : h.w, hq = lo2 ? h.z : h.w;
 #pragma unroll
             for (int k = 0; k < NS; k++) {
-                int sc, m;
-                q4k_scale_min(h, 2 * q + k, sc, m);
+                const int sc = (int)(__builtin_amdgcn_ubfe(hp, ko1 + 8 * k, kw1) |
+                                     (__builtin_amdgcn_ubfe(h.y, ko2 + 8 * k, kw2) << 4));
+                const int m = (int)(__builtin_amdgcn_ubfe(hq, ko3 + 8 * k, kw1) |
+                                    (__builtin_amdgcn_ubfe(h.z, ko2 + 8 * k, kw2) << 4));
                 float an, bn;
                 q4k_nom(dri, mri, sc, m, an, bn);
                 f[k] = kfit(an, bn, 8, (codes >> (8 * k)) & 255u);
