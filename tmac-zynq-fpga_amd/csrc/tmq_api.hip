@@ -157,7 +157,7 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; se = nb * R * 8; break;
     case TMQ_TYPE_Q6_K:
         sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; se = nb * R * 16;
-        sq = nb * 12 * R * 16;
+        sq = nb * 12 * R * 16 + nb * 4 * R * 4;
         break;
     case TMQ_TYPE_F32: sa = nb * 8 * R * 16; break;
     case TMQ_TYPE_F16: sa = nb * 4 * R * 16; break;
@@ -202,7 +202,7 @@ int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
     TmqTensorDev& d = t->dev;
     const char* nm = getenv("TMQ_NOMFMA");
     const uint64_t plane = (uint64_t)d.rows_pad * (uint64_t)d.nb *
-                           (d.type == TMQ_TYPE_Q5_0 ? 16 : d.type == TMQ_TYPE_Q6_K ? 192 : 128);
+                           (d.type == TMQ_TYPE_Q5_0 ? 16 : d.type == TMQ_TYPE_Q6_K ? 208 : 128);
     if (!d.pi || d.clamp || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS || plane >= (1ull << 31)) {
         d.pi = nullptr;
         return 0;

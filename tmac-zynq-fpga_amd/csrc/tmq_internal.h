@@ -56,7 +56,8 @@ struct TmqTensorDev {
                              // (sub-blocks 2q, 2q+1); Q6_K [b][q][r] 4 B (the quarter's four sub-blocks)
     const uint8_t* pq;       // Q6_K codes for the MFMA decoder: chunk 3q+k (k < 3) of block b, [b][12][r] 16 B,
                              // holds sub-block k of quarter q (a code in the low 6 bits of each byte) and, in
-                             // the top 2 bits, bits 2k, 2k+1 of sub-block 3's codes
+                             // the top 2 bits, bits 2k, 2k+1 of sub-block 3's codes; then, at 192 B per
+                             // (row, block), the quarter's four sub-block scales, [b][q][r] 4 B
     const uint4* corr;       // their corrections (TmqCorr), grouped by 64-row group
     const int32_t* corr_off; // [rows_pad/64 + 1] first correction of each group (null: none)
     const float* row_inv;    // Q5_0/K-quants: row_inv; Q8_0: 1/row_scale (guarded)

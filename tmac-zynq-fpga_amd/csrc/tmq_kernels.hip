@@ -1365,9 +1365,8 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
     const uint32_t pb = (uint32_t)R * (uint32_t)nb;  // (row, block) pairs
     const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(t.pa, 128 * pb), rsi = buf_rsrc(t.pi, (FMT == kQ4_K ? 8 : 16) * pb);
     const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(t.pb, (FMT == kQ4_K ? 16 : 64) * pb);
-    const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(FMT == kQ6_K ? t.pc : t.pb, 16 * pb);
     const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(FMT == kQ6_K ? t.pd : t.pb, 2 * pb);
-    const __amdgpu_buffer_rsrc_t rsq = buf_rsrc(FMT == kQ6_K ? t.pq : t.pb, 192 * pb);
+    const __amdgpu_buffer_rsrc_t rsq = buf_rsrc(FMT == kQ6_K ? t.pq : t.pb, 208 * pb);
     const int l16 = lane * 16;
     // stage `slot` <- the wave's quarter i (clamped: refills past the end
     // reload the last quarter, so every step waits for the same count)
@@ -1389,7 +1388,8 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             for (int k = 0; k < 3; k++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rsq, (lds_u8*)(st + 1024 * k), 16, l16,
                                                          ((b * 12 + 3 * q + k) * R + g64) * 16, 0, TMQ_CPOL_NT);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_u8*)(st + 3072), 16, l16, (b * R + g64) * 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsq, (lds_u8*)(st + 3072), 4, lane * 4,
+                                                     (int)(192 * pb) + ((b * 4 + q) * R + g64) * 4, 0, TMQ_CPOL_NT);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsd, (lds_u8*)(st + 4096), 2, lane * 2, (b * R + g64) * 2, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 4352), 4, lane * 4, ((b * 4 + q) * R + g64) * 4,
                                                      0, TMQ_CPOL_NT);
@@ -1493,8 +1493,7 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             const int h = q >> 1, lc = q & 1;
             const tmq_v4i va = *(lv4i*)(st + lane * 16), vb = *(lv4i*)(st + 1024 + lane * 16);
             const tmq_v4i vh = *(lv4i*)(st + 2048 + lane * 16);
-            const uint32_t sc0 = *(lu32c*)(st + 3072 + lane * 16 + 8 * h);
-            const uint32_t sc1 = *(lu32c*)(st + 3072 + lane * 16 + 8 * h + 4);
+            const uint32_t scq = *(lu32c*)(st + 3072 + lane * 4);
             const uint32_t dbits = *(lu16*)(st + 4096 + lane * 4);
             const uint32_t codes = *(lu32c*)(st + 4352 + lane * 4);
 #pragma unroll
@@ -1508,9 +1507,8 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             const float ssri = h2f(dbits) * ri256;
 #pragma unroll
             for (int k = 0; k < NS; k++) {
-                // scale 8h + lc + 2k: byte lc + 2k of the 8 bytes at 8h
-                const uint32_t sw = (k < 2) ? sc0 : sc1;
-                const int sc = (int)(int8_t)(uint8_t)(sw >> (8 * (lc + 2 * (k & 1))));
+                // scale 8h + lc + 2k: byte k of the quarter's scale dword
+                const int sc = (int)(int8_t)(uint8_t)(scq >> (8 * k));
                 f[k] = kfit(ssri * (float)sc, 128.0f, 32, (codes >> (8 * k)) & 255u);
                 uint32_t U[4], T[4];
 #pragma unroll
@@ -3318,6 +3316,12 @@ __global__ __launch_bounds__(256) void q6_pack_kernel(TmqTensorDev t) {
             D[e] = q6_codes(qla, qlb, qhc, k, e) | (((q6_codes(qla, qlb, qhc, 3, e) >> (2 * k)) & 0x03030303u) << 6);
         *(uint4*)(pq + (((size_t)b * 12 + 3 * q + k) * R + r) * 16) = make_uint4(D[0], D[1], D[2], D[3]);
     }
+    // the quarter's scales 8h + lc + 2k, k = 0..3, one byte each
+    const uint4 sc = *(const uint4*)(t.pc + ((size_t)b * R + r) * 16);
+    uint32_t sq = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) sq |= (uint32_t)byte_of(sc, 8 * h + lc + 2 * k) << (8 * k);
+    *(uint32_t*)(pq + R * t.nb * 192 + (((size_t)b * 4 + q) * R + r) * 4) = sq;
 }
 
 // ---------------------------------------------------------------- launchers
