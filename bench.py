@@ -14,8 +14,10 @@ value  = ggml weight bytes streamed per step / step time  (GB/s).  A step is
          launch; K steps back to back between two HIP events on the
          library's stream.
 roofline.achieved = the same bytes / average duration of the GEMV launch:
-         K launches back to back on the prepared activation, timed the same
-         way right after the steps (same warmed clock), against 8 TB/s.
+         200 launches on the prepared activation in 4 blocks that alternate
+         with blocks of whole steps (same clock and cache state), against
+         8 TB/s.  When the launch alone comes out longer than the step blocks
+         beside it, achieved and frac are null.
 warm-up: after a burst of launches the GPU's clock dips for a few hundred
          launches before it settles, so GEMV chain workloads run at least
          MIN_WARMUP untimed steps whatever --warmup asks; the line reports
@@ -195,12 +197,31 @@ def cpu_baseline(seconds):
     return out
 
 
+ROOF_BLOCKS = 4      # interleaved (step block, launch block) pairs of the roofline legs
+ROOF_LAUNCHES = 200  # GEMV launches timed for the roofline, whatever --steps is
+
+
+def time_primed(torch, stream, fn, iters, prime=2):
+    """Average ms of fn over `iters` calls queued behind `prime` untimed
+    ones: the start event is recorded while the GPU is still busy, so the
+    host's time to issue the first timed launch is not counted."""
+    for _ in range(prime):
+        fn()
+    return time_events(torch, stream, fn, iters)
+
+
 def measure(ctx, torch, dev, stream, name, steps, warmup, copies=None):
-    """Returns (desc, weight bytes, step ms, kernel ms, n descriptors, copies).
+    """Returns a dict: desc, weight bytes, step ms (the contract's K steps),
+    kernel ms, the paired step ms, n descriptors, copies.
+
     A step = the activation-quantisation launch + the chain's GEMV launch.
-    The steps are timed as one run of K back to back (events only at the
-    ends: an event between launches costs the step a few microseconds);
-    the GEMV launch alone is timed right after in the same way."""
+    After the warm-up the roofline legs run as ROOF_BLOCKS alternating
+    pairs: a block of steps, then a block of GEMV launches alone (on the
+    activation the steps prepared), each block timed between two HIP events
+    on a primed queue, ROOF_LAUNCHES launches in all; so both legs see the
+    same clock and cache state.  Then the K steps of the contract are timed
+    between two synchronisations (events only at the ends: an event between
+    launches costs the step a few microseconds)."""
     copies = copies or copies_for(name)
     desc_txt, x_d, tensors, descs, ys = build_workload(ctx, torch, dev, name, copies)
     chain = ctx.chain(descs)
@@ -210,14 +231,23 @@ def measure(ctx, torch, dev, stream, name, steps, warmup, copies=None):
         chain.run()
     ctx.sync()
     torch.cuda.synchronize()
+    blk = ROOF_LAUNCHES // ROOF_BLOCKS
+    pair_step, pair_kern = [], []
+    for _ in range(ROOF_BLOCKS):
+        pair_step.append(time_primed(torch, stream, chain.run, blk))
+        pair_kern.append(time_primed(torch, stream, chain.launch, blk))
+    ctx.sync()
+    torch.cuda.synchronize()
     step_ms = time_events(torch, stream, chain.run, steps)
-    kern_ms = time_events(torch, stream, chain.launch, steps)
     ctx.sync()
     torch.cuda.synchronize()
     chain.free()
     for t in tensors:
         t.free()
-    return desc_txt, wbytes, step_ms, kern_ms, len(descs), copies
+    return {"desc": desc_txt, "wbytes": wbytes, "step_ms": step_ms,
+            "kern_ms": float(np.mean(pair_kern)), "pair_step_ms": float(np.mean(pair_step)),
+            "kern_blocks_ms": [round(v, 5) for v in pair_kern],
+            "ndesc": len(descs), "copies": copies}
 
 
 def single_launch_us(ctx, torch, dev, stream, steps):
@@ -419,18 +449,24 @@ def main():
         for name in ("c2", "c3q4k", "c3q6k", "c1"):
             for f in (1.0, 2.0, 4.0):
                 n = copies_for(name, f)
-                _, wb, sm, km, nd, _ = measure(ctx, torch, dev, stream, name, args.steps, args.warmup, n)
+                m = measure(ctx, torch, dev, stream, name, args.steps, args.warmup, n)
+                wb = m["wbytes"]
                 print(json.dumps({"sweep": name, "mall_factor": f, "sets": n, "weight_bytes": wb,
-                                  "ms_per_step": round(sm, 5), "kernel_ms": round(km, 5),
-                                  "step_gbps": round(wb / (sm * 1e-3) / 1e9, 2),
-                                  "kernel_gbps": round(wb / (km * 1e-3) / 1e9, 2)}), flush=True)
+                                  "ms_per_step": round(m["pair_step_ms"], 5), "kernel_ms": round(m["kern_ms"], 5),
+                                  "step_gbps": round(wb / (m["pair_step_ms"] * 1e-3) / 1e9, 2),
+                                  "kernel_gbps": round(wb / (m["kern_ms"] * 1e-3) / 1e9, 2)}), flush=True)
         ctx.close()
         return
     copies = args.sets if wl == "c2" else None
-    desc_txt, wbytes, step_ms, kern_ms, ndesc, copies = measure(ctx, torch, dev, stream, wl, args.steps,
-                                                                args.warmup, copies)
+    m = measure(ctx, torch, dev, stream, wl, args.steps, args.warmup, copies)
+    wbytes, step_ms, kern_ms, pair_ms = m["wbytes"], m["step_ms"], m["kern_ms"], m["pair_step_ms"]
     value = wbytes / (step_ms * 1e-3) / 1e9
     achieved = wbytes / (kern_ms * 1e-3) / 1e9
+    # a step is the activation preparation plus the chain launch, so the
+    # launch alone cannot take longer than the step blocks it alternates
+    # with; if it did, the legs ran in different clock or cache states and
+    # no fraction is reported
+    within = bool(kern_ms <= pair_ms and kern_ms <= step_ms)
     traffic = read_traffic() if wl == "c2" else None
     out = {
         "metric": METRIC,
@@ -447,34 +483,37 @@ def main():
         "dtype": "int16",
         "data": "synthetic (seeded ggml blocks as BASELINE.json specifies per format; x ~ N(0,1))",
         "config": {
-            "workload": f"{desc_txt}; {copies} weight sets cycled ({wbytes} B, "
+            "workload": f"{m['desc']}; {m['copies']} weight sets cycled ({wbytes} B, "
                         f"{wbytes / MALL_BYTES:.2f}x the 256 MiB Infinity Cache), one chain launch per step",
-            "descriptors_per_step": ndesc,
+            "descriptors_per_step": m["ndesc"],
             "weight_bytes_per_step": wbytes,
             "pct_hbm_peak": round(100.0 * value / PEAK_GBPS, 2),
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 2),
+            "achieved": round(achieved, 2) if within else None,
             "peak": PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(achieved / PEAK_GBPS, 4),
+            "frac": round(achieved / PEAK_GBPS, 4) if within else None,
             "traffic": traffic,
             "kernel": "chain_kernel",
             "kernel_ms": round(kern_ms, 5),
-            # a step is the activation preparation plus the chain launch, so
-            # the launch alone cannot take longer; if it did, the two timed
-            # legs ran in different clock or cache states and frac is not to
-            # be trusted
-            "kernel_within_step": bool(kern_ms <= step_ms),
+            "kernel_launches_timed": ROOF_LAUNCHES,
+            "kernel_blocks_ms": m["kern_blocks_ms"],
+            "paired_step_ms": round(pair_ms, 5),
+            "kernel_within_step": within,
         },
     }
     if not args.no_extra and wl == "c2":
         extra = {}
         for name in ("c1", "c3q4k", "c3q6k"):
-            _, wb, sm, km, nd, nc = measure(ctx, torch, dev, stream, name, max(10, args.steps // 2), args.warmup)
-            extra[name] = {"weight_bytes": wb, "descriptors": nd, "weight_sets": nc, "ms_per_launch": round(km, 5),
-                           "ms_per_step": round(sm, 5), "gbps": round(wb / (km * 1e-3) / 1e9, 2),
+            e = measure(ctx, torch, dev, stream, name, ROOF_LAUNCHES, args.warmup)
+            wb, km = e["wbytes"], e["kern_ms"]
+            extra[name] = {"weight_bytes": wb, "descriptors": e["ndesc"], "weight_sets": e["copies"],
+                           "ms_per_launch": round(km, 5), "launches_timed": ROOF_LAUNCHES,
+                           "ms_per_step": round(e["pair_step_ms"], 5),
+                           "kernel_within_step": bool(km <= e["pair_step_ms"]),
+                           "gbps": round(wb / (km * 1e-3) / 1e9, 2),
                            "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
         extra["c2_attn_q_single_launch_us"] = round(single_launch_us(ctx, torch, dev, stream, 50), 2)
         extra["c4_decode"] = decode_bench(ctx, torch, stream)
