@@ -151,6 +151,13 @@ int tmq_matmul(tmq_ctx* ctx, const tmq_tensor* t, const float* x, float* y, int 
 /* The branch `matmul` takes for a tensor type under flags (:474-492):
  * TMQ_PATH_* or a negative status for an unknown type. */
 int tmq_route(uint32_t type, uint32_t flags);
+/* Tiles and MACs one matmul adds to the reference's [FPGA TIMING SUMMARY]
+ * counters (fpga_sim::g_timing, sim/fpga_sim.hpp:148-174) under flags: the
+ * branch tmq_route picks, tiled as its matmul_fpga_* tiles (Q8_0 and INT16
+ * 64x64, Q5_0 8 rows, Q4_K 56x256, Q6_K 32x256; rows*cols MACs; the FP32
+ * loop 0 and 0).  Host only. */
+int tmq_matmul_tiles(uint32_t type, uint32_t flags, uint64_t rows, uint64_t cols, int64_t* tiles,
+                     int64_t* macs);
 /* `matmul` itself: routes by type and flags, host x/y, synchronous. */
 int tmq_matmul_flags(tmq_ctx* ctx, const tmq_tensor* t, uint32_t flags, const float* x, float* y,
                      int rows, int cols);

@@ -195,6 +195,8 @@ class Reference:
         _setup(L, "ref_model_step", None, [_P, _i, _i])
         _setup(L, "ref_model_step_dump", None, [_P, _i, _i, _P])
         _setup(L, "ref_apply_rope", None, [_P, _P, _i])
+        _setup(L, "ref_timing_reset", None, [])
+        _setup(L, "ref_timing_counts", None, [_P, _P])
 
     # ---- whole-model engine (sim/tmac_gguf.cpp:1894-2045), 896-wide only
     HIDDEN, VOCAB, LAYERS = 896, 151936, 24
@@ -246,6 +248,16 @@ class Reference:
         y = np.empty(rows, dtype=np.float32)
         self.lib.ref_matmul_int16(qtype, _ptr(w), w.size, rows, cols, _ptr(x), _ptr(y))
         return y
+
+    def timing_reset(self):
+        self.lib.ref_timing_reset()
+
+    def timing_counts(self):
+        """(tiles, MACs) of g_timing since the last reset"""
+        t = np.zeros(1, dtype=np.int64)
+        m = np.zeros(1, dtype=np.int64)
+        self.lib.ref_timing_counts(_ptr(t), _ptr(m))
+        return int(t[0]), int(m[0])
 
     def model_set_flags(self, flags: int):
         self.lib.ref_model_set_flags(int(flags))

@@ -182,6 +182,13 @@ void ref_model_step_dump(float* hidden, int token, int pos, float* dump) {
         memcpy(dump + (size_t)(l + 1) * HIDDEN_DIM, hidden, sizeof(float) * HIDDEN_DIM);
     }
 }
+// the counters of the [FPGA TIMING SUMMARY] (sim/fpga_sim.hpp:148-174):
+// tiles and MACs every matmul_fpga_* adds (sim/tmac_gguf.cpp:899, :934 ...)
+void ref_timing_reset(void) { fpga_sim::g_timing.reset(); }
+void ref_timing_counts(int64_t* tiles, int64_t* macs) {
+    *tiles = fpga_sim::g_timing.total_tiles;
+    *macs = fpga_sim::g_timing.total_mac_ops;
+}
 // apply_rope (sim/tmac_gguf.cpp:1527): q [14*64], k [2*64] rotated in place
 void ref_apply_rope(float* q, float* k, int pos) { apply_rope(q, k, pos); }
 

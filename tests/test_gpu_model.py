@@ -203,6 +203,63 @@ def test_cli(golden, tmp_path):
         assert np.array_equal(d.view(np.uint32), exp[l].view(np.uint32)), f"layer {l}"
 
 
+SUMMARY_RE = (r"\[FPGA TIMING SUMMARY\] \(GPU\)\n"
+              r"  Tiles: (\d+)\s+MACs: (\d+)\s+GPU: ([\d.]+) ms  NAIVE: ([\d.]+) Gop/s\n"
+              r"  GPU: (\d+) decode steps profiled, ([\d.]+) us of kernels per step \((\d+) tiles, (\d+) MACs\): "
+              r"([\d.]+) Gop/s, ([\d.]+) GB/s of weights")
+
+
+def test_cli_timing_summary(model, golden, tmp_path):
+    """Any --fpga* flag prints the reference's [FPGA TIMING SUMMARY]
+    (sim/fpga_sim.hpp:156-172, sim/tmac_gguf.cpp:2168-2171) with GPU figures:
+    the run's tiles and MACs equal what the compiled reference's counters
+    hold for the same run (tests/golden/timing.npz: per decode step and per
+    logits call), NAIVE Gop/s is MACs over the run's wall time, and the
+    profiled kernel time per step agrees with tmq_model_profile on the same
+    model (the test's own profile of 4 steps); no flag, no summary."""
+    import re
+    import subprocess
+    from conftest import PKG
+    from tmq import model_synth, tmacfile
+    gt = load_golden("timing.npz")
+    exe = os.path.join(PKG, "tmq", "tmq_gguf")
+    path = tmp_path / "c4.tmac"
+    tmacfile.write(path, model_synth.gen_model(int(golden["model_seed"])))
+    prompt = f"{int(golden['prompt'][0])}\n"
+    runs = [("all", ["--fpga-q8", "--fpga-q5-0", "--fpga-q4k", "--fpga-q6-k"]), ("q8q5", ["--fpga-q8", "--fpga-q5-0"]),
+            ("int16", ["--fpga"])]
+    us_cli = []
+    for name, fl in runs:
+        print(f"[model] CLI --generate 6 {' '.join(fl)}", flush=True)
+        r = subprocess.run([exe, str(path), "--generate", "6"] + fl, input=prompt, capture_output=True, text=True,
+                           timeout=300)
+        assert r.returncode == 0, r.stderr
+        m = re.search(SUMMARY_RE, r.stderr)
+        assert m, r.stderr[-2000:]
+        tiles, macs, wall, naive, steps, us, st, sm, gops, gbps = m.groups()
+        step, lg = gt[f"{name}_step"], gt[f"{name}_logits"]
+        # one prompt position and 6 generated ones (each fed), 6 logits calls
+        assert int(tiles) == 7 * int(step[0]) + 6 * int(lg[0]), name
+        assert int(macs) == 7 * int(step[1]) + 6 * int(lg[1]), name
+        assert int(st) == int(step[0] + lg[0]) and int(sm) == int(step[1] + lg[1]), name
+        assert abs(float(naive) - int(macs) / (float(wall) * 1e-3) / 1e9) <= 0.01 * float(naive) + 0.01
+        assert int(steps) == 4
+        assert abs(float(gops) - int(sm) / (float(us) * 1e-6) / 1e9) <= 0.01 * float(gops) + 0.01
+        assert abs(float(gbps) - model.weight_bytes / (float(us) * 1e-6) / 1e9) <= 0.01 * float(gbps) + 0.1
+        if name == "all":
+            us_cli.append(float(us))
+    model.set_flags(31)
+    model.set_graphs(True)
+    model.prompt(golden["prompt"])
+    prof = model.profile(4)
+    us_prof = 1e3 * sum(e - s for _, s, e in prof) / 4
+    print(f"[model] kernel time per step: CLI {us_cli[0]:.1f} us, tmq_model_profile {us_prof:.1f} us", flush=True)
+    assert 0.7 * us_prof <= us_cli[0] <= 1.4 * us_prof
+    r = subprocess.run([exe, str(path), "--generate", "2"], input=prompt, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert "TIMING SUMMARY" not in r.stderr
+
+
 def test_cli_cosim(golden, tmp_path):
     """tmq_gguf --fpga-phaseb --dump-phaseb --dump-tiles 4 --dump-tiles-q5-0 3
     --dump-tiles-q6-k 3 on a one-token prompt against the compiled

@@ -132,3 +132,26 @@ def test_golden_prompt_fixture():
     for i, v in zip(g["top_ids"][0], g["top_vals"][0]):
         if i % 64 == 0:
             assert g["logits_sub"][i // 64] == v
+
+
+def test_timing_counts_match_reference():
+    """tmq_matmul_tiles (host only) counts the tiles and MACs the reference's
+    matmul_fpga_* add to its [FPGA TIMING SUMMARY] (sim/fpga_sim.hpp:148-174):
+    summed over the synthetic C4 model's matmuls of one decode step and one
+    logits call, under every flag set of tests/golden/timing.npz (written by
+    the compiled reference, tests/golden/gen_timing_golden.py)."""
+    import tmq
+    from tmq import model_synth
+    g = load_golden("timing.npz")
+    spec = model_synth.matmul_shapes()
+    for key in g.files:
+        if not key.endswith("_flags"):
+            continue
+        name, flags = key[:-6], int(g[key])
+        step = np.zeros(2, dtype=np.int64)
+        for qt, rows, cols in spec["layers"]:
+            step += tmq.matmul_tiles(qt, flags, rows, cols)
+        qt, rows, cols = spec["logits"]
+        lg = np.array(tmq.matmul_tiles(qt, flags, rows, cols), dtype=np.int64)
+        assert step.tolist() == g[f"{name}_step"].tolist(), name
+        assert lg.tolist() == g[f"{name}_logits"].tolist(), name

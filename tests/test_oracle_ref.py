@@ -105,3 +105,4 @@ def test_oracle_vs_reference_tiles(oracle, reference):
             oracle.tile_kquant(qt, blocks, 40, act256, nc, ri896, a, 870)  # crosses row 896
             reference.tile_kquant(qt, blocks, 40, act256, nc, ri896, b, 870)
             assert np.array_equal(a, b)
+

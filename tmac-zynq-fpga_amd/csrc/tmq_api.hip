@@ -129,8 +129,24 @@ int groups_of(const TmqTensorDev& t) {
     return g64;
 }
 
-// Allocate planes + normalisers for a rows x cols tensor (zero filled).
-int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_tensor** out) {
+// Whether a tensor gets the MFMA decoders' planes (integer fit codes, and
+// for Q6_K the packed code plane): Q5_0 / Q4_K / Q6_K with the row_inv
+// computed at upload, at most TMQ_MFMA_MAX_COLS columns and a weight plane
+// under 2 GiB (the decoders address the planes with 32-bit buffer offsets),
+// unless TMQ_NOMFMA=1 (testing) or the caller does not use them.
+bool mfma_eligible(uint32_t type, uint64_t rows, uint64_t cols, bool ext_row_inv, bool want) {
+    if (!want || ext_row_inv || !tmq_ifit_codes((int)type) || cols > TMQ_MFMA_MAX_COLS) return false;
+    const char* nm = getenv("TMQ_NOMFMA");
+    if (nm && atoi(nm) != 0) return false;
+    const uint64_t nb = cols / (type == TMQ_TYPE_Q5_0 ? 32 : 256);
+    const uint64_t plane = (rows + 63) / 64 * 64 * nb *
+                           (type == TMQ_TYPE_Q5_0 ? 16 : type == TMQ_TYPE_Q6_K ? 208 : 128);
+    return plane < (1ull << 31);
+}
+
+// Allocate planes + normalisers for a rows x cols tensor (zero filled); the
+// MFMA decoders' planes only when `mfma` (mfma_eligible).
+int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, bool mfma, tmq_tensor** out) {
     const int qk = qk_of(type);
     if (!qk) return tmq_fail(TMQ_ERR_ARG, "unsupported tensor type %u", type);
     if (rows == 0 || cols == 0 || cols % qk)
@@ -150,14 +166,14 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
     d.rows_pad = (int)((rows + 63) / 64 * 64);
     d.nb = (int)(cols / qk);
     const size_t R = d.rows_pad, nb = d.nb;
-    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0, si = nb * R * tmq_ifit_codes((int)type), sq = 0;
+    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0, si = mfma ? nb * R * tmq_ifit_codes((int)type) : 0, sq = 0;
     switch (type) {
     case TMQ_TYPE_Q8_0: sa = nb * 2 * R * 16; sd = nb * R * 2; break;
     case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; se = nb * R; break;
     case TMQ_TYPE_Q4_K: sa = nb * 8 * R * 16; sb = nb * R * 16; se = nb * R * 8; break;
     case TMQ_TYPE_Q6_K:
         sa = nb * 8 * R * 16; sb = nb * 4 * R * 16; sc = nb * R * 16; sd = nb * R * 2; se = nb * R * 16;
-        sq = nb * 12 * R * 16 + nb * 4 * R * 4;
+        sq = mfma ? nb * 12 * R * 16 + nb * 4 * R * 4 : 0;
         break;
     case TMQ_TYPE_F32: sa = nb * 8 * R * 16; break;
     case TMQ_TYPE_F16: sa = nb * 4 * R * 16; break;
@@ -193,17 +209,12 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, tmq_
 // Integer fit codes and corrections of the MFMA decoders (t->dev.pi):
 // codes and per-(row, block, fitted unit) correction counts on the device,
 // the offsets of the corrections (rows in order, so each 64-row group's are
-// contiguous) on the host, then the corrections themselves.  Tensors with
-// more than TMQ_MFMA_MAX_COLS columns or a weight plane of 2 GiB or more (the
-// decoders address the planes with 32-bit buffer offsets), tensors with an
-// external row_inv (clamped), and any uploaded under TMQ_NOMFMA=1 (testing)
-// stay on the fitted-float decoders.
+// contiguous) on the host, then the corrections themselves.  A tensor
+// allocated without the plane (mfma_eligible) stays on the fitted-float
+// decoders.
 int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
     TmqTensorDev& d = t->dev;
-    const char* nm = getenv("TMQ_NOMFMA");
-    const uint64_t plane = (uint64_t)d.rows_pad * (uint64_t)d.nb *
-                           (d.type == TMQ_TYPE_Q5_0 ? 16 : d.type == TMQ_TYPE_Q6_K ? 208 : 128);
-    if (!d.pi || d.clamp || (nm && atoi(nm) != 0) || d.cols > TMQ_MFMA_MAX_COLS || plane >= (1ull << 31)) {
+    if (!d.pi || d.clamp) {
         d.pi = nullptr;
         return 0;
     }
@@ -261,12 +272,12 @@ int ifit_build(tmq_ctx* ctx, tmq_tensor* t) {
 // normalisers are computed on the device.
 int tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
                   bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
-                  const float* ext_row_inv, tmq_tensor** out) {
+                  const float* ext_row_inv, tmq_tensor** out, bool want_mfma = true) {
     if (!ctx || !data || !out) return tmq_fail(TMQ_ERR_ARG, "null argument");
     int rc = tmq_rt_set_device(ctx);
     if (rc) return rc;
     tmq_tensor* t = nullptr;
-    rc = tensor_alloc(ctx, type, rows, cols, &t);
+    rc = tensor_alloc(ctx, type, rows, cols, mfma_eligible(type, rows, cols, ext_row_inv != nullptr, want_mfma), &t);
     if (rc) return rc;
     if (n_bytes != t->weight_bytes) {
         tmq_tensor_free(t);
@@ -499,9 +510,9 @@ int tmq_rt_prepare_int16(tmq_ctx* ctx, tmq_tensor* t) {
 
 int tmq_rt_tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
                          bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
-                         tmq_tensor** out) {
+                         tmq_tensor** out, bool mfma) {
     return tensor_create(ctx, type, rows, cols, data, data_on_device, n_bytes, aux, aux_on_device,
-                         nullptr, out);
+                         nullptr, out, mfma);
 }
 
 TmqWork tmq_rt_make_work(const tmq_tensor* t, const uint8_t* act, float* y, int64_t* acc) {
@@ -737,6 +748,28 @@ int tmq_route(uint32_t type, uint32_t flags) {
                      (type == TMQ_TYPE_Q4_K && (flags & TMQ_FLAG_Q4_K)) ||
                      (type == TMQ_TYPE_Q8_0 && (flags & TMQ_FLAG_Q8_0));
     return own ? TMQ_PATH_FPGA : TMQ_PATH_INT16;
+}
+
+// Tiles of one matmul in the reference's tilings, as its matmul_fpga_*
+// count them into g_timing.total_tiles: 64x64 for Q8_0 and INT16
+// (sim/tmac_gguf.cpp:901-934, :965-1078), 8-row x 896 Q5_0 tiles
+// (:1267-1300), 56-row x 256-column Q4_K tiles (:1154-1188) and 32-row x
+// 256-column Q6_K tiles (:1442-1497); rows*cols MACs (:899, :963, :1109,
+// :1233, :1379).  The FP32 loop counts nothing.
+int tmq_matmul_tiles(uint32_t type, uint32_t flags, uint64_t rows, uint64_t cols, int64_t* tiles, int64_t* macs) {
+    if (!tiles || !macs) return tmq_fail(TMQ_ERR_ARG, "null argument");
+    const int path = tmq_route(type, flags);
+    if (path < 0) return path;
+    auto cdiv = [](uint64_t a, uint64_t b) { return (int64_t)((a + b - 1) / b); };
+    *tiles = 0;
+    *macs = 0;
+    if (path == TMQ_PATH_FP32) return TMQ_OK;
+    *macs = (int64_t)(rows * cols);
+    if (path == TMQ_PATH_INT16 || type == TMQ_TYPE_Q8_0) *tiles = cdiv(rows, 64) * cdiv(cols, 64);
+    else if (type == TMQ_TYPE_Q5_0) *tiles = cdiv(rows, 8);
+    else if (type == TMQ_TYPE_Q4_K) *tiles = cdiv(rows, 56) * cdiv(cols, 256);
+    else *tiles = cdiv(rows, 32) * cdiv(cols, 256);
+    return TMQ_OK;
 }
 
 int tmq_tensor_prepare_int16(tmq_ctx* ctx, tmq_tensor* t) {

@@ -30,7 +30,9 @@
 // profiles up to 8 more decode steps launch by launch on the GPU and prints
 // the reference's pipeline timing breakdown (:79-134) per operation, and
 // writes the launches as a Chrome trace (:55-76) to --trace PATH (default
-// /tmp/pipeline_trace.json, the reference's path).
+// /tmp/pipeline_trace.json, the reference's path).  Any --fpga* flag prints
+// the reference's [FPGA TIMING SUMMARY] with GPU figures to stderr at the end
+// (timing_summary).
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
@@ -102,6 +104,69 @@ void perf_report(const std::vector<tmq_launch_time>& lt, int steps, const char* 
     fprintf(f, "]}\n");
     fclose(f);
     fprintf(stderr, "[TRACE] Wrote Chrome trace: %s\n", trace_path);
+}
+
+// Tiles and MACs of one decode step's matmuls (the seven projections of
+// every layer) and of one logits call under flags, counted as the reference's
+// matmul_fpga_* count them (tmq_matmul_tiles).
+struct StepCounts {
+    int64_t step_tiles = 0, step_macs = 0, logit_tiles = 0, logit_macs = 0;
+};
+bool step_counts(const tmq_model* m, const tmq_model_config& cfg, uint32_t flags, StepCounts* out) {
+    static const char* proj[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+    auto add = [&](const char* name, int64_t* tiles, int64_t* macs) {
+        const tmq_tensor* t = tmq_model_tensor(m, name);
+        uint32_t type = 0;
+        uint64_t rows = 0, cols = 0, bytes = 0;
+        int64_t tl = 0, mc = 0;
+        if (!t || tmq_tensor_info(t, &type, &rows, &cols, &bytes) != TMQ_OK ||
+            tmq_matmul_tiles(type, flags, rows, cols, &tl, &mc) != TMQ_OK)
+            return false;
+        *tiles += tl;
+        *macs += mc;
+        return true;
+    };
+    for (int l = 0; l < cfg.n_layers; l++)
+        for (const char* p : proj) {
+            char name[64];
+            snprintf(name, sizeof(name), "blk.%d.%s.weight", l, p);
+            if (!add(name, &out->step_tiles, &out->step_macs)) return false;
+        }
+    return add("token_embd.weight", &out->logit_tiles, &out->logit_macs);
+}
+
+// The reference's [FPGA TIMING SUMMARY] (sim/fpga_sim.hpp:156-172, printed
+// when g_use_fpga is set, sim/tmac_gguf.cpp:2168-2171) for the GPU: the
+// run's tiles and MACs in the reference's tilings, the wall time of its
+// prompt and decode calls and MACs over that time ("NAIVE", as the
+// reference divides by the host time of its matmul calls); then `steps`
+// more decode steps profiled launch by launch (tmq_model_profile): kernel
+// time per step, its MACs over that time and its weight bytes over that
+// time.  To stderr, which carries the engine's other reports.
+int timing_summary(tmq_model* m, const tmq_model_config& cfg, uint32_t flags, int64_t positions,
+                   int64_t logit_calls, double wall_ms) {
+    StepCounts c;
+    if (!step_counts(m, cfg, flags, &c)) return die("timing summary");
+    const int64_t tiles = c.step_tiles * positions + c.logit_tiles * logit_calls;
+    const int64_t macs = c.step_macs * positions + c.logit_macs * logit_calls;
+    if (tiles == 0) return 0;  // as the reference: nothing ran on the accelerator
+    fprintf(stderr, "\n[FPGA TIMING SUMMARY] (GPU)\n");
+    fprintf(stderr, "  Tiles: %-8lld  MACs: %-10lld  GPU: %.2f ms  NAIVE: %.2f Gop/s\n", (long long)tiles,
+            (long long)macs, wall_ms, wall_ms > 0 ? macs / (wall_ms / 1000.0) / 1e9 : 0.0);
+    const int steps = std::min(4, cfg.max_seq - 1 - tmq_model_position(m));
+    if (steps <= 0) return 0;
+    std::vector<tmq_launch_time> lt((size_t)steps * (3 + 6 * (size_t)cfg.n_layers));
+    int n = 0;
+    if (tmq_model_profile(m, steps, lt.data(), (int)lt.size(), &n) != TMQ_OK) return die("profile");
+    double kern_ms = 0.0;
+    for (int i = 0; i < n; i++) kern_ms += lt[i].end_ms - lt[i].start_ms;
+    const double us = 1e3 * kern_ms / steps;
+    const int64_t st = c.step_tiles + c.logit_tiles, sm = c.step_macs + c.logit_macs;
+    fprintf(stderr, "  GPU: %d decode steps profiled, %.2f us of kernels per step (%lld tiles, %lld MACs): "
+                    "%.2f Gop/s, %.1f GB/s of weights\n",
+            steps, us, (long long)st, (long long)sm, sm / (us * 1e-6) / 1e9,
+            tmq_model_weight_bytes(m) / (us * 1e-6) / 1e9);
+    return 0;
 }
 
 }  // namespace
@@ -278,6 +343,7 @@ int main(int argc, char** argv) {
         printf("]\n");
     }
     fflush(stdout);
+    const int run_positions = tmq_model_position(m);  // before --perf advances it
     if (perf) {
         fprintf(stderr, "[PERF] load %.1f ms (%.1f MB of weights, %d layers)\n", t1 - t0,
                 tmq_model_weight_bytes(m) / 1e6, cfg.n_layers);
@@ -297,6 +363,10 @@ int main(int argc, char** argv) {
             lt.resize(n);
             perf_report(lt, steps, trace_path);
         }
+    }
+    int64_t logit_calls = generate_n > 0 ? generate_n : 1;
+    if (flags & TMQ_FLAG_FPGA) {
+        if (timing_summary(m, cfg, flags, run_positions, logit_calls, t3 - t1)) return 1;
     }
     int rc = 0;
     if (rec && phaseb) {

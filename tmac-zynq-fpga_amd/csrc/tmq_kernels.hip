@@ -1297,12 +1297,12 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
 //   Q4_K stage: qs chunks 2q, 2q+1 (1024 B each), header (1024 B), the two
 //               fit codes (256 B);
 //   Q6_K stage: the quarter's three chunks of the packed code plane
-//               (q6_pack_kernel), scales (1024 B each), d (256 B), the four
-//               fit codes (256 B).
+//               (q6_pack_kernel, 1024 B each), the quarter's four sub-block
+//               scales (256 B), d (256 B), the four fit codes (256 B).
 // The activation's operand bytes, 32- and 16-element sums are copied into
 // LDS once per workgroup.
 constexpr int kKqWaves = 4;
-template <int FMT> __host__ __device__ constexpr int kq_stage() { return FMT == kQ4_K ? 3328 : 4608; }
+template <int FMT> __host__ __device__ constexpr int kq_stage() { return FMT == kQ4_K ? 3328 : 3840; }
 template <int FMT> __host__ __device__ constexpr int kq_ndma() { return FMT == kQ4_K ? 4 : 6; }
 template <int FMT> __host__ __device__ constexpr int kq_xa_off() { return kKqWaves * TMQ_MFMA_DEPTH * kq_stage<FMT>(); }
 template <int FMT> __host__ __device__ constexpr int kq_xs_off(int nbx) {
@@ -1390,8 +1390,8 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
                                                          ((b * 12 + 3 * q + k) * R + g64) * 16, 0, TMQ_CPOL_NT);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsq, (lds_u8*)(st + 3072), 4, lane * 4,
                                                      (int)(192 * pb) + ((b * 4 + q) * R + g64) * 4, 0, TMQ_CPOL_NT);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsd, (lds_u8*)(st + 4096), 2, lane * 2, (b * R + g64) * 2, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 4352), 4, lane * 4, ((b * 4 + q) * R + g64) * 4,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsd, (lds_u8*)(st + 3328), 2, lane * 2, (b * R + g64) * 2, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 3584), 4, lane * 4, ((b * 4 + q) * R + g64) * 4,
                                                      0, TMQ_CPOL_NT);
         }
     };
@@ -1494,8 +1494,8 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
             const tmq_v4i va = *(lv4i*)(st + lane * 16), vb = *(lv4i*)(st + 1024 + lane * 16);
             const tmq_v4i vh = *(lv4i*)(st + 2048 + lane * 16);
             const uint32_t scq = *(lu32c*)(st + 3072 + lane * 4);
-            const uint32_t dbits = *(lu16*)(st + 4096 + lane * 4);
-            const uint32_t codes = *(lu32c*)(st + 4352 + lane * 4);
+            const uint32_t dbits = *(lu16*)(st + 3328 + lane * 4);
+            const uint32_t codes = *(lu32c*)(st + 3584 + lane * 4);
 #pragma unroll
             for (int k = 0; k < NS; k++) {
                 const int xb = 8 * b + 4 * h + k;

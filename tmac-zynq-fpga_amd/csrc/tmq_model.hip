@@ -864,8 +864,9 @@ int build_launches(tmq_model* m) {
         Y.dn.P.act.max_bits = m->max_bits + TMQ_MAX_SLOTS * l;
         // fused gate/up: one slot per workgroup; silu_kernel: one atomic slot
         Y.dn.P.act.max_n = Y.fused_gu ? Y.gu.P.w[0].ngroups : 1;
-        if (Y.dn.P.act.max_n > 64 * Y.dn.waves) return tmq_fail(TMQ_ERR_ARG, "more max slots than down threads");
         Y.dn.waves = all_fpga({Y.down}) ? nw_dn : 4;
+        if (Y.dn.P.act.max_n > 64 * Y.dn.waves || Y.dn.P.act.max_n > TMQ_MAX_SLOTS)
+            return tmq_fail(TMQ_ERR_ARG, "more max slots than down threads");
         add_work(Y.dn, Y.down, ad, xs + 3, kc_dn);
     }
     // logits: the residual stream (hid[0] + the last down projection),
@@ -968,7 +969,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
             if (a && a->type == 0 && a->cols == 1 && a->rows == rows && a->n_bytes == rows * 4)
                 aux = (const float*)a->data;
         }
-        int rc = tmq_rt_tensor_create(ctx, e->type, rows, cols, e->data, false, e->n_bytes, aux, false, out);
+        int rc = tmq_rt_tensor_create(ctx, e->type, rows, cols, e->data, false, e->n_bytes, aux, false, out, false);
         if (rc) return tmq_fail(rc, "%s: %s", n.c_str(), tmq_last_error());
         m->owned.push_back(*out);
         m->weight_bytes += e->n_bytes;
@@ -1007,7 +1008,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
                 memcpy(buf.data() + (size_t)(64 * q + 32) * rb, eu->data + (size_t)(32 * q) * rb, 32 * rb);
             }
             rc = tmq_rt_tensor_create(ctx, eg->type, 2 * (uint64_t)I, H, buf.data(), false, buf.size(), nullptr, false,
-                                      &Y.gu_t);
+                                      &Y.gu_t, false);
             if (rc) return tmq_fail(rc, "%sffn_gate/up: %s", p.c_str(), tmq_last_error());
             m->owned.push_back(Y.gu_t);
         }

@@ -65,10 +65,12 @@ int tmq_rt_set_device(tmq_ctx* ctx);
 // 64-row groups of a tensor (Q8_0: 256-row groups, one per workgroup)
 int tmq_rt_groups_of(const TmqTensorDev& t);
 // upload ggml bytes (host or device) into a new tensor; normalisers computed
-// on the device (aux = Q8_0 row_max_abs, optional)
+// on the device (aux = Q8_0 row_max_abs, optional); mfma: also build the
+// planes of the standalone / chain GEMVs' MFMA decoders where the tensor
+// qualifies (the decode engine's and prefill's kernels do not read them)
 int tmq_rt_tensor_create(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* data,
                          bool data_on_device, uint64_t n_bytes, const float* aux, bool aux_on_device,
-                         tmq_tensor** out);
+                         tmq_tensor** out, bool mfma);
 TmqWork tmq_rt_make_work(const tmq_tensor* t, const uint8_t* act, float* y, int64_t* acc);
 // builds the INT16 path planes of t once (matmul_fpga_int16's weights)
 int tmq_rt_prepare_int16(tmq_ctx* ctx, tmq_tensor* t);

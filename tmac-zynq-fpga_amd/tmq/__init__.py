@@ -47,7 +47,7 @@ EXPORTS = [
     "tmq_model_generate_async", "tmq_model_tokens", "tmq_model_hidden", "tmq_model_set_prefill",
     "tmq_model_profile", "tmq_model_set_flags", "tmq_model_get_flags", "tmq_quantize_act",
     "tmq_tensor_q8_scales", "tmq_model_feed_capture", "tmq_model_tensor", "tmq_model_logits_capture",
-    "tmq_model_reset",
+    "tmq_model_reset", "tmq_matmul_tiles",
 ]
 
 
@@ -59,6 +59,13 @@ class LaunchTime(C.Structure):
 def route(qtype: int, flags: int) -> int:
     """the matmul branch (PATH_*) the reference takes for a type under flags"""
     return _check(lib().tmq_route(qtype, flags))
+
+
+def matmul_tiles(qtype: int, flags: int, rows: int, cols: int):
+    """(tiles, MACs) one matmul adds to the reference's timing summary"""
+    t, m = C.c_int64(0), C.c_int64(0)
+    _check(lib().tmq_matmul_tiles(qtype, flags, rows, cols, C.byref(t), C.byref(m)))
+    return t.value, m.value
 
 
 class TmqError(RuntimeError):
@@ -113,6 +120,7 @@ def lib(path: str = LIB_PATH):
         "tmq_gemv_dev_noalloc": (I, [P, P, P, P, P]),
         "tmq_gemv_partials": (I, [P, P, P, P, U64, P]),
         "tmq_route": (I, [U32, U32]),
+        "tmq_matmul_tiles": (I, [U32, U32, U64, U64, P, P]),
         "tmq_matmul_flags": (I, [P, P, U32, P, P, I, I]),
         "tmq_matmul_path": (I, [P, P, I, P, P, I, I]),
         "tmq_gemv_dev_path": (I, [P, P, I, P, P, P]),

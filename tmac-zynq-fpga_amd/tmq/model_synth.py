@@ -76,6 +76,21 @@ def gen_model(seed: int = 2024, n_layers: int = 24, hidden: int = 896, inter: in
     return out
 
 
+def matmul_shapes(n_layers: int = 24, hidden: int = 896, inter: int = 4864, vocab: int = 151936,
+                  n_kv_heads: int = 2, q8_v_layers=QWEN_Q8_V_LAYERS) -> dict:
+    """(type, rows, cols) of every matmul of one decode step in gen_model's
+    map: "layers" lists each layer's q, k, v, output, gate, up, down;
+    "logits" is the tied Q8_0 token_embd."""
+    kv = n_kv_heads * 64
+    layers = []
+    for layer in range(n_layers):
+        big = layer in q8_v_layers
+        layers += [(Q5_0, hidden, hidden), (Q5_0, kv, hidden), (Q8_0 if big else Q5_0, kv, hidden),
+                   (Q5_0, hidden, hidden), (Q5_0, inter, hidden), (Q5_0, inter, hidden),
+                   (Q6_K if big else Q4_K, hidden, inter)]
+    return {"layers": layers, "logits": (Q8_0, vocab, hidden)}
+
+
 def weight_bytes(tensors: list[TmacTensor]) -> int:
     """ggml bytes streamed per decoded token: every quantised matrix once
     (token_embd as the logits matrix)."""
