@@ -166,7 +166,9 @@ int tensor_alloc(tmq_ctx* ctx, uint32_t type, uint64_t rows, uint64_t cols, bool
     d.rows_pad = (int)((rows + 63) / 64 * 64);
     d.nb = (int)(cols / qk);
     const size_t R = d.rows_pad, nb = d.nb;
-    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0, si = mfma ? nb * R * tmq_ifit_codes((int)type) : 0, sq = 0;
+    // integer fit codes: Q5_0 four blocks' codes a dword, [b/4][r] x 4 B
+    size_t sa = 0, sb = 0, sc = 0, sd = 0, se = 0, sq = 0,
+           si = !mfma ? 0 : type == TMQ_TYPE_Q5_0 ? (nb + 3) / 4 * R * 4 : nb * R * tmq_ifit_codes((int)type);
     switch (type) {
     case TMQ_TYPE_Q8_0: sa = nb * 2 * R * 16; sd = nb * R * 2; break;
     case TMQ_TYPE_Q5_0: sa = nb * R * 16; sb = nb * R * 4; sd = nb * R * 2; se = nb * R; break;

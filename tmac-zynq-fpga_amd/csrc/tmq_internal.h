@@ -11,7 +11,8 @@
 //   Q8_0  A: q    [b][2][r] x16B     D: d [b][r] u16
 //   Q5_0  A: D0-D3 [b][r]   x16B     B: D4  [b][r] u32     D: d [b][r] u16
 //         (the 32 5-bit codes repacked into five dwords, tmq_kernels.hip
-//         q5_codes; fit codes E: pe [b][r], integer fit codes pi [b][r])
+//         q5_codes; fit codes E: pe [b][r], integer fit codes pi [b/4][r]
+//         x 4 B, block b's code in byte b % 4)
 //   Q4_K  A: qs   [b][8][r] x16B     B: hdr (d,dmin,scales[12]) [b][r] x16B
 //   Q6_K  A: ql   [b][8][r] x16B     B: qh [b][4][r] x16B   C: sc [b][r] x16B
 //         D: d [b][r] u16
@@ -52,7 +53,7 @@ struct TmqTensorDev {
     const uint8_t* pc;
     const uint8_t* pd;
     const uint8_t* pe;       // fit codes (Q5_0: 1 B, Q4_K: 8 B, Q6_K: 16 B per block and row)
-    const uint8_t* pi;       // integer fit codes of the MFMA decoders: Q5_0 [b][r] 1 B; Q4_K [b][q][r] 2 B
+    const uint8_t* pi;       // integer fit codes of the MFMA decoders: Q5_0 [b/4][r] 4 B (block b in byte b%4); Q4_K [b][q][r] 2 B
                              // (sub-blocks 2q, 2q+1); Q6_K [b][q][r] 4 B (the quarter's four sub-blocks)
     const uint8_t* pq;       // Q6_K codes for the MFMA decoder: chunk 3q+k (k < 3) of block b, [b][12][r] 16 B,
                              // holds sub-block k of quarter q (a code in the low 6 bits of each byte) and, in

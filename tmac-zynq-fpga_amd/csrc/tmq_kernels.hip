@@ -1056,16 +1056,6 @@ __device__ __forceinline__ void q4k_nom(float dri, float mri, int sc, int m, flo
     bn = __builtin_fmaf(an, 8.0f, __builtin_fmaf(-mri, (float)m, 128.0f));
 }
 
-__device__ __forceinline__ Q5Blk q5i_load(const TmqTensorDev& t, int b, int r) {
-    const size_t o = (size_t)b * t.rows_pad + r;
-    Q5Blk k;
-    k.qs = ld16(t.pa + o * 16);
-    k.qh = ld4(t.pb + o * 4);
-    k.d = ld2(t.pd + o * 2);
-    k.e = ld1(t.pi + o);
-    return k;
-}
-
 // block pairs in flight per lane
 #ifndef TMQ_MFMA_DEPTH
 #define TMQ_MFMA_DEPTH 2
@@ -1078,12 +1068,13 @@ typedef __attribute__((address_space(3))) const uint16_t lu16;
 typedef __attribute__((address_space(3))) const uint8_t lu8;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-// Dynamic LDS of the MFMA decoders (mfma_lds_bytes): per wave a ring of
+// Dynamic LDS of the Q5_0 MFMA decoder (mfma_lds_bytes): per wave a ring of
 // TMQ_MFMA_DEPTH stages, each one block of the wave's 64 rows as the LDS DMA
 // lays it down (lane l at 16*l of the qs part, 4*l of the others): qs
-// 1024 B, qh' 256 B, d 256 B, fit code 256 B; then the activation's operand
-// bytes (XA with the zero and ones chunks), the block sums, the waves' row
-// sums and the 64 rows' corrections.
+// 1024 B, qh' 256 B, d 256 B, the fit-code dword (the block's code in byte
+// wave) 256 B; then the activation's operand bytes (XA with the zero and
+// ones chunks), the block sums, the waves' row sums and the 64 rows'
+// corrections.
 constexpr int kMfmaStage = 1792;
 constexpr int kMfmaWaves = gemv_waves(kQ5_0M);
 __host__ __device__ constexpr int mfma_xa_off() { return kMfmaWaves * TMQ_MFMA_DEPTH * kMfmaStage; }
@@ -1164,7 +1155,7 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     // forms an address (the host keeps every plane below 2^31 bytes).
     const uint32_t pl = (uint32_t)(R * (size_t)nb);  // elements per plane
     const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(t.pa, 16 * pl), rsb = buf_rsrc(t.pb, 4 * pl);
-    const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(t.pd, 2 * pl), rsi = buf_rsrc(t.pi, pl);
+    const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(t.pd, 2 * pl), rsi = buf_rsrc(t.pi, 4 * (uint32_t)R * ((nb + 3) / 4));
     const int la16 = lane * 16, la4 = lane * 4, la2 = lane * 2;
     auto issue = [&](int i, int slot) {
         const int blk = __builtin_amdgcn_readfirstlane(min(wave + NW * min(i, ilast), nb - 1));
@@ -1173,7 +1164,10 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)st, 16, la16, 16 * ob, 0, TMQ_CPOL_NT);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_u8*)(st + 1024), 4, la4, 4 * ob, 0, TMQ_CPOL_NT);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsd, (lds_u8*)(st + 1280), 2, la2, 2 * ob, 0, TMQ_CPOL_NT);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 1536), 1, lane, ob, 0, TMQ_CPOL_NT);
+        // the fit codes of blocks 4j .. 4j+3 of a row in one dword (plane
+        // [b/4][r]): the four waves read the same 256 B, each its own byte
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 1536), 4, la4, 4 * ((blk >> 2) * (int)R + g * 64),
+                                                 0, TMQ_CPOL_NT);
     };
 #pragma unroll
     for (int i = 0; i < D; i++) issue(i, i);
@@ -1214,7 +1208,7 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
         }
         k.qh = *(lu32c*)(st + 1024 + lane * 4);
         k.d = *(lu16*)(st + 1280 + lane * 4);
-        k.e = *(lu8*)(st + 1536 + lane * 4);
+        k.e = *(lu8*)(st + 1536 + lane * 4 + (b & 3));
         const uint32_t ao = abase + (uint32_t)b * astride;
         const tmq_v4i A0 = *(lv4i*)(xa + ao), A1 = *(lv4i*)(xa + ao + acoff);
         const int xsv = *(li32*)(xsl + b);
@@ -2864,7 +2858,7 @@ __global__ __launch_bounds__(256) void ifit_kernel(TmqTensorDev t, int pass, int
                                                    const int32_t* off, uint4* corr) {
     const int r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
     if (r >= t.rows_pad) return;
-    const size_t R = t.rows_pad, o = (size_t)b * R + r;
+    const size_t R = t.rows_pad;
     const float inv = t.row_inv[r], ri256 = inv * 256.0f;
     const Q5Blk k = q5_load(t, b, r);
     const float d = h2f(k.d);
@@ -2903,7 +2897,8 @@ __global__ __launch_bounds__(256) void ifit_kernel(TmqTensorDev t, int pass, int
     for (int i = 0; i < 32; i++)
         if (ifit_w(f, u[i]) != gv[i]) bad |= 1u << u[i];
     if (pass == 0) {
-        ((uint8_t*)t.pi)[o] = (uint8_t)best;
+        // blocks 4j .. 4j+3 of row r share a dword (plane [b/4][r] x 4 B)
+        ((uint8_t*)t.pi)[((size_t)(b >> 2) * R + r) * 4 + (b & 3)] = (uint8_t)best;
         cnt[(size_t)r * t.nb + b] = (uint8_t)__builtin_popcount(bad);
         return;
     }
