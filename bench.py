@@ -250,6 +250,32 @@ def measure(ctx, torch, dev, stream, name, steps, warmup, copies=None):
             "ndesc": len(descs), "copies": copies}
 
 
+def sets_scan(ctx, torch, dev, stream, name, lo, hi, step):
+    """Chain kernel time over lo, lo+step, ..., hi weight sets of `name`,
+    each chain over the first sets of one upload of hi sets; one JSON line
+    per point.  Shows how the time steps with the number of workgroups
+    per CU (the launch's last, partly filled round)."""
+    per = len(WORKLOADS[name][1])
+    desc_txt, x_d, tensors, descs, ys = build_workload(ctx, torch, dev, name, hi)
+    for k in range(lo, hi + 1, step):
+        chain = ctx.chain(descs[:k * per])
+        for _ in range(MIN_WARMUP):
+            chain.run()
+        ctx.sync()
+        kern = []
+        for _ in range(ROOF_BLOCKS):
+            time_primed(torch, stream, chain.run, ROOF_LAUNCHES // ROOF_BLOCKS)
+            kern.append(time_primed(torch, stream, chain.launch, ROOF_LAUNCHES // ROOF_BLOCKS))
+        ctx.sync()
+        km = float(np.mean(kern))
+        wb = chain.weight_bytes
+        print(json.dumps({"scan": name, "sets": k, "weight_bytes": wb, "kernel_ms": round(km, 5),
+                          "kernel_gbps": round(wb / (km * 1e-3) / 1e9, 1)}), flush=True)
+        chain.free()
+    for t in tensors:
+        t.free()
+
+
 def single_launch_us(ctx, torch, dev, stream, steps):
     """Latency of one attn_q GEMV launch (896x896 Q5_0), kernel only."""
     desc_txt, x_d, tensors, descs, ys = build_workload(ctx, torch, dev, "c2", copies=1)
@@ -383,6 +409,8 @@ def main():
     ap.add_argument("--sets", type=int, default=None, help="weight sets of the c2 chain (default: 2x the MALL)")
     ap.add_argument("--sets-sweep", action="store_true",
                     help="GEMV GB/s at working sets of 1x, 2x and 4x the Infinity Cache (c2, c3q4k, c3q6k, c1)")
+    ap.add_argument("--sets-scan", nargs=4, metavar=("WORKLOAD", "LO", "HI", "STEP"), default=None,
+                    help="kernel time of one GEMV chain over LO..HI weight sets (prefixes of one upload)")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + ["c4", "c5"],
                     help="c4: only the full-model greedy decode (BASELINE configs[3]); "
@@ -444,6 +472,10 @@ def main():
                             "kernel": "whole prefill (int8 digit MACs / prompt time)"},
                "extra": {"c5_prefill": pf}, "cpu_baseline": cpu}
         print(json.dumps(out), flush=True)
+        return
+    if args.sets_scan:
+        sets_scan(ctx, torch, dev, stream, args.sets_scan[0], *(int(v) for v in args.sets_scan[1:]))
+        ctx.close()
         return
     if args.sets_sweep:
         for name in ("c2", "c3q4k", "c3q6k", "c1"):
