@@ -284,6 +284,68 @@ def test_chain_tall_tensors(ctx, oracle, qt):
         t.free()
 
 
+@pytest.mark.parametrize("qt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("force", [False, True])
+def test_chain_split_tail(ctx, oracle, monkeypatch, qt, force):
+    """A K-quant chain segment of 20 ffn_down tensors (896x4864, 14 groups
+    each) and one 130x1024 tensor (3 groups): 283 groups leave a last round
+    of 27 on 256 CUs, which the chain splits into pieces over super-block
+    ranges (9 a group; 4 for the 4-super-block tensor) that meet through
+    tail slots.  Three runs in a row (each slot must be left clear for the
+    next): int64 row sums and fp32 outputs bit-exact with the oracle, the
+    same as the unsplit chain (TMQ_NOSPLIT=1); with every sub-block forced
+    onto corrections (TMQ_IFIT_FORCE=1) too, which only the first piece of a
+    group adds."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda:0")
+    if force:
+        monkeypatch.setenv("TMQ_IFIT_FORCE", "1")
+    shapes = [(896, 4864)] * 20 + [(130, 1024)]
+    xs = {c: synth.gen_x(c, 40 + c) for c in (1024, 4864)}
+    xd = {c: torch.from_numpy(v).to(dev) for c, v in xs.items()}
+    descs, ys, accs, ws, ts = [], [], [], [], []
+    tr = 56 if qt == Q4_K else 32
+    for i, (rows, cols) in enumerate(shapes):
+        w = synth.gen_weights(qt, rows, cols, 500 + 7 * i + qt)
+        t = ctx.upload(qt, rows, cols, w)
+        y = torch.zeros(rows, dtype=torch.float32, device=dev)
+        a = torch.zeros(rows, dtype=torch.int64, device=dev)
+        ncg = cols // 256
+        nt = ncg * (rows // tr) if rows % tr == 0 else None
+        if nt is None:  # 130 rows: tiles of 10 rows
+            nt, trr = ncg * 13, 10
+        else:
+            trr = tr
+        descs.append((t, xd[cols].data_ptr(), y.data_ptr(), a.data_ptr(), nt, trr, ncg))
+        ys.append(y)
+        accs.append(a)
+        ws.append(w)
+        ts.append(t)
+    exp = []
+    for (rows, cols), w in zip(shapes, ws):
+        x = xs[cols]
+        xq, _ = oracle.quantize_act(x)
+        exp.append((oracle.acc(qt, w, rows, cols, xq, oracle.row_inv(qt, w, rows, cols)),
+                    oracle.matmul(qt, w, x, rows, cols)))
+    for nosplit in (False, True):
+        monkeypatch.setenv("TMQ_NOSPLIT", "1" if nosplit else "0")
+        print(f"[chain] split tail, type {qt}, forced fit {force}, nosplit {nosplit}", flush=True)
+        ch = ctx.chain(descs)
+        for run in range(3):
+            for y, a in zip(ys, accs):
+                y.zero_()
+                a.zero_()
+            ch.run()
+            ctx.sync()
+            for i, (y, a, (ae, ye)) in enumerate(zip(ys, accs, exp)):
+                got = a.cpu().numpy()
+                assert np.array_equal(got, ae), report(f"acc of tensor {i}, run {run}", got, ae)
+                assert np.array_equal(bits(y.cpu().numpy()), bits(ye)), f"y of tensor {i}, run {run}"
+        ch.free()
+    for t in ts:
+        t.free()
+
+
 def test_error_paths(ctx):
     import tmq
     w = synth.gen_weights(Q5_0, 8, 896, 1)

@@ -112,6 +112,7 @@ struct tmq_chain {
     void* works_dev = nullptr;
     void* gmap_dev = nullptr;
     void* act_dev = nullptr;
+    uint64_t* tail_dev = nullptr;  // tail slots of split groups (zero between launches)
     std::vector<Segment> segs;
     uint64_t weight_bytes = 0;
 };
@@ -450,31 +451,71 @@ int run_int16(tmq_ctx* ctx, const tmq_tensor* t, const int16_t* xq, std::vector<
 // Descriptors of one format (and clamp mode) form a segment that runs as one
 // launch of that format's kernel; `works` is reordered by segment and
 // first_group made relative to the segment's first workgroup.
-void plan_segments(std::vector<TmqWork>& works, std::vector<int32_t>& gmap, std::vector<Segment>& segs) {
+//
+// A launch's workgroups run in rounds of one per CU, so a segment of W
+// whole-row groups takes ceil(W / ncu) group times even when its last round
+// holds a few.  With ncu > 0, a K-quant MFMA segment whose last round holds
+// T <= ncu / 2 groups splits each of those T groups into up to ncu / T
+// workgroups over disjoint super-block ranges (at least one each), so that
+// the last round takes a fraction of a group time; each split group gets a
+// tail slot (`nslots` of them) where its pieces add their row sums.
+void plan_segments(std::vector<TmqWork>& works, std::vector<TmqGroupRef>& gmap, std::vector<Segment>& segs,
+                   int ncu, int& nslots) {
     std::stable_sort(works.begin(), works.end(), [](const TmqWork& a, const TmqWork& b) {
         const int fa = tmq_kernel_fmt(a.t), fb = tmq_kernel_fmt(b.t);
         return fa != fb ? fa < fb : a.t.clamp < b.t.clamp;
     });
     gmap.clear();
     segs.clear();
+    nslots = 0;
+    auto close = [&]() {
+        if (segs.empty() || ncu <= 0) return;
+        Segment& sg = segs.back();
+        if (sg.type != TMQ_FMT_Q4_K_MFMA && sg.type != TMQ_FMT_Q6_K_MFMA) return;
+        const int tcount = sg.ngroups % ncu;
+        if (tcount == 0 || ncu / tcount < 2) return;
+        std::vector<TmqGroupRef> last(gmap.end() - tcount, gmap.end());
+        gmap.resize(gmap.size() - tcount);
+        for (const TmqGroupRef& e : last) {
+            const int nb = works[e.work].t.nb;
+            const int pieces = std::min(std::min(ncu / tcount, nb), 32767);
+            if (pieces < 2 || nslots >= 32767) {
+                gmap.push_back(e);
+                continue;
+            }
+            const int slot = nslots++;
+            for (int k = 0; k < pieces; k++) {
+                TmqGroupRef p = e;
+                p.b0 = (uint16_t)((int64_t)k * nb / pieces);
+                p.b1 = (uint16_t)((int64_t)(k + 1) * nb / pieces);
+                p.slot = (int16_t)slot;
+                p.pieces = (int16_t)pieces;
+                gmap.push_back(p);
+            }
+        }
+        sg.ngroups = (int)gmap.size() - sg.gmap_off;
+    };
     for (size_t i = 0; i < works.size(); i++) {
         TmqWork& w = works[i];
         const int fmt = tmq_kernel_fmt(w.t);
-        if (segs.empty() || segs.back().type != fmt || segs.back().clamp != w.t.clamp)
+        if (segs.empty() || segs.back().type != fmt || segs.back().clamp != w.t.clamp) {
+            close();
             segs.push_back(Segment{fmt, w.t.clamp, (int)gmap.size(), 0, 0});
+        }
         Segment& sg = segs.back();
         sg.max_cols = std::max(sg.max_cols, w.t.cols);
         w.first_group = sg.ngroups;
-        for (int g = 0; g < w.ngroups; g++) gmap.push_back((int32_t)i);
+        for (int g = 0; g < w.ngroups; g++) gmap.push_back(TmqGroupRef{(int32_t)i, g, 0, 0, 0, 1});
         sg.ngroups += w.ngroups;
     }
+    close();
 }
 
 int launch_segments(const std::vector<Segment>& segs, const void* works_dev, const void* gmap_dev,
-                    hipStream_t s) {
+                    uint64_t* tail, hipStream_t s) {
     for (const Segment& sg : segs) {
         int e = tmq_launch_chain(sg.type, sg.clamp, sg.max_cols, (const TmqWork*)works_dev,
-                                 (const int32_t*)gmap_dev + sg.gmap_off, sg.ngroups, s);
+                                 (const TmqGroupRef*)gmap_dev + sg.gmap_off, sg.ngroups, tail, s);
         if (e) return tmq_fail(TMQ_ERR_HIP, "chain segment launch: %s", hipGetErrorString((hipError_t)e));
     }
     return 0;
@@ -539,6 +580,7 @@ int tmq_open(int device, tmq_ctx** out) {
         return tmq_fail(TMQ_ERR_NODEV, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
     tmq_ctx* c = new tmq_ctx();
     c->device = device;
+    c->ncu = prop.multiProcessorCount;
     e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
@@ -1040,19 +1082,24 @@ int tmq_chain_create(tmq_ctx* ctx, const tmq_desc* descs, int n, tmq_chain** out
         j.n = ncols_of[kv.second];
     }
     // work list, one segment per format
-    std::vector<int32_t> gmap;
+    std::vector<TmqGroupRef> gmap;
     for (int i = 0; i < n; i++) {
         const tmq_desc& d = descs[i];
         ch->works.push_back(make_work(d.weight, (const uint8_t*)ch->act_dev + act_off[act_of[i]], d.y_dev, d.acc_dev));
         ch->weight_bytes += d.weight->weight_bytes;
     }
-    plan_segments(ch->works, gmap, ch->segs);
+    // TMQ_NOSPLIT=1 (testing): no split groups
+    const char* nsp = getenv("TMQ_NOSPLIT");
+    int nslots = 0;
+    plan_segments(ch->works, gmap, ch->segs, nsp && atoi(nsp) != 0 ? 0 : ctx->ncu, nslots);
     e = hipMalloc(&ch->works_dev, sizeof(TmqWork) * ch->works.size());
-    if (e == hipSuccess) e = hipMalloc(&ch->gmap_dev, sizeof(int32_t) * gmap.size());
+    if (e == hipSuccess) e = hipMalloc(&ch->gmap_dev, sizeof(TmqGroupRef) * gmap.size());
+    if (e == hipSuccess && nslots) e = hipMalloc(&ch->tail_dev, sizeof(uint64_t) * TMQ_TAIL_SLOT_WORDS * nslots);
+    if (e == hipSuccess && nslots) e = hipMemset(ch->tail_dev, 0, sizeof(uint64_t) * TMQ_TAIL_SLOT_WORDS * nslots);
     if (e == hipSuccess)
         e = hipMemcpy(ch->works_dev, ch->works.data(), sizeof(TmqWork) * ch->works.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess)
-        e = hipMemcpy(ch->gmap_dev, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice);
+        e = hipMemcpy(ch->gmap_dev, gmap.data(), sizeof(TmqGroupRef) * gmap.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         tmq_chain_free(ch);
         return tmq_fail(TMQ_ERR_NOMEM, "chain alloc: %s", hipGetErrorString(e));
@@ -1069,7 +1116,7 @@ int tmq_chain_prepare(tmq_ctx* ctx, tmq_chain* ch) {
 
 int tmq_chain_launch(tmq_ctx* ctx, tmq_chain* ch) {
     if (!ctx || !ch) return tmq_fail(TMQ_ERR_ARG, "null argument");
-    return launch_segments(ch->segs, ch->works_dev, ch->gmap_dev, ctx->stream);
+    return launch_segments(ch->segs, ch->works_dev, ch->gmap_dev, ch->tail_dev, ctx->stream);
 }
 
 int tmq_chain_run(tmq_ctx* ctx, tmq_chain* ch) {
@@ -1085,6 +1132,7 @@ int tmq_chain_free(tmq_chain* ch) {
     }
     if (ch->works_dev) (void)hipFree(ch->works_dev);
     if (ch->gmap_dev) (void)hipFree(ch->gmap_dev);
+    if (ch->tail_dev) (void)hipFree(ch->tail_dev);
     if (ch->act_dev) (void)hipFree(ch->act_dev);
     delete ch;
     return 0;
@@ -1132,7 +1180,7 @@ int pb_flush(tmq_ctx* ctx, std::vector<PbItem>& items, uint8_t* arena, uint32_t 
     if (!rc) rc = ctx->acc.ensure(sizeof(int64_t) * acc_total);
     if (rc) return rc;
     std::vector<TmqWork> works;
-    std::vector<int32_t> gmap;
+    std::vector<TmqGroupRef> gmap;
     std::vector<Segment> segs;
     size_t k = 0;
     for (PbItem& it : items)
@@ -1142,13 +1190,16 @@ int pb_flush(tmq_ctx* ctx, std::vector<PbItem>& items, uint8_t* arena, uint32_t 
             works.push_back(make_work(p.t, (const uint8_t*)ctx->act.p + aoff[k], nullptr, (int64_t*)ctx->acc.p + coff[k]));
             k++;
         }
-    plan_segments(works, gmap, segs);
+    // (no split groups: the arena's descriptors are one-off launches)
+    int nslots = 0;
+    plan_segments(works, gmap, segs, 0, nslots);
     rc = ctx->works.ensure(sizeof(TmqWork) * works.size());
-    if (!rc) rc = ctx->gmap.ensure(sizeof(int32_t) * gmap.size());
+    if (!rc) rc = ctx->gmap.ensure(sizeof(TmqGroupRef) * gmap.size());
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(ctx->works.p, works.data(), sizeof(TmqWork) * works.size(), hipMemcpyHostToDevice, ctx->stream));
-    HIP_TRY(hipMemcpyAsync(ctx->gmap.p, gmap.data(), sizeof(int32_t) * gmap.size(), hipMemcpyHostToDevice, ctx->stream));
-    rc = launch_segments(segs, ctx->works.p, ctx->gmap.p, ctx->stream);
+    HIP_TRY(hipMemcpyAsync(ctx->gmap.p, gmap.data(), sizeof(TmqGroupRef) * gmap.size(), hipMemcpyHostToDevice,
+                           ctx->stream));
+    rc = launch_segments(segs, ctx->works.p, ctx->gmap.p, nullptr, ctx->stream);
     if (rc) return rc;
     std::vector<int64_t> acc(acc_total);
     HIP_TRY(hipMemcpyAsync(acc.data(), ctx->acc.p, sizeof(int64_t) * acc_total, hipMemcpyDeviceToHost, ctx->stream));

@@ -256,10 +256,23 @@ static inline int tmq_ifit_subs(int type) { return type == 6 ? 1 : type == 12 ? 
 int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux_max_abs, float* row_inv,
                        float* row_scale, int* bad_flag, hipStream_t s);
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s);
+// One workgroup of a chain launch: row group `group` of works[work] over
+// super-blocks [b0, b1) (b1 = 0: the whole row).  A group split into
+// `pieces` > 1 workgroups (only the K-quant MFMA decoders split) adds its
+// int64 row sums into tail slot `slot`; the piece completing the slot's
+// count finalises the rows and clears the slot for the next launch.
+struct TmqGroupRef {
+    int32_t work, group;
+    uint16_t b0, b1;
+    int16_t slot, pieces;
+};
+// int64 words of a tail slot: 64 row sums, the piece count, padding to 640 B
+#define TMQ_TAIL_SLOT_WORDS 80
 // one launch per chain segment (descriptors of one kernel format
-// (tmq_kernel_fmt) and clamp mode, max_cols = the widest of them)
-int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const int32_t* group_work_dev,
-                     int total_groups, hipStream_t s);
+// (tmq_kernel_fmt) and clamp mode, max_cols = the widest of them); `tail`:
+// zeroed slots of the segment's split groups (null when none)
+int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const TmqGroupRef* groups_dev,
+                     int total_groups, uint64_t* tail, hipStream_t s);
 // dynamic LDS of a standalone / chain GEMV launch of a kernel format
 size_t tmq_gemv_lds_bytes(int fmt, int max_cols);
 // engine GEMV: activation recipe + works of any formats; waves = 16 or 4

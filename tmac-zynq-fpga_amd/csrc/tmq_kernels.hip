@@ -1310,8 +1310,12 @@ template <int FMT> __host__ __device__ constexpr int kq_lds_bytes(int nbx) {
     return kq_part_off<FMT>(nbx) + (kKqWaves + 1) * 64 * 8;
 }
 
+// Row group g over super-blocks [b0, b1) of its rows.  pieces > 1: one of
+// the workgroups sharing the group, which meet in tail slot `slot` (a
+// TmqGroupRef split; the first piece adds the corrections).
 template <int FMT>
-__device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
+__device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, int b1, int slot, int pieces,
+                                              uint64_t* tail) {
     extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
     constexpr int NW = kKqWaves, D = TMQ_MFMA_DEPTH, ST = kq_stage<FMT>(), ND = kq_ndma<FMT>();
     constexpr int NS = FMT == kQ4_K ? 2 : 4;  // sub-blocks per quarter
@@ -1319,9 +1323,13 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
     const int nb = t.nb, nbx = nb * 8, n = t.cols;
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
-    const int nu = 4 * nb;                      // quarters of a row
-    const int nuw = (nu - wave + NW - 1) / NW;  // this wave's quarters (wave-uniform, >= 1)
-    const int c0 = t.corr_off ? t.corr_off[g] : 0, c1 = t.corr_off ? t.corr_off[g + 1] : 0;
+    // quarter u = 4b + q of the row; wave w takes quarters u0 + w + NW*i:
+    // quarter w of each super-block of the range (NW = 4 = quarters per
+    // super-block), b1 - b0 >= 1 of them
+    const int u0 = 4 * b0;
+    const int nuw = b1 - b0;
+    const bool corr = t.corr_off && b0 == 0;
+    const int c0 = corr ? t.corr_off[g] : 0, c1 = corr ? t.corr_off[g + 1] : 0;
     const float inv = t.row_inv[r], ri256 = inv * 256.0f;
     uint8_t* xa = mfma_lds + kq_xa_off<FMT>();
     int32_t* xsl = (int32_t*)(mfma_lds + kq_xs_off<FMT>(nbx));
@@ -1330,23 +1338,29 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
     int64_t* fix = part + NW * 64;
 
     // the activation copy first (global -> LDS), so that waiting for it does
-    // not wait for the ring's stages
+    // not wait for the ring's stages: the range's 16-byte chunks (32 a
+    // super-block) and block sums, at their offsets in the whole row, and
+    // the two chunks of zeros and ones behind the row
     {
         const uint8_t* src = w.act + tmq_act_xa(n);
-        const int n16 = nbx * 4 + 2;
-        for (int i0 = wave * 64; i0 < n16; i0 += NW * 64)
-            if (i0 + lane < n16)
+        const int a0 = 32 * b0, a1 = 32 * b1;
+        for (int i0 = a0 + wave * 64; i0 < a1; i0 += NW * 64)
+            if (i0 + lane < a1)
                 __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
                                                  16, 0, 0);
+        if (wave == NW - 1 && lane < 2)
+            __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(nbx * 4 + lane) * 16),
+                                             (lds_u8*)(xa + nbx * 64), 16, 0, 0);
         const uint8_t* xs = w.act + tmq_act_xs(n);
-        for (int i0 = wave * 64; i0 < nbx; i0 += NW * 64)
-            if (i0 + lane < nbx)
+        const int s0 = 8 * b0, s1 = 8 * b1;
+        for (int i0 = s0 + wave * 64; i0 < s1; i0 += NW * 64)
+            if (i0 + lane < s1)
                 __builtin_amdgcn_global_load_lds((const void*)(xs + (size_t)(i0 + lane) * 4),
                                                  (lds_u8*)((uint8_t*)xsl + i0 * 4), 4, 0, 0);
         if constexpr (FMT == kQ6_K) {
             const uint8_t* x16 = w.act + tmq_act_xs16(n);
-            for (int i0 = wave * 64; i0 < 2 * nbx; i0 += NW * 64)
-                if (i0 + lane < 2 * nbx)
+            for (int i0 = 2 * s0 + wave * 64; i0 < 2 * s1; i0 += NW * 64)
+                if (i0 + lane < 2 * s1)
                     __builtin_amdgcn_global_load_lds((const void*)(x16 + (size_t)(i0 + lane) * 4),
                                                      (lds_u8*)((uint8_t*)xs16l + i0 * 4), 4, 0, 0);
         }
@@ -1365,7 +1379,7 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
     // stage `slot` <- the wave's quarter i (clamped: refills past the end
     // reload the last quarter, so every step waits for the same count)
     auto issue = [&](int i, int slot) {
-        const int u = __builtin_amdgcn_readfirstlane(wave + NW * min(i, ilast));
+        const int u = __builtin_amdgcn_readfirstlane(u0 + wave + NW * min(i, ilast));
         const int b = u >> 2, q = u & 3;
         uint8_t* st = ring + slot * ST;
         if constexpr (FMT == kQ4_K) {
@@ -1439,7 +1453,7 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
     auto step = [&](int i, int slot) {
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<ND * (D - 1)>();
-        const int u = wave + NW * i, b = u >> 2, q = u & 3;
+        const int u = u0 + wave + NW * i, b = u >> 2, q = u & 3;
         const uint8_t* st = ring + slot * ST;
         IFit f[NS];
         tmq_v4i UA[NS][2], TA[NS][2], AA[NS][2];
@@ -1569,10 +1583,31 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
         }
         __syncthreads();
     }
-    if (wave == 0 && r < t.rows) {
-        int64_t tot = fix[lane];
+    if (wave != 0) return;
+    int64_t tot = fix[lane];
 #pragma unroll
-        for (int i = 0; i < NW; i++) tot += part[i * 64 + lane];
+    for (int i = 0; i < NW; i++) tot += part[i * 64 + lane];
+    if (pieces > 1) {
+        // The pieces' row sums meet through device-scope atomics, which
+        // every XCD performs at the same coherence point: each piece adds
+        // its sums and waits for their return before it counts itself in;
+        // the piece whose count completes the slot therefore reads the
+        // whole sums, and leaves the slot zero for the next launch.
+        // Integer addition: the sums do not depend on the order.
+        uint64_t* sl = tail + (size_t)slot * TMQ_TAIL_SLOT_WORDS;
+        const uint64_t prev = __hip_atomic_fetch_add(sl + lane, (uint64_t)tot, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(prev));
+        wait_vm<0>();
+        uint32_t cnt = 0;
+        if (lane == 0)
+            cnt = (uint32_t)__hip_atomic_fetch_add(sl + 64, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        cnt = __builtin_amdgcn_readfirstlane(cnt);
+        if ((int)cnt != pieces - 1) return;
+        tot = (int64_t)__hip_atomic_exchange(sl + lane, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_store(sl + 64, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (r < t.rows) {
         if (w.acc) w.acc[r] = tot;
         // sim/tmac_gguf.cpp:1192-1194 (Q4_K), :1501-1503 (Q6_K):
         // y = (float)((double)acc*x_scale/(double)row_inv)
@@ -1582,15 +1617,16 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g) {
 }
 
 template <int FMT, bool CLAMP>
-__device__ __forceinline__ void run_group(const TmqWork& w, int g) {
+__device__ __forceinline__ void run_group(const TmqWork& w, int g, int b0, int b1, int slot, int pieces,
+                                          uint64_t* tail) {
     if constexpr (FMT == kQ8_0) {
         group_q8(w, g);
     } else if constexpr (FMT == kQ5_0M) {
         group_mfma_q5(w, g);
     } else if constexpr (FMT == kQ4_KM) {
-        group_mfma_kq<kQ4_K>(w, g);
+        group_mfma_kq<kQ4_K>(w, g, b0, b1 ? b1 : w.t.nb, slot, pieces, tail);
     } else if constexpr (FMT == kQ6_KM) {
-        group_mfma_kq<kQ6_K>(w, g);
+        group_mfma_kq<kQ6_K>(w, g, b0, b1 ? b1 : w.t.nb, slot, pieces, tail);
     } else {
         group_ksplit<FMT, CLAMP>(w, g);
     }
@@ -1599,16 +1635,17 @@ __device__ __forceinline__ void run_group(const TmqWork& w, int g) {
 // one GEMV
 template <int FMT, bool CLAMP>
 __global__ __launch_bounds__(64 * gemv_waves(FMT)) void gemv_kernel(TmqWork w) {
-    run_group<FMT, CLAMP>(w, blockIdx.x);
+    run_group<FMT, CLAMP>(w, blockIdx.x, 0, 0, 0, 1, nullptr);
 }
 
 // A chain segment: every descriptor of one format in one launch,
-// workgroup -> (descriptor, group) through the group map.
+// workgroup -> (descriptor, group, super-block range) through the group map.
 template <int FMT, bool CLAMP>
 __global__ __launch_bounds__(64 * gemv_waves(FMT)) void chain_kernel(const TmqWork* __restrict__ works,
-                                                       const int32_t* __restrict__ group_work) {
-    const TmqWork& w = works[group_work[blockIdx.x]];
-    run_group<FMT, CLAMP>(w, blockIdx.x - w.first_group);
+                                                                     const TmqGroupRef* __restrict__ groups,
+                                                                     uint64_t* tail) {
+    const TmqGroupRef ref = groups[blockIdx.x];
+    run_group<FMT, CLAMP>(works[ref.work], ref.group, ref.b0, ref.b1, ref.slot, ref.pieces, tail);
 }
 
 // ------------------------------------------------- INT16 and FP32 paths
@@ -3418,12 +3455,12 @@ size_t tmq_gemv_lds_bytes(int fmt, int max_cols) {
     return 0;
 }
 
-int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const int32_t* group_work_dev,
-                     int total_groups, hipStream_t s) {
+int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const TmqGroupRef* groups_dev,
+                     int total_groups, uint64_t* tail, hipStream_t s) {
     if (total_groups <= 0) return 0;
     void* k = kernel_for<ChainK>(fmt, clamp);
     if (!k) return (int)hipErrorInvalidValue;
-    void* args[] = {&works_dev, &group_work_dev};
+    void* args[] = {&works_dev, &groups_dev, &tail};
     return (int)hipLaunchKernel(k, dim3(total_groups), dim3(64 * gemv_waves(fmt)), args,
                                 tmq_gemv_lds_bytes(fmt, max_cols), s);
 }

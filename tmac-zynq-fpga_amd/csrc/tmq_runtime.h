@@ -48,6 +48,7 @@ struct TmqDevBuf {
 
 struct tmq_ctx {
     int device = 0;
+    int ncu = 0;  // compute units of the device
     hipStream_t stream = nullptr;
     TmqDevBuf x, y, act, acc, misc, works, gmap;
 };
