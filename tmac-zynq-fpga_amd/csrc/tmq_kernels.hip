@@ -1051,10 +1051,16 @@ __device__ __forceinline__ IFit kfit(float an, float bn, int p, uint32_t code) {
 // mri = dmin*row_inv*256 (per block): an = dri*sc, bn = 8*an - mri*m + 128
 // (E(8)*row_inv*256 + 128 up to rounding).  The upload fit and the decoder
 // both use this function.
-__device__ __forceinline__ void q4k_nom(float dri, float mri, int sc, int m, float& an, float& bn) {
-    an = dri * (float)sc;
-    bn = __builtin_fmaf(an, 8.0f, __builtin_fmaf(-mri, (float)m, 128.0f));
+__device__ __forceinline__ void q4k_nomf(float dri, float mri, float sc, float m, float& an, float& bn) {
+    an = dri * sc;
+    bn = __builtin_fmaf(an, 8.0f, __builtin_fmaf(-mri, m, 128.0f));
 }
+__device__ __forceinline__ void q4k_nom(float dri, float mri, int sc, int m, float& an, float& bn) {
+    q4k_nomf(dri, mri, (float)sc, (float)m, an, bn);
+}
+template <bool B> struct BoolC {
+    static constexpr bool value = B;
+};
 
 // block pairs in flight per lane
 #ifndef TMQ_MFMA_DEPTH
@@ -1294,13 +1300,16 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
 //               (q6_pack_kernel, 1024 B each), the quarter's four sub-block
 //               scales (256 B), d (256 B), the four fit codes (256 B).
 // The activation's operand bytes, 32- and 16-element sums are copied into
-// LDS once per workgroup.
+// LDS once per workgroup (the range's part of them for a split group).
 constexpr int kKqWaves = 4;
 template <int FMT> __host__ __device__ constexpr int kq_stage() { return FMT == kQ4_K ? 3328 : 3840; }
 template <int FMT> __host__ __device__ constexpr int kq_ndma() { return FMT == kQ4_K ? 4 : 6; }
 template <int FMT> __host__ __device__ constexpr int kq_xa_off() { return kKqWaves * TMQ_MFMA_DEPTH * kq_stage<FMT>(); }
+// behind the operand bytes: 256 zero bytes, then 256 one bytes (the A rows
+// that hold no activation read there, at the same offsets as the others)
+constexpr int kKqConst = 512;
 template <int FMT> __host__ __device__ constexpr int kq_xs_off(int nbx) {
-    return kq_xa_off<FMT>() + ((nbx * 64 + 32 + 15) & ~15);
+    return kq_xa_off<FMT>() + nbx * 64 + kKqConst;
 }
 template <int FMT> __host__ __device__ constexpr int kq_xs16_off(int nbx) { return kq_xs_off<FMT>(nbx) + ((nbx * 4 + 15) & ~15); }
 template <int FMT> __host__ __device__ constexpr int kq_part_off(int nbx) {
@@ -1348,9 +1357,10 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
             if (i0 + lane < a1)
                 __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
                                                  16, 0, 0);
-        if (wave == NW - 1 && lane < 2)
-            __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(nbx * 4 + lane) * 16),
-                                             (lds_u8*)(xa + nbx * 64), 16, 0, 0);
+        if (wave == NW - 1 && lane < kKqConst / 16) {
+            const uint32_t v = lane < kKqConst / 32 ? 0u : 0x01010101u;
+            *(uint4*)(xa + nbx * 64 + lane * 16) = make_uint4(v, v, v, v);
+        }
         const uint8_t* xs = w.act + tmq_act_xs(n);
         const int s0 = 8 * b0, s1 = 8 * b1;
         for (int i0 = s0 + wave * 64; i0 < s1; i0 += NW * 64)
@@ -1405,16 +1415,19 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
     };
 #pragma unroll
     for (int i = 0; i < D; i++) issue(i, i);
-    // this wave's part of the activation copy has landed; the barrier makes
-    // every part visible (a plain s_barrier: the workgroup fence of
-    // __syncthreads would also wait for the ring's stages)
+    // this wave's part of the activation copy has landed and the constant
+    // bytes are written; the barrier makes every part visible (a plain
+    // s_barrier: the workgroup fence of __syncthreads would also wait for
+    // the ring's stages)
     wait_vm<ND * D>();
-    asm volatile("s_barrier" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // this lane's A operand: rows 4q', 4q'+1 the sub-block's xh and
     // xl - 128 over K group q' (lane >> 4), row 4q'+2 ones, the rest zero;
-    // the 16 elements of (32-element block xb, half hf) at abase +
-    // astride*(64*xb + 32*hf)
+    // the 16 elements of (32-element block xb, half hf) at
+    // ((64*xb + 32*hf) & amask) | abase.  A step's blocks lie at
+    // immediate offsets 0-192 from its first, which the rows of ones and
+    // zeros (amask 0) read inside their 256-byte constant runs.
     // (the offset is a multiple of 32 and abase < 32 where amask is set, so
     // (offset & amask) | abase is one v_and_or)
     uint32_t abase, amask;
@@ -1422,12 +1435,10 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
         const int qg = lane >> 4, m = lane & 15, dg = m & 3;
         const bool own = (m >> 2) == qg;
         const uint32_t zero = (uint32_t)nbx * 64u;
-        abase = own && dg < 2 ? (uint32_t)(dg * 16) : own && dg == 2 ? zero + 16u : zero;
+        abase = own && dg < 2 ? (uint32_t)(dg * 16) : own && dg == 2 ? zero + kKqConst / 2 : zero;
         amask = own && dg < 2 ? 0xffffffffu : 0u;
     }
-    auto aop = [&](int xb, int hf) {
-        return *(lv4i*)(xa + ((((uint32_t)(64 * xb + 32 * hf)) & amask) | abase));
-    };
+    auto abase_of = [&](uint32_t off) { return (off & amask) | abase; };
 
     int64_t acc = 0;
     tmq_v4i Ct = {};
@@ -1439,130 +1450,149 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
         ap[k] = bp[k] = xp[k] = 0;
     }
     const tmq_v4i Z = {};
-    // Q4_K: a wave's quarter is the same in every super-block (wave & 3, as
-    // NW is 4), so sub-blocks s = 2q + k unpack from the header with
-    // wave-uniform fields (q4k_scale_min's cases):
-    //   q < 2:  sc = bits 8s..+5 of dword 1,  m = bits 8s..+5 of dword 2
-    //   q >= 2: s' = s - 4, sc = bits 8s'..+3 of dword 3 | bits 8s'+6, +7 of dword 1 << 4,
-    //           m = bits 8s'+4..+7 of dword 3 | bits 8s'+6, +7 of dword 2 << 4
-    // (a field of width 0 reads as 0)
+    // Q4_K: a wave's quarter q is the same in every super-block (wave & 3,
+    // as NW is 4); its sub-blocks s = 2q + k take their 6-bit scale and min
+    // from the header's scale bytes (q4k_scale_min's cases):
+    //   q < 2:  sc_k = scales[s] & 63, m_k = scales[4 + s] & 63
+    //   q >= 2: s' = s - 4, sc_k = (scales[8 + s'] & 15) | (scales[s'] >> 6) << 4,
+    //           m_k = (scales[8 + s'] >> 4) | (scales[4 + s'] >> 6) << 4
+    // gathered by v_perm as the bytes (sc_0, sc_1, m_0, m_1) of one dword:
+    // bytes s0, s0 + 1 of a header dword and of the next, s0 = 2 * (q & 1)
     static_assert(NW == 4, "the quarter of a wave is wave & 3");
-    const int qw = wave & 3, lo2 = qw < 2;
-    const uint32_t ko1 = lo2 ? 16 * qw : 16 * qw - 32, ko3 = lo2 ? ko1 : ko1 + 4, ko2 = ko1 + 6;
-    const uint32_t kw1 = lo2 ? 6 : 4, kw2 = lo2 ? 0 : 2;
-    auto step = [&](int i, int slot) {
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vm<ND * (D - 1)>();
-        const int u = u0 + wave + NW * i, b = u >> 2, q = u & 3;
-        const uint8_t* st = ring + slot * ST;
-        IFit f[NS];
-        tmq_v4i UA[NS][2], TA[NS][2], AA[NS][2];
-        int xsv[NS];
-        if constexpr (FMT == kQ4_K) {
-            const tmq_v4i qa = *(lv4i*)(st + lane * 16), qb = *(lv4i*)(st + 1024 + lane * 16);
-            const tmq_v4i hv = *(lv4i*)(st + 2048 + lane * 16);
-            const uint32_t codes = *(lu16*)(st + 3072 + lane * 4);
+    const int qw = wave & 3;
+    const uint32_t hs0 = 2u * (uint32_t)(qw & 1);
+    const uint32_t hsel = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(hs0 | (hs0 + 1) << 8 | (hs0 + 4) << 16 | (hs0 + 5) << 24));
+    // the loop, compiled per header case (q < 2 or not; Q6_K: one case)
+    auto run = [&](auto lo2c) {
+        constexpr bool LO2 = decltype(lo2c)::value;
+        auto step = [&](int i, int slot) {
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vm<ND * (D - 1)>();
+            const int u = u0 + wave + NW * i, b = u >> 2, q = u & 3;
+            const uint8_t* st = ring + slot * ST;
+            IFit f[NS];
+            tmq_v4i UA[NS][2], TA[NS][2], AA[NS][2];
+            int xsv[NS];
+            if constexpr (FMT == kQ4_K) {
+                const tmq_v4i qa = *(lv4i*)(st + lane * 16), qb = *(lv4i*)(st + 1024 + lane * 16);
+                const tmq_v4i hv = *(lv4i*)(st + 2048 + lane * 16);
+                const uint32_t codes = *(lu16*)(st + 3072 + lane * 4);
+                // sub-block k, half hf: block 8b + 2q + k
+                const uint32_t ab = abase_of(64u * (uint32_t)(8 * b + 2 * q));
 #pragma unroll
-            for (int k = 0; k < NS; k++) {
-                const int xb = 8 * b + 2 * q + k;
-                AA[k][0] = aop(xb, 0);
-                AA[k][1] = aop(xb, 1);
-                xsv[k] = xsl[xb];
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue(i + D, slot);
-            const uint4 h = make_uint4((uint32_t)hv.x, (uint32_t)hv.y, (uint32_t)hv.z, (uint32_t)hv.w);
-            const float dri = h2f(h.x) * ri256, mri = h2f(h.x >> 16) * ri256;
-            const uint32_t hp = lo2 ? h.y : h.w, hq = lo2 ? h.z : h.w;
+                for (int k = 0; k < NS; k++) {
+                    AA[k][0] = *(lv4i*)(xa + ab + 64 * k);
+                    AA[k][1] = *(lv4i*)(xa + ab + 64 * k + 32);
+                    xsv[k] = xsl[8 * b + 2 * q + k];
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue(i + D, slot);
+                const uint32_t hx = (uint32_t)hv.x, hy = (uint32_t)hv.y, hz = (uint32_t)hv.z, hw = (uint32_t)hv.w;
+                const float dri = h2f(hx) * ri256, mri = h2f(hx >> 16) * ri256;
+                uint32_t scm;
+                if constexpr (LO2)
+                    scm = __builtin_amdgcn_perm(hz, hy, hsel) & 0x3f3f3f3fu;
+                else
+                    scm = (__builtin_amdgcn_perm(hw >> 4, hw, hsel) & 0x0f0f0f0fu) |
+                          ((__builtin_amdgcn_perm(hz, hy, hsel) >> 2) & 0x30303030u);
 #pragma unroll
-            for (int k = 0; k < NS; k++) {
-                const int sc = (int)(__builtin_amdgcn_ubfe(hp, ko1 + 8 * k, kw1) |
-                                     (__builtin_amdgcn_ubfe(h.y, ko2 + 8 * k, kw2) << 4));
-                const int m = (int)(__builtin_amdgcn_ubfe(hq, ko3 + 8 * k, kw1) |
-                                    (__builtin_amdgcn_ubfe(h.z, ko2 + 8 * k, kw2) << 4));
-                float an, bn;
-                q4k_nom(dri, mri, sc, m, an, bn);
-                f[k] = kfit(an, bn, 8, (codes >> (8 * k)) & 255u);
-                const tmq_v4i src[2] = {qa, qb};
+                for (int k = 0; k < NS; k++) {
+                    float an, bn;
+                    q4k_nomf(dri, mri, (float)((scm >> (8 * k)) & 255u), (float)((scm >> (16 + 8 * k)) & 255u), an,
+                             bn);
+                    f[k] = kfit(an, bn, 8, (codes >> (8 * k)) & 255u);
+                    const tmq_v4i src[2] = {qa, qb};
 #pragma unroll
-                for (int hf = 0; hf < 2; hf++) {
+                    for (int hf = 0; hf < 2; hf++) {
+                        uint32_t U[4], T[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const uint32_t v = (uint32_t)src[hf][e];
+                            U[e] = (k ? (v >> 4) : v) & 0x0f0f0f0fu;
+                            T[e] = ifit_t4(U[e], f[k].a2, f[k].b2);
+                        }
+                        UA[k][hf] = tmq_v4i{(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
+                        TA[k][hf] = tmq_v4i{(int)T[0], (int)T[1], (int)T[2], (int)T[3]};
+                    }
+                }
+            } else {
+                const int h = q >> 1, lc = q & 1;
+                const tmq_v4i va = *(lv4i*)(st + lane * 16), vb = *(lv4i*)(st + 1024 + lane * 16);
+                const tmq_v4i vh = *(lv4i*)(st + 2048 + lane * 16);
+                const uint32_t scq = *(lu32c*)(st + 3072 + lane * 4);
+                const uint32_t dbits = *(lu16*)(st + 3328 + lane * 4);
+                const uint32_t codes = *(lu32c*)(st + 3584 + lane * 4);
+                // sub-block k: half lc of block 8b + 4h + k
+                const uint32_t ab = abase_of(64u * (uint32_t)(8 * b + 4 * h) + 32u * (uint32_t)lc);
+#pragma unroll
+                for (int k = 0; k < NS; k++) {
+                    AA[k][0] = *(lv4i*)(xa + ab + 64 * k);
+                    xsv[k] = xs16l[2 * (8 * b + 4 * h + k) + lc];
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue(i + D, slot);
+                const float ssri = h2f(dbits) * ri256;
+#pragma unroll
+                for (int k = 0; k < NS; k++) {
+                    // scale 8h + lc + 2k: byte k of the quarter's scale dword
+                    const int sc = (int)(int8_t)(uint8_t)(scq >> (8 * k));
+                    f[k] = kfit(ssri * (float)sc, 128.0f, 32, (codes >> (8 * k)) & 255u);
                     uint32_t U[4], T[4];
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        const uint32_t v = (uint32_t)src[hf][e];
-                        U[e] = (k ? (v >> 4) : v) & 0x0f0f0f0fu;
+                        // sub-blocks 0-2: the low 6 bits of chunk k; sub-block 3:
+                        // the top 2 bits of chunks 0, 1, 2 as its bits 0-1, 2-3, 4-5
+                        const uint32_t d0 = (uint32_t)va[e], d1 = (uint32_t)vb[e], d2 = (uint32_t)vh[e];
+                        U[e] = k == 0   ? d0 & 0x3f3f3f3fu
+                               : k == 1 ? d1 & 0x3f3f3f3fu
+                               : k == 2 ? d2 & 0x3f3f3f3fu
+                                        : ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0c0c0c0cu) |
+                                              ((d2 >> 2) & 0x30303030u);
                         T[e] = ifit_t4(U[e], f[k].a2, f[k].b2);
                     }
-                    UA[k][hf] = tmq_v4i{(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
-                    TA[k][hf] = tmq_v4i{(int)T[0], (int)T[1], (int)T[2], (int)T[3]};
+                    UA[k][0] = tmq_v4i{(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
+                    TA[k][0] = tmq_v4i{(int)T[0], (int)T[1], (int)T[2], (int)T[3]};
                 }
             }
-        } else {
-            const int h = q >> 1, lc = q & 1;
-            const tmq_v4i va = *(lv4i*)(st + lane * 16), vb = *(lv4i*)(st + 1024 + lane * 16);
-            const tmq_v4i vh = *(lv4i*)(st + 2048 + lane * 16);
-            const uint32_t scq = *(lu32c*)(st + 3072 + lane * 4);
-            const uint32_t dbits = *(lu16*)(st + 3328 + lane * 4);
-            const uint32_t codes = *(lu32c*)(st + 3584 + lane * 4);
+            // the previous quarter's u sums (their MFMAs have long finished)
+#pragma unroll
+            for (int k = 0; k < NS; k++)
+                acc += (int64_t)ap[k] * (Cu[k][0] * 256 + Cu[k][1] + Cu[k][2] * 128) + (int64_t)bp[k] * xp[k];
+            __builtin_amdgcn_sched_barrier(0);  // the read-out before the overwrite
 #pragma unroll
             for (int k = 0; k < NS; k++) {
-                const int xb = 8 * b + 4 * h + k;
-                AA[k][0] = aop(xb, lc);
-                xsv[k] = xs16l[2 * xb + lc];
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue(i + D, slot);
-            const float ssri = h2f(dbits) * ri256;
-#pragma unroll
-            for (int k = 0; k < NS; k++) {
-                // scale 8h + lc + 2k: byte k of the quarter's scale dword
-                const int sc = (int)(int8_t)(uint8_t)(scq >> (8 * k));
-                f[k] = kfit(ssri * (float)sc, 128.0f, 32, (codes >> (8 * k)) & 255u);
-                uint32_t U[4], T[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    // sub-blocks 0-2: the low 6 bits of chunk k; sub-block 3:
-                    // the top 2 bits of chunks 0, 1, 2 as its bits 0-1, 2-3, 4-5
-                    const uint32_t d0 = (uint32_t)va[e], d1 = (uint32_t)vb[e], d2 = (uint32_t)vh[e];
-                    U[e] = k == 0   ? d0 & 0x3f3f3f3fu
-                           : k == 1 ? d1 & 0x3f3f3f3fu
-                           : k == 2 ? d2 & 0x3f3f3f3fu
-                                    : ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0c0c0c0cu) | ((d2 >> 2) & 0x30303030u);
-                    T[e] = ifit_t4(U[e], f[k].a2, f[k].b2);
+                if constexpr (FMT == kQ4_K) {
+                    Cu[k] = mfma16(AA[k][0], UA[k][0], Z);
+                    Cu[k] = mfma16(AA[k][1], UA[k][1], Cu[k]);
+                    Ct = mfma16(AA[k][0], TA[k][0], Ct);
+                    Ct = mfma16(AA[k][1], TA[k][1], Ct);
+                } else {
+                    Cu[k] = mfma16(AA[k][0], UA[k][0], Z);
+                    Ct = mfma16(AA[k][0], TA[k][0], Ct);
                 }
-                UA[k][0] = tmq_v4i{(int)U[0], (int)U[1], (int)U[2], (int)U[3]};
-                TA[k][0] = tmq_v4i{(int)T[0], (int)T[1], (int)T[2], (int)T[3]};
+                ap[k] = f[k].alpha;
+                bp[k] = f[k].beta;
+                xp[k] = xsv[k];
             }
-        }
-        // the previous quarter's u sums (their MFMAs have long finished)
+        };
+        int ib = 0;
+        for (; ib + D <= nuw; ib += D) {
 #pragma unroll
-        for (int k = 0; k < NS; k++)
-            acc += (int64_t)ap[k] * (Cu[k][0] * 256 + Cu[k][1] + Cu[k][2] * 128) + (int64_t)bp[k] * xp[k];
-        __builtin_amdgcn_sched_barrier(0);  // the read-out before the overwrite
-#pragma unroll
-        for (int k = 0; k < NS; k++) {
-            if constexpr (FMT == kQ4_K) {
-                Cu[k] = mfma16(AA[k][0], UA[k][0], Z);
-                Cu[k] = mfma16(AA[k][1], UA[k][1], Cu[k]);
-                Ct = mfma16(AA[k][0], TA[k][0], Ct);
-                Ct = mfma16(AA[k][1], TA[k][1], Ct);
-            } else {
-                Cu[k] = mfma16(AA[k][0], UA[k][0], Z);
-                Ct = mfma16(AA[k][0], TA[k][0], Ct);
-            }
-            ap[k] = f[k].alpha;
-            bp[k] = f[k].beta;
-            xp[k] = xsv[k];
+            for (int i = 0; i < D; i++) step(ib + i, i);
         }
+#pragma unroll
+        for (int i = 0; i < D; i++)
+            if (ib + i < nuw) step(ib + i, i);
     };
-    int ib = 0;
-    for (; ib + D <= nuw; ib += D) {
-#pragma unroll
-        for (int i = 0; i < D; i++) step(ib + i, i);
+    if constexpr (FMT == kQ4_K) {
+        if (qw < 2)
+            run(BoolC<true>{});
+        else
+            run(BoolC<false>{});
+    } else {
+        run(BoolC<true>{});
     }
-#pragma unroll
-    for (int i = 0; i < D; i++)
-        if (ib + i < nuw) step(ib + i, i);
 #pragma unroll
     for (int k = 0; k < NS; k++)
         acc += (int64_t)ap[k] * (Cu[k][0] * 256 + Cu[k][1] + Cu[k][2] * 128) + (int64_t)bp[k] * xp[k];
