@@ -1078,13 +1078,15 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 // TMQ_MFMA_DEPTH stages, each one block of the wave's 64 rows as the LDS DMA
 // lays it down (lane l at 16*l of the qs part, 4*l of the others): qs
 // 1024 B, qh' 256 B, d 256 B, the fit-code dword (the block's code in byte
-// wave) 256 B; then the activation's operand bytes (XA with the zero and
-// ones chunks), the block sums, the waves' row sums and the 64 rows'
+// wave) 256 B; then the activation's operand bytes (XA, then runs of zero
+// and one bytes), the block sums, the waves' row sums and the 64 rows'
 // corrections.
 constexpr int kMfmaStage = 1792;
 constexpr int kMfmaWaves = gemv_waves(kQ5_0M);
 __host__ __device__ constexpr int mfma_xa_off() { return kMfmaWaves * TMQ_MFMA_DEPTH * kMfmaStage; }
-__host__ __device__ constexpr int mfma_xs_off(int nb) { return mfma_xa_off() + ((nb * 64 + 32 + 15) & ~15); }
+// behind the operand bytes: 64 zero bytes, then 64 one bytes
+constexpr int kMfmaConst = 128;
+__host__ __device__ constexpr int mfma_xs_off(int nb) { return mfma_xa_off() + nb * 64 + kMfmaConst; }
 __host__ __device__ constexpr int mfma_part_off(int nb) { return mfma_xs_off(nb) + ((nb * 4 + 15) & ~15); }
 __host__ __device__ constexpr int mfma_lds_bytes(int nb) { return mfma_part_off(nb) + (kMfmaWaves + 1) * 64 * 8; }
 
@@ -1137,11 +1139,15 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     // not wait for the ring's stages
     {
         const uint8_t* src = w.act + tmq_act_xa(n);
-        const int n16 = nb * 4 + 2;
+        const int n16 = nb * 4;
         for (int i0 = wave * 64; i0 < n16; i0 += NW * 64)
             if (i0 + lane < n16)
                 __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
                                                  16, 0, 0);
+        if (wave == NW - 1 && lane < kMfmaConst / 16) {
+            const uint32_t v = lane < kMfmaConst / 32 ? 0u : 0x01010101u;
+            *(uint4*)(xa + nb * 64 + lane * 16) = make_uint4(v, v, v, v);
+        }
         const uint8_t* xs = w.act + tmq_act_xs(n);
         for (int i0 = wave * 64; i0 < nb; i0 += NW * 64)
             if (i0 + lane < nb)
@@ -1177,22 +1183,26 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     };
 #pragma unroll
     for (int i = 0; i < D; i++) issue(i, i);
-    // this wave's part of the activation copy has landed; the barrier makes
-    // every part visible (a plain s_barrier: the workgroup fence of
-    // __syncthreads would also wait for the ring's stages)
+    // this wave's part of the activation copy has landed and the constant
+    // bytes are written; the barrier makes every part visible (a plain
+    // s_barrier: the workgroup fence of __syncthreads would also wait for
+    // the ring's stages)
     wait_vm<4 * D>();
-    asm volatile("s_barrier" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // this lane's A operand: rows 4q, 4q+1 the block's xh and xl - 128 over
-    // K group q, row 4q+2 ones, the rest zero
-    uint32_t abase, astride, acoff;
+    // K group q, row 4q+2 ones, the rest zero: block b's two halves at
+    // abase + b*astride and 32 bytes on (the rows of zeros and ones,
+    // astride 0, read both inside their 64-byte constant runs)
+    const lds_u8* ap0;
+    uint32_t astride;
     {
         const int q = lane >> 4, m = lane & 15, dg = m & 3;
         const bool own = (m >> 2) == q;
         const uint32_t zero = (uint32_t)nb * 64u;
-        abase = own && dg < 2 ? (uint32_t)(dg * 16) : own && dg == 2 ? zero + 16u : zero;
+        const uint32_t abase = own && dg < 2 ? (uint32_t)(dg * 16) : own && dg == 2 ? zero + kMfmaConst / 2 : zero;
         astride = own && dg < 2 ? 64u : 0u;
-        acoff = own && dg < 2 ? 32u : 0u;
+        ap0 = (const lds_u8*)(xa + abase);
     }
 
     int64_t acc = 0;
@@ -1215,8 +1225,8 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
         k.qh = *(lu32c*)(st + 1024 + lane * 4);
         k.d = *(lu16*)(st + 1280 + lane * 4);
         k.e = *(lu8*)(st + 1536 + lane * 4 + (b & 3));
-        const uint32_t ao = abase + (uint32_t)b * astride;
-        const tmq_v4i A0 = *(lv4i*)(xa + ao), A1 = *(lv4i*)(xa + ao + acoff);
+        const lds_u8* xp0 = ap0 + (uint32_t)b * astride;
+        const tmq_v4i A0 = *(lv4i*)xp0, A1 = *(lv4i*)(xp0 + 32);
         const int xsv = *(li32*)(xsl + b);
         // the stage's reads are in registers before its refill overwrites it
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
