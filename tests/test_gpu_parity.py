@@ -346,6 +346,53 @@ def test_chain_split_tail(ctx, oracle, monkeypatch, qt, force):
         t.free()
 
 
+def test_chain_split_tail_q8(ctx, oracle, monkeypatch):
+    """A Q8_0 chain segment of 20 896x896 tensors (4 groups of 256 rows
+    each, the last one half empty) and one 130x896 tensor (1 group): 81
+    groups leave a last round of 81 on 256 CUs, which the chain runs as one
+    workgroup per 64-row quarter, the four waves splitting the row's tiles.
+    Three runs: per-tile int64 sums and fp32 outputs bit-exact with the
+    oracle, the same as the unsplit chain (TMQ_NOSPLIT=1)."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda:0")
+    cols = 896
+    shapes = [896] * 20 + [130]
+    x = synth.gen_x(cols, 77)
+    x_d = torch.from_numpy(x).to(dev)
+    xq, _ = oracle.quantize_act(x)
+    descs, ys, accs, exp, ts = [], [], [], [], []
+    nt = cols // 64
+    for i, rows in enumerate(shapes):
+        w = synth.gen_weights(Q8_0, rows, cols, 900 + i)
+        t = ctx.upload(Q8_0, rows, cols, w)
+        y = torch.zeros(rows, dtype=torch.float32, device=dev)
+        a = torch.zeros(rows * nt, dtype=torch.int64, device=dev)
+        tiles, tr = (rows // 64, 64) if rows % 64 == 0 else (13, 10)
+        descs.append((t, x_d.data_ptr(), y.data_ptr(), a.data_ptr(), tiles, tr, nt))
+        ys.append(y)
+        accs.append(a)
+        ts.append(t)
+        rse = oracle.q8_row_scale(oracle.row_max_abs_q8(w, rows, cols))
+        exp.append((oracle.tiles_q8(w, rows, cols, xq, rse).reshape(-1), oracle.matmul(Q8_0, w, x, rows, cols)))
+    for nosplit in (False, True):
+        monkeypatch.setenv("TMQ_NOSPLIT", "1" if nosplit else "0")
+        print(f"[chain] Q8_0 split tail, nosplit {nosplit}", flush=True)
+        ch = ctx.chain(descs)
+        for run in range(3):
+            for y, a in zip(ys, accs):
+                y.zero_()
+                a.zero_()
+            ch.run()
+            ctx.sync()
+            for i, (y, a, (pe, ye)) in enumerate(zip(ys, accs, exp)):
+                got = a.cpu().numpy()
+                assert np.array_equal(got, pe), report(f"tiles of tensor {i}, run {run}", got, pe)
+                assert np.array_equal(bits(y.cpu().numpy()), bits(ye)), f"y of tensor {i}, run {run}"
+        ch.free()
+    for t in ts:
+        t.free()
+
+
 def test_error_paths(ctx):
     import tmq
     w = synth.gen_weights(Q5_0, 8, 896, 1)

@@ -101,6 +101,7 @@ const char* type_name(uint32_t type) {
 
 struct Segment {
     int type, clamp, gmap_off, ngroups, max_cols;  // type: kernel format (tmq_kernel_fmt)
+    int split;                                     // holds split groups
 };
 
 }  // namespace
@@ -454,11 +455,16 @@ int run_int16(tmq_ctx* ctx, const tmq_tensor* t, const int16_t* xq, std::vector<
 //
 // A launch's workgroups run in rounds of one per CU, so a segment of W
 // whole-row groups takes ceil(W / ncu) group times even when its last round
-// holds a few.  With ncu > 0, a K-quant MFMA segment whose last round holds
-// T <= ncu / 2 groups splits each of those T groups into up to ncu / T
-// workgroups over disjoint super-block ranges (at least one each), so that
-// the last round takes a fraction of a group time; each split group gets a
-// tail slot (`nslots` of them) where its pieces add their row sums.
+// holds a few.  With ncu > 0, a segment whose last round holds T <= ncu / 2
+// groups splits those T groups so that the last round takes a fraction of a
+// group time:
+//  - K-quant MFMA segments: each group into up to ncu / T workgroups over
+//    disjoint super-block ranges (at least one each); each split group gets
+//    a tail slot (`nslots` of them) where its pieces add their row sums;
+//  - Q8_0 segments (256-row groups, one wave per 64 rows) of at most
+//    TMQ_Q8_SPLIT_COLS columns: each group into its four 64-row quarters,
+//    whose four waves split the row's 64-column tiles (no slot: the tiles'
+//    sums meet in the workgroup's LDS).
 void plan_segments(std::vector<TmqWork>& works, std::vector<TmqGroupRef>& gmap, std::vector<Segment>& segs,
                    int ncu, int& nslots) {
     std::stable_sort(works.begin(), works.end(), [](const TmqWork& a, const TmqWork& b) {
@@ -471,11 +477,27 @@ void plan_segments(std::vector<TmqWork>& works, std::vector<TmqGroupRef>& gmap, 
     auto close = [&]() {
         if (segs.empty() || ncu <= 0) return;
         Segment& sg = segs.back();
-        if (sg.type != TMQ_FMT_Q4_K_MFMA && sg.type != TMQ_FMT_Q6_K_MFMA) return;
+        const bool kq = sg.type == TMQ_FMT_Q4_K_MFMA || sg.type == TMQ_FMT_Q6_K_MFMA;
+        const bool q8 = sg.type == TMQ_TYPE_Q8_0 && sg.max_cols <= TMQ_Q8_SPLIT_COLS;
+        if (!kq && !q8) return;
         const int tcount = sg.ngroups % ncu;
         if (tcount == 0 || ncu / tcount < 2) return;
         std::vector<TmqGroupRef> last(gmap.end() - tcount, gmap.end());
         gmap.resize(gmap.size() - tcount);
+        sg.split = 1;
+        if (q8) {
+            for (const TmqGroupRef& e : last)
+                for (int k = 0; k < TMQ_WAVES; k++) {
+                    // quarters past the tensor's padded rows are left out
+                    if ((e.group * TMQ_WAVES + k) * 64 >= works[e.work].t.rows_pad) break;
+                    TmqGroupRef p = e;
+                    p.b0 = (uint16_t)k;
+                    p.pieces = TMQ_WAVES;
+                    gmap.push_back(p);
+                }
+            sg.ngroups = (int)gmap.size() - sg.gmap_off;
+            return;
+        }
         for (const TmqGroupRef& e : last) {
             const int nb = works[e.work].t.nb;
             const int pieces = std::min(std::min(ncu / tcount, nb), 32767);
@@ -500,7 +522,7 @@ void plan_segments(std::vector<TmqWork>& works, std::vector<TmqGroupRef>& gmap, 
         const int fmt = tmq_kernel_fmt(w.t);
         if (segs.empty() || segs.back().type != fmt || segs.back().clamp != w.t.clamp) {
             close();
-            segs.push_back(Segment{fmt, w.t.clamp, (int)gmap.size(), 0, 0});
+            segs.push_back(Segment{fmt, w.t.clamp, (int)gmap.size(), 0, 0, 0});
         }
         Segment& sg = segs.back();
         sg.max_cols = std::max(sg.max_cols, w.t.cols);
@@ -515,7 +537,7 @@ int launch_segments(const std::vector<Segment>& segs, const void* works_dev, con
                     uint64_t* tail, hipStream_t s) {
     for (const Segment& sg : segs) {
         int e = tmq_launch_chain(sg.type, sg.clamp, sg.max_cols, (const TmqWork*)works_dev,
-                                 (const TmqGroupRef*)gmap_dev + sg.gmap_off, sg.ngroups, tail, s);
+                                 (const TmqGroupRef*)gmap_dev + sg.gmap_off, sg.ngroups, sg.split, tail, s);
         if (e) return tmq_fail(TMQ_ERR_HIP, "chain segment launch: %s", hipGetErrorString((hipError_t)e));
     }
     return 0;

@@ -257,10 +257,11 @@ int tmq_launch_rowstat(const TmqTensorDev& t, const float* aux_max_abs, float* r
                        float* row_scale, int* bad_flag, hipStream_t s);
 int tmq_launch_gemv(const TmqWork& w, hipStream_t s);
 // One workgroup of a chain launch: row group `group` of works[work] over
-// super-blocks [b0, b1) (b1 = 0: the whole row).  A group split into
-// `pieces` > 1 workgroups (only the K-quant MFMA decoders split) adds its
-// int64 row sums into tail slot `slot`; the piece completing the slot's
-// count finalises the rows and clears the slot for the next launch.
+// super-blocks [b0, b1) (b1 = 0: the whole row).  A K-quant MFMA group split
+// into `pieces` > 1 workgroups adds its int64 row sums into tail slot
+// `slot`; the piece completing the slot's count finalises the rows and
+// clears the slot for the next launch.  A Q8_0 group split into pieces = 4
+// runs as four workgroups, one per 64-row quarter b0.
 struct TmqGroupRef {
     int32_t work, group;
     uint16_t b0, b1;
@@ -271,8 +272,12 @@ struct TmqGroupRef {
 // one launch per chain segment (descriptors of one kernel format
 // (tmq_kernel_fmt) and clamp mode, max_cols = the widest of them); `tail`:
 // zeroed slots of the segment's split groups (null when none)
+// split: the segment holds split groups (Q8_0 quarters take dynamic LDS)
 int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const TmqGroupRef* groups_dev,
-                     int total_groups, uint64_t* tail, hipStream_t s);
+                     int total_groups, int split, uint64_t* tail, hipStream_t s);
+// widest Q8_0 rows whose chain groups split into quarters (the quarters'
+// 64-column tile sums, 512 B a tile, meet in LDS)
+#define TMQ_Q8_SPLIT_COLS 4096
 // dynamic LDS of a standalone / chain GEMV launch of a kernel format
 size_t tmq_gemv_lds_bytes(int fmt, int max_cols);
 // engine GEMV: activation recipe + works of any formats; waves = 16 or 4

@@ -957,6 +957,41 @@ __device__ __forceinline__ void group_q8(const TmqWork& w, int g) {
     if (w.y && r < t.rows) store_y(w, r, y);
 }
 
+// 64-row quarter `sub` of row group g, a split group of a chain's last
+// round: the four waves take the rows' 64-column tiles w, w + 4, ...; the
+// tiles' int64 sums meet in LDS (dynamic, 512 B a tile) and wave 0 folds
+// them in tile order as group_q8 does.
+__device__ __forceinline__ void group_q8_quarter(const TmqWork& w, int g, int sub) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
+    int64_t* ps = (int64_t*)mfma_lds;
+    const TmqTensorDev& t = w.t;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r0 = (g * TMQ_WAVES + sub) * 64;
+    if (r0 >= t.rows_pad) return;  // the same for the whole workgroup
+    const int r = r0 + lane;
+    const float ri = t.row_inv[r], rs = t.row_scale[r];
+    const Act A = act_view(w.act);
+    const int nt = (t.cols + 63) / 64;
+    for (int tt = wave; tt < nt; tt += TMQ_WAVES) {
+        int sh = 0, sl = 0;
+        const int b0 = 2 * tt, b1 = 2 * tt + 1;
+        const bool has1 = b1 < t.nb;
+        const Q8Blk k0 = q8_load(t, b0, r);
+        const Q8Blk k1 = has1 ? q8_load(t, b1, r) : k0;
+        q8_mac(k0, A, b0, ri, sh, sl);
+        if (has1) q8_mac(k1, A, b1, ri, sh, sl);
+        const int64_t P = (int64_t)sh * 256 + sl;
+        if (w.acc && r < t.rows) w.acc[(size_t)r * nt + tt] = P;
+        ps[tt * 64 + lane] = P;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float y = 0.0f;
+    for (int tt = 0; tt < nt; tt++)
+        y = (float)((double)y + ((double)ps[tt * 64 + lane] * (double)A.xs) * (double)rs);
+    if (w.y && r < t.rows) store_y(w, r, y);
+}
+
 // --------------------------------------------- MFMA decoders (Q5_0)
 // Integer fit.  Within one block of one row the int16 weight of code u is
 // g(u) = clamp16(roundf(fl(E(u) * row_inv))); ifit_kernel picks integers
@@ -1660,7 +1695,10 @@ template <int FMT, bool CLAMP>
 __device__ __forceinline__ void run_group(const TmqWork& w, int g, int b0, int b1, int slot, int pieces,
                                           uint64_t* tail) {
     if constexpr (FMT == kQ8_0) {
-        group_q8(w, g);
+        if (pieces > 1)
+            group_q8_quarter(w, g, b0);
+        else
+            group_q8(w, g);
     } else if constexpr (FMT == kQ5_0M) {
         group_mfma_q5(w, g);
     } else if constexpr (FMT == kQ4_KM) {
@@ -3496,13 +3534,17 @@ size_t tmq_gemv_lds_bytes(int fmt, int max_cols) {
 }
 
 int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev, const TmqGroupRef* groups_dev,
-                     int total_groups, uint64_t* tail, hipStream_t s) {
+                     int total_groups, int split, uint64_t* tail, hipStream_t s) {
     if (total_groups <= 0) return 0;
     void* k = kernel_for<ChainK>(fmt, clamp);
     if (!k) return (int)hipErrorInvalidValue;
+    size_t lds = tmq_gemv_lds_bytes(fmt, max_cols);
+    if (fmt == kQ8_0 && split) {
+        if (max_cols > TMQ_Q8_SPLIT_COLS) return (int)hipErrorInvalidValue;
+        lds = (size_t)((max_cols + 63) / 64) * 64 * 8;
+    }
     void* args[] = {&works_dev, &groups_dev, &tail};
-    return (int)hipLaunchKernel(k, dim3(total_groups), dim3(64 * gemv_waves(fmt)), args,
-                                tmq_gemv_lds_bytes(fmt, max_cols), s);
+    return (int)hipLaunchKernel(k, dim3(total_groups), dim3(64 * gemv_waves(fmt)), args, lds, s);
 }
 
 int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* out, hipStream_t s) {
