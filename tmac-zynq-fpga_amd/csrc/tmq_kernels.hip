@@ -1137,6 +1137,18 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N <= 63, "vmcnt holds 6 bits");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// s_waitcnt vmcnt(STEP * k) for a wave-uniform k in 0..K
+template <int STEP, int K>
+__device__ __forceinline__ void wait_vm_k(int k) {
+    if constexpr (K == 0) {
+        wait_vm<0>();
+    } else {
+        if (k >= K)
+            wait_vm<STEP * K>();
+        else
+            wait_vm_k<STEP, K - 1>(k);
+    }
+}
 
 __device__ __forceinline__ tmq_v4i mfma16(tmq_v4i a, tmq_v4i b, tmq_v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -1191,11 +1203,10 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     }
 
     uint8_t* ring = mfma_lds + wave * D * kMfmaStage;
-    const int ilast = max(nbw - 1, 0);
     const size_t R = t.rows_pad;
-    // stage `slot` <- the wave's block i (clamped: the refills past the end
-    // reload the last block, so every step waits for the same count; a wave
-    // with no block of its own (nb < NW) loads block nb - 1 and uses none)
+    // stage `slot` <- the wave's block i, i < nbw (nothing is loaded past
+    // the wave's last block: every weight byte is read from memory once;
+    // a wave with no block of its own (nb < NW) loads nothing).
     // Buffer loads: the planes' base addresses and sizes in scalar resources,
     // the block's element offset (wave-uniform) in a scalar register and
     // the lane's in a constant vector register, so no vector instruction
@@ -1205,7 +1216,7 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(t.pd, 2 * pl), rsi = buf_rsrc(t.pi, 4 * (uint32_t)R * ((nb + 3) / 4));
     const int la16 = lane * 16, la4 = lane * 4, la2 = lane * 2;
     auto issue = [&](int i, int slot) {
-        const int blk = __builtin_amdgcn_readfirstlane(min(wave + NW * min(i, ilast), nb - 1));
+        const int blk = __builtin_amdgcn_readfirstlane(wave + NW * i);
         const int ob = blk * (int)R + g * 64;
         uint8_t* st = ring + slot * kMfmaStage;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)st, 16, la16, 16 * ob, 0, TMQ_CPOL_NT);
@@ -1217,12 +1228,13 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
                                                  0, TMQ_CPOL_NT);
     };
 #pragma unroll
-    for (int i = 0; i < D; i++) issue(i, i);
-    // this wave's part of the activation copy has landed and the constant
-    // bytes are written; the barrier makes every part visible (a plain
-    // s_barrier: the workgroup fence of __syncthreads would also wait for
-    // the ring's stages)
-    wait_vm<4 * D>();
+    for (int i = 0; i < D; i++)
+        if (i < nbw) issue(i, i);
+    // this wave's part of the activation copy (issued before the ring) has
+    // landed and the constant bytes are written; the barrier makes every
+    // part visible (a plain s_barrier: the workgroup fence of __syncthreads
+    // would also wait for the ring's stages)
+    wait_vm_k<4, D>(min(nbw, D));
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // this lane's A operand: rows 4q, 4q+1 the block's xh and xl - 128 over
@@ -1247,9 +1259,16 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     // the wave's block i from stage `slot`: decode, read out the previous
     // block's u sums (their MFMAs have long finished), then this block's
     // MFMAs into the same accumulator; the stage is refilled D blocks ahead
-    auto step = [&](int i, int slot) {
+    // while that block exists.  FULL: block i + D exists (the stages of
+    // blocks i+1 .. i+D-1 are in flight behind this one); otherwise the
+    // count of stages behind it is min(D - 1, nbw - 1 - i).
+    auto step = [&](int i, int slot, auto fullc) {
+        constexpr bool FULL = decltype(fullc)::value;
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm<4 * (D - 1)>();
+        if constexpr (FULL)
+            wait_vm<4 * (D - 1)>();
+        else
+            wait_vm_k<4, D - 1>(min(D - 1, nbw - 1 - i));
         const int b = wave + NW * i;
         const uint8_t* st = ring + slot * kMfmaStage;
         Q5Blk k;
@@ -1265,7 +1284,7 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
         const int xsv = *(li32*)(xsl + b);
         // the stage's reads are in registers before its refill overwrites it
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        issue(i + D, slot);
+        if (FULL || i + D < nbw) issue(i + D, slot);
         const IFit f = ifit_q5(k.d, ri256, k.e);
         uint32_t U[8], T[8];
 #pragma unroll
@@ -1288,13 +1307,13 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
         xp = xsv;
     };
     int ib = 0;
-    for (; ib + D <= nbw; ib += D) {
+    for (; ib + 2 * D <= nbw; ib += D) {
 #pragma unroll
-        for (int i = 0; i < D; i++) step(ib + i, i);
+        for (int i = 0; i < D; i++) step(ib + i, i, BoolC<true>{});
     }
 #pragma unroll
-    for (int i = 0; i < D; i++)
-        if (ib + i < nbw) step(ib + i, i);
+    for (int i = 0; i < 2 * D - 1; i++)
+        if (ib + i < nbw) step(ib + i, i % D, BoolC<false>{});
     acc += (int64_t)ap * (Cu[0] * 256 + Cu[1] + Cu[2] * 128) + (int64_t)bp * xp;
     acc += (int64_t)Ct[0] * 256 + Ct[1] + (int64_t)Ct[2] * 128;
     // no DMA into the ring may still run past this point
@@ -1422,7 +1441,6 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
     }
 
     uint8_t* ring = mfma_lds + wave * D * ST;
-    const int ilast = max(nuw - 1, 0);
     const int R = t.rows_pad, g64 = g * 64;
     // planes (the host keeps each below 2^31 bytes)
     const uint32_t pb = (uint32_t)R * (uint32_t)nb;  // (row, block) pairs
@@ -1431,10 +1449,10 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
     const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(FMT == kQ6_K ? t.pd : t.pb, 2 * pb);
     const __amdgpu_buffer_rsrc_t rsq = buf_rsrc(FMT == kQ6_K ? t.pq : t.pb, 208 * pb);
     const int l16 = lane * 16;
-    // stage `slot` <- the wave's quarter i (clamped: refills past the end
-    // reload the last quarter, so every step waits for the same count)
+    // stage `slot` <- the wave's quarter i, i < nuw (nothing is loaded past
+    // the wave's last quarter: every weight byte is read from memory once)
     auto issue = [&](int i, int slot) {
-        const int u = __builtin_amdgcn_readfirstlane(u0 + wave + NW * min(i, ilast));
+        const int u = __builtin_amdgcn_readfirstlane(u0 + wave + NW * i);
         const int b = u >> 2, q = u & 3;
         uint8_t* st = ring + slot * ST;
         if constexpr (FMT == kQ4_K) {
@@ -1459,12 +1477,13 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
         }
     };
 #pragma unroll
-    for (int i = 0; i < D; i++) issue(i, i);
-    // this wave's part of the activation copy has landed and the constant
-    // bytes are written; the barrier makes every part visible (a plain
-    // s_barrier: the workgroup fence of __syncthreads would also wait for
-    // the ring's stages)
-    wait_vm<ND * D>();
+    for (int i = 0; i < D; i++)
+        if (i < nuw) issue(i, i);
+    // this wave's part of the activation copy (issued before the ring) has
+    // landed and the constant bytes are written; the barrier makes every
+    // part visible (a plain s_barrier: the workgroup fence of __syncthreads
+    // would also wait for the ring's stages)
+    wait_vm_k<ND, D>(min(nuw, D));
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // this lane's A operand: rows 4q', 4q'+1 the sub-block's xh and
@@ -1511,9 +1530,14 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
     // the loop, compiled per header case (q < 2 or not; Q6_K: one case)
     auto run = [&](auto lo2c) {
         constexpr bool LO2 = decltype(lo2c)::value;
-        auto step = [&](int i, int slot) {
+        // FULL: quarter i + D exists (see group_mfma_q5's step)
+        auto step = [&](int i, int slot, auto fullc) {
+            constexpr bool FULL = decltype(fullc)::value;
             __builtin_amdgcn_sched_barrier(0);
-            wait_vm<ND * (D - 1)>();
+            if constexpr (FULL)
+                wait_vm<ND * (D - 1)>();
+            else
+                wait_vm_k<ND, D - 1>(min(D - 1, nuw - 1 - i));
             const int u = u0 + wave + NW * i, b = u >> 2, q = u & 3;
             const uint8_t* st = ring + slot * ST;
             IFit f[NS];
@@ -1532,7 +1556,7 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
                     xsv[k] = xsl[8 * b + 2 * q + k];
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                issue(i + D, slot);
+                if (FULL || i + D < nuw) issue(i + D, slot);
                 const uint32_t hx = (uint32_t)hv.x, hy = (uint32_t)hv.y, hz = (uint32_t)hv.z, hw = (uint32_t)hv.w;
                 const float dri = h2f(hx) * ri256, mri = h2f(hx >> 16) * ri256;
                 uint32_t scm;
@@ -1576,7 +1600,7 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
                     xsv[k] = xs16l[2 * (8 * b + 4 * h + k) + lc];
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                issue(i + D, slot);
+                if (FULL || i + D < nuw) issue(i + D, slot);
                 const float ssri = h2f(dbits) * ri256;
 #pragma unroll
                 for (int k = 0; k < NS; k++) {
@@ -1622,13 +1646,13 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
             }
         };
         int ib = 0;
-        for (; ib + D <= nuw; ib += D) {
+        for (; ib + 2 * D <= nuw; ib += D) {
 #pragma unroll
-            for (int i = 0; i < D; i++) step(ib + i, i);
+            for (int i = 0; i < D; i++) step(ib + i, i, BoolC<true>{});
         }
 #pragma unroll
-        for (int i = 0; i < D; i++)
-            if (ib + i < nuw) step(ib + i, i);
+        for (int i = 0; i < 2 * D - 1; i++)
+            if (ib + i < nuw) step(ib + i, i % D, BoolC<false>{});
     };
     if constexpr (FMT == kQ4_K) {
         if (qw < 2)
