@@ -125,6 +125,33 @@ def test_graphs_match_eager(model, golden):
     assert np.array_equal(res[0][2].view(np.uint32), res[1][2].view(np.uint32))
 
 
+def test_engine_mfma_decoders(ctx, golden, monkeypatch):
+    """TMQ_ENG_MFMA=1 at load puts the engine's Q5_0 / K-quant projections on
+    the int8 MFMA decoders (operand bytes written by the launch prologue,
+    K chunks of whole blocks / super-blocks, each chunk adding its own
+    columns' corrections): the reference's greedy tokens and the final hidden
+    state bit for bit, graph replays equal to eager launches."""
+    import tmq
+    from tmq import model_synth, tmacfile
+    monkeypatch.setenv("TMQ_ENG_MFMA", "1")
+    print("[model] synthetic C4 model on the MFMA decoders", flush=True)
+    blob = tmacfile.to_bytes(model_synth.gen_model(int(golden["model_seed"])))
+    m = tmq.Model(ctx, blob, max_seq=512)
+    del blob
+    try:
+        exp = golden["tokens"]
+        res = []
+        for graphs in (False, True):
+            m.set_graphs(graphs)
+            m.prompt(golden["prompt"])
+            got = m.generate(int(exp.size))
+            assert np.array_equal(got, exp), f"graphs {graphs}: first difference at {np.flatnonzero(got != exp)[:3]}"
+            res.append(m.hidden())
+            assert np.array_equal(res[-1].view(np.uint32), golden["hidden_final"].view(np.uint32))
+    finally:
+        m.free()
+
+
 def test_errors(model, golden):
     import tmq
     with pytest.raises(tmq.TmqError):

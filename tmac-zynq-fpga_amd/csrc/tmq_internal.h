@@ -282,11 +282,15 @@ int tmq_launch_chain(int fmt, int clamp, int max_cols, const TmqWork* works_dev,
 size_t tmq_gemv_lds_bytes(int fmt, int max_cols);
 // engine GEMV: activation recipe + works of any formats; waves = 16 or 4
 int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s);
+// the checks of tmq_launch_eng_gemv and the kernel's LDS opt-in, without a
+// launch (before stream capture)
+int tmq_prepare_eng_gemv(const TmqEngLaunch& l, int waves);
 // x = silu(g) * u over n rows of two K-split GEMVs; *max_bits = max over
 // the bits of |x| (atomic; zero before)
 int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x, uint32_t* max_bits,
                     hipStream_t s);
-size_t tmq_eng_lds_bytes(int n, int waves);
+// dynamic LDS of an engine launch whose works use kernel formats fa / fb
+size_t tmq_eng_lds_bytes(int n, int waves, int fa, int fb);
 // out[i] = x[i] + finalise(d, i), i < n
 int tmq_launch_resid_view(const float* x, const TmqDeferred& d, int n, float* out, hipStream_t s);
 // zero n int64 K-split accumulators

@@ -14,6 +14,8 @@
 // accumulates w*xh and w*xl pairs in int32 (|sum| < 2^28 per 32-weight
 // block), folded into int64 once per block.
 #include <hip/hip_runtime.h>
+#include <mutex>
+#include <set>
 
 #include <cstdlib>
 #include <type_traits>
@@ -1165,48 +1167,39 @@ __device__ __forceinline__ tmq_v4i mfma16(tmq_v4i a, tmq_v4i b, tmq_v4i c) {
 // stream global -> LDS through each wave's ring (LDS DMA: no registers hold
 // data in flight, and each wait is for the oldest stage alone); the
 // activation's operand bytes are copied into LDS once per workgroup.
-__device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
-    constexpr int NW = kMfmaWaves, D = TMQ_MFMA_DEPTH;
-    const TmqTensorDev& t = w.t;
+// The int64 sums of rows 64g .. 64g+63 over blocks [b0, b1): the NW waves
+// take blocks b0 + wave, b0 + wave + NW, ...  The caller lays out LDS:
+// xa / xsl the activation's operand bytes and block sums over the whole row
+// (with the constant runs at xa + 64 nb), ring NW * D stages, part (NW + 1)
+// * 64 int64.  ready(prime, nbw) must prime the ring (prime()), make xa and
+// xsl visible to every wave and leave no vector-memory operation of its own
+// outstanding behind the primed stages.  The corrections of the group whose
+// elements lie in columns [clo, chi) are added, xq(col) giving their
+// activation values.  STATIC_PRIME: the prime issues D stages whatever the
+// wave's block count (the surplus ones reload a block the wave or its
+// workgroup loads anyway), so that code around it sees a fixed number of
+// memory operations.  Returns the row's sum in wave 0 (after a workgroup
+// barrier; the other waves' values are meaningless).
+template <int NW, bool STATIC_PRIME = false, class Ready, class XQ>
+__device__ __forceinline__ int64_t mfma_q5_rows(const TmqTensorDev& t, int g, int b0, int b1, const uint8_t* xa,
+                                                const int32_t* xsl, uint8_t* ring0, int64_t* part, int clo, int chi,
+                                                Ready&& ready, XQ&& xq) {
+    constexpr int D = TMQ_MFMA_DEPTH;
     const int nb = t.nb;
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
-    const int nbw = (nb - wave + NW - 1) / NW;  // this wave's blocks (wave-uniform, >= 0)
+    const int nbw = max(0, (b1 - b0 - wave + NW - 1) / NW);  // this wave's blocks (wave-uniform)
     // corrections of the group (uniform), fetched first
-    const int c0 = t.corr_off ? t.corr_off[g] : 0, c1 = t.corr_off ? t.corr_off[g + 1] : 0;
+    const bool corr = t.corr_off && chi > clo;
+    const int c0 = corr ? t.corr_off[g] : 0, c1 = corr ? t.corr_off[g + 1] : 0;
     const float inv = t.row_inv[r], ri256 = inv * 256.0f;
-    const int n = t.cols;
-    uint8_t* xa = mfma_lds + mfma_xa_off();
-    int32_t* xsl = (int32_t*)(mfma_lds + mfma_xs_off(nb));
-    int64_t* part = (int64_t*)(mfma_lds + mfma_part_off(nb));
     int64_t* fix = part + NW * 64;
 
-    // the activation copy first (global -> LDS), so that waiting for it does
-    // not wait for the ring's stages
-    {
-        const uint8_t* src = w.act + tmq_act_xa(n);
-        const int n16 = nb * 4;
-        for (int i0 = wave * 64; i0 < n16; i0 += NW * 64)
-            if (i0 + lane < n16)
-                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
-                                                 16, 0, 0);
-        if (wave == NW - 1 && lane < kMfmaConst / 16) {
-            const uint32_t v = lane < kMfmaConst / 32 ? 0u : 0x01010101u;
-            *(uint4*)(xa + nb * 64 + lane * 16) = make_uint4(v, v, v, v);
-        }
-        const uint8_t* xs = w.act + tmq_act_xs(n);
-        for (int i0 = wave * 64; i0 < nb; i0 += NW * 64)
-            if (i0 + lane < nb)
-                __builtin_amdgcn_global_load_lds((const void*)(xs + (size_t)(i0 + lane) * 4),
-                                                 (lds_u8*)((uint8_t*)xsl + i0 * 4), 4, 0, 0);
-    }
-
-    uint8_t* ring = mfma_lds + wave * D * kMfmaStage;
+    uint8_t* ring = ring0 + wave * D * kMfmaStage;
     const size_t R = t.rows_pad;
     // stage `slot` <- the wave's block i, i < nbw (nothing is loaded past
     // the wave's last block: every weight byte is read from memory once;
-    // a wave with no block of its own (nb < NW) loads nothing).
+    // a wave with no block of its own loads nothing).
     // Buffer loads: the planes' base addresses and sizes in scalar resources,
     // the block's element offset (wave-uniform) in a scalar register and
     // the lane's in a constant vector register, so no vector instruction
@@ -1216,7 +1209,10 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     const __amdgpu_buffer_rsrc_t rsd = buf_rsrc(t.pd, 2 * pl), rsi = buf_rsrc(t.pi, 4 * (uint32_t)R * ((nb + 3) / 4));
     const int la16 = lane * 16, la4 = lane * 4, la2 = lane * 2;
     auto issue = [&](int i, int slot) {
-        const int blk = __builtin_amdgcn_readfirstlane(wave + NW * i);
+        // (i < nbw, but for a static prime's surplus stages: the wave's
+        // last block, or the range's first when it has none)
+        const int blk = __builtin_amdgcn_readfirstlane(
+            i < nbw ? b0 + wave + NW * i : nbw > 0 ? b0 + wave + NW * (nbw - 1) : min(b0, nb - 1));
         const int ob = blk * (int)R + g * 64;
         uint8_t* st = ring + slot * kMfmaStage;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_u8*)st, 16, la16, 16 * ob, 0, TMQ_CPOL_NT);
@@ -1227,15 +1223,13 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsi, (lds_u8*)(st + 1536), 4, la4, 4 * ((blk >> 2) * (int)R + g * 64),
                                                  0, TMQ_CPOL_NT);
     };
+    ready(
+        [&] {
 #pragma unroll
-    for (int i = 0; i < D; i++)
-        if (i < nbw) issue(i, i);
-    // this wave's part of the activation copy (issued before the ring) has
-    // landed and the constant bytes are written; the barrier makes every
-    // part visible (a plain s_barrier: the workgroup fence of __syncthreads
-    // would also wait for the ring's stages)
-    wait_vm_k<4, D>(min(nbw, D));
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            for (int i = 0; i < D; i++)
+                if (STATIC_PRIME || i < nbw) issue(i, i);
+        },
+        nbw);
 
     // this lane's A operand: rows 4q, 4q+1 the block's xh and xl - 128 over
     // K group q, row 4q+2 ones, the rest zero: block b's two halves at
@@ -1269,7 +1263,7 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
             wait_vm<4 * (D - 1)>();
         else
             wait_vm_k<4, D - 1>(min(D - 1, nbw - 1 - i));
-        const int b = wave + NW * i;
+        const int b = b0 + wave + NW * i;
         const uint8_t* st = ring + slot * kMfmaStage;
         Q5Blk k;
         {
@@ -1323,23 +1317,72 @@ __device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
     __syncthreads();
     if (c1 > c0) {
         // corrections (uniform branch): delta * sum of xq over their elements
-        const int32_t* x32 = (const int32_t*)(w.act + 16 + 6 * (size_t)n);
         for (int c = c0 + (int)threadIdx.x; c < c1; c += 64 * NW) {
             const uint4 e = t.corr[c];
+            // (a correction's elements lie in one block or sub-block)
+            if ((int)e.y < clo || (int)e.y >= chi) continue;
             int64_t s = 0;
-            for (uint32_t m = e.z; m; m &= m - 1) s += x32[e.y + __builtin_ctz(m)];
+            for (uint32_t m = e.z; m; m &= m - 1) s += xq((int)e.y + __builtin_ctz(m));
             atomicAdd((unsigned long long*)&fix[(int)e.x - g * 64], (unsigned long long)((int64_t)(int32_t)e.w * s));
         }
         __syncthreads();
     }
-    if (wave == 0 && r < t.rows) {
-        int64_t tot = fix[lane];
+    int64_t tot = 0;
+    if (wave == 0) {
+        tot = fix[lane];
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += part[i * 64 + lane];
+    }
+    return tot;
+}
+
+// A standalone / chain row group: the activation's operand bytes copied
+// from the prepared activation (global -> LDS), every block of the row.
+__device__ __forceinline__ void group_mfma_q5(const TmqWork& w, int g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
+    constexpr int NW = kMfmaWaves, D = TMQ_MFMA_DEPTH;
+    const TmqTensorDev& t = w.t;
+    const int nb = t.nb, n = t.cols;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    uint8_t* xa = mfma_lds + mfma_xa_off();
+    int32_t* xsl = (int32_t*)(mfma_lds + mfma_xs_off(nb));
+    int64_t* part = (int64_t*)(mfma_lds + mfma_part_off(nb));
+    // the finalisation's operands, loaded at the start (not behind the sums)
+    const float inv = t.row_inv[r], xsc = *(const float*)w.act;
+    auto ready = [&](auto&& prime, int nbw) {
+        // the activation copy first (global -> LDS), so that waiting for it
+        // does not wait for the ring's stages
+        const uint8_t* src = w.act + tmq_act_xa(n);
+        const int n16 = nb * 4;
+        for (int i0 = wave * 64; i0 < n16; i0 += NW * 64)
+            if (i0 + lane < n16)
+                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
+                                                 16, 0, 0);
+        if (wave == NW - 1 && lane < kMfmaConst / 16) {
+            const uint32_t v = lane < kMfmaConst / 32 ? 0u : 0x01010101u;
+            *(uint4*)(xa + nb * 64 + lane * 16) = make_uint4(v, v, v, v);
+        }
+        const uint8_t* xs = w.act + tmq_act_xs(n);
+        for (int i0 = wave * 64; i0 < nb; i0 += NW * 64)
+            if (i0 + lane < nb)
+                __builtin_amdgcn_global_load_lds((const void*)(xs + (size_t)(i0 + lane) * 4),
+                                                 (lds_u8*)((uint8_t*)xsl + i0 * 4), 4, 0, 0);
+        prime();
+        // this wave's part of the activation copy (issued before the ring)
+        // has landed and the constant bytes are written; the barrier makes
+        // every part visible (a plain s_barrier: the workgroup fence of
+        // __syncthreads would also wait for the ring's stages)
+        wait_vm_k<4, D>(min(nbw, D));
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    const int32_t* x32 = (const int32_t*)(w.act + 16 + 6 * (size_t)n);
+    const int64_t tot = mfma_q5_rows<NW>(t, g, 0, nb, xa, xsl, mfma_lds, part, 0, n, ready,
+                                         [&](int col) { return x32[col]; });
+    if (wave == 0 && r < t.rows) {
         if (w.acc) w.acc[r] = tot;
         // sim/tmac_gguf.cpp:1303-1305: y = 0.0f; y += (double)acc*x_scale/(double)row_inv
-        const float xs = *(const float*)w.act;
-        if (w.y) store_y(w, r, (float)(((double)tot * (double)xs) / (double)inv));
+        if (w.y) store_y(w, r, (float)(((double)tot * (double)xsc) / (double)inv));
     }
 }
 
@@ -1383,17 +1426,18 @@ template <int FMT> __host__ __device__ constexpr int kq_lds_bytes(int nbx) {
     return kq_part_off<FMT>(nbx) + (kKqWaves + 1) * 64 * 8;
 }
 
-// Row group g over super-blocks [b0, b1) of its rows.  pieces > 1: one of
-// the workgroups sharing the group, which meet in tail slot `slot` (a
-// TmqGroupRef split; the first piece adds the corrections).
-template <int FMT>
-__device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, int b1, int slot, int pieces,
-                                              uint64_t* tail) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
+// The int64 sums of rows 64g .. 64g+63 over super-blocks [b0, b1) (b1 > b0)
+// on the K-quant MFMA decoder, with LDS laid out by the caller as for
+// mfma_q5_rows (xs16l: Q6_K's 16-element sums; part (NW + 1) * 64 int64;
+// ring NW * D stages; xa's constant runs kKqConst bytes at xa + 64 * 8nb)
+// and the same ready / corr / xq contract.  Returns the rows' sums in wave 0.
+template <int FMT, bool STATIC_PRIME = false, class Ready, class XQ>
+__device__ __forceinline__ int64_t mfma_kq_rows(const TmqTensorDev& t, int g, int b0, int b1, const uint8_t* xa,
+                                                const int32_t* xsl, const int32_t* xs16l, uint8_t* ring0,
+                                                int64_t* part, int clo, int chi, Ready&& ready, XQ&& xq) {
     constexpr int NW = kKqWaves, D = TMQ_MFMA_DEPTH, ST = kq_stage<FMT>(), ND = kq_ndma<FMT>();
     constexpr int NS = FMT == kQ4_K ? 2 : 4;  // sub-blocks per quarter
-    const TmqTensorDev& t = w.t;
-    const int nb = t.nb, nbx = nb * 8, n = t.cols;
+    const int nb = t.nb, nbx = nb * 8;
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = g * 64 + lane;
     // quarter u = 4b + q of the row; wave w takes quarters u0 + w + NW*i:
@@ -1401,46 +1445,12 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
     // super-block), b1 - b0 >= 1 of them
     const int u0 = 4 * b0;
     const int nuw = b1 - b0;
-    const bool corr = t.corr_off && b0 == 0;
+    const bool corr = t.corr_off && chi > clo;
     const int c0 = corr ? t.corr_off[g] : 0, c1 = corr ? t.corr_off[g + 1] : 0;
     const float inv = t.row_inv[r], ri256 = inv * 256.0f;
-    uint8_t* xa = mfma_lds + kq_xa_off<FMT>();
-    int32_t* xsl = (int32_t*)(mfma_lds + kq_xs_off<FMT>(nbx));
-    int32_t* xs16l = (int32_t*)(mfma_lds + kq_xs16_off<FMT>(nbx));
-    int64_t* part = (int64_t*)(mfma_lds + kq_part_off<FMT>(nbx));
     int64_t* fix = part + NW * 64;
 
-    // the activation copy first (global -> LDS), so that waiting for it does
-    // not wait for the ring's stages: the range's 16-byte chunks (32 a
-    // super-block) and block sums, at their offsets in the whole row, and
-    // the two chunks of zeros and ones behind the row
-    {
-        const uint8_t* src = w.act + tmq_act_xa(n);
-        const int a0 = 32 * b0, a1 = 32 * b1;
-        for (int i0 = a0 + wave * 64; i0 < a1; i0 += NW * 64)
-            if (i0 + lane < a1)
-                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
-                                                 16, 0, 0);
-        if (wave == NW - 1 && lane < kKqConst / 16) {
-            const uint32_t v = lane < kKqConst / 32 ? 0u : 0x01010101u;
-            *(uint4*)(xa + nbx * 64 + lane * 16) = make_uint4(v, v, v, v);
-        }
-        const uint8_t* xs = w.act + tmq_act_xs(n);
-        const int s0 = 8 * b0, s1 = 8 * b1;
-        for (int i0 = s0 + wave * 64; i0 < s1; i0 += NW * 64)
-            if (i0 + lane < s1)
-                __builtin_amdgcn_global_load_lds((const void*)(xs + (size_t)(i0 + lane) * 4),
-                                                 (lds_u8*)((uint8_t*)xsl + i0 * 4), 4, 0, 0);
-        if constexpr (FMT == kQ6_K) {
-            const uint8_t* x16 = w.act + tmq_act_xs16(n);
-            for (int i0 = 2 * s0 + wave * 64; i0 < 2 * s1; i0 += NW * 64)
-                if (i0 + lane < 2 * s1)
-                    __builtin_amdgcn_global_load_lds((const void*)(x16 + (size_t)(i0 + lane) * 4),
-                                                     (lds_u8*)((uint8_t*)xs16l + i0 * 4), 4, 0, 0);
-        }
-    }
-
-    uint8_t* ring = mfma_lds + wave * D * ST;
+    uint8_t* ring = ring0 + wave * D * ST;
     const int R = t.rows_pad, g64 = g * 64;
     // planes (the host keeps each below 2^31 bytes)
     const uint32_t pb = (uint32_t)R * (uint32_t)nb;  // (row, block) pairs
@@ -1452,7 +1462,11 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
     // stage `slot` <- the wave's quarter i, i < nuw (nothing is loaded past
     // the wave's last quarter: every weight byte is read from memory once)
     auto issue = [&](int i, int slot) {
-        const int u = __builtin_amdgcn_readfirstlane(u0 + wave + NW * i);
+        // (i < nuw, but for a static prime's surplus stages: the last
+        // quarter, or the row's first super-block's when the range is empty)
+        const int u = __builtin_amdgcn_readfirstlane(i < nuw ? u0 + wave + NW * i
+                                                     : nuw > 0 ? u0 + wave + NW * (nuw - 1)
+                                                               : 4 * min(b0, nb - 1) + wave);
         const int b = u >> 2, q = u & 3;
         uint8_t* st = ring + slot * ST;
         if constexpr (FMT == kQ4_K) {
@@ -1476,15 +1490,13 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
                                                      0, TMQ_CPOL_NT);
         }
     };
+    ready(
+        [&] {
 #pragma unroll
-    for (int i = 0; i < D; i++)
-        if (i < nuw) issue(i, i);
-    // this wave's part of the activation copy (issued before the ring) has
-    // landed and the constant bytes are written; the barrier makes every
-    // part visible (a plain s_barrier: the workgroup fence of __syncthreads
-    // would also wait for the ring's stages)
-    wait_vm_k<ND, D>(min(nuw, D));
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            for (int i = 0; i < D; i++)
+                if (STATIC_PRIME || i < nuw) issue(i, i);
+        },
+        nuw);
 
     // this lane's A operand: rows 4q', 4q'+1 the sub-block's xh and
     // xl - 128 over K group q' (lane >> 4), row 4q'+2 ones, the rest zero;
@@ -1673,19 +1685,83 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
     __syncthreads();
     if (c1 > c0) {
         // corrections (uniform branch): delta * sum of xq over their elements
-        const int32_t* x32 = (const int32_t*)(w.act + 16 + 6 * (size_t)n);
         for (int c = c0 + (int)threadIdx.x; c < c1; c += 64 * NW) {
             const uint4 e = t.corr[c];
+            // (a correction's elements lie in one block or sub-block)
+            if ((int)e.y < clo || (int)e.y >= chi) continue;
             int64_t s = 0;
-            for (uint32_t m = e.z; m; m &= m - 1) s += x32[e.y + __builtin_ctz(m)];
+            for (uint32_t m = e.z; m; m &= m - 1) s += xq((int)e.y + __builtin_ctz(m));
             atomicAdd((unsigned long long*)&fix[(int)e.x - g * 64], (unsigned long long)((int64_t)(int32_t)e.w * s));
         }
         __syncthreads();
     }
-    if (wave != 0) return;
-    int64_t tot = fix[lane];
+    int64_t tot = 0;
+    if (wave == 0) {
+        tot = fix[lane];
 #pragma unroll
-    for (int i = 0; i < NW; i++) tot += part[i * 64 + lane];
+        for (int i = 0; i < NW; i++) tot += part[i * 64 + lane];
+    }
+    return tot;
+}
+
+// A standalone / chain row group over super-blocks [b0, b1).  pieces > 1:
+// one of the workgroups sharing the group, which meet in tail slot `slot`
+// (a TmqGroupRef split; each piece adds the corrections of its columns).
+template <int FMT>
+__device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, int b1, int slot, int pieces,
+                                              uint64_t* tail) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mfma_lds[];
+    constexpr int NW = kKqWaves, D = TMQ_MFMA_DEPTH, ND = kq_ndma<FMT>();
+    const TmqTensorDev& t = w.t;
+    const int nb = t.nb, nbx = nb * 8, n = t.cols;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    uint8_t* xa = mfma_lds + kq_xa_off<FMT>();
+    int32_t* xsl = (int32_t*)(mfma_lds + kq_xs_off<FMT>(nbx));
+    int32_t* xs16l = (int32_t*)(mfma_lds + kq_xs16_off<FMT>(nbx));
+    int64_t* part = (int64_t*)(mfma_lds + kq_part_off<FMT>(nbx));
+    // the finalisation's operands, loaded at the start (not behind the sums)
+    const float inv = t.row_inv[r], xsc = *(const float*)w.act;
+    auto ready = [&](auto&& prime, int nuw) {
+        // the activation copy first (global -> LDS), so that waiting for it
+        // does not wait for the ring's stages: the range's 16-byte chunks
+        // (32 a super-block) and block sums, at their offsets in the whole
+        // row, and the runs of zeros and ones behind the row
+        const uint8_t* src = w.act + tmq_act_xa(n);
+        const int a0 = 32 * b0, a1 = 32 * b1;
+        for (int i0 = a0 + wave * 64; i0 < a1; i0 += NW * 64)
+            if (i0 + lane < a1)
+                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i0 + lane) * 16), (lds_u8*)(xa + i0 * 16),
+                                                 16, 0, 0);
+        if (wave == NW - 1 && lane < kKqConst / 16) {
+            const uint32_t v = lane < kKqConst / 32 ? 0u : 0x01010101u;
+            *(uint4*)(xa + nbx * 64 + lane * 16) = make_uint4(v, v, v, v);
+        }
+        const uint8_t* xs = w.act + tmq_act_xs(n);
+        const int s0 = 8 * b0, s1 = 8 * b1;
+        for (int i0 = s0 + wave * 64; i0 < s1; i0 += NW * 64)
+            if (i0 + lane < s1)
+                __builtin_amdgcn_global_load_lds((const void*)(xs + (size_t)(i0 + lane) * 4),
+                                                 (lds_u8*)((uint8_t*)xsl + i0 * 4), 4, 0, 0);
+        if constexpr (FMT == kQ6_K) {
+            const uint8_t* x16 = w.act + tmq_act_xs16(n);
+            for (int i0 = 2 * s0 + wave * 64; i0 < 2 * s1; i0 += NW * 64)
+                if (i0 + lane < 2 * s1)
+                    __builtin_amdgcn_global_load_lds((const void*)(x16 + (size_t)(i0 + lane) * 4),
+                                                     (lds_u8*)((uint8_t*)xs16l + i0 * 4), 4, 0, 0);
+        }
+        prime();
+        // this wave's part of the activation copy (issued before the ring)
+        // has landed and the constant bytes are written; the barrier makes
+        // every part visible (a plain s_barrier: the workgroup fence of
+        // __syncthreads would also wait for the ring's stages)
+        wait_vm_k<ND, D>(min(nuw, D));
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    const int32_t* x32 = (const int32_t*)(w.act + 16 + 6 * (size_t)n);
+    int64_t tot = mfma_kq_rows<FMT>(t, g, b0, b1, xa, xsl, xs16l, mfma_lds, part, 256 * b0, 256 * b1, ready,
+                                    [&](int col) { return x32[col]; });
+    if (wave != 0) return;
     if (pieces > 1) {
         // The pieces' row sums meet through device-scope atomics, which
         // every XCD performs at the same coherence point: each piece adds
@@ -1710,8 +1786,7 @@ __device__ __forceinline__ void group_mfma_kq(const TmqWork& w, int g, int b0, i
         if (w.acc) w.acc[r] = tot;
         // sim/tmac_gguf.cpp:1192-1194 (Q4_K), :1501-1503 (Q6_K):
         // y = (float)((double)acc*x_scale/(double)row_inv)
-        const float xs = *(const float*)w.act;
-        if (w.y) store_y(w, r, (float)(((double)tot * (double)xs) / (double)inv));
+        if (w.y) store_y(w, r, (float)(((double)tot * (double)xsc) / (double)inv));
     }
 }
 
@@ -2007,8 +2082,13 @@ __device__ float tensor_elem(const TmqTensorDev& t, int r, int j) {
 }
 
 // LDS carve-up of an engine workgroup: x[n] fp32 | xh[n/2] xl[n/2] (the
-// squares of RMSNorm alias xh/xl before the quantisation) | part[NW*64] int64
-// | red[64] | spec[16*64] spec_c[16] (the norm's segmented sum)
+// squares of RMSNorm alias xh/xl before the quantisation) | part[(NW+1)*64]
+// int64 | red[64] | spec[16*64] spec_c[16] (the norm's segmented sum) | the
+// MFMA decoders' weight ring (ring bytes, 16-aligned).  An MFMA format's
+// activation operand bytes (64 a 32-column block, then 512 bytes of
+// constant runs), block sums (n/32 int32) and 16-column sums (n/16 int32)
+// take the place of xh/xl where they fit (eng_mx_bytes <= 4n), else follow
+// the ring.
 struct EngLds {
     float* x;
     uint32_t* xh;
@@ -2017,16 +2097,30 @@ struct EngLds {
     float* red;
     float* spec;
     int* spec_c;
+    uint8_t* ring;
+    uint8_t* mxa;
+    int32_t* mxs;
+    int32_t* mxs16;
 };
-__device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw) {
+__host__ __device__ constexpr size_t eng_base_bytes(int n, int nw) {
+    return (8 * (size_t)n + 8 * 64 * ((size_t)nw + 1) + 256 + 4 * (16 * 64 + 16) + 15) & ~(size_t)15;
+}
+__host__ __device__ constexpr size_t eng_mx_bytes(int n) {
+    return 2 * (size_t)n + 512 + (size_t)n / 8 + (size_t)n / 4;
+}
+__device__ __forceinline__ EngLds eng_lds(unsigned char* base, int n, int nw, size_t ring_bytes) {
     EngLds L;
     L.x = (float*)base;
     L.xh = (uint32_t*)(base + 4 * (size_t)n);
     L.xl = L.xh + n / 2;
     L.part = (int64_t*)(base + 8 * (size_t)n);
-    L.red = (float*)(L.part + nw * 64);
+    L.red = (float*)(L.part + (nw + 1) * 64);
     L.spec = L.red + 64;
     L.spec_c = (int*)(L.spec + 16 * 64);
+    L.ring = base + eng_base_bytes(n, nw);
+    L.mxa = eng_mx_bytes(n) <= 4 * (size_t)n ? (uint8_t*)L.xh : L.ring + ring_bytes;
+    L.mxs = (int32_t*)(L.mxa + 2 * (size_t)n + 512);
+    L.mxs16 = L.mxs + n / 32;
     return L;
 }
 
@@ -2218,7 +2312,10 @@ __device__ __forceinline__ float seq_sum_spec(const float* v, int n, float* scr,
 // save.)
 template <int NW, int FMT, bool MULTI = false>
 constexpr int eng_norm_segs() { return NW < 16 || MULTI || FMT == kQ6_K ? 4 : 8; }
-template <int NW, int SEGS, class Pre>
+// MX: 0 quantises columns [c0, c1) into xh/xl; an MFMA format (kQ5_0M,
+// kQ4_KM, kQ6_KM) into that decoder's operand bytes and sums (mxa, mxs,
+// mxs16) with its constant runs ([c0, c1) whole 32-column blocks).
+template <int NW, int SEGS, int MX = 0, class Pre>
 __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& L, int c0, int c1, Pre&& pre) {
     constexpr int EP = NW >= 16 ? 1 : 4;
     const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
@@ -2337,16 +2434,50 @@ __device__ __forceinline__ float eng_prologue(const TmqEngAct& a, const EngLds& 
     for (int i = 0; i < (int)(nt >> 6); i++) mm = fmaxf(mm, L.red[2 + i]);
     if (norm) mm = mm * s;
     const float xs = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
-    for (int k = (c0 >> 1) + tid; k < (c1 >> 1); k += nt) {
-        float u = L.x[2 * k], v = L.x[2 * k + 1];
-        if (norm) {
-            u = u * s;
-            v = v * s;
+    if constexpr (MX != 0) {
+        // element i: xh byte at 64*(i/32) + 32*(i/16 % 2) + i%16, xl - 128
+        // 16 bytes on; the sums of 16 and 32 consecutive elements from the
+        // lanes of one 16-lane row and of two (c0, c1 and every 64-element
+        // step being whole blocks, a row's lanes are all inside or all
+        // outside [c0, c1))
+        uint8_t* xa = L.mxa;
+        for (int base = c0; base < c1; base += nt) {
+            const int i = base + tid;
+            int p = 0;
+            if (i < c1) {
+                float u = L.x[i];
+                if (norm) u = u * s;
+                p = (int)(int16_t)roundf(u / xs);
+                const int o = 64 * (i >> 5) + 32 * ((i >> 4) & 1) + (i & 15);
+                xa[o] = (uint8_t)(p >> 8);
+                xa[o + 16] = (uint8_t)((p & 255) ^ 128);
+            }
+            const int s16 = tmq_row_sum(p);
+            const int s32 = s16 + __shfl_xor(s16, 16);
+            if (i < c1) {
+                if (MX == kQ6_KM && (tid & 15) == 0) L.mxs16[i >> 4] = s16;
+                if ((tid & 31) == 0) L.mxs[i >> 5] = s32;
+            }
         }
-        const int p = (int)(int16_t)roundf(u / xs);
-        const int q = (int)(int16_t)roundf(v / xs);
-        L.xh[k] = ((uint32_t)(p >> 8) & 0xffffu) | ((uint32_t)(q >> 8) << 16);
-        L.xl[k] = ((uint32_t)p & 0xffu) | (((uint32_t)q & 0xffu) << 16);
+        // the constant runs behind the row: zeros then ones, 64 bytes each
+        // (Q5_0 decoder) or 256 (K-quants)
+        constexpr int CR = MX == kQ5_0M ? 64 : 256;
+        if (tid < CR / 8) {
+            const uint32_t v = tid < CR / 16 ? 0u : 0x01010101u;
+            *(uint4*)(xa + 64 * (n >> 5) + 16 * tid) = make_uint4(v, v, v, v);
+        }
+    } else {
+        for (int k = (c0 >> 1) + tid; k < (c1 >> 1); k += nt) {
+            float u = L.x[2 * k], v = L.x[2 * k + 1];
+            if (norm) {
+                u = u * s;
+                v = v * s;
+            }
+            const int p = (int)(int16_t)roundf(u / xs);
+            const int q = (int)(int16_t)roundf(v / xs);
+            L.xh[k] = ((uint32_t)(p >> 8) & 0xffffu) | ((uint32_t)(q >> 8) << 16);
+            L.xl[k] = ((uint32_t)p & 0xffu) | (((uint32_t)q & 0xffu) << 16);
+        }
     }
     __syncthreads();
     return xs;
@@ -2423,6 +2554,75 @@ __device__ __forceinline__ void eng_group_k(const TmqEngAct& a, const EngLds& L,
         int64_t tot = 0;
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += L.part[i * 64 + lane];
+        if (w.kacc) {
+            __hip_atomic_fetch_add(w.kacc + r, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            if (w.acc) w.acc[r] = tot;
+            if (w.y) store_y(w, r, (float)(((double)tot * (double)xs) / (double)inv));
+        }
+    }
+}
+
+// Weight-ring bytes of an engine launch's MFMA format (0: not an MFMA format)
+__host__ __device__ constexpr size_t eng_ring_bytes(int fmt, int nw) {
+    return fmt == kQ5_0M   ? (size_t)nw * TMQ_MFMA_DEPTH * kMfmaStage
+           : fmt == kQ4_KM ? (size_t)kKqWaves * TMQ_MFMA_DEPTH * kq_stage<kQ4_K>()
+           : fmt == kQ6_KM ? (size_t)kKqWaves * TMQ_MFMA_DEPTH * kq_stage<kQ6_K>()
+                           : 0;
+}
+
+// Q5_0 / K-quant row group g, K chunk c on the MFMA decoders: chunk c of kc
+// takes blocks (Q5_0) or super-blocks (K-quants) [c*nb/kc, (c+1)*nb/kc),
+// whose columns the prologue quantises into the decoder's operand bytes
+// while the ring's first stages load; the chunk adds the corrections of its
+// own columns.  The int64 row sums go where eng_group_k sends them.
+template <int FMT, int NW, bool MULTI>
+__device__ __forceinline__ void eng_group_mfma(const TmqEngAct& a, const EngLds& L, const TmqWork& w, int gi) {
+    const TmqTensorDev& t = w.t;
+    const int kc = w.kc, g = gi / kc, c = gi - g * kc;
+    const int nb = t.nb, b0 = c * nb / kc, b1 = (c + 1) * nb / kc;
+    constexpr int QK = FMT == kQ5_0M ? 32 : 256;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int r = g * 64 + lane;
+    const float inv = t.row_inv[r];
+    float xs = 1.0f;
+    // the prologue runs the prime between its loads and their use; after
+    // it the stages have long landed (the wait also covers the prologue's
+    // own stores), so the loop starts with no operation in flight
+    auto ready = [&](auto&& prime, int) {
+        xs = eng_prologue<NW, eng_norm_segs<NW, FMT, MULTI>(), FMT>(a, L, b0 * QK, b1 * QK, prime);
+        wait_vm<0>();
+    };
+    // a correction's activation value from the operand bytes
+    auto xq = [&](int col) {
+        const int o = 64 * (col >> 5) + 32 * ((col >> 4) & 1) + (col & 15);
+        return (int)(int8_t)L.mxa[o] * 256 + (int)(L.mxa[o + 16] ^ 128u);
+    };
+    int64_t tot;
+    if constexpr (FMT == kQ5_0M)
+        tot = mfma_q5_rows<NW, true>(t, g, b0, b1, L.mxa, L.mxs, L.ring, L.part, b0 * QK, b1 * QK, ready, xq);
+    else
+        tot = mfma_kq_rows<FMT == kQ4_KM ? kQ4_K : kQ6_K, true>(t, g, b0, b1, L.mxa, L.mxs, L.mxs16, L.ring, L.part,
+                                                               b0 * QK, b1 * QK, ready, xq);
+    if (w.xs_out && gi == 0 && threadIdx.x == 0) *w.xs_out = xs;
+    if (wave != 0) return;
+    if (w.silu) {
+        // fused SwiGLU, as eng_group_k
+        const float f = (float)(((double)tot * (double)xs) / (double)inv);
+        const float up = __shfl_down(f, 32);
+        float m = __int_as_float(0x7fc00000);  // lanes 32-63: fmaxf's identity
+        if (lane < 32) {
+            const float v = (f / (1.0f + tmq_math::tmq_expf(-f))) * up;
+            w.silu[g * 32 + lane] = v;
+            m = fabsf(v);
+        }
+        m = tmq_wave_max(m);
+        if (lane == 0)
+            __hip_atomic_store(w.silu_max + g, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (r < t.rows) {
         if (w.kacc) {
             __hip_atomic_fetch_add(w.kacc + r, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
@@ -2615,6 +2815,7 @@ __device__ __forceinline__ void eng_dispatch(const TmqEngAct& a, const EngLds& L
     else if constexpr (FMT == kI16) eng_group_i16_split<NW, MULTI>(a, L, w, g);
     else if constexpr (FMT == kI16_DIRECT) eng_group_i16<NW>(a, L, w, g);
     else if constexpr (FMT == kF32P) eng_group_f32<NW, MULTI>(a, L, w, g);
+    else if constexpr (FMT == kQ5_0M || FMT == kQ4_KM || FMT == kQ6_KM) eng_group_mfma<FMT, NW, MULTI>(a, L, w, g);
     else eng_group_k<FMT, NW, MULTI>(a, L, w, g);
 }
 
@@ -2633,7 +2834,9 @@ __global__ __launch_bounds__(NW * 64) void eng_gemv_kernel(TmqEngLaunch P) {
         return;
     }
     extern __shared__ __attribute__((aligned(16))) unsigned char eng_smem[];
-    const EngLds L = eng_lds(eng_smem, P.act.n, NW);
+    constexpr size_t RB = eng_ring_bytes(FA, NW) > eng_ring_bytes(FB, NW) ? eng_ring_bytes(FA, NW)
+                                                                          : eng_ring_bytes(FB, NW);
+    const EngLds L = eng_lds(eng_smem, P.act.n, NW, RB);
     if constexpr (!MULTI) {
         // one work: every launch parameter sits at a fixed kernarg offset,
         // so all of them come in the first batch of scalar loads
@@ -3584,13 +3787,24 @@ int tmq_launch_zero_acc(int64_t* p, size_t n, hipStream_t s) {
     return (int)hipGetLastError();
 }
 
-size_t tmq_eng_lds_bytes(int n, int waves) { return 8 * (size_t)n + 8 * 64 * (size_t)waves + 256 + 4 * (16 * 64 + 16); }
+size_t tmq_eng_lds_bytes(int n, int waves, int fa, int fb) {
+    const size_t rb = std::max(eng_ring_bytes(fa, waves), eng_ring_bytes(fb, waves));
+    const bool mx = fa == kQ5_0M || fa == kQ4_KM || fa == kQ6_KM || fb == kQ5_0M || fb == kQ4_KM || fb == kQ6_KM;
+    return eng_base_bytes(n, waves) + rb + (mx && eng_mx_bytes(n) > 4 * (size_t)n ? eng_mx_bytes(n) : 0);
+}
 
 template <int NW, bool MULTI>
 static void* eng_kernel_for(int fa, int fb) {
 #define TMQ_ENG_K(A, B) (void*)eng_gemv_kernel<NW, A, B, MULTI>
     if (fa == kQ5_0 && fb == kQ5_0) return TMQ_ENG_K(kQ5_0, kQ5_0);
     if (fa == kQ5_0 && fb == kQ8_0) return TMQ_ENG_K(kQ5_0, kQ8_0);
+    if (fa == kQ5_0M && fb == kQ5_0M) return TMQ_ENG_K(kQ5_0M, kQ5_0M);
+    if (fa == kQ5_0M && fb == kQ8_0) return TMQ_ENG_K(kQ5_0M, kQ8_0);
+    if constexpr (NW == 4) {
+        // the K-quant MFMA decoders take a quarter super-block per wave
+        if (fa == kQ4_KM && fb == kQ4_KM) return TMQ_ENG_K(kQ4_KM, kQ4_KM);
+        if (fa == kQ6_KM && fb == kQ6_KM) return TMQ_ENG_K(kQ6_KM, kQ6_KM);
+    }
     if (fa == kQ4_K && fb == kQ4_K) return TMQ_ENG_K(kQ4_K, kQ4_K);
     if (fa == kQ6_K && fb == kQ6_K) return TMQ_ENG_K(kQ6_K, kQ6_K);
     if (fa == kQ8_0 && fb == kQ8_0) return TMQ_ENG_K(kQ8_0, kQ8_0);
@@ -3610,15 +3824,18 @@ static void* eng_kernel_for(int fa, int fb) {
     return nullptr;
 }
 
-int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
-    if (l.ngroups <= 0) return 0;
+// The kernel and dynamic LDS of an engine launch (checks its shape); the
+// kernel opted into its LDS when that is above 64 KiB.
+static int eng_resolve(const TmqEngLaunch& l, int waves, void** kernel, size_t* lds) {
     if (l.act.n <= 0 || l.act.n > TMQ_ENG_MAXN || l.act.n % 2 || l.nworks < 1 || l.nworks > TMQ_ENG_MAXW)
         return (int)hipErrorInvalidValue;
     // format of the first and the last work (the others must match the first)
     auto code = [](const TmqWork& w) {
         if (w.path == TMQ_WPATH_INT16) return w.kacc ? kI16 : kI16_DIRECT;
         if (w.path == TMQ_WPATH_FP32) return kF32P;
-        return w.t.type == kQ8_0 && !w.kacc ? kQ8_DIRECT : w.t.type;
+        if (w.t.type == kQ8_0) return w.kacc ? kQ8_0 : kQ8_DIRECT;
+        // the MFMA decoders where the tensor carries their planes
+        return tmq_kernel_fmt(w.t);
     };
     const int fa = code(l.w[0]), fb = code(l.w[l.nworks - 1]);
     for (int i = 1; i + 1 < l.nworks; i++)
@@ -3627,6 +3844,12 @@ int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
     for (int i = 0; i < l.nworks; i++) {
         if ((int64_t)l.w[i].t.nb * 4 * (l.w[i].kc > 0 ? l.w[i].kc : 1) >= ((int64_t)1 << 31))
             return (int)hipErrorInvalidValue;
+        // MFMA chunks are whole blocks / super-blocks of a row of at most
+        // TMQ_MFMA_MAX_COLS columns, the activation's width
+        const int f = code(l.w[i]);
+        if ((f == kQ5_0M || f == kQ4_KM || f == kQ6_KM) &&
+            (l.w[i].kc < 1 || l.w[i].kc > l.w[i].t.nb || l.w[i].t.cols != l.act.n || l.act.n % 32))
+            return (int)hipErrorInvalidValue;
         if (l.w[i].path == TMQ_WPATH_INT16 && (!l.w[i].t.pw || !l.w[i].t.rs16)) return (int)hipErrorInvalidValue;
         if (l.w[i].path == TMQ_WPATH_FP32 && l.w[i].t.cols != l.act.n) return (int)hipErrorInvalidValue;
     }
@@ -3634,11 +3857,38 @@ int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
     if (l.nworks > 1) k = waves == 16 ? eng_kernel_for<16, true>(fa, fb) : waves == 4 ? eng_kernel_for<4, true>(fa, fb) : nullptr;
     else k = waves == 16 ? eng_kernel_for<16, false>(fa, fb) : waves == 4 ? eng_kernel_for<4, false>(fa, fb) : nullptr;
     if (!k) return (int)hipErrorInvalidValue;
+    if (l.rope_out && (!l.rope_src || !l.rope_state || l.rope_max_pos < 1)) return (int)hipErrorInvalidValue;
+    *lds = tmq_eng_lds_bytes(l.act.n, waves, fa, fb);
+    *kernel = k;
+    if (*lds > 64 * 1024) {
+        // (once per kernel: dynamic LDS above 64 KiB is opted into)
+        static std::mutex mu;
+        static std::set<void*> done;
+        std::lock_guard<std::mutex> lk(mu);
+        if (!done.count(k)) {
+            hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            if (e != hipSuccess) return (int)e;
+            done.insert(k);
+        }
+    }
+    return 0;
+}
+
+int tmq_prepare_eng_gemv(const TmqEngLaunch& l, int waves) {
+    void* k = nullptr;
+    size_t lds = 0;
+    return eng_resolve(l, waves, &k, &lds);
+}
+
+int tmq_launch_eng_gemv(const TmqEngLaunch& l, int waves, hipStream_t s) {
+    if (l.ngroups <= 0) return 0;
+    void* k = nullptr;
+    size_t lds = 0;
+    const int rc = eng_resolve(l, waves, &k, &lds);
+    if (rc) return rc;
     TmqEngLaunch arg = l;
     void* args[] = {&arg};
-    if (l.rope_out && (!l.rope_src || !l.rope_state || l.rope_max_pos < 1)) return (int)hipErrorInvalidValue;
-    return (int)hipLaunchKernel(k, dim3(l.ngroups + (l.rope_out ? 1 : 0)), dim3(64 * waves), args,
-                                tmq_eng_lds_bytes(l.act.n, waves), s);
+    return (int)hipLaunchKernel(k, dim3(l.ngroups + (l.rope_out ? 1 : 0)), dim3(64 * waves), args, lds, s);
 }
 
 int tmq_launch_silu(const TmqDeferred& g, const TmqDeferred& u, int n, float* x, uint32_t* max_bits,

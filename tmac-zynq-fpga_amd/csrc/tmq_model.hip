@@ -759,8 +759,10 @@ int build_launches(tmq_model* m) {
             w.y = (float*)kacc;
             w.ngroups = (g64 + ln.waves - 1) / ln.waves;
         } else {
-            const int units = (t->dev.type == TMQ_TYPE_Q8_0 || w.path == TMQ_WPATH_INT16)
-                                  ? (t->dev.cols + 63) / 64
+            // (the MFMA decoders split a row by whole blocks / super-blocks)
+            const int units = (t->dev.type == TMQ_TYPE_Q8_0 || w.path == TMQ_WPATH_INT16) ? (t->dev.cols + 63) / 64
+                              : tmq_kernel_fmt(t->dev) != t->dev.type
+                                  ? t->dev.nb
                                   : t->dev.nb * (t->dev.type == TMQ_TYPE_Q5_0 ? 1 : 4);
             if (kc > units) kc = units;
             if (kc < 1) kc = 1;
@@ -887,6 +889,19 @@ int build_launches(tmq_model* m) {
         m->logits_l.P.nworks = 1;
         m->logits_l.P.ngroups = w.ngroups;
     }
+    // every launch checked, and its kernel's LDS opted into, before any
+    // graph capture
+    for (int l = 0; l < L; l++) {
+        const Layer& Y = m->layers[l];
+        for (const Launch* ln : {&Y.qkv, &Y.o_l, &Y.gu, &Y.dn}) {
+            const int e = tmq_prepare_eng_gemv(ln->P, ln->waves);
+            if (e) return tmq_fail(TMQ_ERR_HIP, "layer %d engine launch: %s", l, hipGetErrorString((hipError_t)e));
+        }
+    }
+    {
+        const int e = tmq_prepare_eng_gemv(m->logits_l.P, m->logits_l.waves);
+        if (e) return tmq_fail(TMQ_ERR_HIP, "logits launch: %s", hipGetErrorString((hipError_t)e));
+    }
     // captured step graphs hold the old launches
     if (m->g_feed) (void)hipGraphExecDestroy(m->g_feed);
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
@@ -950,6 +965,12 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
         memcpy(fv.data() + at, e->data, (size_t)count * 4);
         return 0;
     };
+    // TMQ_ENG_MFMA=1: the engine's Q5_0 / K-quant projections run on the
+    // MFMA decoders (their tensors carry the integer-fit planes).  Off by
+    // default: a decode launch gives each wave one or two blocks, where the
+    // fitted-float decoders finish sooner (the MFMA path's correction loads,
+    // barriers and accumulator read-out sit on the launch's critical path).
+    const bool eng_mfma = env_int("TMQ_ENG_MFMA", 0) != 0;
     auto upload = [&](const std::string& n, uint64_t rows, uint64_t cols, tmq_tensor** out) -> int {
         const Entry* e = get(n);
         if (!e) return tmq_fail(TMQ_ERR_ARG, "model lacks %s", n.c_str());
@@ -969,7 +990,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
             if (a && a->type == 0 && a->cols == 1 && a->rows == rows && a->n_bytes == rows * 4)
                 aux = (const float*)a->data;
         }
-        int rc = tmq_rt_tensor_create(ctx, e->type, rows, cols, e->data, false, e->n_bytes, aux, false, out, false);
+        int rc = tmq_rt_tensor_create(ctx, e->type, rows, cols, e->data, false, e->n_bytes, aux, false, out, eng_mfma);
         if (rc) return tmq_fail(rc, "%s: %s", n.c_str(), tmq_last_error());
         m->owned.push_back(*out);
         m->weight_bytes += e->n_bytes;
@@ -1008,7 +1029,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
                 memcpy(buf.data() + (size_t)(64 * q + 32) * rb, eu->data + (size_t)(32 * q) * rb, 32 * rb);
             }
             rc = tmq_rt_tensor_create(ctx, eg->type, 2 * (uint64_t)I, H, buf.data(), false, buf.size(), nullptr, false,
-                                      &Y.gu_t, false);
+                                      &Y.gu_t, eng_mfma);
             if (rc) return tmq_fail(rc, "%sffn_gate/up: %s", p.c_str(), tmq_last_error());
             m->owned.push_back(Y.gu_t);
         }
