@@ -1817,8 +1817,11 @@ __global__ __launch_bounds__(64 * gemv_waves(FMT)) void gemv_kernel(TmqWork w) {
 
 // A chain segment: every descriptor of one format in one launch,
 // workgroup -> (descriptor, group, super-block range) through the group map.
+// The Q5_0 decoder is held to 64 registers, eight waves a SIMD (1.5 % a C2
+// launch over seven; the Q4_K decoder at five would spill).
 template <int FMT, bool CLAMP>
-__global__ __launch_bounds__(64 * gemv_waves(FMT)) void chain_kernel(const TmqWork* __restrict__ works,
+__global__ __launch_bounds__(64 * gemv_waves(FMT), FMT == kQ5_0M ? 8 : 1) void chain_kernel(
+    const TmqWork* __restrict__ works,
                                                                      const TmqGroupRef* __restrict__ groups,
                                                                      uint64_t* tail) {
     const TmqGroupRef ref = groups[blockIdx.x];
