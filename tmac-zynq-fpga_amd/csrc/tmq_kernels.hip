@@ -1821,9 +1821,7 @@ __global__ __launch_bounds__(64 * gemv_waves(FMT)) void gemv_kernel(TmqWork w) {
 // launch over seven; the Q4_K decoder at five would spill).
 template <int FMT, bool CLAMP>
 __global__ __launch_bounds__(64 * gemv_waves(FMT), FMT == kQ5_0M ? 8 : 1) void chain_kernel(
-    const TmqWork* __restrict__ works,
-                                                                     const TmqGroupRef* __restrict__ groups,
-                                                                     uint64_t* tail) {
+    const TmqWork* __restrict__ works, const TmqGroupRef* __restrict__ groups, uint64_t* tail) {
     const TmqGroupRef ref = groups[blockIdx.x];
     run_group<FMT, CLAMP>(works[ref.work], ref.group, ref.b0, ref.b1, ref.slot, ref.pieces, tail);
 }
