@@ -42,7 +42,7 @@ def prompt_of(n, seed):
     return np.random.default_rng(seed).integers(0, 151936, size=n).astype(np.int32)
 
 
-@pytest.mark.parametrize("n", [2, 37, 100, 300])
+@pytest.mark.parametrize("n", [2, 37, 100, 200, 300, 512])
 def test_prefill_matches_sequential(model, n):
     toks = prompt_of(n, 1000 + n)
     print(f"[prefill] n={n} sequential", flush=True)

@@ -8,44 +8,49 @@
 // s_load_dword per 64-byte line of the argument struct (in one asm statement
 // so that nothing is scheduled between them), then one wait.  The compiler
 // otherwise loads them where each is first needed, behind the branches that
-// depend on earlier ones: a round trip (~0.3 us) each.
+// depend on earlier ones: a round trip (~0.3 us) each.  The loaded values are
+// not used: the destinations are scratch registers the compiler picks (dead
+// after the statement), so the kernel's SGPR count, which bounds how many
+// waves a SIMD holds, does not grow.
 template <int BYTES>
 static __device__ __forceinline__ void tmq_warm_kernargs() {
     constexpr int N = (BYTES + 63) / 64;
     static_assert(N >= 1 && N <= 16, "one to sixteen lines");
     const auto p = __builtin_amdgcn_kernarg_segment_ptr();
+    int d[16];
     if constexpr (N == 1)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "memory");
+        asm volatile("s_load_dword %0, %1, 0x0\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]) : "s"(p) : "memory");
     else if constexpr (N == 2)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "memory");
+        asm volatile("s_load_dword %0, %2, 0x0\n" "s_load_dword %1, %2, 0x40\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]) : "s"(p) : "memory");
     else if constexpr (N == 3)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "memory");
+        asm volatile("s_load_dword %0, %3, 0x0\n" "s_load_dword %1, %3, 0x40\n" "s_load_dword %2, %3, 0x80\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]) : "s"(p) : "memory");
     else if constexpr (N == 4)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "memory");
+        asm volatile("s_load_dword %0, %4, 0x0\n" "s_load_dword %1, %4, 0x40\n" "s_load_dword %2, %4, 0x80\n" "s_load_dword %3, %4, 0xc0\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]) : "s"(p) : "memory");
     else if constexpr (N == 5)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "memory");
+        asm volatile("s_load_dword %0, %5, 0x0\n" "s_load_dword %1, %5, 0x40\n" "s_load_dword %2, %5, 0x80\n" "s_load_dword %3, %5, 0xc0\n" "s_load_dword %4, %5, 0x100\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]) : "s"(p) : "memory");
     else if constexpr (N == 6)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "memory");
+        asm volatile("s_load_dword %0, %6, 0x0\n" "s_load_dword %1, %6, 0x40\n" "s_load_dword %2, %6, 0x80\n" "s_load_dword %3, %6, 0xc0\n" "s_load_dword %4, %6, 0x100\n" "s_load_dword %5, %6, 0x140\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]) : "s"(p) : "memory");
     else if constexpr (N == 7)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "memory");
+        asm volatile("s_load_dword %0, %7, 0x0\n" "s_load_dword %1, %7, 0x40\n" "s_load_dword %2, %7, 0x80\n" "s_load_dword %3, %7, 0xc0\n" "s_load_dword %4, %7, 0x100\n" "s_load_dword %5, %7, 0x140\n" "s_load_dword %6, %7, 0x180\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]) : "s"(p) : "memory");
     else if constexpr (N == 8)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "memory");
+        asm volatile("s_load_dword %0, %8, 0x0\n" "s_load_dword %1, %8, 0x40\n" "s_load_dword %2, %8, 0x80\n" "s_load_dword %3, %8, 0xc0\n" "s_load_dword %4, %8, 0x100\n" "s_load_dword %5, %8, 0x140\n" "s_load_dword %6, %8, 0x180\n" "s_load_dword %7, %8, 0x1c0\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]) : "s"(p) : "memory");
     else if constexpr (N == 9)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "memory");
+        asm volatile("s_load_dword %0, %9, 0x0\n" "s_load_dword %1, %9, 0x40\n" "s_load_dword %2, %9, 0x80\n" "s_load_dword %3, %9, 0xc0\n" "s_load_dword %4, %9, 0x100\n" "s_load_dword %5, %9, 0x140\n" "s_load_dword %6, %9, 0x180\n" "s_load_dword %7, %9, 0x1c0\n" "s_load_dword %8, %9, 0x200\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]) : "s"(p) : "memory");
     else if constexpr (N == 10)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "memory");
+        asm volatile("s_load_dword %0, %10, 0x0\n" "s_load_dword %1, %10, 0x40\n" "s_load_dword %2, %10, 0x80\n" "s_load_dword %3, %10, 0xc0\n" "s_load_dword %4, %10, 0x100\n" "s_load_dword %5, %10, 0x140\n" "s_load_dword %6, %10, 0x180\n" "s_load_dword %7, %10, 0x1c0\n" "s_load_dword %8, %10, 0x200\n" "s_load_dword %9, %10, 0x240\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]) : "s"(p) : "memory");
     else if constexpr (N == 11)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "memory");
+        asm volatile("s_load_dword %0, %11, 0x0\n" "s_load_dword %1, %11, 0x40\n" "s_load_dword %2, %11, 0x80\n" "s_load_dword %3, %11, 0xc0\n" "s_load_dword %4, %11, 0x100\n" "s_load_dword %5, %11, 0x140\n" "s_load_dword %6, %11, 0x180\n" "s_load_dword %7, %11, 0x1c0\n" "s_load_dword %8, %11, 0x200\n" "s_load_dword %9, %11, 0x240\n" "s_load_dword %10, %11, 0x280\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10]) : "s"(p) : "memory");
     else if constexpr (N == 12)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "memory");
+        asm volatile("s_load_dword %0, %12, 0x0\n" "s_load_dword %1, %12, 0x40\n" "s_load_dword %2, %12, 0x80\n" "s_load_dword %3, %12, 0xc0\n" "s_load_dword %4, %12, 0x100\n" "s_load_dword %5, %12, 0x140\n" "s_load_dword %6, %12, 0x180\n" "s_load_dword %7, %12, 0x1c0\n" "s_load_dword %8, %12, 0x200\n" "s_load_dword %9, %12, 0x240\n" "s_load_dword %10, %12, 0x280\n" "s_load_dword %11, %12, 0x2c0\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10]), "=&s"(d[11]) : "s"(p) : "memory");
     else if constexpr (N == 13)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "memory");
+        asm volatile("s_load_dword %0, %13, 0x0\n" "s_load_dword %1, %13, 0x40\n" "s_load_dword %2, %13, 0x80\n" "s_load_dword %3, %13, 0xc0\n" "s_load_dword %4, %13, 0x100\n" "s_load_dword %5, %13, 0x140\n" "s_load_dword %6, %13, 0x180\n" "s_load_dword %7, %13, 0x1c0\n" "s_load_dword %8, %13, 0x200\n" "s_load_dword %9, %13, 0x240\n" "s_load_dword %10, %13, 0x280\n" "s_load_dword %11, %13, 0x2c0\n" "s_load_dword %12, %13, 0x300\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10]), "=&s"(d[11]), "=&s"(d[12]) : "s"(p) : "memory");
     else if constexpr (N == 14)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_load_dword s93, %0, 0x340\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "memory");
+        asm volatile("s_load_dword %0, %14, 0x0\n" "s_load_dword %1, %14, 0x40\n" "s_load_dword %2, %14, 0x80\n" "s_load_dword %3, %14, 0xc0\n" "s_load_dword %4, %14, 0x100\n" "s_load_dword %5, %14, 0x140\n" "s_load_dword %6, %14, 0x180\n" "s_load_dword %7, %14, 0x1c0\n" "s_load_dword %8, %14, 0x200\n" "s_load_dword %9, %14, 0x240\n" "s_load_dword %10, %14, 0x280\n" "s_load_dword %11, %14, 0x2c0\n" "s_load_dword %12, %14, 0x300\n" "s_load_dword %13, %14, 0x340\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10]), "=&s"(d[11]), "=&s"(d[12]), "=&s"(d[13]) : "s"(p) : "memory");
     else if constexpr (N == 15)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_load_dword s93, %0, 0x340\n" "s_load_dword s94, %0, 0x380\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "memory");
+        asm volatile("s_load_dword %0, %15, 0x0\n" "s_load_dword %1, %15, 0x40\n" "s_load_dword %2, %15, 0x80\n" "s_load_dword %3, %15, 0xc0\n" "s_load_dword %4, %15, 0x100\n" "s_load_dword %5, %15, 0x140\n" "s_load_dword %6, %15, 0x180\n" "s_load_dword %7, %15, 0x1c0\n" "s_load_dword %8, %15, 0x200\n" "s_load_dword %9, %15, 0x240\n" "s_load_dword %10, %15, 0x280\n" "s_load_dword %11, %15, 0x2c0\n" "s_load_dword %12, %15, 0x300\n" "s_load_dword %13, %15, 0x340\n" "s_load_dword %14, %15, 0x380\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10]), "=&s"(d[11]), "=&s"(d[12]), "=&s"(d[13]), "=&s"(d[14]) : "s"(p) : "memory");
     else if constexpr (N == 16)
-        asm volatile("s_load_dword s80, %0, 0x0\n" "s_load_dword s81, %0, 0x40\n" "s_load_dword s82, %0, 0x80\n" "s_load_dword s83, %0, 0xc0\n" "s_load_dword s84, %0, 0x100\n" "s_load_dword s85, %0, 0x140\n" "s_load_dword s86, %0, 0x180\n" "s_load_dword s87, %0, 0x1c0\n" "s_load_dword s88, %0, 0x200\n" "s_load_dword s89, %0, 0x240\n" "s_load_dword s90, %0, 0x280\n" "s_load_dword s91, %0, 0x2c0\n" "s_load_dword s92, %0, 0x300\n" "s_load_dword s93, %0, 0x340\n" "s_load_dword s94, %0, 0x380\n" "s_load_dword s95, %0, 0x3c0\n" "s_waitcnt lgkmcnt(0)" : : "s"(p) : "s80", "s81", "s82", "s83", "s84", "s85", "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95", "memory");
+        asm volatile("s_load_dword %0, %16, 0x0\n" "s_load_dword %1, %16, 0x40\n" "s_load_dword %2, %16, 0x80\n" "s_load_dword %3, %16, 0xc0\n" "s_load_dword %4, %16, 0x100\n" "s_load_dword %5, %16, 0x140\n" "s_load_dword %6, %16, 0x180\n" "s_load_dword %7, %16, 0x1c0\n" "s_load_dword %8, %16, 0x200\n" "s_load_dword %9, %16, 0x240\n" "s_load_dword %10, %16, 0x280\n" "s_load_dword %11, %16, 0x2c0\n" "s_load_dword %12, %16, 0x300\n" "s_load_dword %13, %16, 0x340\n" "s_load_dword %14, %16, 0x380\n" "s_load_dword %15, %16, 0x3c0\n" "s_waitcnt lgkmcnt(0)" : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10]), "=&s"(d[11]), "=&s"(d[12]), "=&s"(d[13]), "=&s"(d[14]), "=&s"(d[15]) : "s"(p) : "memory");
+    (void)d;
 }
 
 // Wave reductions by DPP lane moves (VALU only; __shfl_xor is a chain of six

@@ -619,6 +619,7 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         at.p0 = p0;
         at.n_heads = c.n_heads;
         at.n_kv = c.n_kv_heads;
+        at.ncu = m->ctx->ncu;
         LAUNCH_TRY(tmq_launch_pf_attn(at, s));
         // attn_output, split over K; the residual and the finalisation go
         // with the ffn_norm input

@@ -158,6 +158,8 @@ struct TmqPfAttn {
     const float* vc;
     float* ctx;                // [T][H]
     int32_t T, p0, n_heads, n_kv;
+    int32_t ncu;               // compute units of the device (0: unknown)
+    int32_t deal;              // set by the launch: workgroups dealt over the CUs in rounds
 };
 
 // The decode engine's state after the last token of a prefill: the

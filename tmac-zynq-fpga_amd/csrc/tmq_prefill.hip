@@ -476,22 +476,55 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
 // registers; LDS holds the exp terms, then the weights, of every position.
 typedef __attribute__((address_space(4))) const float cf32;
 constexpr int VCH = 32;    // positions per V chunk
-constexpr int VT_LD = 36;  // floats between dimensions of a transposed V chunk
+// A transposed V chunk: dimension d's VCH positions in 32 floats, float4
+// group j of them at group j ^ ((d >> 1) & 7), so that a float4 read by 16
+// consecutive dimensions covers all 64 banks once
+static __device__ __forceinline__ int vt_idx(int d, int pr) {
+    return d * VCH + ((((pr >> 2) ^ ((d >> 1) & 7)) << 2) | (pr & 3));
+}
+static __device__ __forceinline__ int vt_grp(int d, int j) { return d * VCH + ((j ^ ((d >> 1) & 7)) << 2); }
+
+// acc += w_j * v_j for 16 positions base + j in order, w_j = lane j of the
+// lane's 16-lane row of e; with PART, the terms of positions >= nr are added
+// as +0 (acc is never -0, so acc + 0 = acc; the V values read there are
+// never used)
+template <int J>
+static __device__ __forceinline__ float row_bcast(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x150 + J, 0xf, 0xf, true));
+}
+template <bool PART, int... J>
+static __device__ __forceinline__ float ctx_half(float acc, float e, const float* v, int base, int nr,
+                                                 std::integer_sequence<int, J...>) {
+    ((acc += PART ? (base + J < nr ? row_bcast<J>(e) * v[J] : 0.0f) : row_bcast<J>(e) * v[J]), ...);
+    return acc;
+}
 template <int NPASS>
-__global__ __launch_bounds__(512, NPASS <= 2 ? 4 : 2) void pf_attn_kernel(TmqPfAttn a) {
+__global__ __launch_bounds__(512, NPASS <= 2 ? 8 : NPASS == 4 ? 6 : 4) void pf_attn_kernel(TmqPfAttn a) {
     tmq_warm_kernargs<sizeof(TmqPfAttn)>();
     extern __shared__ float lds[];
     __shared__ float stat[2][8];
     __shared__ float red[8][8];  // [wave][head] maxima
     __shared__ uint64_t tab[32];
-    // V chunks of VCH positions, transposed (dimension-major, VT_LD apart)
-    // so that the lane of dimension d reads four positions at once;
-    // double-buffered.  (About 34 KiB of LDS a workgroup with the exp terms
+    // V chunks of VCH positions, transposed (dimension-major, vt_idx) so
+    // that the lane of dimension d reads four positions at once;
+    // double-buffered.  (Under 32 KiB of LDS a workgroup with the exp terms
     // of 512 positions, and at most 64 registers: four workgroups a CU, so
     // that the launch's 2 x T workgroups run in one round.)
-    __shared__ __attribute__((aligned(16))) float vb2[2][64 * VT_LD];
-    // the longest (latest) positions first
-    const int t = a.T - 1 - (int)blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    __shared__ __attribute__((aligned(16))) float vb2[2][64 * VCH];
+    // Which (token, KV head) this workgroup takes.  Ranked by length (the
+    // latest tokens, with the most positions, first), the launch's
+    // workgroups go out in that order; with `deal`, when all of them are
+    // resident at once (four a CU), the CU that takes workgroup i takes
+    // i + ncu, i + 2 ncu, ..., so the ranks are dealt in a snake (forward
+    // in even rounds of ncu, backward in odd ones) and every CU gets about
+    // the same number of positions.
+    int rank = blockIdx.x + a.T * blockIdx.y;
+    if (a.deal) {
+        const int r = rank / a.ncu, c = rank - r * a.ncu;
+        const int n = min(a.ncu, a.T * a.n_kv - r * a.ncu);
+        rank = r * a.ncu + ((r & 1) ? n - 1 - c : c);
+    }
+    const int t = a.T - 1 - rank / a.n_kv, g = rank - (rank / a.n_kv) * a.n_kv, tid = threadIdx.x;
     const int qpk = a.n_heads / a.n_kv, KV = a.n_kv * 64, H = a.n_heads * 64;
     const int np = a.p0 + t + 1, npad = (np + 3) & ~3;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
@@ -620,10 +653,10 @@ __global__ __launch_bounds__(512, NPASS <= 2 ? 4 : 2) void pf_attn_kernel(TmqPfA
     // float4 = one chunk; a wave's lanes take the chunk's 32 positions of two
     // groups of four dimensions)
     auto put_v = [&](float* vt, int pr, int q4, float4 v) {
-        vt[(4 * q4 + 0) * VT_LD + pr] = v.x;
-        vt[(4 * q4 + 1) * VT_LD + pr] = v.y;
-        vt[(4 * q4 + 2) * VT_LD + pr] = v.z;
-        vt[(4 * q4 + 3) * VT_LD + pr] = v.w;
+        vt[vt_idx(4 * q4 + 0, pr)] = v.x;
+        vt[vt_idx(4 * q4 + 1, pr)] = v.y;
+        vt[vt_idx(4 * q4 + 2, pr)] = v.z;
+        vt[vt_idx(4 * q4 + 3, pr)] = v.w;
     };
     static_assert(VCH * 16 == 512, "one float4 a thread per chunk");
     {
@@ -639,58 +672,23 @@ __global__ __launch_bounds__(512, NPASS <= 2 ? 4 : 2) void pf_attn_kernel(TmqPfA
         float4 pre;
         if (ppr < nr1) pre = *(const float4*)(vbase + (size_t)(c1 + ppr) * KV + 4 * pq4);
         if (wv < qpk) {
+            // the chunk's weights in registers: lane i of every 16-lane row
+            // holds position h + i of each half h, and each multiply takes
+            // its weight by row_newbcast (no broadcast LDS reads); the
+            // lane's dimension of the half's V rows in four float4 reads
             const float* e = ex + wv * npad + c0;
-            const float* vt = vb2[buf] + ln * VT_LD;
-            int pr = 0;
-            // steps of 8 positions, each step's LDS reads issued during the
-            // previous step's adds
-            float4 ea[2], va[2], eb[2], vb[2];
-            auto ld = [&](float4* ev, float4* vv, int o) {
+            const float* vt = vb2[buf];
+            const int r = ln & 15;
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    ev[j] = *(const float4*)(e + o + 4 * j);
-                    vv[j] = *(const float4*)(vt + o + 4 * j);
-                }
-            };
-            auto mac = [&](const float4* ev, const float4* vv) {
+            for (int h = 0; h < VCH; h += 16) {
+                const float eh = e[min(h + r, nr - 1)];
+                float4 vv[4];
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    acc += ev[j].x * vv[j].x;
-                    acc += ev[j].y * vv[j].y;
-                    acc += ev[j].z * vv[j].z;
-                    acc += ev[j].w * vv[j].w;
-                }
-            };
-            if (nr == VCH) {
-                ld(ea, va, 0);
-#pragma unroll
-                for (int o = 0; o < VCH; o += 16) {
-                    ld(eb, vb, o + 8);
-                    mac(ea, va);
-                    if (o + 16 < VCH) ld(ea, va, o + 16);
-                    mac(eb, vb);
-                }
-                pr = VCH;
-            }
-            for (; pr + 8 <= nr; pr += 8) {
-                ld(ea, va, pr);
-                mac(ea, va);
-            }
-            if (pr < nr) {
-                // the last 1-7 positions: reads clamped into range, the
-                // terms past the end added as +0 (acc is never -0)
-                float ev[8], vv[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int q = min(pr + j, nr - 1);
-                    ev[j] = e[q];
-                    vv[j] = vt[q];
-                }
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float m = ev[j] * vv[j];
-                    acc += pr + j < nr ? m : 0.0f;
-                }
+                for (int i = 0; i < 4; i++) vv[i] = *(const float4*)(vt + vt_grp(ln, h / 4 + i));
+                if (nr == VCH)
+                    acc = ctx_half<false>(acc, eh, (const float*)vv, 0, nr, std::make_integer_sequence<int, 16>{});
+                else
+                    acc = ctx_half<true>(acc, eh, (const float*)vv, h, nr, std::make_integer_sequence<int, 16>{});
             }
         }
         if (ppr < nr1) put_v(vb2[buf ^ 1], ppr, pq4, pre);
@@ -888,8 +886,15 @@ int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s) {
         return (int)hipErrorInvalidValue;
     const size_t lds = tmq_pf_attn_lds(qpk, np);
     if (lds > TMQ_PF_ATTN_LDS_MAX) return (int)hipErrorInvalidValue;
-    // registers for the scores of np positions (512 per pass)
-    if (np <= 512) return launch_attn<1>(a, lds, s);
+    // registers for the scores of np positions (512 per pass).  Up to 512
+    // positions four workgroups fit a CU (64 VGPRs, at most 80 SGPRs, LDS
+    // under 40 KiB), and a launch of at most 4 x ncu workgroups is resident
+    // at once: dealt in a snake.
+    if (np <= 512) {
+        TmqPfAttn b = a;
+        b.deal = a.ncu > 0 && a.T * a.n_kv <= 4 * a.ncu && a.T * a.n_kv > a.ncu;
+        return launch_attn<1>(b, lds, s);
+    }
     if (np <= 1024) return launch_attn<2>(a, lds, s);
     if (np <= 2048) return launch_attn<4>(a, lds, s);
     return launch_attn<8>(a, lds, s);
