@@ -111,6 +111,43 @@ def test_prefill_errors(model):
         model.set_prefill(-1)
 
 
+@pytest.mark.parametrize("n, chunk", [(300, 512), (150, 64)])
+def test_gu_quant_paths(model, monkeypatch, n, chunk):
+    """The gate/up GEMM quantises the SwiGLU rows for the down projection in
+    its own epilogue (its workgroups of one token tile wait for each other's
+    row maxima); TMQ_PF_GUQ=0 takes the separate act kernel instead.  Both
+    leave the same bits."""
+    toks = prompt_of(n, 3300 + n)
+    res = {}
+    for guq in ("0", "1"):
+        monkeypatch.setenv("TMQ_PF_GUQ", guq)
+        print(f"[prefill] n={n} chunk={chunk} TMQ_PF_GUQ={guq}", flush=True)
+        res[guq] = run(model, toks, chunk)
+    (l0, h0, g0), (l1, h1, g1) = res["0"], res["1"]
+    assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32))
+    assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32))
+    assert g1.tolist() == g0.tolist()
+
+
+def test_gu_quant_wait_limit(model, monkeypatch):
+    """A gate/up workgroup whose wait for its token tile runs out of polls
+    (forced from the host: a limit of 0 polls) flags the prefill, which then
+    fails; every kernel still ends.  The next prompt runs normally."""
+    import tmq
+    toks = prompt_of(100, 4100)
+    monkeypatch.setenv("TMQ_PF_GUQ", "1")
+    monkeypatch.setenv("TMQ_PF_GUQ_SPIN", "0")
+    model.set_prefill(512)
+    print("[prefill] gate/up wait limit 0", flush=True)
+    with pytest.raises(tmq.TmqError, match="ran out of polls"):
+        model.prompt(toks)
+    monkeypatch.delenv("TMQ_PF_GUQ_SPIN")
+    l0, h0, g0 = run(model, toks, 0)
+    l1, h1, g1 = run(model, toks, 512)
+    assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32))
+    assert g1.tolist() == g0.tolist()
+
+
 def test_norm_sum_fallback(ctx, model, monkeypatch):
     """RMSNorm's sequential sum of squares runs in segments from speculated
     starting values, each checked against the exact end of the segment

@@ -154,10 +154,13 @@ struct TmqDeferred {
 // Decode-engine state in device memory.  pos = the position being processed
 // (-1 after a reset); it is advanced by the first kernel of a step, so a
 // captured step replays without host involvement.  err != 0 stops the step.
+// pf_err != 0: a wait of the prefill's gate/up workgroups for the rest of
+// their token tile ran out of polls (the prompt then fails).
 struct TmqEngState {
     int32_t pos;
     int32_t err;
-    int32_t pad_[2];
+    int32_t pf_err;
+    int32_t pad_;
 };
 
 // Activation recipe of an engine GEMV launch: every workgroup computes the

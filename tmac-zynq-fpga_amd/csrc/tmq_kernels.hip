@@ -3448,6 +3448,10 @@ __global__ __launch_bounds__(256) void pf_act_kernel(TmqPfAct a) {
     const int t = blockIdx.x, n = a.n, tid = threadIdx.x, nt = blockDim.x;
     const int wave = tid >> 6, lane = tid & 63, nc = n / TMQ_PF_CHUNK, ng = n >> 2;
     int8_t* dp = a.out.d;
+    // the next GU GEMM's per-token sums and token-tile counters (quantising
+    // epilogue), for every row
+    if (tid == 0 && a.zero_tsum) a.zero_tsum[t] = 0;
+    if (t * nt + tid < a.zero_ncnt) a.zero_cnt[32 * (t * nt + tid)] = 0u;
     if (t >= a.T) {
         for (int gi = tid; gi < ng; gi += nt) {
             const size_t o = tmq_pf_off(t, 4 * gi, n, 0);

@@ -130,6 +130,7 @@ struct Prefill {
     float* xs[4] = {nullptr, nullptr, nullptr, nullptr};
     int64_t* part = nullptr;
     uint32_t* max_bits = nullptr;
+    uint32_t* gq_cnt = nullptr;  // arrival counters of the quantising GU epilogue, one a token tile
     int dn_split = 4;
     int o_split = 2;   // attn_output GEMM split over K (finalised by the ffn_norm input)
     int qkv_split = 1; // q/k/v GEMM split over K (finished by pf_qkv_fin)
@@ -342,6 +343,7 @@ int check_state(tmq_model* m) {
     HIP_TRY(hipMemcpyAsync(&st, m->state, sizeof st, hipMemcpyDeviceToHost, m->ctx->stream));
     HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     if (st.err) return tmq_fail(TMQ_ERR_ARG, "decode step failed on the device (token or position out of range)");
+    if (st.pf_err) return tmq_fail(TMQ_ERR_HIP, "prefill: a gate/up workgroup's wait for its token tile ran out of polls");
     if (st.pos != m->pos) return tmq_fail(TMQ_ERR_HIP, "device position %d != expected %d", st.pos, m->pos);
     return 0;
 }
@@ -431,6 +433,9 @@ int pf_build_buffers(tmq_model* m, int chunk) {
                                    (size_t)P.qkv_split * T * (H + 2 * KV) + (size_t)T * KV * (H / TMQ_PF_CHUNK));
     parts.push_back({(void**)&P.part, 8 * part_n});
     parts.push_back({(void**)&P.max_bits, 4 * (size_t)T});
+    // the GU epilogue's counters and flags: 128 bytes each, per token tile
+    // one counter and one flag a workgroup (row tile)
+    parts.push_back({(void**)&P.gq_cnt, 128 * (size_t)(T / 32) * (I / 32 + 1)});
     for (int i = 0; i < 4; i++) {
         const int K = i == 3 ? I : H;
         P.in[i].rows = T;
@@ -506,6 +511,14 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
     const int tile_gu = pf_tile(P.tile[2], H, {2 * I}), tile_dn = pf_tile(P.tile[3], I, {H});
     const int T_pad = (T + 127) & ~127;  // whole 128-token GEMM tiles
     hipStream_t s = m->ctx->stream;
+    // gate/up quantises the SwiGLU rows itself where all its workgroups are
+    // resident at once (TMQ_PF_GUQ=0: the separate act kernel); its wait
+    // gives up after TMQ_PF_GUQ_SPIN polls
+    int gq_tiles = 0;
+    const bool gq = env_int("TMQ_PF_GUQ", 1) != 0 &&
+                    tmq_pf_gu_quant_fits(tile_gu, T_pad, I, m->ctx->ncu, &gq_tiles) && gq_tiles <= P.chunk / 32;
+    const int gq_words = gq_tiles * (I / 32 + 1);  // (row tiles of any GU tile: at most I / 32)
+    const int gq_spin = std::max(0, env_int("TMQ_PF_GUQ_SPIN", 1 << 20));
     auto fv = [&](long o) -> const float* { return o < 0 ? nullptr : m->fvec + o; };
     auto act = [&](int mode, int set, const float* x, const float* w, int n) {
         TmqPfAct a{};
@@ -643,6 +656,11 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         a2.d1.T_pad = T_pad;
         a2.x_out = P.x1;
         a2.zero_bits = P.max_bits;
+        if (gq) {
+            a2.zero_tsum = P.in[3].tsum;
+            a2.zero_cnt = P.gq_cnt;
+            a2.zero_ncnt = gq_words;
+        }
         LAUNCH_TRY(tmq_launch_pf_act(a2, s));
         g = gemm(TMQ_PF_GU, W.gu, 2);
         g.nseg = 2;
@@ -651,11 +669,23 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
         g.seg[1] = pf_seg(Y.up, I, nullptr);
         g.s_out = P.s;
         g.max_bits = P.max_bits;
+        if (gq) {
+            // the SwiGLU rows quantised for the down projection in the epilogue
+            g.gq_d = P.in[3].d;
+            g.gq_tsum = P.in[3].tsum;
+            g.gq_xs = P.xs[3];
+            g.gq_cnt = P.gq_cnt;
+            g.gq_err = &m->state->pf_err;
+            g.gq_spin = gq_spin;
+            g.gq_ntiles = gq_tiles;
+        }
         LAUNCH_TRY(tmq_launch_pf_gemm(g, tile_gu, s));
+        if (!gq) {
+            TmqPfAct a3 = act(TMQ_PF_SILU, 3, P.s, nullptr, I);
+            a3.max_bits = P.max_bits;
+            LAUNCH_TRY(tmq_launch_pf_act(a3, s));
+        }
         // down projection, split over K; finalised by the next layer's input
-        TmqPfAct a3 = act(TMQ_PF_SILU, 3, P.s, nullptr, I);
-        a3.max_bits = P.max_bits;
-        LAUNCH_TRY(tmq_launch_pf_act(a3, s));
         g = gemm(TMQ_PF_PART, W.dn, 3);
         g.split = std::min(P.dn_split, I / pf_stage_cols(tile_dn));
         g.part = P.part;
@@ -1110,7 +1140,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
     std::vector<float2> rope((size_t)max_seq * 32);
     tmq_math::rope_table(c.rope_base, TMQ_HEAD_DIM, max_seq, (float*)rope.data());
     HIP_TRY(hipMemcpyAsync(m->rope, rope.data(), sizeof(float2) * rope.size(), hipMemcpyHostToDevice, s));
-    TmqEngState st{-1, 0, {0, 0}};
+    TmqEngState st{-1, 0, 0, 0};
     HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
     HIP_TRY(hipStreamSynchronize(s));
     m->use_graphs = env_int("TMQ_GRAPHS", 1) != 0;
@@ -1124,7 +1154,7 @@ int build_model(tmq_model* m, const std::vector<Entry>& ents, int max_seq) {
 
 int reset(tmq_model* m) {
     hipStream_t s = m->ctx->stream;
-    TmqEngState st{-1, 0, {0, 0}};
+    TmqEngState st{-1, 0, 0, 0};
     HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
     m->pos = -1;
     return 0;
@@ -1213,8 +1243,9 @@ int tmq_model_prompt(tmq_model* m, const int32_t* tokens, int n) {
     if (m->prefill_chunk > 0 && !m->prefill_off && m->flags == TMQ_FLAGS_ALL && n >= 2) {
         if ((rc = pf_prompt(m, n, &done))) return rc;
         if (done > 0) {
-            TmqEngState st{done - 1, 0, {0, 0}};
-            HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, m->ctx->stream));
+            // pos and err only: pf_err keeps what the prefill left
+            TmqEngState st{done - 1, 0, 0, 0};
+            HIP_TRY(hipMemcpyAsync(m->state, &st, 2 * sizeof(int32_t), hipMemcpyHostToDevice, m->ctx->stream));
             m->pos = done - 1;
         }
     }

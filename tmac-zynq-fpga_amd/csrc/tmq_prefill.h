@@ -81,6 +81,9 @@ struct TmqPfAct {
     TmqPfPart d1;              // RESID_NORM
     float* x_out;              // EMBED/RESID: the value before the norm, [T][n]
     uint32_t* zero_bits;       // NORM: per-token max slots cleared for the next GU GEMM (or null)
+    int32_t* zero_tsum;        // per token (all T_pad rows): cleared for a quantising GU GEMM (or null)
+    uint32_t* zero_cnt;        // words 32 i, i < zero_ncnt: its counters and flags, cleared
+    int32_t zero_ncnt, pad_;
     const int32_t* tokens;     // EMBED: token ids by position
     TmqTensorDev emb;          // EMBED: quantised embedding
     TmqPfPlanes out;           // digit planes [T_pad][n]
@@ -127,6 +130,21 @@ struct TmqPfGemm {
     int64_t* part;             // [split][T_pad][rows]
     // QKV, QKVS: the Q8_0 segment's per-tile sums
     int64_t* tpart;            // [K/64][seg rows][T_pad]
+    // GU with gq_d set: the SwiGLU rows quantised in the epilogue, as
+    // pf_act_kernel's SILU mode would (digit planes of T_pad rows, the sums
+    // of q - 128 per token, x_scale per token; the per-chunk sums are not
+    // formed: only a Q8_0 weight reads them, and no down projection is Q8_0
+    // here).  The workgroups of a token tile meet in gq_cnt[tile] once their
+    // max atomics are in, which needs every workgroup of the launch resident
+    // at once (tmq_pf_gu_quant_fits); a wait past gq_spin polls sets *gq_err
+    // and goes on.  gq_cnt and gq_tsum start at zero (the ffn_norm act
+    // kernel clears them).
+    int8_t* gq_d;
+    int32_t* gq_tsum;
+    float* gq_xs;
+    uint32_t* gq_cnt;          // words 32 i: the tiles' counters, then per tile one flag a workgroup
+    int32_t* gq_err;
+    int32_t gq_spin, gq_ntiles;
 };
 
 // q, k, v rows finished from the int64 sums a QKV / QKVS GEMM left: the split
@@ -199,6 +217,10 @@ int tmq_launch_pf_act(const TmqPfAct& a, hipStream_t s);
 // 3 = 64 x 128 with two stage buffers (three workgroups per CU), 4 = 64 x 64
 // with K split in halves between the workgroup's waves (K a multiple of 128)
 int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s);
+// Whether every workgroup of a GU launch over T_pad tokens (tile, gu_rows)
+// is resident at once on ncu CUs (the quantising epilogue's wait needs it);
+// the token tiles of the launch in *ntiles.
+bool tmq_pf_gu_quant_fits(int tile, int T_pad, int gu_rows, int ncu, int* ntiles);
 int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);
 int tmq_launch_pf_qkv_fin(const TmqPfQkvFin& f, hipStream_t s);

@@ -103,6 +103,92 @@ __device__ __forceinline__ void wait_stages(int k) {
     }
 }
 
+// The quantising epilogue of a GU launch (TmqPfGemm.gq_d).  Once every max
+// atomic of the workgroup is in (vmcnt counts them), the workgroup counts
+// itself in its token tile's counter and waits until all gridDim.x *
+// gridDim.z workgroups of the tile have (all of them are resident at once:
+// the host checked), so that max_bits holds each token's max |s| over its
+// whole row.  widx: the workgroup's index in its tile.
+// Then, as pf_act_kernel's SILU mode: x_scale = max / 32767 (1 below
+// 1e-10), q = (int16)round(s / x_scale) into the digit planes (a high byte,
+// and a low byte ^ 128), the sums of q - 128 per token (atomics: each
+// workgroup of the tile adds its columns), x_scale per token (one wave per
+// token block: xs_writer); rows at or past T get zero digits and x_scale 1.
+// The wave holds token blocks tb0 .. tb0 + WTB - 1 and columns [32 s,
+// 32 s + 32) of the SwiGLU rows: lane l token l & 31, columns
+// 8q + 4 (l >> 5) + k (k < 4) as element 4q + k of gsv.
+template <int WTB>
+__device__ __forceinline__ void pf_gu_quant(const TmqPfGemm& g, const float (&gsv)[WTB][16], int tile, int widx, int tb0,
+                                            int s, bool xs_writer, int lane) {
+    // the wait: the tile's counter, then one release flag a workgroup
+    // (128 bytes apart), set by the last to arrive; each workgroup polls
+    // its own flag only, so the polls queue behind no other atomics
+    __shared__ int s_last;
+    const int need = gridDim.x * gridDim.z;
+    uint32_t* cnt = g.gq_cnt + 32 * tile;
+    uint32_t* flag = g.gq_cnt + 32 * (g.gq_ntiles + tile * need);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)need - 1u;
+    __syncthreads();
+    if (s_last) {
+        for (int i = threadIdx.x; i < need; i += blockDim.x)
+            __hip_atomic_store(flag + 32 * i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (threadIdx.x == 0) {
+        // (read by a read-modify-write: the value at the coherence point)
+        uint32_t* mine = flag + 32 * widx;
+        for (int it = 0; __hip_atomic_fetch_or(mine, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; it++) {
+            if (it >= g.gq_spin) {
+                __hip_atomic_store(g.gq_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+        }
+    }
+    __syncthreads();
+    const int h = lane >> 5, K32 = g.gu_rows >> 5;
+#pragma unroll
+    for (int j = 0; j < WTB; j++) {
+        const int tb = tb0 + j, t = tb * 32 + (lane & 31);
+        const bool live = t < g.T;
+        const uint32_t mb =
+            live ? __hip_atomic_fetch_or(g.max_bits + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        const float mm = __builtin_bit_cast(float, mb);
+        const float xs = (mm < 1e-10f) ? 1.0f : mm / 32767.0f;
+        uint32_t hi[4], lo[4];
+        int sum = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            hi[q] = lo[q] = 0u;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int v = (int)(int16_t)roundf(gsv[j][4 * q + k] / xs);
+                hi[q] |= ((uint32_t)(v >> 8) & 255u) << (8 * k);
+                lo[q] |= (((uint32_t)v & 255u) ^ 128u) << (8 * k);
+                sum += v - 128;
+            }
+            if (!live) hi[q] = lo[q] = 0u;
+        }
+        // a plane row (tmq_pf_off) is 16 columns of one token: half h of the
+        // block's columns goes to lane (l & 31) + 32h, whose dwords are runs
+        // q = 0, 1 (h = 0) or 2, 3 (h = 1) of lanes l & 31 and (l & 31) + 32
+        // in turn
+        const uint32_t sh0 = h ? hi[0] : hi[2], sh1 = h ? hi[1] : hi[3];
+        const uint32_t sl0 = h ? lo[0] : lo[2], sl1 = h ? lo[1] : lo[3];
+        const uint32_t rh0 = __shfl_xor(sh0, 32), rh1 = __shfl_xor(sh1, 32);
+        const uint32_t rl0 = __shfl_xor(sl0, 32), rl1 = __shfl_xor(sl1, 32);
+        const uint4 vh = h ? make_uint4(rh0, hi[2], rh1, hi[3]) : make_uint4(hi[0], rh0, hi[1], rh1);
+        const uint4 vl = h ? make_uint4(rl0, lo[2], rl1, lo[3]) : make_uint4(lo[0], rl0, lo[1], rl1);
+        int8_t* dst = g.gq_d + ((((size_t)tb * K32 + s) * 2) * 64 + lane) * 16;
+        *(uint4*)dst = vh;
+        *(uint4*)(dst + 1024) = vl;
+        const int tot = sum + __shfl_xor(sum, 32);
+        if (live && lane < 32) __hip_atomic_fetch_add(g.gq_tsum + t, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (xs_writer && lane < 32) g.gq_xs[t] = live ? xs : 1.0f;
+    }
+}
+
 template <int MODE, int TILE>
 __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gemm_kernel(TmqPfGemm g) {
     tmq_warm_kernargs<sizeof(TmqPfGemm)>();
@@ -399,6 +485,7 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     };
 
     // elements v = 4q .. 4q+3 of a lane are 4 consecutive rows: one float4
+    float gsv[MODE == TMQ_PF_GU ? WTB : 1][16];  // GU: the SwiGLU values (quantised after the wait)
 #pragma unroll
     for (int j = 0; j < WTB; j++) {
         const int t = tw0 + j * 32 + (lane & 31);
@@ -441,29 +528,36 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
             float m = 0.0f;
             const int j0 = rblk(2 * wr) * 32;
             const Exp2TabLds tab{c_tab};
-            float* tp = (float*)&lds[0][0] + wave * (32 * 36);
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float sv[4];
+            for (int q = 0; q < 4; q++)
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const float gv = fin(0, j, 4 * q + k);
-                    sv[k] = (gv / (1.0f + tmq_math::tmq_expf_tab(-gv, tab))) * fin(1, j, 4 * q + k);
-                    m = fmaxf(m, fabsf(sv[k]));
+                    const float sv = (gv / (1.0f + tmq_math::tmq_expf_tab(-gv, tab))) * fin(1, j, 4 * q + k);
+                    gsv[j][4 * q + k] = sv;
+                    m = fmaxf(m, fabsf(sv));
                 }
-                *(float4*)(tp + (lane & 31) * 36 + blk_row(4 * q, lane)) = make_float4(sv[0], sv[1], sv[2], sv[3]);
-            }
+            if (!g.gq_d) {
+                float* tp = (float*)&lds[0][0] + wave * (32 * 36);
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int tt = (lane >> 3) + 8 * k, c = lane & 7, ts = tw0 + j * 32 + tt;
-                const float4 val = *(const float4*)(tp + tt * 36 + 4 * c);
-                if (ts < g.T) *(float4*)(g.s_out + (size_t)ts * g.gu_rows + j0 + 4 * c) = val;
+                for (int q = 0; q < 4; q++)
+                    *(float4*)(tp + (lane & 31) * 36 + blk_row(4 * q, lane)) =
+                        make_float4(gsv[j][4 * q], gsv[j][4 * q + 1], gsv[j][4 * q + 2], gsv[j][4 * q + 3]);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int tt = (lane >> 3) + 8 * k, c = lane & 7, ts = tw0 + j * 32 + tt;
+                    const float4 val = *(const float4*)(tp + tt * 36 + 4 * c);
+                    if (ts < g.T) *(float4*)(g.s_out + (size_t)ts * g.gu_rows + j0 + 4 * c) = val;
+                }
             }
             m = fmaxf(m, __shfl_xor(m, 32));
             if (live && lane < 32)
                 __hip_atomic_fetch_max(g.max_bits + t, __builtin_bit_cast(uint32_t, m), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
         }
+    }
+    if constexpr (MODE == TMQ_PF_GU) {
+        if (g.gq_d) pf_gu_quant<WTB>(g, gsv, by, bx + gridDim.x * bz, tblk0 + wt * WTB, rblk(2 * wr), wr == 0 && bx == 0, lane);
     }
 }
 
@@ -835,6 +929,32 @@ size_t tmq_pf_attn_lds(int qpk, int npos) {
     return sizeof(float) * (size_t)qpk * npad;
 }
 
+namespace {
+template <int TILE>
+bool gu_quant_fits(int T_pad, int gu_rows, int ncu, int* ntiles) {
+    typedef TileGeo<TILE> G;
+    const long rt = gu_rows / (16 * G::NRB), tt = (T_pad + 32 * G::NTB - 1) / (32 * G::NTB);
+    int per = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)pf_gemm_kernel<TMQ_PF_GU, TILE>, 256, 0) !=
+        hipSuccess)
+        return false;
+    *ntiles = (int)tt;
+    return rt * tt <= (long)per * ncu;
+}
+}  // namespace
+
+bool tmq_pf_gu_quant_fits(int tile, int T_pad, int gu_rows, int ncu, int* ntiles) {
+    *ntiles = 0;
+    if (ncu <= 0 || T_pad <= 0 || gu_rows <= 0) return false;
+    switch (tile) {
+    case 0: return gu_quant_fits<0>(T_pad, gu_rows, ncu, ntiles);
+    case 1: return gu_quant_fits<1>(T_pad, gu_rows, ncu, ntiles);
+    case 2: return gu_quant_fits<2>(T_pad, gu_rows, ncu, ntiles);
+    case 3: return gu_quant_fits<3>(T_pad, gu_rows, ncu, ntiles);
+    }
+    return false;  // (tile 4 takes no GU launch)
+}
+
 int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
     // shapes the kernel assumes: 64-column chunks, whole token tiles of the
     // operand planes, whole row tiles (GU: gate/up tiles of NRB/2 blocks),
@@ -846,6 +966,8 @@ int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
         g.split > g.K / (32 * ks))
         return (int)hipErrorInvalidValue;
     if (g.mode != TMQ_PF_PART && g.mode != TMQ_PF_QKVS && g.split != 1) return (int)hipErrorInvalidValue;
+    if (g.gq_d && (g.mode != TMQ_PF_GU || !g.gq_tsum || !g.gq_xs || !g.gq_cnt || !g.gq_err || !g.max_bits))
+        return (int)hipErrorInvalidValue;
     if (g.mode == TMQ_PF_GU) {
         // (the SwiGLU epilogue needs both blocks of a wave: no K groups)
         if (tile == 4 || g.gu_rows % (16 * nrb) || g.rows != 2 * g.gu_rows) return (int)hipErrorInvalidValue;
