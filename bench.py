@@ -549,7 +549,7 @@ def main():
                            "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
         extra["c2_attn_q_single_launch_us"] = round(single_launch_us(ctx, torch, dev, stream, 50), 2)
         extra["c4_decode"] = decode_bench(ctx, torch, stream)
-        extra["c5_prefill"] = prefill_bench(ctx)
+        extra["c5_prefill"] = prefill_bench(ctx, 512, 20)
         out["extra"] = extra
     ctx.close()
     if not args.no_cpu:

@@ -129,6 +129,24 @@ def test_gu_quant_paths(model, monkeypatch, n, chunk):
     assert g1.tolist() == g0.tolist()
 
 
+@pytest.mark.parametrize("n, chunk", [(512, 512), (150, 64)])
+def test_prefill_graph_replays(model, monkeypatch, n, chunk):
+    """A prefill is captured once per prompt length and replayed: every
+    replay (with eager decode steps and synchronisations between them)
+    leaves the bits of the prefill launched one kernel at a time."""
+    toks = prompt_of(n, 5200 + n)
+    monkeypatch.setenv("TMQ_PF_GRAPH", "0")
+    print(f"[prefill] n={n} chunk={chunk} eager", flush=True)
+    l0, h0, g0 = run(model, toks, chunk)
+    monkeypatch.setenv("TMQ_PF_GRAPH", "1")
+    for rep in range(3):
+        print(f"[prefill] n={n} chunk={chunk} graph replay {rep}", flush=True)
+        l1, h1, g1 = run(model, toks, chunk)
+        assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32)), f"replay {rep}"
+        assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32)), f"replay {rep}"
+        assert g1.tolist() == g0.tolist()
+
+
 def test_gu_quant_wait_limit(model, monkeypatch):
     """A gate/up workgroup whose wait for its token tile runs out of polls
     (forced from the host: a limit of 0 polls) flags the prefill, which then

@@ -135,6 +135,15 @@ struct Prefill {
     int o_split = 2;   // attn_output GEMM split over K (finalised by the ffn_norm input)
     int qkv_split = 1; // q/k/v GEMM split over K (finished by pf_qkv_fin)
     int tile[4] = {4, 4, 3, 1};  // GEMM workgroup tiles: qkv, o, gate/up, down (tmq_launch_pf_gemm)
+    // captured prefills, by prompt length, chunk and the settings the
+    // launches read (a capture holds the chunk buffers' addresses: dropped
+    // with them)
+    struct Graph {
+        int lim, chunk, guq, spin;
+        hipGraphExec_t g;
+    };
+    std::vector<Graph> graphs;
+    int cap_lim = 0, cap_chunk = 0;  // what the capture in progress runs
 };
 
 struct tmq_model {
@@ -189,6 +198,7 @@ void model_release(tmq_model* m) {
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
     for (tmq_tensor* t : m->owned) tmq_tensor_free(t);
     if (m->dmem) (void)hipFree(m->dmem);
+    for (auto& g : m->pf.graphs) (void)hipGraphExecDestroy(g.g);
     if (m->pf.wmem) (void)hipFree(m->pf.wmem);
     if (m->pf.amem) (void)hipFree(m->pf.amem);
     delete m;
@@ -415,6 +425,8 @@ int pf_build_buffers(tmq_model* m, int chunk) {
     if (P.amem && P.chunk == chunk) return 0;
     if (P.amem) {
         HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+        for (auto& g : P.graphs) (void)hipGraphExecDestroy(g.g);
+        P.graphs.clear();
         (void)hipFree(P.amem);
         P.amem = nullptr;
     }
@@ -706,6 +718,16 @@ int pf_run_chunk(tmq_model* m, int p0, int T, bool last) {
     return 0;
 }
 
+// Every chunk of positions [0, lim).
+int pf_run_all(tmq_model* m, int lim, int chunk) {
+    for (int p0 = 0; p0 < lim; p0 += chunk) {
+        const int T = std::min(chunk, lim - p0);
+        const int rc = pf_run_chunk(m, p0, T, p0 + T >= lim);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 // Positions [0, n) of a prompt whose tokens are on the device: as many as
 // the prefill's attention can hold go through in chunks; returns how many.
 int pf_prompt(tmq_model* m, int n, int* done) {
@@ -718,10 +740,32 @@ int pf_prompt(tmq_model* m, int n, int* done) {
     if (!m->pf.built && (rc = pf_build_weights(m))) return rc;
     const int chunk = std::min(m->prefill_chunk, lim);
     if ((rc = pf_build_buffers(m, (chunk + 127) & ~127))) return rc;
-    for (int p0 = 0; p0 < lim; p0 += chunk) {
-        const int T = std::min(chunk, lim - p0);
-        if ((rc = pf_run_chunk(m, p0, T, p0 + T >= lim))) return rc;
+    Prefill& P = m->pf;
+    // one HIP graph per prompt length (TMQ_PF_GRAPH=0: launched one by one)
+    if (!m->use_graphs || env_int("TMQ_PF_GRAPH", 1) == 0) {
+        if ((rc = pf_run_all(m, lim, chunk))) return rc;
+        *done = lim;
+        return 0;
     }
+    const int guq = env_int("TMQ_PF_GUQ", 1), spin = env_int("TMQ_PF_GUQ_SPIN", 1 << 20);
+    hipGraphExec_t ge = nullptr;
+    for (const auto& g : P.graphs)
+        if (g.lim == lim && g.chunk == chunk && g.guq == guq && g.spin == spin) ge = g.g;
+    if (!ge) {
+        // the launches' one-time set-up (kernel attributes) before the capture
+        if ((rc = tmq_pf_prepare())) return tmq_fail(TMQ_ERR_HIP, "prefill set-up: %s", hipGetErrorString((hipError_t)rc));
+        if (P.graphs.size() >= 8) {
+            HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+            for (auto& g : P.graphs) (void)hipGraphExecDestroy(g.g);
+            P.graphs.clear();
+        }
+        P.cap_lim = lim;
+        P.cap_chunk = chunk;
+        if ((rc = capture(m, [](tmq_model* mm) { return pf_run_all(mm, mm->pf.cap_lim, mm->pf.cap_chunk); }, &ge)))
+            return rc;
+        P.graphs.push_back({lim, chunk, guq, spin, ge});
+    }
+    HIP_TRY(hipGraphLaunch(ge, m->ctx->stream));
     *done = lim;
     return 0;
 }

@@ -222,6 +222,9 @@ int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s);
 // the token tiles of the launch in *ntiles.
 bool tmq_pf_gu_quant_fits(int tile, int T_pad, int gu_rows, int ncu, int* ntiles);
 int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s);
+// One-time set-up of the prefill launches (the attention kernels' dynamic
+// LDS limit), so that a stream capture of them makes no such call.
+int tmq_pf_prepare();
 int tmq_launch_pf_handoff(const TmqPfHandoff& h, hipStream_t s);
 int tmq_launch_pf_qkv_fin(const TmqPfQkvFin& f, hipStream_t s);
 size_t tmq_pf_attn_lds(int qpk, int npos);

@@ -930,14 +930,19 @@ size_t tmq_pf_attn_lds(int qpk, int npos) {
 }
 
 namespace {
+// resident GU workgroups a CU per tile (0: not known yet), from the first use
+int gu_per_cu[4] = {0, 0, 0, 0};
 template <int TILE>
 bool gu_quant_fits(int T_pad, int gu_rows, int ncu, int* ntiles) {
     typedef TileGeo<TILE> G;
     const long rt = gu_rows / (16 * G::NRB), tt = (T_pad + 32 * G::NTB - 1) / (32 * G::NTB);
-    int per = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)pf_gemm_kernel<TMQ_PF_GU, TILE>, 256, 0) !=
-        hipSuccess)
+    int& per = gu_per_cu[TILE];
+    if (per == 0 &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)pf_gemm_kernel<TMQ_PF_GU, TILE>, 256, 0) !=
+            hipSuccess) {
+        per = 0;
         return false;
+    }
     *ntiles = (int)tt;
     return rt * tt <= (long)per * ncu;
 }
@@ -988,19 +993,31 @@ int tmq_launch_pf_gemm(const TmqPfGemm& g, int tile, hipStream_t s) {
 }
 
 namespace {
+bool pf_prepared = false;
 template <int NPASS>
 int launch_attn(const TmqPfAttn& a, size_t lds, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)pf_attn_kernel<NPASS>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, TMQ_PF_ATTN_LDS_MAX);
-        if (e != hipSuccess) return (int)e;
-        attr = true;
+    if (!pf_prepared) {
+        const int e = tmq_pf_prepare();
+        if (e) return e;
     }
     hipLaunchKernelGGL((pf_attn_kernel<NPASS>), dim3(a.T, a.n_kv), dim3(512), lds, s, a);
     return (int)hipGetLastError();
 }
 }  // namespace
+
+int tmq_pf_prepare() {
+    if (pf_prepared) return 0;
+    for (const void* f : {(const void*)pf_attn_kernel<1>, (const void*)pf_attn_kernel<2>,
+                          (const void*)pf_attn_kernel<4>, (const void*)pf_attn_kernel<8>}) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, TMQ_PF_ATTN_LDS_MAX);
+        if (e != hipSuccess) return (int)e;
+    }
+    // (and the GU occupancies the quantising epilogue's check reads)
+    int nt = 0;
+    for (int tile = 0; tile < 4; tile++) (void)tmq_pf_gu_quant_fits(tile, 128, 64, 1, &nt);
+    pf_prepared = true;
+    return 0;
+}
 
 int tmq_launch_pf_attn(const TmqPfAttn& a, hipStream_t s) {
     const int qpk = a.n_heads / a.n_kv, np = a.p0 + a.T;
