@@ -14,31 +14,40 @@
 // involvement.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "tmq_device.h"
 #include "tmq_engine.h"
 #include "tmq_mathf.h"
 
 namespace {
 
+typedef __attribute__((address_space(3))) float lds_f32;
+
 // RoPE (sim/tmac_gguf.cpp:1527-1554, adjacent pairs, cos/sin table from the
 // host) + KV cache append (:1616-1617) + attention of one query head
-// (:1619-1655).  One workgroup per query head; head_dim is 64.  The q/k/v
-// terms and the RoPE row of this step (copied by the qkv launch) are read at
-// entry, before the position arrives, so the q/k/v finalisation waits for one
-// memory round trip; then the cached K row of each thread's first position
-// and the first 64 V rows (rows below the position: reading the rows not yet
-// written, as a position-free read would, measured 3 % slower per step).
+// (:1619-1655).  One workgroup of 8 waves per query head; head_dim is 64.
+// The q/k/v terms and the RoPE row of this step (copied by the qkv launch)
+// are read at entry, before the position arrives.  Once it has, every
+// thread loads the cached key row of its position (positions tid + 512 i,
+// the first pass at once) and the workgroup's waves put the cached V rows
+// into LDS by DMA (`vcap` rows at a time, all of them up to that count), so
+// that no phase after the scores waits on memory.  The sums are formed in
+// the reference's order: each score over d ascending, the exp sum and each
+// context dimension over positions ascending, one lane per sum.
 template <bool Q8, bool K8, bool V8>
-__global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
+__global__ __launch_bounds__(512) void attn_kernel(TmqAttnArgs a) {
     tmq_warm_kernargs<sizeof(TmqAttnArgs)>();
-    extern __shared__ float lds[];
-    float* sc = lds;                  // scores, max_pos
-    float* ex = lds + a.max_pos;      // exp terms / weights, max_pos
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int mp4 = (a.max_pos + 3) & ~3;  // (16-byte aligned regions)
+    float* sc = lds;                       // scores, max_pos
+    float* ex = lds + mp4;                 // exp terms / weights, max_pos
+    float* vb = lds + 2 * mp4;             // V rows [vcap][64]
     __shared__ float qr[64], kr[64], vn[64];
-    __shared__ float vbuf[2][64][64];
     __shared__ float red[8];
-    __shared__ float s_stat[2];
-    const int h = blockIdx.x, tid = threadIdx.x;
+    __shared__ float s_stat[1];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int qpk = a.n_heads / a.n_kv;
     const int kv = h / qpk;
     const int KV = a.n_kv * 64;
@@ -46,37 +55,25 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     // before the position arrives (valid addresses whatever it is)
     const int j = tid & 31, jv = tid & 63;
     const double qxs = (double)*a.q.xs, kxs = (double)*a.k.xs, vxs = (double)*a.v.xs;
-    const TmqFinRaw<Q8> fq0 = fin_load<Q8>(a.q, h * 64 + 2 * j), fq1 = fin_load<Q8>(a.q, h * 64 + 2 * j + 1);
-    const TmqFinRaw<K8> fk0 = fin_load<K8>(a.k, kv * 64 + 2 * j), fk1 = fin_load<K8>(a.k, kv * 64 + 2 * j + 1);
-    const TmqFinRaw<V8> fv = fin_load<V8>(a.v, kv * 64 + jv);
+    TmqFinRaw<Q8> fq0{}, fq1{};
+    TmqFinRaw<K8> fk0{}, fk1{};
+    TmqFinRaw<V8> fv{};
+    if (tid < 32) {
+        fq0 = fin_load<Q8>(a.q, h * 64 + 2 * j);
+        fq1 = fin_load<Q8>(a.q, h * 64 + 2 * j + 1);
+        fk0 = fin_load<K8>(a.k, kv * 64 + 2 * j);
+        fk1 = fin_load<K8>(a.k, kv * 64 + 2 * j + 1);
+    } else if (tid >= 64 && tid < 128) {
+        fv = fin_load<V8>(a.v, kv * 64 + jv);
+    }
     const float2 cs = a.rope_cur[j];
     const float* kb = a.kc + kv * 64;
-    const float* vb = a.vc + kv * 64;
+    const float* vbase = a.vc + kv * 64;
     const int pos = a.state->pos;
     if (a.state->err || pos < 0 || pos >= a.max_pos) return;
-    float4 kk[16];
-    {
-        const float4* kp = (const float4*)(kb + (size_t)min(tid, max(pos - 1, 0)) * KV);
-#pragma unroll
-        for (int i = 0; i < 16; i++) kk[i] = kp[i];
-    }
-    // V rows 0..63 below pos (thread: rows tid/16 + 16 u, 16-byte column tid % 16)
-    float4 v0[4];
-    const int nv0 = max(min(64, pos), 1);
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int pr = (tid >> 4) + 16 * u;
-        v0[u] = *(const float4*)(vb + (size_t)min(pr, nv0 - 1) * KV + 4 * (tid & 15));
-    }
-    // V rows [c0, c0+64) of cached positions (< pos) into vbuf[buf], by the
-    // threads from `first` on
-    auto stage = [&](int c0, int buf, int first) {
-        const int nrow = min(64, pos - c0);
-        for (int i = tid - first; i < nrow * 16; i += blockDim.x - first) {
-            const int pr = i >> 4, q4 = i & 15;
-            *(float4*)&vbuf[buf][pr][4 * q4] = *(const float4*)(vb + (size_t)(c0 + pr) * KV + 4 * q4);
-        }
-    };
+    const int vcap = a.vcap;
+    // (the q/k/v loads went out with the position's: finished first, so that
+    // their registers are free before the key row's)
     if (tid < 32) {
         const float q0 = fin_finish<Q8>(a.q, fq0, qxs), q1 = fin_finish<Q8>(a.q, fq1, qxs);
         qr[2 * tid] = q0 * cs.x - q1 * cs.y;
@@ -87,18 +84,31 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     } else if (tid >= 64 && tid < 128) {
         vn[tid - 64] = fin_finish<V8>(a.v, fv, vxs);
     }
+    // the cached key row of position tid (< pos; position pos is kr)
+    float4 kk[16];
+    {
+        const float4* kp = (const float4*)(kb + (size_t)min(tid, max(pos - 1, 0)) * KV);
 #pragma unroll
-    for (int u = 0; u < 4; u++) *(float4*)&vbuf[0][(tid >> 4) + 16 * u][4 * (tid & 15)] = v0[u];
-    __syncthreads();
-    if (tid < 64) {
-        if (h % qpk == 0) {
-            a.kc[(size_t)pos * KV + kv * 64 + tid] = kr[tid];
-            a.vc[(size_t)pos * KV + kv * 64 + tid] = vn[tid];
+        for (int i = 0; i < 16; i++) kk[i] = kp[i];
+    }
+    // V rows [base, base + n) of the cache into vb[0, n) by DMA: wave w
+    // takes rows 4w + 32i .. +3, lane l row + l / 16, 16 bytes at 4 (l % 16)
+    // (rows past n re-read row n - 1 into vb rows below vcap: never used)
+    auto stage_v = [&](int base, int n) {
+        for (int r0 = 4 * wave; r0 < n; r0 += 32) {
+            const int rr = min(r0 + (lane >> 4), n - 1);
+            __builtin_amdgcn_global_load_lds((const void*)(vbase + (size_t)(base + rr) * KV + 4 * (lane & 15)),
+                                             (lds_f32*)(vb + r0 * 64), 16, 0, 0);
         }
-        if (pos < 64) vbuf[0][pos][tid] = vn[tid];
+    };
+    stage_v(0, min(pos, vcap));
+    __syncthreads();
+    if (tid < 64 && h % qpk == 0) {
+        a.kc[(size_t)pos * KV + kv * 64 + tid] = kr[tid];
+        a.vc[(size_t)pos * KV + kv * 64 + tid] = vn[tid];
     }
     // scores[p] = sum_d q[d]*k[p][d] (d ascending), / sqrt(64)
-    for (int p = tid; p <= pos; p += blockDim.x) {
+    for (int p = tid; p <= pos; p += 512) {
         float s = 0.0f;
         if (p == pos) {
             for (int d = 0; d < 64; d++) s += qr[d] * kr[d];
@@ -120,12 +130,14 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     }
     __syncthreads();
     float m = -__builtin_inff();
-    for (int p = tid; p <= pos; p += blockDim.x) m = fmaxf(m, sc[p]);
+    for (int p = tid; p <= pos; p += 512) m = fmaxf(m, sc[p]);
     m = tmq_wave_max(m);
-    if ((tid & 63) == 0) red[tid >> 6] = m;
+    if (lane == 0) red[wave] = m;
     __syncthreads();
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = tid; p <= pos; p += blockDim.x) ex[p] = tmq_math::tmq_expf(sc[p] - mx);
+    float mx = red[0];
+#pragma unroll
+    for (int w = 1; w < 8; w++) mx = fmaxf(mx, red[w]);
+    for (int p = tid; p <= pos; p += 512) ex[p] = tmq_math::tmq_expf(sc[p] - mx);
     __syncthreads();
     if (tid == 0) {
         // exp_sum in position order (:1648-1649), 16 terms per batch of LDS reads
@@ -134,13 +146,13 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
         for (; p + 16 <= pos + 1; p += 16) {
             float4 v[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = *(const float4*)(ex + p + 4 * j);
+            for (int jj = 0; jj < 4; jj++) v[jj] = *(const float4*)(ex + p + 4 * jj);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                es += v[j].x;
-                es += v[j].y;
-                es += v[j].z;
-                es += v[j].w;
+            for (int jj = 0; jj < 4; jj++) {
+                es += v[jj].x;
+                es += v[jj].y;
+                es += v[jj].z;
+                es += v[jj].w;
             }
         }
         for (; p <= pos; p++) es += ex[p];
@@ -148,36 +160,38 @@ __global__ __launch_bounds__(256) void attn_kernel(TmqAttnArgs a) {
     }
     __syncthreads();
     const float ls = s_stat[0];
-    for (int p = tid; p <= pos; p += blockDim.x) ex[p] = tmq_math::tmq_expf(sc[p] - ls);
+    for (int p = tid; p <= pos; p += 512) ex[p] = tmq_math::tmq_expf(sc[p] - ls);
+    // this wave's V copies have landed; the barrier makes every wave's visible
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    // context[d] = sum_p w[p]*v[p][d] (p ascending): wave 0 adds chunk c0
-    // while waves 1-3 stage the next 64 rows
+    // context[d] = sum_p w[p]*v[p][d] (p ascending) in wave 0, vcap staged
+    // rows at a time (the row of position pos is vn)
     float acc = 0.0f;
-    int buf = 0;
-    for (int c0 = 0; c0 <= pos; c0 += 64) {
-        const int c1 = c0 + 64;
-        if (c1 <= pos && tid >= 64) {
-            stage(c1, buf ^ 1, 64);
-            if (c1 + 64 > pos && tid < 128) vbuf[buf ^ 1][pos - c1][tid - 64] = vn[tid - 64];
+    for (int base = 0; base <= pos; base += vcap) {
+        const int nb = min(vcap, pos + 1 - base);  // positions of this pass
+        if (base > 0) {
+            __syncthreads();  // wave 0 is done with the previous rows
+            stage_v(base, min(vcap, pos - base));
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
         }
-        if (tid < 64) {
-            const int nrow = min(64, pos + 1 - c0);
+        if (wave == 0) {
+            if (pos - base < nb) vb[(pos - base) * 64 + lane] = vn[lane];
+            const float* e = ex + base;
             int pr = 0;
-            for (; pr + 4 <= nrow; pr += 4) {
-                const float4 e4 = *(const float4*)(ex + c0 + pr);
-                const float v0 = vbuf[buf][pr][tid], v1 = vbuf[buf][pr + 1][tid];
-                const float v2 = vbuf[buf][pr + 2][tid], v3 = vbuf[buf][pr + 3][tid];
+            for (; pr + 4 <= nb; pr += 4) {
+                const float4 e4 = *(const float4*)(e + pr);
+                const float v0 = vb[pr * 64 + lane], v1 = vb[(pr + 1) * 64 + lane];
+                const float v2 = vb[(pr + 2) * 64 + lane], v3 = vb[(pr + 3) * 64 + lane];
                 acc += e4.x * v0;
                 acc += e4.y * v1;
                 acc += e4.z * v2;
                 acc += e4.w * v3;
             }
-            for (; pr < nrow; pr++) acc += ex[c0 + pr] * vbuf[buf][pr][tid];
+            for (; pr < nb; pr++) acc += e[pr] * vb[pr * 64 + lane];
         }
-        __syncthreads();
-        buf ^= 1;
     }
-    if (tid < 64) a.ctx[h * 64 + tid] = acc;
+    if (wave == 0) a.ctx[h * 64 + lane] = acc;
 }
 
 // Greedy pick from the logits GEMV's per-wave candidates (largest logit,
@@ -217,12 +231,50 @@ __global__ void advance_kernel(TmqEngState* state, int max_pos) {
 
 }  // namespace
 
-int tmq_launch_attn(const TmqAttnArgs& a, hipStream_t s) {
+namespace {
+const void* attn_fns[8] = {
+    (const void*)attn_kernel<false, false, false>, (const void*)attn_kernel<false, false, true>,
+    (const void*)attn_kernel<false, true, false>,  (const void*)attn_kernel<false, true, true>,
+    (const void*)attn_kernel<true, false, false>,  (const void*)attn_kernel<true, false, true>,
+    (const void*)attn_kernel<true, true, false>,   (const void*)attn_kernel<true, true, true>};
+bool attn_prepared = false;
+}  // namespace
+
+int tmq_attn_vcap(int max_pos) {
+    const int mp4 = (max_pos + 3) & ~3;
+    const int lim = (TMQ_ATTN_LDS_MAX / 4 - 2 * mp4) / 64;
+    const int all = (max_pos + 63) & ~63;
+    return std::min(all, lim & ~63);
+}
+size_t tmq_attn_lds(int max_pos) {
+    return sizeof(float) * ((size_t)2 * ((max_pos + 3) & ~3) + (size_t)64 * tmq_attn_vcap(max_pos));
+}
+
+int tmq_attn_prepare() {
+    if (attn_prepared) return 0;
+    for (const void* f : attn_fns) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, TMQ_ATTN_LDS_MAX);
+        if (e != hipSuccess) return (int)e;
+    }
+    attn_prepared = true;
+    return 0;
+}
+
+int tmq_launch_attn(const TmqAttnArgs& a0, hipStream_t s) {
     // q, k, v: K-split sums (ntiles 0) or Q8_0 tile sums (at most TMQ_FIN_MAXT tiles)
-    if (a.q.ntiles > TMQ_FIN_MAXT || a.k.ntiles > TMQ_FIN_MAXT || a.v.ntiles > TMQ_FIN_MAXT)
+    if (a0.q.ntiles > TMQ_FIN_MAXT || a0.k.ntiles > TMQ_FIN_MAXT || a0.v.ntiles > TMQ_FIN_MAXT)
         return (int)hipErrorInvalidValue;
-    const dim3 grid(a.n_heads), blk(256);
-    const size_t lds = sizeof(float) * 2 * a.max_pos;
+    if (a0.max_pos < 1 || a0.max_pos > TMQ_MAX_POS || a0.n_kv < 1 || a0.n_heads % a0.n_kv)
+        return (int)hipErrorInvalidValue;
+    TmqAttnArgs a = a0;
+    a.vcap = tmq_attn_vcap(a.max_pos);
+    if (a.vcap < 64) return (int)hipErrorInvalidValue;
+    if (!attn_prepared) {
+        const int e = tmq_attn_prepare();
+        if (e) return e;
+    }
+    const dim3 grid(a.n_heads), blk(512);
+    const size_t lds = tmq_attn_lds(a.max_pos);
     const int code = (a.q.ntiles > 0 ? 4 : 0) | (a.k.ntiles > 0 ? 2 : 0) | (a.v.ntiles > 0 ? 1 : 0);
     switch (code) {
     case 0: hipLaunchKernelGGL((attn_kernel<false, false, false>), grid, blk, lds, s, a); break;

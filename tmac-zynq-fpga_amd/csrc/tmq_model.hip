@@ -779,6 +779,8 @@ int pf_prompt(tmq_model* m, int n, int* done) {
 // get_logits, i.e. `matmul` of token_embd (:1852-1866, :2033-2037).
 int build_launches(tmq_model* m) {
     const tmq_model_config& c = m->cfg;
+    // the attention's dynamic LDS limit, set before any capture
+    if (const int e = tmq_attn_prepare()) return tmq_fail(TMQ_ERR_HIP, "attention set-up: %s", hipGetErrorString((hipError_t)e));
     const int L = c.n_layers, H = c.hidden, I = c.inter;
     const uint32_t flags = m->flags;
     auto path_of = [&](const tmq_tensor* t) {
