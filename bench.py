@@ -309,10 +309,21 @@ def decode_bench(ctx, torch, stream, tokens=128, warmup=8):
     ms = time_events(torch, stream, lambda: m.generate_async(tokens), 1) / tokens
     got = m.tokens(1, tokens)
     wb = m.weight_bytes
+    # beside it (not the line's figure): the same decode with the cache
+    # already at 384 positions (a seeded 384-token prompt through the
+    # batched prefill), 64 steps up to position 447
+    long_toks = np.random.Generator(np.random.PCG64(384)).integers(0, 151936, size=384).astype(np.int32)
+    m.prompt(long_toks)
+    m.generate(4)
+    m.prompt(long_toks)
+    ctx.sync()
+    ms_long = time_events(torch, stream, lambda: m.generate_async(64), 1) / 64
     m.free()
     return {"tokens": tokens, "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 1),
             "weight_gbps": round(wb / (ms * 1e-3) / 1e9, 1), "weight_bytes_per_token": wb,
-            "first_tokens": got[:8].tolist()}
+            "first_tokens": got[:8].tolist(),
+            "after_384_token_prompt": {"positions": "384-447", "ms_per_token": round(ms_long, 4),
+                                       "tok_s": round(1e3 / ms_long, 1)}}
 
 
 # int8 MACs per token of the batched prefill: four digit products per
