@@ -291,7 +291,7 @@ def single_launch_us(ctx, torch, dev, stream, steps):
     return ms * 1e3
 
 
-def decode_bench(ctx, torch, stream, tokens=128, warmup=8):
+def decode_bench(ctx, torch, stream, tokens=128, warmup=8, long_ctx=True):
     """greedy batch-1 decode of the synthetic Qwen2-0.5B
     model (tmq.model_synth, seed 2024) from one seeded prompt token; one
     step = logits GEMV + argmax + embedding + 24 layers, graph-replayed."""
@@ -309,21 +309,23 @@ def decode_bench(ctx, torch, stream, tokens=128, warmup=8):
     ms = time_events(torch, stream, lambda: m.generate_async(tokens), 1) / tokens
     got = m.tokens(1, tokens)
     wb = m.weight_bytes
-    # beside it (not the line's figure): the same decode with the cache
-    # already at 384 positions (a seeded 384-token prompt through the
-    # batched prefill), 64 steps up to position 447
-    long_toks = np.random.Generator(np.random.PCG64(384)).integers(0, 151936, size=384).astype(np.int32)
-    m.prompt(long_toks)
-    m.generate(4)
-    m.prompt(long_toks)
-    ctx.sync()
-    ms_long = time_events(torch, stream, lambda: m.generate_async(64), 1) / 64
+    out = {"tokens": tokens, "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+           "weight_gbps": round(wb / (ms * 1e-3) / 1e9, 1), "weight_bytes_per_token": wb,
+           "first_tokens": got[:8].tolist()}
+    if long_ctx:
+        # beside it (not the line's figure): the same decode with the cache
+        # already at 384 positions (a seeded 384-token prompt through the
+        # batched prefill), 64 steps up to position 447
+        long_toks = np.random.Generator(np.random.PCG64(384)).integers(0, 151936, size=384).astype(np.int32)
+        m.prompt(long_toks)
+        m.generate(4)
+        m.prompt(long_toks)
+        ctx.sync()
+        ms_long = time_events(torch, stream, lambda: m.generate_async(64), 1) / 64
+        out["after_384_token_prompt"] = {"positions": "384-447", "ms_per_token": round(ms_long, 4),
+                                         "tok_s": round(1e3 / ms_long, 1)}
     m.free()
-    return {"tokens": tokens, "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 1),
-            "weight_gbps": round(wb / (ms * 1e-3) / 1e9, 1), "weight_bytes_per_token": wb,
-            "first_tokens": got[:8].tolist(),
-            "after_384_token_prompt": {"positions": "384-447", "ms_per_token": round(ms_long, 4),
-                                       "tok_s": round(1e3 / ms_long, 1)}}
+    return out
 
 
 # int8 MACs per token of the batched prefill: four digit products per
@@ -427,6 +429,8 @@ def main():
                     help="c4: only the full-model greedy decode (BASELINE configs[3]); "
                          "c5: only the 512-token batched prefill (BASELINE configs[4])")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE GEMV configs")
+    ap.add_argument("--no-long-ctx", action="store_true",
+                    help="decode legs: skip the steps with the cache at 384 positions")
     args = ap.parse_args()
     dflt = {"c4": (128, 8), "c5": (20, 1)}.get(args.workload, (200, 400))
     if args.steps is None:
@@ -450,7 +454,8 @@ def main():
     stream = torch.cuda.ExternalStream(ctx.stream)
     wl = args.workload
     if wl == "c4":
-        dec = decode_bench(ctx, torch, stream, tokens=min(args.steps, 500), warmup=args.warmup)
+        dec = decode_bench(ctx, torch, stream, tokens=min(args.steps, 500), warmup=args.warmup,
+                           long_ctx=not args.no_long_ctx)
         ctx.close()
         out = {"metric": "Qwen2-0.5B batch-1 greedy decode tok/s", "value": dec["tok_s"], "unit": "tok/s",
                "n_gpus": 1, "steps": dec["tokens"], "warmup": args.warmup, "ms_per_step": dec["ms_per_token"],
@@ -559,7 +564,7 @@ def main():
                            "gbps": round(wb / (km * 1e-3) / 1e9, 2),
                            "pct_hbm_peak": round(100.0 * wb / (km * 1e-3) / 1e9 / PEAK_GBPS, 2)}
         extra["c2_attn_q_single_launch_us"] = round(single_launch_us(ctx, torch, dev, stream, 50), 2)
-        extra["c4_decode"] = decode_bench(ctx, torch, stream)
+        extra["c4_decode"] = decode_bench(ctx, torch, stream, long_ctx=not args.no_long_ctx)
         extra["c5_prefill"] = prefill_bench(ctx, 512, 20)
         out["extra"] = extra
     ctx.close()
