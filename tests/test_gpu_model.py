@@ -125,6 +125,29 @@ def test_graphs_match_eager(model, golden):
     assert np.array_equal(res[0][2].view(np.uint32), res[1][2].view(np.uint32))
 
 
+@pytest.mark.parametrize("max_seq", [61, 130])
+def test_cache_capacity_free(ctx, golden, max_seq):
+    """The attention's LDS holds the scores, weights and staged V rows of up
+    to max_seq positions (16-byte aligned regions, V rows in whole 64s): a
+    model whose max_seq is no multiple of 4 or 64 decodes the reference's
+    greedy tokens and final state of the same steps."""
+    import tmq
+    from tmq import model_synth, tmacfile
+    n = min(max_seq - 2, int(golden["tokens"].size))
+    print(f"[model] max_seq {max_seq}: {n} greedy steps", flush=True)
+    blob = tmacfile.to_bytes(model_synth.gen_model(int(golden["model_seed"])))
+    m = tmq.Model(ctx, blob, max_seq=max_seq)
+    del blob
+    try:
+        m.prompt(golden["prompt"])
+        got = m.generate(n)
+        assert np.array_equal(got, golden["tokens"][:n])
+        if n == golden["tokens"].size:
+            assert np.array_equal(m.hidden().view(np.uint32), golden["hidden_final"].view(np.uint32))
+    finally:
+        m.free()
+
+
 def test_engine_mfma_decoders(ctx, golden, monkeypatch):
     """TMQ_ENG_MFMA=1 at load puts the engine's Q5_0 / K-quant projections on
     the int8 MFMA decoders (operand bytes written by the launch prologue,
