@@ -130,7 +130,7 @@ struct Prefill {
     float* xs[4] = {nullptr, nullptr, nullptr, nullptr};
     int64_t* part = nullptr;
     uint32_t* max_bits = nullptr;
-    uint32_t* gq_cnt = nullptr;  // arrival counters of the quantising GU epilogue, one a token tile
+    uint32_t* gq_cnt = nullptr;  // the quantising GU epilogue's counters and release flags (TmqPfGemm.gq_cnt)
     int dn_split = 4;
     int o_split = 2;   // attn_output GEMM split over K (finalised by the ffn_norm input)
     int qkv_split = 1; // q/k/v GEMM split over K (finished by pf_qkv_fin)
