@@ -431,6 +431,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE GEMV configs")
     ap.add_argument("--no-long-ctx", action="store_true",
                     help="decode legs: skip the steps with the cache at 384 positions")
+    ap.add_argument("--prompt-tokens", type=int, default=512,
+                    help="c5: prompt length (BASELINE configs[4] is 512; shorter ones show the fixed costs)")
     args = ap.parse_args()
     dflt = {"c4": (128, 8), "c5": (20, 1)}.get(args.workload, (200, 400))
     if args.steps is None:
@@ -468,7 +470,10 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if wl == "c5":
-        pf = prefill_bench(ctx, 512, max(3, min(args.steps, 20)))
+        n_pf = args.prompt_tokens
+        if not 1 <= n_pf <= 4096:
+            sys.exit("bench.py: --prompt-tokens must be 1..4096")
+        pf = prefill_bench(ctx, n_pf, max(3, min(args.steps, 20)))
         ctx.close()
         cpu = None
         if not args.no_cpu:
@@ -476,13 +481,15 @@ def main():
             if dec is not None:
                 # the reference's process_prompt is the same per-token step
                 cpu = dict(dec, sample=dec["sample"] + "; process_prompt runs the same step per prompt token")
-        out = {"metric": "Qwen2-0.5B batched prefill tok/s (512-token prompt)", "value": pf["tok_s"],
+        out = {"metric": f"Qwen2-0.5B batched prefill tok/s ({n_pf}-token prompt)", "value": pf["tok_s"],
                "unit": "tok/s", "n_gpus": 1, "steps": max(3, min(args.steps, 20)), "warmup": 1,
                "ms_per_step": pf["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                "dtype": "int8 (exact int16 x int16 as digit products)",
-               "data": "synthetic Qwen2-0.5B-shaped model (tmq.model_synth seed 2024), 512 seeded token ids",
-               "config": {"workload": "BASELINE configs[4]: 512-token prompt, 24 layers, batched prefill "
-                          "(bit-exact with the one-token-at-a-time prompt)", "prompt_tokens": 512},
+               "data": f"synthetic Qwen2-0.5B-shaped model (tmq.model_synth seed 2024), {n_pf} seeded token ids",
+               "config": {"workload": ("BASELINE configs[4]: 512-token prompt" if n_pf == 512 else
+                                       f"{n_pf}-token prompt (BASELINE configs[4] is 512)") +
+                          ", 24 layers, batched prefill (bit-exact with the one-token-at-a-time prompt)",
+                          "prompt_tokens": n_pf},
                "roofline": {"bound": "mfma", "achieved": pf["int8_tops"], "peak": MFMA_I8_PEAK_TOPS,
                             "unit": "TFLOP/s", "frac": pf["mfma_frac"], "traffic": None,
                             "kernel": "whole prefill (int8 digit MACs / prompt time)"},
