@@ -69,24 +69,45 @@ template <> struct Tile<3> { static constexpr int NWR = 1, NWT = 4, WTB = 1, NBU
 template <> struct Tile<4> { static constexpr int NWR = 1, NWT = 2, WTB = 1, NBUF = 3, KG = 2; };  // 64 x 64, K in halves
 constexpr int KC = 2;  // column steps (of 32) per stage and K group
 
-template <int TILE>
+template <int TILE, bool TR = false>
 struct TileGeo {
     static constexpr int KG = Tile<TILE>::KG;
     static constexpr int KS = KC * KG;                                 // column steps per stage
     static constexpr int NRB = 2 * Tile<TILE>::NWR;                    // row blocks per workgroup
     static constexpr int NTB = Tile<TILE>::NWT * Tile<TILE>::WTB;      // token blocks per workgroup
     static constexpr int FRAGS = (NRB + NTB) * KS * 2;                 // 1 KiB fragments per stage
-    static constexpr int FPW = FRAGS / 4;                              // per wave
-    static constexpr int STAGE = FRAGS * 1024;
+    static constexpr int FPW = FRAGS / 4;                              // memory operations per wave and stage
     static constexpr int NBUF = Tile<TILE>::NBUF;
     static constexpr int GW = Tile<TILE>::NWR * Tile<TILE>::NWT;       // waves per K group
+    // TREG (asked for by TR): with one wave row, each wave's token fragments
+    // are its own, so the wave loads them into registers (a ring of NBUF
+    // stages) and only the weight fragments, which the waves share, go
+    // through LDS
+    static constexpr bool TREG = TR && Tile<TILE>::NWR == 1;
+    static constexpr int LFR = TREG ? NRB * KS * 2 : FRAGS;            // LDS fragments per stage
+    static constexpr int LPW = LFR / 4;                                // their copies per wave
+    static constexpr int TPW = TREG ? Tile<TILE>::WTB * KC * 2 : 0;    // token loads per wave
     // int32 digit sums a wave holds: 2 x WTB blocks x 3 accumulators x 16
     static constexpr int ACCW = 2 * Tile<TILE>::WTB * 3 * 16;
+    // the ring also holds the epilogue's K-group exchange and transposes
+    static constexpr int EPI = KG == 2 ? KG * GW * (ACCW / 2) * 64 * 4 : 4 * 32 * 34 * 8;
+    static constexpr int STAGE = LFR * 1024 > (EPI + NBUF - 1) / NBUF ? LFR * 1024 : ((EPI + NBUF - 1) / NBUF + 1023) / 1024 * 1024;
     static_assert(GW * KG == 4 && KG <= 2, "four waves, K in one or two groups");
+    static_assert(LFR % 4 == 0 && LPW + TPW == FPW, "whole copies per wave; the same operations per stage");
     static_assert((NBUF - 1) * FPW <= 63, "vmcnt holds 6 bits");
-    static_assert(KG * GW * (ACCW / 2) * 64 * 4 <= NBUF * STAGE, "the K groups' exchanged sums fit the stage ring");
+    static_assert(KG * GW * (ACCW / 2) * 64 * 4 <= NBUF * STAGE || KG == 1, "the K groups' exchanged sums fit the stage ring");
     static_assert(NBUF * STAGE >= 4 * 32 * 34 * 8, "the epilogue's transpose slices fit the stage ring");
 };
+
+template <typename F, int... B>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, B...>) {
+    (f(std::integral_constant<int, B>{}), ...);
+}
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>), in order
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
 
 // s_waitcnt vmcnt(k * FPW): the copies of the k newest stages may still be
 // in flight
@@ -193,7 +214,11 @@ template <int MODE, int TILE>
 __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gemm_kernel(TmqPfGemm g) {
     tmq_warm_kernargs<sizeof(TmqPfGemm)>();
     typedef Tile<TILE> C;
-    typedef TileGeo<TILE> G;
+    // token fragments in registers for gate/up and attn_output (measured:
+    // gate/up 35.4 -> 34.2 us, attn_output 8.6 -> 8.3; q/k/v and down were
+    // slower that way, 13.4 -> 15.6 and 16.1 -> 17.9)
+    constexpr bool TR = MODE == TMQ_PF_GU || (MODE == TMQ_PF_PART && TILE == 4);
+    typedef TileGeo<TILE, TR> G;
     constexpr int WTB = C::WTB;
     constexpr bool QKVM = MODE == TMQ_PF_QKV || MODE == TMQ_PF_QKVS;    // q|k|v segments
     constexpr bool PARTM = MODE == TMQ_PF_PART || MODE == TMQ_PF_QKVS;  // int64 sums out
@@ -266,13 +291,13 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         pre_rw = g.rw_t[row];
         pre_bias = hasb ? Sg.bias[rr] : 0.0f;
     }
-    // stage st -> buffer b: fragment f of FRAGS (run f / 2KC = one row or
-    // token block, KC column steps x 2 digits contiguous on both sides);
-    // wave w issues f = w, w+4, ...  K is a multiple of 32*KC.
+    // stage st -> buffer b: fragment f of LFR (run f / 2KS = one row or
+    // token block, KS column steps x 2 digits contiguous on both sides);
+    // wave w issues f = w, w+4, ...  K is a multiple of 32*KS.
     auto issue = [&](int st, int b) {
         const int ks = (st0 + st) * G::KS;
 #pragma unroll
-        for (int k = 0; k < G::FPW; k++) {
+        for (int k = 0; k < G::LPW; k++) {
             const int f = wave + 4 * k;  // wave-uniform
             const int run = f / (G::KS * 2), in = f % (G::KS * 2);
             const bool wgt = run < G::NRB;
@@ -286,6 +311,21 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
     // (column step kc of the wave's K group)
     auto frag = [&](int b, int run, int kc, int d) -> tmq_v4i {
         return *(const tmq_v4i*)(lds[b] + ((size_t)(run * G::KS + kg * KC + kc) * 2 + d) * 1024 + lane * 16);
+    };
+    // TREG: the wave's token fragments of stage st (its WTB blocks, its K
+    // group's KC column steps, both digits), the bytes issue() would have
+    // copied for them
+    typedef tmq_v4i TokStage[WTB][KC][2];
+    auto tload = [&](int st, TokStage& dst) {
+        const int ks = (st0 + st) * G::KS + kg * KC;
+#pragma unroll
+        for (int j = 0; j < WTB; j++) {
+            const int8_t* src = g.x + ((size_t)(tblk0 + wt * WTB + j) * nks + ks) * 2048 + lane * 16;
+#pragma unroll
+            for (int kc = 0; kc < KC; kc++)
+#pragma unroll
+                for (int d = 0; d < 2; d++) dst[j][kc][d] = *(const tmq_v4i*)(src + (kc * 2 + d) * 1024);
+        }
     };
 
     tmq_v16i acc[2][WTB][3];
@@ -325,15 +365,32 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
         }
     }
 
-    for (int st = 0; st < G::NBUF - 1 && st < nst; st++) issue(st, st);
+    // the token ring (TREG): slot b holds the stage that LDS buffer b holds
+    TokStage tk[G::TREG ? G::NBUF : 1];
+    static_for<G::NBUF - 1>([&](auto sc) {
+        constexpr int st = decltype(sc)::value;
+        if (st < nst) {
+            issue(st, st);
+            if constexpr (G::TREG) tload(st, tk[st]);
+        }
+    });
     // the K loop, compiled twice: with the Q8_0 tile sums (Q8 true) and
-    // without them, so that the common loop carries none of their registers
+    // without them, so that the common loop carries none of their registers;
+    // unrolled by NBUF so that every ring slot is a fixed set of registers
+    // (stage st in buffer and slot st % NBUF)
     auto kloop = [&](auto q8c) {
     constexpr bool Q8 = decltype(q8c)::value;
-    for (int st = 0; st < nst; st++) {
-        const int b = st % G::NBUF;
-        // refill the buffer the previous iteration finished with
-        if (st + G::NBUF - 1 < nst) issue(st + G::NBUF - 1, (st + G::NBUF - 1) % G::NBUF);
+    for (int sb = 0; sb < nst; sb += G::NBUF)
+    static_for<G::NBUF>([&](auto bc) {
+        constexpr int b = decltype(bc)::value;
+        const int st = sb + b;
+        if (st >= nst) return;
+        // refill the buffer (and slot) the previous iteration finished with
+        if (st + G::NBUF - 1 < nst) {
+            constexpr int nb = (b + G::NBUF - 1) % G::NBUF;
+            issue(st + G::NBUF - 1, nb);
+            if constexpr (G::TREG) tload(st + G::NBUF - 1, tk[nb]);
+        }
         wait_stages<G::FPW, G::NBUF>(min(G::NBUF - 1, nst - 1 - st));
         // the stage's LDS copies are complete in this wave (vmcnt above);
         // the barrier makes them complete in all.  A plain s_barrier (the
@@ -350,7 +407,14 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
 #pragma unroll
                 for (int j = 0; j < WTB; j++) {
                     const int tr = G::NRB + wt * WTB + j;
-                    const tmq_v4i c = frag(b, tr, kc, 0), e = frag(b, tr, kc, 1);
+                    tmq_v4i c, e;
+                    if constexpr (G::TREG) {
+                        c = tk[b][j][kc][0];
+                        e = tk[b][j][kc][1];
+                    } else {
+                        c = frag(b, tr, kc, 0);
+                        e = frag(b, tr, kc, 1);
+                    }
                     acc[0][j][0] = mfma(a0, c, acc[0][j][0]);
                     acc[1][j][0] = mfma(a1, c, acc[1][j][0]);
                     acc[0][j][1] = mfma(a0, e, acc[0][j][1]);
@@ -384,9 +448,9 @@ __global__ __launch_bounds__(256, TILE == 1 ? 2 : TILE == 3 ? 3 : 1) void pf_gem
             }
         }
         // every wave's reads of buffer b are done (their values fed the
-        // MFMAs above) before the next iteration copies stage st+2 into it
+        // MFMAs above) before the next iteration copies a stage into it
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    }
+    });
     };
     if (QKVM && q8) kloop(std::integral_constant<bool, true>{});
     else kloop(std::integral_constant<bool, false>{});
