@@ -42,7 +42,8 @@ def prompt_of(n, seed):
     return np.random.default_rng(seed).integers(0, 151936, size=n).astype(np.int32)
 
 
-@pytest.mark.parametrize("n", [2, 37, 100, 200, 300, 512])
+# (1 token; either side of a 32-token block and of a 128-token GEMM tile)
+@pytest.mark.parametrize("n", [1, 2, 31, 33, 37, 100, 127, 128, 129, 200, 257, 300, 512])
 def test_prefill_matches_sequential(model, n):
     toks = prompt_of(n, 1000 + n)
     print(f"[prefill] n={n} sequential", flush=True)
@@ -55,12 +56,14 @@ def test_prefill_matches_sequential(model, n):
     assert model.tokens(0, n).tolist() == toks.tolist()
 
 
-def test_prefill_chunks(model):
-    """chunks of 64 tokens: later chunks attend to the cache the earlier ones wrote"""
-    toks = prompt_of(150, 77)
-    print("[prefill] chunked 64 vs sequential", flush=True)
+@pytest.mark.parametrize("n, chunk", [(150, 64), (385, 128), (260, 256)])
+def test_prefill_chunks(model, n, chunk):
+    """chunks of 64-256 tokens, the last one ragged: later chunks attend to
+    the cache the earlier ones wrote"""
+    toks = prompt_of(n, 77 + n)
+    print(f"[prefill] n={n} chunked {chunk} vs sequential", flush=True)
     l0, h0, g0 = run(model, toks, 0)
-    l1, h1, g1 = run(model, toks, 64)
+    l1, h1, g1 = run(model, toks, chunk)
     assert np.array_equal(h1.view(np.uint32), h0.view(np.uint32))
     assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32))
     assert g1.tolist() == g0.tolist()
